@@ -1,0 +1,71 @@
+"""NumPy restatement of vllmlite/attention.py:21-98. Test infrastructure only.
+
+The operations, their shapes and their order are the reference's, so that the
+fp32 results (and the CPU time) are those of the reference.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def build_rope(head_dim: int, max_pos: int, theta: float = 10000.0):
+    """attention.py:21-25: fp32 angle table pos * theta^(-2i/D); returns (cos, sin) [max_pos, D/2]."""
+    inv = 1.0 / (theta ** (np.arange(0, head_dim, 2, dtype=np.float32) / head_dim))
+    ang = np.arange(max_pos, dtype=np.float32)[:, None] * inv[None, :]
+    return np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+
+
+def apply_rope(x: np.ndarray, positions: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """attention.py:28-37: rotate interleaved (even, odd) pairs of each head. x [T, H, D]."""
+    c = cos[positions][:, None, :]
+    s = sin[positions][:, None, :]
+    even = x[..., 0::2]
+    odd = x[..., 1::2]
+    out = np.empty_like(x)
+    out[..., 0::2] = even * c - odd * s
+    out[..., 1::2] = even * s + odd * c
+    return out
+
+
+def gather_slots(block_ids, block_size: int, count: int) -> np.ndarray:
+    """attention.py:40-44: flat slots of positions 0..count-1 through a block table."""
+    bids = np.asarray(block_ids, dtype=np.int64)
+    return (bids[:, None] * block_size + np.arange(block_size, dtype=np.int64)[None, :]).reshape(-1)[:count]
+
+
+def write_kv(cache_k, cache_v, k, v, slots) -> None:
+    """attention.py:47-49: scatter rows into the flat [slots, Hkv, D] cache."""
+    cache_k[slots] = k
+    cache_v[slots] = v
+
+
+def softmax_(x: np.ndarray) -> np.ndarray:
+    """attention.py:52-56, in place over the last axis."""
+    x -= x.max(axis=-1, keepdims=True)
+    np.exp(x, out=x)
+    x /= x.sum(axis=-1, keepdims=True)
+    return x
+
+
+def paged_attention(q, cache_k, cache_v, read_slots, n_kv_heads: int, scale: float) -> np.ndarray:
+    """attention.py:59-98, one sequence. q [q_len, H, D]; read_slots are all
+    ctx slots of the sequence in position order; query j sits at position
+    ctx - q_len + j and sees keys 0..that position (mask only when q_len > 1)."""
+    q_len, n_heads, d = q.shape
+    ctx = read_slots.shape[0]
+    rep = n_heads // n_kv_heads
+    k = cache_k[read_slots]
+    v = cache_v[read_slots]
+    qg = q.transpose(1, 0, 2).reshape(n_kv_heads, rep * q_len, d)
+    scores = np.matmul(qg, k.transpose(1, 2, 0))
+    scores *= scale
+    if q_len > 1:
+        qpos = np.arange(ctx - q_len, ctx)[:, None]
+        kpos = np.arange(ctx)[None, :]
+        scores = scores.reshape(n_kv_heads, rep, q_len, ctx)
+        scores[:, :, kpos > qpos] = -np.inf
+        scores = scores.reshape(n_kv_heads, rep * q_len, ctx)
+    softmax_(scores)
+    out = np.matmul(scores, v.transpose(1, 0, 2))
+    return out.reshape(n_heads, q_len, d).transpose(1, 0, 2)

@@ -1,0 +1,117 @@
+"""Writes the golden fixtures that only the reference itself can pin.
+
+Run in the build container (where the reference is mounted read-only at
+/root/reference), never on a GPU machine:
+
+    python tests/golden/make_golden.py
+
+Outputs (small JSON, committed):
+  cfg0_streams.json   per-request greedy output ids of the 48-request mix
+                      (6 layers, d 384, H8/Hkv4, d_ff 1024, max_len 512,
+                      block 16, 512 blocks, max_seqs 16, budget 1024, seed 0)
+                      plus the top-1 minus top-2 logit margin of each emitted
+                      token, and the step count;
+  weights_sha256.json sha256 of every weight tensor for that model config and
+                      for the small invariance-test config;
+  small_streams.json  greedy streams of the 4 invariance prompts on the small
+                      engine (2 layers, d 64, H4/Hkv2, d_ff 128).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+
+REF = "/root/reference"
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REF)
+
+from vllmlite.config import CacheConfig, EngineConfig, ModelConfig, SchedulerConfig  # noqa: E402
+from vllmlite.engine import LLMEngine  # noqa: E402
+from vllmlite.model import Layer, TinyLlama  # noqa: E402
+from vllmlite.sequence import SamplingParams  # noqa: E402
+from bench.bench import make_workload  # noqa: E402
+
+
+def weight_hashes(mc):
+    m = TinyLlama(mc, 16)
+    out = {"tok_emb": hashlib.sha256(m.tok_emb.tobytes()).hexdigest(),
+           "lm_head": hashlib.sha256(m.lm_head.tobytes()).hexdigest(),
+           "final_norm": hashlib.sha256(m.final_norm.tobytes()).hexdigest()}
+    for i, layer in enumerate(m.layers):
+        for name in Layer.__slots__:
+            out[f"layers.{i}.{name}"] = hashlib.sha256(getattr(layer, name).tobytes()).hexdigest()
+    return out
+
+
+def run_with_margins(engine, reqs):
+    """Drive the engine; record each emitted token's top1-top2 logit margin."""
+    margins = {rid: [] for rid, _, _ in reqs}
+    real_execute = engine.runner.execute
+    captured = {}
+
+    def execute(sched):
+        logits, rows = real_execute(sched)
+        captured["sched"], captured["logits"], captured["rows"] = sched, logits, rows
+        return logits, rows
+
+    engine.runner.execute = execute
+    for rid, ids, params in reqs:
+        engine.add_request(params=params, request_id=rid, prompt_token_ids=ids)
+    while engine.has_work:
+        before = {rid: len(s.output_token_ids) for rid, s in engine.seqs.items()}
+        engine.step()
+        sched = captured.get("sched")
+        if sched is None:
+            continue
+        for i, item in enumerate(sched.scheduled):
+            seq = item.seq
+            if len(seq.output_token_ids) > before[seq.request_id]:
+                row0, count = captured["rows"][i]
+                row = np.sort(captured["logits"][row0 + count - 1].astype(np.float64))
+                margins[seq.request_id].append(float(row[-1] - row[-2]))
+        captured.clear()
+    return margins
+
+
+def main():
+    mc = ModelConfig(n_layers=6, n_heads=8, n_kv_heads=4, d_model=384, d_ff=1024,
+                     vocab_size=261, max_seq_len=512)
+    cc = CacheConfig(block_size=16, num_blocks=512, enable_prefix_caching=False)
+    sc = SchedulerConfig(max_seqs=16, max_batched_tokens=1024)
+    reqs = make_workload(48, np.random.default_rng(0), 16, 256, 16, 192, 0)
+    eng = LLMEngine(EngineConfig(model=mc, cache=cc, scheduler=sc))
+    margins = run_with_margins(eng, reqs)
+    streams = {rid: [int(t) for t in eng.seqs[rid].output_token_ids] for rid, _, _ in reqs}
+    prompts = {rid: [int(t) for t in ids] for rid, ids, _ in reqs}
+    with open(os.path.join(HERE, "cfg0_streams.json"), "w") as f:
+        json.dump({"steps": eng.total_steps, "prompts": prompts, "streams": streams,
+                   "margins": {k: [round(x, 6) for x in v] for k, v in margins.items()}}, f)
+
+    small = ModelConfig(n_layers=2, n_heads=4, n_kv_heads=2, d_model=64, d_ff=128, max_seq_len=512)
+    with open(os.path.join(HERE, "weights_sha256.json"), "w") as f:
+        json.dump({"cfg0": weight_hashes(mc), "small": weight_hashes(small)}, f, indent=0)
+
+    prompts4 = ["the quick brown fox jumps over", "a",
+                "systems programming is mostly about memory and never about", "hello"]
+    e2 = LLMEngine(EngineConfig(
+        model=ModelConfig(n_layers=2, n_heads=4, n_kv_heads=2, d_model=64, d_ff=128, max_seq_len=512),
+        cache=CacheConfig(block_size=16, num_blocks=512, enable_prefix_caching=False),
+        scheduler=SchedulerConfig(max_seqs=8, max_batched_tokens=1024)))
+    p = SamplingParams(max_tokens=20, temperature=0.0, ignore_eos=True)
+    ids = [e2.add_request(x, p) for x in prompts4]
+    while e2.has_work:
+        e2.step()
+    with open(os.path.join(HERE, "small_streams.json"), "w") as f:
+        json.dump({"prompts": prompts4, "max_tokens": 20,
+                   "streams": [e2.seqs[i].output_token_ids for i in ids]}, f)
+    print("wrote fixtures; cfg0 steps", eng.total_steps,
+          "min margin", min(min(v) for v in margins.values() if v))
+
+
+if __name__ == "__main__":
+    main()

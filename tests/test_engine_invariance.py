@@ -1,0 +1,156 @@
+"""Greedy output must not depend on paging, chunking, batching, prefix caching
+or preemption (the reference's tests/test_engine.py:57-204), here on the
+restated caller side driving the NumPy oracle runner. The expected streams are
+the reference's own, from tests/golden/small_streams.json."""
+
+import json
+import os
+
+import pytest
+
+from vllmlite_amd.sequence import SamplingParams
+
+from helpers import PROMPTS, build, run
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden", "small_streams.json")
+
+
+def reference():
+    with open(GOLD) as f:
+        g = json.load(f)
+    assert g["prompts"] == PROMPTS
+    return g["streams"]
+
+
+def test_default_engine_matches_reference_streams():
+    assert run(build(), PROMPTS, check_counts=True) == reference()
+
+
+@pytest.mark.parametrize("block_size", [1, 4, 16, 64])
+def test_block_size_does_not_change_output(block_size):
+    assert run(build(block_size=block_size), PROMPTS) == reference()
+
+
+def test_prefix_caching_does_not_change_output():
+    assert run(build(prefix_cache=True), PROMPTS, check_counts=True) == reference()
+
+
+@pytest.mark.parametrize("max_batched", [8, 33, 64, 4096])
+def test_chunked_prefill_does_not_change_output(max_batched):
+    assert run(build(max_batched=max_batched), PROMPTS) == reference()
+
+
+def test_no_chunked_prefill_matches():
+    assert run(build(chunked=False, max_batched=4096), PROMPTS) == reference()
+
+
+@pytest.mark.parametrize("max_seqs", [1, 2, 3, 8])
+def test_batch_composition_does_not_change_output(max_seqs):
+    assert run(build(max_seqs=max_seqs), PROMPTS) == reference()
+
+
+def test_single_request_matches_batched():
+    assert [run(build(), [p])[0] for p in PROMPTS] == reference()
+
+
+def test_preemption_preserves_output():
+    engine = build(block_size=4, num_blocks=24, max_seqs=8, prefix_cache=False)
+    got = run(engine, PROMPTS, check_counts=True)
+    assert engine.scheduler.total_preemptions > 0
+    assert got == reference()
+
+
+def test_preemption_with_prefix_cache_preserves_output():
+    engine = build(block_size=4, num_blocks=24, max_seqs=8, prefix_cache=True)
+    got = run(engine, PROMPTS, check_counts=True)
+    assert engine.scheduler.total_preemptions > 0
+    assert got == reference()
+
+
+def test_all_blocks_returned_when_idle():
+    engine = build(prefix_cache=False)
+    run(engine, PROMPTS)
+    a = engine.scheduler.blocks.allocator
+    assert a.num_free == a.num_blocks
+    assert all(b.is_free for b in a.blocks)
+
+
+def test_prefix_cache_hits_on_repeated_prompt():
+    engine = build(block_size=4, prefix_cache=True)
+    long = "the same long system prompt that two requests happen to share, word for word"
+    run(engine, [long + " one"], max_tokens=4, check_counts=True)
+    run(engine, [long + " two"], max_tokens=4, check_counts=True)
+    assert engine.scheduler.blocks.stats()["prefix_hit_rate"] > 0
+    assert engine.seqs["req-1"].cached_prefix_tokens >= len(long) - 8
+
+
+def test_prefix_cache_only_reuses_a_genuinely_matching_prefix():
+    engine = build(block_size=4, prefix_cache=True)
+    run(engine, ["aaaaaaaaaaaaaaaaaaaaaaaa"], max_tokens=4)
+    run(engine, ["bbbbbbbbbbbbbbbbbbbbbbbb"], max_tokens=4)
+    assert engine.seqs["req-1"].cached_prefix_tokens == 0
+
+
+def test_max_tokens_is_respected():
+    engine = build()
+    rid = engine.add_request("hello there", SamplingParams(max_tokens=7, temperature=0.0, ignore_eos=True))
+    while engine.has_work:
+        engine.step()
+    assert len(engine.seqs[rid].output_token_ids) == 7
+    assert engine.seqs[rid].stop_reason == "length"
+
+
+def test_stop_string_truncates_text():
+    engine = build()
+    rid = engine.add_request("hello", SamplingParams(max_tokens=40, temperature=0.0, ignore_eos=True))
+    while engine.has_work:
+        engine.step()
+    full = engine.get_text(rid)
+    assert len(full) > 3
+    stop_at = full[2:4]
+    e2 = build()
+    rid2 = e2.add_request("hello", SamplingParams(max_tokens=40, temperature=0.0,
+                                                  ignore_eos=True, stop=[stop_at]))
+    while e2.has_work:
+        e2.step()
+    assert stop_at not in e2.get_text(rid2)
+    assert e2.seqs[rid2].stop_reason == "stop"
+
+
+def test_abort_frees_the_blocks():
+    engine = build()
+    rid = engine.add_request("hello there friend", SamplingParams(max_tokens=50, temperature=0.0, ignore_eos=True))
+    engine.step()
+    engine.step()
+    assert engine.abort(rid)
+    assert not engine.has_work
+    a = engine.scheduler.blocks.allocator
+    assert a.num_free == a.num_blocks
+
+
+def test_prompt_larger_than_cache_is_rejected_not_hung():
+    engine = build(block_size=4, num_blocks=4, max_seqs=2)
+    rid = engine.add_request("x" * 400, SamplingParams(max_tokens=5, temperature=0.0, ignore_eos=True))
+    outs = []
+    for _ in range(50):
+        outs += engine.step()
+        if not engine.has_work:
+            break
+    assert not engine.has_work
+    assert any(o.request_id == rid and o.finished for o in outs)
+
+
+def test_seeded_sampling_is_reproducible():
+    a, b = build(), build()
+    p = SamplingParams(max_tokens=16, temperature=0.9, top_p=0.95, seed=7, ignore_eos=True)
+    ra, rb = a.add_request("hello", p), b.add_request("hello", p)
+    while a.has_work:
+        a.step()
+    while b.has_work:
+        b.step()
+    assert a.seqs[ra].output_token_ids == b.seqs[rb].output_token_ids
+
+
+def test_empty_token_list_rejected():
+    with pytest.raises(ValueError):
+        build().add_request(params=SamplingParams(), prompt_token_ids=[])
