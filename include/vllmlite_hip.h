@@ -1,0 +1,148 @@
+/*
+ * C ABI of the MI355X (gfx950) ragged paged-attention step.
+ *
+ * Conventions shared by every entry point:
+ *   - pointers are device pointers unless the parameter name ends in _host;
+ *   - `stream` is a hipStream_t (NULL = the null stream); work is enqueued
+ *     asynchronously and nothing synchronises;
+ *   - no entry point allocates device memory; scratch space is passed in as
+ *     `workspace` / `workspace_bytes`;
+ *   - the return value is 0 (VL_OK), a negative VL_E* argument error, or a
+ *     positive hipError_t; vl_last_error() returns the message of the last
+ *     failure on the calling thread. Nothing throws across this boundary.
+ *   - dtype is VL_DTYPE_F32 (float) or VL_DTYPE_BF16 (raw bfloat16 bits).
+ *
+ * Cache layout is the reference's (vllmlite/runner.py:41-44): one tensor per
+ * layer and per K/V of shape [num_slots, num_kv_heads, head_dim], where slot
+ * = block_id * block_size + offset (vllmlite/block.py:154-156).
+ */
+#ifndef VLLMLITE_HIP_H
+#define VLLMLITE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VL_OK 0
+#define VL_EINVAL (-1)
+#define VL_DTYPE_F32 0
+#define VL_DTYPE_BF16 1
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* vl_last_error(void);
+
+/* ABI revision of this library; bumped when a signature changes. */
+int vl_abi_version(void);
+
+/*
+ * K1 reshape-and-cache. Replaces write_kv (vllmlite/attention.py:47-49) as
+ * called per sequence per layer at vllmlite/model.py:109:
+ *   key_cache[slot_mapping[t]] = key[t]; value_cache[slot_mapping[t]] = value[t]
+ * for t < num_tokens. key/value rows are [num_kv_heads, head_dim] contiguous,
+ * `key_stride`/`value_stride` elements apart. A negative slot skips the token.
+ * Bit-exact copy.
+ */
+int vl_reshape_and_cache(const void* key, const void* value, int64_t key_stride,
+                         int64_t value_stride, void* key_cache, void* value_cache,
+                         const int32_t* slot_mapping, int64_t num_tokens, int num_kv_heads,
+                         int head_dim, int dtype, void* stream);
+
+/*
+ * K3 copy-on-write block copy. Replaces NumpyRunner._do_cow
+ * (vllmlite/runner.py:54-60): for each pair (src, dst) of `block_pairs`
+ * [num_pairs, 2] and each layer l < num_layers, copies block_elems elements
+ * from base + l*layer_stride + src*block_elems to ... + dst*block_elems, for
+ * the K and the V cache. Pairs are processed in parallel, which equals the
+ * reference's in-order loop because no dst is another pair's src and dsts are
+ * distinct (fresh blocks, vllmlite/block_manager.py:77-85); the caller must
+ * guarantee that. Bit-exact copy.
+ */
+int vl_copy_blocks(void* key_cache, void* value_cache, const int32_t* block_pairs, int num_pairs,
+                   int num_layers, int64_t layer_stride, int64_t block_elems, int dtype,
+                   void* stream);
+
+/*
+ * Workspace bytes vl_paged_attention works best with for this batch shape.
+ * Any size >= vl_paged_attention_min_workspace() is correct: with less room
+ * the kernel splits long contexts into fewer partitions.
+ */
+size_t vl_paged_attention_workspace_size(int num_seqs, int num_tokens, int num_heads,
+                                         int head_dim, int max_context_len);
+size_t vl_paged_attention_min_workspace(int num_seqs);
+
+/*
+ * K2 ragged paged attention, decode + chunked prefill + speculative verify in
+ * one call. Replaces paged_attention (vllmlite/attention.py:59-98) called per
+ * sequence at vllmlite/model.py:107-112. Sequence i owns query tokens
+ * [query_start_loc[i], query_start_loc[i+1]) of `query` [num_tokens, num_heads,
+ * head_dim] (rows `query_stride` elements apart) and seq_lens[i] cached tokens
+ * (this step's K/V already written) reached through block_tables[i,
+ * 0..ceil(seq_lens[i]/block_size)). Query j of a sequence with q_len tokens
+ * sits at position seq_lens[i] - q_len + j and attends keys 0..position
+ * (causal; a single query sees the whole context). Head h reads KV head
+ * h / (num_heads / num_kv_heads). out [num_tokens, num_heads, head_dim],
+ * contiguous, dtype of the query. Accumulation is fp32.
+ */
+int vl_paged_attention(void* out, const void* query, int64_t query_stride, const void* key_cache,
+                       const void* value_cache, const int32_t* block_tables,
+                       int block_table_stride, const int32_t* seq_lens,
+                       const int32_t* query_start_loc, int num_seqs, int num_tokens,
+                       int num_heads, int num_kv_heads, int head_dim, int block_size,
+                       float scale, int dtype, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/*
+ * K4a RMSNorm, optionally fused with the residual add that precedes it
+ * (vllmlite/model.py:17-19 used at 96, 116, 119):
+ *   if residual != NULL: residual[r] += x[r] (x = residual afterwards)
+ *   out[r] = x[r] / sqrt(mean(x[r]^2) + eps) * weight
+ * rows of `dim` floats, fp32 only.
+ */
+int vl_rms_norm(float* out, float* residual, const float* x, const float* weight, int64_t rows,
+                int dim, float eps, void* stream);
+
+/*
+ * SwiGLU gate of the TinyLlama MLP (vllmlite/model.py:22-23, 117): for a
+ * fused projection gate_up [rows, 2*d_ff] = [h@w_gate | h@w_up],
+ * out[r, j] = silu(gate) * up with silu(x) = x / (1 + exp(-x)). fp32 only.
+ */
+int vl_silu_mul(float* out, const float* gate_up, int64_t rows, int d_ff, void* stream);
+
+/*
+ * K4b RoPE fused with the K/V scatter. For a fused projection row
+ * qkv[t] = [q (num_heads*head_dim) | k (num_kv_heads*head_dim) | v (...)]
+ * (`qkv_stride` elements apart), rotates interleaved (even, odd) pairs of q
+ * and k by cos/sin[positions[t]] (tables [max_pos, head_dim/2], fp32;
+ * vllmlite/attention.py:21-37), writes rotated q to q_out [num_tokens,
+ * num_heads, head_dim] and rotated k / plain v to the caches at
+ * slot_mapping[t] (vllmlite/attention.py:47-49). fp32 only.
+ */
+int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_out, float* key_cache,
+                      float* value_cache, const int32_t* positions, const int32_t* slot_mapping,
+                      const float* cos_table, const float* sin_table, int64_t num_tokens,
+                      int num_heads, int num_kv_heads, int head_dim, void* stream);
+
+/*
+ * K5 greedy acceptance. Replaces verify (vllmlite/speculative.py:86-100).
+ * Sequence i owns logits rows row_start[i] .. row_start[i] + num_drafts[i]
+ * (vocab floats each, `row_stride` apart) and drafts[i, 0..num_drafts[i]).
+ * picked[r] = argmax(row r), ties to the lowest index (numpy's argmax). Writes
+ * out_tokens[i, 0..max_drafts] = picked while it equals the draft, then the
+ * first mismatch (or, all matched, the bonus row's pick); unused entries -1;
+ * num_accepted[i] = drafts accepted. Integer outputs are exact.
+ */
+int vl_greedy_verify(const float* logits, int64_t row_stride, int vocab, const int32_t* row_start,
+                     const int32_t* num_drafts, const int32_t* drafts, int max_drafts,
+                     int32_t* out_tokens, int32_t* num_accepted, int num_seqs, void* stream);
+
+/* Row-wise argmax (ties to the lowest index) of rows x vocab fp32 logits. */
+int vl_argmax_rows(const float* logits, int64_t row_stride, int64_t rows, int vocab, int32_t* out,
+                   void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VLLMLITE_HIP_H */

@@ -1,0 +1,235 @@
+"""GPU parity of every kernel against the oracle, through the C ABI.
+
+Bars: copies and scatters bit-exact; fp32 attention rtol 1e-4 / atol 1e-5
+(the reference's own tolerance, tests/test_attention.py:57); bf16 attention
+rtol/atol 2e-2 against fp32 oracle math on bf16-rounded inputs; argmax and
+greedy acceptance exact.
+"""
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from batches import bf16_round, make_batch, oracle_attention  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+def ops():
+    from vllmlite_amd import ops as o
+    return o
+
+
+def dev(x, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    return t if dtype is None else t.to(dtype)
+
+
+def to_np(t):
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy()
+
+
+def run_attention(b, dtype, ws_bytes=None):
+    o = ops()
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    q = dev(b["q"], tdt)
+    kc, vc = dev(b["k_cache"], tdt), dev(b["v_cache"], tdt)
+    out = torch.empty_like(q)
+    S, T = len(b["seq_lens"]), b["q"].shape[0]
+    if ws_bytes is None:
+        ws_bytes = o.paged_attention_workspace_size(S, T, b["H"], b["D"], int(b["seq_lens"].max()))
+    ws = o.AttentionWorkspace().get(ws_bytes)
+    o.paged_attention(out, q, kc, vc, dev(b["block_tables"]), dev(b["seq_lens"]), dev(b["qsl"]),
+                      b["scale"], b["bs"], ws)
+    return to_np(out)
+
+
+def expected(b, dtype):
+    if dtype == "f32":
+        return oracle_attention(b)
+    return oracle_attention(b, bf16_round(b["q"]), bf16_round(b["k_cache"]), bf16_round(b["v_cache"]))
+
+
+def check(got, want, dtype):
+    assert np.isfinite(got).all()
+    if dtype == "f32":
+        np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
+    else:
+        np.testing.assert_allclose(got, want, rtol=2e-2, atol=2e-2)
+
+
+# -- the reference's grid (tests/test_attention.py:33-57), one sequence per launch
+@pytest.mark.parametrize("q_len", [1, 5, 17])
+@pytest.mark.parametrize("H,Hkv", [(4, 4), (8, 2), (6, 1)])
+@pytest.mark.parametrize("bs", [1, 4, 16])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_reference_grid(q_len, H, Hkv, bs, dtype):
+    b = make_batch([(q_len, 37)], H, Hkv, 8, bs, seed=0)
+    check(run_attention(b, dtype), expected(b, dtype), dtype)
+
+
+MIXED = [(1, 1), (1, 37), (5, 40), (17, 17), (1, 300), (64, 700), (3, 1025), (1, 16), (9, 33)]
+
+
+@pytest.mark.parametrize("shape", [(8, 4, 48), (32, 8, 128), (4, 2, 16), (6, 3, 64)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_mixed_prefill_decode_one_launch(shape, dtype):
+    H, Hkv, D = shape
+    b = make_batch(MIXED, H, Hkv, D, 16, seed=1)
+    check(run_attention(b, dtype), expected(b, dtype), dtype)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_long_context_split_and_small_workspace(dtype):
+    b = make_batch([(1, 5000), (4, 3000), (1, 70)], 8, 2, 64, 16, seed=2)
+    want = expected(b, dtype)
+    check(run_attention(b, dtype), want, dtype)
+    # a workspace with room for the plan only: no context splitting at all
+    o = ops()
+    check(run_attention(b, dtype, ws_bytes=o.lib().vl_paged_attention_min_workspace(3)), want, dtype)
+
+
+def test_bad_arguments_raise():
+    o = ops()
+    b = make_batch([(1, 20)], 6, 3, 8, 4)
+    q = dev(b["q"])
+    kc = dev(b["k_cache"])
+    out = torch.empty_like(q)
+    ws = o.AttentionWorkspace().get(1 << 16)
+    with pytest.raises(ValueError):
+        o.paged_attention(out, q, kc, kc, dev(b["block_tables"]), dev(b["seq_lens"]),
+                          dev(b["qsl"][:1]), b["scale"], b["bs"], ws)
+    rc = o.lib().vl_paged_attention(None, None, 0, None, None, None, 0, None, None, 1, 1, 6, 4, 8,
+                                    4, 1.0, 0, None, 0, None)
+    assert rc == -1 and b"multiple" in o.lib().vl_last_error()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_reshape_and_cache_bit_exact(dtype):
+    from oracle.attention import write_kv
+    o = ops()
+    rng = np.random.default_rng(3)
+    T, Hkv, D, slots = 77, 4, 48, 500
+    qkv = torch.from_numpy(rng.standard_normal((T, (8 + 2 * Hkv) * D)).astype(np.float32)).to(dtype)
+    k = qkv[:, 8 * D:(8 + Hkv) * D].view(T, Hkv, D)
+    v = qkv[:, (8 + Hkv) * D:].view(T, Hkv, D)
+    slot = rng.permutation(slots)[:T].astype(np.int32)
+    kc = torch.from_numpy(rng.standard_normal((slots, Hkv, D)).astype(np.float32)).to(dtype)
+    vc = kc.clone() * 2
+    want_k, want_v = kc.clone().float().numpy(), vc.clone().float().numpy()
+    write_kv(want_k, want_v, k.float().numpy(), v.float().numpy(), slot)
+    dqkv = qkv.cuda()
+    dk = dqkv[:, 8 * D:(8 + Hkv) * D].view(T, Hkv, D)
+    dv = dqkv[:, (8 + Hkv) * D:].view(T, Hkv, D)
+    dkc, dvc = kc.cuda(), vc.cuda()
+    o.reshape_and_cache(dk, dv, dkc, dvc, dev(slot))
+    assert np.array_equal(to_np(dkc), want_k) and np.array_equal(to_np(dvc), want_v)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_copy_blocks_bit_exact(dtype):
+    from oracle.runner import NumpyRunner
+    from vllmlite_amd.config import CacheConfig, ModelConfig
+    o = ops()
+    mc = ModelConfig(n_layers=3, n_heads=8, n_kv_heads=4, d_model=384, d_ff=64, max_seq_len=64)
+    cc = CacheConfig(block_size=16, num_blocks=100)
+    r = NumpyRunner(mc, cc)
+    rng = np.random.default_rng(4)
+    r.cache_k[...] = rng.standard_normal(r.cache_k.shape)
+    r.cache_v[...] = rng.standard_normal(r.cache_v.shape)
+    r.cache_k[...] = torch.from_numpy(r.cache_k).to(dtype).float().numpy()
+    r.cache_v[...] = torch.from_numpy(r.cache_v).to(dtype).float().numpy()
+    dk, dv = dev(r.cache_k, dtype), dev(r.cache_v, dtype)
+    # 48 pairs, several sharing a source, destinations distinct and never a source
+    srcs = rng.integers(0, 20, size=48)
+    dsts = 20 + rng.permutation(80)[:48]
+    pairs = [(int(s), int(d)) for s, d in zip(srcs, dsts)]
+    r.do_cow(pairs)
+    o.copy_blocks(dk, dv, dev(np.array(pairs, np.int32)), 16)
+    assert np.array_equal(to_np(dk), r.cache_k) and np.array_equal(to_np(dv), r.cache_v)
+
+
+def test_rms_norm_and_residual():
+    from oracle.model import rms_norm
+    o = ops()
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((37, 384)).astype(np.float32)
+    res = rng.standard_normal((37, 384)).astype(np.float32)
+    w = rng.standard_normal(384).astype(np.float32)
+    out = torch.empty(37, 384, device="cuda")
+    dres = dev(res)
+    o.rms_norm(out, dev(x), dev(w), 1e-5, residual=dres)
+    np.testing.assert_array_equal(to_np(dres), res + x)
+    np.testing.assert_allclose(to_np(out), rms_norm(res + x, w), rtol=2e-6, atol=1e-6)
+
+
+def test_silu_mul():
+    from oracle.model import silu
+    o = ops()
+    rng = np.random.default_rng(6)
+    gu = (rng.standard_normal((19, 2 * 1024)) * 4).astype(np.float32)
+    out = torch.empty(19, 1024, device="cuda")
+    o.silu_mul(out, dev(gu))
+    np.testing.assert_allclose(to_np(out), silu(gu[:, :1024]) * gu[:, 1024:], rtol=2e-6, atol=1e-7)
+
+
+def test_rope_and_cache_matches_oracle():
+    from oracle.attention import apply_rope, build_rope
+    o = ops()
+    rng = np.random.default_rng(7)
+    T, H, Hkv, D = 29, 8, 4, 48
+    qkv = rng.standard_normal((T, (H + 2 * Hkv) * D)).astype(np.float32)
+    pos = rng.integers(0, 512, size=T).astype(np.int32)
+    slots = rng.permutation(300)[:T].astype(np.int32)
+    cos, sin = build_rope(D, 512)
+    kc = torch.zeros(300, Hkv, D, device="cuda")
+    vc = torch.zeros(300, Hkv, D, device="cuda")
+    qo = torch.empty(T, H, D, device="cuda")
+    o.rope_and_cache(dev(qkv), qo, kc, vc, dev(pos), dev(slots), dev(cos), dev(sin), H, Hkv, D)
+    q = qkv[:, :H * D].reshape(T, H, D)
+    k = qkv[:, H * D:(H + Hkv) * D].reshape(T, Hkv, D)
+    v = qkv[:, (H + Hkv) * D:].reshape(T, Hkv, D)
+    np.testing.assert_array_equal(to_np(qo), apply_rope(q, pos, cos, sin))
+    np.testing.assert_array_equal(to_np(kc)[slots], apply_rope(k, pos, cos, sin))
+    np.testing.assert_array_equal(to_np(vc)[slots], v)
+
+
+def test_argmax_rows_numpy_ties_and_nan():
+    o = ops()
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((64, 32000)).astype(np.float32)
+    x[3, [5, 900, 31999]] = 50.0            # tie -> lowest index
+    x[4, [7, 8]] = np.nan                    # first NaN wins
+    x[5, :] = -np.inf
+    x[6, -1] = 1e30
+    out = torch.empty(64, dtype=torch.int32, device="cuda")
+    o.argmax_rows(dev(x), out)
+    assert to_np(out).astype(np.int64).tolist() == np.argmax(x, axis=-1).tolist()
+
+
+def test_greedy_verify_matches_oracle():
+    from oracle.greedy import verify
+    o = ops()
+    rng = np.random.default_rng(9)
+    S, K, V = 64, 4, 32000
+    nd = rng.integers(0, K + 1, size=S).astype(np.int32)
+    rows = nd + 1
+    row_start = np.zeros(S, np.int32)
+    row_start[1:] = np.cumsum(rows)[:-1]
+    logits = rng.standard_normal((int(rows.sum()), V)).astype(np.float32)
+    drafts = np.zeros((S, K), np.int32)
+    for s in range(S):
+        acc = int(rng.integers(0, nd[s] + 1))
+        for r in range(nd[s]):
+            best = int(np.argmax(logits[row_start[s] + r]))
+            drafts[s, r] = best if r < acc else (best + 1) % V
+    out = torch.empty(S, K + 1, dtype=torch.int32, device="cuda")
+    nacc = torch.empty(S, dtype=torch.int32, device="cuda")
+    o.greedy_verify(dev(logits), dev(row_start), dev(nd), dev(drafts), out, nacc)
+    got, got_acc = to_np(out).astype(np.int64), to_np(nacc).astype(np.int64)
+    for s in range(S):
+        toks, acc = verify(logits[row_start[s]:row_start[s] + rows[s]], list(drafts[s, :nd[s]]))
+        assert got_acc[s] == acc
+        assert got[s, :len(toks)].tolist() == toks and (got[s, len(toks):] == -1).all()

@@ -1,0 +1,184 @@
+// K1 reshape-and-cache, K3 copy-on-write block copy, K4b RoPE + scatter.
+//
+// All three are pure data movement over the flat per-layer cache
+// [num_slots, num_kv_heads, head_dim]. They are HBM-bound byte copies: each
+// workgroup moves whole rows with the widest aligned vector the operands allow.
+#include "vl_common.h"
+
+namespace {
+
+template <typename V>
+__global__ void __launch_bounds__(256) scatter_rows_kernel(
+    const char* __restrict__ key, const char* __restrict__ value, int64_t key_stride_b,
+    int64_t value_stride_b, char* __restrict__ kc, char* __restrict__ vc,
+    const int32_t* __restrict__ slots, int64_t num_tokens, int nvec) {
+  for (int64_t t = blockIdx.x; t < num_tokens; t += gridDim.x) {
+    const int slot = slots[t];
+    if (slot < 0) continue;
+    const int64_t row_b = (int64_t)nvec * sizeof(V);
+    const V* ks = reinterpret_cast<const V*>(key + t * key_stride_b);
+    const V* vs = reinterpret_cast<const V*>(value + t * value_stride_b);
+    V* kd = reinterpret_cast<V*>(kc + (int64_t)slot * row_b);
+    V* vd = reinterpret_cast<V*>(vc + (int64_t)slot * row_b);
+    for (int i = threadIdx.x; i < nvec; i += blockDim.x) {
+      kd[i] = ks[i];
+      vd[i] = vs[i];
+    }
+  }
+}
+
+template <typename V>
+__global__ void __launch_bounds__(256) copy_blocks_kernel(char* __restrict__ kc,
+                                                          char* __restrict__ vc,
+                                                          const int32_t* __restrict__ pairs,
+                                                          int64_t layer_stride_b, int nvec) {
+  const int p = blockIdx.x;
+  const int layer = blockIdx.y;
+  char* base = (blockIdx.z == 0 ? kc : vc) + (int64_t)layer * layer_stride_b;
+  const int64_t blk_b = (int64_t)nvec * sizeof(V);
+  const V* src = reinterpret_cast<const V*>(base + (int64_t)pairs[2 * p] * blk_b);
+  V* dst = reinterpret_cast<V*>(base + (int64_t)pairs[2 * p + 1] * blk_b);
+  for (int i = threadIdx.x; i < nvec; i += blockDim.x) dst[i] = src[i];
+}
+
+inline bool aligned(const void* p, int64_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Interleaved-pair rotation with the reference's fp32 rounding: each product
+// is rounded, then the difference/sum (vllmlite/attention.py:35-36). Contraction
+// into fma is disabled so results match numpy's elementwise float32 math.
+__device__ __forceinline__ void rotate_pair(float e, float o, float c, float s, float* oe,
+                                            float* oo) {
+#pragma clang fp contract(off)
+  float ec = e * c, os = o * s, es = e * s, oc = o * c;
+  *oe = ec - os;
+  *oo = es + oc;
+}
+
+__global__ void __launch_bounds__(256) rope_and_cache_kernel(
+    const float* __restrict__ qkv, int64_t qkv_stride, float* __restrict__ q_out,
+    float* __restrict__ kc, float* __restrict__ vc, const int32_t* __restrict__ positions,
+    const int32_t* __restrict__ slots, const float* __restrict__ cos_t,
+    const float* __restrict__ sin_t, int64_t num_tokens, int nh, int nkv, int hd) {
+  const int half = hd >> 1;
+  const int q_pairs = nh * half;
+  const int k_pairs = nkv * half;
+  const int v_elems = nkv * hd;
+  for (int64_t t = blockIdx.x; t < num_tokens; t += gridDim.x) {
+    const float* row = qkv + t * qkv_stride;
+    const int pos = positions[t];
+    const int slot = slots[t];
+    const float* c = cos_t + (int64_t)pos * half;
+    const float* s = sin_t + (int64_t)pos * half;
+    for (int i = threadIdx.x; i < q_pairs + k_pairs; i += blockDim.x) {
+      const int pi = (i < q_pairs) ? i : i - q_pairs;
+      const int head = pi / half, pr = pi - head * half;
+      const float* src = (i < q_pairs ? row : row + nh * hd) + head * hd + 2 * pr;
+      float oe, oo;
+      rotate_pair(src[0], src[1], c[pr], s[pr], &oe, &oo);
+      float* dst = (i < q_pairs) ? q_out + t * (int64_t)nh * hd + head * hd + 2 * pr
+                                 : (slot >= 0 ? kc + (int64_t)slot * v_elems + head * hd + 2 * pr
+                                              : nullptr);
+      if (dst) {
+        dst[0] = oe;
+        dst[1] = oo;
+      }
+    }
+    if (slot >= 0) {
+      const float* vs = row + (nh + nkv) * hd;
+      float* vd = vc + (int64_t)slot * v_elems;
+      for (int i = threadIdx.x; i < v_elems; i += blockDim.x) vd[i] = vs[i];
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int vl_reshape_and_cache(const void* key, const void* value, int64_t key_stride,
+                                    int64_t value_stride, void* key_cache, void* value_cache,
+                                    const int32_t* slot_mapping, int64_t num_tokens,
+                                    int num_kv_heads, int head_dim, int dtype, void* stream) {
+  VL_CHECK_ARG(dtype == VL_DTYPE_F32 || dtype == VL_DTYPE_BF16, "bad dtype %d", dtype);
+  VL_CHECK_ARG(num_tokens >= 0 && num_kv_heads > 0 && head_dim > 0, "bad shape");
+  if (num_tokens == 0) return VL_OK;
+  VL_CHECK_ARG(key && value && key_cache && value_cache && slot_mapping, "null pointer");
+  const int es = dtype == VL_DTYPE_F32 ? 4 : 2;
+  const int64_t row_b = (int64_t)num_kv_heads * head_dim * es;
+  const int64_t ks_b = key_stride * es, vs_b = value_stride * es;
+  VL_CHECK_ARG(key_stride >= num_kv_heads * (int64_t)head_dim &&
+                   value_stride >= num_kv_heads * (int64_t)head_dim,
+               "row stride smaller than a row");
+  hipStream_t st = (hipStream_t)stream;
+  const int grid = (int)(num_tokens < 65536 ? num_tokens : 65536);
+  auto ok = [&](int64_t a) {
+    return row_b % a == 0 && ks_b % a == 0 && vs_b % a == 0 && aligned(key, a) &&
+           aligned(value, a) && aligned(key_cache, a) && aligned(value_cache, a);
+  };
+  if (ok(16)) {
+    const int nvec = (int)(row_b / 16);
+    scatter_rows_kernel<uint4><<<grid, nvec < 256 ? ((nvec + 63) / 64) * 64 : 256, 0, st>>>(
+        (const char*)key, (const char*)value, ks_b, vs_b, (char*)key_cache, (char*)value_cache,
+        slot_mapping, num_tokens, nvec);
+  } else if (ok(4)) {
+    const int nvec = (int)(row_b / 4);
+    scatter_rows_kernel<uint32_t><<<grid, 256, 0, st>>>(
+        (const char*)key, (const char*)value, ks_b, vs_b, (char*)key_cache, (char*)value_cache,
+        slot_mapping, num_tokens, nvec);
+  } else {
+    VL_CHECK_ARG(ok(2), "operands not 2-byte aligned");
+    const int nvec = (int)(row_b / 2);
+    scatter_rows_kernel<uint16_t><<<grid, 256, 0, st>>>(
+        (const char*)key, (const char*)value, ks_b, vs_b, (char*)key_cache, (char*)value_cache,
+        slot_mapping, num_tokens, nvec);
+  }
+  VL_CHECK_LAUNCH();
+  return VL_OK;
+}
+
+extern "C" int vl_copy_blocks(void* key_cache, void* value_cache, const int32_t* block_pairs,
+                              int num_pairs, int num_layers, int64_t layer_stride,
+                              int64_t block_elems, int dtype, void* stream) {
+  VL_CHECK_ARG(dtype == VL_DTYPE_F32 || dtype == VL_DTYPE_BF16, "bad dtype %d", dtype);
+  VL_CHECK_ARG(num_pairs >= 0 && num_layers > 0 && block_elems > 0 && layer_stride >= 0,
+               "bad shape");
+  VL_CHECK_ARG(num_layers <= 65535, "too many layers");
+  if (num_pairs == 0) return VL_OK;
+  VL_CHECK_ARG(key_cache && value_cache && block_pairs, "null pointer");
+  const int es = dtype == VL_DTYPE_F32 ? 4 : 2;
+  const int64_t blk_b = block_elems * es, ls_b = layer_stride * es;
+  hipStream_t st = (hipStream_t)stream;
+  dim3 grid(num_pairs, num_layers, 2);
+  if (blk_b % 16 == 0 && ls_b % 16 == 0 && aligned(key_cache, 16) && aligned(value_cache, 16)) {
+    copy_blocks_kernel<uint4><<<grid, 256, 0, st>>>((char*)key_cache, (char*)value_cache,
+                                                    block_pairs, ls_b, (int)(blk_b / 16));
+  } else if (blk_b % 4 == 0 && ls_b % 4 == 0 && aligned(key_cache, 4) && aligned(value_cache, 4)) {
+    copy_blocks_kernel<uint32_t><<<grid, 256, 0, st>>>((char*)key_cache, (char*)value_cache,
+                                                       block_pairs, ls_b, (int)(blk_b / 4));
+  } else {
+    copy_blocks_kernel<uint16_t><<<grid, 256, 0, st>>>((char*)key_cache, (char*)value_cache,
+                                                       block_pairs, ls_b, (int)(blk_b / 2));
+  }
+  VL_CHECK_LAUNCH();
+  return VL_OK;
+}
+
+extern "C" int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_out,
+                                 float* key_cache, float* value_cache, const int32_t* positions,
+                                 const int32_t* slot_mapping, const float* cos_table,
+                                 const float* sin_table, int64_t num_tokens, int num_heads,
+                                 int num_kv_heads, int head_dim, void* stream) {
+  VL_CHECK_ARG(num_tokens >= 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0 &&
+                   head_dim % 2 == 0,
+               "bad shape");
+  VL_CHECK_ARG(qkv_stride >= (int64_t)(num_heads + 2 * num_kv_heads) * head_dim,
+               "qkv row stride too small");
+  if (num_tokens == 0) return VL_OK;
+  VL_CHECK_ARG(qkv && q_out && key_cache && value_cache && positions && slot_mapping &&
+                   cos_table && sin_table,
+               "null pointer");
+  const int grid = (int)(num_tokens < 65536 ? num_tokens : 65536);
+  rope_and_cache_kernel<<<grid, 128, 0, (hipStream_t)stream>>>(
+      qkv, qkv_stride, q_out, key_cache, value_cache, positions, slot_mapping, cos_table,
+      sin_table, num_tokens, num_heads, num_kv_heads, head_dim);
+  VL_CHECK_LAUNCH();
+  return VL_OK;
+}

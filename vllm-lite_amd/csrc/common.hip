@@ -1,0 +1,31 @@
+// Error reporting and device queries shared by all entry points.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "vl_common.h"
+
+static thread_local char g_err[512] = "";
+
+void vl_set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+extern "C" const char* vl_last_error(void) { return g_err; }
+
+extern "C" int vl_abi_version(void) { return 1; }
+
+int vl_num_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}

@@ -1,0 +1,87 @@
+// Shared device/host helpers for the gfx950 kernels of the paged-attention step.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/vllmlite_hip.h"
+
+// ---------------------------------------------------------------- errors ----
+// Every entry point returns 0, a negative VL_E* argument error, or a positive
+// hipError_t; the message of the last failure on the calling thread is kept
+// for vl_last_error().
+void vl_set_error(const char* fmt, ...);
+
+#define VL_CHECK_ARG(cond, ...)              \
+  do {                                       \
+    if (!(cond)) {                           \
+      vl_set_error(__VA_ARGS__);             \
+      return VL_EINVAL;                      \
+    }                                        \
+  } while (0)
+
+#define VL_CHECK_HIP(expr)                                                        \
+  do {                                                                            \
+    hipError_t e_ = (expr);                                                       \
+    if (e_ != hipSuccess) {                                                       \
+      vl_set_error("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, \
+                   __LINE__);                                                     \
+      return (int)e_;                                                             \
+    }                                                                             \
+  } while (0)
+
+#define VL_CHECK_LAUNCH() VL_CHECK_HIP(hipGetLastError())
+
+// Number of compute units of the current device (cached per device).
+int vl_num_cus();
+
+// ----------------------------------------------------------------- dtypes ---
+// bf16 is carried as its raw 16 bits (uint16_t) so that copies stay bit-exact.
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+
+// Round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Low / high bf16 of a packed pair as fp32.
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+template <typename T>
+struct Elem;
+template <>
+struct Elem<float> {
+  static __device__ __forceinline__ float load(const float* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void store(float* p, int64_t i, float v) { p[i] = v; }
+};
+template <>
+struct Elem<uint16_t> {
+  static __device__ __forceinline__ float load(const uint16_t* p, int64_t i) {
+    return bf16_to_f32(p[i]);
+  }
+  static __device__ __forceinline__ void store(uint16_t* p, int64_t i, float v) {
+    p[i] = f32_to_bf16(v);
+  }
+};
+
+// ------------------------------------------------------- wave reductions ----
+// 64-lane wavefront reductions through ds_swizzle-free shuffles.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__host__ __device__ __forceinline__ int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }

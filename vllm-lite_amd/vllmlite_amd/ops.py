@@ -1,0 +1,249 @@
+"""ctypes binding of the gfx950 C-ABI library (include/vllmlite_hip.h).
+
+Device memory and streams come from PyTorch-ROCm; every call passes raw device
+pointers and torch's current stream to the library. The library is loaded
+after `import torch` so that it binds the HIP runtime torch already loaded
+(both carry the soname libamdhip64.so.7). There is no fallback: if the
+library is missing, `lib()` raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import torch
+
+from .build import LIB_PATH
+
+F32, BF16 = 0, 1
+_c_void_p = ctypes.c_void_p
+_i32, _i64, _f32, _size = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
+
+# name -> (restype, argtypes); must list every function of include/vllmlite_hip.h
+SIGNATURES = {
+    "vl_last_error": (ctypes.c_char_p, []),
+    "vl_abi_version": (_i32, []),
+    "vl_reshape_and_cache": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
+                                    _c_void_p, _i64, _i32, _i32, _i32, _c_void_p]),
+    "vl_copy_blocks": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i64, _i64, _i32,
+                              _c_void_p]),
+    "vl_paged_attention_workspace_size": (_size, [_i32, _i32, _i32, _i32, _i32]),
+    "vl_paged_attention_min_workspace": (_size, [_i32]),
+    "vl_paged_attention": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
+                                  _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32,
+                                  _f32, _i32, _c_void_p, _size, _c_void_p]),
+    "vl_rms_norm": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _f32,
+                           _c_void_p]),
+    "vl_silu_mul": (_i32, [_c_void_p, _c_void_p, _i64, _i32, _c_void_p]),
+    "vl_rope_and_cache": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                 _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32,
+                                 _c_void_p]),
+    "vl_greedy_verify": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i32,
+                                _c_void_p, _c_void_p, _i32, _c_void_p]),
+    "vl_argmax_rows": (_i32, [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p]),
+}
+
+_LIB: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"HIP library not built: {LIB_PATH} is missing "
+                "(run `python -m vllmlite_amd.build` or __graft_entry__.build())")
+        handle = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = handle
+    return _LIB
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().vl_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return F32
+    if t.dtype == torch.bfloat16:
+        return BF16
+    raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _dev_i32(t: torch.Tensor, name: str) -> None:
+    _need(t.is_cuda and t.dtype == torch.int32 and t.is_contiguous(),
+          f"{name} must be a contiguous int32 device tensor")
+
+
+# ------------------------------------------------------------------ K1 -----
+def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, key_cache: torch.Tensor,
+                      value_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """key/value [T, Hkv, D] (rows may be strided), caches [slots, Hkv, D]."""
+    T, hkv, d = key.shape
+    _need(value.shape == key.shape, "key/value shapes differ")
+    _need(key_cache.shape[1:] == (hkv, d) and value_cache.shape == key_cache.shape,
+          "cache shape mismatch")
+    _need(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
+    for t in (key, value):
+        _need(t.stride(2) == 1 and t.stride(1) == d, "key/value rows must be [Hkv, D] contiguous")
+    _need(key.dtype == value.dtype == key_cache.dtype == value_cache.dtype, "dtype mismatch")
+    _dev_i32(slot_mapping, "slot_mapping")
+    _need(slot_mapping.numel() == T, "slot_mapping length != tokens")
+    _check(lib().vl_reshape_and_cache(_ptr(key), _ptr(value), key.stride(0), value.stride(0),
+                                      _ptr(key_cache), _ptr(value_cache), _ptr(slot_mapping), T,
+                                      hkv, d, _dtype_code(key), _stream()),
+           "vl_reshape_and_cache")
+
+
+# ------------------------------------------------------------------ K3 -----
+def copy_blocks(key_cache: torch.Tensor, value_cache: torch.Tensor, block_pairs: torch.Tensor,
+                block_size: int) -> None:
+    """Caches [L, slots, Hkv, D]; block_pairs int32 [n, 2] on the device."""
+    _need(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
+    _need(key_cache.shape == value_cache.shape and key_cache.dim() == 4, "cache shape mismatch")
+    _dev_i32(block_pairs, "block_pairs")
+    n = block_pairs.shape[0]
+    L, slots, hkv, d = key_cache.shape
+    _check(lib().vl_copy_blocks(_ptr(key_cache), _ptr(value_cache), _ptr(block_pairs), n, L,
+                                slots * hkv * d, block_size * hkv * d, _dtype_code(key_cache),
+                                _stream()),
+           "vl_copy_blocks")
+
+
+# ------------------------------------------------------------------ K2 -----
+class AttentionWorkspace:
+    """Reusable device scratch for paged_attention (grows on demand)."""
+
+    def __init__(self, device=None):
+        self.device = device
+        self.buf: Optional[torch.Tensor] = None
+
+    def get(self, nbytes: int) -> torch.Tensor:
+        nbytes = max(256, (int(nbytes) + 255) // 256 * 256)
+        if self.buf is None or self.buf.numel() < nbytes:
+            self.buf = torch.empty(nbytes, dtype=torch.uint8, device=self.device or "cuda")
+        return self.buf
+
+
+def paged_attention_workspace_size(num_seqs, num_tokens, num_heads, head_dim, max_context_len):
+    return int(lib().vl_paged_attention_workspace_size(num_seqs, num_tokens, num_heads, head_dim,
+                                                       max_context_len))
+
+
+def paged_attention(out: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
+                    value_cache: torch.Tensor, block_tables: torch.Tensor, seq_lens: torch.Tensor,
+                    query_start_loc: torch.Tensor, scale: float, block_size: int,
+                    workspace: torch.Tensor, max_context_len: Optional[int] = None) -> None:
+    """query [T, H, D] (token rows may be strided), caches [slots, Hkv, D],
+    block_tables int32 [S, W], seq_lens int32 [S], query_start_loc int32 [S+1]."""
+    T, H, D = query.shape
+    _need(query.stride(2) == 1 and query.stride(1) == D, "query rows must be [H, D] contiguous")
+    _need(out.shape == (T, H, D) and out.is_contiguous() and out.dtype == query.dtype,
+          "out must be a contiguous [T, H, D] tensor of the query dtype")
+    _need(key_cache.dim() == 3 and key_cache.shape == value_cache.shape and key_cache.shape[2] == D,
+          "cache shape mismatch")
+    _need(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
+    _need(key_cache.dtype == query.dtype == value_cache.dtype, "dtype mismatch")
+    hkv = key_cache.shape[1]
+    _need(H % hkv == 0, "num_heads must be a multiple of num_kv_heads")
+    for t, n in ((block_tables, "block_tables"), (seq_lens, "seq_lens"),
+                 (query_start_loc, "query_start_loc")):
+        _dev_i32(t, n)
+    S = seq_lens.numel()
+    _need(query_start_loc.numel() == S + 1 and block_tables.dim() == 2 and
+          block_tables.shape[0] == S, "metadata shapes disagree")
+    _need(workspace.is_cuda and workspace.data_ptr() % 256 == 0, "workspace must be 256-aligned")
+    _check(lib().vl_paged_attention(_ptr(out), _ptr(query), query.stride(0), _ptr(key_cache),
+                                    _ptr(value_cache), _ptr(block_tables), block_tables.stride(0),
+                                    _ptr(seq_lens), _ptr(query_start_loc), S, T, H, hkv, D,
+                                    block_size, float(scale), _dtype_code(query),
+                                    _ptr(workspace), workspace.numel() * workspace.element_size(),
+                                    _stream()),
+           "vl_paged_attention")
+
+
+# ------------------------------------------------------------------ K4 -----
+def rms_norm(out: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5,
+             residual: Optional[torch.Tensor] = None) -> None:
+    """fp32 rows; with `residual`, residual += x first and the sum is normalised."""
+    rows, dim = x.shape
+    for t in (out, x, weight) + ((residual,) if residual is not None else ()):
+        _need(t.is_contiguous() and t.dtype == torch.float32, "fp32 contiguous tensors required")
+    _need(out.shape == x.shape and weight.numel() == dim, "shape mismatch")
+    _need(residual is None or residual.shape == x.shape, "residual shape mismatch")
+    _check(lib().vl_rms_norm(_ptr(out), _ptr(residual), _ptr(x), _ptr(weight), rows, dim,
+                             float(eps), _stream()), "vl_rms_norm")
+
+
+def silu_mul(out: torch.Tensor, gate_up: torch.Tensor) -> None:
+    rows, two_f = gate_up.shape
+    _need(out.shape == (rows, two_f // 2) and out.is_contiguous() and gate_up.is_contiguous(),
+          "shape mismatch")
+    _check(lib().vl_silu_mul(_ptr(out), _ptr(gate_up), rows, two_f // 2, _stream()),
+           "vl_silu_mul")
+
+
+def rope_and_cache(qkv: torch.Tensor, q_out: torch.Tensor, key_cache: torch.Tensor,
+                   value_cache: torch.Tensor, positions: torch.Tensor, slot_mapping: torch.Tensor,
+                   cos: torch.Tensor, sin: torch.Tensor, num_heads: int, num_kv_heads: int,
+                   head_dim: int) -> None:
+    T = qkv.shape[0]
+    _need(qkv.stride(1) == 1 and qkv.shape[1] >= (num_heads + 2 * num_kv_heads) * head_dim,
+          "qkv rows must hold q|k|v")
+    _need(q_out.shape == (T, num_heads, head_dim) and q_out.is_contiguous(), "q_out shape")
+    _need(key_cache.shape[1:] == (num_kv_heads, head_dim) and key_cache.is_contiguous(),
+          "cache shape")
+    _dev_i32(positions, "positions")
+    _dev_i32(slot_mapping, "slot_mapping")
+    _need(cos.shape == sin.shape and cos.shape[1] == head_dim // 2, "rope table shape")
+    _check(lib().vl_rope_and_cache(_ptr(qkv), qkv.stride(0), _ptr(q_out), _ptr(key_cache),
+                                   _ptr(value_cache), _ptr(positions), _ptr(slot_mapping),
+                                   _ptr(cos), _ptr(sin), T, num_heads, num_kv_heads, head_dim,
+                                   _stream()), "vl_rope_and_cache")
+
+
+# ------------------------------------------------------------------ K5 -----
+def greedy_verify(logits: torch.Tensor, row_start: torch.Tensor, num_drafts: torch.Tensor,
+                  drafts: torch.Tensor, out_tokens: torch.Tensor,
+                  num_accepted: torch.Tensor) -> None:
+    """logits fp32 [R, V]; drafts int32 [S, K]; out_tokens int32 [S, K+1]."""
+    _need(logits.dtype == torch.float32 and logits.stride(1) == 1, "logits must be fp32 rows")
+    S, K = drafts.shape
+    for t, n in ((row_start, "row_start"), (num_drafts, "num_drafts"), (drafts, "drafts"),
+                 (out_tokens, "out_tokens"), (num_accepted, "num_accepted")):
+        _dev_i32(t, n)
+    _need(out_tokens.shape == (S, K + 1) and num_accepted.numel() == S and
+          row_start.numel() == S and num_drafts.numel() == S, "shape mismatch")
+    _check(lib().vl_greedy_verify(_ptr(logits), logits.stride(0), logits.shape[1],
+                                  _ptr(row_start), _ptr(num_drafts), _ptr(drafts), K,
+                                  _ptr(out_tokens), _ptr(num_accepted), S, _stream()),
+           "vl_greedy_verify")
+
+
+def argmax_rows(logits: torch.Tensor, out: torch.Tensor) -> None:
+    _need(logits.dtype == torch.float32 and logits.stride(1) == 1, "logits must be fp32 rows")
+    _dev_i32(out, "out")
+    _need(out.numel() == logits.shape[0], "out length")
+    _check(lib().vl_argmax_rows(_ptr(logits), logits.stride(0), logits.shape[0], logits.shape[1],
+                                _ptr(out), _stream()), "vl_argmax_rows")
