@@ -84,15 +84,39 @@ size_t vl_paged_attention_min_workspace(int num_seqs);
  * sits at position seq_lens[i] - q_len + j and attends keys 0..position
  * (causal; a single query sees the whole context). Head h reads KV head
  * h / (num_heads / num_kv_heads). out [num_tokens, num_heads, head_dim],
- * contiguous, dtype of the query. Accumulation is fp32.
+ * contiguous, dtype of the query. Accumulation is fp32. max_query_len is the
+ * caller's bound on the per-sequence query count (0 = unknown); with 1 the
+ * call launches only the decode kernel. A bound that is too small leaves the
+ * longer sequences' outputs unwritten (it never reads or writes out of bounds).
  */
 int vl_paged_attention(void* out, const void* query, int64_t query_stride, const void* key_cache,
                        const void* value_cache, const int32_t* block_tables,
                        int block_table_stride, const int32_t* seq_lens,
                        const int32_t* query_start_loc, int num_seqs, int num_tokens,
                        int num_heads, int num_kv_heads, int head_dim, int block_size,
-                       float scale, int dtype, void* workspace, size_t workspace_bytes,
-                       void* stream);
+                       float scale, int dtype, int max_query_len, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/*
+ * The two halves of vl_paged_attention, for callers that run several
+ * attention calls over the same batch (one per layer): _plan reads only
+ * seq_lens / query_start_loc and writes the work decomposition into the
+ * workspace; _run performs the attention using the plan currently in that
+ * workspace, which must come from a _plan call with the same lengths, head
+ * counts, head_dim, block_size, dtype and workspace size (stream-ordered before
+ * it). vl_paged_attention is _plan followed by _run.
+ */
+int vl_paged_attention_plan(const int32_t* seq_lens, const int32_t* query_start_loc,
+                            int num_seqs, int num_tokens, int num_heads, int num_kv_heads,
+                            int head_dim, int block_size, int dtype, void* workspace,
+                            size_t workspace_bytes, void* stream);
+int vl_paged_attention_run(void* out, const void* query, int64_t query_stride,
+                           const void* key_cache, const void* value_cache,
+                           const int32_t* block_tables, int block_table_stride,
+                           const int32_t* seq_lens, const int32_t* query_start_loc, int num_seqs,
+                           int num_tokens, int num_heads, int num_kv_heads, int head_dim,
+                           int block_size, float scale, int dtype, int max_query_len,
+                           void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * K4a RMSNorm, optionally fused with the residual add that precedes it

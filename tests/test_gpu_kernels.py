@@ -31,7 +31,7 @@ def to_np(t):
     return t.float().cpu().numpy()
 
 
-def run_attention(b, dtype, ws_bytes=None):
+def run_attention(b, dtype, ws_bytes=None, exact_max_q=True):
     o = ops()
     tdt = torch.float32 if dtype == "f32" else torch.bfloat16
     q = dev(b["q"], tdt)
@@ -41,8 +41,9 @@ def run_attention(b, dtype, ws_bytes=None):
     if ws_bytes is None:
         ws_bytes = o.paged_attention_workspace_size(S, T, b["H"], b["D"], int(b["seq_lens"].max()))
     ws = o.AttentionWorkspace().get(ws_bytes)
+    max_q = int(np.diff(b["qsl"]).max())
     o.paged_attention(out, q, kc, vc, dev(b["block_tables"]), dev(b["seq_lens"]), dev(b["qsl"]),
-                      b["scale"], b["bs"], ws)
+                      b["scale"], b["bs"], ws, max_query_len=max_q if exact_max_q else 0)
     return to_np(out)
 
 
@@ -102,7 +103,7 @@ def test_bad_arguments_raise():
         o.paged_attention(out, q, kc, kc, dev(b["block_tables"]), dev(b["seq_lens"]),
                           dev(b["qsl"][:1]), b["scale"], b["bs"], ws)
     rc = o.lib().vl_paged_attention(None, None, 0, None, None, None, 0, None, None, 1, 1, 6, 4, 8,
-                                    4, 1.0, 0, None, 0, None)
+                                    4, 1.0, 0, 0, None, 0, None)
     assert rc == -1 and b"multiple" in o.lib().vl_last_error()
 
 
@@ -233,3 +234,48 @@ def test_greedy_verify_matches_oracle():
         toks, acc = verify(logits[row_start[s]:row_start[s] + rows[s]], list(drafts[s, :nd[s]]))
         assert got_acc[s] == acc
         assert got[s, :len(toks)].tolist() == toks and (got[s, len(toks):] == -1).all()
+
+
+DECODE_CTX = [1, 5, 15, 16, 17, 100, 255, 256, 257, 1000, 4097, 64, 8192]
+
+
+@pytest.mark.parametrize("exact_max_q", [True, False])
+def test_bandwidth_decode_path_matches_oracle(exact_max_q):
+    """bf16 / D 128 / 32 heads over 8 KV heads / block 16: the bandwidth kernel."""
+    b = make_batch([(1, c) for c in DECODE_CTX], 32, 8, 128, 16, seed=11)
+    check(run_attention(b, "bf16", exact_max_q=exact_max_q), expected(b, "bf16"), "bf16")
+
+
+def test_bandwidth_decode_chunks_without_split():
+    """Workspace with no room for partials: each item loops over 256-token chunks."""
+    o = ops()
+    b = make_batch([(1, c) for c in (3000, 700, 257, 16)], 32, 8, 128, 16, seed=12)
+    got = run_attention(b, "bf16", ws_bytes=o.lib().vl_paged_attention_min_workspace(4))
+    check(got, expected(b, "bf16"), "bf16")
+
+
+def test_bandwidth_decode_with_16_kv_heads():
+    b = make_batch([(1, c) for c in (33, 600)], 64, 16, 128, 16, seed=13)
+    check(run_attention(b, "bf16"), expected(b, "bf16"), "bf16")
+
+
+def test_plan_once_run_per_layer():
+    """One plan serves several runs over different caches (one per layer)."""
+    o = ops()
+    b0 = make_batch([(1, 300), (7, 50), (1, 2000)], 32, 8, 128, 16, seed=20, num_blocks=200)
+    ws = o.AttentionWorkspace().get(o.paged_attention_workspace_size(3, 9, 32, 128, 2000))
+    bt, sl, qsl = dev(b0["block_tables"]), dev(b0["seq_lens"]), dev(b0["qsl"])
+    for layer in range(3):
+        rng = np.random.default_rng(100 + layer)
+        b = dict(b0)
+        b["q"] = rng.standard_normal(b0["q"].shape).astype(np.float32)
+        for name in ("k_cache", "v_cache"):
+            fresh = rng.standard_normal(b0[name].shape).astype(np.float32)
+            b[name] = np.where(np.isnan(b0[name]), np.nan, fresh).astype(np.float32)
+        q = dev(b["q"], torch.bfloat16)
+        kc, vc = dev(b["k_cache"], torch.bfloat16), dev(b["v_cache"], torch.bfloat16)
+        if layer == 0:
+            o.paged_attention_plan(q, kc, sl, qsl, 16, ws)
+        out = torch.empty_like(q)
+        o.paged_attention_run(out, q, kc, vc, bt, sl, qsl, b["scale"], 16, ws, max_query_len=7)
+        check(to_np(out), expected(b, "bf16"), "bf16")

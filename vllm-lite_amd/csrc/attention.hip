@@ -2,40 +2,55 @@
 // one call (vllmlite/attention.py:59-98 applied per sequence at
 // vllmlite/model.py:107-112).
 //
-// Three launches on the caller's stream, no host synchronisation:
-//  1. plan    one workgroup reads seq_lens / query_start_loc and writes, into
-//             the workspace, per-sequence work-item offsets, the number of
-//             context partitions and where split partials go. The partition
-//             length doubles until the split partials fit the workspace, so
-//             any workspace >= the minimum is correct.
-//  2. attend  a persistent grid walks the item list. Each item is one
-//             (sequence, query token, head, context partition); a wavefront
-//             streams the partition's keys 64 at a time through the block
-//             table with an online (running max / running sum) softmax.
-//  3. combine sequences whose context was split merge their partials with
-//             the usual max-rescaled log-sum-exp.
+// A call is a plan followed by a run, both on the caller's stream and without
+// host synchronisation:
+//  plan     one workgroup reads seq_lens / query_start_loc and writes into the
+//           workspace, per sequence, its work-item offsets, its number of
+//           context partitions and where split partials go. The partition
+//           length starts at 256 tokens and doubles until the split partials
+//           fit the workspace, so any workspace >= the minimum is correct.
+//           The plan depends only on the lengths, so one plan serves every
+//           layer of a step.
+//  run      decode sequences of the bf16 / head_dim 128 / 4-query-heads-per-
+//           KV-head / block-16 shape go to the bandwidth kernel (one
+//           wavefront per (sequence, partition, KV head), a 4-wave workgroup
+//           per 4 adjacent KV heads); everything else goes to the generic
+//           kernel (one wavefront per (sequence, query, head, partition)).
+//           Sequences whose context was split are merged by the combine
+//           kernel (max-rescaled log-sum-exp).
+//
+// Softmax runs in the base-2 domain: scores are pre-multiplied by
+// scale * log2(e) and exponentiated with exp2, which is the same function.
 #include "vl_common.h"
 
 namespace {
 
-constexpr int kHdrInts = 64;      // header: [0] n_items, [1] partition tokens, [2] split rows
+constexpr int kHdrInts = 64;  // [0] fast items [1] generic items [2] partition len [3] split rows
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxHeadDim = 256;
-constexpr int kSplitMaxQ = 16;    // only sequences with <= this many queries split their context
-constexpr int kPart0 = 256;       // first partition length tried by the planner
+constexpr int kSplitMaxQ = 16;  // only sequences with <= this many queries split their context
+constexpr int kPart0 = 256;     // first partition length tried by the planner
+constexpr float kLog2e = 1.4426950408889634f;
+
+// bandwidth-kernel shape
+constexpr int kFD = 128;   // head_dim
+constexpr int kFRep = 4;   // query heads per KV head
+constexpr int kFBs = 16;   // block size
+constexpr int kFChunk = 16;  // blocks per softmax chunk (256 tokens)
 
 struct Layout {
   int32_t* hdr;
-  int32_t* item_off;   // [S+1]
-  int32_t* nparts;     // [S]
-  int32_t* split_base; // [S] first partial row, or -1
-  float2* ml;          // [cap_rows] (running max, running sum)
-  float* po;           // [cap_rows, D] unnormalised partial outputs
+  int32_t* fast_off;    // [S+1] bandwidth-kernel workgroup items
+  int32_t* gen_off;     // [S+1] generic wavefront items
+  int32_t* nparts;      // [S]
+  int32_t* split_base;  // [S] first partial row, or -1
+  float2* ml;           // [cap_rows] (running max (log2 domain), running sum)
+  float* po;            // [cap_rows, D] unnormalised partial outputs
   int64_t cap_rows;
 };
 
 inline size_t plan_bytes(int S) {
-  size_t b = kHdrInts * 4 + (size_t)(3 * S + 1) * 4;
+  size_t b = kHdrInts * 4 + (size_t)(4 * S + 2) * 4;
   return (b + 255) & ~(size_t)255;
 }
 
@@ -43,15 +58,22 @@ inline Layout make_layout(void* ws, size_t bytes, int S, int D) {
   Layout L;
   char* p = (char*)ws;
   L.hdr = (int32_t*)p;
-  L.item_off = L.hdr + kHdrInts;
-  L.nparts = L.item_off + S + 1;
+  L.fast_off = L.hdr + kHdrInts;
+  L.gen_off = L.fast_off + S + 1;
+  L.nparts = L.gen_off + S + 1;
   L.split_base = L.nparts + S;
   const size_t pb = plan_bytes(S);
   const size_t per_row = (size_t)(D + 2) * 4;
-  L.cap_rows = bytes > pb ? (int64_t)((bytes - pb) / per_row) : 0;
+  // rows: 8-byte (m, l) pairs, then a 256-byte aligned [rows, D] float array
+  int64_t rows = bytes > pb + 256 ? (int64_t)((bytes - pb - 256) / per_row) : 0;
+  L.cap_rows = rows;
   L.ml = (float2*)(p + pb);
-  L.po = (float*)(p + pb + (size_t)L.cap_rows * 8);
+  L.po = (float*)(p + pb + (((size_t)rows * 8 + 255) & ~(size_t)255));
   return L;
+}
+
+inline bool fast_shape(int dtype, int H, int Hkv, int D, int bs) {
+  return dtype == VL_DTYPE_BF16 && D == kFD && bs == kFBs && Hkv % 4 == 0 && H == kFRep * Hkv;
 }
 
 __device__ __forceinline__ int upper_bound_le(const int32_t* a, int n, int x) {
@@ -83,10 +105,28 @@ __device__ int64_t block_exclusive_scan(int64_t v, int64_t* total) {
   return incl - v;
 }
 
+struct SeqWork {
+  int np;        // context partitions
+  int64_t fast;  // bandwidth-kernel workgroup items
+  int64_t gen;   // generic wavefront items
+  int64_t rows;  // split partial rows
+};
+
+__device__ __forceinline__ SeqWork seq_work(int q, int c, int P, int H, int Hkv, bool fast) {
+  SeqWork w;
+  w.np = (q > 0 && q <= kSplitMaxQ && c > P) ? (c + P - 1) / P : 1;
+  const bool bw = fast && q == 1 && c > 0;
+  w.fast = bw ? (int64_t)w.np * (Hkv / 4) : 0;
+  w.gen = bw ? 0 : (int64_t)max(q, 0) * H * w.np;
+  w.rows = w.np > 1 ? (int64_t)q * H * w.np : 0;
+  return w;
+}
+
 __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
-    const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H,
-    int64_t cap_rows, int32_t* __restrict__ hdr, int32_t* __restrict__ item_off,
-    int32_t* __restrict__ nparts, int32_t* __restrict__ split_base) {
+    const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H, int Hkv,
+    bool fast, int64_t cap_rows, int32_t* __restrict__ hdr, int32_t* __restrict__ fast_off,
+    int32_t* __restrict__ gen_off, int32_t* __restrict__ nparts,
+    int32_t* __restrict__ split_base) {
   __shared__ unsigned long long need;
   __shared__ int part_len;
   const int t = threadIdx.x;
@@ -98,10 +138,8 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     __syncthreads();
     const int P = part_len;
     unsigned long long mine = 0;
-    for (int i = t; i < S; i += kPlanThreads) {
-      const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
-      if (q > 0 && q <= kSplitMaxQ && c > P) mine += (unsigned long long)q * H * ((c + P - 1) / P);
-    }
+    for (int i = t; i < S; i += kPlanThreads)
+      mine += seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, H, Hkv, fast).rows;
     if (mine) atomicAdd(&need, mine);
     __syncthreads();
     const bool fits = need <= (unsigned long long)cap_rows || P >= (1 << 30);
@@ -111,50 +149,52 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     __syncthreads();
   }
   const int P = part_len;
-  // 2. per-sequence items and split rows, contiguous chunk of sequences per thread
+  // 2. offsets; every thread owns a contiguous chunk of sequences
   const int chunk = (S + kPlanThreads - 1) / kPlanThreads;
   const int s0 = min(S, t * chunk), s1 = min(S, s0 + chunk);
-  int64_t items = 0, rows = 0;
+  int64_t f = 0, g = 0, r = 0;
   for (int i = s0; i < s1; ++i) {
-    const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
-    const int np = (q > 0 && q <= kSplitMaxQ && c > P) ? (c + P - 1) / P : 1;
-    items += (int64_t)max(q, 0) * H * np;
-    if (np > 1) rows += (int64_t)q * H * np;
+    const SeqWork w = seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, H, Hkv, fast);
+    f += w.fast, g += w.gen, r += w.rows;
   }
-  int64_t tot_items, tot_rows;
-  int64_t io = block_exclusive_scan(items, &tot_items);
-  int64_t ro = block_exclusive_scan(rows, &tot_rows);
+  int64_t tf, tg, tr;
+  int64_t fo = block_exclusive_scan(f, &tf);
+  int64_t go = block_exclusive_scan(g, &tg);
+  int64_t ro = block_exclusive_scan(r, &tr);
   for (int i = s0; i < s1; ++i) {
-    const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
-    const int np = (q > 0 && q <= kSplitMaxQ && c > P) ? (c + P - 1) / P : 1;
-    item_off[i] = (int32_t)io;
-    nparts[i] = np;
-    split_base[i] = np > 1 ? (int32_t)ro : -1;
-    io += (int64_t)max(q, 0) * H * np;
-    if (np > 1) ro += (int64_t)q * H * np;
+    const SeqWork w = seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, H, Hkv, fast);
+    fast_off[i] = (int32_t)fo;
+    gen_off[i] = (int32_t)go;
+    nparts[i] = w.np;
+    split_base[i] = w.np > 1 ? (int32_t)ro : -1;
+    fo += w.fast, go += w.gen, ro += w.rows;
   }
   if (t == 0) {
-    item_off[S] = (int32_t)tot_items;
-    hdr[0] = (int32_t)tot_items;
-    hdr[1] = P;
-    hdr[2] = (int32_t)tot_rows;
+    fast_off[S] = (int32_t)tf;
+    gen_off[S] = (int32_t)tg;
+    hdr[0] = (int32_t)tf;
+    hdr[1] = (int32_t)tg;
+    hdr[2] = P;
+    hdr[3] = (int32_t)tr;
   }
 }
+
+// ------------------------------------------------------------ generic -----
 
 template <typename T>
 __global__ void __launch_bounds__(64) attend_generic_kernel(
     T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const T* __restrict__ kc,
     const T* __restrict__ vc, const int32_t* __restrict__ bt, int bt_stride,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H, int Hkv,
-    int D, int bs, float scale, const int32_t* __restrict__ hdr,
+    int D, int bs, float scale_log2, const int32_t* __restrict__ hdr,
     const int32_t* __restrict__ item_off, const int32_t* __restrict__ nparts,
     const int32_t* __restrict__ split_base, float2* __restrict__ ml, float* __restrict__ po) {
   __shared__ float q_s[kMaxHeadDim];
   __shared__ float p_s[64];
   __shared__ int64_t row_s[64];
   const int lane = threadIdx.x;
-  const int n_items = hdr[0];
-  const int P = hdr[1];
+  const int n_items = hdr[1];
+  const int P = hdr[2];
   const int rep = H / Hkv;
   const int64_t slot_stride = (int64_t)Hkv * D;
   constexpr int kR = kMaxHeadDim / 64;
@@ -193,12 +233,12 @@ __global__ void __launch_bounds__(64) attend_generic_kernel(
         const T* kr = kc + row;
         float dot = 0.f;
         for (int d = 0; d < D; ++d) dot += q_s[d] * Elem<T>::load(kr, d);
-        s = dot * scale;
+        s = dot * scale_log2;
       }
       const float cmax = wave_max(s);
       const float m_new = fmaxf(m, cmax);
-      const float alpha = (m == -__builtin_inff()) ? 0.f : expf(m - m_new);
-      const float p = (key < kend) ? expf(s - m_new) : 0.f;
+      const float alpha = (m == -__builtin_inff()) ? 0.f : exp2f(m - m_new);
+      const float p = (key < kend) ? exp2f(s - m_new) : 0.f;
       l = l * alpha + wave_sum(p);
       p_s[lane] = p;
       row_s[lane] = row;
@@ -239,11 +279,324 @@ __global__ void __launch_bounds__(64) attend_generic_kernel(
   }
 }
 
+// ---------------------------------------------------- bandwidth decode -----
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float c) {
+  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.x),
+                                      __builtin_bit_cast(bf16x2_t, b.x), c, false);
+  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.y),
+                                      __builtin_bit_cast(bf16x2_t, b.y), c, false);
+  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.z),
+                                      __builtin_bit_cast(bf16x2_t, b.z), c, false);
+  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.w),
+                                      __builtin_bit_cast(bf16x2_t, b.w), c, false);
+  return c;
+}
+
+// sum over the 4 lanes of a quad, result in every lane (DPP quad_perm)
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+  return v;
+}
+
+// Reduce over lanes that share (lane & 3): xor 4, 8, 16, 32.
+__device__ __forceinline__ float stride4_max(float v) {
+#pragma unroll
+  for (int o = 4; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float stride4_sum(float v) {
+#pragma unroll
+  for (int o = 4; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// One workgroup item = (decode sequence, context partition, group of 4 KV
+// heads); wavefront w takes KV head 4*group + w. Per 16-token block a
+// wavefront reads 4 KB of K and 4 KB of V for its KV head.
+//   QK: lane l reads token l/4 of the block, 16-byte chunks (l&3)+4j of the
+//       head row (j < 4); four v_dot2_f32_bf16 per chunk and query head,
+//       then a quad DPP sum gives every lane of the quad the 4 heads' scores.
+//   PV: lane l reads dims chunk l&15 of tokens (l>>4)+4t (t < 4); the
+//       probabilities of those tokens come through LDS; accumulators are 4
+//       heads x 8 dims per lane, summed over the 4 token groups at the end.
+__global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
+    uint16_t* __restrict__ out, const uint16_t* __restrict__ query, int64_t q_stride,
+    // not __restrict__: restrict-qualified loads are treated as invariant and
+    // may be scheduled past the compiler barriers that batch them
+    const uint16_t* kc, const uint16_t* vc,
+    const int32_t* __restrict__ bt, int bt_stride, const int32_t* __restrict__ seq_lens,
+    const int32_t* __restrict__ qsl, int S, int Hkv, float scale_log2,
+    const int32_t* __restrict__ hdr, const int32_t* __restrict__ item_off,
+    const int32_t* __restrict__ nparts, const int32_t* __restrict__ split_base,
+    float2* __restrict__ ml, float* __restrict__ po) {
+  __shared__ float4 p_lds[4][kFChunk * 16];  // per wave: [block][token] -> 4 heads
+  __shared__ uint4 q_lds[4][kFRep * 16];       // per wave: 4 heads x 128 bf16
+  __shared__ float4 acc_lds[4][8 * 64];        // per wave: accumulators between chunks
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int qp = lane & 3, tk = lane >> 2;     // QK mapping
+  const int vcn = lane & 15, vg = lane >> 4;  // PV mapping
+  const int n_items = hdr[0];
+  const int P = hdr[2];
+  const int H = Hkv * kFRep;
+  const int64_t tok_stride = (int64_t)Hkv * kFD;  // elements per cache slot
+  float4* pw = p_lds[wave];
+
+  for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
+    const int i = upper_bound_le(item_off, S + 1, it);
+    const int local = it - item_off[i];
+    const int np = nparts[i];
+    const int part = local % np;
+    const int kvh = (local / np) * 4 + wave;
+    const int ctx = seq_lens[i];
+    const int tok = qsl[i];
+    const int kbeg = np > 1 ? part * P : 0;
+    const int kend = np > 1 ? min(ctx, kbeg + P) : ctx;
+    const int32_t* table = bt + (int64_t)i * bt_stride;
+
+    // query of the 4 heads to LDS: [head][16-byte chunk]
+    uint4* qw = q_lds[wave];
+    {
+      const uint16_t* qb = query + (int64_t)tok * q_stride + (int64_t)kvh * kFRep * kFD;
+      qw[lane] = *reinterpret_cast<const uint4*>(qb + lane * 8);
+    }
+    const int64_t kv_off = (int64_t)kvh * kFD;
+
+    float m_run = -__builtin_inff();  // per head qp (lanes share qp)
+    float l_run = 0.f;
+    float4* stash = acc_lds[wave] + lane;  // stash[64 * k]: conflict-free
+    __syncthreads();
+    float* pf = reinterpret_cast<float*>(pw);  // [block][token][head] scores, then probabilities
+    // byte offsets of this lane inside a block (a block is 16 slots x Hkv x 128 bf16)
+    const uint32_t k_lane = (uint32_t)((tk * tok_stride + kv_off) * 2) + qp * 16;
+    const uint32_t v_lane = (uint32_t)((vg * tok_stride + kv_off) * 2) + vcn * 16;
+    const uint32_t v_tstep = (uint32_t)(4 * tok_stride * 2);
+    const int64_t blk_bytes = (int64_t)kFBs * tok_stride * 2;
+    const char* kbytes = reinterpret_cast<const char*>(kc);
+    const char* vbytes = reinterpret_cast<const char*>(vc);
+    for (int c0 = kbeg; c0 < kend; c0 += kFChunk * kFBs) {
+      const int nblk = min(kFChunk, (kend - c0 + kFBs - 1) / kFBs);
+      const int b0 = c0 / kFBs;
+      // block ids of the chunk: lane b holds block b, broadcast with readlane
+      const int my_bid = lane < nblk ? table[b0 + lane] : 0;
+      // ---- QK: 4 blocks per step, loads issued back to back (blocks past the
+      // chunk end re-read the last block and are masked)
+      float cmax = -__builtin_inff();
+#pragma unroll 1
+      for (int g = 0; g < nblk; g += 4) {
+        // keeps the query reads below inside the loop: hoisting them would pin
+        // 64 registers for the whole item and halve the occupancy
+        asm volatile("" ::: "memory");
+        uint4 kb[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int bid = __builtin_amdgcn_readlane(my_bid, min(g + u, nblk - 1));
+          const char* bp = kbytes + (int64_t)bid * blk_bytes + k_lane;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) kb[u][j] = *reinterpret_cast<const uint4*>(bp + j * 64);
+        }
+        uint4 q[kFRep][4];
+#pragma unroll
+        for (int h = 0; h < kFRep; ++h)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) q[h][j] = qw[h * 16 + qp + 4 * j];
+        // all 16 loads of the group go out before any of them is consumed
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          float a[kFRep];
+#pragma unroll
+          for (int h = 0; h < kFRep; ++h) {
+            float d = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) d = dot8(q[h][j], kb[u][j], d);
+            a[h] = quad_sum(d);
+          }
+          const float mine = qp == 0 ? a[0] : qp == 1 ? a[1] : qp == 2 ? a[2] : a[3];
+          const int key = c0 + (g + u) * kFBs + tk;
+          const bool ok = (g + u < nblk) && key < kend;
+          const float sv = ok ? mine * scale_log2 : -__builtin_inff();
+          cmax = fmaxf(cmax, sv);
+          pf[((g + u) * 16 + tk) * 4 + qp] = sv;
+        }
+      }
+      // ---- online softmax update for head qp
+      cmax = stride4_max(cmax);
+      const float m_new = fmaxf(m_run, cmax);
+      const float alpha = m_run == -__builtin_inff() ? 0.f : exp2f(m_run - m_new);
+      float lsum = 0.f;
+      const int nb4 = (nblk + 3) & ~3;
+#pragma unroll 4
+      for (int b = 0; b < nb4; ++b) {
+        const int ix = (b * 16 + tk) * 4 + qp;
+        const float sv = pf[ix];
+        const float p = sv == -__builtin_inff() ? 0.f : exp2f(sv - m_new);
+        pf[ix] = p;
+        lsum += p;
+      }
+      lsum = stride4_sum(lsum);
+      l_run = l_run * alpha + lsum;
+      m_run = m_new;
+      // accumulators: zero on the first chunk, else the stash rescaled
+      float acc[kFRep][8];
+      if (c0 == kbeg) {
+#pragma unroll
+        for (int h = 0; h < kFRep; ++h)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+      } else {
+#pragma unroll
+        for (int h = 0; h < kFRep; ++h) {
+          const float ah = __shfl(alpha, h, 64);
+          const float4 x0 = stash[64 * (2 * h)], x1 = stash[64 * (2 * h + 1)];
+          acc[h][0] = x0.x * ah, acc[h][1] = x0.y * ah, acc[h][2] = x0.z * ah, acc[h][3] = x0.w * ah;
+          acc[h][4] = x1.x * ah, acc[h][5] = x1.y * ah, acc[h][6] = x1.z * ah, acc[h][7] = x1.w * ah;
+        }
+      }
+      __syncthreads();
+      // ---- PV: 4 blocks per step; probabilities past the context are 0 and
+      // the V rows there are zeroed so poisoned slots cannot leak in
+#pragma unroll 1
+      for (int g = 0; g < nblk; g += 4) {
+        uint4 vb[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int bid = __builtin_amdgcn_readlane(my_bid, min(g + u, nblk - 1));
+          const char* bp = vbytes + (int64_t)bid * blk_bytes + v_lane;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) vb[u][t] = *reinterpret_cast<const uint4*>(bp + t * v_tstep);
+        }
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int key = c0 + (g + u) * kFBs + vg + 4 * t;
+            const bool ok = (g + u < nblk) && key < kend;
+            const float4 p4 = pw[(g + u) * 16 + vg + 4 * t];
+            const uint4 w = ok ? vb[u][t] : make_uint4(0, 0, 0, 0);
+            const float v[8] = {bf16lo(w.x), bf16hi(w.x), bf16lo(w.y), bf16hi(w.y),
+                                bf16lo(w.z), bf16hi(w.z), bf16lo(w.w), bf16hi(w.w)};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              acc[0][e] += p4.x * v[e];
+              acc[1][e] += p4.y * v[e];
+              acc[2][e] += p4.z * v[e];
+              acc[3][e] += p4.w * v[e];
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < kFRep; ++h) {
+        stash[64 * (2 * h)] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+        stash[64 * (2 * h + 1)] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+      }
+      __syncthreads();
+    }
+    float acc[kFRep][8];
+#pragma unroll
+    for (int h = 0; h < kFRep; ++h) {
+      const float4 x0 = stash[64 * (2 * h)], x1 = stash[64 * (2 * h + 1)];
+      acc[h][0] = x0.x, acc[h][1] = x0.y, acc[h][2] = x0.z, acc[h][3] = x0.w;
+      acc[h][4] = x1.x, acc[h][5] = x1.y, acc[h][6] = x1.z, acc[h][7] = x1.w;
+    }
+    // ---- sum the 4 token groups, then lanes 0..15 write 8 dims x 4 heads
+#pragma unroll
+    for (int h = 0; h < kFRep; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float a = acc[h][e];
+        a += __shfl_xor(a, 16, 64);
+        a += __shfl_xor(a, 32, 64);
+        acc[h][e] = a;
+      }
+    float l_h[kFRep], m_h[kFRep];
+#pragma unroll
+    for (int h = 0; h < kFRep; ++h) {
+      l_h[h] = __shfl(l_run, h, 64);
+      m_h[h] = __shfl(m_run, h, 64);
+    }
+    if (vg == 0) {
+      if (np == 1) {
+#pragma unroll
+        for (int h = 0; h < kFRep; ++h) {
+          const float inv = l_h[h] > 0.f ? 1.f / l_h[h] : 0.f;
+          uint4 o;
+          o.x = (uint32_t)f32_to_bf16(acc[h][0] * inv) | ((uint32_t)f32_to_bf16(acc[h][1] * inv) << 16);
+          o.y = (uint32_t)f32_to_bf16(acc[h][2] * inv) | ((uint32_t)f32_to_bf16(acc[h][3] * inv) << 16);
+          o.z = (uint32_t)f32_to_bf16(acc[h][4] * inv) | ((uint32_t)f32_to_bf16(acc[h][5] * inv) << 16);
+          o.w = (uint32_t)f32_to_bf16(acc[h][6] * inv) | ((uint32_t)f32_to_bf16(acc[h][7] * inv) << 16);
+          *reinterpret_cast<uint4*>(out + ((int64_t)tok * H + kvh * kFRep + h) * kFD + vcn * 8) = o;
+        }
+      } else {
+#pragma unroll
+        for (int h = 0; h < kFRep; ++h) {
+          const int64_t prow = (int64_t)split_base[i] + (int64_t)(kvh * kFRep + h) * np + part;
+          float4* dst = reinterpret_cast<float4*>(po + prow * kFD + vcn * 8);
+          dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+          dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+          if (vcn == 0) ml[prow] = make_float2(m_h[h], l_h[h]);
+        }
+      }
+    }
+  }
+}
+
+// --------------------------------------------------------------- combine --
+
+// Merge of the bandwidth kernel's split sequences: one workgroup per decode
+// sequence, a thread per (head, 8-dim chunk); partials are read once.
+__global__ void __launch_bounds__(256) combine_decode_bf16_kernel(
+    uint16_t* __restrict__ out, const int32_t* __restrict__ qsl,
+    const int32_t* __restrict__ seq_lens, int S, int H, const int32_t* __restrict__ nparts,
+    const int32_t* __restrict__ split_base, const float2* __restrict__ ml,
+    const float* __restrict__ po) {
+  for (int i = blockIdx.x; i < S; i += gridDim.x) {
+    const int np = nparts[i];
+    if (np <= 1 || qsl[i + 1] - qsl[i] != 1 || seq_lens[i] <= 0) continue;
+    const int tok = qsl[i];
+    const int64_t base = split_base[i];
+    for (int idx = threadIdx.x; idx < H * 16; idx += blockDim.x) {
+      const int head = idx >> 4, ch = idx & 15;
+      const int64_t row0 = base + (int64_t)head * np;
+      float M = -__builtin_inff();
+      for (int p = 0; p < np; ++p) M = fmaxf(M, ml[row0 + p].x);
+      float L = 0.f, a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int p = 0; p < np; ++p) {
+        const float2 v = ml[row0 + p];
+        if (v.x == -__builtin_inff()) continue;
+        const float w = exp2f(v.x - M);
+        L += v.y * w;
+        const float4* src = reinterpret_cast<const float4*>(po + (row0 + p) * kFD + ch * 8);
+        const float4 x0 = src[0], x1 = src[1];
+        a[0] += x0.x * w, a[1] += x0.y * w, a[2] += x0.z * w, a[3] += x0.w * w;
+        a[4] += x1.x * w, a[5] += x1.y * w, a[6] += x1.z * w, a[7] += x1.w * w;
+      }
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      uint4 o;
+      o.x = (uint32_t)f32_to_bf16(a[0] * inv) | ((uint32_t)f32_to_bf16(a[1] * inv) << 16);
+      o.y = (uint32_t)f32_to_bf16(a[2] * inv) | ((uint32_t)f32_to_bf16(a[3] * inv) << 16);
+      o.z = (uint32_t)f32_to_bf16(a[4] * inv) | ((uint32_t)f32_to_bf16(a[5] * inv) << 16);
+      o.w = (uint32_t)f32_to_bf16(a[6] * inv) | ((uint32_t)f32_to_bf16(a[7] * inv) << 16);
+      *reinterpret_cast<uint4*>(out + ((int64_t)tok * H + head) * kFD + ch * 8) = o;
+    }
+  }
+}
+
+
 template <typename T>
 __global__ void __launch_bounds__(64) combine_kernel(
-    T* __restrict__ out, const int32_t* __restrict__ qsl, int S, int T_, int H, int D,
-    const int32_t* __restrict__ nparts, const int32_t* __restrict__ split_base,
-    const float2* __restrict__ ml, const float* __restrict__ po) {
+    T* __restrict__ out, const int32_t* __restrict__ qsl, const int32_t* __restrict__ seq_lens,
+    int S, int T_, int H, int D, bool fast, const int32_t* __restrict__ nparts,
+    const int32_t* __restrict__ split_base, const float2* __restrict__ ml,
+    const float* __restrict__ po) {
   const int lane = threadIdx.x;
   const int64_t pairs = (int64_t)T_ * H;
   for (int64_t pr = blockIdx.x; pr < pairs; pr += gridDim.x) {
@@ -251,6 +604,7 @@ __global__ void __launch_bounds__(64) combine_kernel(
     const int i = upper_bound_le(qsl, S, tok);
     const int np = nparts[i];
     if (np <= 1) continue;
+    if (fast && qsl[i + 1] - qsl[i] == 1 && seq_lens[i] > 0) continue;  // merged in place
     const int j = tok - qsl[i];
     const int64_t row0 = (int64_t)split_base[i] + (int64_t)(j * H + h) * np;
     float M = -__builtin_inff();
@@ -258,39 +612,95 @@ __global__ void __launch_bounds__(64) combine_kernel(
     float L = 0.f;
     for (int p = 0; p < np; ++p) {
       const float2 v = ml[row0 + p];
-      if (v.x != -__builtin_inff()) L += v.y * expf(v.x - M);
+      if (v.x != -__builtin_inff()) L += v.y * exp2f(v.x - M);
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
     for (int d = lane; d < D; d += 64) {
       float a = 0.f;
       for (int p = 0; p < np; ++p) {
         const float2 v = ml[row0 + p];
-        if (v.x != -__builtin_inff()) a += po[(row0 + p) * D + d] * expf(v.x - M);
+        if (v.x != -__builtin_inff()) a += po[(row0 + p) * D + d] * exp2f(v.x - M);
       }
       Elem<T>::store(out + ((int64_t)tok * H + h) * D, d, a * inv);
     }
   }
 }
 
-template <typename T>
-int launch_attention(void* out, const void* query, int64_t q_stride, const void* kc,
-                     const void* vc, const int32_t* bt, int bt_stride, const int32_t* seq_lens,
-                     const int32_t* qsl, int S, int T_, int H, int Hkv, int D, int bs,
-                     float scale, const Layout& L, hipStream_t st) {
-  plan_kernel<<<1, kPlanThreads, 0, st>>>(seq_lens, qsl, S, H, L.cap_rows, L.hdr, L.item_off,
-                                          L.nparts, L.split_base);
-  VL_CHECK_LAUNCH();
-  const int grid = vl_num_cus() * 16;
-  attend_generic_kernel<T><<<grid, 64, 0, st>>>(
-      (T*)out, (const T*)query, q_stride, (const T*)kc, (const T*)vc, bt, bt_stride, seq_lens,
-      qsl, S, H, Hkv, D, bs, scale, L.hdr, L.item_off, L.nparts, L.split_base, L.ml, L.po);
-  VL_CHECK_LAUNCH();
-  const int64_t pairs = (int64_t)T_ * H;
-  const int cgrid = (int)(pairs < 65536 ? pairs : 65536);
-  combine_kernel<T><<<cgrid, 64, 0, st>>>((T*)out, qsl, S, T_, H, D, L.nparts, L.split_base,
-                                          L.ml, L.po);
+struct Args {
+  void* out;
+  const void* query;
+  int64_t q_stride;
+  const void* kc;
+  const void* vc;
+  const int32_t* bt;
+  int bt_stride;
+  const int32_t* seq_lens;
+  const int32_t* qsl;
+  int S, T, H, Hkv, D, bs;
+  float scale;
+  int dtype;
+};
+
+int check_args(const Args& a, const void* ws, size_t ws_bytes, bool need_kv) {
+  VL_CHECK_ARG(a.dtype == VL_DTYPE_F32 || a.dtype == VL_DTYPE_BF16, "bad dtype %d", a.dtype);
+  VL_CHECK_ARG(a.S >= 0 && a.T >= 0, "bad batch size");
+  VL_CHECK_ARG(a.H > 0 && a.Hkv > 0 && a.H % a.Hkv == 0,
+               "num_heads must be a positive multiple of num_kv_heads");
+  VL_CHECK_ARG(a.D > 0 && a.D <= kMaxHeadDim, "head_dim must be in 1..%d", kMaxHeadDim);
+  VL_CHECK_ARG(a.bs > 0 && a.bt_stride >= 0, "bad block table");
+  if (need_kv) VL_CHECK_ARG(a.q_stride >= (int64_t)a.H * a.D, "query row stride too small");
+  if (a.S == 0 || a.T == 0) return VL_OK;
+  VL_CHECK_ARG(a.seq_lens && a.qsl && ws, "null pointer");
+  if (need_kv)
+    VL_CHECK_ARG(a.out && a.query && a.kc && a.vc && a.bt, "null pointer");
+  VL_CHECK_ARG(ws_bytes >= plan_bytes(a.S), "workspace too small: %zu < %zu", ws_bytes,
+               plan_bytes(a.S));
+  VL_CHECK_ARG(((uintptr_t)ws & 255) == 0, "workspace must be 256-byte aligned");
+  return VL_OK;
+}
+
+int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
+  const Layout L = make_layout(ws, ws_bytes, a.S, a.D);
+  const bool fast = fast_shape(a.dtype, a.H, a.Hkv, a.D, a.bs);
+  plan_kernel<<<1, kPlanThreads, 0, st>>>(a.seq_lens, a.qsl, a.S, a.H, a.Hkv, fast, L.cap_rows,
+                                          L.hdr, L.fast_off, L.gen_off, L.nparts, L.split_base);
   VL_CHECK_LAUNCH();
   return VL_OK;
+}
+
+template <typename T>
+int do_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) {
+  const Layout L = make_layout(ws, ws_bytes, a.S, a.D);
+  const float sl2 = a.scale * kLog2e;
+  const int ncu = vl_num_cus();
+  const bool fast = fast_shape(a.dtype, a.H, a.Hkv, a.D, a.bs);
+  if (fast) {
+    attend_decode_bf16_kernel<<<ncu * 8, 256, 0, st>>>(
+        (uint16_t*)a.out, (const uint16_t*)a.query, a.q_stride, (const uint16_t*)a.kc,
+        (const uint16_t*)a.vc, a.bt, a.bt_stride, a.seq_lens, a.qsl, a.S, a.Hkv, sl2, L.hdr,
+        L.fast_off, L.nparts, L.split_base, L.ml, L.po);
+    VL_CHECK_LAUNCH();
+    combine_decode_bf16_kernel<<<a.S < 4096 ? a.S : 4096, 256, 0, st>>>(
+        (uint16_t*)a.out, a.qsl, a.seq_lens, a.S, a.H, L.nparts, L.split_base, L.ml, L.po);
+    VL_CHECK_LAUNCH();
+    if (max_q == 1) return VL_OK;  // every sequence was a decode: nothing else to run
+  }
+  attend_generic_kernel<T><<<ncu * 16, 64, 0, st>>>(
+      (T*)a.out, (const T*)a.query, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.bt,
+      a.bt_stride, a.seq_lens, a.qsl, a.S, a.H, a.Hkv, a.D, a.bs, sl2, L.hdr, L.gen_off, L.nparts,
+      L.split_base, L.ml, L.po);
+  VL_CHECK_LAUNCH();
+  const int64_t pairs = (int64_t)a.T * a.H;
+  const int cgrid = (int)(pairs < 65536 ? pairs : 65536);
+  combine_kernel<T><<<cgrid, 64, 0, st>>>((T*)a.out, a.qsl, a.seq_lens, a.S, a.T, a.H, a.D, fast,
+                                          L.nparts, L.split_base, L.ml, L.po);
+  VL_CHECK_LAUNCH();
+  return VL_OK;
+}
+
+int dispatch_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) {
+  return a.dtype == VL_DTYPE_F32 ? do_run<float>(a, max_q, ws, ws_bytes, st)
+                                 : do_run<uint16_t>(a, max_q, ws, ws_bytes, st);
 }
 
 }  // namespace
@@ -309,7 +719,40 @@ extern "C" size_t vl_paged_attention_workspace_size(int num_seqs, int num_tokens
   if (parts < 1) parts = 1;
   if (parts > 64) parts = 64;
   const int64_t rows = parts > 1 ? split_tokens * num_heads * parts : 0;
-  return plan_bytes(num_seqs) + (size_t)rows * (size_t)(head_dim + 2) * 4;
+  return plan_bytes(num_seqs) + 256 + (size_t)rows * (size_t)(head_dim + 2) * 4;
+}
+
+extern "C" int vl_paged_attention_plan(const int32_t* seq_lens, const int32_t* query_start_loc,
+                                       int num_seqs, int num_tokens, int num_heads,
+                                       int num_kv_heads, int head_dim, int block_size, int dtype,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+  Args a{};
+  a.seq_lens = seq_lens, a.qsl = query_start_loc, a.S = num_seqs, a.T = num_tokens;
+  a.H = num_heads, a.Hkv = num_kv_heads, a.D = head_dim, a.bs = block_size, a.dtype = dtype;
+  int rc = check_args(a, workspace, workspace_bytes, false);
+  if (rc || a.S == 0 || a.T == 0) return rc;
+  return do_plan(a, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int vl_paged_attention_run(void* out, const void* query, int64_t query_stride,
+                                      const void* key_cache, const void* value_cache,
+                                      const int32_t* block_tables, int block_table_stride,
+                                      const int32_t* seq_lens, const int32_t* query_start_loc,
+                                      int num_seqs, int num_tokens, int num_heads,
+                                      int num_kv_heads, int head_dim, int block_size, float scale,
+                                      int dtype, int max_query_len, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  Args a{out, query, query_stride, key_cache, value_cache, block_tables, block_table_stride,
+         seq_lens, query_start_loc, num_seqs, num_tokens, num_heads, num_kv_heads, head_dim,
+         block_size, scale, dtype};
+  int rc = check_args(a, workspace, workspace_bytes, true);
+  if (rc || a.S == 0 || a.T == 0) return rc;
+  if (fast_shape(dtype, num_heads, num_kv_heads, head_dim, block_size))
+    VL_CHECK_ARG((query_stride % 8) == 0 && ((uintptr_t)query & 15) == 0 &&
+                     ((uintptr_t)out & 15) == 0 && ((uintptr_t)key_cache & 15) == 0 &&
+                     ((uintptr_t)value_cache & 15) == 0,
+                 "bf16 operands must be 16-byte aligned");
+  return dispatch_run(a, max_query_len, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" int vl_paged_attention(void* out, const void* query, int64_t query_stride,
@@ -318,31 +761,14 @@ extern "C" int vl_paged_attention(void* out, const void* query, int64_t query_st
                                   const int32_t* seq_lens, const int32_t* query_start_loc,
                                   int num_seqs, int num_tokens, int num_heads, int num_kv_heads,
                                   int head_dim, int block_size, float scale, int dtype,
-                                  void* workspace, size_t workspace_bytes, void* stream) {
-  VL_CHECK_ARG(dtype == VL_DTYPE_F32 || dtype == VL_DTYPE_BF16, "bad dtype %d", dtype);
-  VL_CHECK_ARG(num_seqs >= 0 && num_tokens >= 0, "bad batch size");
-  VL_CHECK_ARG(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
-               "num_heads must be a positive multiple of num_kv_heads");
-  VL_CHECK_ARG(head_dim > 0 && head_dim <= kMaxHeadDim, "head_dim must be in 1..%d", kMaxHeadDim);
-  VL_CHECK_ARG(block_size > 0 && block_table_stride >= 0, "bad block table");
-  VL_CHECK_ARG(query_stride >= (int64_t)num_heads * head_dim, "query row stride too small");
-  if (num_seqs == 0 || num_tokens == 0) return VL_OK;
-  VL_CHECK_ARG(out && query && key_cache && value_cache && block_tables && seq_lens &&
-                   query_start_loc && workspace,
-               "null pointer");
-  VL_CHECK_ARG(workspace_bytes >= vl_paged_attention_min_workspace(num_seqs),
-               "workspace too small: %zu < %zu", workspace_bytes,
-               vl_paged_attention_min_workspace(num_seqs));
-  VL_CHECK_ARG(((uintptr_t)workspace & 255) == 0, "workspace must be 256-byte aligned");
-  const Layout L = make_layout(workspace, workspace_bytes, num_seqs, head_dim);
-  hipStream_t st = (hipStream_t)stream;
-  if (dtype == VL_DTYPE_F32)
-    return launch_attention<float>(out, query, query_stride, key_cache, value_cache,
-                                   block_tables, block_table_stride, seq_lens, query_start_loc,
-                                   num_seqs, num_tokens, num_heads, num_kv_heads, head_dim,
-                                   block_size, scale, L, st);
-  return launch_attention<uint16_t>(out, query, query_stride, key_cache, value_cache, block_tables,
-                                    block_table_stride, seq_lens, query_start_loc, num_seqs,
-                                    num_tokens, num_heads, num_kv_heads, head_dim, block_size,
-                                    scale, L, st);
+                                  int max_query_len, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  int rc = vl_paged_attention_plan(seq_lens, query_start_loc, num_seqs, num_tokens, num_heads,
+                                   num_kv_heads, head_dim, block_size, dtype, workspace,
+                                   workspace_bytes, stream);
+  if (rc) return rc;
+  return vl_paged_attention_run(out, query, query_stride, key_cache, value_cache, block_tables,
+                                block_table_stride, seq_lens, query_start_loc, num_seqs,
+                                num_tokens, num_heads, num_kv_heads, head_dim, block_size, scale,
+                                dtype, max_query_len, workspace, workspace_bytes, stream);
 }

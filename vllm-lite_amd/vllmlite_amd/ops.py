@@ -33,7 +33,13 @@ SIGNATURES = {
     "vl_paged_attention_min_workspace": (_size, [_i32]),
     "vl_paged_attention": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
                                   _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32,
-                                  _f32, _i32, _c_void_p, _size, _c_void_p]),
+                                  _f32, _i32, _i32, _c_void_p, _size, _c_void_p]),
+    "vl_paged_attention_plan": (_i32, [_c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32,
+                                       _i32, _c_void_p, _size, _c_void_p]),
+    "vl_paged_attention_run": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,
+                                      _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32,
+                                      _i32, _i32, _i32, _f32, _i32, _i32, _c_void_p, _size,
+                                      _c_void_p]),
     "vl_rms_norm": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _f32,
                            _c_void_p]),
     "vl_silu_mul": (_i32, [_c_void_p, _c_void_p, _i64, _i32, _c_void_p]),
@@ -151,12 +157,8 @@ def paged_attention_workspace_size(num_seqs, num_tokens, num_heads, head_dim, ma
                                                        max_context_len))
 
 
-def paged_attention(out: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
-                    value_cache: torch.Tensor, block_tables: torch.Tensor, seq_lens: torch.Tensor,
-                    query_start_loc: torch.Tensor, scale: float, block_size: int,
-                    workspace: torch.Tensor, max_context_len: Optional[int] = None) -> None:
-    """query [T, H, D] (token rows may be strided), caches [slots, Hkv, D],
-    block_tables int32 [S, W], seq_lens int32 [S], query_start_loc int32 [S+1]."""
+def _attn_check(out, query, key_cache, value_cache, block_tables, seq_lens, query_start_loc,
+                workspace):
     T, H, D = query.shape
     _need(query.stride(2) == 1 and query.stride(1) == D, "query rows must be [H, D] contiguous")
     _need(out.shape == (T, H, D) and out.is_contiguous() and out.dtype == query.dtype,
@@ -174,13 +176,59 @@ def paged_attention(out: torch.Tensor, query: torch.Tensor, key_cache: torch.Ten
     _need(query_start_loc.numel() == S + 1 and block_tables.dim() == 2 and
           block_tables.shape[0] == S, "metadata shapes disagree")
     _need(workspace.is_cuda and workspace.data_ptr() % 256 == 0, "workspace must be 256-aligned")
-    _check(lib().vl_paged_attention(_ptr(out), _ptr(query), query.stride(0), _ptr(key_cache),
-                                    _ptr(value_cache), _ptr(block_tables), block_tables.stride(0),
-                                    _ptr(seq_lens), _ptr(query_start_loc), S, T, H, hkv, D,
-                                    block_size, float(scale), _dtype_code(query),
-                                    _ptr(workspace), workspace.numel() * workspace.element_size(),
-                                    _stream()),
+    return T, H, hkv, D, S
+
+
+def _attn_args(out, query, key_cache, value_cache, block_tables, seq_lens, query_start_loc,
+               scale, block_size, workspace, max_query_len, T, H, hkv, D, S):
+    return (_ptr(out), _ptr(query), query.stride(0), _ptr(key_cache), _ptr(value_cache),
+            _ptr(block_tables), block_tables.stride(0), _ptr(seq_lens), _ptr(query_start_loc),
+            S, T, H, hkv, D, block_size, float(scale), _dtype_code(query), int(max_query_len),
+            _ptr(workspace), workspace.numel() * workspace.element_size(), _stream())
+
+
+def paged_attention(out: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
+                    value_cache: torch.Tensor, block_tables: torch.Tensor, seq_lens: torch.Tensor,
+                    query_start_loc: torch.Tensor, scale: float, block_size: int,
+                    workspace: torch.Tensor, max_query_len: int = 0) -> None:
+    """query [T, H, D] (token rows may be strided), caches [slots, Hkv, D],
+    block_tables int32 [S, W], seq_lens int32 [S], query_start_loc int32 [S+1].
+    max_query_len: host-known bound on per-sequence queries (0 = unknown)."""
+    dims = _attn_check(out, query, key_cache, value_cache, block_tables, seq_lens,
+                       query_start_loc, workspace)
+    _check(lib().vl_paged_attention(*_attn_args(out, query, key_cache, value_cache, block_tables,
+                                                seq_lens, query_start_loc, scale, block_size,
+                                                workspace, max_query_len, *dims)),
            "vl_paged_attention")
+
+
+def paged_attention_plan(query: torch.Tensor, key_cache: torch.Tensor, seq_lens: torch.Tensor,
+                         query_start_loc: torch.Tensor, block_size: int,
+                         workspace: torch.Tensor) -> None:
+    """Plan once per batch; reuse with paged_attention_run for every layer."""
+    T, H, D = query.shape
+    hkv = key_cache.shape[-2]
+    _dev_i32(seq_lens, "seq_lens")
+    _dev_i32(query_start_loc, "query_start_loc")
+    S = seq_lens.numel()
+    _need(query_start_loc.numel() == S + 1, "query_start_loc length")
+    _need(workspace.is_cuda and workspace.data_ptr() % 256 == 0, "workspace must be 256-aligned")
+    _check(lib().vl_paged_attention_plan(_ptr(seq_lens), _ptr(query_start_loc), S, T, H, hkv, D,
+                                         block_size, _dtype_code(query), _ptr(workspace),
+                                         workspace.numel() * workspace.element_size(), _stream()),
+           "vl_paged_attention_plan")
+
+
+def paged_attention_run(out, query, key_cache, value_cache, block_tables, seq_lens,
+                        query_start_loc, scale, block_size, workspace,
+                        max_query_len: int = 0) -> None:
+    dims = _attn_check(out, query, key_cache, value_cache, block_tables, seq_lens,
+                       query_start_loc, workspace)
+    _check(lib().vl_paged_attention_run(*_attn_args(out, query, key_cache, value_cache,
+                                                    block_tables, seq_lens, query_start_loc,
+                                                    scale, block_size, workspace, max_query_len,
+                                                    *dims)),
+           "vl_paged_attention_run")
 
 
 # ------------------------------------------------------------------ K4 -----
