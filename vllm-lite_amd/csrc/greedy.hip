@@ -70,7 +70,7 @@ __global__ void __launch_bounds__(256) verify_pick_kernel(
     const int32_t* __restrict__ row_start, const int32_t* __restrict__ num_drafts,
     int max_drafts, int32_t* __restrict__ out_tokens) {
   const int s = blockIdx.x, j = blockIdx.y;
-  const int nd = num_drafts[s];
+  const int nd = min(max(num_drafts[s], 0), max_drafts);
   if (j > nd) return;
   const ArgBest b = block_argmax(logits + (int64_t)(row_start[s] + j) * stride, vocab);
   if (threadIdx.x == 0) out_tokens[(int64_t)s * (max_drafts + 1) + j] = b.i;
@@ -82,7 +82,7 @@ __global__ void verify_accept_kernel(const int32_t* __restrict__ num_drafts,
                                      int32_t* __restrict__ num_accepted, int num_seqs) {
   const int s = blockIdx.x * blockDim.x + threadIdx.x;
   if (s >= num_seqs) return;
-  const int nd = num_drafts[s];
+  const int nd = min(max(num_drafts[s], 0), max_drafts);
   int32_t* o = out_tokens + (int64_t)s * (max_drafts + 1);
   const int32_t* d = drafts + (int64_t)s * max_drafts;
   int acc = nd;
