@@ -139,6 +139,75 @@ def cpu_baseline(torch, b, budget_s=12.0):
                       f"BLAS threads {blas_threads}"}
 
 
+def cfg0_engine_config():
+    """The 48-request mix's engine: TinyLlama 6 layers, d 384, H8/Hkv4, d_ff 1024,
+    vocab 261, max_len 512; 512 blocks of 16, no prefix cache; 16 seqs, budget 1024."""
+    from vllmlite_amd.config import CacheConfig, EngineConfig, ModelConfig, SchedulerConfig
+    return EngineConfig(
+        model=ModelConfig(n_layers=6, n_heads=8, n_kv_heads=4, d_model=384, d_ff=1024,
+                          vocab_size=261, max_seq_len=512),
+        cache=CacheConfig(block_size=16, num_blocks=512, enable_prefix_caching=False),
+        scheduler=SchedulerConfig(max_seqs=16, max_batched_tokens=1024))
+
+
+def run_mix(runner, cfg):
+    """One pass of the mix: wall from the first add_request until drained
+    (the reference's run_paged, bench/bench.py:74-109)."""
+    from vllmlite_amd.engine import LLMEngine
+    from vllmlite_amd.workload import mixed_lengths
+    eng = LLMEngine(cfg, runner=runner)
+    reqs = mixed_lengths(0, 48, 0)
+    t0 = time.perf_counter()
+    for rid, ids, p in reqs:
+        eng.add_request(params=p, request_id=rid, prompt_token_ids=ids)
+    while eng.has_work:
+        eng.step()
+    wall = time.perf_counter() - t0
+    streams = {rid: list(eng.seqs[rid].output_token_ids) for rid, _, _ in reqs}
+    return wall, eng.total_output_tokens, eng.total_steps, streams
+
+
+def e2e_leg(repeat=3, cpu=True):
+    """Output tok/s of the 48-request mix through HipRunner (one warm-up pass,
+    then best of `repeat`; the runner and its captured graphs persist across
+    passes, each pass gets a fresh engine), and the same mix through the NumPy
+    oracle runner on this host's cores (warm-up on a 4-request mix, best of
+    `repeat`)."""
+    import json as _json
+    from vllmlite_amd.hip_runner import HipRunner
+    cfg = cfg0_engine_config()
+    runner = HipRunner(cfg.model, cfg.cache)
+    run_mix(runner, cfg)
+    best = min((run_mix(runner, cfg) for _ in range(repeat)), key=lambda r: r[0])
+    wall, toks, steps, streams = best
+    with open(os.path.join(ROOT, "tests", "golden", "cfg0_streams.json")) as f:
+        gold = _json.load(f)["streams"]
+    same = sum(streams[r] == gold[r] for r in gold)
+    out = {"workload": "48-request ragged mix (prompts 17-251, outputs 16-192, greedy), "
+                       "TinyLlama 6L d384 H8/Hkv4 d_ff1024 fp32, block 16, 512 blocks, "
+                       "16 seqs, budget 1024",
+           "output_tok_per_s": round(toks / wall, 1), "wall_s": round(wall, 4),
+           "steps": steps, "us_per_step": round(wall / steps * 1e6, 1),
+           "output_tokens": toks, "streams_identical_to_reference": f"{same}/{len(gold)}"}
+    if cpu:
+        from oracle.runner import NumpyRunner
+        from vllmlite_amd.engine import LLMEngine
+        from vllmlite_amd.workload import make_workload
+        warm = make_workload(4, np.random.default_rng(99), 16, 64, 8, 16)
+        eng = LLMEngine(cfg, runner=NumpyRunner(cfg.model, cfg.cache))
+        for rid, ids, p in warm:
+            eng.add_request(params=p, request_id=rid, prompt_token_ids=ids)
+        while eng.has_work:
+            eng.step()
+        cpu_best = min((run_mix(NumpyRunner(cfg.model, cfg.cache), cfg) for _ in range(repeat)),
+                       key=lambda r: r[0])
+        cpu_tps = cpu_best[1] / cpu_best[0]
+        out["cpu_numpy_tok_per_s"] = round(cpu_tps, 1)
+        out["cpu_cores"] = len(os.sched_getaffinity(0))
+        out["speedup_vs_cpu_numpy"] = round(toks / wall / cpu_tps, 2)
+    return out
+
+
 def copy_ceiling(torch, nbytes=2 << 30, iters=10):
     a = torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda")
     c = torch.empty_like(a)
@@ -160,6 +229,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the 48-request mix leg")
     ap.add_argument("--profile-mode", action="store_true",
                     help="only the timed attention runs (for rocprofv3 passes)")
     args = ap.parse_args()
@@ -229,6 +299,10 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch, b)
+    del b, out, ws
+    torch.cuda.empty_cache()
+    if not args.no_e2e:
+        line["e2e"] = e2e_leg(cpu=not args.no_cpu)
     print(json.dumps(line), flush=True)
 
 

@@ -49,3 +49,25 @@ def test_no_compute_without_gpu_needed_for_queries():
         lib.vl_paged_attention_min_workspace(256)
     lib.vl_abi_version.restype = ctypes.c_int
     assert lib.vl_abi_version() == 1
+
+
+def test_hip_runner_refuses_to_run_without_a_gpu():
+    """No CPU fallback: without a device the runner raises instead of computing."""
+    torch = pytest.importorskip("torch")
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    from vllmlite_amd.config import EngineConfig
+    from vllmlite_amd.hip_runner import HipRunner
+    cfg = EngineConfig()
+    with pytest.raises(RuntimeError):
+        HipRunner(cfg.model, cfg.cache)
+
+
+def test_engine_default_backend_is_the_hip_runner():
+    from vllmlite_amd.config import EngineConfig
+    from vllmlite_amd.runner import make_runner
+    torch = pytest.importorskip("torch")
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    with pytest.raises(RuntimeError):
+        make_runner(EngineConfig())

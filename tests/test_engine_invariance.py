@@ -154,3 +154,29 @@ def test_seeded_sampling_is_reproducible():
 def test_empty_token_list_rejected():
     with pytest.raises(ValueError):
         build().add_request(params=SamplingParams(), prompt_token_ids=[])
+
+
+def test_fork_shares_blocks_and_copy_on_write_keeps_streams():
+    """fork_request: children share the parent's partial tail block, their
+    first write emits CoW pairs (block_manager.py:77-85) and, greedy on the
+    same context, they continue exactly as the parent does."""
+    engine = build(block_size=4)
+    p = SamplingParams(max_tokens=6, temperature=0.0, ignore_eos=True)
+    rid = engine.add_request("copy on write please", p)
+    engine.step()
+    kids = [engine.fork_request(rid, f"kid{i}") for i in range(3)]
+    cows = []
+    real = engine.runner.execute
+
+    def execute(sched):
+        cows.extend(sched.cow)
+        return real(sched)
+
+    engine.runner.execute = execute
+    while engine.has_work:
+        engine.step()
+    assert len(cows) == 3 and len({d for _, d in cows}) == 3
+    want = engine.seqs[rid].output_token_ids
+    assert all(engine.seqs[k].output_token_ids == want for k in kids)
+    a = engine.scheduler.blocks.allocator
+    assert a.num_free == a.num_blocks

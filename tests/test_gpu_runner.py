@@ -1,0 +1,165 @@
+"""HipRunner behind the unchanged engine: greedy streams equal the reference's
+and are invariant to paging, chunking, batching, prefix caching, preemption
+and speculation (the reference's tests/test_engine.py:57-204 and
+tests/test_speculative.py:63-101), with the expected streams taken from the
+reference itself (tests/golden/*.json).
+
+Bar: identical greedy token streams, except at an argmax near-tie. A
+divergence is accepted only where the reference's own top-1/top-2 logit margin
+at that token is below NEAR_TIE (fp32 reductions in a different order move
+logits by ~1e-6 relative); every other difference fails.
+"""
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from vllmlite_amd.engine import LLMEngine  # noqa: E402
+from vllmlite_amd.speculative import NgramProposer  # noqa: E402
+from vllmlite_amd.workload import mixed_lengths  # noqa: E402
+
+from helpers import PROMPTS, cfg0_config, run, small_cfg  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+NEAR_TIE = 1e-4
+
+
+def _gold(name):
+    with open(os.path.join(GOLD, name)) as f:
+        return json.load(f)
+
+
+def hip_engine(use_graphs=True, **kw):
+    from vllmlite_amd.hip_runner import HipRunner
+    cfg = small_cfg(**kw)
+    return LLMEngine(cfg, runner=HipRunner(cfg.model, cfg.cache, use_graphs=use_graphs))
+
+
+def small_reference():
+    g = _gold("small_streams.json")
+    assert g["prompts"] == PROMPTS
+    return g["streams"]
+
+
+def test_cfg0_mix_matches_reference_streams():
+    """The 48-request ragged mix end to end: 260 steps, 3179 tokens, the
+    reference's greedy streams token for token (near-ties excepted)."""
+    from vllmlite_amd.hip_runner import HipRunner
+    g = _gold("cfg0_streams.json")
+    cfg = cfg0_config(False)
+    eng = LLMEngine(cfg, runner=HipRunner(cfg.model, cfg.cache))
+    reqs = mixed_lengths(0, 48, 0)
+    for rid, ids, p in reqs:
+        eng.add_request(params=p, request_id=rid, prompt_token_ids=ids)
+    while eng.has_work:
+        eng.step()
+    diverged = []
+    for rid, _, _ in reqs:
+        got, want = eng.seqs[rid].output_token_ids, g["streams"][rid]
+        assert len(got) == len(want), rid
+        for j, (a, b) in enumerate(zip(got, want)):
+            if a != b:
+                diverged.append((rid, j, g["margins"][rid][j]))
+                break
+    for rid, j, margin in diverged:
+        assert margin < NEAR_TIE, f"{rid} diverges at token {j} with reference margin {margin}"
+    assert eng.total_steps == g["steps"] == 260
+    print("diverged at near-ties:", diverged)
+
+
+def test_default_engine_matches_reference_streams():
+    assert run(hip_engine(), PROMPTS, check_counts=True) == small_reference()
+
+
+def test_graph_replay_equals_eager_logits():
+    """Every step's logits from HIP-graph replay are bitwise those of eager runs."""
+    a, b = hip_engine(use_graphs=True), hip_engine(use_graphs=False)
+    seen = []
+    for eng in (a, b):
+        logs = []
+        real = eng.runner.execute
+
+        def execute(sched, real=real, logs=logs):
+            lg, rows = real(sched)
+            logs.append(lg.copy())
+            return lg, rows
+
+        eng.runner.execute = execute
+        run(eng, PROMPTS)
+        seen.append(logs)
+    assert len(seen[0]) == len(seen[1])
+    for x, y in zip(*seen):
+        assert np.array_equal(x, y)
+
+
+@pytest.mark.parametrize("block_size", [1, 4, 16, 64])
+def test_block_size_does_not_change_output(block_size):
+    assert run(hip_engine(block_size=block_size), PROMPTS) == small_reference()
+
+
+def test_prefix_caching_does_not_change_output():
+    assert run(hip_engine(prefix_cache=True), PROMPTS, check_counts=True) == small_reference()
+
+
+@pytest.mark.parametrize("max_batched", [8, 33, 64, 4096])
+def test_chunked_prefill_does_not_change_output(max_batched):
+    assert run(hip_engine(max_batched=max_batched), PROMPTS) == small_reference()
+
+
+@pytest.mark.parametrize("max_seqs", [1, 3])
+def test_batch_composition_does_not_change_output(max_seqs):
+    assert run(hip_engine(max_seqs=max_seqs), PROMPTS) == small_reference()
+
+
+def test_preemption_preserves_output():
+    engine = hip_engine(block_size=4, num_blocks=24, max_seqs=8, prefix_cache=True)
+    got = run(engine, PROMPTS, check_counts=True)
+    assert engine.scheduler.total_preemptions > 0
+    assert got == small_reference()
+
+
+@pytest.mark.parametrize("k", [1, 4])
+def test_speculation_matches_plain_greedy(k):
+    e = hip_engine()
+    e.spec_k = k
+    e.proposer = NgramProposer(k)
+    rep = ["abcdefgh abcdefgh abcdefgh abcdefgh abcdefgh abcdefgh abcdefgh abcdefgh"]
+    plain = run(hip_engine(), rep, max_tokens=40)
+    assert run(e, rep, max_tokens=40) == plain
+    assert e.spec.accepted > 0
+
+
+def test_copy_on_write_fork_matches_oracle_runner():
+    """A forked parent with a partial tail block: the children's first decode
+    step writes into the shared block, so the block manager emits CoW pairs;
+    the HipRunner's logits must match the NumPy oracle runner's."""
+    from oracle.runner import NumpyRunner
+    from vllmlite_amd.hip_runner import HipRunner
+    from vllmlite_amd.sequence import SamplingParams
+
+    cfg = small_cfg(block_size=4)
+    outs = []
+    for factory in (NumpyRunner, HipRunner):
+        eng = LLMEngine(cfg, runner=factory(cfg.model, cfg.cache))
+        p = SamplingParams(max_tokens=6, temperature=0.0, ignore_eos=True)
+        rid = eng.add_request("copy on write please", p)
+        eng.step()  # prefill: 20 tokens -> a partial 6th block
+        kids = [eng.fork_request(rid, f"kid{i}") for i in range(3)]
+        cows = []
+        real = eng.runner.execute
+
+        def execute(sched, real=real, cows=cows):
+            cows.extend(sched.cow)
+            return real(sched)
+
+        eng.runner.execute = execute
+        while eng.has_work:
+            eng.step()
+        assert cows, "no copy-on-write pair was scheduled"
+        outs.append([eng.seqs[r].output_token_ids for r in [rid] + kids])
+    assert outs[0] == outs[1]

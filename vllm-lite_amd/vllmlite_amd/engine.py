@@ -78,6 +78,32 @@ class LLMEngine:
     def abort(self, request_id: str) -> bool:
         return self.scheduler.abort(request_id)
 
+    def fork_request(self, parent_id: str, child_id: str) -> str:
+        """Start a running copy of a running request that shares all of its
+        blocks, partial tail included (BlockManager.fork,
+        vllmlite/block_manager.py:133-137; the reference defines the fork but
+        no engine path calls it). The child's first write into the shared tail
+        makes append_slots emit a copy-on-write pair. Used by the
+        shared-prefix workload to exercise the CoW path."""
+        parent = self.seqs[parent_id]
+        if parent not in self.scheduler.running:
+            raise ValueError(f"{parent_id} is not running")
+        if child_id in self.seqs:
+            raise ValueError(f"{child_id} exists")
+        child = Sequence(child_id, list(parent.prompt_token_ids), parent.params)
+        child.output_token_ids = list(parent.output_token_ids)
+        child.num_computed = parent.num_computed
+        child.status = parent.status
+        child.first_token_at = parent.first_token_at
+        self.scheduler.blocks.fork(parent, child)
+        self.scheduler.blocks.live_tokens += child.table.num_filled
+        self.scheduler.running.append(child)
+        self.seqs[child_id] = child
+        src = self.detok[parent_id]
+        self.detok[child_id] = _Detok(src.text, src.consumed)
+        self.rngs[child_id] = np.random.default_rng(parent.params.seed)
+        return child_id
+
     def release(self, request_id: str) -> None:
         self.seqs.pop(request_id, None)
         self.detok.pop(request_id, None)

@@ -1,0 +1,266 @@
+"""HipRunner: the ModelRunner boundary (vllmlite/runner.py:19-100) on one MI355X.
+
+execute(SchedulerOutput) -> (logits, rows), exactly as the reference's
+NumpyRunner: logits is a host float32 array [R, vocab], rows[i] = (first_row,
+count) for scheduled sequence i, count = min(1 + drafts, tokens)
+(runner.py:86-90). Per call:
+
+  1. copy-on-write pairs, in list order, before any K/V write
+     (runner.py:54-64): one vl_copy_blocks launch over all layers;
+  2. the ragged batch is flattened on the host into one int32 record
+     [token_ids | positions | slot_mapping | logits_idx | query_start_loc |
+     seq_lens | block_tables] (runner.py:62-100, block.py:154-156) and sent
+     with a single host-to-device copy from pinned memory;
+  3. the TinyLlama forward (model.py:80-120) runs on the device: embedding
+     gather, then per layer fused RMSNorm(+residual), one QKV GEMM, RoPE fused
+     with the K/V slot scatter, the ragged paged attention (planned once per
+     step, run per layer), the output GEMM, fused RMSNorm(+residual), one
+     gate|up GEMM, SwiGLU, the down GEMM; finally RMSNorm and the tied lm_head
+     on the logits rows only;
+  4. one device-to-host copy of the logits rows and a stream synchronisation.
+
+Step 3 is captured once per shape bucket (tokens, sequences and logits rows
+each rounded up to a power of two) into a HIP graph and replayed afterwards;
+padded tokens belong to no sequence, carry slot -1 (no cache write) and
+position 0, padded sequences have no tokens and no context, and the rows they
+produce are never read. GEMMs are PyTorch (hipBLASLt) in fp32 with TF32-style
+reduced precision off; everything else is the gfx950 library.
+
+The engine calls execute serially, possibly from a different thread each time
+(async_engine.py:47): every call selects the runner's device and stream.
+"""
+
+from __future__ import annotations
+
+from typing import Dict, List, Tuple
+
+import numpy as np
+import torch
+
+from . import ops
+from .model import model_weights, pack_weights, rope_tables
+from .runner import ModelRunner
+
+
+def _bucket(n: int, floor: int) -> int:
+    b = floor
+    while b < n:
+        b *= 2
+    return b
+
+
+class _Shape:
+    """Offsets of one bucket's int32 record and views of the device buffers."""
+
+    def __init__(self, Tb: int, Sb: int, Rb: int, W: int):
+        self.Tb, self.Sb, self.Rb, self.W = Tb, Sb, Rb, W
+        o = 0
+        self.tok, o = o, o + Tb
+        self.pos, o = o, o + Tb
+        self.slot, o = o, o + Tb
+        self.lidx, o = o, o + Rb
+        self.qsl, o = o, o + Sb + 1
+        self.lens, o = o, o + Sb
+        self.bt, o = o, o + Sb * W
+        self.n_ints = o
+
+
+class HipRunner(ModelRunner):
+    def __init__(self, model_cfg, cache_cfg, weights: Dict[str, np.ndarray] = None,
+                 device=None, use_graphs: bool = True):
+        if not torch.cuda.is_available():
+            raise RuntimeError("HipRunner needs a visible MI355X (torch.cuda.is_available() is False)")
+        ops.lib()  # fail now, loudly, if the gfx950 library is not built
+        torch.backends.cuda.matmul.allow_tf32 = False
+        self.model_cfg = model_cfg
+        self.cache_cfg = cache_cfg
+        self.block_size = cache_cfg.block_size
+        self.device = torch.device(device) if device is not None else torch.device(
+            "cuda", torch.cuda.current_device())
+        self.use_graphs = use_graphs
+        mc = model_cfg
+        self.H, self.Hkv, self.hd = mc.n_heads, mc.n_kv_heads, mc.head_dim
+        self.scale = float(1.0 / np.sqrt(mc.head_dim))
+        with torch.cuda.device(self.device):
+            self.stream = torch.cuda.Stream(self.device)
+            w = weights if weights is not None else model_weights(mc)
+            self.w = pack_weights(mc, w, torch, self.device)
+            cos, sin = rope_tables(mc.head_dim, mc.max_seq_len)
+            self.cos = torch.from_numpy(cos).to(self.device)
+            self.sin = torch.from_numpy(sin).to(self.device)
+            slots = cache_cfg.num_blocks * cache_cfg.block_size
+            shape = (mc.n_layers, slots, mc.n_kv_heads, mc.head_dim)
+            self.cache_k = torch.zeros(shape, dtype=torch.float32, device=self.device)
+            self.cache_v = torch.zeros(shape, dtype=torch.float32, device=self.device)
+        self.W = max(1, -(-mc.max_seq_len // self.block_size))
+        self._cap_T = 0
+        self._graphs: Dict[Tuple[int, int, int], torch.cuda.CUDAGraph] = {}
+        self._pool = None
+
+    # ------------------------------------------------------------ interface --
+    @property
+    def vocab_size(self) -> int:
+        return self.model_cfg.vocab_size
+
+    @property
+    def cache_bytes(self) -> int:
+        return (self.cache_k.numel() + self.cache_v.numel()) * 4
+
+    def execute(self, out) -> Tuple[np.ndarray, List[Tuple[int, int]]]:
+        with torch.cuda.device(self.device), torch.cuda.stream(self.stream):
+            if out.cow:
+                self._copy_on_write(out.cow)
+            shape, rows, R = self._stage(out)
+            key = (shape.Tb, shape.Sb, shape.Rb)
+            g = self._graphs.get(key)
+            if g is not None:
+                g.replay()
+            else:
+                self._forward(shape)
+                if self.use_graphs:
+                    self._capture(shape, key)
+            self._logits_host[:R].copy_(self._logits[:R], non_blocking=True)
+            self.stream.synchronize()
+            return self._logits_host_np[:R].copy(), rows
+
+    # -------------------------------------------------------------- staging --
+    def _ensure_capacity(self, T: int, W: int) -> None:
+        if T <= self._cap_T and W <= self.W:
+            return
+        cap = _bucket(max(T, self._cap_T), 64)
+        self.W = max(self.W, W)
+        self._graphs.clear()
+        self._pool = None
+        mc, dev = self.model_cfg, self.device
+        H, Hkv, hd = self.H, self.Hkv, self.hd
+        f32 = dict(dtype=torch.float32, device=dev)
+        n_ints = _Shape(cap, cap, cap, self.W).n_ints
+        self._meta = torch.zeros(n_ints, dtype=torch.int32, device=dev)
+        self._meta_host = torch.zeros(n_ints, dtype=torch.int32, pin_memory=True)
+        self._meta_np = self._meta_host.numpy()
+        self._x = torch.zeros(cap, mc.d_model, **f32)
+        self._h = torch.zeros(cap, mc.d_model, **f32)
+        self._delta = torch.zeros(cap, mc.d_model, **f32)
+        self._qkv = torch.zeros(cap, (H + 2 * Hkv) * hd, **f32)
+        self._q = torch.zeros(cap, H, hd, **f32)
+        self._attn = torch.zeros(cap, H, hd, **f32)
+        self._gu = torch.zeros(cap, 2 * mc.d_ff, **f32)
+        self._act = torch.zeros(cap, mc.d_ff, **f32)
+        self._hsel = torch.zeros(cap, mc.d_model, **f32)
+        self._logits = torch.zeros(cap, mc.vocab_size, **f32)
+        self._logits_host = torch.zeros(cap, mc.vocab_size, dtype=torch.float32, pin_memory=True)
+        self._logits_host_np = self._logits_host.numpy()
+        ws = ops.paged_attention_workspace_size(cap, cap, H, hd, mc.max_seq_len + 64)
+        self._ws = ops.AttentionWorkspace(dev).get(ws)
+        self._cap_T = cap
+
+    def _stage(self, out):
+        """Flatten the scheduled batch into the pinned record and send it."""
+        bs = self.block_size
+        sched = out.scheduled
+        S = len(sched)
+        starts = np.empty(S, np.int64)
+        ns = np.empty(S, np.int64)
+        counts = np.empty(S, np.int64)
+        toks: List[int] = []
+        width = 1
+        for i, item in enumerate(sched):
+            seq = item.seq
+            st, n = seq.num_computed, item.num_tokens
+            starts[i], ns[i] = st, n
+            toks += seq.token_slice(st, st + n)
+            counts[i] = min(1 + len(seq.draft_token_ids), n)
+            nb = len(seq.table.block_ids)
+            if (st + n) > nb * bs:
+                raise ValueError(f"sequence {seq.request_id}: {st + n} tokens but only {nb} blocks")
+            if st + n > self.model_cfg.max_seq_len:
+                # the reference fails the same way indexing its RoPE table
+                raise IndexError(f"position {st + n - 1} beyond max_seq_len "
+                                 f"{self.model_cfg.max_seq_len}")
+            width = max(width, nb)
+        T = int(ns.sum())
+        R = int(counts.sum())
+        self._ensure_capacity(T, width)
+        shape = _Shape(_bucket(T, 16), _bucket(S, 8), _bucket(R, 8), self.W)
+        m = self._meta_np
+        qsl = np.zeros(S + 1, np.int64)
+        np.cumsum(ns, out=qsl[1:])
+        seq_of_tok = np.repeat(np.arange(S), ns)
+        pos = np.arange(T, dtype=np.int64) - qsl[:-1][seq_of_tok] + starts[seq_of_tok]
+        bt = m[shape.bt:shape.bt + shape.Sb * shape.W].reshape(shape.Sb, shape.W)
+        bt[:] = 0
+        for i, item in enumerate(sched):
+            ids = item.seq.table.block_ids
+            bt[i, :len(ids)] = ids
+        slots = bt[seq_of_tok, pos // bs].astype(np.int64) * bs + pos % bs
+        Tb, Sb, Rb = shape.Tb, shape.Sb, shape.Rb
+        m[shape.tok:shape.tok + T] = toks
+        m[shape.tok + T:shape.tok + Tb] = 0
+        m[shape.pos:shape.pos + T] = pos
+        m[shape.pos + T:shape.pos + Tb] = 0
+        m[shape.slot:shape.slot + T] = slots
+        m[shape.slot + T:shape.slot + Tb] = -1
+        rsl = np.zeros(S + 1, np.int64)
+        np.cumsum(counts, out=rsl[1:])
+        seq_of_row = np.repeat(np.arange(S), counts)
+        m[shape.lidx:shape.lidx + R] = (qsl[1:][seq_of_row] - counts[seq_of_row]
+                                        + np.arange(R) - rsl[:-1][seq_of_row])
+        m[shape.lidx + R:shape.lidx + Rb] = 0
+        m[shape.qsl:shape.qsl + S + 1] = qsl
+        m[shape.qsl + S + 1:shape.qsl + Sb + 1] = T
+        m[shape.lens:shape.lens + S] = starts + ns
+        m[shape.lens + S:shape.lens + Sb] = 0
+        n = shape.n_ints
+        self._meta[:n].copy_(self._meta_host[:n], non_blocking=True)
+        rows = [(int(rsl[i]), int(counts[i])) for i in range(S)]
+        return shape, rows, R
+
+    # -------------------------------------------------------------- forward --
+    def _copy_on_write(self, pairs) -> None:
+        p = torch.tensor(pairs, dtype=torch.int32).reshape(-1, 2).to(self.device, non_blocking=False)
+        ops.copy_blocks(self.cache_k, self.cache_v, p, self.block_size)
+
+    def _forward(self, s: _Shape) -> None:
+        mc = self.model_cfg
+        Tb, Sb, Rb = s.Tb, s.Sb, s.Rb
+        meta = self._meta
+        tok = meta[s.tok:s.tok + Tb]
+        pos = meta[s.pos:s.pos + Tb]
+        slot = meta[s.slot:s.slot + Tb]
+        lidx = meta[s.lidx:s.lidx + Rb]
+        qsl = meta[s.qsl:s.qsl + Sb + 1]
+        lens = meta[s.lens:s.lens + Sb]
+        bt = meta[s.bt:s.bt + Sb * s.W].view(Sb, s.W)
+        x, h, delta = self._x[:Tb], self._h[:Tb], self._delta[:Tb]
+        qkv, q, attn = self._qkv[:Tb], self._q[:Tb], self._attn[:Tb]
+        gu, act = self._gu[:Tb], self._act[:Tb]
+        W = self.w
+        torch.index_select(W["tok_emb"], 0, tok, out=x)
+        ops.rms_norm(h, x, W["layers"][0]["attn_norm"])
+        ops.paged_attention_plan(q, self.cache_k[0], lens, qsl, self.block_size, self._ws)
+        n_layers = mc.n_layers
+        for li, L in enumerate(W["layers"]):
+            kc, vc = self.cache_k[li], self.cache_v[li]
+            torch.mm(h, L["w_qkv"], out=qkv)
+            ops.rope_and_cache(qkv, q, kc, vc, pos, slot, self.cos, self.sin, self.H, self.Hkv,
+                               self.hd)
+            ops.paged_attention_run(attn, q, kc, vc, bt, lens, qsl, self.scale, self.block_size,
+                                    self._ws)
+            torch.mm(attn.view(Tb, -1), L["wo"], out=delta)
+            ops.rms_norm(h, delta, L["ffn_norm"], residual=x)
+            torch.mm(h, L["w_gate_up"], out=gu)
+            ops.silu_mul(act, gu)
+            torch.mm(act, L["w_down"], out=delta)
+            nxt = W["layers"][li + 1]["attn_norm"] if li + 1 < n_layers else W["final_norm"]
+            ops.rms_norm(h, delta, nxt, residual=x)
+        hsel = self._hsel[:Rb]
+        torch.index_select(h, 0, lidx, out=hsel)
+        torch.mm(hsel, W["lm_head"], out=self._logits[:Rb])
+
+    def _capture(self, s: _Shape, key) -> None:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, pool=self._pool, stream=self.stream):
+            self._forward(s)
+        if self._pool is None:
+            self._pool = g.pool()
+        self._graphs[key] = g
