@@ -230,6 +230,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-e2e", action="store_true", help="skip the 48-request mix leg")
+    ap.add_argument("--e2e-only", action="store_true",
+                    help="only the 48-request mix through HipRunner (for rocprofv3 passes)")
     ap.add_argument("--profile-mode", action="store_true",
                     help="only the timed attention runs (for rocprofv3 passes)")
     args = ap.parse_args()
@@ -242,6 +244,9 @@ def main():
     from vllmlite_amd import ops
 
     torch.cuda.set_device(0)
+    if args.e2e_only:
+        print(json.dumps({"e2e": e2e_leg(cpu=False)}), flush=True)
+        return
     b = build_decode_batch(torch)
     nbytes = algorithmic_bytes(b["ctx"])
     out = torch.empty_like(b["q"])
