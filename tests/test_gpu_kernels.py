@@ -279,3 +279,46 @@ def test_plan_once_run_per_layer():
         out = torch.empty_like(q)
         o.paged_attention_run(out, q, kc, vc, bt, sl, qsl, b["scale"], 16, ws, max_query_len=7)
         check(to_np(out), expected(b, "bf16"), "bf16")
+
+
+# -- MFMA tile path (multi-query rows: chunked prefill, speculative verify) ----
+TILE_SHAPES = [("f32", 8, 4, 48), ("f32", 8, 2, 64), ("f32", 4, 4, 16), ("f32", 16, 4, 128),
+               ("f32", 4, 1, 32), ("bf16", 32, 8, 128), ("bf16", 8, 2, 64), ("bf16", 6, 3, 128)]
+
+
+@pytest.mark.parametrize("dtype,H,Hkv,D", TILE_SHAPES)
+@pytest.mark.parametrize("bs", [1, 16])
+def test_tile_prefill_chunks_with_prior_context(dtype, H, Hkv, D, bs):
+    """Chunks that start mid-block after prior context, causal within the chunk,
+    plus decodes and a 1-token context, all in one call."""
+    seqs = [(37, 37), (100, 133), (1, 90), (64, 64 + 200), (17, 500), (3, 3), (2, 40)]
+    b = make_batch(seqs, H, Hkv, D, bs, seed=30 + D + bs)
+    check(run_attention(b, dtype), expected(b, dtype), dtype)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_tile_speculative_verify_rows_split_over_long_context(dtype):
+    """5 queries per sequence over long contexts: the context is split into
+    partitions and merged; also with no room for partials."""
+    seqs = [(5, 3000), (5, 1025), (5, 5), (4, 700), (5, 6001)]
+    b = make_batch(seqs, 32, 8, 128, 16, seed=40)
+    want = expected(b, dtype)
+    check(run_attention(b, dtype), want, dtype)
+    o = ops()
+    check(run_attention(b, dtype, ws_bytes=o.lib().vl_paged_attention_min_workspace(len(seqs))),
+          want, dtype)
+
+
+def test_tile_fp32_meets_the_reference_tolerance_at_the_tinyllama_shape():
+    """fp32, 8 Q heads over 4 KV heads, D 48 (the TinyLlama mix): a 1024-token
+    budget of prefill chunks, rtol 1e-4 / atol 1e-5 as the reference's test."""
+    seqs = [(256, 256), (251, 251), (200, 300), (17, 480), (100, 100), (1, 77), (1, 512)]
+    b = make_batch(seqs, 8, 4, 48, 16, seed=41)
+    got = run_attention(b, "f32")
+    np.testing.assert_allclose(got, oracle_attention(b), rtol=1e-4, atol=1e-5)
+
+
+def test_tile_many_rows_per_kv_head():
+    """A 512-token chunk: 2048 (token, head) rows per KV head, 32 row blocks."""
+    b = make_batch([(512, 512 + 300), (1, 2000)], 32, 8, 128, 16, seed=42)
+    check(run_attention(b, "bf16"), expected(b, "bf16"), "bf16")

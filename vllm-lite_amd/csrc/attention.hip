@@ -21,11 +21,14 @@
 //
 // Softmax runs in the base-2 domain: scores are pre-multiplied by
 // scale * log2(e) and exponentiated with exp2, which is the same function.
+#include <type_traits>
+
 #include "vl_common.h"
 
 namespace {
 
 constexpr int kHdrInts = 64;  // [0] fast items [1] generic items [2] partition len [3] split rows
+                              // [4] tile items
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxHeadDim = 256;
 constexpr int kSplitMaxQ = 16;  // only sequences with <= this many queries split their context
@@ -38,10 +41,16 @@ constexpr int kFRep = 4;   // query heads per KV head
 constexpr int kFBs = 16;   // block size
 constexpr int kFChunk = 16;  // blocks per softmax chunk (256 tokens)
 
+// MFMA tile-kernel shape: 4 wavefronts x 16 (token, head) rows per workgroup,
+// 32 keys per LDS tile
+constexpr int kTileRows = 64;
+constexpr int kTileKeys = 32;
+
 struct Layout {
   int32_t* hdr;
   int32_t* fast_off;    // [S+1] bandwidth-kernel workgroup items
   int32_t* gen_off;     // [S+1] generic wavefront items
+  int32_t* tile_off;    // [S+1] MFMA tile workgroup items
   int32_t* nparts;      // [S]
   int32_t* split_base;  // [S] first partial row, or -1
   float2* ml;           // [cap_rows] (running max (log2 domain), running sum)
@@ -50,7 +59,7 @@ struct Layout {
 };
 
 inline size_t plan_bytes(int S) {
-  size_t b = kHdrInts * 4 + (size_t)(4 * S + 2) * 4;
+  size_t b = kHdrInts * 4 + (size_t)(5 * S + 3) * 4;
   return (b + 255) & ~(size_t)255;
 }
 
@@ -60,7 +69,8 @@ inline Layout make_layout(void* ws, size_t bytes, int S, int D) {
   L.hdr = (int32_t*)p;
   L.fast_off = L.hdr + kHdrInts;
   L.gen_off = L.fast_off + S + 1;
-  L.nparts = L.gen_off + S + 1;
+  L.tile_off = L.gen_off + S + 1;
+  L.nparts = L.tile_off + S + 1;
   L.split_base = L.nparts + S;
   const size_t pb = plan_bytes(S);
   const size_t per_row = (size_t)(D + 2) * 4;
@@ -74,6 +84,12 @@ inline Layout make_layout(void* ws, size_t bytes, int S, int D) {
 
 inline bool fast_shape(int dtype, int H, int Hkv, int D, int bs) {
   return dtype == VL_DTYPE_BF16 && D == kFD && bs == kFBs && Hkv % 4 == 0 && H == kFRep * Hkv;
+}
+
+// head_dims with an MFMA tile instantiation
+inline bool tile_shape(int dtype, int D) {
+  if (dtype == VL_DTYPE_BF16) return D == 64 || D == 128;
+  return D == 16 || D == 32 || D == 48 || D == 64 || D == 128;
 }
 
 __device__ __forceinline__ int upper_bound_le(const int32_t* a, int n, int x) {
@@ -108,24 +124,34 @@ __device__ int64_t block_exclusive_scan(int64_t v, int64_t* total) {
 struct SeqWork {
   int np;        // context partitions
   int64_t fast;  // bandwidth-kernel workgroup items
+  int64_t tile;  // MFMA tile workgroup items
   int64_t gen;   // generic wavefront items
   int64_t rows;  // split partial rows
 };
 
-__device__ __forceinline__ SeqWork seq_work(int q, int c, int P, int H, int Hkv, bool fast) {
+// Routing: single-query sequences of the bandwidth shape go to the decode
+// kernel; everything else goes to the MFMA tile kernel when the shape has one
+// (one workgroup per 64-row block of (token, head-in-group) rows per KV head
+// and partition), else to the generic kernel.
+__device__ __forceinline__ SeqWork seq_work(int q, int c, int P, int H, int Hkv, bool fast,
+                                            bool tile) {
   SeqWork w;
   w.np = (q > 0 && q <= kSplitMaxQ && c > P) ? (c + P - 1) / P : 1;
-  const bool bw = fast && q == 1 && c > 0;
+  const bool live = q > 0 && c > 0;
+  const bool bw = fast && q == 1 && live;
+  const bool tl = !bw && tile && live;
   w.fast = bw ? (int64_t)w.np * (Hkv / 4) : 0;
-  w.gen = bw ? 0 : (int64_t)max(q, 0) * H * w.np;
+  w.tile = tl ? (int64_t)w.np * Hkv * cdiv(q * (H / Hkv), kTileRows) : 0;
+  w.gen = (bw || tl) ? 0 : (int64_t)max(q, 0) * H * w.np;
   w.rows = w.np > 1 ? (int64_t)q * H * w.np : 0;
   return w;
 }
 
 __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H, int Hkv,
-    bool fast, int64_t cap_rows, int32_t* __restrict__ hdr, int32_t* __restrict__ fast_off,
-    int32_t* __restrict__ gen_off, int32_t* __restrict__ nparts,
+    bool fast, bool tile, int64_t cap_rows, int32_t* __restrict__ hdr,
+    int32_t* __restrict__ fast_off, int32_t* __restrict__ gen_off,
+    int32_t* __restrict__ tile_off, int32_t* __restrict__ nparts,
     int32_t* __restrict__ split_base) {
   __shared__ unsigned long long need;
   __shared__ int part_len;
@@ -139,7 +165,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     const int P = part_len;
     unsigned long long mine = 0;
     for (int i = t; i < S; i += kPlanThreads)
-      mine += seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, H, Hkv, fast).rows;
+      mine += seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, H, Hkv, fast, tile).rows;
     if (mine) atomicAdd(&need, mine);
     __syncthreads();
     const bool fits = need <= (unsigned long long)cap_rows || P >= (1 << 30);
@@ -152,30 +178,34 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
   // 2. offsets; every thread owns a contiguous chunk of sequences
   const int chunk = (S + kPlanThreads - 1) / kPlanThreads;
   const int s0 = min(S, t * chunk), s1 = min(S, s0 + chunk);
-  int64_t f = 0, g = 0, r = 0;
+  int64_t f = 0, g = 0, r = 0, x = 0;
   for (int i = s0; i < s1; ++i) {
-    const SeqWork w = seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, H, Hkv, fast);
-    f += w.fast, g += w.gen, r += w.rows;
+    const SeqWork w = seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, H, Hkv, fast, tile);
+    f += w.fast, g += w.gen, r += w.rows, x += w.tile;
   }
-  int64_t tf, tg, tr;
+  int64_t tf, tg, tr, tx;
   int64_t fo = block_exclusive_scan(f, &tf);
   int64_t go = block_exclusive_scan(g, &tg);
   int64_t ro = block_exclusive_scan(r, &tr);
+  int64_t xo = block_exclusive_scan(x, &tx);
   for (int i = s0; i < s1; ++i) {
-    const SeqWork w = seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, H, Hkv, fast);
+    const SeqWork w = seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, H, Hkv, fast, tile);
     fast_off[i] = (int32_t)fo;
     gen_off[i] = (int32_t)go;
+    tile_off[i] = (int32_t)xo;
     nparts[i] = w.np;
     split_base[i] = w.np > 1 ? (int32_t)ro : -1;
-    fo += w.fast, go += w.gen, ro += w.rows;
+    fo += w.fast, go += w.gen, ro += w.rows, xo += w.tile;
   }
   if (t == 0) {
     fast_off[S] = (int32_t)tf;
     gen_off[S] = (int32_t)tg;
+    tile_off[S] = (int32_t)tx;
     hdr[0] = (int32_t)tf;
     hdr[1] = (int32_t)tg;
     hdr[2] = P;
     hdr[3] = (int32_t)tr;
+    hdr[4] = (int32_t)tx;
   }
 }
 
@@ -276,6 +306,290 @@ __global__ void __launch_bounds__(64) attend_generic_kernel(
       if (lane == 0) ml[prow] = make_float2(m, l);
     }
     __syncthreads();
+  }
+}
+
+
+// ----------------------------------------------------------- MFMA tiles ----
+//
+// Multi-query attention (chunked prefill, speculative verify) on the matrix
+// cores. One workgroup item = (sequence, KV head, block of 64 rows, context
+// partition); a row is a (query token j, head r of the KV head's group) pair,
+// row = j * rep + r, so the 4 query heads of a GQA group share every K/V tile.
+// Wavefront w owns rows 16w..16w+15 of the block.
+//
+// Per 32-key tile (staged in LDS by the whole workgroup, V transposed):
+//   S^T[32 keys x 16 rows] = K . Q^T   two 16x16 output tiles; lane l holds
+//                                      row l%16 and keys 4(l/16)+i (+16)
+//   online softmax per row (the row's 16 keys of a tile sit in the 4 lanes
+//   l%16 + 16g, so a row max is a register max plus two xor shuffles)
+//   O^T[D x 16 rows] += V^T . P^T      the probabilities are already in the
+//                                      B-operand registers: k-slot e of lane
+//                                      group g is key 4g+e (e<4) or 16+4g+e-4
+//                                      and V^T is read from LDS in that order.
+// bf16 uses v_mfma_f32_16x16x32_bf16 (P rounded to bf16, fp32 accumulation);
+// fp32 uses v_mfma_f32_16x16x4f32, so fp32 inputs keep fp32 products.
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T, int D>
+struct TileLds;
+template <int D>
+struct TileLds<uint16_t, D> {
+  static constexpr int kRow = D + 8;           // K row stride (bf16), 16-byte aligned
+  static constexpr int vRow = kTileKeys + 4;   // V^T row stride (bf16)
+  uint16_t k[kTileKeys * kRow];
+  uint16_t vt[D * vRow];
+};
+template <int D>
+struct TileLds<float, D> {
+  static constexpr int kRow = D + 1;
+  static constexpr int vRow = D + 1;
+  float k[kTileKeys * kRow];
+  float v[kTileKeys * vRow];
+};
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256) attend_tile_kernel(
+    T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const T* __restrict__ kc,
+    const T* __restrict__ vc, const int32_t* __restrict__ bt, int bt_stride,
+    const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H, int Hkv,
+    int bs, float scale_log2, const int32_t* __restrict__ hdr, const int32_t* __restrict__ item_off,
+    const int32_t* __restrict__ nparts, const int32_t* __restrict__ split_base,
+    float2* __restrict__ ml, float* __restrict__ po) {
+  constexpr bool kBf16 = sizeof(T) == 2;
+  constexpr int kDT = D / 16;                 // 16-wide d tiles of the output
+  constexpr int kKS = kBf16 ? D / 32 : D / 4;  // k-steps of the QK^T product
+  using Lds = TileLds<T, D>;
+  __shared__ Lds lds;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int col = lane & 15;  // the lane's row within the wave's 16 rows
+  const int grp = lane >> 4;  // lane group: which keys / d chunk it holds
+  const int n_items = hdr[4];
+  const int P = hdr[2];
+  const int rep = H / Hkv;
+  const int64_t slot_stride = (int64_t)Hkv * D;
+
+  for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
+    const int i = upper_bound_le(item_off, S + 1, it);
+    const int q_len = qsl[i + 1] - qsl[i];
+    const int ctx = seq_lens[i];
+    const int np = nparts[i];
+    const int local = it - item_off[i];
+    const int part = local % np;
+    const int kvh = (local / np) % Hkv;
+    const int rb = (local / np) / Hkv;
+    const int nrows = q_len * rep;
+    const int kbeg = np > 1 ? part * P : 0;
+    const int kend = np > 1 ? min(ctx, kbeg + P) : ctx;
+    // keys the block's last row can see bound the tiles the workgroup loads
+    const int blk_last = min(nrows - 1, rb * kTileRows + kTileRows - 1);
+    const int kend_wg = min(kend, ctx - q_len + blk_last / rep + 1);
+    const int row0 = rb * kTileRows + wave * 16;
+    const int wave_last = min(nrows - 1, row0 + 15);
+    const int kend_wave = row0 < nrows ? min(kend, ctx - q_len + wave_last / rep + 1) : kbeg;
+    const int my_row = row0 + col;
+    const bool row_ok = my_row < nrows;
+    const int j = row_ok ? my_row / rep : 0;
+    const int head = kvh * rep + (row_ok ? my_row - (my_row / rep) * rep : 0);
+    const int tok = qsl[i] + j;
+    const int qpos = ctx - q_len + j;
+    const int32_t* table = bt + (int64_t)i * bt_stride;
+
+    // Q^T operand of the QK^T product, kept in registers for the whole item
+    typename std::conditional<kBf16, bf16x8_t, float>::type qop[kKS];
+    {
+      const T* qrow = query + (int64_t)tok * q_stride + (int64_t)head * D;
+#pragma unroll
+      for (int s = 0; s < kKS; ++s) {
+        if constexpr (kBf16) {
+          uint4 w = row_ok ? *reinterpret_cast<const uint4*>(qrow + 32 * s + 8 * grp)
+                           : make_uint4(0, 0, 0, 0);
+          qop[s] = __builtin_bit_cast(bf16x8_t, w);
+        } else {
+          qop[s] = row_ok ? qrow[4 * s + grp] : 0.f;
+        }
+      }
+    }
+    f32x4_t acc[kDT];
+#pragma unroll
+    for (int u = 0; u < kDT; ++u) acc[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float m_run = -__builtin_inff();
+    float l_part = 0.f;  // this lane's share of the row sum
+
+    for (int k0 = kbeg; k0 < kend_wg; k0 += kTileKeys) {
+      __syncthreads();  // the previous tile has been consumed
+      // ---- stage K and V of keys [k0, k0+32) in LDS; keys >= kend_wg are 0
+      if constexpr (kBf16) {
+        constexpr int kChunks = D / 8;  // 16-byte chunks per head row
+        for (int idx = threadIdx.x; idx < kTileKeys * kChunks; idx += 256) {
+          const int kk = idx / kChunks, c = idx - kk * kChunks;
+          const int key = k0 + kk;
+          uint4 w = make_uint4(0, 0, 0, 0);
+          if (key < kend_wg) {
+            const int64_t slot = (int64_t)table[key / bs] * bs + key % bs;
+            w = *reinterpret_cast<const uint4*>(kc + slot * slot_stride + (int64_t)kvh * D + c * 8);
+          }
+          *reinterpret_cast<uint4*>(&lds.k[kk * Lds::kRow + c * 8]) = w;
+        }
+        // V: a thread takes two adjacent keys of one 8-dim chunk and writes
+        // their 8 (key, key+1) pairs transposed
+        for (int idx = threadIdx.x; idx < (kTileKeys / 2) * kChunks; idx += 256) {
+          const int kp = idx / kChunks, c = idx - kp * kChunks;
+          const int key = k0 + 2 * kp;
+          uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
+          if (key < kend_wg) {
+            const int64_t slot = (int64_t)table[key / bs] * bs + key % bs;
+            a = *reinterpret_cast<const uint4*>(vc + slot * slot_stride + (int64_t)kvh * D + c * 8);
+          }
+          if (key + 1 < kend_wg) {
+            const int64_t slot = (int64_t)table[(key + 1) / bs] * bs + (key + 1) % bs;
+            b = *reinterpret_cast<const uint4*>(vc + slot * slot_stride + (int64_t)kvh * D + c * 8);
+          }
+          const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+          uint32_t* dst = reinterpret_cast<uint32_t*>(lds.vt);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int d = c * 8 + 2 * e;
+            dst[(d * Lds::vRow + 2 * kp) >> 1] = (av[e] & 0xffffu) | (bv[e] << 16);
+            dst[((d + 1) * Lds::vRow + 2 * kp) >> 1] = (av[e] >> 16) | (bv[e] & 0xffff0000u);
+          }
+        }
+      } else {
+        constexpr int kVec = D / 4;  // float4 per head row
+        for (int idx = threadIdx.x; idx < kTileKeys * kVec; idx += 256) {
+          const int kk = idx / kVec, c = idx - kk * kVec;
+          const int key = k0 + kk;
+          float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+          if (key < kend_wg) {
+            const int64_t slot = (int64_t)table[key / bs] * bs + key % bs;
+            const int64_t off = slot * slot_stride + (int64_t)kvh * D + c * 4;
+            a = *reinterpret_cast<const float4*>(kc + off);
+            b = *reinterpret_cast<const float4*>(vc + off);
+          }
+          float* kd = &lds.k[kk * Lds::kRow + c * 4];
+          float* vd = &lds.v[kk * Lds::vRow + c * 4];
+          kd[0] = a.x, kd[1] = a.y, kd[2] = a.z, kd[3] = a.w;
+          vd[0] = b.x, vd[1] = b.y, vd[2] = b.z, vd[3] = b.w;
+        }
+      }
+      __syncthreads();
+      if (k0 >= kend_wave) continue;  // every row of this wave is past its causal end
+
+      // ---- S^T = K Q^T for the two 16-key halves
+      f32x4_t sc[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        sc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < kKS; ++s) {
+          if constexpr (kBf16) {
+            const uint4 w = *reinterpret_cast<const uint4*>(
+                &lds.k[(16 * t + col) * Lds::kRow + 32 * s + 8 * grp]);
+            sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, w),
+                                                            qop[s], sc[t], 0, 0, 0);
+          } else {
+            const float a = lds.k[(16 * t + col) * Lds::kRow + 4 * s + grp];
+            sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, qop[s], sc[t], 0, 0, 0);
+          }
+        }
+      }
+      // ---- mask, online softmax (base 2)
+      float sv[2][4];
+      float cmax = -__builtin_inff();
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int key = k0 + 16 * t + 4 * grp + e;
+          const bool ok = row_ok && key <= qpos && key < kend;
+          sv[t][e] = ok ? sc[t][e] * scale_log2 : -__builtin_inff();
+          cmax = fmaxf(cmax, sv[t][e]);
+        }
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+      const float m_new = fmaxf(m_run, cmax);
+      const float alpha = m_new == -__builtin_inff() ? 1.f : exp2f(m_run - m_new);
+      float pv[2][4];
+      float psum = 0.f;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pv[t][e] = sv[t][e] == -__builtin_inff() ? 0.f : exp2f(sv[t][e] - m_new);
+          psum += pv[t][e];
+        }
+      l_part = l_part * alpha + psum;
+      m_run = m_new;
+#pragma unroll
+      for (int u = 0; u < kDT; ++u) acc[u] *= alpha;
+      // ---- O^T += V^T P^T
+      if constexpr (kBf16) {
+        uint4 pw;
+        pw.x = pack_bf16x2(pv[0][0], pv[0][1]);
+        pw.y = pack_bf16x2(pv[0][2], pv[0][3]);
+        pw.z = pack_bf16x2(pv[1][0], pv[1][1]);
+        pw.w = pack_bf16x2(pv[1][2], pv[1][3]);
+        const bf16x8_t pop = __builtin_bit_cast(bf16x8_t, pw);
+#pragma unroll
+        for (int u = 0; u < kDT; ++u) {
+          const uint16_t* vrow = &lds.vt[(16 * u + col) * Lds::vRow];
+          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * grp);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * grp);
+          const uint4 vw = make_uint4(lo.x, lo.y, hi.x, hi.y);
+          acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, vw), pop,
+                                                           acc[u], 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float* vrow = &lds.v[(16 * t + 4 * grp + e) * Lds::vRow];
+#pragma unroll
+            for (int u = 0; u < kDT; ++u)
+              acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * u + col], pv[t][e], acc[u],
+                                                            0, 0, 0);
+          }
+      }
+    }
+    // ---- row sums over the 4 lane groups, then write
+    float l_row = l_part;
+    l_row += __shfl_xor(l_row, 16, 64);
+    l_row += __shfl_xor(l_row, 32, 64);
+    if (row_ok) {
+      if (np == 1) {
+        const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
+        T* orow = out + ((int64_t)tok * H + head) * D;
+#pragma unroll
+        for (int u = 0; u < kDT; ++u) {
+          const int d = 16 * u + 4 * grp;
+          if constexpr (kBf16) {
+            uint2 o;
+            o.x = pack_bf16x2(acc[u][0] * inv, acc[u][1] * inv);
+            o.y = pack_bf16x2(acc[u][2] * inv, acc[u][3] * inv);
+            *reinterpret_cast<uint2*>(orow + d) = o;
+          } else {
+            *reinterpret_cast<float4*>(orow + d) =
+                make_float4(acc[u][0] * inv, acc[u][1] * inv, acc[u][2] * inv, acc[u][3] * inv);
+          }
+        }
+      } else {
+        const int64_t prow = (int64_t)split_base[i] + (int64_t)(j * H + head) * np + part;
+        float* dst = po + prow * D;
+#pragma unroll
+        for (int u = 0; u < kDT; ++u)
+          *reinterpret_cast<float4*>(dst + 16 * u + 4 * grp) =
+              make_float4(acc[u][0], acc[u][1], acc[u][2], acc[u][3]);
+        if (grp == 0) ml[prow] = make_float2(m_run, l_row);
+      }
+    }
   }
 }
 
@@ -662,10 +976,42 @@ int check_args(const Args& a, const void* ws, size_t ws_bytes, bool need_kv) {
 int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
   const Layout L = make_layout(ws, ws_bytes, a.S, a.D);
   const bool fast = fast_shape(a.dtype, a.H, a.Hkv, a.D, a.bs);
-  plan_kernel<<<1, kPlanThreads, 0, st>>>(a.seq_lens, a.qsl, a.S, a.H, a.Hkv, fast, L.cap_rows,
-                                          L.hdr, L.fast_off, L.gen_off, L.nparts, L.split_base);
+  const bool tile = tile_shape(a.dtype, a.D);
+  plan_kernel<<<1, kPlanThreads, 0, st>>>(a.seq_lens, a.qsl, a.S, a.H, a.Hkv, fast, tile,
+                                          L.cap_rows, L.hdr, L.fast_off, L.gen_off, L.tile_off,
+                                          L.nparts, L.split_base);
   VL_CHECK_LAUNCH();
   return VL_OK;
+}
+
+template <typename T, int D>
+int launch_tile_d(const Args& a, const Layout& L, float sl2, int ncu, hipStream_t st) {
+  attend_tile_kernel<T, D><<<ncu * 4, 256, 0, st>>>(
+      (T*)a.out, (const T*)a.query, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.bt, a.bt_stride,
+      a.seq_lens, a.qsl, a.S, a.H, a.Hkv, a.bs, sl2, L.hdr, L.tile_off, L.nparts, L.split_base,
+      L.ml, L.po);
+  VL_CHECK_LAUNCH();
+  return VL_OK;
+}
+
+template <typename T>
+int launch_tile(const Args& a, const Layout& L, float sl2, int ncu, hipStream_t st) {
+  if constexpr (sizeof(T) == 2) {
+    switch (a.D) {
+      case 64: return launch_tile_d<T, 64>(a, L, sl2, ncu, st);
+      case 128: return launch_tile_d<T, 128>(a, L, sl2, ncu, st);
+    }
+  } else {
+    switch (a.D) {
+      case 16: return launch_tile_d<T, 16>(a, L, sl2, ncu, st);
+      case 32: return launch_tile_d<T, 32>(a, L, sl2, ncu, st);
+      case 48: return launch_tile_d<T, 48>(a, L, sl2, ncu, st);
+      case 64: return launch_tile_d<T, 64>(a, L, sl2, ncu, st);
+      case 128: return launch_tile_d<T, 128>(a, L, sl2, ncu, st);
+    }
+  }
+  VL_CHECK_ARG(false, "no tile kernel for head_dim %d", a.D);
+  return VL_EINVAL;
 }
 
 template <typename T>
@@ -685,11 +1031,16 @@ int do_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) 
     VL_CHECK_LAUNCH();
     if (max_q == 1) return VL_OK;  // every sequence was a decode: nothing else to run
   }
-  attend_generic_kernel<T><<<ncu * 16, 64, 0, st>>>(
-      (T*)a.out, (const T*)a.query, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.bt,
-      a.bt_stride, a.seq_lens, a.qsl, a.S, a.H, a.Hkv, a.D, a.bs, sl2, L.hdr, L.gen_off, L.nparts,
-      L.split_base, L.ml, L.po);
-  VL_CHECK_LAUNCH();
+  if (tile_shape(a.dtype, a.D)) {
+    int rc = launch_tile<T>(a, L, sl2, ncu, st);
+    if (rc) return rc;
+  } else {
+    attend_generic_kernel<T><<<ncu * 16, 64, 0, st>>>(
+        (T*)a.out, (const T*)a.query, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.bt,
+        a.bt_stride, a.seq_lens, a.qsl, a.S, a.H, a.Hkv, a.D, a.bs, sl2, L.hdr, L.gen_off,
+        L.nparts, L.split_base, L.ml, L.po);
+    VL_CHECK_LAUNCH();
+  }
   const int64_t pairs = (int64_t)a.T * a.H;
   const int cgrid = (int)(pairs < 65536 ? pairs : 65536);
   combine_kernel<T><<<cgrid, 64, 0, st>>>((T*)a.out, a.qsl, a.seq_lens, a.S, a.T, a.H, a.D, fast,
@@ -747,11 +1098,12 @@ extern "C" int vl_paged_attention_run(void* out, const void* query, int64_t quer
          block_size, scale, dtype};
   int rc = check_args(a, workspace, workspace_bytes, true);
   if (rc || a.S == 0 || a.T == 0) return rc;
-  if (fast_shape(dtype, num_heads, num_kv_heads, head_dim, block_size))
+  if (fast_shape(dtype, num_heads, num_kv_heads, head_dim, block_size) ||
+      tile_shape(dtype, head_dim))
     VL_CHECK_ARG((query_stride % 8) == 0 && ((uintptr_t)query & 15) == 0 &&
                      ((uintptr_t)out & 15) == 0 && ((uintptr_t)key_cache & 15) == 0 &&
                      ((uintptr_t)value_cache & 15) == 0,
-                 "bf16 operands must be 16-byte aligned");
+                 "query, out and caches must be 16-byte aligned (query rows a multiple of 8 elements)");
   return dispatch_run(a, max_query_len, workspace, workspace_bytes, (hipStream_t)stream);
 }
 
