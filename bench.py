@@ -234,6 +234,9 @@ def main():
                     help="only the 48-request mix through HipRunner (for rocprofv3 passes)")
     ap.add_argument("--profile-mode", action="store_true",
                     help="only the timed attention runs (for rocprofv3 passes)")
+    ap.add_argument("--copy-only", action="store_true",
+                    help="only 5 device copies of 1 GiB (calibrates rocprofv3 FETCH_SIZE / "
+                         "WRITE_SIZE against a kernel of known traffic)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the attention step runs on a single MI355X "
@@ -244,6 +247,15 @@ def main():
     from vllmlite_amd import ops
 
     torch.cuda.set_device(0)
+    if args.copy_only:
+        a = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda")
+        c = torch.empty_like(a)
+        for _ in range(5):
+            c.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_only": True, "bytes_read_per_copy": a.numel() * 2,
+                          "bytes_written_per_copy": c.numel() * 2}), flush=True)
+        return
     if args.e2e_only:
         print(json.dumps({"e2e": e2e_leg(cpu=False)}), flush=True)
         return

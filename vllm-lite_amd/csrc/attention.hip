@@ -14,13 +14,16 @@
 //  run      decode sequences of the bf16 / head_dim 128 / 4-query-heads-per-
 //           KV-head / block-16 shape go to the bandwidth kernel (one
 //           wavefront per (sequence, partition, KV head), a 4-wave workgroup
-//           per 4 adjacent KV heads); everything else goes to the generic
-//           kernel (one wavefront per (sequence, query, head, partition)).
-//           Sequences whose context was split are merged by the combine
-//           kernel (max-rescaled log-sum-exp).
+//           per 4 adjacent KV heads), which merges its own split sequences;
+//           multi-query sequences go to the MFMA tile kernel when the head
+//           dim has an instantiation, else to the generic kernel (one
+//           wavefront per (sequence, query, head, partition)). Their split
+//           sequences are merged by the combine kernel (max-rescaled
+//           log-sum-exp).
 //
 // Softmax runs in the base-2 domain: scores are pre-multiplied by
 // scale * log2(e) and exponentiated with exp2, which is the same function.
+#include <algorithm>
 #include <type_traits>
 
 #include "vl_common.h"
@@ -28,11 +31,14 @@
 namespace {
 
 constexpr int kHdrInts = 64;  // [0] fast items [1] generic items [2] partition len [3] split rows
-                              // [4] tile items
+                              // [4] tile items [8] bandwidth-kernel work counter
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxHeadDim = 256;
 constexpr int kSplitMaxQ = 16;  // only sequences with <= this many queries split their context
-constexpr int kPart0 = 256;     // first partition length tried by the planner
+#ifndef VL_PART0
+#define VL_PART0 256
+#endif
+constexpr int kPart0 = VL_PART0;  // first partition length tried by the planner
 constexpr float kLog2e = 1.4426950408889634f;
 
 // bandwidth-kernel shape
@@ -40,6 +46,14 @@ constexpr int kFD = 128;   // head_dim
 constexpr int kFRep = 4;   // query heads per KV head
 constexpr int kFBs = 16;   // block size
 constexpr int kFChunk = 16;  // blocks per softmax chunk (256 tokens)
+#ifndef VL_BK
+#define VL_BK 4
+#endif
+#ifndef VL_BV
+#define VL_BV 4
+#endif
+constexpr int kBK = VL_BK;  // blocks per K load burst
+constexpr int kBV = VL_BV;  // blocks per V load burst
 
 // MFMA tile-kernel shape: 4 wavefronts x 16 (token, head) rows per workgroup,
 // 32 keys per LDS tile
@@ -98,6 +112,26 @@ __device__ __forceinline__ int upper_bound_le(const int32_t* a, int n, int x) {
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
     if (a[mid] <= x) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// The same search done by a whole wavefront: each round the 64 lanes probe
+// 64 evenly spaced entries of the remaining range and a ballot picks the
+// sub-range, so n <= 4097 takes 2 rounds of (independent) loads instead of
+// log2(n) dependent ones. Every lane of the wavefront must call it; all get
+// the result.
+__device__ __forceinline__ int wave_upper_bound_le(const int32_t* a, int n, int x) {
+  const int lane = threadIdx.x & 63;
+  int lo = 0, len = n;
+  while (len > 1) {
+    const int step = (len + 63) >> 6;
+    const int off = lane * step;
+    const bool le = off < len && a[lo + off] <= x;
+    const uint64_t m = __ballot(le);
+    const int k = 63 - __builtin_clzll(m);  // lane 0 always passes: a[lo] <= x
+    lo += k * step;
+    len = min(step, len - k * step);
   }
   return lo;
 }
@@ -206,6 +240,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     hdr[2] = P;
     hdr[3] = (int32_t)tr;
     hdr[4] = (int32_t)tx;
+    hdr[8] = 0;
   }
 }
 
@@ -229,7 +264,7 @@ __global__ void __launch_bounds__(64) attend_generic_kernel(
   const int64_t slot_stride = (int64_t)Hkv * D;
   constexpr int kR = kMaxHeadDim / 64;
   for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
-    const int i = upper_bound_le(item_off, S + 1, it);
+    const int i = wave_upper_bound_le(item_off, S + 1, it);
     const int q_len = qsl[i + 1] - qsl[i];
     const int ctx = seq_lens[i];
     const int np = nparts[i];
@@ -377,7 +412,7 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
   const int64_t slot_stride = (int64_t)Hkv * D;
 
   for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
-    const int i = upper_bound_le(item_off, S + 1, it);
+    const int i = wave_upper_bound_le(item_off, S + 1, it);
     const int q_len = qsl[i + 1] - qsl[i];
     const int ctx = seq_lens[i];
     const int np = nparts[i];
@@ -630,7 +665,12 @@ __device__ __forceinline__ float stride4_sum(float v) {
 
 // One workgroup item = (decode sequence, context partition, group of 4 KV
 // heads); wavefront w takes KV head 4*group + w. Per 16-token block a
-// wavefront reads 4 KB of K and 4 KB of V for its KV head.
+// wavefront reads 4 KB of K and 4 KB of V for its KV head. The groups of one
+// partition are adjacent items.
+//   Split sequences write unnormalised partials and (max, sum) per head;
+//   combine_decode_bf16_kernel merges them. (Merging in the last-arriving
+//   workgroup needs a device-scope release per workgroup, which on gfx950
+//   writes back the XCD's whole L2 and made the kernel 3x slower.)
 //   QK: lane l reads token l/4 of the block, 16-byte chunks (l&3)+4j of the
 //       head row (j < 4); four v_dot2_f32_bf16 per chunk and query head,
 //       then a quad DPP sum gives every lane of the quad the 4 heads' scores.
@@ -644,10 +684,11 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
     const uint16_t* kc, const uint16_t* vc,
     const int32_t* __restrict__ bt, int bt_stride, const int32_t* __restrict__ seq_lens,
     const int32_t* __restrict__ qsl, int S, int Hkv, float scale_log2,
-    const int32_t* __restrict__ hdr, const int32_t* __restrict__ item_off,
+    const int32_t* __restrict__ hdr, int32_t* work, const int32_t* __restrict__ item_off,
     const int32_t* __restrict__ nparts, const int32_t* __restrict__ split_base,
     float2* __restrict__ ml, float* __restrict__ po) {
   __shared__ float4 p_lds[4][kFChunk * 16];  // per wave: [block][token] -> 4 heads
+  __shared__ int next_lds;
   __shared__ uint4 q_lds[4][kFRep * 16];       // per wave: 4 heads x 128 bf16
   __shared__ float4 acc_lds[4][8 * 64];        // per wave: accumulators between chunks
   const int wave = threadIdx.x >> 6;
@@ -660,12 +701,20 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
   const int64_t tok_stride = (int64_t)Hkv * kFD;  // elements per cache slot
   float4* pw = p_lds[wave];
 
-  for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
-    const int i = upper_bound_le(item_off, S + 1, it);
+  // Persistent workgroups (as many as fit on the chip): the first item is
+  // blockIdx.x, later ones are claimed from the work counter, the next one at
+  // the start of the current item so that the atomic's latency is hidden.
+  // The counter is zeroed by the plan and, after each run, by the merge kernel.
+  int it = blockIdx.x;
+  while (it < n_items) {
+    int nxt = 0;
+    if (threadIdx.x == 0) nxt = (int)gridDim.x + atomicAdd(work, 1);
+    const int i = wave_upper_bound_le(item_off, S + 1, it);
     const int local = it - item_off[i];
     const int np = nparts[i];
-    const int part = local % np;
-    const int kvh = (local / np) * 4 + wave;
+    const int groups = Hkv >> 2;
+    const int part = local / groups;
+    const int kvh = (local - part * groups) * 4 + wave;
     const int ctx = seq_lens[i];
     const int tok = qsl[i];
     const int kbeg = np > 1 ? part * P : 0;
@@ -683,7 +732,7 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
     float m_run = -__builtin_inff();  // per head qp (lanes share qp)
     float l_run = 0.f;
     float4* stash = acc_lds[wave] + lane;  // stash[64 * k]: conflict-free
-    __syncthreads();
+    // every LDS region here is private to its wavefront: no workgroup barriers
     float* pf = reinterpret_cast<float*>(pw);  // [block][token][head] scores, then probabilities
     // byte offsets of this lane inside a block (a block is 16 slots x Hkv x 128 bf16)
     const uint32_t k_lane = (uint32_t)((tk * tok_stride + kv_off) * 2) + qp * 16;
@@ -701,36 +750,43 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
       // chunk end re-read the last block and are masked)
       float cmax = -__builtin_inff();
 #pragma unroll 1
-      for (int g = 0; g < nblk; g += 4) {
+      for (int g = 0; g < nblk; g += kBK) {
         // keeps the query reads below inside the loop: hoisting them would pin
         // 64 registers for the whole item and halve the occupancy
         asm volatile("" ::: "memory");
-        uint4 kb[4][4];
+        uint4 kb[kBK][4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kBK; ++u) {
           const int bid = __builtin_amdgcn_readlane(my_bid, min(g + u, nblk - 1));
           const char* bp = kbytes + (int64_t)bid * blk_bytes + k_lane;
 #pragma unroll
           for (int j = 0; j < 4; ++j) kb[u][j] = *reinterpret_cast<const uint4*>(bp + j * 64);
         }
-        uint4 q[kFRep][4];
-#pragma unroll
-        for (int h = 0; h < kFRep; ++h)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) q[h][j] = qw[h * 16 + qp + 4 * j];
         // all 16 loads of the group go out before any of them is consumed
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
+        // one query head at a time (its 4 chunks from LDS): 16 registers of
+        // query live instead of 64
+        float a4[kBK][kFRep];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          float a[kFRep];
+        for (int h = 0; h < kFRep; ++h) {
+          uint4 q[4];
 #pragma unroll
-          for (int h = 0; h < kFRep; ++h) {
+          for (int j = 0; j < 4; ++j) q[j] = qw[h * 16 + qp + 4 * j];
+#pragma unroll
+          for (int u = 0; u < kBK; ++u) {
             float d = 0.f;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) d = dot8(q[h][j], kb[u][j], d);
-            a[h] = quad_sum(d);
+            for (int j = 0; j < 4; ++j) d = dot8(q[j], kb[u][j], d);
+            a4[u][h] = d;
           }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int u = 0; u < kBK; ++u) {
+          float a[kFRep];
+#pragma unroll
+          for (int h = 0; h < kFRep; ++h) a[h] = quad_sum(a4[u][h]);
           const float mine = qp == 0 ? a[0] : qp == 1 ? a[1] : qp == 2 ? a[2] : a[3];
           const int key = c0 + (g + u) * kFBs + tk;
           const bool ok = (g + u < nblk) && key < kend;
@@ -743,15 +799,30 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
       cmax = stride4_max(cmax);
       const float m_new = fmaxf(m_run, cmax);
       const float alpha = m_run == -__builtin_inff() ? 0.f : exp2f(m_run - m_new);
+      // exponentials, in place, two blocks per step: lane l takes head
+      // qp = l & 3 of the token pair (t, t + 4), t = ((l >> 2) & 3) + 8 * ((l >> 4)
+      // & 1), of block 2 * step + (l >> 5), rounds both probabilities to bf16
+      // and stores them packed as word slot * 4 + qp of the block's score
+      // area, slot = t % 4 + 4 * (t / 8): the PV pass then reads one pair's 4
+      // heads as a uint4. The block's scores are all read before its first
+      // half is overwritten (one wavefront, LDS in program order). The row
+      // sum adds the rounded values, the weights PV actually uses.
       float lsum = 0.f;
-      const int nb4 = (nblk + 3) & ~3;
-#pragma unroll 4
-      for (int b = 0; b < nb4; ++b) {
-        const int ix = (b * 16 + tk) * 4 + qp;
-        const float sv = pf[ix];
-        const float p = sv == -__builtin_inff() ? 0.f : exp2f(sv - m_new);
-        pf[ix] = p;
-        lsum += p;
+      // through every block the PV pass reads (bursts of kBV); blocks past
+      // the chunk end get p = 0
+      const int nb4 = (nblk + kBV - 1) / kBV * kBV;
+      {
+        const int pt = ((lane >> 2) & 3) + 8 * ((lane >> 4) & 1);
+        const int pslot = ((lane >> 2) & 3) + 4 * ((lane >> 4) & 1);
+        uint32_t* pf32 = reinterpret_cast<uint32_t*>(pf);
+        for (int b = lane >> 5; b < nb4; b += 2) {
+          const float s0 = b < nblk ? pf[(b * 16 + pt) * 4 + qp] : -__builtin_inff();
+          const float s1 = b < nblk ? pf[(b * 16 + pt + 4) * 4 + qp] : -__builtin_inff();
+          const uint16_t h0 = f32_to_bf16(s0 == -__builtin_inff() ? 0.f : exp2f(s0 - m_new));
+          const uint16_t h1 = f32_to_bf16(s1 == -__builtin_inff() ? 0.f : exp2f(s1 - m_new));
+          lsum += bf16_to_f32(h0) + bf16_to_f32(h1);
+          pf32[b * 64 + pslot * 4 + qp] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+        }
       }
       lsum = stride4_sum(lsum);
       l_run = l_run * alpha + lsum;
@@ -772,14 +843,14 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
           acc[h][4] = x1.x * ah, acc[h][5] = x1.y * ah, acc[h][6] = x1.z * ah, acc[h][7] = x1.w * ah;
         }
       }
-      __syncthreads();
       // ---- PV: 4 blocks per step; probabilities past the context are 0 and
-      // the V rows there are zeroed so poisoned slots cannot leak in
+      // the V rows there are zeroed so poisoned slots cannot leak in (a NaN
+      // times 0 would)
 #pragma unroll 1
-      for (int g = 0; g < nblk; g += 4) {
-        uint4 vb[4][4];
+      for (int g = 0; g < nblk; g += kBV) {
+        uint4 vb[kBV][4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kBV; ++u) {
           const int bid = __builtin_amdgcn_readlane(my_bid, min(g + u, nblk - 1));
           const char* bp = vbytes + (int64_t)bid * blk_bytes + v_lane;
 #pragma unroll
@@ -787,22 +858,35 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
         }
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
+        // rows (vg, vg + 4) and (vg + 8, vg + 12) pair up: v_perm builds a
+        // (row0, row1) bf16 pair per dim and v_dot2_f32_bf16 applies the
+        // pair's probabilities, 4 heads at a time
+        const uint4* pp4 = reinterpret_cast<const uint4*>(pw);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kBV; ++u) {
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int key = c0 + (g + u) * kFBs + vg + 4 * t;
-            const bool ok = (g + u < nblk) && key < kend;
-            const float4 p4 = pw[(g + u) * 16 + vg + 4 * t];
-            const uint4 w = ok ? vb[u][t] : make_uint4(0, 0, 0, 0);
-            const float v[8] = {bf16lo(w.x), bf16hi(w.x), bf16lo(w.y), bf16hi(w.y),
-                                bf16lo(w.z), bf16hi(w.z), bf16lo(w.w), bf16hi(w.w)};
+          for (int j = 0; j < 2; ++j) {
+            const int key0 = c0 + (g + u) * kFBs + vg + 8 * j;
+            const uint32_t keep0 = key0 < kend ? 0xffffffffu : 0u;
+            const uint32_t keep1 = key0 + 4 < kend ? 0xffffffffu : 0u;
+            const uint4 w0 = vb[u][2 * j], w1 = vb[u][2 * j + 1];
+            const uint32_t a0[4] = {w0.x & keep0, w0.y & keep0, w0.z & keep0, w0.w & keep0};
+            const uint32_t a1[4] = {w1.x & keep1, w1.y & keep1, w1.z & keep1, w1.w & keep1};
+            const uint4 pp = pp4[(g + u) * 16 + vg + 4 * j];
+            const uint32_t ph[kFRep] = {pp.x, pp.y, pp.z, pp.w};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              acc[0][e] += p4.x * v[e];
-              acc[1][e] += p4.y * v[e];
-              acc[2][e] += p4.z * v[e];
-              acc[3][e] += p4.w * v[e];
+            for (int m = 0; m < 4; ++m) {
+              const uint32_t lo = __builtin_amdgcn_perm(a1[m], a0[m], 0x05040100u);
+              const uint32_t hi = __builtin_amdgcn_perm(a1[m], a0[m], 0x07060302u);
+#pragma unroll
+              for (int h = 0; h < kFRep; ++h) {
+                acc[h][2 * m] = __builtin_amdgcn_fdot2_f32_bf16(
+                    __builtin_bit_cast(bf16x2_t, ph[h]), __builtin_bit_cast(bf16x2_t, lo),
+                    acc[h][2 * m], false);
+                acc[h][2 * m + 1] = __builtin_amdgcn_fdot2_f32_bf16(
+                    __builtin_bit_cast(bf16x2_t, ph[h]), __builtin_bit_cast(bf16x2_t, hi),
+                    acc[h][2 * m + 1], false);
+              }
             }
           }
         }
@@ -812,7 +896,6 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
         stash[64 * (2 * h)] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
         stash[64 * (2 * h + 1)] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
       }
-      __syncthreads();
     }
     float acc[kFRep][8];
 #pragma unroll
@@ -860,50 +943,61 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
         }
       }
     }
+    if (threadIdx.x == 0) next_lds = nxt;
+    __syncthreads();
+    it = next_lds;
+    __syncthreads();  // every wavefront has read next_lds before it is rewritten
   }
 }
 
 // --------------------------------------------------------------- combine --
 
-// Merge of the bandwidth kernel's split sequences: one workgroup per decode
-// sequence, a thread per (head, 8-dim chunk); partials are read once.
+// Merge of the bandwidth kernel's split sequences: one wavefront per
+// (decode sequence, query head). Lane p first takes partition p's (max, sum)
+// to form the log-sum-exp weights; then each lane owns 2 of the 128 dims and
+// streams the partitions' partial rows with independent loads.
 __global__ void __launch_bounds__(256) combine_decode_bf16_kernel(
     uint16_t* __restrict__ out, const int32_t* __restrict__ qsl,
     const int32_t* __restrict__ seq_lens, int S, int H, const int32_t* __restrict__ nparts,
     const int32_t* __restrict__ split_base, const float2* __restrict__ ml,
-    const float* __restrict__ po) {
-  for (int i = blockIdx.x; i < S; i += gridDim.x) {
+    const float* __restrict__ po, int32_t* __restrict__ work) {
+  // the bandwidth kernel of this run has finished: reset its work counter
+  if (blockIdx.x == 0 && threadIdx.x == 0) *work = 0;
+  const int lane = threadIdx.x & 63;
+  const int64_t n_units = (int64_t)S * H;
+  for (int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); u < n_units;
+       u += (int64_t)gridDim.x * 4) {
+    const int i = (int)(u / H), h = (int)(u - (u / H) * H);
     const int np = nparts[i];
     if (np <= 1 || qsl[i + 1] - qsl[i] != 1 || seq_lens[i] <= 0) continue;
-    const int tok = qsl[i];
-    const int64_t base = split_base[i];
-    for (int idx = threadIdx.x; idx < H * 16; idx += blockDim.x) {
-      const int head = idx >> 4, ch = idx & 15;
-      const int64_t row0 = base + (int64_t)head * np;
-      float M = -__builtin_inff();
-      for (int p = 0; p < np; ++p) M = fmaxf(M, ml[row0 + p].x);
-      float L = 0.f, a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int p = 0; p < np; ++p) {
-        const float2 v = ml[row0 + p];
-        if (v.x == -__builtin_inff()) continue;
-        const float w = exp2f(v.x - M);
+    const int64_t row0 = (int64_t)split_base[i] + (int64_t)h * np;
+    float M = -__builtin_inff();
+    for (int p = lane; p < np; p += 64) M = fmaxf(M, ml[row0 + p].x);
+    M = wave_max(M);
+    float L = 0.f, a0 = 0.f, a1 = 0.f;
+    for (int p0 = 0; p0 < np; p0 += 64) {
+      float w = 0.f;
+      if (p0 + lane < np) {
+        const float2 v = ml[row0 + p0 + lane];
+        w = v.x == -__builtin_inff() ? 0.f : exp2f(v.x - M);
         L += v.y * w;
-        const float4* src = reinterpret_cast<const float4*>(po + (row0 + p) * kFD + ch * 8);
-        const float4 x0 = src[0], x1 = src[1];
-        a[0] += x0.x * w, a[1] += x0.y * w, a[2] += x0.z * w, a[3] += x0.w * w;
-        a[4] += x1.x * w, a[5] += x1.y * w, a[6] += x1.z * w, a[7] += x1.w * w;
       }
-      const float inv = L > 0.f ? 1.f / L : 0.f;
-      uint4 o;
-      o.x = (uint32_t)f32_to_bf16(a[0] * inv) | ((uint32_t)f32_to_bf16(a[1] * inv) << 16);
-      o.y = (uint32_t)f32_to_bf16(a[2] * inv) | ((uint32_t)f32_to_bf16(a[3] * inv) << 16);
-      o.z = (uint32_t)f32_to_bf16(a[4] * inv) | ((uint32_t)f32_to_bf16(a[5] * inv) << 16);
-      o.w = (uint32_t)f32_to_bf16(a[6] * inv) | ((uint32_t)f32_to_bf16(a[7] * inv) << 16);
-      *reinterpret_cast<uint4*>(out + ((int64_t)tok * H + head) * kFD + ch * 8) = o;
+      const int n = min(64, np - p0);
+      const float* src = po + (row0 + p0) * kFD + 2 * lane;
+#pragma unroll 8
+      for (int p = 0; p < n; ++p) {
+        const float wp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), p));
+        const float2 x = *reinterpret_cast<const float2*>(src + (int64_t)p * kFD);
+        a0 += wp * x.x;
+        a1 += wp * x.y;
+      }
     }
+    L = wave_sum(L);
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    reinterpret_cast<uint32_t*>(out + ((int64_t)qsl[i] * H + h) * kFD)[lane] =
+        (uint32_t)f32_to_bf16(a0 * inv) | ((uint32_t)f32_to_bf16(a1 * inv) << 16);
   }
 }
-
 
 template <typename T>
 __global__ void __launch_bounds__(64) combine_kernel(
@@ -973,6 +1067,23 @@ int check_args(const Args& a, const void* ws, size_t ws_bytes, bool need_kv) {
   return VL_OK;
 }
 
+// Workgroups of the bandwidth kernel that are resident at once on the
+// current device (its grid is persistent), cached per device.
+int decode_grid() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (!cached[dev]) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attend_decode_bf16_kernel, 256, 0) !=
+            hipSuccess ||
+        per_cu <= 0)
+      per_cu = 2;
+    cached[dev] = per_cu * vl_num_cus();
+  }
+  return cached[dev];
+}
+
 int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
   const Layout L = make_layout(ws, ws_bytes, a.S, a.D);
   const bool fast = fast_shape(a.dtype, a.H, a.Hkv, a.D, a.bs);
@@ -1021,13 +1132,16 @@ int do_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) 
   const int ncu = vl_num_cus();
   const bool fast = fast_shape(a.dtype, a.H, a.Hkv, a.D, a.bs);
   if (fast) {
-    attend_decode_bf16_kernel<<<ncu * 8, 256, 0, st>>>(
+    attend_decode_bf16_kernel<<<decode_grid(), 256, 0, st>>>(
         (uint16_t*)a.out, (const uint16_t*)a.query, a.q_stride, (const uint16_t*)a.kc,
         (const uint16_t*)a.vc, a.bt, a.bt_stride, a.seq_lens, a.qsl, a.S, a.Hkv, sl2, L.hdr,
-        L.fast_off, L.nparts, L.split_base, L.ml, L.po);
+        L.hdr + 8, L.fast_off, L.nparts, L.split_base, L.ml, L.po);
     VL_CHECK_LAUNCH();
-    combine_decode_bf16_kernel<<<a.S < 4096 ? a.S : 4096, 256, 0, st>>>(
-        (uint16_t*)a.out, a.qsl, a.seq_lens, a.S, a.H, L.nparts, L.split_base, L.ml, L.po);
+    const int64_t units = (int64_t)a.S * a.H;
+    const int cgrid = (int)std::min<int64_t>((units + 3) / 4, (int64_t)ncu * 16);
+    combine_decode_bf16_kernel<<<cgrid, 256, 0, st>>>((uint16_t*)a.out, a.qsl, a.seq_lens, a.S,
+                                                       a.H, L.nparts, L.split_base, L.ml, L.po,
+                                                       L.hdr + 8);
     VL_CHECK_LAUNCH();
     if (max_q == 1) return VL_OK;  // every sequence was a decode: nothing else to run
   }

@@ -18,7 +18,10 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.normpath(os.path.join(HERE, "..", "csrc"))
 INCLUDE = os.path.normpath(os.path.join(HERE, "..", "..", "include"))
 LIB_DIR = os.path.join(HERE, "lib")
-LIB_PATH = os.path.join(LIB_DIR, "libvllmlite_hip.so")
+DEFAULT_LIB_PATH = os.path.join(LIB_DIR, "libvllmlite_hip.so")
+# another build of the same sources (e.g. compiled with different -D tuning
+# constants) can be loaded instead by naming it in VLLMLITE_HIP_LIB
+LIB_PATH = os.environ.get("VLLMLITE_HIP_LIB") or DEFAULT_LIB_PATH
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 HIP_FLAGS = [
@@ -32,17 +35,18 @@ def sources():
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIB_PATH + ".tmp"
-    cmd = [HIPCC, *HIP_FLAGS, "-I", INCLUDE, "-I", CSRC, *sources(), "-o", tmp]
+def build(verbose: bool = False, out: str = DEFAULT_LIB_PATH, defines=()) -> str:
+    os.makedirs(os.path.dirname(out), exist_ok=True)
+    tmp = out + ".tmp"
+    cmd = [HIPCC, *HIP_FLAGS, *[f"-D{d}" for d in defines], "-I", INCLUDE, "-I", CSRC,
+           *sources(), "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed ({r.returncode}):\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
