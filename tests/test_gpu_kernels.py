@@ -322,3 +322,31 @@ def test_tile_many_rows_per_kv_head():
     """A 512-token chunk: 2048 (token, head) rows per KV head, 32 row blocks."""
     b = make_batch([(512, 512 + 300), (1, 2000)], 32, 8, 128, 16, seed=42)
     check(run_attention(b, "bf16"), expected(b, "bf16"), "bf16")
+
+
+def test_bandwidth_decode_split_merge_across_repeated_runs():
+    """A ragged decode batch (contexts 64..6000, so many sequences are split
+    into ranges merged inside the kernel) run 4 times under one plan with
+    fresh K/V each time: a merge that read another run's partials, or a
+    counter left non-zero, would fail a later run."""
+    o = ops()
+    rng = np.random.default_rng(50)
+    ctxs = [int(c) for c in np.clip(rng.lognormal(np.log(900), 0.8, size=48), 64, 6000)]
+    b0 = make_batch([(1, c) for c in ctxs], 32, 8, 128, 16, seed=51)
+    S = len(ctxs)
+    ws = o.AttentionWorkspace().get(o.paged_attention_workspace_size(S, S, 32, 128, max(ctxs)))
+    bt, sl, qsl = dev(b0["block_tables"]), dev(b0["seq_lens"]), dev(b0["qsl"])
+    for run in range(4):
+        r = np.random.default_rng(200 + run)
+        b = dict(b0)
+        b["q"] = r.standard_normal(b0["q"].shape).astype(np.float32)
+        for name in ("k_cache", "v_cache"):
+            fresh = r.standard_normal(b0[name].shape).astype(np.float32)
+            b[name] = np.where(np.isnan(b0[name]), np.nan, fresh).astype(np.float32)
+        q = dev(b["q"], torch.bfloat16)
+        kc, vc = dev(b["k_cache"], torch.bfloat16), dev(b["v_cache"], torch.bfloat16)
+        if run == 0:
+            o.paged_attention_plan(q, kc, sl, qsl, 16, ws)
+        out = torch.empty_like(q)
+        o.paged_attention_run(out, q, kc, vc, bt, sl, qsl, b["scale"], 16, ws, max_query_len=1)
+        check(to_np(out), expected(b, "bf16"), "bf16")

@@ -30,8 +30,10 @@
 
 namespace {
 
-constexpr int kHdrInts = 64;  // [0] fast items [1] generic items [2] partition len [3] split rows
-                              // [4] tile items [8] bandwidth-kernel work counter
+constexpr int kHdrInts = 64;  // [0] bandwidth-kernel items [1] generic items [2] partition len
+                              // [3] split rows [4] tile items [5] full ranges [6] tail ranges
+                              // [7] range length [8] bandwidth-kernel work counter
+                              // [9] bandwidth-kernel workgroups finished
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxHeadDim = 256;
 constexpr int kSplitMaxQ = 16;  // only sequences with <= this many queries split their context
@@ -50,7 +52,7 @@ constexpr int kFChunk = 16;  // blocks per softmax chunk (256 tokens)
 #define VL_BK 4
 #endif
 #ifndef VL_BV
-#define VL_BV 4
+#define VL_BV 2
 #endif
 constexpr int kBK = VL_BK;  // blocks per K load burst
 constexpr int kBV = VL_BV;  // blocks per V load burst
@@ -67,13 +69,14 @@ struct Layout {
   int32_t* tile_off;    // [S+1] MFMA tile workgroup items
   int32_t* nparts;      // [S]
   int32_t* split_base;  // [S] first partial row, or -1
+  int32_t* tail_order;  // [S] sequences with a short last range, longest first
   float2* ml;           // [cap_rows] (running max (log2 domain), running sum)
   float* po;            // [cap_rows, D] unnormalised partial outputs
   int64_t cap_rows;
 };
 
 inline size_t plan_bytes(int S) {
-  size_t b = kHdrInts * 4 + (size_t)(5 * S + 3) * 4;
+  size_t b = kHdrInts * 4 + (size_t)(6 * S + 3) * 4;
   return (b + 255) & ~(size_t)255;
 }
 
@@ -86,6 +89,7 @@ inline Layout make_layout(void* ws, size_t bytes, int S, int D) {
   L.tile_off = L.gen_off + S + 1;
   L.nparts = L.tile_off + S + 1;
   L.split_base = L.nparts + S;
+  L.tail_order = L.split_base + S;
   const size_t pb = plan_bytes(S);
   const size_t per_row = (size_t)(D + 2) * 4;
   // rows: 8-byte (m, l) pairs, then a 256-byte aligned [rows, D] float array
@@ -157,90 +161,168 @@ __device__ int64_t block_exclusive_scan(int64_t v, int64_t* total) {
 
 struct SeqWork {
   int np;        // context partitions
-  int64_t fast;  // bandwidth-kernel workgroup items
+  int64_t full;  // bandwidth kernel: ranges of exactly R tokens
+  int64_t tail;  // bandwidth kernel: 1 if the last range is shorter
   int64_t tile;  // MFMA tile workgroup items
   int64_t gen;   // generic wavefront items
   int64_t rows;  // split partial rows
 };
 
 // Routing: single-query sequences of the bandwidth shape go to the decode
-// kernel; everything else goes to the MFMA tile kernel when the shape has one
-// (one workgroup per 64-row block of (token, head-in-group) rows per KV head
-// and partition), else to the generic kernel.
-__device__ __forceinline__ SeqWork seq_work(int q, int c, int P, int H, int Hkv, bool fast,
+// kernel, whose context is cut into ranges of R tokens (the last one
+// shorter); everything else goes to the MFMA tile kernel when the shape has
+// one (one workgroup per 64-row block of (token, head-in-group) rows per KV
+// head and partition of P tokens), else to the generic kernel.
+__device__ __forceinline__ bool is_bw(int q, int c, bool fast) { return fast && q == 1 && c > 0; }
+
+__device__ __forceinline__ SeqWork seq_work(int q, int c, int P, int R, int H, int Hkv, bool fast,
                                             bool tile) {
   SeqWork w;
-  w.np = (q > 0 && q <= kSplitMaxQ && c > P) ? (c + P - 1) / P : 1;
   const bool live = q > 0 && c > 0;
-  const bool bw = fast && q == 1 && live;
+  const bool bw = is_bw(q, c, fast);
   const bool tl = !bw && tile && live;
-  w.fast = bw ? (int64_t)w.np * (Hkv / 4) : 0;
+  if (bw) {
+    w.np = (c + R - 1) / R;
+    w.full = c / R;
+    w.tail = (c % R) != 0;
+  } else {
+    w.np = (q > 0 && q <= kSplitMaxQ && c > P) ? (c + P - 1) / P : 1;
+    w.full = w.tail = 0;
+  }
   w.tile = tl ? (int64_t)w.np * Hkv * cdiv(q * (H / Hkv), kTileRows) : 0;
   w.gen = (bw || tl) ? 0 : (int64_t)max(q, 0) * H * w.np;
-  w.rows = w.np > 1 ? (int64_t)q * H * w.np : 0;
+  // a split decode sequence also keeps one arrival counter per KV head in
+  // the rows after its partials
+  w.rows = w.np > 1 ? (int64_t)q * H * w.np + (bw ? Hkv : 0) : 0;
   return w;
 }
 
+#ifndef VL_RANGE_MAX
+#define VL_RANGE_MAX 1024
+#endif
+#ifndef VL_ITEMS_PER_WG
+#define VL_ITEMS_PER_WG 4
+#endif
+constexpr int kRangeMax = VL_RANGE_MAX;       // longest decode range the planner starts with
+constexpr int kItemsPerWg = VL_ITEMS_PER_WG;  // decode items aimed for per resident workgroup
+constexpr int kTailBuckets = 1024;
+static_assert(kTailBuckets == kPlanThreads, "one tail bucket per plan thread");
+
+// One workgroup. Chooses the bandwidth kernel's range length R (the smallest
+// power of two in 64..kRangeMax that leaves at most target_items (range, KV head)
+// items, i.e. a few per resident workgroup: longer ranges mean fewer split
+// partials to write and merge, shorter ones keep every CU busy) and the
+// multi-query partition length P (256), doubling both until the split
+// partials fit the workspace. Then writes per-sequence offsets and the order
+// in which the shorter last ranges are handed out: longest first, after all
+// full ranges, so the kernel ends on its smallest items.
 __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H, int Hkv,
-    bool fast, bool tile, int64_t cap_rows, int32_t* __restrict__ hdr,
+    bool fast, bool tile, int64_t cap_rows, int target_items, int32_t* __restrict__ hdr,
     int32_t* __restrict__ fast_off, int32_t* __restrict__ gen_off,
     int32_t* __restrict__ tile_off, int32_t* __restrict__ nparts,
-    int32_t* __restrict__ split_base) {
-  __shared__ unsigned long long need;
-  __shared__ int part_len;
+    int32_t* __restrict__ split_base, int32_t* __restrict__ tail_order,
+    float2* __restrict__ ml) {
+  __shared__ unsigned long long need, bw_tokens;
+  __shared__ int part_len, range_len;
+  __shared__ int hist[kTailBuckets];
   const int t = threadIdx.x;
-  if (t == 0) part_len = kPart0;
+  if (t == 0) part_len = kPart0, bw_tokens = 0;
+  for (int k = t; k < kTailBuckets; k += kPlanThreads) hist[k] = 0;
   __syncthreads();
-  // 1. smallest power-of-two multiple of kPart0 whose split partials fit
+  // 0. range length from the decode tokens and the target item count
+  {
+    unsigned long long mine = 0;
+    for (int i = t; i < S; i += kPlanThreads) {
+      const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
+      if (is_bw(q, c, fast)) mine += (unsigned long long)c;
+    }
+    if (mine) atomicAdd(&bw_tokens, mine);
+    __syncthreads();
+    if (t == 0) {
+      int R = 64;
+      while (R < kRangeMax && bw_tokens * (unsigned long long)Hkv >
+                             (unsigned long long)max(target_items, 1) * (unsigned long long)R)
+        R *= 2;
+      range_len = R;
+    }
+    __syncthreads();
+  }
+  // 1. double P and R until the split partials fit
   for (;;) {
     if (t == 0) need = 0;
     __syncthreads();
-    const int P = part_len;
+    const int P = part_len, R = range_len;
     unsigned long long mine = 0;
     for (int i = t; i < S; i += kPlanThreads)
-      mine += seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, H, Hkv, fast, tile).rows;
+      mine += seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, R, H, Hkv, fast, tile).rows;
     if (mine) atomicAdd(&need, mine);
     __syncthreads();
-    const bool fits = need <= (unsigned long long)cap_rows || P >= (1 << 30);
+    const bool fits = need <= (unsigned long long)cap_rows || (P >= (1 << 29) && R >= (1 << 29));
     __syncthreads();
     if (fits) break;
-    if (t == 0) part_len = P * 2;
+    if (t == 0) part_len = min(P * 2, 1 << 29), range_len = min(R * 2, 1 << 29);
     __syncthreads();
   }
-  const int P = part_len;
+  const int P = part_len, R = range_len;
   // 2. offsets; every thread owns a contiguous chunk of sequences
   const int chunk = (S + kPlanThreads - 1) / kPlanThreads;
   const int s0 = min(S, t * chunk), s1 = min(S, s0 + chunk);
-  int64_t f = 0, g = 0, r = 0, x = 0;
+  // tail ranges are bucketed by their length in blocks, longest first
+  const int rblocks = R / kFBs;
+  auto tail_key = [&](int c) {
+    const int blocks = ((c % R) + kFBs - 1) / kFBs;  // 1 .. rblocks
+    const int k = rblocks <= kTailBuckets ? blocks - 1
+                                          : (int)((int64_t)(blocks - 1) * kTailBuckets / rblocks);
+    return kTailBuckets - 1 - k;  // ascending key = descending length
+  };
+  int64_t f = 0, g = 0, r = 0, x = 0, tl = 0;
   for (int i = s0; i < s1; ++i) {
-    const SeqWork w = seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, H, Hkv, fast, tile);
-    f += w.fast, g += w.gen, r += w.rows, x += w.tile;
+    const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
+    const SeqWork w = seq_work(q, c, P, R, H, Hkv, fast, tile);
+    f += w.full, g += w.gen, r += w.rows, x += w.tile, tl += w.tail;
+    if (w.tail) atomicAdd(&hist[tail_key(c)], 1);
   }
-  int64_t tf, tg, tr, tx;
+  int64_t tf, tg, tr, tx, ttl;
   int64_t fo = block_exclusive_scan(f, &tf);
   int64_t go = block_exclusive_scan(g, &tg);
   int64_t ro = block_exclusive_scan(r, &tr);
   int64_t xo = block_exclusive_scan(x, &tx);
+  block_exclusive_scan(tl, &ttl);
+  // bucket starts (kTailBuckets == kPlanThreads: one bucket per thread)
+  int64_t dummy;
+  const int64_t hstart = block_exclusive_scan(hist[t], &dummy);
+  __syncthreads();
+  hist[t] = (int)hstart;
+  __syncthreads();
   for (int i = s0; i < s1; ++i) {
-    const SeqWork w = seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, H, Hkv, fast, tile);
+    const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
+    const SeqWork w = seq_work(q, c, P, R, H, Hkv, fast, tile);
     fast_off[i] = (int32_t)fo;
     gen_off[i] = (int32_t)go;
     tile_off[i] = (int32_t)xo;
     nparts[i] = w.np;
     split_base[i] = w.np > 1 ? (int32_t)ro : -1;
-    fo += w.fast, go += w.gen, ro += w.rows, xo += w.tile;
+    if (w.tail) tail_order[atomicAdd(&hist[tail_key(c)], 1)] = i;
+    if (w.np > 1 && is_bw(q, c, fast))  // arrival counters start at 0
+      for (int k = 0; k < Hkv; ++k)
+        reinterpret_cast<int32_t*>(ml + ro + (int64_t)H * w.np + k)[0] = 0;
+    fo += w.full, go += w.gen, ro += w.rows, xo += w.tile;
   }
   if (t == 0) {
     fast_off[S] = (int32_t)tf;
     gen_off[S] = (int32_t)tg;
     tile_off[S] = (int32_t)tx;
-    hdr[0] = (int32_t)tf;
+    hdr[0] = (int32_t)((tf + ttl) * Hkv);
     hdr[1] = (int32_t)tg;
     hdr[2] = P;
     hdr[3] = (int32_t)tr;
     hdr[4] = (int32_t)tx;
+    hdr[5] = (int32_t)tf;
+    hdr[6] = (int32_t)ttl;
+    hdr[7] = R;
     hdr[8] = 0;
+    hdr[9] = 0;
   }
 }
 
@@ -644,6 +726,13 @@ __device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float c) {
   return c;
 }
 
+// Two floats as one 64-bit word (for 8-byte device-scope stores and loads).
+__device__ __forceinline__ uint64_t pack2(float lo, float hi) {
+  return (uint64_t)__float_as_uint(lo) | ((uint64_t)__float_as_uint(hi) << 32);
+}
+__device__ __forceinline__ float lo_f(uint64_t w) { return __uint_as_float((uint32_t)w); }
+__device__ __forceinline__ float hi_f(uint64_t w) { return __uint_as_float((uint32_t)(w >> 32)); }
+
 // sum over the 4 lanes of a quad, result in every lane (DPP quad_perm)
 __device__ __forceinline__ float quad_sum(float v) {
   v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
@@ -663,20 +752,35 @@ __device__ __forceinline__ float stride4_sum(float v) {
   return v;
 }
 
-// One workgroup item = (decode sequence, context partition, group of 4 KV
-// heads); wavefront w takes KV head 4*group + w. Per 16-token block a
-// wavefront reads 4 KB of K and 4 KB of V for its KV head. The groups of one
-// partition are adjacent items.
-//   Split sequences write unnormalised partials and (max, sum) per head;
-//   combine_decode_bf16_kernel merges them. (Merging in the last-arriving
-//   workgroup needs a device-scope release per workgroup, which on gfx950
-//   writes back the XCD's whole L2 and made the kernel 3x slower.)
-//   QK: lane l reads token l/4 of the block, 16-byte chunks (l&3)+4j of the
+// One workgroup item = (decode sequence, KV head, range of the context);
+// the 4 wavefronts split the range's 16-token blocks (wavefront w takes
+// blocks w, w + 4, ...), each for the KV head's 4 query heads, and merge
+// their (max, sum, output) in LDS at the end, so an item writes one output
+// row per query head, or one partial row when the sequence has several
+// ranges. Items are (range, KV head) with the KV heads of a range adjacent;
+// full ranges come first, then the shorter last ranges, longest first.
+// Persistent workgroups claim items from a counter.
+//   QK: lane l reads token l/4 of a block, 16-byte chunks (l&3)+4j of the
 //       head row (j < 4); four v_dot2_f32_bf16 per chunk and query head,
 //       then a quad DPP sum gives every lane of the quad the 4 heads' scores.
-//   PV: lane l reads dims chunk l&15 of tokens (l>>4)+4t (t < 4); the
-//       probabilities of those tokens come through LDS; accumulators are 4
-//       heads x 8 dims per lane, summed over the 4 token groups at the end.
+//   softmax: scores through LDS, per head max over the wavefront's chunk of
+//       up to 16 blocks, exponentials rounded to bf16 (the sum adds the
+//       rounded values).
+//   PV: lane l reads dims chunk l&15 of tokens (l>>4)+4t (t < 4); token
+//       pairs (t, t + 4) become bf16 pairs for v_dot2_f32_bf16; 4 heads x 8
+//       dims of fp32 accumulators per lane, summed over the 4 token groups
+//       at the end.
+//   Split sequences are merged in the kernel, by the last workgroup to
+//   finish a range of the (sequence, KV head): every workgroup writes its
+//   unnormalised partial and (max, sum) per query head with device-scope
+//   stores (written through to the point of coherence of all XCDs), waits
+//   until they have completed, then counts itself in the sequence's arrival
+//   counter with a device-scope atomic; the one that sees the count complete
+//   reads the partials with device-scope loads, merges them (max-rescaled
+//   log-sum-exp) and resets the counter. No cache-wide fence is needed: a
+//   device-scope release or acquire writes back / invalidates the XCD's
+//   whole L2 on gfx950, which made a fenced version 3x slower.
+//   The last workgroup to leave resets the work counter for the next run.
 __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
     uint16_t* __restrict__ out, const uint16_t* __restrict__ query, int64_t q_stride,
     // not __restrict__: restrict-qualified loads are treated as invariant and
@@ -684,22 +788,31 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
     const uint16_t* kc, const uint16_t* vc,
     const int32_t* __restrict__ bt, int bt_stride, const int32_t* __restrict__ seq_lens,
     const int32_t* __restrict__ qsl, int S, int Hkv, float scale_log2,
-    const int32_t* __restrict__ hdr, int32_t* work, const int32_t* __restrict__ item_off,
-    const int32_t* __restrict__ nparts, const int32_t* __restrict__ split_base,
-    float2* __restrict__ ml, float* __restrict__ po) {
+    const int32_t* __restrict__ hdr, int32_t* work, const int32_t* __restrict__ full_off,
+    const int32_t* __restrict__ tail_order, const int32_t* __restrict__ nparts,
+    const int32_t* __restrict__ split_base, float2* ml, float* po) {
   __shared__ float4 p_lds[4][kFChunk * 16];  // per wave: [block][token] -> 4 heads
-  __shared__ int next_lds;
   __shared__ uint4 q_lds[4][kFRep * 16];       // per wave: 4 heads x 128 bf16
-  __shared__ float4 acc_lds[4][8 * 64];        // per wave: accumulators between chunks
+  __shared__ float4 acc_lds[4][8 * 64];        // per wave: accumulators between chunks,
+                                               // then its merged [head][dim] result
+  __shared__ float2 wml_lds[4][kFRep];         // per wave: (max, sum) per head
+  __shared__ int next_lds, last_lds;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int qp = lane & 3, tk = lane >> 2;     // QK mapping
   const int vcn = lane & 15, vg = lane >> 4;  // PV mapping
   const int n_items = hdr[0];
-  const int P = hdr[2];
+  const int n_full = hdr[5];
+  const int R = hdr[7];
   const int H = Hkv * kFRep;
   const int64_t tok_stride = (int64_t)Hkv * kFD;  // elements per cache slot
   float4* pw = p_lds[wave];
+  uint4* qw = q_lds[wave];
+  float4* stash = acc_lds[wave] + lane;  // stash[64 * k]: conflict-free
+  float* pf = reinterpret_cast<float*>(pw);  // [block][token][head] scores, then probabilities
+  const int64_t blk_bytes = (int64_t)kFBs * tok_stride * 2;
+  const char* kbytes = reinterpret_cast<const char*>(kc);
+  const char* vbytes = reinterpret_cast<const char*>(vc);
 
   // Persistent workgroups (as many as fit on the chip): the first item is
   // blockIdx.x, later ones are claimed from the work counter, the next one at
@@ -709,50 +822,58 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
   while (it < n_items) {
     int nxt = 0;
     if (threadIdx.x == 0) nxt = (int)gridDim.x + atomicAdd(work, 1);
-    const int i = wave_upper_bound_le(item_off, S + 1, it);
-    const int local = it - item_off[i];
+    const int unit = it / Hkv;
+    const int kvh = it - unit * Hkv;
+    int i, part;
+    if (unit < n_full) {
+      i = wave_upper_bound_le(full_off, S + 1, unit);
+      part = unit - full_off[i];
+    } else {
+      i = tail_order[unit - n_full];
+      part = seq_lens[i] / R;
+    }
     const int np = nparts[i];
-    const int groups = Hkv >> 2;
-    const int part = local / groups;
-    const int kvh = (local - part * groups) * 4 + wave;
     const int ctx = seq_lens[i];
     const int tok = qsl[i];
-    const int kbeg = np > 1 ? part * P : 0;
-    const int kend = np > 1 ? min(ctx, kbeg + P) : ctx;
+    const int kbeg = part * R;
+    const int kend = min(ctx, kbeg + R);
     const int32_t* table = bt + (int64_t)i * bt_stride;
+    // blocks of this wavefront: kbeg/16 + wave + 4k, k < nw
+    const int ublk = (kend - kbeg + kFBs - 1) / kFBs;
+    const int nw = ublk > wave ? (ublk - wave + 3) >> 2 : 0;
+    const int wb0 = kbeg / kFBs + wave;  // first block; stride 4
 
     // query of the 4 heads to LDS: [head][16-byte chunk]
-    uint4* qw = q_lds[wave];
     {
       const uint16_t* qb = query + (int64_t)tok * q_stride + (int64_t)kvh * kFRep * kFD;
       qw[lane] = *reinterpret_cast<const uint4*>(qb + lane * 8);
     }
     const int64_t kv_off = (int64_t)kvh * kFD;
-
-    float m_run = -__builtin_inff();  // per head qp (lanes share qp)
-    float l_run = 0.f;
-    float4* stash = acc_lds[wave] + lane;  // stash[64 * k]: conflict-free
-    // every LDS region here is private to its wavefront: no workgroup barriers
-    float* pf = reinterpret_cast<float*>(pw);  // [block][token][head] scores, then probabilities
     // byte offsets of this lane inside a block (a block is 16 slots x Hkv x 128 bf16)
     const uint32_t k_lane = (uint32_t)((tk * tok_stride + kv_off) * 2) + qp * 16;
     const uint32_t v_lane = (uint32_t)((vg * tok_stride + kv_off) * 2) + vcn * 16;
     const uint32_t v_tstep = (uint32_t)(4 * tok_stride * 2);
-    const int64_t blk_bytes = (int64_t)kFBs * tok_stride * 2;
-    const char* kbytes = reinterpret_cast<const char*>(kc);
-    const char* vbytes = reinterpret_cast<const char*>(vc);
-    for (int c0 = kbeg; c0 < kend; c0 += kFChunk * kFBs) {
-      const int nblk = min(kFChunk, (kend - c0 + kFBs - 1) / kFBs);
-      const int b0 = c0 / kFBs;
+
+    float m_run = -__builtin_inff();  // per head qp (lanes share qp)
+    float l_run = 0.f;
+    float acc[kFRep][8];  // (re)defined before each chunk's PV pass
+#pragma unroll
+    for (int h = 0; h < kFRep; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+    // every LDS region above is private to its wavefront until the merge
+    for (int c = 0; c < nw; c += kFChunk) {
+      const int nblk = min(kFChunk, nw - c);
       // block ids of the chunk: lane b holds block b, broadcast with readlane
-      const int my_bid = lane < nblk ? table[b0 + lane] : 0;
-      // ---- QK: 4 blocks per step, loads issued back to back (blocks past the
-      // chunk end re-read the last block and are masked)
+      const int my_bid = lane < nblk ? table[wb0 + 4 * (c + lane)] : 0;
+      const int key0 = (wb0 + 4 * c) * kFBs;  // first key of chunk block 0; block b adds 64 b
+      // ---- QK: kBK blocks per step, loads issued back to back (blocks past
+      // the chunk end re-read the last block and are masked)
       float cmax = -__builtin_inff();
 #pragma unroll 1
       for (int g = 0; g < nblk; g += kBK) {
         // keeps the query reads below inside the loop: hoisting them would pin
-        // 64 registers for the whole item and halve the occupancy
+        // 64 registers for the whole item and lower the occupancy
         asm volatile("" ::: "memory");
         uint4 kb[kBK][4];
 #pragma unroll
@@ -762,7 +883,7 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
 #pragma unroll
           for (int j = 0; j < 4; ++j) kb[u][j] = *reinterpret_cast<const uint4*>(bp + j * 64);
         }
-        // all 16 loads of the group go out before any of them is consumed
+        // all loads of the group go out before any of them is consumed
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
         // one query head at a time (its 4 chunks from LDS): 16 registers of
@@ -788,7 +909,7 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
 #pragma unroll
           for (int h = 0; h < kFRep; ++h) a[h] = quad_sum(a4[u][h]);
           const float mine = qp == 0 ? a[0] : qp == 1 ? a[1] : qp == 2 ? a[2] : a[3];
-          const int key = c0 + (g + u) * kFBs + tk;
+          const int key = key0 + (g + u) * 4 * kFBs + tk;
           const bool ok = (g + u < nblk) && key < kend;
           const float sv = ok ? mine * scale_log2 : -__builtin_inff();
           cmax = fmaxf(cmax, sv);
@@ -810,12 +931,12 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
       float lsum = 0.f;
       // through every block the PV pass reads (bursts of kBV); blocks past
       // the chunk end get p = 0
-      const int nb4 = (nblk + kBV - 1) / kBV * kBV;
+      const int nbp = (nblk + kBV - 1) / kBV * kBV;
       {
         const int pt = ((lane >> 2) & 3) + 8 * ((lane >> 4) & 1);
         const int pslot = ((lane >> 2) & 3) + 4 * ((lane >> 4) & 1);
         uint32_t* pf32 = reinterpret_cast<uint32_t*>(pf);
-        for (int b = lane >> 5; b < nb4; b += 2) {
+        for (int b = lane >> 5; b < nbp; b += 2) {
           const float s0 = b < nblk ? pf[(b * 16 + pt) * 4 + qp] : -__builtin_inff();
           const float s1 = b < nblk ? pf[(b * 16 + pt + 4) * 4 + qp] : -__builtin_inff();
           const uint16_t h0 = f32_to_bf16(s0 == -__builtin_inff() ? 0.f : exp2f(s0 - m_new));
@@ -827,14 +948,12 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
       lsum = stride4_sum(lsum);
       l_run = l_run * alpha + lsum;
       m_run = m_new;
-      // accumulators: zero on the first chunk, else the stash rescaled
-      float acc[kFRep][8];
-      if (c0 == kbeg) {
+      if (c == 0) {
 #pragma unroll
         for (int h = 0; h < kFRep; ++h)
 #pragma unroll
           for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
-      } else {
+      } else {  // a later chunk: the previous chunks' accumulators, rescaled
 #pragma unroll
         for (int h = 0; h < kFRep; ++h) {
           const float ah = __shfl(alpha, h, 64);
@@ -843,9 +962,9 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
           acc[h][4] = x1.x * ah, acc[h][5] = x1.y * ah, acc[h][6] = x1.z * ah, acc[h][7] = x1.w * ah;
         }
       }
-      // ---- PV: 4 blocks per step; probabilities past the context are 0 and
-      // the V rows there are zeroed so poisoned slots cannot leak in (a NaN
-      // times 0 would)
+      // ---- PV: kBV blocks per step; probabilities past the context are 0
+      // and the V rows there are zeroed so poisoned slots cannot leak in (a
+      // NaN times 0 would)
 #pragma unroll 1
       for (int g = 0; g < nblk; g += kBV) {
         uint4 vb[kBV][4];
@@ -866,9 +985,9 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
         for (int u = 0; u < kBV; ++u) {
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
-            const int key0 = c0 + (g + u) * kFBs + vg + 8 * j;
-            const uint32_t keep0 = key0 < kend ? 0xffffffffu : 0u;
-            const uint32_t keep1 = key0 + 4 < kend ? 0xffffffffu : 0u;
+            const int key = key0 + (g + u) * 4 * kFBs + vg + 8 * j;
+            const uint32_t keep0 = (g + u < nblk && key < kend) ? 0xffffffffu : 0u;
+            const uint32_t keep1 = (g + u < nblk && key + 4 < kend) ? 0xffffffffu : 0u;
             const uint4 w0 = vb[u][2 * j], w1 = vb[u][2 * j + 1];
             const uint32_t a0[4] = {w0.x & keep0, w0.y & keep0, w0.z & keep0, w0.w & keep0};
             const uint32_t a1[4] = {w1.x & keep1, w1.y & keep1, w1.z & keep1, w1.w & keep1};
@@ -891,20 +1010,15 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
           }
         }
       }
+      if (c + kFChunk < nw) {  // another chunk follows: park the accumulators
 #pragma unroll
-      for (int h = 0; h < kFRep; ++h) {
-        stash[64 * (2 * h)] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-        stash[64 * (2 * h + 1)] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+        for (int h = 0; h < kFRep; ++h) {
+          stash[64 * (2 * h)] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+          stash[64 * (2 * h + 1)] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+        }
       }
     }
-    float acc[kFRep][8];
-#pragma unroll
-    for (int h = 0; h < kFRep; ++h) {
-      const float4 x0 = stash[64 * (2 * h)], x1 = stash[64 * (2 * h + 1)];
-      acc[h][0] = x0.x, acc[h][1] = x0.y, acc[h][2] = x0.z, acc[h][3] = x0.w;
-      acc[h][4] = x1.x, acc[h][5] = x1.y, acc[h][6] = x1.z, acc[h][7] = x1.w;
-    }
-    // ---- sum the 4 token groups, then lanes 0..15 write 8 dims x 4 heads
+    // ---- sum the 4 token groups; lanes 0..15 then hold 8 dims x 4 heads
 #pragma unroll
     for (int h = 0; h < kFRep; ++h)
 #pragma unroll
@@ -914,90 +1028,103 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
         a += __shfl_xor(a, 32, 64);
         acc[h][e] = a;
       }
-    float l_h[kFRep], m_h[kFRep];
-#pragma unroll
-    for (int h = 0; h < kFRep; ++h) {
-      l_h[h] = __shfl(l_run, h, 64);
-      m_h[h] = __shfl(m_run, h, 64);
-    }
+    // ---- merge the 4 wavefronts through LDS (the wave's stash area holds its
+    // [head][128] result)
+    float* wres = reinterpret_cast<float*>(acc_lds[wave]);
     if (vg == 0) {
+#pragma unroll
+      for (int h = 0; h < kFRep; ++h) {
+        float4* dst = reinterpret_cast<float4*>(wres + h * kFD + vcn * 8);
+        dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+        dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+      }
+    }
+    if (lane < kFRep) wml_lds[wave][lane] = make_float2(m_run, l_run);  // lane h holds head h
+    __syncthreads();
+    {
+      // thread: head h = tid / 64, dims 2 (tid % 64), +1
+      const int h = threadIdx.x >> 6, d = 2 * lane;
+      float M = -__builtin_inff();
+#pragma unroll
+      for (int w = 0; w < 4; ++w) M = fmaxf(M, wml_lds[w][h].x);
+      float L = 0.f, a0 = 0.f, a1 = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float2 v = wml_lds[w][h];
+        const float wt = v.x == -__builtin_inff() ? 0.f : exp2f(v.x - M);
+        const float2 x = *reinterpret_cast<const float2*>(
+            reinterpret_cast<const float*>(acc_lds[w]) + h * kFD + d);
+        L += v.y * wt;
+        a0 += x.x * wt;
+        a1 += x.y * wt;
+      }
+      const int qh = kvh * kFRep + h;
       if (np == 1) {
-#pragma unroll
-        for (int h = 0; h < kFRep; ++h) {
-          const float inv = l_h[h] > 0.f ? 1.f / l_h[h] : 0.f;
-          uint4 o;
-          o.x = (uint32_t)f32_to_bf16(acc[h][0] * inv) | ((uint32_t)f32_to_bf16(acc[h][1] * inv) << 16);
-          o.y = (uint32_t)f32_to_bf16(acc[h][2] * inv) | ((uint32_t)f32_to_bf16(acc[h][3] * inv) << 16);
-          o.z = (uint32_t)f32_to_bf16(acc[h][4] * inv) | ((uint32_t)f32_to_bf16(acc[h][5] * inv) << 16);
-          o.w = (uint32_t)f32_to_bf16(acc[h][6] * inv) | ((uint32_t)f32_to_bf16(acc[h][7] * inv) << 16);
-          *reinterpret_cast<uint4*>(out + ((int64_t)tok * H + kvh * kFRep + h) * kFD + vcn * 8) = o;
-        }
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        reinterpret_cast<uint32_t*>(out + ((int64_t)tok * H + qh) * kFD)[lane] =
+            (uint32_t)f32_to_bf16(a0 * inv) | ((uint32_t)f32_to_bf16(a1 * inv) << 16);
       } else {
-#pragma unroll
-        for (int h = 0; h < kFRep; ++h) {
-          const int64_t prow = (int64_t)split_base[i] + (int64_t)(kvh * kFRep + h) * np + part;
-          float4* dst = reinterpret_cast<float4*>(po + prow * kFD + vcn * 8);
-          dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-          dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
-          if (vcn == 0) ml[prow] = make_float2(m_h[h], l_h[h]);
+        const int64_t prow = (int64_t)split_base[i] + (int64_t)qh * np + part;
+        __hip_atomic_store(reinterpret_cast<uint64_t*>(po + prow * kFD + d), pack2(a0, a1),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0)
+          __hip_atomic_store(reinterpret_cast<uint64_t*>(ml + prow), pack2(M, L), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the stores have completed
+      }
+    }
+    if (np > 1) {  // uniform over the workgroup
+      __syncthreads();  // every thread's partial stores have completed
+      if (threadIdx.x == 0) {
+        int32_t* cnt = reinterpret_cast<int32_t*>(ml + split_base[i] + (int64_t)H * np + kvh);
+        const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_lds = prev == np - 1;
+        if (prev == np - 1) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (last_lds) {
+        asm volatile("" ::: "memory");  // no load below moves above the arrival
+        const int h = threadIdx.x >> 6, d = 2 * lane;
+        const int qh = kvh * kFRep + h;
+        const int64_t r0 = (int64_t)split_base[i] + (int64_t)qh * np;
+        const uint64_t* mlw = reinterpret_cast<const uint64_t*>(ml + r0);
+        float M = -__builtin_inff();
+        for (int p = 0; p < np; ++p)
+          M = fmaxf(M, lo_f(__hip_atomic_load(mlw + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
+        float L = 0.f, a0 = 0.f, a1 = 0.f;
+#pragma unroll 4
+        for (int p = 0; p < np; ++p) {
+          const uint64_t mlp = __hip_atomic_load(mlw + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const uint64_t xp = __hip_atomic_load(
+              reinterpret_cast<const uint64_t*>(po + (r0 + p) * kFD + d), __ATOMIC_RELAXED,
+              __HIP_MEMORY_SCOPE_AGENT);
+          const float m = lo_f(mlp);
+          const float wt = m == -__builtin_inff() ? 0.f : exp2f(m - M);
+          L += hi_f(mlp) * wt;
+          a0 += lo_f(xp) * wt;
+          a1 += hi_f(xp) * wt;
         }
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        reinterpret_cast<uint32_t*>(out + ((int64_t)tok * H + qh) * kFD)[lane] =
+            (uint32_t)f32_to_bf16(a0 * inv) | ((uint32_t)f32_to_bf16(a1 * inv) << 16);
       }
     }
     if (threadIdx.x == 0) next_lds = nxt;
-    __syncthreads();
+    __syncthreads();  // the merge has read every wavefront's LDS; next_lds is set
     it = next_lds;
-    __syncthreads();  // every wavefront has read next_lds before it is rewritten
+  }
+  // every work-counter claim of this workgroup has returned (the last one
+  // ended the loop): the last workgroup out resets both counters
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(work + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == (int)gridDim.x - 1) {
+      __hip_atomic_store(work, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(work + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
 // --------------------------------------------------------------- combine --
-
-// Merge of the bandwidth kernel's split sequences: one wavefront per
-// (decode sequence, query head). Lane p first takes partition p's (max, sum)
-// to form the log-sum-exp weights; then each lane owns 2 of the 128 dims and
-// streams the partitions' partial rows with independent loads.
-__global__ void __launch_bounds__(256) combine_decode_bf16_kernel(
-    uint16_t* __restrict__ out, const int32_t* __restrict__ qsl,
-    const int32_t* __restrict__ seq_lens, int S, int H, const int32_t* __restrict__ nparts,
-    const int32_t* __restrict__ split_base, const float2* __restrict__ ml,
-    const float* __restrict__ po, int32_t* __restrict__ work) {
-  // the bandwidth kernel of this run has finished: reset its work counter
-  if (blockIdx.x == 0 && threadIdx.x == 0) *work = 0;
-  const int lane = threadIdx.x & 63;
-  const int64_t n_units = (int64_t)S * H;
-  for (int64_t u = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); u < n_units;
-       u += (int64_t)gridDim.x * 4) {
-    const int i = (int)(u / H), h = (int)(u - (u / H) * H);
-    const int np = nparts[i];
-    if (np <= 1 || qsl[i + 1] - qsl[i] != 1 || seq_lens[i] <= 0) continue;
-    const int64_t row0 = (int64_t)split_base[i] + (int64_t)h * np;
-    float M = -__builtin_inff();
-    for (int p = lane; p < np; p += 64) M = fmaxf(M, ml[row0 + p].x);
-    M = wave_max(M);
-    float L = 0.f, a0 = 0.f, a1 = 0.f;
-    for (int p0 = 0; p0 < np; p0 += 64) {
-      float w = 0.f;
-      if (p0 + lane < np) {
-        const float2 v = ml[row0 + p0 + lane];
-        w = v.x == -__builtin_inff() ? 0.f : exp2f(v.x - M);
-        L += v.y * w;
-      }
-      const int n = min(64, np - p0);
-      const float* src = po + (row0 + p0) * kFD + 2 * lane;
-#pragma unroll 8
-      for (int p = 0; p < n; ++p) {
-        const float wp = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), p));
-        const float2 x = *reinterpret_cast<const float2*>(src + (int64_t)p * kFD);
-        a0 += wp * x.x;
-        a1 += wp * x.y;
-      }
-    }
-    L = wave_sum(L);
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    reinterpret_cast<uint32_t*>(out + ((int64_t)qsl[i] * H + h) * kFD)[lane] =
-        (uint32_t)f32_to_bf16(a0 * inv) | ((uint32_t)f32_to_bf16(a1 * inv) << 16);
-  }
-}
 
 template <typename T>
 __global__ void __launch_bounds__(64) combine_kernel(
@@ -1088,9 +1215,11 @@ int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
   const Layout L = make_layout(ws, ws_bytes, a.S, a.D);
   const bool fast = fast_shape(a.dtype, a.H, a.Hkv, a.D, a.bs);
   const bool tile = tile_shape(a.dtype, a.D);
+  // a few bandwidth-kernel items per resident workgroup
+  const int target_items = fast ? kItemsPerWg * decode_grid() : 0;
   plan_kernel<<<1, kPlanThreads, 0, st>>>(a.seq_lens, a.qsl, a.S, a.H, a.Hkv, fast, tile,
-                                          L.cap_rows, L.hdr, L.fast_off, L.gen_off, L.tile_off,
-                                          L.nparts, L.split_base);
+                                          L.cap_rows, target_items, L.hdr, L.fast_off, L.gen_off,
+                                          L.tile_off, L.nparts, L.split_base, L.tail_order, L.ml);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
@@ -1135,13 +1264,7 @@ int do_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) 
     attend_decode_bf16_kernel<<<decode_grid(), 256, 0, st>>>(
         (uint16_t*)a.out, (const uint16_t*)a.query, a.q_stride, (const uint16_t*)a.kc,
         (const uint16_t*)a.vc, a.bt, a.bt_stride, a.seq_lens, a.qsl, a.S, a.Hkv, sl2, L.hdr,
-        L.hdr + 8, L.fast_off, L.nparts, L.split_base, L.ml, L.po);
-    VL_CHECK_LAUNCH();
-    const int64_t units = (int64_t)a.S * a.H;
-    const int cgrid = (int)std::min<int64_t>((units + 3) / 4, (int64_t)ncu * 16);
-    combine_decode_bf16_kernel<<<cgrid, 256, 0, st>>>((uint16_t*)a.out, a.qsl, a.seq_lens, a.S,
-                                                       a.H, L.nparts, L.split_base, L.ml, L.po,
-                                                       L.hdr + 8);
+        L.hdr + 8, L.fast_off, L.tail_order, L.nparts, L.split_base, L.ml, L.po);
     VL_CHECK_LAUNCH();
     if (max_q == 1) return VL_OK;  // every sequence was a decode: nothing else to run
   }
@@ -1177,13 +1300,20 @@ extern "C" size_t vl_paged_attention_min_workspace(int num_seqs) {
 extern "C" size_t vl_paged_attention_workspace_size(int num_seqs, int num_tokens, int num_heads,
                                                     int head_dim, int max_context_len) {
   if (num_seqs < 0 || num_tokens < 0 || num_heads <= 0 || head_dim <= 0) return 0;
-  const int64_t split_tokens = num_tokens < (int64_t)num_seqs * kSplitMaxQ
-                                   ? num_tokens
-                                   : (int64_t)num_seqs * kSplitMaxQ;
-  int64_t parts = (max_context_len + kPart0 - 1) / kPart0;
-  if (parts < 1) parts = 1;
-  if (parts > 64) parts = 64;
-  const int64_t rows = parts > 1 ? split_tokens * num_heads * parts : 0;
+  const int64_t S = num_seqs, H = num_heads;
+  const int64_t ctx = max_context_len > 0 ? max_context_len : 1;
+  // multi-query rows split into partitions of 256 tokens (up to 64)
+  const int64_t split_tokens = num_tokens < S * kSplitMaxQ ? num_tokens : S * kSplitMaxQ;
+  int64_t parts = std::min<int64_t>(std::max<int64_t>(cdiv64(ctx, kPart0), 1), 64);
+  const int64_t rows_tile = parts > 1 ? split_tokens * H * parts : 0;
+  // decode ranges: as short as 64 tokens for small batches, at most a few
+  // items per resident workgroup (plus one short range per sequence) and at
+  // most 1024 tokens long otherwise
+  const int64_t rows_fast =
+      std::min<int64_t>(S * H * cdiv64(ctx, 64),
+                        4 * kItemsPerWg * (int64_t)decode_grid() +
+                            S * H * (cdiv64(ctx, kRangeMax) + 1));
+  const int64_t rows = std::max(rows_tile, rows_fast);
   return plan_bytes(num_seqs) + 256 + (size_t)rows * (size_t)(head_dim + 2) * 4;
 }
 
