@@ -1,26 +1,37 @@
 #!/usr/bin/env python3
 """Benchmark of the ragged paged-attention step on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--profile-mode]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e]
+                    [--legs decode,mixed,verify,cow,e2e] [--profile-mode LEG]
+                    [--copy-only]
 
-The timed workload is the 256-sequence ragged decode batch: 256 sequences of
-one query token, context lengths lognormal (median 1024, sigma 0.6) clipped
-to 64..8192, 32 query heads over 8 KV heads, head_dim 128, bf16 Q/K/V
-~N(0,1), block size 16, block tables drawn as consecutive slices of a seeded
-permutation of a 2^17-block pool (8.6 GB of K/V; every block a sequence does
+The headline (`value`) is the 256-sequence ragged decode batch: 256 sequences
+of one query token, context lognormal (median 1024, sigma 0.6) clipped to
+64..8192, 32 query heads over 8 KV heads, head_dim 128, bf16 Q/K/V ~N(0,1),
+block size 16, block tables drawn as consecutive slices of a seeded
+permutation of a 2^17-block pool (8.6 GB of K/V; every slot a sequence does
 not own is NaN). A step is one paged-attention run over that batch with the
-inputs already resident in HBM; the work plan is built once outside the timed
-region, as the runner does once per step for all layers.
+inputs resident in HBM; the work plan is built once outside the timed region,
+as the runner does once per step for all of a model's layers.
 
-The JSON line reports:
+One JSON line:
   value         algorithmic HBM bytes per step / measured step time (GB/s)
-  roofline      the attention kernel's average duration from HIP events on
-                torch's stream, algorithmic bytes / that, against 8 TB/s
-  cpu_baseline  the NumPy oracle (the reference's per-sequence paged_attention
-                on fp32 copies of the same bf16 data), timed on this host
-Algorithmic bytes = sum(ctx) * 2 (K,V) * 8 heads * 128 * 2 B + Q read + out
-write (256 * 32 * 128 * 2 B each) + block-table entries read (4 B per block)
-+ seq_lens (4 B per sequence): each K/V element once, no block padding.
+  roofline      the decode launch's average duration from HIP events on the
+                stream it is launched on; achieved = algorithmic bytes / that,
+                against 8 TB/s; traffic = FETCH_SIZE + WRITE_SIZE bytes per
+                launch from the committed rocprofv3 summary, scaled by the
+                same counters on a 1 GiB copy
+  cpu_baseline  the oracle's NumPy paged_attention (the reference's kernel)
+                on fp32 copies of a bounded sample of the same batch
+  legs          the other synthetic workloads, each with absolute numbers and
+                roofline fractions: mixed prefill+decode in one launch, the
+                speculative-verify step with GPU greedy acceptance, the
+                copy-on-write block copy, and the 48-request end-to-end mix
+                (plus the shared-prefix mix) through HipRunner next to the
+                NumPy runner on this host's cores.
+Algorithmic bytes count each K/V element once and never the padding of a
+partly filled block; flops count 4 * head_dim per unmasked (query, key) pair
+and query head.
 """
 
 from __future__ import annotations
@@ -28,6 +39,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -40,73 +52,67 @@ for _p in (ROOT, os.path.join(ROOT, "vllm-lite_amd")):
 
 METRIC = "paged-attn HBM GB/s (% of peak) + e2e output tok/s on 48-req ragged mix"
 PEAK_HBM_GBS = 8000.0
-S, H, HKV, D, BS, POOL = 256, 32, 8, 128, 16, 1 << 17
-SIGMA = 0.6
+PEAK_BF16_TFLOPS = 2500.0
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "decode_256seq_traffic.md")
 
 
-def decode_lengths(seed=0, n=S, sigma=SIGMA):
-    rng = np.random.default_rng(seed)
-    ctx = np.clip(np.rint(rng.lognormal(np.log(1024.0), sigma, size=n)), 64, 8192).astype(np.int64)
-    return ctx, rng
+def events(torch, n):
+    return [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(n)]
 
 
-def algorithmic_bytes(ctx):
-    nblk = (ctx + BS - 1) // BS
-    return int(ctx.sum() * 2 * HKV * D * 2 + 2 * len(ctx) * H * D * 2 + nblk.sum() * 4 + 4 * len(ctx))
+def mean_ms(ev):
+    return float(np.mean([a.elapsed_time(b) for a, b in ev]))
 
 
-def build_decode_batch(torch, seed=0):
-    """Device tensors of the 256-sequence batch; returns a dict."""
-    ctx, rng = decode_lengths(seed)
-    nblk = (ctx + BS - 1) // BS
-    perm = rng.permutation(POOL).astype(np.int64)
-    W = int(nblk.max())
-    tables = np.zeros((S, W), np.int32)
-    off = 0
-    owned = []
-    for i in range(S):
-        t = perm[off:off + nblk[i]]
-        off += nblk[i]
-        tables[i, :nblk[i]] = t
-        owned.append((t[:, None] * BS + np.arange(BS)[None, :]).reshape(-1)[:ctx[i]])
-    slots = torch.from_numpy(np.concatenate(owned)).cuda()
-    g = torch.Generator(device="cuda")
-    g.manual_seed(seed)
-    dev = "cuda"
-    kc = torch.full((POOL * BS, HKV, D), float("nan"), dtype=torch.bfloat16, device=dev)
-    vc = torch.full((POOL * BS, HKV, D), float("nan"), dtype=torch.bfloat16, device=dev)
-    n = slots.numel()
-    kc[slots] = torch.randn((n, HKV, D), generator=g, device=dev).to(torch.bfloat16)
-    vc[slots] = torch.randn((n, HKV, D), generator=g, device=dev).to(torch.bfloat16)
-    q = torch.randn((S, H, D), generator=g, device=dev).to(torch.bfloat16)
-    qsl = torch.arange(S + 1, dtype=torch.int32, device=dev)
-    return dict(ctx=ctx, tables_np=tables, q=q, kc=kc, vc=vc,
-                bt=torch.from_numpy(tables).cuda(), seq_lens=torch.from_numpy(ctx.astype(np.int32)).cuda(),
-                qsl=qsl, scale=1.0 / np.sqrt(D))
+def decode_leg(torch, ops, syn, steps, warmup, profile_only=False):
+    b = syn.build(torch, syn.decode_256_seqs(0))
+    # this step's K/V are part of the cached context for the decode-only batch
+    b["kc"][b["slot_mapping"].long()] = b["knew"]
+    b["vc"][b["slot_mapping"].long()] = b["vnew"]
+    S = len(b["seqs"])
+    out = torch.empty_like(b["q"])
+    ws = ops.AttentionWorkspace().get(
+        ops.paged_attention_workspace_size(S, S, syn.H, syn.D, int(b["ctx"].max())))
+    ops.paged_attention_plan(b["q"], b["kc"], b["seq_lens"], b["qsl"], syn.BS, ws)
+
+    def step():
+        ops.paged_attention_run(out, b["q"], b["kc"], b["vc"], b["bt"], b["seq_lens"], b["qsl"],
+                                b["scale"], syn.BS, ws, max_query_len=1)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = events(torch, steps)
+    t0 = time.perf_counter()
+    for e0, e1 in ev:
+        e0.record()
+        step()
+        e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    res = {"kernel_ms": mean_ms(ev), "ms_per_step": wall * 1e3 / steps,
+           "bytes": syn.algorithmic_bytes(b, with_scatter=False), "batch": b}
+    if not profile_only:
+        res["check_rel_err"] = syn.torch_reference_check(
+            torch, b, out, np.linspace(0, S - 1, 8).astype(int))
+    return res
 
 
-def spot_check(torch, b, out, n_check=6):
-    """A few sequences against the oracle on fp32 copies (not timed)."""
-    from oracle.attention import gather_slots, paged_attention
-    idx = np.linspace(0, S - 1, n_check).astype(int)
-    worst = 0.0
-    for i in idx:
-        t = b["tables_np"][i, :(b["ctx"][i] + BS - 1) // BS]
-        slots = gather_slots(t, BS, int(b["ctx"][i]))
-        sl = torch.from_numpy(slots).cuda()
-        k = b["kc"][sl].float().cpu().numpy()
-        v = b["vc"][sl].float().cpu().numpy()
-        q = b["q"][i:i + 1].float().cpu().numpy()
-        want = paged_attention(q, k, v, np.arange(len(slots)), HKV, b["scale"])
-        got = out[i:i + 1].float().cpu().numpy()
-        err = np.abs(got - want).max() / max(1e-6, np.abs(want).max())
-        worst = max(worst, float(err))
-    return worst
+def traffic_from_summary():
+    """FETCH_SIZE + WRITE_SIZE bytes per decode launch (copy-calibrated) as
+    recorded in the committed rocprofv3 summary, or None."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", f.read())
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
 
 
 def cpu_baseline(torch, b, budget_s=12.0):
     """The oracle's per-sequence paged_attention (the reference's NumPy
-    kernel) on fp32 copies of a bounded sample of the sequences."""
+    kernel) on fp32 copies of a bounded sample of the decode batch."""
     from oracle.attention import gather_slots, paged_attention
     try:
         from threadpoolctl import threadpool_info
@@ -114,49 +120,206 @@ def cpu_baseline(torch, b, budget_s=12.0):
     except Exception:  # pragma: no cover
         blas_threads = 1
     cores = len(os.sched_getaffinity(0))
-    # compact copy of a sample of sequences (every 8th), fp32
+    S = len(b["seqs"])
     sample = list(range(0, S, 8))
     data = []
     for i in sample:
-        t = b["tables_np"][i, :(b["ctx"][i] + BS - 1) // BS]
-        slots = gather_slots(t, BS, int(b["ctx"][i]))
+        nb = (int(b["ctx"][i]) + b["bs"] - 1) // b["bs"]
+        slots = gather_slots(b["tables_np"][i, :nb], b["bs"], int(b["ctx"][i]))
         sl = torch.from_numpy(slots).cuda()
         data.append((b["q"][i:i + 1].float().cpu().numpy(), b["kc"][sl].float().cpu().numpy(),
                      b["vc"][sl].float().cpu().numpy(), np.arange(len(slots))))
+    ctx = b["ctx"][sample]
+    per_pass = int(ctx.sum()) * 2 * b["Hkv"] * b["D"] * 2 + 2 * len(sample) * b["H"] * b["D"] * 2
     done_bytes, t0, reps = 0, time.perf_counter(), 0
     while True:
-        for (q, k, v, rs), i in zip(data, sample):
-            paged_attention(q, k, v, rs, HKV, b["scale"])
+        for q, k, v, rs in data:
+            paged_attention(q, k, v, rs, b["Hkv"], b["scale"])
         reps += 1
-        done_bytes += algorithmic_bytes(b["ctx"][sample])
+        done_bytes += per_pass
         if time.perf_counter() - t0 > budget_s or reps >= 50:
             break
     dt = time.perf_counter() - t0
-    return {"value": round(done_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": int(min(cores, blas_threads)),
-            "kind": "port",
-            "sample": f"{len(sample)} of {S} sequences (every 8th), {reps} passes, fp32 NumPy, "
-                      f"bytes counted at the bf16 workload size; {cores} visible cores, "
-                      f"BLAS threads {blas_threads}"}
+    return {"value": round(done_bytes / dt / 1e9, 3), "unit": "GB/s",
+            "cores": int(min(cores, blas_threads)), "kind": "port",
+            "sample": f"{len(sample)} of {S} sequences (every 8th), {reps} passes of the oracle's "
+                      f"NumPy paged_attention on fp32 copies, bytes counted at the bf16 size; "
+                      f"{cores} visible cores, BLAS threads {blas_threads}"}
 
 
-def cfg0_engine_config():
+def mixed_leg(torch, ops, syn, steps, warmup, profile_only=False):
+    """Scatter + plan + one attention launch over 16 prefill chunks and 200
+    decodes; also the prefill chunks alone and the decodes alone."""
+    out = {}
+    full = syn.mixed_8392_seqs(0)
+    parts = {"mixed": full, "prefill_only": full[200:], "decode_only": full[:200]}
+    for name, seqs in parts.items():
+        if profile_only and name != "mixed":
+            continue
+        b = syn.build(torch, seqs, seed=2)
+        S, T = len(seqs), int(b["q_lens"].sum())
+        o = torch.empty_like(b["q"])
+        ws = ops.AttentionWorkspace().get(
+            ops.paged_attention_workspace_size(S, T, syn.H, syn.D, int(b["ctx"].max())))
+
+        def step():
+            ops.reshape_and_cache(b["knew"], b["vnew"], b["kc"], b["vc"], b["slot_mapping"])
+            ops.paged_attention_plan(b["q"], b["kc"], b["seq_lens"], b["qsl"], syn.BS, ws)
+            ops.paged_attention_run(o, b["q"], b["kc"], b["vc"], b["bt"], b["seq_lens"], b["qsl"],
+                                    b["scale"], syn.BS, ws, max_query_len=b["max_q"])
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        ev = events(torch, steps)
+        for e0, e1 in ev:
+            e0.record()
+            step()
+            e1.record()
+        torch.cuda.synchronize()
+        ms = mean_ms(ev)
+        nbytes, flops = syn.algorithmic_bytes(b), syn.attention_flops(b)
+        roof_ms = max(nbytes / (PEAK_HBM_GBS * 1e9), flops / (PEAK_BF16_TFLOPS * 1e12)) * 1e3
+        r = {"us": round(ms * 1e3, 1), "tokens": T, "sequences": S, "sum_ctx": int(b["ctx"].sum()),
+             "algorithmic_bytes": nbytes, "attention_flops": flops,
+             "GBs": round(nbytes / ms / 1e6, 1), "hbm_frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
+             "TFLOPs": round(flops / ms / 1e9, 1),
+             "mfma_frac": round(flops / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+             "roofline_us": round(roof_ms * 1e3, 1), "roofline_frac": round(roof_ms / ms, 4)}
+        if not profile_only:
+            pick = [int(i) for i in np.linspace(0, S - 1, 6).astype(int)]
+            r["check_rel_err"] = syn.torch_reference_check(torch, b, o, pick)
+        out[name] = r
+        del b, o, ws
+        torch.cuda.empty_cache()
+    out["workload"] = ("16 prefill chunks x 512 tokens with 0-2048 prior context + 200 decodes "
+                       "with context 128-4096, H32/Hkv8/D128 bf16, block 16; a step = K/V scatter "
+                       "of every new token + plan + one attention launch")
+    return out
+
+
+def verify_leg(torch, ops, syn, steps, warmup, profile_only=False):
+    """64 sequences x 5 query positions over contexts 1024..32768, then
+    greedy acceptance of 4 drafts from fp32 logits [320, 32000]."""
+    b = syn.build(torch, syn.verify_64x5_seqs(0), seed=3)
+    S, T = len(b["seqs"]), int(b["q_lens"].sum())
+    V, K = 32000, 4
+    o = torch.empty_like(b["q"])
+    ws = ops.AttentionWorkspace().get(
+        ops.paged_attention_workspace_size(S, T, syn.H, syn.D, int(b["ctx"].max())))
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    logits = torch.randn((T, V), generator=g, device="cuda")
+    rng = np.random.default_rng(5)
+    accept = rng.integers(0, K + 1, size=S)
+    picks = torch.argmax(logits, dim=1).cpu().numpy()
+    drafts = np.zeros((S, K), np.int32)
+    for s in range(S):
+        for r in range(K):
+            p = int(picks[s * 5 + r])
+            drafts[s, r] = p if r < accept[s] else (p + 1) % V
+    row_start = torch.arange(0, T, 5, dtype=torch.int32, device="cuda")
+    nd = torch.full((S,), K, dtype=torch.int32, device="cuda")
+    dr = torch.from_numpy(drafts).cuda()
+    toks = torch.empty((S, K + 1), dtype=torch.int32, device="cuda")
+    nacc = torch.empty((S,), dtype=torch.int32, device="cuda")
+
+    def step():
+        ops.reshape_and_cache(b["knew"], b["vnew"], b["kc"], b["vc"], b["slot_mapping"])
+        ops.paged_attention_plan(b["q"], b["kc"], b["seq_lens"], b["qsl"], syn.BS, ws)
+        ops.paged_attention_run(o, b["q"], b["kc"], b["vc"], b["bt"], b["seq_lens"], b["qsl"],
+                                b["scale"], syn.BS, ws, max_query_len=5)
+        ops.greedy_verify(logits, row_start, nd, dr, toks, nacc)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = events(torch, steps)
+    for e0, e1 in ev:
+        e0.record()
+        step()
+        e1.record()
+    torch.cuda.synchronize()
+    ms = mean_ms(ev)
+    nbytes = syn.algorithmic_bytes(b) + T * V * 4 + S * (K + 2) * 4 * 2
+    flops = syn.attention_flops(b)
+    r = {"us": round(ms * 1e3, 1), "sum_ctx": int(b["ctx"].sum()), "algorithmic_bytes": nbytes,
+         "attention_flops": flops, "GBs": round(nbytes / ms / 1e6, 1),
+         "hbm_frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
+         "workload": "64 sequences x 5 query positions (4 n-gram drafts + 1), context 1024-32768 "
+                     "uniform, H32/Hkv8/D128 bf16, block 16; a step = scatter + plan + attention "
+                     "+ greedy acceptance on logits [320, 32000] fp32"}
+    if not profile_only:
+        got_acc = nacc.cpu().numpy()
+        got_tok = toks.cpu().numpy()
+        ok = bool((got_acc == accept).all())
+        for s in range(S):
+            want = [int(picks[s * 5 + r]) for r in range(accept[s] + 1)]
+            ok = ok and got_tok[s, :len(want)].tolist() == want and bool((got_tok[s, len(want):] == -1).all())
+        r["acceptance_exact"] = ok
+        r["check_rel_err"] = syn.torch_reference_check(torch, b, o, [0, 21, 42, 63])
+    del b, o, ws, logits
+    torch.cuda.empty_cache()
+    return r
+
+
+def cow_leg(torch, ops, steps, warmup):
+    """Copy-on-write of 48 partially filled shared tail blocks across the 6
+    layers of the TinyLlama fp32 cache (K and V); the copies rotate over 8
+    caches (600 MB) so that the 14 MB copied is not served from the
+    Infinity Cache."""
+    L, slots, hkv, hd, bs = 6, 512 * 16, 4, 48, 16
+    caches = [(torch.randn((L, slots, hkv, hd), device="cuda"),
+               torch.randn((L, slots, hkv, hd), device="cuda")) for _ in range(8)]
+    rng = np.random.default_rng(6)
+    src = rng.integers(0, 256, size=48)
+    dst = 256 + rng.permutation(256)[:48]
+    pairs = torch.from_numpy(np.stack([src, dst], 1).astype(np.int32)).cuda()
+    for _ in range(warmup):
+        ops.copy_blocks(*caches[0], pairs, bs)
+    torch.cuda.synchronize()
+    ev = events(torch, steps)
+    for n, (e0, e1) in enumerate(ev):
+        kc, vc = caches[n % 8]
+        e0.record()
+        ops.copy_blocks(kc, vc, pairs, bs)
+        e1.record()
+    torch.cuda.synchronize()
+    ms = mean_ms(ev)
+    nbytes = 48 * L * bs * hkv * hd * 4 * 2 * 2
+    ok = True
+    for kc, vc in caches:  # every cache has been copied at least once
+        for c in (kc, vc):
+            blk = c.view(L, slots // bs, bs, hkv, hd)
+            ok = ok and bool(torch.equal(blk[:, torch.from_numpy(dst).cuda().long()],
+                                         blk[:, torch.from_numpy(src).cuda().long()]))
+    del caches
+    torch.cuda.empty_cache()
+    return {"us": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
+            "GBs": round(nbytes / ms / 1e6, 1), "hbm_frac": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
+            "bit_exact": ok,
+            "workload": "48 (src, dst) block pairs x 6 layers x K and V, TinyLlama cache "
+                        "[6, 8192 slots, 4, 48] fp32, block 16"}
+
+
+def engine_config(prefix_cache=False):
     """The 48-request mix's engine: TinyLlama 6 layers, d 384, H8/Hkv4, d_ff 1024,
-    vocab 261, max_len 512; 512 blocks of 16, no prefix cache; 16 seqs, budget 1024."""
+    vocab 261, max_len 512; 512 blocks of 16; 16 seqs, budget 1024."""
     from vllmlite_amd.config import CacheConfig, EngineConfig, ModelConfig, SchedulerConfig
     return EngineConfig(
         model=ModelConfig(n_layers=6, n_heads=8, n_kv_heads=4, d_model=384, d_ff=1024,
                           vocab_size=261, max_seq_len=512),
-        cache=CacheConfig(block_size=16, num_blocks=512, enable_prefix_caching=False),
+        cache=CacheConfig(block_size=16, num_blocks=512, enable_prefix_caching=prefix_cache),
         scheduler=SchedulerConfig(max_seqs=16, max_batched_tokens=1024))
 
 
-def run_mix(runner, cfg):
+def run_mix(runner, cfg, shared_prefix=0):
     """One pass of the mix: wall from the first add_request until drained
     (the reference's run_paged, bench/bench.py:74-109)."""
     from vllmlite_amd.engine import LLMEngine
     from vllmlite_amd.workload import mixed_lengths
     eng = LLMEngine(cfg, runner=runner)
-    reqs = mixed_lengths(0, 48, 0)
+    reqs = mixed_lengths(0, 48, shared_prefix)
     t0 = time.perf_counter()
     for rid, ids, p in reqs:
         eng.add_request(params=p, request_id=rid, prompt_token_ids=ids)
@@ -167,28 +330,29 @@ def run_mix(runner, cfg):
     return wall, eng.total_output_tokens, eng.total_steps, streams
 
 
-def e2e_leg(repeat=3, cpu=True):
+def e2e_leg(repeat=3, cpu=True, shared_prefix=0):
     """Output tok/s of the 48-request mix through HipRunner (one warm-up pass,
     then best of `repeat`; the runner and its captured graphs persist across
     passes, each pass gets a fresh engine), and the same mix through the NumPy
     oracle runner on this host's cores (warm-up on a 4-request mix, best of
     `repeat`)."""
-    import json as _json
     from vllmlite_amd.hip_runner import HipRunner
-    cfg = cfg0_engine_config()
+    cfg = engine_config(prefix_cache=shared_prefix > 0)
     runner = HipRunner(cfg.model, cfg.cache)
-    run_mix(runner, cfg)
-    best = min((run_mix(runner, cfg) for _ in range(repeat)), key=lambda r: r[0])
-    wall, toks, steps, streams = best
-    with open(os.path.join(ROOT, "tests", "golden", "cfg0_streams.json")) as f:
-        gold = _json.load(f)["streams"]
-    same = sum(streams[r] == gold[r] for r in gold)
-    out = {"workload": "48-request ragged mix (prompts 17-251, outputs 16-192, greedy), "
-                       "TinyLlama 6L d384 H8/Hkv4 d_ff1024 fp32, block 16, 512 blocks, "
-                       "16 seqs, budget 1024",
+    run_mix(runner, cfg, shared_prefix)
+    wall, toks, steps, streams = min((run_mix(runner, cfg, shared_prefix) for _ in range(repeat)),
+                                     key=lambda r: r[0])
+    out = {"workload": ("48-request ragged mix" + (f" behind a {shared_prefix}-token shared prefix, "
+                                                   "prefix cache on" if shared_prefix else "") +
+                        " (greedy), TinyLlama 6L d384 H8/Hkv4 d_ff1024 fp32, block 16, 512 blocks, "
+                        "16 seqs, budget 1024"),
            "output_tok_per_s": round(toks / wall, 1), "wall_s": round(wall, 4),
-           "steps": steps, "us_per_step": round(wall / steps * 1e6, 1),
-           "output_tokens": toks, "streams_identical_to_reference": f"{same}/{len(gold)}"}
+           "steps": steps, "us_per_step": round(wall / steps * 1e6, 1), "output_tokens": toks}
+    if shared_prefix == 0:
+        with open(os.path.join(ROOT, "tests", "golden", "cfg0_streams.json")) as f:
+            gold = json.load(f)["streams"]
+        same = sum(streams[r] == gold[r] for r in gold)
+        out["streams_identical_to_reference"] = f"{same}/{len(gold)}"
     if cpu:
         from oracle.runner import NumpyRunner
         from vllmlite_amd.engine import LLMEngine
@@ -199,12 +363,13 @@ def e2e_leg(repeat=3, cpu=True):
             eng.add_request(params=p, request_id=rid, prompt_token_ids=ids)
         while eng.has_work:
             eng.step()
-        cpu_best = min((run_mix(NumpyRunner(cfg.model, cfg.cache), cfg) for _ in range(repeat)),
-                       key=lambda r: r[0])
+        cpu_best = min((run_mix(NumpyRunner(cfg.model, cfg.cache), cfg, shared_prefix)
+                        for _ in range(repeat)), key=lambda r: r[0])
         cpu_tps = cpu_best[1] / cpu_best[0]
         out["cpu_numpy_tok_per_s"] = round(cpu_tps, 1)
         out["cpu_cores"] = len(os.sched_getaffinity(0))
         out["speedup_vs_cpu_numpy"] = round(toks / wall / cpu_tps, 2)
+        out["cpu_streams_identical"] = cpu_best[3] == streams
     return out
 
 
@@ -228,12 +393,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--no-e2e", action="store_true", help="skip the 48-request mix leg")
-    ap.add_argument("--e2e-only", action="store_true",
-                    help="only the 48-request mix through HipRunner (for rocprofv3 passes)")
-    ap.add_argument("--profile-mode", action="store_true",
-                    help="only the timed attention runs (for rocprofv3 passes)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end mixes")
+    ap.add_argument("--legs", default="decode,mixed,verify,cow,e2e",
+                    help="comma-separated legs to run (decode is always run)")
+    ap.add_argument("--profile-mode", default=None, metavar="LEG",
+                    help="only the timed launches of one leg (decode, mixed, verify, cow, e2e), "
+                         "for rocprofv3 passes")
     ap.add_argument("--copy-only", action="store_true",
                     help="only 5 device copies of 1 GiB (calibrates rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE against a kernel of known traffic)")
@@ -245,6 +411,7 @@ def main():
 
     import torch
     from vllmlite_amd import ops
+    from vllmlite_amd import synthetic as syn
 
     torch.cuda.set_device(0)
     if args.copy_only:
@@ -256,49 +423,31 @@ def main():
         print(json.dumps({"copy_only": True, "bytes_read_per_copy": a.numel() * 2,
                           "bytes_written_per_copy": c.numel() * 2}), flush=True)
         return
-    if args.e2e_only:
-        print(json.dumps({"e2e": e2e_leg(cpu=False)}), flush=True)
-        return
-    b = build_decode_batch(torch)
-    nbytes = algorithmic_bytes(b["ctx"])
-    out = torch.empty_like(b["q"])
-    ws = ops.AttentionWorkspace().get(
-        ops.paged_attention_workspace_size(S, S, H, D, int(b["ctx"].max())))
-    ops.paged_attention_plan(b["q"], b["kc"], b["seq_lens"], b["qsl"], BS, ws)
-
-    def step():
-        ops.paged_attention_run(out, b["q"], b["kc"], b["vc"], b["bt"], b["seq_lens"], b["qsl"],
-                                b["scale"], BS, ws, max_query_len=1)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for e0, e1 in ev:
-        e0.record()
-        step()
-        e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    kernel_ms = float(np.mean([e0.elapsed_time(e1) for e0, e1 in ev]))
-    ms_per_step = wall * 1e3 / args.steps
     if args.profile_mode:
-        print(json.dumps({"profile_mode": True, "kernel_ms": kernel_ms}))
+        leg = args.profile_mode
+        fn = {"decode": lambda: decode_leg(torch, ops, syn, args.steps, args.warmup, True),
+              "mixed": lambda: mixed_leg(torch, ops, syn, args.steps, args.warmup, True),
+              "verify": lambda: verify_leg(torch, ops, syn, args.steps, args.warmup, True),
+              "cow": lambda: cow_leg(torch, ops, args.steps, args.warmup),
+              "e2e": lambda: e2e_leg(cpu=False)}[leg]
+        r = fn()
+        r.pop("batch", None)
+        print(json.dumps({"profile_mode": leg, "result": r}), flush=True)
         return
 
-    rel_err = spot_check(torch, b, out)
-    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    legs = set(args.legs.split(","))
+    d = decode_leg(torch, ops, syn, args.steps, args.warmup)
+    b = d.pop("batch")
+    nbytes = d["bytes"]
+    achieved = nbytes / (d["kernel_ms"] * 1e-3) / 1e9
     line = {
         "metric": METRIC,
-        "value": round(nbytes / (ms_per_step * 1e-3) / 1e9, 1),
+        "value": round(nbytes / (d["ms_per_step"] * 1e-3) / 1e9, 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(d["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -309,17 +458,27 @@ def main():
                                "2^17-block pool",
                    "sum_ctx": int(b["ctx"].sum()), "algorithmic_bytes": nbytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None},
-        "kernel_us": round(kernel_ms * 1e3, 2),
-        "copy_ceiling_gbs": round(copy_ceiling(torch), 1),
-        "spot_check_max_rel_err": rel_err,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": traffic_from_summary()},
+        "kernel_us": round(d["kernel_ms"] * 1e3, 2),
+        "check_rel_err": d["check_rel_err"],
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch, b)
-    del b, out, ws
+    del b
     torch.cuda.empty_cache()
-    if not args.no_e2e:
+    line["copy_ceiling_gbs"] = round(copy_ceiling(torch), 1)
+    extra = {}
+    if "mixed" in legs:
+        extra["mixed_prefill_decode"] = mixed_leg(torch, ops, syn, 20, 3)
+    if "verify" in legs:
+        extra["spec_verify"] = verify_leg(torch, ops, syn, 20, 3)
+    if "cow" in legs:
+        extra["copy_on_write"] = cow_leg(torch, ops, 50, 5)
+    if "e2e" in legs and not args.no_e2e:
         line["e2e"] = e2e_leg(cpu=not args.no_cpu)
+        extra["e2e_shared_prefix"] = e2e_leg(cpu=not args.no_cpu, shared_prefix=256)
+    line["legs"] = extra
     print(json.dumps(line), flush=True)
 
 
