@@ -58,9 +58,9 @@ constexpr int kBK = VL_BK;  // blocks per K load burst
 constexpr int kBV = VL_BV;  // blocks per V load burst
 
 // MFMA tile-kernel shape: 4 wavefronts x 16 (token, head) rows per workgroup,
-// 32 keys per LDS tile
+// 64 keys per LDS tile
 constexpr int kTileRows = 64;
-constexpr int kTileKeys = 32;
+constexpr int kTileKeys = 64;
 
 struct Layout {
   int32_t* hdr;
@@ -105,7 +105,8 @@ inline bool fast_shape(int dtype, int H, int Hkv, int D, int bs) {
 }
 
 // head_dims with an MFMA tile instantiation
-inline bool tile_shape(int dtype, int D) {
+inline bool tile_shape(int dtype, int D, int bs) {
+  if (bs <= 0 || (bs & (bs - 1)) != 0) return false;  // block math is shifts and masks
   if (dtype == VL_DTYPE_BF16) return D == 64 || D == 128;
   return D == 16 || D == 32 || D == 48 || D == 64 || D == 128;
 }
@@ -218,26 +219,35 @@ static_assert(kTailBuckets == kPlanThreads, "one tail bucket per plan thread");
 // full ranges, so the kernel ends on its smallest items.
 __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H, int Hkv,
-    bool fast, bool tile, int64_t cap_rows, int target_items, int32_t* __restrict__ hdr,
+    bool fast, bool tile, int64_t cap_rows, int target_items, int tile_target,
+    int32_t* __restrict__ hdr,
     int32_t* __restrict__ fast_off, int32_t* __restrict__ gen_off,
     int32_t* __restrict__ tile_off, int32_t* __restrict__ nparts,
     int32_t* __restrict__ split_base, int32_t* __restrict__ tail_order,
     float2* __restrict__ ml) {
-  __shared__ unsigned long long need, bw_tokens;
+  __shared__ unsigned long long need, bw_tokens, tile_keys;
   __shared__ int part_len, range_len;
   __shared__ int hist[kTailBuckets];
   const int t = threadIdx.x;
-  if (t == 0) part_len = kPart0, bw_tokens = 0;
+  if (t == 0) part_len = kPart0, bw_tokens = 0, tile_keys = 0;
   for (int k = t; k < kTailBuckets; k += kPlanThreads) hist[k] = 0;
   __syncthreads();
-  // 0. range length from the decode tokens and the target item count
+  // 0. range length from the decode tokens and the target item count; the
+  // same for the partition length of the splittable multi-query sequences
+  // (at most kSplitMaxQ queries), counted in (KV head, 64-row block) units
   {
-    unsigned long long mine = 0;
+    unsigned long long mine = 0, mine_t = 0;
+    const int rep = H / Hkv;
     for (int i = t; i < S; i += kPlanThreads) {
       const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
-      if (is_bw(q, c, fast)) mine += (unsigned long long)c;
+      if (is_bw(q, c, fast)) {
+        mine += (unsigned long long)c;
+      } else if (tile && q > 0 && q <= kSplitMaxQ && c > 0) {
+        mine_t += (unsigned long long)c * cdiv(q * rep, kTileRows);
+      }
     }
     if (mine) atomicAdd(&bw_tokens, mine);
+    if (mine_t) atomicAdd(&tile_keys, mine_t);
     __syncthreads();
     if (t == 0) {
       int R = 64;
@@ -245,6 +255,11 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
                              (unsigned long long)max(target_items, 1) * (unsigned long long)R)
         R *= 2;
       range_len = R;
+      int P = kPart0;
+      while (P < (1 << 20) && tile_keys * (unsigned long long)Hkv >
+                                  (unsigned long long)max(tile_target, 1) * (unsigned long long)P)
+        P *= 2;
+      part_len = P;
     }
     __syncthreads();
   }
@@ -432,22 +447,28 @@ __global__ void __launch_bounds__(64) attend_generic_kernel(
 // Multi-query attention (chunked prefill, speculative verify) on the matrix
 // cores. One workgroup item = (sequence, KV head, block of 64 rows, context
 // partition); a row is a (query token j, head r of the KV head's group) pair,
-// row = j * rep + r, so the 4 query heads of a GQA group share every K/V tile.
+// row = j * rep + r, so the query heads of a GQA group share every K/V tile.
 // Wavefront w owns rows 16w..16w+15 of the block.
 //
-// Per 32-key tile (staged in LDS by the whole workgroup, V transposed):
-//   S^T[32 keys x 16 rows] = K . Q^T   two 16x16 output tiles; lane l holds
-//                                      row l%16 and keys 4(l/16)+i (+16)
-//   online softmax per row (the row's 16 keys of a tile sit in the 4 lanes
+// Keys stream in tiles of 64 through one LDS buffer (K row-major, V
+// transposed): while a tile is computed, the next one's K/V are already in
+// flight into registers (each thread gathers its keys through the block
+// table), and are written to LDS between two barriers once every wavefront
+// is done with the current tile.
+//   S^T[64 keys x 16 rows] = K . Q^T   four 16x16 output tiles; lane l holds
+//                                      row l%16 and keys 16t + 4(l/16) + i
+//   online softmax per row (a row's 64 keys of a tile sit in the 4 lanes
 //   l%16 + 16g, so a row max is a register max plus two xor shuffles)
 //   O^T[D x 16 rows] += V^T . P^T      the probabilities are already in the
-//                                      B-operand registers: k-slot e of lane
-//                                      group g is key 4g+e (e<4) or 16+4g+e-4
-//                                      and V^T is read from LDS in that order.
+//                                      B-operand registers: for keys 32h..,
+//                                      k-slot e of lane group g is key
+//                                      32h + 4g + e (e < 4) or 32h + 16 + 4g
+//                                      + e - 4, and V^T is read in that order.
 // bf16 uses v_mfma_f32_16x16x32_bf16 (P rounded to bf16, fp32 accumulation);
 // fp32 uses v_mfma_f32_16x16x4f32, so fp32 inputs keep fp32 products.
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 template <typename T, int D>
@@ -455,7 +476,11 @@ struct TileLds;
 template <int D>
 struct TileLds<uint16_t, D> {
   static constexpr int kRow = D + 8;           // K row stride (bf16), 16-byte aligned
-  static constexpr int vRow = kTileKeys + 4;   // V^T row stride (bf16)
+  static constexpr int vRow = kTileKeys + 8;   // V^T row stride (bf16), 16-byte aligned
+  static constexpr int kChunks = D / 8;        // 16-byte chunks per head row
+  // prefetch units per thread: K (key, chunk); V (4 keys, chunk)
+  static constexpr int kUnits = kTileKeys * kChunks / 256;
+  static constexpr int vUnits = (kTileKeys / 4) * kChunks;  // threads < vUnits take one
   uint16_t k[kTileKeys * kRow];
   uint16_t vt[D * vRow];
 };
@@ -463,6 +488,9 @@ template <int D>
 struct TileLds<float, D> {
   static constexpr int kRow = D + 1;
   static constexpr int vRow = D + 1;
+  static constexpr int kChunks = D / 4;        // float4 chunks per head row
+  static constexpr int kUnits = (kTileKeys * kChunks + 255) / 256;
+  static constexpr int vUnits = 0;             // V goes with K (same key, chunk)
   float k[kTileKeys * kRow];
   float v[kTileKeys * vRow];
 };
@@ -471,18 +499,28 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
 }
 
+
+// Two floats to packed bf16 with the hardware conversion (v_cvt_pk_bf16_f32,
+// round to nearest even, as f32_to_bf16 for every finite value).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 template <typename T, int D>
 __global__ void __launch_bounds__(256) attend_tile_kernel(
     T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const T* __restrict__ kc,
     const T* __restrict__ vc, const int32_t* __restrict__ bt, int bt_stride,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H, int Hkv,
-    int bs, float scale_log2, const int32_t* __restrict__ hdr, const int32_t* __restrict__ item_off,
-    const int32_t* __restrict__ nparts, const int32_t* __restrict__ split_base,
-    float2* __restrict__ ml, float* __restrict__ po) {
+    int bs_log2, float scale_log2, const int32_t* __restrict__ hdr,
+    const int32_t* __restrict__ item_off, const int32_t* __restrict__ nparts,
+    const int32_t* __restrict__ split_base, float2* __restrict__ ml, float* __restrict__ po) {
   constexpr bool kBf16 = sizeof(T) == 2;
   constexpr int kDT = D / 16;                 // 16-wide d tiles of the output
   constexpr int kKS = kBf16 ? D / 32 : D / 4;  // k-steps of the QK^T product
   using Lds = TileLds<T, D>;
+  static_assert(!kBf16 || (Lds::kUnits * 256 == kTileKeys * Lds::kChunks && Lds::vUnits <= 256),
+                "bf16 tile staging assumes head_dim 64 or 128");
   __shared__ Lds lds;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -517,7 +555,9 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
     const int head = kvh * rep + (row_ok ? my_row - (my_row / rep) * rep : 0);
     const int tok = qsl[i] + j;
     const int qpos = ctx - q_len + j;
+    const int qpos_wave_min = ctx - q_len + row0 / rep;  // earliest query row of the wave
     const int32_t* table = bt + (int64_t)i * bt_stride;
+    const int64_t kv_off = (int64_t)kvh * D;
 
     // Q^T operand of the QK^T product, kept in registers for the whole item
     typename std::conditional<kBf16, bf16x8_t, float>::type qop[kKS];
@@ -540,69 +580,106 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
     float m_run = -__builtin_inff();
     float l_part = 0.f;  // this lane's share of the row sum
 
-    for (int k0 = kbeg; k0 < kend_wg; k0 += kTileKeys) {
-      __syncthreads();  // the previous tile has been consumed
-      // ---- stage K and V of keys [k0, k0+32) in LDS; keys >= kend_wg are 0
+    // ---- prefetch registers: this thread's share of one tile's K and V
+    const uint32_t blk_elems = (uint32_t)slot_stride << bs_log2;
+    const uint32_t bs_mask = (1u << bs_log2) - 1;
+    auto row_of = [&](int key) -> int64_t {  // element offset of key's head row
+      const uint32_t blk = (uint32_t)table[key >> bs_log2];
+      return (int64_t)((uint64_t)blk * blk_elems) +
+             (int64_t)((key & bs_mask) * (uint32_t)slot_stride) + kv_off;
+    };
+    uint4 pk[Lds::kUnits], pv[kBf16 ? 4 : Lds::kUnits];
+    auto prefetch = [&](int k0) {
       if constexpr (kBf16) {
-        constexpr int kChunks = D / 8;  // 16-byte chunks per head row
-        for (int idx = threadIdx.x; idx < kTileKeys * kChunks; idx += 256) {
-          const int kk = idx / kChunks, c = idx - kk * kChunks;
+#pragma unroll
+        for (int r = 0; r < Lds::kUnits; ++r) {
+          const int idx = threadIdx.x + 256 * r;
+          const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
           const int key = k0 + kk;
-          uint4 w = make_uint4(0, 0, 0, 0);
-          if (key < kend_wg) {
-            const int64_t slot = (int64_t)table[key / bs] * bs + key % bs;
-            w = *reinterpret_cast<const uint4*>(kc + slot * slot_stride + (int64_t)kvh * D + c * 8);
-          }
-          *reinterpret_cast<uint4*>(&lds.k[kk * Lds::kRow + c * 8]) = w;
+          pk[r] = key < kend_wg ? *reinterpret_cast<const uint4*>(kc + row_of(key) + c * 8)
+                                : make_uint4(0, 0, 0, 0);
         }
-        // V: a thread takes two adjacent keys of one 8-dim chunk and writes
-        // their 8 (key, key+1) pairs transposed
-        for (int idx = threadIdx.x; idx < (kTileKeys / 2) * kChunks; idx += 256) {
-          const int kp = idx / kChunks, c = idx - kp * kChunks;
-          const int key = k0 + 2 * kp;
-          uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
-          if (key < kend_wg) {
-            const int64_t slot = (int64_t)table[key / bs] * bs + key % bs;
-            a = *reinterpret_cast<const uint4*>(vc + slot * slot_stride + (int64_t)kvh * D + c * 8);
-          }
-          if (key + 1 < kend_wg) {
-            const int64_t slot = (int64_t)table[(key + 1) / bs] * bs + (key + 1) % bs;
-            b = *reinterpret_cast<const uint4*>(vc + slot * slot_stride + (int64_t)kvh * D + c * 8);
-          }
-          const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
-          uint32_t* dst = reinterpret_cast<uint32_t*>(lds.vt);
+        // V: four consecutive keys of one 8-dim chunk; the key quad varies
+        // fastest over the lanes so the transposed LDS stores hit distinct banks
+        if (threadIdx.x < Lds::vUnits) {
+          const int kq = threadIdx.x & (kTileKeys / 4 - 1), c = threadIdx.x / (kTileKeys / 4);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int d = c * 8 + 2 * e;
-            dst[(d * Lds::vRow + 2 * kp) >> 1] = (av[e] & 0xffffu) | (bv[e] << 16);
-            dst[((d + 1) * Lds::vRow + 2 * kp) >> 1] = (av[e] >> 16) | (bv[e] & 0xffff0000u);
+            const int key = k0 + 4 * kq + e;
+            pv[e] = key < kend_wg ? *reinterpret_cast<const uint4*>(vc + row_of(key) + c * 8)
+                                  : make_uint4(0, 0, 0, 0);
           }
         }
       } else {
-        constexpr int kVec = D / 4;  // float4 per head row
-        for (int idx = threadIdx.x; idx < kTileKeys * kVec; idx += 256) {
-          const int kk = idx / kVec, c = idx - kk * kVec;
+#pragma unroll
+        for (int r = 0; r < Lds::kUnits; ++r) {
+          const int idx = threadIdx.x + 256 * r;
+          const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
           const int key = k0 + kk;
-          float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-          if (key < kend_wg) {
-            const int64_t slot = (int64_t)table[key / bs] * bs + key % bs;
-            const int64_t off = slot * slot_stride + (int64_t)kvh * D + c * 4;
-            a = *reinterpret_cast<const float4*>(kc + off);
-            b = *reinterpret_cast<const float4*>(vc + off);
-          }
-          float* kd = &lds.k[kk * Lds::kRow + c * 4];
-          float* vd = &lds.v[kk * Lds::vRow + c * 4];
-          kd[0] = a.x, kd[1] = a.y, kd[2] = a.z, kd[3] = a.w;
-          vd[0] = b.x, vd[1] = b.y, vd[2] = b.z, vd[3] = b.w;
+          const bool ok = idx < kTileKeys * Lds::kChunks && key < kend_wg;
+          const int64_t off = ok ? row_of(key) + c * 4 : 0;
+          pk[r] = ok ? *reinterpret_cast<const uint4*>(kc + off) : make_uint4(0, 0, 0, 0);
+          pv[r] = ok ? *reinterpret_cast<const uint4*>(vc + off) : make_uint4(0, 0, 0, 0);
         }
       }
+    };
+    auto stage = [&]() {  // prefetch registers -> LDS
+      if constexpr (kBf16) {
+#pragma unroll
+        for (int r = 0; r < Lds::kUnits; ++r) {
+          const int idx = threadIdx.x + 256 * r;
+          const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
+          *reinterpret_cast<uint4*>(&lds.k[kk * Lds::kRow + c * 8]) = pk[r];
+        }
+        if (threadIdx.x < Lds::vUnits) {
+          const int kq = threadIdx.x & (kTileKeys / 4 - 1), c = threadIdx.x / (kTileKeys / 4);
+          const uint32_t w[4][4] = {{pv[0].x, pv[0].y, pv[0].z, pv[0].w},
+                                    {pv[1].x, pv[1].y, pv[1].z, pv[1].w},
+                                    {pv[2].x, pv[2].y, pv[2].z, pv[2].w},
+                                    {pv[3].x, pv[3].y, pv[3].z, pv[3].w}};
+#pragma unroll
+          for (int m = 0; m < 4; ++m) {
+            // dims 8c + 2m (low halves) and 8c + 2m + 1 (high halves) of keys 4kq..4kq+3
+            const uint32_t lo01 = __builtin_amdgcn_perm(w[1][m], w[0][m], 0x05040100u);
+            const uint32_t lo23 = __builtin_amdgcn_perm(w[3][m], w[2][m], 0x05040100u);
+            const uint32_t hi01 = __builtin_amdgcn_perm(w[1][m], w[0][m], 0x07060302u);
+            const uint32_t hi23 = __builtin_amdgcn_perm(w[3][m], w[2][m], 0x07060302u);
+            const int d = c * 8 + 2 * m;
+            *reinterpret_cast<uint2*>(&lds.vt[d * Lds::vRow + 4 * kq]) = make_uint2(lo01, lo23);
+            *reinterpret_cast<uint2*>(&lds.vt[(d + 1) * Lds::vRow + 4 * kq]) = make_uint2(hi01, hi23);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < Lds::kUnits; ++r) {
+          const int idx = threadIdx.x + 256 * r;
+          if (idx < kTileKeys * Lds::kChunks) {
+            const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
+            float* kd = &lds.k[kk * Lds::kRow + c * 4];
+            float* vd = &lds.v[kk * Lds::vRow + c * 4];
+            kd[0] = __uint_as_float(pk[r].x), kd[1] = __uint_as_float(pk[r].y);
+            kd[2] = __uint_as_float(pk[r].z), kd[3] = __uint_as_float(pk[r].w);
+            vd[0] = __uint_as_float(pv[r].x), vd[1] = __uint_as_float(pv[r].y);
+            vd[2] = __uint_as_float(pv[r].z), vd[3] = __uint_as_float(pv[r].w);
+          }
+        }
+      }
+    };
+
+    const int ntile = kend_wg > kbeg ? (kend_wg - kbeg + kTileKeys - 1) / kTileKeys : 0;
+    if (ntile > 0) prefetch(kbeg);
+    for (int ti = 0; ti < ntile; ++ti) {
+      const int k0 = kbeg + ti * kTileKeys;
+      __syncthreads();  // the previous tile (or item) is done with the LDS buffer
+      stage();
       __syncthreads();
+      if (ti + 1 < ntile) prefetch(k0 + kTileKeys);  // in flight during the compute below
       if (k0 >= kend_wave) continue;  // every row of this wave is past its causal end
 
-      // ---- S^T = K Q^T for the two 16-key halves
-      f32x4_t sc[2];
+      // ---- S^T = K Q^T for the four 16-key subtiles
+      f32x4_t sc[4];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < 4; ++t) {
         sc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < kKS; ++s) {
@@ -617,30 +694,43 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
           }
         }
       }
-      // ---- mask, online softmax (base 2)
-      float sv[2][4];
+      // ---- mask, online softmax (base 2); a tile every row of the wave
+      // sees in full needs no per-key test (rows past the block's end only
+      // feed their own, never written, lanes)
+      float sv[4][4];
       float cmax = -__builtin_inff();
+      const bool full = k0 + kTileKeys - 1 <= qpos_wave_min && k0 + kTileKeys <= kend;
+      if (full) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int key = k0 + 16 * t + 4 * grp + e;
-          const bool ok = row_ok && key <= qpos && key < kend;
-          sv[t][e] = ok ? sc[t][e] * scale_log2 : -__builtin_inff();
-          cmax = fmaxf(cmax, sv[t][e]);
-        }
+          for (int e = 0; e < 4; ++e) {
+            sv[t][e] = sc[t][e] * scale_log2;
+            cmax = fmaxf(cmax, sv[t][e]);
+          }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int key = k0 + 16 * t + 4 * grp + e;
+            const bool ok = row_ok && key <= qpos && key < kend;
+            sv[t][e] = ok ? sc[t][e] * scale_log2 : -__builtin_inff();
+            cmax = fmaxf(cmax, sv[t][e]);
+          }
+      }
       cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
       cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
       const float m_new = fmaxf(m_run, cmax);
       const float alpha = m_new == -__builtin_inff() ? 1.f : exp2f(m_run - m_new);
-      float pv[2][4];
+      float pr[4][4];
       float psum = 0.f;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          pv[t][e] = sv[t][e] == -__builtin_inff() ? 0.f : exp2f(sv[t][e] - m_new);
-          psum += pv[t][e];
+          pr[t][e] = sv[t][e] == -__builtin_inff() ? 0.f : exp2f(sv[t][e] - m_new);
+          psum += pr[t][e];
         }
       l_part = l_part * alpha + psum;
       m_run = m_new;
@@ -648,30 +738,33 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
       for (int u = 0; u < kDT; ++u) acc[u] *= alpha;
       // ---- O^T += V^T P^T
       if constexpr (kBf16) {
-        uint4 pw;
-        pw.x = pack_bf16x2(pv[0][0], pv[0][1]);
-        pw.y = pack_bf16x2(pv[0][2], pv[0][3]);
-        pw.z = pack_bf16x2(pv[1][0], pv[1][1]);
-        pw.w = pack_bf16x2(pv[1][2], pv[1][3]);
-        const bf16x8_t pop = __builtin_bit_cast(bf16x8_t, pw);
 #pragma unroll
-        for (int u = 0; u < kDT; ++u) {
-          const uint16_t* vrow = &lds.vt[(16 * u + col) * Lds::vRow];
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * grp);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * grp);
-          const uint4 vw = make_uint4(lo.x, lo.y, hi.x, hi.y);
-          acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, vw), pop,
-                                                           acc[u], 0, 0, 0);
+        for (int hh = 0; hh < 2; ++hh) {
+          uint4 pw;
+          pw.x = cvt_pk_bf16(pr[2 * hh][0], pr[2 * hh][1]);
+          pw.y = cvt_pk_bf16(pr[2 * hh][2], pr[2 * hh][3]);
+          pw.z = cvt_pk_bf16(pr[2 * hh + 1][0], pr[2 * hh + 1][1]);
+          pw.w = cvt_pk_bf16(pr[2 * hh + 1][2], pr[2 * hh + 1][3]);
+          const bf16x8_t pop = __builtin_bit_cast(bf16x8_t, pw);
+#pragma unroll
+          for (int u = 0; u < kDT; ++u) {
+            const uint16_t* vrow = &lds.vt[(16 * u + col) * Lds::vRow + 32 * hh];
+            const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * grp);
+            const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * grp);
+            const uint4 vw = make_uint4(lo.x, lo.y, hi.x, hi.y);
+            acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, vw), pop,
+                                                             acc[u], 0, 0, 0);
+          }
         }
       } else {
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float* vrow = &lds.v[(16 * t + 4 * grp + e) * Lds::vRow];
 #pragma unroll
             for (int u = 0; u < kDT; ++u)
-              acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * u + col], pv[t][e], acc[u],
+              acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * u + col], pr[t][e], acc[u],
                                                             0, 0, 0);
           }
       }
@@ -689,8 +782,8 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
           const int d = 16 * u + 4 * grp;
           if constexpr (kBf16) {
             uint2 o;
-            o.x = pack_bf16x2(acc[u][0] * inv, acc[u][1] * inv);
-            o.y = pack_bf16x2(acc[u][2] * inv, acc[u][3] * inv);
+            o.x = cvt_pk_bf16(acc[u][0] * inv, acc[u][1] * inv);
+            o.y = cvt_pk_bf16(acc[u][2] * inv, acc[u][3] * inv);
             *reinterpret_cast<uint2*>(orow + d) = o;
           } else {
             *reinterpret_cast<float4*>(orow + d) =
@@ -712,7 +805,6 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
 
 // ---------------------------------------------------- bandwidth decode -----
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float c) {
   c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.x),
@@ -1211,14 +1303,19 @@ int decode_grid() {
   return cached[dev];
 }
 
+// Workgroups the MFMA tile kernel is launched with (it loops over its items).
+int tile_grid() { return vl_num_cus() * 4; }
+
 int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
   const Layout L = make_layout(ws, ws_bytes, a.S, a.D);
   const bool fast = fast_shape(a.dtype, a.H, a.Hkv, a.D, a.bs);
-  const bool tile = tile_shape(a.dtype, a.D);
+  const bool tile = tile_shape(a.dtype, a.D, a.bs);
   // a few bandwidth-kernel items per resident workgroup
   const int target_items = fast ? kItemsPerWg * decode_grid() : 0;
+  const int tile_target = kItemsPerWg * tile_grid();
   plan_kernel<<<1, kPlanThreads, 0, st>>>(a.seq_lens, a.qsl, a.S, a.H, a.Hkv, fast, tile,
-                                          L.cap_rows, target_items, L.hdr, L.fast_off, L.gen_off,
+                                          L.cap_rows, target_items, tile_target, L.hdr,
+                                          L.fast_off, L.gen_off,
                                           L.tile_off, L.nparts, L.split_base, L.tail_order, L.ml);
   VL_CHECK_LAUNCH();
   return VL_OK;
@@ -1226,10 +1323,10 @@ int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
 
 template <typename T, int D>
 int launch_tile_d(const Args& a, const Layout& L, float sl2, int ncu, hipStream_t st) {
-  attend_tile_kernel<T, D><<<ncu * 4, 256, 0, st>>>(
+  attend_tile_kernel<T, D><<<tile_grid(), 256, 0, st>>>(
       (T*)a.out, (const T*)a.query, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.bt, a.bt_stride,
-      a.seq_lens, a.qsl, a.S, a.H, a.Hkv, a.bs, sl2, L.hdr, L.tile_off, L.nparts, L.split_base,
-      L.ml, L.po);
+      a.seq_lens, a.qsl, a.S, a.H, a.Hkv, __builtin_ctz(a.bs), sl2, L.hdr, L.tile_off, L.nparts,
+      L.split_base, L.ml, L.po);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
@@ -1268,7 +1365,7 @@ int do_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) 
     VL_CHECK_LAUNCH();
     if (max_q == 1) return VL_OK;  // every sequence was a decode: nothing else to run
   }
-  if (tile_shape(a.dtype, a.D)) {
+  if (tile_shape(a.dtype, a.D, a.bs)) {
     int rc = launch_tile<T>(a, L, sl2, ncu, st);
     if (rc) return rc;
   } else {
@@ -1343,7 +1440,7 @@ extern "C" int vl_paged_attention_run(void* out, const void* query, int64_t quer
   int rc = check_args(a, workspace, workspace_bytes, true);
   if (rc || a.S == 0 || a.T == 0) return rc;
   if (fast_shape(dtype, num_heads, num_kv_heads, head_dim, block_size) ||
-      tile_shape(dtype, head_dim))
+      tile_shape(dtype, head_dim, block_size))
     VL_CHECK_ARG((query_stride % 8) == 0 && ((uintptr_t)query & 15) == 0 &&
                      ((uintptr_t)out & 15) == 0 && ((uintptr_t)key_cache & 15) == 0 &&
                      ((uintptr_t)value_cache & 15) == 0,
