@@ -287,10 +287,13 @@ TILE_SHAPES = [("f32", 8, 4, 48), ("f32", 8, 2, 64), ("f32", 4, 4, 16), ("f32", 
 
 
 @pytest.mark.parametrize("dtype,H,Hkv,D", TILE_SHAPES)
-@pytest.mark.parametrize("bs", [1, 16])
+@pytest.mark.parametrize("bs", [1, 4, 16, 32])
 def test_tile_prefill_chunks_with_prior_context(dtype, H, Hkv, D, bs):
     """Chunks that start mid-block after prior context, causal within the chunk,
-    plus decodes and a 1-token context, all in one call."""
+    plus decodes and a 1-token context, all in one call. Block sizes cover
+    every staging path: per-key block lookups (1), per-quad V lookups (4),
+    one block per 16-key K unit (16, 32); the unowned tail slots of a
+    sequence's last block are NaN."""
     seqs = [(37, 37), (100, 133), (1, 90), (64, 64 + 200), (17, 500), (3, 3), (2, 40)]
     b = make_batch(seqs, H, Hkv, D, bs, seed=30 + D + bs)
     check(run_attention(b, dtype), expected(b, dtype), dtype)

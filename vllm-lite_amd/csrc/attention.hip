@@ -34,6 +34,7 @@ constexpr int kHdrInts = 64;  // [0] bandwidth-kernel items [1] generic items [2
                               // [3] split rows [4] tile items [5] full ranges [6] tail ranges
                               // [7] range length [8] bandwidth-kernel work counter
                               // [9] bandwidth-kernel workgroups finished
+                              // [10] 32-row tile items
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxHeadDim = 256;
 constexpr int kSplitMaxQ = 16;  // only sequences with <= this many queries split their context
@@ -70,13 +71,14 @@ struct Layout {
   int32_t* nparts;      // [S]
   int32_t* split_base;  // [S] first partial row, or -1
   int32_t* tail_order;  // [S] sequences with a short last range, longest first
+  int32_t* wide_off;    // [S+1] 32-row MFMA tile workgroup items
   float2* ml;           // [cap_rows] (running max (log2 domain), running sum)
   float* po;            // [cap_rows, D] unnormalised partial outputs
   int64_t cap_rows;
 };
 
 inline size_t plan_bytes(int S) {
-  size_t b = kHdrInts * 4 + (size_t)(6 * S + 3) * 4;
+  size_t b = kHdrInts * 4 + (size_t)(7 * S + 4) * 4;
   return (b + 255) & ~(size_t)255;
 }
 
@@ -90,6 +92,7 @@ inline Layout make_layout(void* ws, size_t bytes, int S, int D) {
   L.nparts = L.tile_off + S + 1;
   L.split_base = L.nparts + S;
   L.tail_order = L.split_base + S;
+  L.wide_off = L.tail_order + S;
   const size_t pb = plan_bytes(S);
   const size_t per_row = (size_t)(D + 2) * 4;
   // rows: 8-byte (m, l) pairs, then a 256-byte aligned [rows, D] float array
@@ -164,7 +167,8 @@ struct SeqWork {
   int np;        // context partitions
   int64_t full;  // bandwidth kernel: ranges of exactly R tokens
   int64_t tail;  // bandwidth kernel: 1 if the last range is shorter
-  int64_t tile;  // MFMA tile workgroup items
+  int64_t tile;  // MFMA tile workgroup items (16-row wavefronts)
+  int64_t wide;  // MFMA tile workgroup items (32-row wavefronts)
   int64_t gen;   // generic wavefront items
   int64_t rows;  // split partial rows
 };
@@ -173,11 +177,13 @@ struct SeqWork {
 // kernel, whose context is cut into ranges of R tokens (the last one
 // shorter); everything else goes to the MFMA tile kernel when the shape has
 // one (one workgroup per 64-row block of (token, head-in-group) rows per KV
-// head and partition of P tokens), else to the generic kernel.
+// head and partition of P tokens; sequences with more than kSplitMaxQ
+// queries take 128-row blocks of 32-row wavefronts when `wide`), else to the
+// generic kernel.
 __device__ __forceinline__ bool is_bw(int q, int c, bool fast) { return fast && q == 1 && c > 0; }
 
 __device__ __forceinline__ SeqWork seq_work(int q, int c, int P, int R, int H, int Hkv, bool fast,
-                                            bool tile) {
+                                            bool tile, bool wide) {
   SeqWork w;
   const bool live = q > 0 && c > 0;
   const bool bw = is_bw(q, c, fast);
@@ -190,7 +196,9 @@ __device__ __forceinline__ SeqWork seq_work(int q, int c, int P, int R, int H, i
     w.np = (q > 0 && q <= kSplitMaxQ && c > P) ? (c + P - 1) / P : 1;
     w.full = w.tail = 0;
   }
-  w.tile = tl ? (int64_t)w.np * Hkv * cdiv(q * (H / Hkv), kTileRows) : 0;
+  const bool wd = tl && wide && q > kSplitMaxQ;  // never split (np == 1)
+  w.tile = tl && !wd ? (int64_t)w.np * Hkv * cdiv(q * (H / Hkv), kTileRows) : 0;
+  w.wide = wd ? (int64_t)Hkv * cdiv(q * (H / Hkv), 2 * kTileRows) : 0;
   w.gen = (bw || tl) ? 0 : (int64_t)max(q, 0) * H * w.np;
   // a split decode sequence also keeps one arrival counter per KV head in
   // the rows after its partials
@@ -219,12 +227,12 @@ static_assert(kTailBuckets == kPlanThreads, "one tail bucket per plan thread");
 // full ranges, so the kernel ends on its smallest items.
 __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H, int Hkv,
-    bool fast, bool tile, int64_t cap_rows, int target_items, int tile_target,
+    bool fast, bool tile, bool wide, int64_t cap_rows, int target_items, int tile_target,
     int32_t* __restrict__ hdr,
     int32_t* __restrict__ fast_off, int32_t* __restrict__ gen_off,
     int32_t* __restrict__ tile_off, int32_t* __restrict__ nparts,
     int32_t* __restrict__ split_base, int32_t* __restrict__ tail_order,
-    float2* __restrict__ ml) {
+    int32_t* __restrict__ wide_off, float2* __restrict__ ml) {
   __shared__ unsigned long long need, bw_tokens, tile_keys;
   __shared__ int part_len, range_len;
   __shared__ int hist[kTailBuckets];
@@ -270,7 +278,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     const int P = part_len, R = range_len;
     unsigned long long mine = 0;
     for (int i = t; i < S; i += kPlanThreads)
-      mine += seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, R, H, Hkv, fast, tile).rows;
+      mine += seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, R, H, Hkv, fast, tile, wide).rows;
     if (mine) atomicAdd(&need, mine);
     __syncthreads();
     const bool fits = need <= (unsigned long long)cap_rows || (P >= (1 << 29) && R >= (1 << 29));
@@ -291,19 +299,20 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
                                           : (int)((int64_t)(blocks - 1) * kTailBuckets / rblocks);
     return kTailBuckets - 1 - k;  // ascending key = descending length
   };
-  int64_t f = 0, g = 0, r = 0, x = 0, tl = 0;
+  int64_t f = 0, g = 0, r = 0, x = 0, tl = 0, wd = 0;
   for (int i = s0; i < s1; ++i) {
     const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
-    const SeqWork w = seq_work(q, c, P, R, H, Hkv, fast, tile);
-    f += w.full, g += w.gen, r += w.rows, x += w.tile, tl += w.tail;
+    const SeqWork w = seq_work(q, c, P, R, H, Hkv, fast, tile, wide);
+    f += w.full, g += w.gen, r += w.rows, x += w.tile, tl += w.tail, wd += w.wide;
     if (w.tail) atomicAdd(&hist[tail_key(c)], 1);
   }
-  int64_t tf, tg, tr, tx, ttl;
+  int64_t tf, tg, tr, tx, ttl, twd;
   int64_t fo = block_exclusive_scan(f, &tf);
   int64_t go = block_exclusive_scan(g, &tg);
   int64_t ro = block_exclusive_scan(r, &tr);
   int64_t xo = block_exclusive_scan(x, &tx);
   block_exclusive_scan(tl, &ttl);
+  int64_t wo = block_exclusive_scan(wd, &twd);
   // bucket starts (kTailBuckets == kPlanThreads: one bucket per thread)
   int64_t dummy;
   const int64_t hstart = block_exclusive_scan(hist[t], &dummy);
@@ -312,22 +321,24 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
   __syncthreads();
   for (int i = s0; i < s1; ++i) {
     const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
-    const SeqWork w = seq_work(q, c, P, R, H, Hkv, fast, tile);
+    const SeqWork w = seq_work(q, c, P, R, H, Hkv, fast, tile, wide);
     fast_off[i] = (int32_t)fo;
     gen_off[i] = (int32_t)go;
     tile_off[i] = (int32_t)xo;
+    wide_off[i] = (int32_t)wo;
     nparts[i] = w.np;
     split_base[i] = w.np > 1 ? (int32_t)ro : -1;
     if (w.tail) tail_order[atomicAdd(&hist[tail_key(c)], 1)] = i;
     if (w.np > 1 && is_bw(q, c, fast))  // arrival counters start at 0
       for (int k = 0; k < Hkv; ++k)
         reinterpret_cast<int32_t*>(ml + ro + (int64_t)H * w.np + k)[0] = 0;
-    fo += w.full, go += w.gen, ro += w.rows, xo += w.tile;
+    fo += w.full, go += w.gen, ro += w.rows, xo += w.tile, wo += w.wide;
   }
   if (t == 0) {
     fast_off[S] = (int32_t)tf;
     gen_off[S] = (int32_t)tg;
     tile_off[S] = (int32_t)tx;
+    wide_off[S] = (int32_t)twd;
     hdr[0] = (int32_t)((tf + ttl) * Hkv);
     hdr[1] = (int32_t)tg;
     hdr[2] = P;
@@ -338,6 +349,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     hdr[7] = R;
     hdr[8] = 0;
     hdr[9] = 0;
+    hdr[10] = (int32_t)twd;
   }
 }
 
@@ -470,6 +482,13 @@ __global__ void __launch_bounds__(64) attend_generic_kernel(
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte global load as a native vector (a uint4 struct copy can become an
+// aggregate memcpy that keeps a register array in scratch memory)
+__device__ __forceinline__ uint4 load16(const void* p) {
+  return __builtin_bit_cast(uint4, *reinterpret_cast<const u32x4_t*>(p));
+}
 
 template <typename T, int D>
 struct TileLds;
@@ -500,6 +519,11 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 
+// 2^x by the hardware's v_exp_f32 (about 1 ulp; results below 2^-126 may
+// flush to zero, far below a softmax row sum's fp32 resolution). exp2f adds
+// a range reduction for denormal results that costs six more VALU ops.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // Two floats to packed bf16 with the hardware conversion (v_cvt_pk_bf16_f32,
 // round to nearest even, as f32_to_bf16 for every finite value).
 __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
@@ -507,7 +531,13 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-template <typename T, int D>
+// RW = rows per wavefront: 16 (v_mfma_f32_16x16x32_bf16 / 16x16x4f32, 64-row
+// workgroups; short-query sequences, which may be split into partitions, and
+// fp32) or 32 (bf16 v_mfma_f32_32x32x16_bf16, 128-row workgroups, for long
+// query chunks: each K/V tile read from LDS feeds twice the rows). With RW 32
+// a lane holds row l%32; its S^T values are keys 32t + 8(r/4) + 4(l/32) + r%4
+// (r < 16) and its O^T values dims 32u + 8(r/4) + 4(l/32) + r%4.
+template <typename T, int D, int RW>
 __global__ void __launch_bounds__(256) attend_tile_kernel(
     T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const T* __restrict__ kc,
     const T* __restrict__ vc, const int32_t* __restrict__ bt, int bt_stride,
@@ -516,17 +546,23 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
     const int32_t* __restrict__ item_off, const int32_t* __restrict__ nparts,
     const int32_t* __restrict__ split_base, float2* __restrict__ ml, float* __restrict__ po) {
   constexpr bool kBf16 = sizeof(T) == 2;
-  constexpr int kDT = D / 16;                 // 16-wide d tiles of the output
-  constexpr int kKS = kBf16 ? D / 32 : D / 4;  // k-steps of the QK^T product
+  constexpr bool kW = RW == 32;
+  static_assert(RW == 16 || (RW == 32 && kBf16), "32-row wavefronts are bf16 only");
+  constexpr int kRows = 4 * RW;                          // rows per workgroup item
+  constexpr int kDT = D / (kW ? 32 : 16);                // d tiles of the output
+  constexpr int kKS = kW ? D / 16 : kBf16 ? D / 32 : D / 4;  // k-steps of the QK^T product
+  constexpr int kST = kTileKeys / (kW ? 32 : 16);        // key subtiles per LDS tile
+  constexpr int kCV = kW ? 16 : 4;                       // accumulator values per subtile
   using Lds = TileLds<T, D>;
+  using AccT = float __attribute__((ext_vector_type(kCV)));
   static_assert(!kBf16 || (Lds::kUnits * 256 == kTileKeys * Lds::kChunks && Lds::vUnits <= 256),
                 "bf16 tile staging assumes head_dim 64 or 128");
   __shared__ Lds lds;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int col = lane & 15;  // the lane's row within the wave's 16 rows
-  const int grp = lane >> 4;  // lane group: which keys / d chunk it holds
-  const int n_items = hdr[4];
+  const int col = lane & (RW - 1);  // the lane's row within the wave's rows
+  const int grp = lane / RW;        // lane group: which keys / d chunk it holds
+  const int n_items = hdr[kW ? 10 : 4];
   const int P = hdr[2];
   const int rep = H / Hkv;
   const int64_t slot_stride = (int64_t)Hkv * D;
@@ -535,7 +571,7 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
     const int i = wave_upper_bound_le(item_off, S + 1, it);
     const int q_len = qsl[i + 1] - qsl[i];
     const int ctx = seq_lens[i];
-    const int np = nparts[i];
+    const int np = kW ? 1 : nparts[i];
     const int local = it - item_off[i];
     const int part = local % np;
     const int kvh = (local / np) % Hkv;
@@ -544,10 +580,10 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
     const int kbeg = np > 1 ? part * P : 0;
     const int kend = np > 1 ? min(ctx, kbeg + P) : ctx;
     // keys the block's last row can see bound the tiles the workgroup loads
-    const int blk_last = min(nrows - 1, rb * kTileRows + kTileRows - 1);
+    const int blk_last = min(nrows - 1, rb * kRows + kRows - 1);
     const int kend_wg = min(kend, ctx - q_len + blk_last / rep + 1);
-    const int row0 = rb * kTileRows + wave * 16;
-    const int wave_last = min(nrows - 1, row0 + 15);
+    const int row0 = rb * kRows + wave * RW;
+    const int wave_last = min(nrows - 1, row0 + RW - 1);
     const int kend_wave = row0 < nrows ? min(kend, ctx - q_len + wave_last / rep + 1) : kbeg;
     const int my_row = row0 + col;
     const bool row_ok = my_row < nrows;
@@ -566,17 +602,19 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
 #pragma unroll
       for (int s = 0; s < kKS; ++s) {
         if constexpr (kBf16) {
-          uint4 w = row_ok ? *reinterpret_cast<const uint4*>(qrow + 32 * s + 8 * grp)
-                           : make_uint4(0, 0, 0, 0);
+          const int d0 = kW ? 16 * s + 8 * grp : 32 * s + 8 * grp;
+          uint4 w = row_ok ? *reinterpret_cast<const uint4*>(qrow + d0) : make_uint4(0, 0, 0, 0);
           qop[s] = __builtin_bit_cast(bf16x8_t, w);
         } else {
           qop[s] = row_ok ? qrow[4 * s + grp] : 0.f;
         }
       }
     }
-    f32x4_t acc[kDT];
+    AccT acc[kDT];
 #pragma unroll
-    for (int u = 0; u < kDT; ++u) acc[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < kDT; ++u)
+#pragma unroll
+      for (int r = 0; r < kCV; ++r) acc[u][r] = 0.f;
     float m_run = -__builtin_inff();
     float l_part = 0.f;  // this lane's share of the row sum
 
@@ -589,25 +627,56 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
              (int64_t)((key & bs_mask) * (uint32_t)slot_stride) + kv_off;
     };
     uint4 pk[Lds::kUnits], pv[kBf16 ? 4 : Lds::kUnits];
+    // bf16 staging: K unit r of a tile is keys k0 + kUnitKeys r + threadIdx / kChunks,
+    // chunk threadIdx % kChunks; with blocks of >= kUnitKeys slots the unit lies
+    // in one block whose id is uniform over the workgroup (tile starts are
+    // multiples of 64). Keys past the workgroup's end are masked: K reads stay
+    // in the last key's block (finite or not, the score is replaced by -inf);
+    // V reads re-read the last key, finite values whose weights are zero.
+    constexpr int kUnitKeys = 256 / Lds::kChunks;
+    const bool unit_blocks = (1 << bs_log2) >= kUnitKeys;
+    const uint32_t k_thr_off =
+        (uint32_t)(threadIdx.x / Lds::kChunks) * (uint32_t)slot_stride + (threadIdx.x % Lds::kChunks) * 8;
     auto prefetch = [&](int k0) {
       if constexpr (kBf16) {
+        if (unit_blocks) {
+          const int klast = (kend_wg - 1) & ~(kUnitKeys - 1);
 #pragma unroll
-        for (int r = 0; r < Lds::kUnits; ++r) {
-          const int idx = threadIdx.x + 256 * r;
-          const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
-          const int key = k0 + kk;
-          pk[r] = key < kend_wg ? *reinterpret_cast<const uint4*>(kc + row_of(key) + c * 8)
-                                : make_uint4(0, 0, 0, 0);
+          for (int r = 0; r < Lds::kUnits; ++r) {
+            const int kr = min(k0 + kUnitKeys * r, klast);
+            const T* base = kc + (int64_t)((uint64_t)(uint32_t)table[kr >> bs_log2] * blk_elems) + kv_off;
+            pk[r] = load16(base + ((uint32_t)(kr & bs_mask) * (uint32_t)slot_stride + k_thr_off));
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < Lds::kUnits; ++r) {
+            const int idx = threadIdx.x + 256 * r;
+            const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
+            const int key = min(k0 + kk, kend_wg - 1);
+            pk[r] = load16(kc + row_of(key) + c * 8);
+          }
         }
-        // V: four consecutive keys of one 8-dim chunk; the key quad varies
-        // fastest over the lanes so the transposed LDS stores hit distinct banks
-        if (threadIdx.x < Lds::vUnits) {
+        // V: four consecutive keys of one 8-dim chunk (one block: block sizes
+        // are powers of two >= 4 here); the key quad varies fastest over the
+        // lanes so the transposed LDS stores hit distinct banks
+        if (Lds::vUnits == 256 || threadIdx.x < Lds::vUnits) {
           const int kq = threadIdx.x & (kTileKeys / 4 - 1), c = threadIdx.x / (kTileKeys / 4);
+          const int kv0 = k0 + 4 * kq;
+          if (bs_log2 >= 2) {
+            const int vb = min(kv0, kend_wg - 1);
+            const T* base = vc + (int64_t)((uint64_t)(uint32_t)table[vb >> bs_log2] * blk_elems) +
+                            kv_off + c * 8;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int key = k0 + 4 * kq + e;
-            pv[e] = key < kend_wg ? *reinterpret_cast<const uint4*>(vc + row_of(key) + c * 8)
-                                  : make_uint4(0, 0, 0, 0);
+            for (int e = 0; e < 4; ++e) {
+              const int key = min(kv0 + e, kend_wg - 1);
+              pv[e] = load16(base + (uint32_t)(key & bs_mask) * (uint32_t)slot_stride);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int key = min(kv0 + e, kend_wg - 1);
+              pv[e] = load16(vc + row_of(key) + c * 8);
+            }
           }
         }
       } else {
@@ -631,7 +700,7 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
           const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
           *reinterpret_cast<uint4*>(&lds.k[kk * Lds::kRow + c * 8]) = pk[r];
         }
-        if (threadIdx.x < Lds::vUnits) {
+        if (Lds::vUnits == 256 || threadIdx.x < Lds::vUnits) {
           const int kq = threadIdx.x & (kTileKeys / 4 - 1), c = threadIdx.x / (kTileKeys / 4);
           const uint32_t w[4][4] = {{pv[0].x, pv[0].y, pv[0].z, pv[0].w},
                                     {pv[1].x, pv[1].y, pv[1].z, pv[1].w},
@@ -665,6 +734,10 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
         }
       }
     };
+    // key of accumulator value r of subtile t for this lane
+    auto key_of = [&](int k0, int t, int r) {
+      return kW ? k0 + 32 * t + 8 * (r >> 2) + 4 * grp + (r & 3) : k0 + 16 * t + 4 * grp + r;
+    };
 
     const int ntile = kend_wg > kbeg ? (kend_wg - kbeg + kTileKeys - 1) / kTileKeys : 0;
     if (ntile > 0) prefetch(kbeg);
@@ -676,14 +749,20 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
       if (ti + 1 < ntile) prefetch(k0 + kTileKeys);  // in flight during the compute below
       if (k0 >= kend_wave) continue;  // every row of this wave is past its causal end
 
-      // ---- S^T = K Q^T for the four 16-key subtiles
-      f32x4_t sc[4];
+      // ---- S^T = K Q^T for the key subtiles
+      AccT sc[kST];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        sc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < kST; ++t) {
+#pragma unroll
+        for (int r = 0; r < kCV; ++r) sc[t][r] = 0.f;
 #pragma unroll
         for (int s = 0; s < kKS; ++s) {
-          if constexpr (kBf16) {
+          if constexpr (kW) {
+            const uint4 w = *reinterpret_cast<const uint4*>(
+                &lds.k[(32 * t + col) * Lds::kRow + 16 * s + 8 * grp]);
+            sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, w),
+                                                            qop[s], sc[t], 0, 0, 0);
+          } else if constexpr (kBf16) {
             const uint4 w = *reinterpret_cast<const uint4*>(
                 &lds.k[(16 * t + col) * Lds::kRow + 32 * s + 8 * grp]);
             sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, w),
@@ -694,50 +773,80 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
           }
         }
       }
-      // ---- mask, online softmax (base 2); a tile every row of the wave
+      // ---- mask, online softmax (base 2). A tile every row of the wave
       // sees in full needs no per-key test (rows past the block's end only
-      // feed their own, never written, lanes)
-      float sv[4][4];
+      // feed their own, never written, lanes). The exponent reference m_run
+      // moves only when a row's tile max exceeds it by more than kLazy: the
+      // weights then stay below 2^kLazy (exact in fp32, relative error in
+      // bf16 unchanged), so the accumulator rescale is a rare wave-uniform
+      // branch instead of a multiply of every accumulator per tile.
+      constexpr float kLazy = 8.f;
       float cmax = -__builtin_inff();
       const bool full = k0 + kTileKeys - 1 <= qpos_wave_min && k0 + kTileKeys <= kend;
-      if (full) {
+      if (!full) {
+        // value (t, r) holds key key_of(k0, t, r) = key_of(k0, 0, 0) + a constant;
+        // rows past the end (row_ok false) use query 0's limit and are never written
+        const int lim = min(qpos + 1, kend) - key_of(k0, 0, 0);
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < kST; ++t)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            sv[t][e] = sc[t][e] * scale_log2;
-            cmax = fmaxf(cmax, sv[t][e]);
-          }
-      } else {
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int key = k0 + 16 * t + 4 * grp + e;
-            const bool ok = row_ok && key <= qpos && key < kend;
-            sv[t][e] = ok ? sc[t][e] * scale_log2 : -__builtin_inff();
-            cmax = fmaxf(cmax, sv[t][e]);
-          }
+          for (int r = 0; r < kCV; ++r)
+            sc[t][r] = key_of(0, t, r) - 4 * grp < lim ? sc[t][r] : -__builtin_inff();
       }
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+#pragma unroll
+      for (int t = 0; t < kST; ++t)
+#pragma unroll
+        for (int r = 0; r < kCV; ++r) cmax = fmaxf(cmax, sc[t][r]);
+      if constexpr (!kW) cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
       cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
-      const float m_new = fmaxf(m_run, cmax);
-      const float alpha = m_new == -__builtin_inff() ? 1.f : exp2f(m_run - m_new);
-      float pr[4][4];
+      const float cm = cmax * scale_log2;
+      if (__any(cm > m_run + kLazy)) {
+        const float m_new = fmaxf(m_run, cm);
+        const float alpha = m_new == -__builtin_inff() ? 1.f : exp2_fast(m_run - m_new);
+        l_part *= alpha;
+#pragma unroll
+        for (int u = 0; u < kDT; ++u) acc[u] *= alpha;
+        m_run = m_new;
+      }
+      // masked scores are -inf and give 0; a row with nothing unmasked yet
+      // keeps m_run = -inf and uses reference 0
+      const float neg_ref = m_run == -__builtin_inff() ? 0.f : -m_run;
+      float pr[kST][kCV];
       float psum = 0.f;
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < kST; ++t)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          pr[t][e] = sv[t][e] == -__builtin_inff() ? 0.f : exp2f(sv[t][e] - m_new);
-          psum += pr[t][e];
+        for (int r = 0; r < kCV; ++r) {
+          pr[t][r] = exp2_fast(fmaf(sc[t][r], scale_log2, neg_ref));
+          psum += pr[t][r];
         }
-      l_part = l_part * alpha + psum;
-      m_run = m_new;
-#pragma unroll
-      for (int u = 0; u < kDT; ++u) acc[u] *= alpha;
+      l_part += psum;
       // ---- O^T += V^T P^T
-      if constexpr (kBf16) {
+      if constexpr (kW) {
+        // 16-key k-steps: subtile t, half h covers keys 32t + 16h ..; this
+        // lane's values r = 8h .. 8h+7 are exactly the B operand's k-slots
+#pragma unroll
+        for (int t = 0; t < kST; ++t)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            uint4 pw;
+            pw.x = cvt_pk_bf16(pr[t][8 * hh + 0], pr[t][8 * hh + 1]);
+            pw.y = cvt_pk_bf16(pr[t][8 * hh + 2], pr[t][8 * hh + 3]);
+            pw.z = cvt_pk_bf16(pr[t][8 * hh + 4], pr[t][8 * hh + 5]);
+            pw.w = cvt_pk_bf16(pr[t][8 * hh + 6], pr[t][8 * hh + 7]);
+            const bf16x8_t pop = __builtin_bit_cast(bf16x8_t, pw);
+            const int kb = 32 * t + 16 * hh + 4 * grp;
+#pragma unroll
+            for (int u = 0; u < kDT; ++u) {
+              const uint16_t* vrow = &lds.vt[(32 * u + col) * Lds::vRow + kb];
+              const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+              const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+              const uint4 vw = make_uint4(lo.x, lo.y, hi.x, hi.y);
+              acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vw),
+                                                               pop, acc[u], 0, 0, 0);
+            }
+          }
+      } else if constexpr (kBf16) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           uint4 pw;
@@ -758,7 +867,7 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
         }
       } else {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < kST; ++t)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float* vrow = &lds.v[(16 * t + 4 * grp + e) * Lds::vRow];
@@ -769,34 +878,38 @@ __global__ void __launch_bounds__(256) attend_tile_kernel(
           }
       }
     }
-    // ---- row sums over the 4 lane groups, then write
+    // ---- row sums over the lane groups, then write
     float l_row = l_part;
-    l_row += __shfl_xor(l_row, 16, 64);
+    if constexpr (!kW) l_row += __shfl_xor(l_row, 16, 64);
     l_row += __shfl_xor(l_row, 32, 64);
     if (row_ok) {
       if (np == 1) {
         const float inv = l_row > 0.f ? 1.f / l_row : 0.f;
         T* orow = out + ((int64_t)tok * H + head) * D;
 #pragma unroll
-        for (int u = 0; u < kDT; ++u) {
-          const int d = 16 * u + 4 * grp;
-          if constexpr (kBf16) {
-            uint2 o;
-            o.x = cvt_pk_bf16(acc[u][0] * inv, acc[u][1] * inv);
-            o.y = cvt_pk_bf16(acc[u][2] * inv, acc[u][3] * inv);
-            *reinterpret_cast<uint2*>(orow + d) = o;
-          } else {
-            *reinterpret_cast<float4*>(orow + d) =
-                make_float4(acc[u][0] * inv, acc[u][1] * inv, acc[u][2] * inv, acc[u][3] * inv);
+        for (int u = 0; u < kDT; ++u)
+#pragma unroll
+          for (int b4 = 0; b4 < kCV / 4; ++b4) {
+            const int d = kW ? 32 * u + 8 * b4 + 4 * grp : 16 * u + 4 * grp;
+            const float x0 = acc[u][4 * b4] * inv, x1 = acc[u][4 * b4 + 1] * inv;
+            const float x2 = acc[u][4 * b4 + 2] * inv, x3 = acc[u][4 * b4 + 3] * inv;
+            if constexpr (kBf16) {
+              *reinterpret_cast<uint2*>(orow + d) = make_uint2(cvt_pk_bf16(x0, x1), cvt_pk_bf16(x2, x3));
+            } else {
+              *reinterpret_cast<float4*>(orow + d) = make_float4(x0, x1, x2, x3);
+            }
           }
-        }
       } else {
         const int64_t prow = (int64_t)split_base[i] + (int64_t)(j * H + head) * np + part;
         float* dst = po + prow * D;
 #pragma unroll
         for (int u = 0; u < kDT; ++u)
-          *reinterpret_cast<float4*>(dst + 16 * u + 4 * grp) =
-              make_float4(acc[u][0], acc[u][1], acc[u][2], acc[u][3]);
+#pragma unroll
+          for (int b4 = 0; b4 < kCV / 4; ++b4) {
+            const int d = kW ? 32 * u + 8 * b4 + 4 * grp : 16 * u + 4 * grp;
+            *reinterpret_cast<float4*>(dst + d) = make_float4(
+                acc[u][4 * b4], acc[u][4 * b4 + 1], acc[u][4 * b4 + 2], acc[u][4 * b4 + 3]);
+          }
         if (grp == 0) ml[prow] = make_float2(m_run, l_row);
       }
     }
@@ -1313,38 +1426,49 @@ int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
   // a few bandwidth-kernel items per resident workgroup
   const int target_items = fast ? kItemsPerWg * decode_grid() : 0;
   const int tile_target = kItemsPerWg * tile_grid();
-  plan_kernel<<<1, kPlanThreads, 0, st>>>(a.seq_lens, a.qsl, a.S, a.H, a.Hkv, fast, tile,
+  const bool wide = tile && a.dtype == VL_DTYPE_BF16;
+  plan_kernel<<<1, kPlanThreads, 0, st>>>(a.seq_lens, a.qsl, a.S, a.H, a.Hkv, fast, tile, wide,
                                           L.cap_rows, target_items, tile_target, L.hdr,
-                                          L.fast_off, L.gen_off,
-                                          L.tile_off, L.nparts, L.split_base, L.tail_order, L.ml);
+                                          L.fast_off, L.gen_off, L.tile_off, L.nparts,
+                                          L.split_base, L.tail_order, L.wide_off, L.ml);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
 
-template <typename T, int D>
-int launch_tile_d(const Args& a, const Layout& L, float sl2, int ncu, hipStream_t st) {
-  attend_tile_kernel<T, D><<<tile_grid(), 256, 0, st>>>(
+template <typename T, int D, int RW>
+int launch_tile_d(const Args& a, const Layout& L, float sl2, hipStream_t st) {
+  attend_tile_kernel<T, D, RW><<<tile_grid(), 256, 0, st>>>(
       (T*)a.out, (const T*)a.query, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.bt, a.bt_stride,
-      a.seq_lens, a.qsl, a.S, a.H, a.Hkv, __builtin_ctz(a.bs), sl2, L.hdr, L.tile_off, L.nparts,
-      L.split_base, L.ml, L.po);
+      a.seq_lens, a.qsl, a.S, a.H, a.Hkv, __builtin_ctz(a.bs), sl2, L.hdr,
+      RW == 32 ? L.wide_off : L.tile_off, L.nparts, L.split_base, L.ml, L.po);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
 
+// The 16-row tile kernel always (short-query and fp32 items); for bf16 also
+// the 32-row kernel when a sequence may have more than kSplitMaxQ queries.
 template <typename T>
-int launch_tile(const Args& a, const Layout& L, float sl2, int ncu, hipStream_t st) {
+int launch_tile(const Args& a, const Layout& L, float sl2, int max_q, hipStream_t st) {
+  const bool wide = sizeof(T) == 2 && (max_q <= 0 || max_q > kSplitMaxQ);
+  int rc = VL_OK;
   if constexpr (sizeof(T) == 2) {
     switch (a.D) {
-      case 64: return launch_tile_d<T, 64>(a, L, sl2, ncu, st);
-      case 128: return launch_tile_d<T, 128>(a, L, sl2, ncu, st);
+      case 64:
+        rc = launch_tile_d<T, 64, 16>(a, L, sl2, st);
+        if (!rc && wide) rc = launch_tile_d<T, 64, 32>(a, L, sl2, st);
+        return rc;
+      case 128:
+        rc = launch_tile_d<T, 128, 16>(a, L, sl2, st);
+        if (!rc && wide) rc = launch_tile_d<T, 128, 32>(a, L, sl2, st);
+        return rc;
     }
   } else {
     switch (a.D) {
-      case 16: return launch_tile_d<T, 16>(a, L, sl2, ncu, st);
-      case 32: return launch_tile_d<T, 32>(a, L, sl2, ncu, st);
-      case 48: return launch_tile_d<T, 48>(a, L, sl2, ncu, st);
-      case 64: return launch_tile_d<T, 64>(a, L, sl2, ncu, st);
-      case 128: return launch_tile_d<T, 128>(a, L, sl2, ncu, st);
+      case 16: return launch_tile_d<T, 16, 16>(a, L, sl2, st);
+      case 32: return launch_tile_d<T, 32, 16>(a, L, sl2, st);
+      case 48: return launch_tile_d<T, 48, 16>(a, L, sl2, st);
+      case 64: return launch_tile_d<T, 64, 16>(a, L, sl2, st);
+      case 128: return launch_tile_d<T, 128, 16>(a, L, sl2, st);
     }
   }
   VL_CHECK_ARG(false, "no tile kernel for head_dim %d", a.D);
@@ -1366,7 +1490,7 @@ int do_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) 
     if (max_q == 1) return VL_OK;  // every sequence was a decode: nothing else to run
   }
   if (tile_shape(a.dtype, a.D, a.bs)) {
-    int rc = launch_tile<T>(a, L, sl2, ncu, st);
+    int rc = launch_tile<T>(a, L, sl2, max_q, st);
     if (rc) return rc;
   } else {
     attend_generic_kernel<T><<<ncu * 16, 64, 0, st>>>(
