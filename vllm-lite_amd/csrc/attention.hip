@@ -538,7 +538,7 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
 // a lane holds row l%32; its S^T values are keys 32t + 8(r/4) + 4(l/32) + r%4
 // (r < 16) and its O^T values dims 32u + 8(r/4) + 4(l/32) + r%4.
 template <typename T, int D, int RW>
-__global__ void __launch_bounds__(256) attend_tile_kernel(
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) attend_tile_kernel(
     T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const T* __restrict__ kc,
     const T* __restrict__ vc, const int32_t* __restrict__ bt, int bt_stride,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H, int Hkv,
