@@ -35,6 +35,12 @@ constexpr int kHdrInts = 64;  // [0] bandwidth-kernel items [1] generic items [2
                               // [7] range length [8] bandwidth-kernel work counter
                               // [9] bandwidth-kernel workgroups finished
                               // [10] 32-row tile items
+                              // [12] split sequences for the combine kernel
+                              // [11] 1: bandwidth-kernel decodes and tile items
+                              // together (the step kernel runs them, the
+                              // decode and tile kernels exit)
+                              // [16..25] step kernel: work counters of the decode
+                              // queue and the 8 tile queues, workgroups finished
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxHeadDim = 256;
 constexpr int kSplitMaxQ = 16;  // only sequences with <= this many queries split their context
@@ -72,13 +78,14 @@ struct Layout {
   int32_t* split_base;  // [S] first partial row, or -1
   int32_t* tail_order;  // [S] sequences with a short last range, longest first
   int32_t* wide_off;    // [S+1] 32-row MFMA tile workgroup items
+  int32_t* cmb_seq;     // [S] split sequences the combine kernel merges
   float2* ml;           // [cap_rows] (running max (log2 domain), running sum)
   float* po;            // [cap_rows, D] unnormalised partial outputs
   int64_t cap_rows;
 };
 
 inline size_t plan_bytes(int S) {
-  size_t b = kHdrInts * 4 + (size_t)(7 * S + 4) * 4;
+  size_t b = kHdrInts * 4 + (size_t)(8 * S + 5) * 4;
   return (b + 255) & ~(size_t)255;
 }
 
@@ -93,6 +100,7 @@ inline Layout make_layout(void* ws, size_t bytes, int S, int D) {
   L.split_base = L.nparts + S;
   L.tail_order = L.split_base + S;
   L.wide_off = L.tail_order + S;
+  L.cmb_seq = L.wide_off + S + 1;
   const size_t pb = plan_bytes(S);
   const size_t per_row = (size_t)(D + 2) * 4;
   // rows: 8-byte (m, l) pairs, then a 256-byte aligned [rows, D] float array
@@ -232,7 +240,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     int32_t* __restrict__ fast_off, int32_t* __restrict__ gen_off,
     int32_t* __restrict__ tile_off, int32_t* __restrict__ nparts,
     int32_t* __restrict__ split_base, int32_t* __restrict__ tail_order,
-    int32_t* __restrict__ wide_off, float2* __restrict__ ml) {
+    int32_t* __restrict__ wide_off, int32_t* __restrict__ cmb_seq, float2* __restrict__ ml) {
   __shared__ unsigned long long need, bw_tokens, tile_keys;
   __shared__ int part_len, range_len;
   __shared__ int hist[kTailBuckets];
@@ -299,14 +307,16 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
                                           : (int)((int64_t)(blocks - 1) * kTailBuckets / rblocks);
     return kTailBuckets - 1 - k;  // ascending key = descending length
   };
-  int64_t f = 0, g = 0, r = 0, x = 0, tl = 0, wd = 0;
+  int64_t f = 0, g = 0, r = 0, x = 0, tl = 0, wd = 0, cm = 0;
   for (int i = s0; i < s1; ++i) {
     const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
     const SeqWork w = seq_work(q, c, P, R, H, Hkv, fast, tile, wide);
     f += w.full, g += w.gen, r += w.rows, x += w.tile, tl += w.tail, wd += w.wide;
+    cm += w.np > 1 && !is_bw(q, c, fast);
     if (w.tail) atomicAdd(&hist[tail_key(c)], 1);
   }
-  int64_t tf, tg, tr, tx, ttl, twd;
+  int64_t tf, tg, tr, tx, ttl, twd, tcm;
+  int64_t co = block_exclusive_scan(cm, &tcm);
   int64_t fo = block_exclusive_scan(f, &tf);
   int64_t go = block_exclusive_scan(g, &tg);
   int64_t ro = block_exclusive_scan(r, &tr);
@@ -329,6 +339,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     nparts[i] = w.np;
     split_base[i] = w.np > 1 ? (int32_t)ro : -1;
     if (w.tail) tail_order[atomicAdd(&hist[tail_key(c)], 1)] = i;
+    if (w.np > 1 && !is_bw(q, c, fast)) cmb_seq[co++] = i;
     if (w.np > 1 && is_bw(q, c, fast))  // arrival counters start at 0
       for (int k = 0; k < Hkv; ++k)
         reinterpret_cast<int32_t*>(ml + ro + (int64_t)H * w.np + k)[0] = 0;
@@ -350,6 +361,9 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     hdr[8] = 0;
     hdr[9] = 0;
     hdr[10] = (int32_t)twd;
+    hdr[11] = (tf + ttl) > 0 && (tx + twd) > 0;
+    hdr[12] = (int32_t)tcm;
+    for (int k = 16; k < 26; ++k) hdr[k] = 0;
   }
 }
 
@@ -531,20 +545,47 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// threadIdx.x, with kOpaque through an opaque move: values an item derives
+// from it are then recomputed per item instead of being hoisted out of a
+// persistent kernel's item loop, where they would stay live across the other
+// item kinds.
+template <bool kOpaque>
+__device__ __forceinline__ int item_tid() {
+  int t = threadIdx.x;
+  if constexpr (kOpaque) asm volatile("" : "+v"(t));
+  return t;
+}
+
+// Kernel parameters shared by the tile and decode items: the batch, the
+// plan's per-sequence arrays (full_off / tail_order: the decode items' range
+// order). They stay plain restrict-qualified kernel parameters so that the
+// compiler reads the plan's arrays with scalar loads. K/V are not restrict:
+// restrict-qualified loads are treated as invariant and may be scheduled past
+// the compiler barriers that batch them.
+#define VL_ATTN_PARAMS(T)                                                                    \
+  T *__restrict__ out, const T *__restrict__ query, int64_t q_stride, const T *kc,          \
+      const T *vc, const int32_t *__restrict__ bt, int bt_stride,                           \
+      const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ qsl, int S, int H,   \
+      int Hkv, int bs_log2, float scale_log2, const int32_t *__restrict__ full_off,          \
+      const int32_t *__restrict__ tail_order, const int32_t *__restrict__ nparts,            \
+      const int32_t *__restrict__ split_base, float2 *ml, float *po
+#define VL_ATTN_ARGS \
+  out, query, q_stride, kc, vc, bt, bt_stride, seq_lens, qsl, S, H, Hkv, bs_log2, scale_log2, \
+      full_off, tail_order, nparts, split_base, ml, po
+
+
+// One workgroup item of the tile kernel (256 threads; the caller's LDS).
 // RW = rows per wavefront: 16 (v_mfma_f32_16x16x32_bf16 / 16x16x4f32, 64-row
 // workgroups; short-query sequences, which may be split into partitions, and
 // fp32) or 32 (bf16 v_mfma_f32_32x32x16_bf16, 128-row workgroups, for long
 // query chunks: each K/V tile read from LDS feeds twice the rows). With RW 32
 // a lane holds row l%32; its S^T values are keys 32t + 8(r/4) + 4(l/32) + r%4
 // (r < 16) and its O^T values dims 32u + 8(r/4) + 4(l/32) + r%4.
-template <typename T, int D, int RW>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) attend_tile_kernel(
-    T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const T* __restrict__ kc,
-    const T* __restrict__ vc, const int32_t* __restrict__ bt, int bt_stride,
-    const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H, int Hkv,
-    int bs_log2, float scale_log2, const int32_t* __restrict__ hdr,
-    const int32_t* __restrict__ item_off, const int32_t* __restrict__ nparts,
-    const int32_t* __restrict__ split_base, float2* __restrict__ ml, float* __restrict__ po) {
+template <typename T, int D, int RW, bool kMixed>
+__device__ __forceinline__ void tile_body(TileLds<T, D>& lds, int it, int P,
+                                          const int32_t* __restrict__ item_off,
+                                          VL_ATTN_PARAMS(T)) {
+  const int tid = item_tid<kMixed>();
   constexpr bool kBf16 = sizeof(T) == 2;
   constexpr bool kW = RW == 32;
   static_assert(RW == 16 || (RW == 32 && kBf16), "32-row wavefronts are bf16 only");
@@ -557,17 +598,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
   using AccT = float __attribute__((ext_vector_type(kCV)));
   static_assert(!kBf16 || (Lds::kUnits * 256 == kTileKeys * Lds::kChunks && Lds::vUnits <= 256),
                 "bf16 tile staging assumes head_dim 64 or 128");
-  __shared__ Lds lds;
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
   const int col = lane & (RW - 1);  // the lane's row within the wave's rows
   const int grp = lane / RW;        // lane group: which keys / d chunk it holds
-  const int n_items = hdr[kW ? 10 : 4];
-  const int P = hdr[2];
   const int rep = H / Hkv;
   const int64_t slot_stride = (int64_t)Hkv * D;
 
-  for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
+  {
     const int i = wave_upper_bound_le(item_off, S + 1, it);
     const int q_len = qsl[i + 1] - qsl[i];
     const int ctx = seq_lens[i];
@@ -636,7 +674,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
     constexpr int kUnitKeys = 256 / Lds::kChunks;
     const bool unit_blocks = (1 << bs_log2) >= kUnitKeys;
     const uint32_t k_thr_off =
-        (uint32_t)(threadIdx.x / Lds::kChunks) * (uint32_t)slot_stride + (threadIdx.x % Lds::kChunks) * 8;
+        (uint32_t)(tid / Lds::kChunks) * (uint32_t)slot_stride + (tid % Lds::kChunks) * 8;
     auto prefetch = [&](int k0) {
       if constexpr (kBf16) {
         if (unit_blocks) {
@@ -650,7 +688,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
         } else {
 #pragma unroll
           for (int r = 0; r < Lds::kUnits; ++r) {
-            const int idx = threadIdx.x + 256 * r;
+            const int idx = tid + 256 * r;
             const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
             const int key = min(k0 + kk, kend_wg - 1);
             pk[r] = load16(kc + row_of(key) + c * 8);
@@ -659,8 +697,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
         // V: four consecutive keys of one 8-dim chunk (one block: block sizes
         // are powers of two >= 4 here); the key quad varies fastest over the
         // lanes so the transposed LDS stores hit distinct banks
-        if (Lds::vUnits == 256 || threadIdx.x < Lds::vUnits) {
-          const int kq = threadIdx.x & (kTileKeys / 4 - 1), c = threadIdx.x / (kTileKeys / 4);
+        if (Lds::vUnits == 256 || tid < Lds::vUnits) {
+          const int kq = tid & (kTileKeys / 4 - 1), c = tid / (kTileKeys / 4);
           const int kv0 = k0 + 4 * kq;
           if (bs_log2 >= 2) {
             const int vb = min(kv0, kend_wg - 1);
@@ -682,7 +720,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
       } else {
 #pragma unroll
         for (int r = 0; r < Lds::kUnits; ++r) {
-          const int idx = threadIdx.x + 256 * r;
+          const int idx = tid + 256 * r;
           const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
           const int key = k0 + kk;
           const bool ok = idx < kTileKeys * Lds::kChunks && key < kend_wg;
@@ -696,12 +734,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
       if constexpr (kBf16) {
 #pragma unroll
         for (int r = 0; r < Lds::kUnits; ++r) {
-          const int idx = threadIdx.x + 256 * r;
+          const int idx = tid + 256 * r;
           const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
           *reinterpret_cast<uint4*>(&lds.k[kk * Lds::kRow + c * 8]) = pk[r];
         }
-        if (Lds::vUnits == 256 || threadIdx.x < Lds::vUnits) {
-          const int kq = threadIdx.x & (kTileKeys / 4 - 1), c = threadIdx.x / (kTileKeys / 4);
+        if (Lds::vUnits == 256 || tid < Lds::vUnits) {
+          const int kq = tid & (kTileKeys / 4 - 1), c = tid / (kTileKeys / 4);
           const uint32_t w[4][4] = {{pv[0].x, pv[0].y, pv[0].z, pv[0].w},
                                     {pv[1].x, pv[1].y, pv[1].z, pv[1].w},
                                     {pv[2].x, pv[2].y, pv[2].z, pv[2].w},
@@ -721,7 +759,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
       } else {
 #pragma unroll
         for (int r = 0; r < Lds::kUnits; ++r) {
-          const int idx = threadIdx.x + 256 * r;
+          const int idx = tid + 256 * r;
           if (idx < kTileKeys * Lds::kChunks) {
             const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
             float* kd = &lds.k[kk * Lds::kRow + c * 4];
@@ -916,6 +954,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
   }
 }
 
+// RW = rows per wavefront (see tile_body). Items are strided over a grid
+// of resident workgroups.
+template <typename T, int D, int RW>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) attend_tile_kernel(
+    VL_ATTN_PARAMS(T), const int32_t* __restrict__ hdr, const int32_t* __restrict__ item_off) {
+  __shared__ TileLds<T, D> lds;
+  const int P = hdr[2];
+  if (hdr[11]) return;  // a mixed batch: the step kernel has these items
+  const int n_items = hdr[RW == 32 ? 10 : 4];
+  for (int it = blockIdx.x; it < n_items; it += gridDim.x)
+    tile_body<T, D, RW, false>(lds, it, P, item_off, VL_ATTN_ARGS);
+}
+
 // ---------------------------------------------------- bandwidth decode -----
 
 
@@ -986,47 +1037,35 @@ __device__ __forceinline__ float stride4_sum(float v) {
 //   device-scope release or acquire writes back / invalidates the XCD's
 //   whole L2 on gfx950, which made a fenced version 3x slower.
 //   The last workgroup to leave resets the work counter for the next run.
-__global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
-    uint16_t* __restrict__ out, const uint16_t* __restrict__ query, int64_t q_stride,
-    // not __restrict__: restrict-qualified loads are treated as invariant and
-    // may be scheduled past the compiler barriers that batch them
-    const uint16_t* kc, const uint16_t* vc,
-    const int32_t* __restrict__ bt, int bt_stride, const int32_t* __restrict__ seq_lens,
-    const int32_t* __restrict__ qsl, int S, int Hkv, float scale_log2,
-    const int32_t* __restrict__ hdr, int32_t* work, const int32_t* __restrict__ full_off,
-    const int32_t* __restrict__ tail_order, const int32_t* __restrict__ nparts,
-    const int32_t* __restrict__ split_base, float2* ml, float* po) {
-  __shared__ float4 p_lds[4][kFChunk * 16];  // per wave: [block][token] -> 4 heads
-  __shared__ uint4 q_lds[4][kFRep * 16];       // per wave: 4 heads x 128 bf16
-  __shared__ float4 acc_lds[4][8 * 64];        // per wave: accumulators between chunks,
-                                               // then its merged [head][dim] result
-  __shared__ float2 wml_lds[4][kFRep];         // per wave: (max, sum) per head
-  __shared__ int next_lds, last_lds;
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
+struct DecodeLds {
+  float4 p[4][kFChunk * 16];  // per wave: [block][token] -> 4 heads
+  uint4 q[4][kFRep * 16];     // per wave: 4 heads x 128 bf16
+  float4 acc[4][8 * 64];      // per wave: accumulators between chunks, then its
+                              // merged [head][dim] result
+  float2 wml[4][kFRep];       // per wave: (max, sum) per head
+  int last;
+};
+
+// One item (see above) by the 256 threads of a workgroup; n_full / R from
+// the plan header.
+template <bool kMixed>
+__device__ __forceinline__ void decode_body(DecodeLds& s, int it, int n_full, int R,
+                                            VL_ATTN_PARAMS(uint16_t)) {
+  const int tid = item_tid<kMixed>();
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
   const int qp = lane & 3, tk = lane >> 2;     // QK mapping
   const int vcn = lane & 15, vg = lane >> 4;  // PV mapping
-  const int n_items = hdr[0];
-  const int n_full = hdr[5];
-  const int R = hdr[7];
-  const int H = Hkv * kFRep;
+  // H = Hkv * kFRep (the bandwidth-kernel shape)
   const int64_t tok_stride = (int64_t)Hkv * kFD;  // elements per cache slot
-  float4* pw = p_lds[wave];
-  uint4* qw = q_lds[wave];
-  float4* stash = acc_lds[wave] + lane;  // stash[64 * k]: conflict-free
+  float4* pw = s.p[wave];
+  uint4* qw = s.q[wave];
+  float4* stash = s.acc[wave] + lane;  // stash[64 * k]: conflict-free
   float* pf = reinterpret_cast<float*>(pw);  // [block][token][head] scores, then probabilities
   const int64_t blk_bytes = (int64_t)kFBs * tok_stride * 2;
   const char* kbytes = reinterpret_cast<const char*>(kc);
   const char* vbytes = reinterpret_cast<const char*>(vc);
-
-  // Persistent workgroups (as many as fit on the chip): the first item is
-  // blockIdx.x, later ones are claimed from the work counter, the next one at
-  // the start of the current item so that the atomic's latency is hidden.
-  // The counter is zeroed by the plan and, after each run, by the merge kernel.
-  int it = blockIdx.x;
-  while (it < n_items) {
-    int nxt = 0;
-    if (threadIdx.x == 0) nxt = (int)gridDim.x + atomicAdd(work, 1);
+  {
     const int unit = it / Hkv;
     const int kvh = it - unit * Hkv;
     int i, part;
@@ -1235,7 +1274,7 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
       }
     // ---- merge the 4 wavefronts through LDS (the wave's stash area holds its
     // [head][128] result)
-    float* wres = reinterpret_cast<float*>(acc_lds[wave]);
+    float* wres = reinterpret_cast<float*>(s.acc[wave]);
     if (vg == 0) {
 #pragma unroll
       for (int h = 0; h < kFRep; ++h) {
@@ -1244,21 +1283,21 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
         dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
       }
     }
-    if (lane < kFRep) wml_lds[wave][lane] = make_float2(m_run, l_run);  // lane h holds head h
+    if (lane < kFRep) s.wml[wave][lane] = make_float2(m_run, l_run);  // lane h holds head h
     __syncthreads();
     {
       // thread: head h = tid / 64, dims 2 (tid % 64), +1
-      const int h = threadIdx.x >> 6, d = 2 * lane;
+      const int h = tid >> 6, d = 2 * lane;
       float M = -__builtin_inff();
 #pragma unroll
-      for (int w = 0; w < 4; ++w) M = fmaxf(M, wml_lds[w][h].x);
+      for (int w = 0; w < 4; ++w) M = fmaxf(M, s.wml[w][h].x);
       float L = 0.f, a0 = 0.f, a1 = 0.f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const float2 v = wml_lds[w][h];
+        const float2 v = s.wml[w][h];
         const float wt = v.x == -__builtin_inff() ? 0.f : exp2f(v.x - M);
         const float2 x = *reinterpret_cast<const float2*>(
-            reinterpret_cast<const float*>(acc_lds[w]) + h * kFD + d);
+            reinterpret_cast<const float*>(s.acc[w]) + h * kFD + d);
         L += v.y * wt;
         a0 += x.x * wt;
         a1 += x.y * wt;
@@ -1280,16 +1319,16 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
     }
     if (np > 1) {  // uniform over the workgroup
       __syncthreads();  // every thread's partial stores have completed
-      if (threadIdx.x == 0) {
+      if (tid == 0) {
         int32_t* cnt = reinterpret_cast<int32_t*>(ml + split_base[i] + (int64_t)H * np + kvh);
         const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last_lds = prev == np - 1;
+        s.last = prev == np - 1;
         if (prev == np - 1) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       __syncthreads();
-      if (last_lds) {
+      if (s.last) {
         asm volatile("" ::: "memory");  // no load below moves above the arrival
-        const int h = threadIdx.x >> 6, d = 2 * lane;
+        const int h = tid >> 6, d = 2 * lane;
         const int qh = kvh * kFRep + h;
         const int64_t r0 = (int64_t)split_base[i] + (int64_t)qh * np;
         const uint64_t* mlw = reinterpret_cast<const uint64_t*>(ml + r0);
@@ -1314,54 +1353,183 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
             (uint32_t)f32_to_bf16(a0 * inv) | ((uint32_t)f32_to_bf16(a1 * inv) << 16);
       }
     }
-    if (threadIdx.x == 0) next_lds = nxt;
-    __syncthreads();  // the merge has read every wavefront's LDS; next_lds is set
-    it = next_lds;
   }
-  // every work-counter claim of this workgroup has returned (the last one
-  // ended the loop): the last workgroup out resets both counters
+}
+
+// The last workgroup to leave a persistent kernel (every claim of every
+// workgroup has returned) zeroes the work counters counters[0..n) and the
+// exit counter counters[n] for the next run.
+__device__ __forceinline__ void leave_and_reset(int32_t* counters, int n) {
   if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(work + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int prev =
+        __hip_atomic_fetch_add(counters + n, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (prev == (int)gridDim.x - 1) {
-      __hip_atomic_store(work, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(work + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int k = 0; k <= n; ++k)
+        __hip_atomic_store(counters + k, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
 
+__global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
+    VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hdr, int32_t* work) {
+  __shared__ DecodeLds s;
+  __shared__ int next_lds;
+  const int n_items = hdr[0];
+  const int n_full = hdr[5];
+  const int R = hdr[7];
+  // Persistent workgroups (as many as fit on the chip): the first item is
+  // blockIdx.x, later ones are claimed from the work counter, the next one at
+  // the start of the current item so that the atomic's latency is hidden.
+  // The counter is zeroed by the plan and, after each run, by the last
+  // workgroup to leave.
+  int it = blockIdx.x;
+  while (it < n_items) {
+    int nxt = 0;
+    if (threadIdx.x == 0) nxt = (int)gridDim.x + atomicAdd(work, 1);
+    decode_body<false>(s, it, n_full, R, VL_ATTN_ARGS);
+    if (threadIdx.x == 0) next_lds = nxt;
+    __syncthreads();  // the merge has read every wavefront's LDS; next_lds is set
+    it = next_lds;
+  }
+  leave_and_reset(work, 1);
+}
+
+// ------------------------------------------------------------------ step --
+
+// One launch for a whole batch of the bandwidth-kernel shape (bf16, head_dim
+// 128, 4 query heads per KV head, 16-token blocks): decode items and MFMA
+// tile items (32-row, then 16-row), each kind from its own queues. Tile
+// items are dealt to 8 queues by item % 8 and a workgroup drains the queue of
+// its XCD (workgroups are dispatched round-robin over the 8 XCDs, so
+// blockIdx % 8 names it) before it helps the others: consecutive tile items
+// are the KV heads of one row block, so each XCD's L2 holds the K/V of its
+// own KV heads, which the other row blocks of the sequence read again. Half
+// of the persistent workgroups start on the tile queues and half on the
+// decode queue, so the compute units hold MFMA-bound and HBM-bound work at
+// the same time; a workgroup whose queues have run dry moves to the others.
+// The two item kinds share the LDS allocation. counters: [0] decode queue,
+// [1 + x] tile queue x, [9] workgroups finished.
+constexpr size_t kStepLds =
+    sizeof(TileLds<uint16_t, kFD>) > sizeof(DecodeLds) ? sizeof(TileLds<uint16_t, kFD>)
+                                                         : sizeof(DecodeLds);
+constexpr int kXcds = 8;
+#ifndef VL_STEP_TILE_FIRST
+#define VL_STEP_TILE_FIRST 2  // one in this many workgroups starts on the tile queues
+#endif
+
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+attend_step_bf16_kernel(VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hdr,
+                        const int32_t* __restrict__ wide_off, const int32_t* __restrict__ tile_off,
+                        int32_t* counters, int always) {
+  __shared__ __align__(16) unsigned char smem[kStepLds];
+  __shared__ int claim_lds;
+  auto& tl = *reinterpret_cast<TileLds<uint16_t, kFD>*>(smem);
+  auto& dl = *reinterpret_cast<DecodeLds*>(smem);
+  if (!always && !hdr[11]) return;  // not a mixed batch: the decode and tile kernels run it
+  const int P = hdr[2];
+  const int n_wide = hdr[10], n_tiles = n_wide + hdr[4], n_dec = hdr[0];
+  const int n_full = hdr[5], R = hdr[7];
+  const int xcd = blockIdx.x % kXcds;
+  const bool tiles_first = (blockIdx.x / kXcds) % VL_STEP_TILE_FIRST == 0;
+  for (int v = 0; v <= kXcds; ++v) {  // the decode queue and the 8 tile queues, in turn
+    const int qid = tiles_first ? (v < kXcds ? 1 + (xcd + v) % kXcds : 0)
+                                : (v == 0 ? 0 : 1 + (xcd + v - 1) % kXcds);
+    const bool tiles = qid != 0;
+    const int stride = tiles ? kXcds : 1, base = tiles ? qid - 1 : 0;
+    const int n = tiles ? n_tiles : n_dec;
+    __syncthreads();  // every thread has read the previous queue's last claim
+    if (threadIdx.x == 0) {
+      // a queue seen empty is skipped without an atomic; one thread decides,
+      // so the whole workgroup takes the same branch around the barriers
+      const int seen = __hip_atomic_load(counters + qid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      claim_lds = seen * stride + base >= n ? -1 : atomicAdd(counters + qid, 1);
+    }
+    __syncthreads();
+    if (claim_lds < 0) continue;
+    int it = claim_lds * stride + base;
+    while (it < n) {
+      int nxt = 0;
+      if (threadIdx.x == 0) nxt = atomicAdd(counters + qid, 1);  // the next item, claimed early
+      if (!tiles)
+        decode_body<true>(dl, it, n_full, R, VL_ATTN_ARGS);
+      else if (it < n_wide)
+        tile_body<uint16_t, kFD, 32, true>(tl, it, P, wide_off, VL_ATTN_ARGS);
+      else
+        tile_body<uint16_t, kFD, 16, true>(tl, it - n_wide, P, tile_off, VL_ATTN_ARGS);
+      __syncthreads();  // the item is done with the LDS; claim_lds has been read
+      if (threadIdx.x == 0) claim_lds = nxt;
+      __syncthreads();
+      it = claim_lds * stride + base;
+    }
+  }
+  leave_and_reset(counters, kXcds + 1);
+}
+
 // --------------------------------------------------------------- combine --
 
+// Merges the partitions of the split multi-query sequences (listed by the
+// plan): one workgroup per (sequence, query head) item, wavefront w takes the
+// sequence's query tokens w, w + 4, .... Lane p holds partition p's (max,
+// sum) and weight (64 partitions at a time); the output dims lane + 64k are
+// then summed over the partitions with the weights read lane by lane, so the
+// partial loads are independent of each other.
 template <typename T>
-__global__ void __launch_bounds__(64) combine_kernel(
-    T* __restrict__ out, const int32_t* __restrict__ qsl, const int32_t* __restrict__ seq_lens,
-    int S, int T_, int H, int D, bool fast, const int32_t* __restrict__ nparts,
-    const int32_t* __restrict__ split_base, const float2* __restrict__ ml,
-    const float* __restrict__ po) {
-  const int lane = threadIdx.x;
-  const int64_t pairs = (int64_t)T_ * H;
-  for (int64_t pr = blockIdx.x; pr < pairs; pr += gridDim.x) {
-    const int tok = (int)(pr / H), h = (int)(pr - (pr / H) * H);
-    const int i = upper_bound_le(qsl, S, tok);
+__global__ void __launch_bounds__(256) combine_kernel(
+    T* __restrict__ out, const int32_t* __restrict__ qsl, int H, int D,
+    const int32_t* __restrict__ hdr, const int32_t* __restrict__ cmb_seq,
+    const int32_t* __restrict__ nparts, const int32_t* __restrict__ split_base,
+    const float2* __restrict__ ml, const float* __restrict__ po) {
+  constexpr int kDk = kMaxHeadDim / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t items = (int64_t)hdr[12] * H;
+  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+    const int k = (int)(item / H), h = (int)(item - (item / H) * H);
+    const int i = cmb_seq[k];
     const int np = nparts[i];
-    if (np <= 1) continue;
-    if (fast && qsl[i + 1] - qsl[i] == 1 && seq_lens[i] > 0) continue;  // merged in place
-    const int j = tok - qsl[i];
-    const int64_t row0 = (int64_t)split_base[i] + (int64_t)(j * H + h) * np;
-    float M = -__builtin_inff();
-    for (int p = 0; p < np; ++p) M = fmaxf(M, ml[row0 + p].x);
-    float L = 0.f;
-    for (int p = 0; p < np; ++p) {
-      const float2 v = ml[row0 + p];
-      if (v.x != -__builtin_inff()) L += v.y * exp2f(v.x - M);
-    }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    for (int d = lane; d < D; d += 64) {
-      float a = 0.f;
-      for (int p = 0; p < np; ++p) {
-        const float2 v = ml[row0 + p];
-        if (v.x != -__builtin_inff()) a += po[(row0 + p) * D + d] * exp2f(v.x - M);
+    const int q = qsl[i + 1] - qsl[i];
+    for (int j = wave; j < q; j += 4) {
+      const int64_t row0 = (int64_t)split_base[i] + (int64_t)(j * H + h) * np;
+      float M = -__builtin_inff();
+      for (int p = lane; p < np; p += 64) M = fmaxf(M, ml[row0 + p].x);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+      float L = 0.f, acc[kDk];
+#pragma unroll
+      for (int e = 0; e < kDk; ++e) acc[e] = 0.f;
+      for (int p0 = 0; p0 < np; p0 += 64) {
+        float w = 0.f;
+        if (p0 + lane < np) {
+          const float2 v = ml[row0 + p0 + lane];
+          w = v.x == -__builtin_inff() ? 0.f : exp2_fast(v.x - M);
+          L += v.y * w;
+        }
+        const int cnt = min(64, np - p0);
+        const float* src = po + (row0 + p0) * D;
+        auto wt = [&](int u) {
+          return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u));
+        };
+        int u = 0;
+        for (; u + 4 <= cnt; u += 4) {  // four partitions' loads in flight
+#pragma unroll
+          for (int e = 0; e < kDk; ++e) {
+            if (lane + 64 * e >= D) continue;
+            const float* x = src + (int64_t)u * D + lane + 64 * e;
+            const float x0 = x[0], x1 = x[D], x2 = x[2 * D], x3 = x[3 * D];
+            acc[e] += x0 * wt(u) + x1 * wt(u + 1) + x2 * wt(u + 2) + x3 * wt(u + 3);
+          }
+        }
+        for (; u < cnt; ++u)
+#pragma unroll
+          for (int e = 0; e < kDk; ++e)
+            if (lane + 64 * e < D) acc[e] += src[(int64_t)u * D + lane + 64 * e] * wt(u);
       }
-      Elem<T>::store(out + ((int64_t)tok * H + h) * D, d, a * inv);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      T* dst = out + ((int64_t)(qsl[i] + j) * H + h) * D;
+#pragma unroll
+      for (int e = 0; e < kDk; ++e)
+        if (lane + 64 * e < D) Elem<T>::store(dst, lane + 64 * e, acc[e] * inv);
     }
   }
 }
@@ -1416,6 +1584,21 @@ int decode_grid() {
   return cached[dev];
 }
 
+int step_grid() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (!cached[dev]) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attend_step_bf16_kernel, 256, 0) !=
+            hipSuccess ||
+        per_cu <= 0)
+      per_cu = 2;
+    cached[dev] = per_cu * vl_num_cus();
+  }
+  return cached[dev];
+}
+
 // Workgroups the MFMA tile kernel is launched with (it loops over its items).
 int tile_grid() { return vl_num_cus() * 4; }
 
@@ -1430,17 +1613,22 @@ int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
   plan_kernel<<<1, kPlanThreads, 0, st>>>(a.seq_lens, a.qsl, a.S, a.H, a.Hkv, fast, tile, wide,
                                           L.cap_rows, target_items, tile_target, L.hdr,
                                           L.fast_off, L.gen_off, L.tile_off, L.nparts,
-                                          L.split_base, L.tail_order, L.wide_off, L.ml);
+                                          L.split_base, L.tail_order, L.wide_off, L.cmb_seq,
+                                          L.ml);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
 
+// The VL_ATTN_PARAMS arguments of a launch (inside do_run / launch_tile_d).
+#define VL_ATTN_LAUNCH_ARGS(T)                                                                  \
+  (T*)a.out, (const T*)a.query, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.bt, a.bt_stride,  \
+      a.seq_lens, a.qsl, a.S, a.H, a.Hkv, __builtin_ctz(a.bs), sl2, L.fast_off, L.tail_order,   \
+      L.nparts, L.split_base, L.ml, L.po
+
 template <typename T, int D, int RW>
 int launch_tile_d(const Args& a, const Layout& L, float sl2, hipStream_t st) {
   attend_tile_kernel<T, D, RW><<<tile_grid(), 256, 0, st>>>(
-      (T*)a.out, (const T*)a.query, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.bt, a.bt_stride,
-      a.seq_lens, a.qsl, a.S, a.H, a.Hkv, __builtin_ctz(a.bs), sl2, L.hdr,
-      RW == 32 ? L.wide_off : L.tile_off, L.nparts, L.split_base, L.ml, L.po);
+      VL_ATTN_LAUNCH_ARGS(T), L.hdr, RW == 32 ? L.wide_off : L.tile_off);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
@@ -1482,14 +1670,26 @@ int do_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) 
   const int ncu = vl_num_cus();
   const bool fast = fast_shape(a.dtype, a.H, a.Hkv, a.D, a.bs);
   if (fast) {
-    attend_decode_bf16_kernel<<<decode_grid(), 256, 0, st>>>(
-        (uint16_t*)a.out, (const uint16_t*)a.query, a.q_stride, (const uint16_t*)a.kc,
-        (const uint16_t*)a.vc, a.bt, a.bt_stride, a.seq_lens, a.qsl, a.S, a.Hkv, sl2, L.hdr,
-        L.hdr + 8, L.fast_off, L.tail_order, L.nparts, L.split_base, L.ml, L.po);
+    if (max_q == 1) {  // every sequence is a decode
+      attend_decode_bf16_kernel<<<decode_grid(), 256, 0, st>>>(VL_ATTN_LAUNCH_ARGS(uint16_t),
+                                                               L.hdr, L.hdr + 8);
+      VL_CHECK_LAUNCH();
+      return VL_OK;
+    }
+    // A known bound: the step kernel runs a batch of decodes and multi-query
+    // sequences (the plan's flag, read on the device) and the tile kernels,
+    // which are faster on their own, run one without decodes. An unknown
+    // bound: the step kernel runs the whole batch.
+    const bool step_all = max_q <= 0;
+    attend_step_bf16_kernel<<<step_grid(), 256, 0, st>>>(VL_ATTN_LAUNCH_ARGS(uint16_t), L.hdr,
+                                                         L.wide_off, L.tile_off, L.hdr + 16,
+                                                         step_all ? 1 : 0);
     VL_CHECK_LAUNCH();
-    if (max_q == 1) return VL_OK;  // every sequence was a decode: nothing else to run
-  }
-  if (tile_shape(a.dtype, a.D, a.bs)) {
+    if (!step_all) {
+      const int rc = launch_tile<T>(a, L, sl2, max_q, st);
+      if (rc) return rc;
+    }
+  } else if (tile_shape(a.dtype, a.D, a.bs)) {
     int rc = launch_tile<T>(a, L, sl2, max_q, st);
     if (rc) return rc;
   } else {
@@ -1499,10 +1699,8 @@ int do_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) 
         L.nparts, L.split_base, L.ml, L.po);
     VL_CHECK_LAUNCH();
   }
-  const int64_t pairs = (int64_t)a.T * a.H;
-  const int cgrid = (int)(pairs < 65536 ? pairs : 65536);
-  combine_kernel<T><<<cgrid, 64, 0, st>>>((T*)a.out, a.qsl, a.seq_lens, a.S, a.T, a.H, a.D, fast,
-                                          L.nparts, L.split_base, L.ml, L.po);
+  combine_kernel<T><<<ncu * 8, 256, 0, st>>>((T*)a.out, a.qsl, a.H, a.D, L.hdr, L.cmb_seq,
+                                            L.nparts, L.split_base, L.ml, L.po);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
