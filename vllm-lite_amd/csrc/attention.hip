@@ -71,43 +71,54 @@ constexpr int kTileKeys = 64;
 
 struct Layout {
   int32_t* hdr;
-  int32_t* fast_off;    // [S+1] bandwidth-kernel workgroup items
   int32_t* gen_off;     // [S+1] generic wavefront items
   int32_t* tile_off;    // [S+1] MFMA tile workgroup items
   int32_t* nparts;      // [S]
   int32_t* split_base;  // [S] first partial row, or -1
-  int32_t* tail_order;  // [S] sequences with a short last range, longest first
   int32_t* wide_off;    // [S+1] 32-row MFMA tile workgroup items
   int32_t* cmb_seq;     // [S] split sequences the combine kernel merges
+  int4* desc;           // [S + cap_rows] bandwidth-kernel ranges: (sequence, range,
+                        // context length, query token); full ranges in sequence
+                        // order, then the short last ranges, longest first
   float2* ml;           // [cap_rows] (running max (log2 domain), running sum)
   float* po;            // [cap_rows, D] unnormalised partial outputs
   int64_t cap_rows;
 };
 
 inline size_t plan_bytes(int S) {
-  size_t b = kHdrInts * 4 + (size_t)(8 * S + 5) * 4;
+  size_t b = kHdrInts * 4 + (size_t)(6 * S + 3) * 4;
   return (b + 255) & ~(size_t)255;
 }
+
+// Bytes of a workspace without partial rows: the plan, S range descriptors
+// and alignment padding.
+inline size_t fixed_bytes(int S) { return plan_bytes(S) + (size_t)S * 16 + 768; }
+
+// Workspace bytes per partial row: its (max, sum), D floats and a range
+// descriptor (a split sequence has at least as many rows as ranges).
+inline size_t row_bytes(int D) { return (size_t)(D + 2) * 4 + 16; }
 
 inline Layout make_layout(void* ws, size_t bytes, int S, int D) {
   Layout L;
   char* p = (char*)ws;
   L.hdr = (int32_t*)p;
-  L.fast_off = L.hdr + kHdrInts;
-  L.gen_off = L.fast_off + S + 1;
+  L.gen_off = L.hdr + kHdrInts;
   L.tile_off = L.gen_off + S + 1;
   L.nparts = L.tile_off + S + 1;
   L.split_base = L.nparts + S;
-  L.tail_order = L.split_base + S;
-  L.wide_off = L.tail_order + S;
+  L.wide_off = L.split_base + S;
   L.cmb_seq = L.wide_off + S + 1;
   const size_t pb = plan_bytes(S);
-  const size_t per_row = (size_t)(D + 2) * 4;
-  // rows: 8-byte (m, l) pairs, then a 256-byte aligned [rows, D] float array
-  int64_t rows = bytes > pb + 256 ? (int64_t)((bytes - pb - 256) / per_row) : 0;
+  // descriptors, 8-byte (m, l) pairs and a [rows, D] float array, each
+  // 256-byte aligned
+  const size_t fb = fixed_bytes(S);
+  const int64_t rows = bytes > fb ? (int64_t)((bytes - fb) / row_bytes(D)) : 0;
+  auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
   L.cap_rows = rows;
-  L.ml = (float2*)(p + pb);
-  L.po = (float*)(p + pb + (((size_t)rows * 8 + 255) & ~(size_t)255));
+  L.desc = (int4*)(p + pb);
+  const size_t ml_at = align(pb + (size_t)(S + rows) * 16);
+  L.ml = (float2*)(p + ml_at);
+  L.po = (float*)(p + align(ml_at + (size_t)rows * 8));
   return L;
 }
 
@@ -236,11 +247,10 @@ static_assert(kTailBuckets == kPlanThreads, "one tail bucket per plan thread");
 __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H, int Hkv,
     bool fast, bool tile, bool wide, int64_t cap_rows, int target_items, int tile_target,
-    int32_t* __restrict__ hdr,
-    int32_t* __restrict__ fast_off, int32_t* __restrict__ gen_off,
+    int32_t* __restrict__ hdr, int32_t* __restrict__ gen_off,
     int32_t* __restrict__ tile_off, int32_t* __restrict__ nparts,
-    int32_t* __restrict__ split_base, int32_t* __restrict__ tail_order,
-    int32_t* __restrict__ wide_off, int32_t* __restrict__ cmb_seq, float2* __restrict__ ml) {
+    int32_t* __restrict__ split_base, int32_t* __restrict__ wide_off,
+    int32_t* __restrict__ cmb_seq, int4* __restrict__ desc, float2* __restrict__ ml) {
   __shared__ unsigned long long need, bw_tokens, tile_keys;
   __shared__ int part_len, range_len;
   __shared__ int hist[kTailBuckets];
@@ -332,13 +342,13 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
   for (int i = s0; i < s1; ++i) {
     const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
     const SeqWork w = seq_work(q, c, P, R, H, Hkv, fast, tile, wide);
-    fast_off[i] = (int32_t)fo;
+    for (int k = 0; k < w.full; ++k) desc[fo + k] = make_int4(i, k, c, qsl[i]);
     gen_off[i] = (int32_t)go;
     tile_off[i] = (int32_t)xo;
     wide_off[i] = (int32_t)wo;
     nparts[i] = w.np;
     split_base[i] = w.np > 1 ? (int32_t)ro : -1;
-    if (w.tail) tail_order[atomicAdd(&hist[tail_key(c)], 1)] = i;
+    if (w.tail) desc[tf + atomicAdd(&hist[tail_key(c)], 1)] = make_int4(i, c / R, c, qsl[i]);
     if (w.np > 1 && !is_bw(q, c, fast)) cmb_seq[co++] = i;
     if (w.np > 1 && is_bw(q, c, fast))  // arrival counters start at 0
       for (int k = 0; k < Hkv; ++k)
@@ -346,7 +356,6 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     fo += w.full, go += w.gen, ro += w.rows, xo += w.tile, wo += w.wide;
   }
   if (t == 0) {
-    fast_off[S] = (int32_t)tf;
     gen_off[S] = (int32_t)tg;
     tile_off[S] = (int32_t)tx;
     wide_off[S] = (int32_t)twd;
@@ -557,8 +566,7 @@ __device__ __forceinline__ int item_tid() {
 }
 
 // Kernel parameters shared by the tile and decode items: the batch, the
-// plan's per-sequence arrays (full_off / tail_order: the decode items' range
-// order). They stay plain restrict-qualified kernel parameters so that the
+// plan's per-sequence arrays and the decode items' range descriptors. They stay plain restrict-qualified kernel parameters so that the
 // compiler reads the plan's arrays with scalar loads. K/V are not restrict:
 // restrict-qualified loads are treated as invariant and may be scheduled past
 // the compiler barriers that batch them.
@@ -566,12 +574,12 @@ __device__ __forceinline__ int item_tid() {
   T *__restrict__ out, const T *__restrict__ query, int64_t q_stride, const T *kc,          \
       const T *vc, const int32_t *__restrict__ bt, int bt_stride,                           \
       const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ qsl, int S, int H,   \
-      int Hkv, int bs_log2, float scale_log2, const int32_t *__restrict__ full_off,          \
-      const int32_t *__restrict__ tail_order, const int32_t *__restrict__ nparts,            \
+      int Hkv, int bs_log2, float scale_log2, const int4 *__restrict__ desc,                 \
+      const int32_t *__restrict__ nparts,                                                    \
       const int32_t *__restrict__ split_base, float2 *ml, float *po
 #define VL_ATTN_ARGS \
   out, query, q_stride, kc, vc, bt, bt_stride, seq_lens, qsl, S, H, Hkv, bs_log2, scale_log2, \
-      full_off, tail_order, nparts, split_base, ml, po
+      desc, nparts, split_base, ml, po
 
 
 // One workgroup item of the tile kernel (256 threads; the caller's LDS).
@@ -1046,10 +1054,37 @@ struct DecodeLds {
   int last;
 };
 
-// One item (see above) by the 256 threads of a workgroup; n_full / R from
-// the plan header.
+// An item's prologue: its range descriptor (sequence, range, context length,
+// query token), this lane's 16 bytes of the KV head's 4 query heads, and
+// (lane b < 16) block b of the wavefront's first chunk.
+struct DecodeItem {
+  int4 d;
+  uint4 q;
+  int bid0;
+};
+
+// The prologue of item `it` with descriptor d (a scalar load): the query and
+// the first chunk's block ids, loaded together.
+__device__ __forceinline__ DecodeItem decode_fetch(int4 d, int it, int R, int Hkv, int wave,
+                                                   int lane, const uint16_t* __restrict__ query,
+                                                   int64_t q_stride,
+                                                   const int32_t* __restrict__ bt, int bt_stride) {
+  DecodeItem x;
+  x.d = d;
+  const int kvh = it % Hkv;
+  x.q = load16(query + (int64_t)d.w * q_stride + (int64_t)kvh * kFRep * kFD + lane * 8);
+  const int kbeg = d.y * R, kend = min(d.z, kbeg + R);
+  const int ublk = (kend - kbeg + kFBs - 1) / kFBs;
+  const int nw = ublk > wave ? (ublk - wave + 3) >> 2 : 0;
+  const int wb0 = kbeg / kFBs + wave;
+  x.bid0 = lane < min(kFChunk, nw) ? bt[(int64_t)d.x * bt_stride + wb0 + 4 * lane] : 0;
+  return x;
+}
+
+// One item (see above) by the 256 threads of a workgroup, from its prologue
+// `cur`; R from the plan header.
 template <bool kMixed>
-__device__ __forceinline__ void decode_body(DecodeLds& s, int it, int n_full, int R,
+__device__ __forceinline__ void decode_body(DecodeLds& s, int it, const DecodeItem& cur, int R,
                                             VL_ATTN_PARAMS(uint16_t)) {
   const int tid = item_tid<kMixed>();
   const int wave = tid >> 6;
@@ -1066,19 +1101,9 @@ __device__ __forceinline__ void decode_body(DecodeLds& s, int it, int n_full, in
   const char* kbytes = reinterpret_cast<const char*>(kc);
   const char* vbytes = reinterpret_cast<const char*>(vc);
   {
-    const int unit = it / Hkv;
-    const int kvh = it - unit * Hkv;
-    int i, part;
-    if (unit < n_full) {
-      i = wave_upper_bound_le(full_off, S + 1, unit);
-      part = unit - full_off[i];
-    } else {
-      i = tail_order[unit - n_full];
-      part = seq_lens[i] / R;
-    }
+    const int kvh = it % Hkv;
+    const int i = cur.d.x, part = cur.d.y, ctx = cur.d.z, tok = cur.d.w;
     const int np = nparts[i];
-    const int ctx = seq_lens[i];
-    const int tok = qsl[i];
     const int kbeg = part * R;
     const int kend = min(ctx, kbeg + R);
     const int32_t* table = bt + (int64_t)i * bt_stride;
@@ -1087,11 +1112,7 @@ __device__ __forceinline__ void decode_body(DecodeLds& s, int it, int n_full, in
     const int nw = ublk > wave ? (ublk - wave + 3) >> 2 : 0;
     const int wb0 = kbeg / kFBs + wave;  // first block; stride 4
 
-    // query of the 4 heads to LDS: [head][16-byte chunk]
-    {
-      const uint16_t* qb = query + (int64_t)tok * q_stride + (int64_t)kvh * kFRep * kFD;
-      qw[lane] = *reinterpret_cast<const uint4*>(qb + lane * 8);
-    }
+    qw[lane] = cur.q;  // query of the 4 heads to LDS: [head][16-byte chunk]
     const int64_t kv_off = (int64_t)kvh * kFD;
     // byte offsets of this lane inside a block (a block is 16 slots x Hkv x 128 bf16)
     const uint32_t k_lane = (uint32_t)((tk * tok_stride + kv_off) * 2) + qp * 16;
@@ -1109,7 +1130,7 @@ __device__ __forceinline__ void decode_body(DecodeLds& s, int it, int n_full, in
     for (int c = 0; c < nw; c += kFChunk) {
       const int nblk = min(kFChunk, nw - c);
       // block ids of the chunk: lane b holds block b, broadcast with readlane
-      const int my_bid = lane < nblk ? table[wb0 + 4 * (c + lane)] : 0;
+      const int my_bid = c == 0 ? cur.bid0 : lane < nblk ? table[wb0 + 4 * (c + lane)] : 0;
       const int key0 = (wb0 + 4 * c) * kFBs;  // first key of chunk block 0; block b adds 64 b
       // ---- QK: kBK blocks per step, loads issued back to back (blocks past
       // the chunk end re-read the last block and are masked)
@@ -1375,8 +1396,8 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
   __shared__ DecodeLds s;
   __shared__ int next_lds;
   const int n_items = hdr[0];
-  const int n_full = hdr[5];
   const int R = hdr[7];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   // Persistent workgroups (as many as fit on the chip): the first item is
   // blockIdx.x, later ones are claimed from the work counter, the next one at
   // the start of the current item so that the atomic's latency is hidden.
@@ -1386,7 +1407,9 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
   while (it < n_items) {
     int nxt = 0;
     if (threadIdx.x == 0) nxt = (int)gridDim.x + atomicAdd(work, 1);
-    decode_body<false>(s, it, n_full, R, VL_ATTN_ARGS);
+    decode_body<false>(
+        s, it, decode_fetch(desc[it / Hkv], it, R, Hkv, wave, lane, query, q_stride, bt, bt_stride),
+        R, VL_ATTN_ARGS);
     if (threadIdx.x == 0) next_lds = nxt;
     __syncthreads();  // the merge has read every wavefront's LDS; next_lds is set
     it = next_lds;
@@ -1428,7 +1451,7 @@ attend_step_bf16_kernel(VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hd
   if (!always && !hdr[11]) return;  // not a mixed batch: the decode and tile kernels run it
   const int P = hdr[2];
   const int n_wide = hdr[10], n_tiles = n_wide + hdr[4], n_dec = hdr[0];
-  const int n_full = hdr[5], R = hdr[7];
+  const int R = hdr[7];
   const int xcd = blockIdx.x % kXcds;
   const bool tiles_first = (blockIdx.x / kXcds) % VL_STEP_TILE_FIRST == 0;
   for (int v = 0; v <= kXcds; ++v) {  // the decode queue and the 8 tile queues, in turn
@@ -1451,7 +1474,10 @@ attend_step_bf16_kernel(VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hd
       int nxt = 0;
       if (threadIdx.x == 0) nxt = atomicAdd(counters + qid, 1);  // the next item, claimed early
       if (!tiles)
-        decode_body<true>(dl, it, n_full, R, VL_ATTN_ARGS);
+        decode_body<true>(dl, it,
+                          decode_fetch(desc[it / Hkv], it, R, Hkv, threadIdx.x >> 6,
+                                       threadIdx.x & 63, query, q_stride, bt, bt_stride),
+                          R, VL_ATTN_ARGS);
       else if (it < n_wide)
         tile_body<uint16_t, kFD, 32, true>(tl, it, P, wide_off, VL_ATTN_ARGS);
       else
@@ -1561,8 +1587,8 @@ int check_args(const Args& a, const void* ws, size_t ws_bytes, bool need_kv) {
   VL_CHECK_ARG(a.seq_lens && a.qsl && ws, "null pointer");
   if (need_kv)
     VL_CHECK_ARG(a.out && a.query && a.kc && a.vc && a.bt, "null pointer");
-  VL_CHECK_ARG(ws_bytes >= plan_bytes(a.S), "workspace too small: %zu < %zu", ws_bytes,
-               plan_bytes(a.S));
+  VL_CHECK_ARG(ws_bytes >= fixed_bytes(a.S), "workspace too small: %zu < %zu", ws_bytes,
+               fixed_bytes(a.S));
   VL_CHECK_ARG(((uintptr_t)ws & 255) == 0, "workspace must be 256-byte aligned");
   return VL_OK;
 }
@@ -1612,9 +1638,8 @@ int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
   const bool wide = tile && a.dtype == VL_DTYPE_BF16;
   plan_kernel<<<1, kPlanThreads, 0, st>>>(a.seq_lens, a.qsl, a.S, a.H, a.Hkv, fast, tile, wide,
                                           L.cap_rows, target_items, tile_target, L.hdr,
-                                          L.fast_off, L.gen_off, L.tile_off, L.nparts,
-                                          L.split_base, L.tail_order, L.wide_off, L.cmb_seq,
-                                          L.ml);
+                                          L.gen_off, L.tile_off, L.nparts, L.split_base,
+                                          L.wide_off, L.cmb_seq, L.desc, L.ml);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
@@ -1622,8 +1647,8 @@ int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
 // The VL_ATTN_PARAMS arguments of a launch (inside do_run / launch_tile_d).
 #define VL_ATTN_LAUNCH_ARGS(T)                                                                  \
   (T*)a.out, (const T*)a.query, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.bt, a.bt_stride,  \
-      a.seq_lens, a.qsl, a.S, a.H, a.Hkv, __builtin_ctz(a.bs), sl2, L.fast_off, L.tail_order,   \
-      L.nparts, L.split_base, L.ml, L.po
+      a.seq_lens, a.qsl, a.S, a.H, a.Hkv, __builtin_ctz(a.bs), sl2, L.desc, L.nparts,          \
+      L.split_base, L.ml, L.po
 
 template <typename T, int D, int RW>
 int launch_tile_d(const Args& a, const Layout& L, float sl2, hipStream_t st) {
@@ -1713,7 +1738,7 @@ int dispatch_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_
 }  // namespace
 
 extern "C" size_t vl_paged_attention_min_workspace(int num_seqs) {
-  return plan_bytes(num_seqs < 0 ? 0 : num_seqs);
+  return fixed_bytes(num_seqs < 0 ? 0 : num_seqs);
 }
 
 extern "C" size_t vl_paged_attention_workspace_size(int num_seqs, int num_tokens, int num_heads,
@@ -1733,7 +1758,7 @@ extern "C" size_t vl_paged_attention_workspace_size(int num_seqs, int num_tokens
                         4 * kItemsPerWg * (int64_t)decode_grid() +
                             S * H * (cdiv64(ctx, kRangeMax) + 1));
   const int64_t rows = std::max(rows_tile, rows_fast);
-  return plan_bytes(num_seqs) + 256 + (size_t)rows * (size_t)(head_dim + 2) * 4;
+  return fixed_bytes(num_seqs) + (size_t)rows * row_bytes(head_dim);
 }
 
 extern "C" int vl_paged_attention_plan(const int32_t* seq_lens, const int32_t* query_start_loc,
