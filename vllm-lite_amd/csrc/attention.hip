@@ -165,21 +165,55 @@ __device__ __forceinline__ int wave_upper_bound_le(const int32_t* a, int n, int 
 
 // Exclusive scan of one int64 per thread across the workgroup; returns the
 // thread's offset and writes the total to *total.
-__device__ int64_t block_exclusive_scan(int64_t v, int64_t* total) {
-  __shared__ int64_t buf[kPlanThreads];
-  const int t = threadIdx.x;
-  buf[t] = v;
+// Exclusive prefix sums over the plan workgroup of N values per thread at
+// once (v is replaced by its prefix; total gets the sums): a shuffle scan
+// within each wavefront, a shuffle scan of the wavefront totals by the first
+// wavefront, then every thread adds its wavefront's offset. Three barriers
+// for all N values. The counts are item, row and sequence counts, which the
+// plan stores as int32.
+template <int N>
+__device__ void block_exclusive_scan(int (&v)[N], int (&total)[N]) {
+  constexpr int kWaves = kPlanThreads / 64;
+  __shared__ int wsum[kWaves + 1][N];  // wavefront offsets, then the total
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  int incl[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k) incl[k] = v[k];
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1)  // the N scans interleaved
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      const int a = __shfl_up(incl[k], o, 64);
+      if (lane >= o) incl[k] += a;
+    }
+  if (lane == 63)
+#pragma unroll
+    for (int k = 0; k < N; ++k) wsum[w][k] = incl[k];
   __syncthreads();
-  for (int o = 1; o < kPlanThreads; o <<= 1) {
-    const int64_t a = t >= o ? buf[t - o] : 0;
-    __syncthreads();
-    buf[t] += a;
-    __syncthreads();
+  if (w == 0) {
+    int x[N], inc[N];
+#pragma unroll
+    for (int k = 0; k < N; ++k) x[k] = inc[k] = lane < kWaves ? wsum[lane][k] : 0;
+#pragma unroll
+    for (int o = 1; o < kWaves; o <<= 1)
+#pragma unroll
+      for (int k = 0; k < N; ++k) {
+        const int a = __shfl_up(inc[k], o, 64);
+        if (lane >= o) inc[k] += a;
+      }
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      if (lane < kWaves) wsum[lane][k] = inc[k] - x[k];
+      if (lane == kWaves - 1) wsum[kWaves][k] = inc[k];
+    }
   }
-  const int64_t incl = buf[t];
-  *total = buf[kPlanThreads - 1];
   __syncthreads();
-  return incl - v;
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    v[k] = wsum[w][k] + incl[k] - v[k];
+    total[k] = wsum[kWaves][k];
+  }
+  __syncthreads();  // wsum may be reused
 }
 
 struct SeqWork {
@@ -325,17 +359,15 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     cm += w.np > 1 && !is_bw(q, c, fast);
     if (w.tail) atomicAdd(&hist[tail_key(c)], 1);
   }
-  int64_t tf, tg, tr, tx, ttl, twd, tcm;
-  int64_t co = block_exclusive_scan(cm, &tcm);
-  int64_t fo = block_exclusive_scan(f, &tf);
-  int64_t go = block_exclusive_scan(g, &tg);
-  int64_t ro = block_exclusive_scan(r, &tr);
-  int64_t xo = block_exclusive_scan(x, &tx);
-  block_exclusive_scan(tl, &ttl);
-  int64_t wo = block_exclusive_scan(wd, &twd);
+  int sc[7] = {(int)f, (int)g, (int)r, (int)x, (int)tl, (int)wd, (int)cm}, tot[7];
+  block_exclusive_scan(sc, tot);
+  int64_t fo = sc[0], go = sc[1], ro = sc[2], xo = sc[3], wo = sc[5], co = sc[6];
+  const int64_t tf = tot[0], tg = tot[1], tr = tot[2], tx = tot[3], ttl = tot[4], twd = tot[5],
+                tcm = tot[6];
   // bucket starts (kTailBuckets == kPlanThreads: one bucket per thread)
-  int64_t dummy;
-  const int64_t hstart = block_exclusive_scan(hist[t], &dummy);
+  int hs[1] = {hist[t]}, htot[1];
+  block_exclusive_scan(hs, htot);
+  const int64_t hstart = hs[0];
   __syncthreads();
   hist[t] = (int)hstart;
   __syncthreads();
