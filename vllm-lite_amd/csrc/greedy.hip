@@ -20,39 +20,64 @@ __device__ __forceinline__ bool arg_better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
+// Each thread scans its elements in increasing index order, so a strict
+// greater-than keeps the lowest index among its equal maxima and NaNs only
+// need their first index (ni); the reduction then merges (value, index)
+// pairs with arg_better, a NaN anywhere winning with its lowest index. A row
+// of -inf (no thread took a value) gives index 0.
 __device__ ArgBest block_argmax(const float* __restrict__ row, int vocab) {
+  constexpr int kNone = 0x7fffffff;
   float bv = -__builtin_inff();
-  int bi = 0x7fffffff;
+  int bi = kNone, ni = kNone;
+  auto take = [&](float e, int idx) {
+    if (e > bv) bv = e, bi = idx;
+    if (e != e && ni == kNone) ni = idx;
+  };
   const bool vec = (((uintptr_t)row) & 15) == 0;
   const int nv = vec ? vocab / 4 : 0;
   const float4* r4 = reinterpret_cast<const float4*>(row);
-  for (int i = threadIdx.x; i < nv; i += blockDim.x) {
-    const float4 q = r4[i];
-    const float e[4] = {q.x, q.y, q.z, q.w};
+  const int step = blockDim.x;
+  int i = threadIdx.x;
+  for (; i + 3 * step < nv; i += 4 * step) {  // four 16-byte loads in flight
+    float4 q[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (arg_better(e[k], 4 * i + k, bv, bi)) bv = e[k], bi = 4 * i + k;
+    for (int u = 0; u < 4; ++u) q[u] = r4[i + u * step];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int base = 4 * (i + u * step);
+      take(q[u].x, base), take(q[u].y, base + 1), take(q[u].z, base + 2), take(q[u].w, base + 3);
+    }
   }
-  for (int i = 4 * nv + threadIdx.x; i < vocab; i += blockDim.x)
-    if (arg_better(row[i], i, bv, bi)) bv = row[i], bi = i;
+  // the remaining 16-byte chunks keep the per-thread index order: chunk i
+  // and later ones all follow every chunk this thread has taken
+  for (; i < nv; i += step) {
+    const float4 q = r4[i];
+    take(q.x, 4 * i), take(q.y, 4 * i + 1), take(q.z, 4 * i + 2), take(q.w, 4 * i + 3);
+  }
+  for (int k = 4 * nv + threadIdx.x; k < vocab; k += step) take(row[k], k);
   // wave then workgroup reduction
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(bv, o, 64);
     const int oi = __shfl_xor(bi, o, 64);
     if (arg_better(ov, oi, bv, bi)) bv = ov, bi = oi;
+    ni = min(ni, __shfl_xor(ni, o, 64));
   }
   __shared__ float sv[16];
-  __shared__ int si[16];
+  __shared__ int si[16], sn[16];
   const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  if ((threadIdx.x & 63) == 0) sv[w] = bv, si[w] = bi;
+  if ((threadIdx.x & 63) == 0) sv[w] = bv, si[w] = bi, sn[w] = ni;
   __syncthreads();
   bv = sv[0];
   bi = si[0];
-  for (int k = 1; k < nw; ++k)
+  ni = sn[0];
+  for (int k = 1; k < nw; ++k) {
     if (arg_better(sv[k], si[k], bv, bi)) bv = sv[k], bi = si[k];
+    ni = min(ni, sn[k]);
+  }
   __syncthreads();
-  return {bv, bi};
+  if (ni != kNone) return {__builtin_nanf(""), ni};
+  return {bv, bi == kNone ? 0 : bi};
 }
 
 __global__ void __launch_bounds__(256) argmax_rows_kernel(const float* __restrict__ logits,
