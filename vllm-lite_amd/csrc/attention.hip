@@ -45,7 +45,7 @@ constexpr int kPlanThreads = 1024;
 constexpr int kMaxHeadDim = 256;
 constexpr int kSplitMaxQ = 16;  // only sequences with <= this many queries split their context
 #ifndef VL_PART0
-#define VL_PART0 256
+#define VL_PART0 64
 #endif
 constexpr int kPart0 = VL_PART0;  // first partition length tried by the planner
 constexpr float kLog2e = 1.4426950408889634f;
@@ -267,6 +267,10 @@ __device__ __forceinline__ SeqWork seq_work(int q, int c, int P, int R, int H, i
 #endif
 constexpr int kRangeMax = VL_RANGE_MAX;       // longest decode range the planner starts with
 constexpr int kItemsPerWg = VL_ITEMS_PER_WG;  // decode items aimed for per resident workgroup
+#ifndef VL_TILE_ITEMS_PER_WG
+#define VL_TILE_ITEMS_PER_WG 4
+#endif
+constexpr int kTileItemsPerWg = VL_TILE_ITEMS_PER_WG;  // split tile items aimed for per workgroup
 constexpr int kTailBuckets = 1024;
 static_assert(kTailBuckets == kPlanThreads, "one tail bucket per plan thread");
 
@@ -1666,7 +1670,7 @@ int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
   const bool tile = tile_shape(a.dtype, a.D, a.bs);
   // a few bandwidth-kernel items per resident workgroup
   const int target_items = fast ? kItemsPerWg * decode_grid() : 0;
-  const int tile_target = kItemsPerWg * tile_grid();
+  const int tile_target = kTileItemsPerWg * tile_grid();
   const bool wide = tile && a.dtype == VL_DTYPE_BF16;
   plan_kernel<<<1, kPlanThreads, 0, st>>>(a.seq_lens, a.qsl, a.S, a.H, a.Hkv, fast, tile, wide,
                                           L.cap_rows, target_items, tile_target, L.hdr,
