@@ -30,6 +30,9 @@ extern "C" {
 #define VL_EINVAL (-1)
 #define VL_DTYPE_F32 0
 #define VL_DTYPE_BF16 1
+#define VL_LINEAR_STORE 0      /* vl_linear_rows: out = f(x) @ W */
+#define VL_LINEAR_ACCUMULATE 1 /* out += f(x) @ W (the residual add) */
+#define VL_LINEAR_SWIGLU 2     /* out = silu(f(x) @ W[:, :n]) * (f(x) @ W[:, n:2n]) */
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* vl_last_error(void);
@@ -148,6 +151,27 @@ int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_out, float*
                       float* value_cache, const int32_t* positions, const int32_t* slot_mapping,
                       const float* cos_table, const float* sin_table, int64_t num_tokens,
                       int num_heads, int num_kv_heads, int head_dim, void* stream);
+
+/*
+ * K6 fp32 projections of the TinyLlama forward for at most 16 token rows
+ * (the decode steps), with their neighbours fused: f(x) = x, or when
+ * norm_weight != NULL the RMSNorm of each row of x times norm_weight (as
+ * vl_rms_norm computes it), then by mode
+ *   VL_LINEAR_STORE       out = f(x) @ W           (q/k/v: model.py:96-101;
+ *                                                  lm_head: model.py:119-120)
+ *   VL_LINEAR_ACCUMULATE  out += f(x) @ W          (the residual adds,
+ *                                                  model.py:114, 117)
+ *   VL_LINEAR_SWIGLU      out = silu(f(x) @ W[:, :n]) * (f(x) @ W[:, n:2n])
+ *                                                  (model.py:116-117, with
+ *                                                  W = [w_gate | w_up])
+ * x [rows, k] (16-byte aligned, row stride a multiple of 4), W [k, n] (or
+ * [k, 2n]) row-major with row stride weight_stride, out [rows, n]; out must
+ * not overlap x. rows <= 16, k a multiple of 16, k <= 1024 (512 for SWIGLU).
+ * fp32 throughout.
+ */
+int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_stride,
+                   const float* weight, int64_t weight_stride, const float* norm_weight,
+                   float eps, int rows, int k, int n, int mode, void* stream);
 
 /*
  * K5 greedy acceptance. Replaces verify (vllmlite/speculative.py:86-100).

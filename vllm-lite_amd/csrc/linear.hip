@@ -1,0 +1,197 @@
+// K6 fp32 projections of the TinyLlama forward for batches of at most 16
+// token rows (the decode steps), with the RMSNorm before them and the
+// residual add or SwiGLU gate after them fused in (vllmlite/model.py:96-101,
+// 114, 116-117, 119-120).
+//
+// One workgroup computes 16 rows x 16 output columns: the 4 wavefronts split
+// K four ways on v_mfma_f32_16x16x4f32, each loading its weight operands
+// straight into registers (all loads in flight at once) while the rows of x
+// are staged in LDS and normalised there; the four partial tiles are summed
+// in a fixed order. hipBLASLt runs these shapes as separate launches of
+// ~7 us each; here a projection and its neighbours are one.
+#include "vl_common.h"
+
+namespace {
+
+constexpr int kRowsMax = 16;
+constexpr int kCols = 16;
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// silu(g) * u with each step rounded like numpy's float32 elementwise ops
+__device__ __forceinline__ float silu_times_f32(float g, float u) {
+#pragma clang fp contract(off)
+  const float s = g / (1.0f + expf(-g));
+  return s * u;
+}
+
+// MODE 0: out = f(x) @ w; 1: out += f(x) @ w; 2: out = silu(f(x) @ w[:, :n]) *
+// (f(x) @ w[:, up_off : up_off + n]). f(x) = x, or with NORM the RMSNorm of x
+// (as rms_norm_kernel computes it) times norm_w.
+template <int MODE, bool NORM, int KMAX>
+__global__ void __launch_bounds__(256) linear_rows_kernel(
+    float* __restrict__ out, int64_t ldo, const float* __restrict__ x, int64_t ldx,
+    const float* __restrict__ w, int64_t ldw, int up_off, const float* __restrict__ norm_w,
+    float eps, int M, int K, int N) {
+  constexpr int kSlices = MODE == 2 ? 2 : 1;
+  constexpr int KP = KMAX + 4;  // xs row stride: rows 4 words apart, so the
+                                // 16 rows x 4 k of an A read hit 64 banks
+  constexpr int kSteps = KMAX / 16;  // 16x16x4 steps per wavefront at K = KMAX
+  __shared__ float xs[kRowsMax * KP];
+  __shared__ float red[kSlices][4][kRowsMax * kCols];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c0 = blockIdx.x * kCols;
+  const int m = lane & 15, j = lane >> 4;
+  const int kb = wave * (K / 4);  // wavefront w takes k in [w K/4, (w+1) K/4)
+  const int nsteps = K / 16;
+
+  // ---- the B operand straight into registers: step i of wavefront w needs
+  // w[kb + 4i + l/16][c0 + l%16] in lane l (columns past the end read 0);
+  // every load is issued before any is used
+  // (loads outside the shape read a clamped, valid element that is then
+  // multiplied by 0: columns past N, and steps past K / 4 of this wavefront,
+  // whose A values belong to the next wavefront's range. A select would let
+  // the compiler turn each load into a branch that waits for it.)
+  float wb[kSlices][kSteps];
+  const float colmask = c0 + m < N ? 1.f : 0.f;
+#pragma unroll
+  for (int s = 0; s < kSlices; ++s) {
+    const float* src = w + (s ? up_off : 0) + min(c0 + m, N - 1) + (int64_t)(kb + j) * ldw;
+#pragma unroll
+    for (int i = 0; i < kSteps; ++i)
+      wb[s][i] = src[(int64_t)(4 * min(i, nsteps - 1)) * ldw] * (i < nsteps ? colmask : 0.f);
+  }
+  // the norm weights of this lane's columns k = lane + 64 i (clamped loads)
+  float gw[KMAX / 64];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int i = 0; i < KMAX / 64; ++i) gw[i] = norm_w[min(lane + 64 * i, K - 1)];
+  }
+  // ---- x rows to LDS (rows >= M are zero): thread t takes row t / 16 and
+  // float4 columns t % 16 + 16 u
+  {
+    const int r = tid >> 4, q = tid & 15;
+    const int kq = K / 4;
+    float4 xv[KMAX / 64];
+    const float* xr = x + (int64_t)min(r, M - 1) * ldx;
+#pragma unroll
+    for (int u = 0; u < KMAX / 64; ++u) {
+      const int k4 = q + 16 * u;
+      const float z = r < M && k4 < kq ? 1.f : 0.f;  // rows past M, columns past K: 0
+      const float4 v = *reinterpret_cast<const float4*>(xr + 4 * min(k4, kq - 1));
+      xv[u] = make_float4(v.x * z, v.y * z, v.z * z, v.w * z);
+    }
+#pragma unroll
+    for (int u = 0; u < KMAX / 64; ++u)
+      *reinterpret_cast<float4*>(&xs[r * KP + 4 * (q + 16 * u)]) = xv[u];
+  }
+  __syncthreads();
+
+  if constexpr (NORM) {
+    // rows r = wave, wave + 4, ...: the sum of squares over k = lane + 64 i in
+    // increasing i, then the wavefront sum, as rms_norm_kernel
+    // (the 4 rows of a wavefront interleaved; columns past K hold zeros)
+    float ss[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < KMAX / 64; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float a = xs[(wave + 4 * q) * KP + lane + 64 * i];
+        ss[q] += a * a;
+      }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float rms = sqrtf(wave_sum(ss[q]) / (float)K + eps);
+      float* row = &xs[(wave + 4 * q) * KP + lane];
+#pragma unroll
+      for (int i = 0; i < KMAX / 64; ++i)
+        if (lane + 64 * i < K) row[64 * i] = (row[64 * i] / rms) * gw[i];
+    }
+    __syncthreads();
+  }
+
+  // ---- lane l supplies A[l%16][l/16] and B[l/16][l%16] of each 16x16x4 step
+  f32x4_t acc[kSlices];
+#pragma unroll
+  for (int s = 0; s < kSlices; ++s) acc[s] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+  const float* arow = &xs[m * KP + kb + j];
+  // all A reads first, then the MFMA chain (the reads of steps past K / 4
+  // stay inside the row and meet zero weights)
+  float av[kSteps];
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i) av[i] = arow[4 * i];
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i)
+#pragma unroll
+    for (int s = 0; s < kSlices; ++s)
+      acc[s] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], wb[s][i], acc[s], 0, 0, 0);
+  // C layout: lane l holds rows 4(l/16) + i of column l%16
+#pragma unroll
+  for (int s = 0; s < kSlices; ++s)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[s][wave][(4 * j + i) * kCols + m] = acc[s][i];
+  __syncthreads();
+
+  const int r = tid / kCols, c = tid - r * kCols;
+  if (r >= M || c0 + c >= N) return;
+  float v[kSlices];
+#pragma unroll
+  for (int s = 0; s < kSlices; ++s)
+    v[s] = ((red[s][0][tid] + red[s][1][tid]) + red[s][2][tid]) + red[s][3][tid];
+  float* dst = out + (int64_t)r * ldo + c0 + c;
+  if constexpr (MODE == 0) {
+    *dst = v[0];
+  } else if constexpr (MODE == 1) {
+    *dst = *dst + v[0];
+  } else {
+    *dst = silu_times_f32(v[0], v[1]);
+  }
+}
+
+template <int MODE, bool NORM, int KMAX>
+int launch(float* out, int64_t ldo, const float* x, int64_t ldx, const float* w, int64_t ldw,
+           int up_off, const float* norm_w, float eps, int M, int K, int N, hipStream_t st) {
+  const int grid = (N + kCols - 1) / kCols;
+  linear_rows_kernel<MODE, NORM, KMAX><<<grid, 256, 0, st>>>(out, ldo, x, ldx, w, ldw, up_off,
+                                                             norm_w, eps, M, K, N);
+  VL_CHECK_LAUNCH();
+  return VL_OK;
+}
+
+}  // namespace
+
+extern "C" int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_stride,
+                              const float* weight, int64_t weight_stride,
+                              const float* norm_weight, float eps, int rows, int k, int n,
+                              int mode, void* stream) {
+  VL_CHECK_ARG(rows >= 0 && rows <= kRowsMax, "rows must be in 0..%d", kRowsMax);
+  VL_CHECK_ARG(mode >= VL_LINEAR_STORE && mode <= VL_LINEAR_SWIGLU, "bad mode %d", mode);
+  VL_CHECK_ARG(k > 0 && k % 16 == 0 && k <= 1024, "k must be a multiple of 16, at most 1024");
+  VL_CHECK_ARG(n > 0, "n must be positive");
+  if (rows == 0) return VL_OK;
+  VL_CHECK_ARG(out && x && weight, "null pointer");
+  VL_CHECK_ARG((((uintptr_t)x) & 15) == 0 && x_stride % 4 == 0,
+               "x must be 16-byte aligned with a row stride that is a multiple of 4");
+  VL_CHECK_ARG(x_stride >= k && out_stride >= n, "row strides too small");
+  const int64_t wcols = mode == VL_LINEAR_SWIGLU ? 2 * (int64_t)n : n;
+  VL_CHECK_ARG(weight_stride >= wcols, "weight row stride too small");
+  hipStream_t st = (hipStream_t)stream;
+  const bool nrm = norm_weight != nullptr;
+  // KMAX, the unrolled depth, is the smallest of 384 / 512 / 1024 that holds k
+#define VL_LINEAR_K(MODE, NORM)                                                              \
+  (k <= 384 ? launch<MODE, NORM, 384>(out, out_stride, x, x_stride, weight, weight_stride,    \
+                                      MODE == 2 ? n : 0, norm_weight, eps, rows, k, n, st)    \
+   : k <= 512 ? launch<MODE, NORM, 512>(out, out_stride, x, x_stride, weight, weight_stride,  \
+                                        MODE == 2 ? n : 0, norm_weight, eps, rows, k, n, st)  \
+              : launch<MODE, NORM, 1024>(out, out_stride, x, x_stride, weight, weight_stride, \
+                                         MODE == 2 ? n : 0, norm_weight, eps, rows, k, n, st))
+  switch (mode) {
+    case VL_LINEAR_STORE:
+      return nrm ? VL_LINEAR_K(0, true) : VL_LINEAR_K(0, false);
+    case VL_LINEAR_ACCUMULATE:
+      return nrm ? VL_LINEAR_K(1, true) : VL_LINEAR_K(1, false);
+    default:
+      return nrm ? VL_LINEAR_K(2, true) : VL_LINEAR_K(2, false);
+  }
+#undef VL_LINEAR_K
+}

@@ -16,15 +16,17 @@ count) for scheduled sequence i, count = min(1 + drafts, tokens)
      with the K/V slot scatter, the ragged paged attention (planned once per
      step, run per layer), the output GEMM, fused RMSNorm(+residual), one
      gate|up GEMM, SwiGLU, the down GEMM; finally RMSNorm and the tied lm_head
-     on the logits rows only;
+     on the logits rows only. Steps of at most 16 tokens (the decode steps)
+     run each projection as one vl_linear_rows launch with the RMSNorm before
+     it and the residual add or SwiGLU after it fused in;
   4. one device-to-host copy of the logits rows and a stream synchronisation.
 
 Step 3 is captured once per shape bucket (tokens, sequences and logits rows
 each rounded up to a power of two) into a HIP graph and replayed afterwards;
 padded tokens belong to no sequence, carry slot -1 (no cache write) and
 position 0, padded sequences have no tokens and no context, and the rows they
-produce are never read. GEMMs are PyTorch (hipBLASLt) in fp32 with TF32-style
-reduced precision off; everything else is the gfx950 library.
+produce are never read. The larger steps' GEMMs are PyTorch (hipBLASLt) in fp32
+with TF32-style reduced precision off; everything else is the gfx950 library.
 
 The engine calls execute serially, possibly from a different thread each time
 (async_engine.py:47): every call selects the runner's device and stream.
@@ -146,6 +148,9 @@ class HipRunner(ModelRunner):
         self._attn = torch.zeros(cap, H, hd, **f32)
         self._gu = torch.zeros(cap, 2 * mc.d_ff, **f32)
         self._act = torch.zeros(cap, mc.d_ff, **f32)
+        # the fused small-batch projections cover d_model and d_ff up to their limits
+        self._fused_rows = (mc.d_model % 16 == 0 and mc.d_ff % 16 == 0 and mc.d_model <= 512
+                            and mc.d_ff <= 1024)
         self._hsel = torch.zeros(cap, mc.d_model, **f32)
         self._logits = torch.zeros(cap, mc.vocab_size, **f32)
         self._logits_host = torch.zeros(cap, mc.vocab_size, dtype=torch.float32, pin_memory=True)
@@ -236,6 +241,9 @@ class HipRunner(ModelRunner):
         gu, act = self._gu[:Tb], self._act[:Tb]
         W = self.w
         torch.index_select(W["tok_emb"], 0, tok, out=x)
+        if Tb <= ops.LINEAR_ROWS_MAX and self._fused_rows:
+            self._forward_rows(s, x, qkv, q, attn, act, tok, pos, slot, lidx, qsl, lens, bt)
+            return
         ops.rms_norm(h, x, W["layers"][0]["attn_norm"])
         ops.paged_attention_plan(q, self.cache_k[0], lens, qsl, self.block_size, self._ws)
         n_layers = mc.n_layers
@@ -256,6 +264,29 @@ class HipRunner(ModelRunner):
         hsel = self._hsel[:Rb]
         torch.index_select(h, 0, lidx, out=hsel)
         torch.mm(hsel, W["lm_head"], out=self._logits[:Rb])
+
+    def _forward_rows(self, s: _Shape, x, qkv, q, attn, act, tok, pos, slot, lidx, qsl, lens,
+                      bt) -> None:
+        """The forward for at most 16 token rows (the decode steps): each
+        projection is one vl_linear_rows launch with its RMSNorm, residual
+        add or SwiGLU fused in, so a layer is QKV, RoPE + cache, attention,
+        output (+= residual), gate|up (SwiGLU), down (+= residual)."""
+        W, Tb, Rb = self.w, s.Tb, s.Rb
+        ops.paged_attention_plan(q, self.cache_k[0], lens, qsl, self.block_size, self._ws)
+        for li, L in enumerate(W["layers"]):
+            kc, vc = self.cache_k[li], self.cache_v[li]
+            ops.linear_rows(qkv, x, L["w_qkv"], L["attn_norm"], mode=ops.LINEAR_STORE)
+            ops.rope_and_cache(qkv, q, kc, vc, pos, slot, self.cos, self.sin, self.H, self.Hkv,
+                               self.hd)
+            ops.paged_attention_run(attn, q, kc, vc, bt, lens, qsl, self.scale, self.block_size,
+                                    self._ws)
+            ops.linear_rows(x, attn.view(Tb, -1), L["wo"], mode=ops.LINEAR_ACCUMULATE)
+            ops.linear_rows(act, x, L["w_gate_up"], L["ffn_norm"], mode=ops.LINEAR_SWIGLU)
+            ops.linear_rows(x, act, L["w_down"], mode=ops.LINEAR_ACCUMULATE)
+        hsel = self._hsel[:Rb]
+        torch.index_select(x, 0, lidx, out=hsel)
+        ops.linear_rows(self._logits[:Rb], hsel, W["lm_head"], W["final_norm"],
+                        mode=ops.LINEAR_STORE)
 
     def _capture(self, s: _Shape, key) -> None:
         g = torch.cuda.CUDAGraph()

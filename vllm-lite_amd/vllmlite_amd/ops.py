@@ -49,6 +49,8 @@ SIGNATURES = {
     "vl_greedy_verify": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i32,
                                 _c_void_p, _c_void_p, _i32, _c_void_p]),
     "vl_argmax_rows": (_i32, [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p]),
+    "vl_linear_rows": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _f32,
+                              _i32, _i32, _i32, _i32, _c_void_p]),
 }
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -242,6 +244,27 @@ def rms_norm(out: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, eps: floa
     _need(residual is None or residual.shape == x.shape, "residual shape mismatch")
     _check(lib().vl_rms_norm(_ptr(out), _ptr(residual), _ptr(x), _ptr(weight), rows, dim,
                              float(eps), _stream()), "vl_rms_norm")
+
+
+LINEAR_STORE, LINEAR_ACCUMULATE, LINEAR_SWIGLU = 0, 1, 2
+LINEAR_ROWS_MAX = 16
+
+
+def linear_rows(out: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
+                norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
+                mode: int = LINEAR_STORE) -> None:
+    """out (=, += or SwiGLU of) f(x) @ weight for at most 16 fp32 rows; f is
+    the RMSNorm times norm_weight when given (see vl_linear_rows)."""
+    rows, k = x.shape
+    n = out.shape[1]
+    for t in (out, x, weight) + ((norm_weight,) if norm_weight is not None else ()):
+        _need(t.dtype == torch.float32 and t.stride(-1) == 1, "fp32 row-major tensors required")
+    _need(out.shape[0] == rows and weight.shape[0] == k, "shape mismatch")
+    _need(weight.shape[1] >= (2 * n if mode == LINEAR_SWIGLU else n), "weight too narrow")
+    _need(norm_weight is None or norm_weight.numel() == k, "norm weight shape mismatch")
+    _check(lib().vl_linear_rows(_ptr(out), out.stride(0), _ptr(x), x.stride(0), _ptr(weight),
+                                weight.stride(0), _ptr(norm_weight), float(eps), rows, k, n, mode,
+                                _stream()), "vl_linear_rows")
 
 
 def silu_mul(out: torch.Tensor, gate_up: torch.Tensor) -> None:
