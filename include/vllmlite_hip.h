@@ -174,6 +174,22 @@ int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_str
                    float eps, int rows, int k, int n, int mode, void* stream);
 
 /*
+ * K6b the QKV projection of a decode step fused with RoPE and the K/V
+ * scatter (vllmlite/model.py:96-103, 109; vllmlite/attention.py:21-37,
+ * 47-49): qkv = f(x) @ weight (weight [k, (num_heads + 2 num_kv_heads) *
+ * head_dim], f as in vl_linear_rows), then exactly what vl_rope_and_cache
+ * does with that row: rotated q to q_out [rows, num_heads * head_dim],
+ * rotated k and plain v to the caches at slot_mapping[r] (skipped when < 0).
+ * rows <= 16, k a multiple of 16, k <= 1024, head_dim even. fp32.
+ */
+int vl_qkv_rope_cache(float* q_out, float* key_cache, float* value_cache, const float* x,
+                      int64_t x_stride, const float* weight, int64_t weight_stride,
+                      const float* norm_weight, float eps, const int32_t* positions,
+                      const int32_t* slot_mapping, const float* cos_table, const float* sin_table,
+                      int rows, int k, int num_heads, int num_kv_heads, int head_dim,
+                      void* stream);
+
+/*
  * K5 greedy acceptance. Replaces verify (vllmlite/speculative.py:86-100).
  * Sequence i owns logits rows row_start[i] .. row_start[i] + num_drafts[i]
  * (vocab floats each, `row_stride` apart) and drafts[i, 0..num_drafts[i]).

@@ -99,3 +99,37 @@ def test_bad_arguments_raise():
     with pytest.raises(RuntimeError):
         o.linear_rows(torch.zeros((4, 384), device="cuda"), torch.zeros((4, 100), device="cuda"),
                       torch.zeros((100, 384), device="cuda"))
+
+
+@pytest.mark.parametrize("rows", [1, 13, 16])
+@pytest.mark.parametrize("shape", [(8, 4, 48, 384), (4, 2, 16, 64)])
+def test_qkv_rope_cache_equals_projection_then_rope(rows, shape):
+    """vl_qkv_rope_cache gives the same bits as vl_linear_rows followed by
+    vl_rope_and_cache: rotated q, rotated k and v at each row's slot, rows
+    with slot -1 writing q only."""
+    o = _ops()
+    H, Hkv, D, k = shape
+    n = (H + 2 * Hkv) * D
+    rng = np.random.default_rng(rows + D)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    x = dev(rng.standard_normal((rows, k)).astype(np.float32))
+    w = dev((0.05 * rng.standard_normal((k, n))).astype(np.float32))
+    g = dev((1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32))
+    pos = dev(rng.integers(0, 64, rows).astype(np.int32))
+    slots = rng.permutation(40)[:rows].astype(np.int32)
+    slots[::5] = -1
+    slot = dev(slots)
+    ang = rng.standard_normal((64, D // 2)).astype(np.float32)
+    cos, sin = dev(np.cos(ang)), dev(np.sin(ang))
+    kc1, vc1 = (torch.full((40, Hkv, D), float("nan"), device="cuda") for _ in range(2))
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    q1 = torch.empty((rows, H, D), device="cuda")
+    q2 = torch.empty_like(q1)
+    qkv = torch.empty((rows, n), device="cuda")
+    o.linear_rows(qkv, x, w, g, mode=o.LINEAR_STORE)
+    o.rope_and_cache(qkv, q1, kc1, vc1, pos, slot, cos, sin, H, Hkv, D)
+    o.qkv_rope_cache(q2.view(rows, -1), kc2, vc2, x, w, g, pos, slot, cos, sin, H, Hkv, D)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2)
+    assert torch.equal(kc1.nan_to_num(7.0), kc2.nan_to_num(7.0))
+    assert torch.equal(vc1.nan_to_num(7.0), vc2.nan_to_num(7.0))

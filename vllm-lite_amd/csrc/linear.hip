@@ -25,14 +25,39 @@ __device__ __forceinline__ float silu_times_f32(float g, float u) {
   return s * u;
 }
 
+// Interleaved-pair rotation with the reference's fp32 rounding (each product
+// rounded, then the difference / sum; vllmlite/attention.py:35-36), as the
+// RoPE kernel computes it.
+__device__ __forceinline__ void rotate_pair_f32(float e, float o, float c, float s, float* oe,
+                                                float* oo) {
+#pragma clang fp contract(off)
+  float ec = e * c, os = o * s, es = e * s, oc = o * c;
+  *oe = ec - os;
+  *oo = es + oc;
+}
+
+// Where MODE 3 puts the columns [q | k | v] of a fused QKV projection.
+struct RopeCache {
+  float* q_out;  // [rows, nh * hd]
+  float* kc;     // [slots, nkv * hd]
+  float* vc;
+  const int32_t* positions;
+  const int32_t* slots;
+  const float* cos_t;  // [max_pos, hd / 2]
+  const float* sin_t;
+  int nh, nkv, hd;
+};
+
 // MODE 0: out = f(x) @ w; 1: out += f(x) @ w; 2: out = silu(f(x) @ w[:, :n]) *
-// (f(x) @ w[:, up_off : up_off + n]). f(x) = x, or with NORM the RMSNorm of x
-// (as rms_norm_kernel computes it) times norm_w.
+// (f(x) @ w[:, up_off : up_off + n]); 3: f(x) @ w is a [q | k | v] row: q and k
+// rotated by RoPE, q to rc.q_out, k and v to the caches at the row's slot.
+// f(x) = x, or with NORM the RMSNorm of x (as rms_norm_kernel computes it)
+// times norm_w.
 template <int MODE, bool NORM, int KMAX>
 __global__ void __launch_bounds__(256) linear_rows_kernel(
     float* __restrict__ out, int64_t ldo, const float* __restrict__ x, int64_t ldx,
     const float* __restrict__ w, int64_t ldw, int up_off, const float* __restrict__ norm_w,
-    float eps, int M, int K, int N) {
+    float eps, int M, int K, int N, const RopeCache rc) {
   constexpr int kSlices = MODE == 2 ? 2 : 1;
   constexpr int KP = KMAX + 4;  // xs row stride: rows 4 words apart, so the
                                 // 16 rows x 4 k of an A read hit 64 banks
@@ -111,9 +136,14 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(
   }
 
   // ---- lane l supplies A[l%16][l/16] and B[l/16][l%16] of each 16x16x4 step
-  f32x4_t acc[kSlices];
+  // four independent accumulators per slice (steps i % 4), so consecutive
+  // MFMAs do not wait for each other's results
+  constexpr int kAcc = kSteps >= 4 ? 4 : 1;
+  f32x4_t acc4[kSlices][kAcc];
 #pragma unroll
-  for (int s = 0; s < kSlices; ++s) acc[s] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < kSlices; ++s)
+#pragma unroll
+    for (int q = 0; q < kAcc; ++q) acc4[s][q] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
   const float* arow = &xs[m * KP + kb + j];
   // all A reads first, then the MFMA chain (the reads of steps past K / 4
   // stay inside the row and meet zero weights)
@@ -124,7 +154,15 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(
   for (int i = 0; i < kSteps; ++i)
 #pragma unroll
     for (int s = 0; s < kSlices; ++s)
-      acc[s] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], wb[s][i], acc[s], 0, 0, 0);
+      acc4[s][i % kAcc] =
+          __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], wb[s][i], acc4[s][i % kAcc], 0, 0, 0);
+  f32x4_t acc[kSlices];
+#pragma unroll
+  for (int s = 0; s < kSlices; ++s) {
+    acc[s] = acc4[s][0];
+#pragma unroll
+    for (int q = 1; q < kAcc; ++q) acc[s] += acc4[s][q];
+  }
   // C layout: lane l holds rows 4(l/16) + i of column l%16
 #pragma unroll
   for (int s = 0; s < kSlices; ++s)
@@ -138,22 +176,46 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(
 #pragma unroll
   for (int s = 0; s < kSlices; ++s)
     v[s] = ((red[s][0][tid] + red[s][1][tid]) + red[s][2][tid]) + red[s][3][tid];
-  float* dst = out + (int64_t)r * ldo + c0 + c;
   if constexpr (MODE == 0) {
-    *dst = v[0];
+    out[(int64_t)r * ldo + c0 + c] = v[0];
   } else if constexpr (MODE == 1) {
+    float* dst = out + (int64_t)r * ldo + c0 + c;
     *dst = *dst + v[0];
+  } else if constexpr (MODE == 2) {
+    out[(int64_t)r * ldo + c0 + c] = silu_times_f32(v[0], v[1]);
   } else {
-    *dst = silu_times_f32(v[0], v[1]);
+    // the pair partner of column c is c ^ 1 in the same tile (head_dim even,
+    // tiles 16 columns)
+    const int pt = r * kCols + (c ^ 1);
+    const float partner = ((red[0][0][pt] + red[0][1][pt]) + red[0][2][pt]) + red[0][3][pt];
+    const int col = c0 + c, qd = rc.nh * rc.hd, kd = rc.nkv * rc.hd;
+    const int slot = rc.slots[r];
+    if (col < qd + kd) {
+      const int base = col < qd ? col : col - qd;
+      const int d = base % rc.hd, half = rc.hd >> 1;
+      const int64_t tab = (int64_t)rc.positions[r] * half + (d >> 1);
+      const bool odd = d & 1;
+      float oe, oo;
+      rotate_pair_f32(odd ? partner : v[0], odd ? v[0] : partner, rc.cos_t[tab], rc.sin_t[tab],
+                      &oe, &oo);
+      const float val = odd ? oo : oe;
+      if (col < qd)
+        rc.q_out[(int64_t)r * qd + col] = val;
+      else if (slot >= 0)
+        rc.kc[(int64_t)slot * kd + base] = val;
+    } else if (slot >= 0) {
+      rc.vc[(int64_t)slot * kd + (col - qd - kd)] = v[0];
+    }
   }
 }
 
 template <int MODE, bool NORM, int KMAX>
 int launch(float* out, int64_t ldo, const float* x, int64_t ldx, const float* w, int64_t ldw,
-           int up_off, const float* norm_w, float eps, int M, int K, int N, hipStream_t st) {
+           int up_off, const float* norm_w, float eps, int M, int K, int N, hipStream_t st,
+           const RopeCache& rc = RopeCache{}) {
   const int grid = (N + kCols - 1) / kCols;
   linear_rows_kernel<MODE, NORM, KMAX><<<grid, 256, 0, st>>>(out, ldo, x, ldx, w, ldw, up_off,
-                                                             norm_w, eps, M, K, N);
+                                                             norm_w, eps, M, K, N, rc);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
@@ -194,4 +256,36 @@ extern "C" int vl_linear_rows(float* out, int64_t out_stride, const float* x, in
       return nrm ? VL_LINEAR_K(2, true) : VL_LINEAR_K(2, false);
   }
 #undef VL_LINEAR_K
+}
+
+extern "C" int vl_qkv_rope_cache(float* q_out, float* key_cache, float* value_cache,
+                                 const float* x, int64_t x_stride, const float* weight,
+                                 int64_t weight_stride, const float* norm_weight, float eps,
+                                 const int32_t* positions, const int32_t* slot_mapping,
+                                 const float* cos_table, const float* sin_table, int rows, int k,
+                                 int num_heads, int num_kv_heads, int head_dim, void* stream) {
+  VL_CHECK_ARG(rows >= 0 && rows <= kRowsMax, "rows must be in 0..%d", kRowsMax);
+  VL_CHECK_ARG(k > 0 && k % 16 == 0 && k <= 1024, "k must be a multiple of 16, at most 1024");
+  VL_CHECK_ARG(num_heads > 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0,
+               "bad head shape (head_dim even)");
+  if (rows == 0) return VL_OK;
+  VL_CHECK_ARG(q_out && key_cache && value_cache && x && weight && positions && slot_mapping &&
+                   cos_table && sin_table,
+               "null pointer");
+  VL_CHECK_ARG((((uintptr_t)x) & 15) == 0 && x_stride % 4 == 0 && x_stride >= k,
+               "x must be 16-byte aligned with a row stride that is a multiple of 4");
+  const int n = (num_heads + 2 * num_kv_heads) * head_dim;
+  VL_CHECK_ARG(weight_stride >= n, "weight row stride too small");
+  RopeCache rc;
+  rc.q_out = q_out, rc.kc = key_cache, rc.vc = value_cache, rc.positions = positions;
+  rc.slots = slot_mapping, rc.cos_t = cos_table, rc.sin_t = sin_table;
+  rc.nh = num_heads, rc.nkv = num_kv_heads, rc.hd = head_dim;
+  hipStream_t st = (hipStream_t)stream;
+  const bool nrm = norm_weight != nullptr;
+#define VL_QKV(NORM, KM) \
+  launch<3, NORM, KM>(nullptr, 0, x, x_stride, weight, weight_stride, 0, norm_weight, eps, rows, k, n, st, rc)
+  if (k <= 384) return nrm ? VL_QKV(true, 384) : VL_QKV(false, 384);
+  if (k <= 512) return nrm ? VL_QKV(true, 512) : VL_QKV(false, 512);
+  return nrm ? VL_QKV(true, 1024) : VL_QKV(false, 1024);
+#undef VL_QKV
 }

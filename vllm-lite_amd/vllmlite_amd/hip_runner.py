@@ -242,7 +242,7 @@ class HipRunner(ModelRunner):
         W = self.w
         torch.index_select(W["tok_emb"], 0, tok, out=x)
         if Tb <= ops.LINEAR_ROWS_MAX and self._fused_rows:
-            self._forward_rows(s, x, qkv, q, attn, act, tok, pos, slot, lidx, qsl, lens, bt)
+            self._forward_rows(s, x, q, attn, act, pos, slot, lidx, qsl, lens, bt)
             return
         ops.rms_norm(h, x, W["layers"][0]["attn_norm"])
         ops.paged_attention_plan(q, self.cache_k[0], lens, qsl, self.block_size, self._ws)
@@ -265,19 +265,18 @@ class HipRunner(ModelRunner):
         torch.index_select(h, 0, lidx, out=hsel)
         torch.mm(hsel, W["lm_head"], out=self._logits[:Rb])
 
-    def _forward_rows(self, s: _Shape, x, qkv, q, attn, act, tok, pos, slot, lidx, qsl, lens,
+    def _forward_rows(self, s: _Shape, x, q, attn, act, pos, slot, lidx, qsl, lens,
                       bt) -> None:
         """The forward for at most 16 token rows (the decode steps): each
-        projection is one vl_linear_rows launch with its RMSNorm, residual
-        add or SwiGLU fused in, so a layer is QKV, RoPE + cache, attention,
-        output (+= residual), gate|up (SwiGLU), down (+= residual)."""
+        projection is one launch with its RMSNorm, residual add, SwiGLU or
+        RoPE + K/V scatter fused in, so a layer is QKV (+ RoPE + cache),
+        attention, output (+= residual), gate|up (SwiGLU), down (+= residual)."""
         W, Tb, Rb = self.w, s.Tb, s.Rb
         ops.paged_attention_plan(q, self.cache_k[0], lens, qsl, self.block_size, self._ws)
         for li, L in enumerate(W["layers"]):
             kc, vc = self.cache_k[li], self.cache_v[li]
-            ops.linear_rows(qkv, x, L["w_qkv"], L["attn_norm"], mode=ops.LINEAR_STORE)
-            ops.rope_and_cache(qkv, q, kc, vc, pos, slot, self.cos, self.sin, self.H, self.Hkv,
-                               self.hd)
+            ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, x, L["w_qkv"], L["attn_norm"], pos, slot,
+                               self.cos, self.sin, self.H, self.Hkv, self.hd)
             ops.paged_attention_run(attn, q, kc, vc, bt, lens, qsl, self.scale, self.block_size,
                                     self._ws)
             ops.linear_rows(x, attn.view(Tb, -1), L["wo"], mode=ops.LINEAR_ACCUMULATE)

@@ -51,6 +51,9 @@ SIGNATURES = {
     "vl_argmax_rows": (_i32, [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p]),
     "vl_linear_rows": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _f32,
                               _i32, _i32, _i32, _i32, _c_void_p]),
+    "vl_qkv_rope_cache": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
+                                 _i64, _c_void_p, _f32, _c_void_p, _c_void_p, _c_void_p,
+                                 _c_void_p, _i32, _i32, _i32, _i32, _i32, _c_void_p]),
 }
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -265,6 +268,25 @@ def linear_rows(out: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
     _check(lib().vl_linear_rows(_ptr(out), out.stride(0), _ptr(x), x.stride(0), _ptr(weight),
                                 weight.stride(0), _ptr(norm_weight), float(eps), rows, k, n, mode,
                                 _stream()), "vl_linear_rows")
+
+
+def qkv_rope_cache(q_out: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                   x: torch.Tensor, weight: torch.Tensor, norm_weight: Optional[torch.Tensor],
+                   positions: torch.Tensor, slot_mapping: torch.Tensor, cos: torch.Tensor,
+                   sin: torch.Tensor, num_heads: int, num_kv_heads: int, head_dim: int,
+                   eps: float = 1e-5) -> None:
+    """QKV projection of <= 16 rows fused with RoPE and the K/V scatter (see
+    vl_qkv_rope_cache)."""
+    rows, k = x.shape
+    for t in (q_out, key_cache, value_cache, x, weight, cos, sin):
+        _need(t.dtype == torch.float32 and t.stride(-1) == 1, "fp32 row-major tensors required")
+    _need(weight.shape[0] == k and positions.numel() >= rows and slot_mapping.numel() >= rows,
+          "shape mismatch")
+    _check(lib().vl_qkv_rope_cache(_ptr(q_out), _ptr(key_cache), _ptr(value_cache), _ptr(x),
+                                   x.stride(0), _ptr(weight), weight.stride(0), _ptr(norm_weight),
+                                   float(eps), _ptr(positions), _ptr(slot_mapping), _ptr(cos),
+                                   _ptr(sin), rows, k, num_heads, num_kv_heads, head_dim,
+                                   _stream()), "vl_qkv_rope_cache")
 
 
 def silu_mul(out: torch.Tensor, gate_up: torch.Tensor) -> None:
