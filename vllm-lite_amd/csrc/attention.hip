@@ -1052,6 +1052,57 @@ __device__ __forceinline__ float stride4_sum(float v) {
   return v;
 }
 
+// One output row's merge of np partitions written by other workgroups
+// (device-scope loads): lane p holds partition p's (max, sum) and weight, 64
+// partitions at a time; every lane sums its two dims over the partitions with
+// the weights read lane by lane, four partitions' loads in flight (relaxed
+// atomic loads are not batched by the compiler unless written out).
+// xrow: the lane's dims of partition 0; xstride: 8-byte words between
+// partitions. Returns the normalised pair.
+__device__ __forceinline__ float2 merge_partitions(const uint64_t* mlw, const uint64_t* xrow,
+                                                   int64_t xstride, int np, int lane) {
+  auto ld = [](const uint64_t* a) {
+    return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  float M = -__builtin_inff();
+  for (int p = lane; p < np; p += 64) M = fmaxf(M, lo_f(ld(mlw + p)));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+  float L = 0.f, a0 = 0.f, a1 = 0.f;
+  for (int p0 = 0; p0 < np; p0 += 64) {
+    float wgt = 0.f;
+    if (p0 + lane < np) {
+      const uint64_t v = ld(mlw + p0 + lane);
+      wgt = lo_f(v) == -__builtin_inff() ? 0.f : exp2_fast(lo_f(v) - M);
+      L += hi_f(v) * wgt;
+    }
+    auto wt = [&](int u) {
+      return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), u));
+    };
+    const int cnt = min(64, np - p0);
+    const uint64_t* src = xrow + (int64_t)p0 * xstride;
+    int u = 0;
+    for (; u + 4 <= cnt; u += 4) {
+      const uint64_t x0 = ld(src + (int64_t)u * xstride);
+      const uint64_t x1 = ld(src + (int64_t)(u + 1) * xstride);
+      const uint64_t x2 = ld(src + (int64_t)(u + 2) * xstride);
+      const uint64_t x3 = ld(src + (int64_t)(u + 3) * xstride);
+      a0 += lo_f(x0) * wt(u), a1 += hi_f(x0) * wt(u);
+      a0 += lo_f(x1) * wt(u + 1), a1 += hi_f(x1) * wt(u + 1);
+      a0 += lo_f(x2) * wt(u + 2), a1 += hi_f(x2) * wt(u + 2);
+      a0 += lo_f(x3) * wt(u + 3), a1 += hi_f(x3) * wt(u + 3);
+    }
+    for (; u < cnt; ++u) {
+      const uint64_t x = ld(src + (int64_t)u * xstride);
+      a0 += lo_f(x) * wt(u), a1 += hi_f(x) * wt(u);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  return make_float2(a0 * inv, a1 * inv);
+}
+
 // One workgroup item = (decode sequence, KV head, range of the context);
 // the 4 wavefronts split the range's 16-token blocks (wavefront w takes
 // blocks w, w + 4, ...), each for the KV head's 4 query heads, and merge
@@ -1388,26 +1439,11 @@ __device__ __forceinline__ void decode_body(DecodeLds& s, int it, const DecodeIt
         const int h = tid >> 6, d = 2 * lane;
         const int qh = kvh * kFRep + h;
         const int64_t r0 = (int64_t)split_base[i] + (int64_t)qh * np;
-        const uint64_t* mlw = reinterpret_cast<const uint64_t*>(ml + r0);
-        float M = -__builtin_inff();
-        for (int p = 0; p < np; ++p)
-          M = fmaxf(M, lo_f(__hip_atomic_load(mlw + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
-        float L = 0.f, a0 = 0.f, a1 = 0.f;
-#pragma unroll 4
-        for (int p = 0; p < np; ++p) {
-          const uint64_t mlp = __hip_atomic_load(mlw + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          const uint64_t xp = __hip_atomic_load(
-              reinterpret_cast<const uint64_t*>(po + (r0 + p) * kFD + d), __ATOMIC_RELAXED,
-              __HIP_MEMORY_SCOPE_AGENT);
-          const float m = lo_f(mlp);
-          const float wt = m == -__builtin_inff() ? 0.f : exp2f(m - M);
-          L += hi_f(mlp) * wt;
-          a0 += lo_f(xp) * wt;
-          a1 += hi_f(xp) * wt;
-        }
-        const float inv = L > 0.f ? 1.f / L : 0.f;
+        const float2 o = merge_partitions(
+            reinterpret_cast<const uint64_t*>(ml + r0),
+            reinterpret_cast<const uint64_t*>(po + r0 * kFD + d), kFD / 2, np, lane);
         reinterpret_cast<uint32_t*>(out + ((int64_t)tok * H + qh) * kFD)[lane] =
-            (uint32_t)f32_to_bf16(a0 * inv) | ((uint32_t)f32_to_bf16(a1 * inv) << 16);
+            (uint32_t)f32_to_bf16(o.x) | ((uint32_t)f32_to_bf16(o.y) << 16);
       }
     }
   }
