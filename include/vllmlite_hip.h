@@ -164,14 +164,16 @@ int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_out, float*
  *   VL_LINEAR_SWIGLU      out = silu(f(x) @ W[:, :n]) * (f(x) @ W[:, n:2n])
  *                                                  (model.py:116-117, with
  *                                                  W = [w_gate | w_up])
- * x [rows, k] (16-byte aligned, row stride a multiple of 4), W [k, n] (or
- * [k, 2n]) row-major with row stride weight_stride, out [rows, n]; out must
- * not overlap x. rows <= 16, k a multiple of 16, k <= 1024 (512 for SWIGLU).
- * fp32 throughout.
+ * x [*, k] (16-byte aligned, row stride a multiple of 4); row r of the
+ * input is x[row_index[r]] when row_index != NULL (the gather of the logits
+ * rows, runner.py:90), else x[r]. W [k, n] (or [k, 2n]) row-major with row
+ * stride weight_stride, out [rows, n]; out must not overlap x. rows <= 16, k
+ * a multiple of 16, k <= 1024. fp32 throughout.
  */
 int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_stride,
-                   const float* weight, int64_t weight_stride, const float* norm_weight,
-                   float eps, int rows, int k, int n, int mode, void* stream);
+                   const int32_t* row_index, const float* weight, int64_t weight_stride,
+                   const float* norm_weight, float eps, int rows, int k, int n, int mode,
+                   void* stream);
 
 /*
  * K6b the QKV projection of a decode step fused with RoPE and the K/V
@@ -180,10 +182,14 @@ int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_str
  * head_dim], f as in vl_linear_rows), then exactly what vl_rope_and_cache
  * does with that row: rotated q to q_out [rows, num_heads * head_dim],
  * rotated k and plain v to the caches at slot_mapping[r] (skipped when < 0).
- * rows <= 16, k a multiple of 16, k <= 1024, head_dim even. fp32.
+ * Input rows are x[row_index[r]] when row_index != NULL (the embedding
+ * gather tok_emb[token_ids], model.py:93), and when x_out != NULL the rows
+ * read (before the norm) are also written to x_out [rows, k] (the residual
+ * stream). rows <= 16, k a multiple of 16, k <= 1024, head_dim even. fp32.
  */
 int vl_qkv_rope_cache(float* q_out, float* key_cache, float* value_cache, const float* x,
-                      int64_t x_stride, const float* weight, int64_t weight_stride,
+                      int64_t x_stride, const int32_t* row_index, float* x_out,
+                      const float* weight, int64_t weight_stride,
                       const float* norm_weight, float eps, const int32_t* positions,
                       const int32_t* slot_mapping, const float* cos_table, const float* sin_table,
                       int rows, int k, int num_heads, int num_kv_heads, int head_dim,

@@ -133,3 +133,52 @@ def test_qkv_rope_cache_equals_projection_then_rope(rows, shape):
     assert torch.equal(q1, q2)
     assert torch.equal(kc1.nan_to_num(7.0), kc2.nan_to_num(7.0))
     assert torch.equal(vc1.nan_to_num(7.0), vc2.nan_to_num(7.0))
+
+
+def test_row_index_gathers_input_rows():
+    """With row_index the input rows are x[row_index] (the logits-row gather,
+    vllmlite/runner.py:90): the same bits as gathering first."""
+    o = _ops()
+    rng = np.random.default_rng(11)
+    x = torch.from_numpy(rng.standard_normal((40, 384)).astype(np.float32)).cuda()
+    w = torch.from_numpy((0.05 * rng.standard_normal((384, 261))).astype(np.float32)).cuda()
+    g = torch.from_numpy((1.0 + 0.1 * rng.standard_normal(384)).astype(np.float32)).cuda()
+    idx = torch.from_numpy(rng.integers(0, 40, 9).astype(np.int32)).cuda()
+    got = torch.empty((9, 261), device="cuda")
+    o.linear_rows(got, x, w, g, mode=o.LINEAR_STORE, row_index=idx)
+    want = torch.empty_like(got)
+    o.linear_rows(want, x[idx.long()].contiguous(), w, g, mode=o.LINEAR_STORE)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+def test_qkv_rope_cache_embedding_gather_and_residual_copy():
+    """Layer 0 reads its rows straight from the embedding table
+    (tok_emb[token_ids], vllmlite/model.py:93) and writes them out as the
+    residual stream: the same bits as gathering first, and x_out equal to
+    the gathered rows."""
+    o = _ops()
+    H, Hkv, D, k, rows = 8, 4, 48, 384, 11
+    n = (H + 2 * Hkv) * D
+    rng = np.random.default_rng(12)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    table = dev(rng.standard_normal((50, k)).astype(np.float32))
+    ids = dev(rng.integers(0, 50, rows).astype(np.int32))
+    w = dev((0.05 * rng.standard_normal((k, n))).astype(np.float32))
+    g = dev((1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32))
+    pos = dev(rng.integers(0, 64, rows).astype(np.int32))
+    slot = dev(rng.permutation(30)[:rows].astype(np.int32))
+    ang = rng.standard_normal((64, D // 2)).astype(np.float32)
+    cos, sin = dev(np.cos(ang)), dev(np.sin(ang))
+    kc1, vc1 = (torch.zeros((30, Hkv, D), device="cuda") for _ in range(2))
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    q1 = torch.empty((rows, H * D), device="cuda")
+    q2 = torch.empty_like(q1)
+    x_out = torch.full((rows, k), float("nan"), device="cuda")
+    o.qkv_rope_cache(q1, kc1, vc1, table[ids.long()].contiguous(), w, g, pos, slot, cos, sin, H,
+                     Hkv, D)
+    o.qkv_rope_cache(q2, kc2, vc2, table, w, g, pos, slot, cos, sin, H, Hkv, D, row_index=ids,
+                     x_out=x_out)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    assert torch.equal(x_out, table[ids.long()])

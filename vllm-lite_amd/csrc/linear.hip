@@ -57,7 +57,8 @@ template <int MODE, bool NORM, int KMAX>
 __global__ void __launch_bounds__(256) linear_rows_kernel(
     float* __restrict__ out, int64_t ldo, const float* __restrict__ x, int64_t ldx,
     const float* __restrict__ w, int64_t ldw, int up_off, const float* __restrict__ norm_w,
-    float eps, int M, int K, int N, const RopeCache rc) {
+    float eps, int M, int K, int N, const RopeCache rc, const int32_t* __restrict__ row_index,
+    float* __restrict__ x_out) {
   constexpr int kSlices = MODE == 2 ? 2 : 1;
   constexpr int KP = KMAX + 4;  // xs row stride: rows 4 words apart, so the
                                 // 16 rows x 4 k of an A read hit 64 banks
@@ -93,12 +94,14 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(
     for (int i = 0; i < KMAX / 64; ++i) gw[i] = norm_w[min(lane + 64 * i, K - 1)];
   }
   // ---- x rows to LDS (rows >= M are zero): thread t takes row t / 16 and
-  // float4 columns t % 16 + 16 u
+  // float4 columns t % 16 + 16 u; row r is x[row_index[r]] when an index is
+  // given, and workgroup 0 copies the rows it read to x_out when given
   {
     const int r = tid >> 4, q = tid & 15;
     const int kq = K / 4;
     float4 xv[KMAX / 64];
-    const float* xr = x + (int64_t)min(r, M - 1) * ldx;
+    const int rr = min(r, M - 1);
+    const float* xr = x + (int64_t)(row_index ? row_index[rr] : rr) * ldx;
 #pragma unroll
     for (int u = 0; u < KMAX / 64; ++u) {
       const int k4 = q + 16 * u;
@@ -109,6 +112,12 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(
 #pragma unroll
     for (int u = 0; u < KMAX / 64; ++u)
       *reinterpret_cast<float4*>(&xs[r * KP + 4 * (q + 16 * u)]) = xv[u];
+    if (x_out && blockIdx.x == 0 && r < M) {
+#pragma unroll
+      for (int u = 0; u < KMAX / 64; ++u)
+        if (q + 16 * u < kq)
+          *reinterpret_cast<float4*>(x_out + (int64_t)r * K + 4 * (q + 16 * u)) = xv[u];
+    }
   }
   __syncthreads();
 
@@ -212,10 +221,10 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(
 template <int MODE, bool NORM, int KMAX>
 int launch(float* out, int64_t ldo, const float* x, int64_t ldx, const float* w, int64_t ldw,
            int up_off, const float* norm_w, float eps, int M, int K, int N, hipStream_t st,
-           const RopeCache& rc = RopeCache{}) {
+           const int32_t* row_index, const RopeCache& rc = RopeCache{}, float* x_out = nullptr) {
   const int grid = (N + kCols - 1) / kCols;
-  linear_rows_kernel<MODE, NORM, KMAX><<<grid, 256, 0, st>>>(out, ldo, x, ldx, w, ldw, up_off,
-                                                             norm_w, eps, M, K, N, rc);
+  linear_rows_kernel<MODE, NORM, KMAX><<<grid, 256, 0, st>>>(
+      out, ldo, x, ldx, w, ldw, up_off, norm_w, eps, M, K, N, rc, row_index, x_out);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
@@ -223,9 +232,9 @@ int launch(float* out, int64_t ldo, const float* x, int64_t ldx, const float* w,
 }  // namespace
 
 extern "C" int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_stride,
-                              const float* weight, int64_t weight_stride,
-                              const float* norm_weight, float eps, int rows, int k, int n,
-                              int mode, void* stream) {
+                              const int32_t* row_index, const float* weight,
+                              int64_t weight_stride, const float* norm_weight, float eps,
+                              int rows, int k, int n, int mode, void* stream) {
   VL_CHECK_ARG(rows >= 0 && rows <= kRowsMax, "rows must be in 0..%d", kRowsMax);
   VL_CHECK_ARG(mode >= VL_LINEAR_STORE && mode <= VL_LINEAR_SWIGLU, "bad mode %d", mode);
   VL_CHECK_ARG(k > 0 && k % 16 == 0 && k <= 1024, "k must be a multiple of 16, at most 1024");
@@ -242,11 +251,14 @@ extern "C" int vl_linear_rows(float* out, int64_t out_stride, const float* x, in
   // KMAX, the unrolled depth, is the smallest of 384 / 512 / 1024 that holds k
 #define VL_LINEAR_K(MODE, NORM)                                                              \
   (k <= 384 ? launch<MODE, NORM, 384>(out, out_stride, x, x_stride, weight, weight_stride,    \
-                                      MODE == 2 ? n : 0, norm_weight, eps, rows, k, n, st)    \
+                                      MODE == 2 ? n : 0, norm_weight, eps, rows, k, n, st,     \
+                                      row_index)                                               \
    : k <= 512 ? launch<MODE, NORM, 512>(out, out_stride, x, x_stride, weight, weight_stride,  \
-                                        MODE == 2 ? n : 0, norm_weight, eps, rows, k, n, st)  \
+                                        MODE == 2 ? n : 0, norm_weight, eps, rows, k, n, st,   \
+                                        row_index)                                             \
               : launch<MODE, NORM, 1024>(out, out_stride, x, x_stride, weight, weight_stride, \
-                                         MODE == 2 ? n : 0, norm_weight, eps, rows, k, n, st))
+                                         MODE == 2 ? n : 0, norm_weight, eps, rows, k, n, st,  \
+                                         row_index))
   switch (mode) {
     case VL_LINEAR_STORE:
       return nrm ? VL_LINEAR_K(0, true) : VL_LINEAR_K(0, false);
@@ -259,7 +271,8 @@ extern "C" int vl_linear_rows(float* out, int64_t out_stride, const float* x, in
 }
 
 extern "C" int vl_qkv_rope_cache(float* q_out, float* key_cache, float* value_cache,
-                                 const float* x, int64_t x_stride, const float* weight,
+                                 const float* x, int64_t x_stride, const int32_t* row_index,
+                                 float* x_out, const float* weight,
                                  int64_t weight_stride, const float* norm_weight, float eps,
                                  const int32_t* positions, const int32_t* slot_mapping,
                                  const float* cos_table, const float* sin_table, int rows, int k,
@@ -283,7 +296,8 @@ extern "C" int vl_qkv_rope_cache(float* q_out, float* key_cache, float* value_ca
   hipStream_t st = (hipStream_t)stream;
   const bool nrm = norm_weight != nullptr;
 #define VL_QKV(NORM, KM) \
-  launch<3, NORM, KM>(nullptr, 0, x, x_stride, weight, weight_stride, 0, norm_weight, eps, rows, k, n, st, rc)
+  launch<3, NORM, KM>(nullptr, 0, x, x_stride, weight, weight_stride, 0, norm_weight, eps, rows, k, \
+                      n, st, row_index, rc, x_out)
   if (k <= 384) return nrm ? VL_QKV(true, 384) : VL_QKV(false, 384);
   if (k <= 512) return nrm ? VL_QKV(true, 512) : VL_QKV(false, 512);
   return nrm ? VL_QKV(true, 1024) : VL_QKV(false, 1024);

@@ -240,10 +240,10 @@ class HipRunner(ModelRunner):
         qkv, q, attn = self._qkv[:Tb], self._q[:Tb], self._attn[:Tb]
         gu, act = self._gu[:Tb], self._act[:Tb]
         W = self.w
-        torch.index_select(W["tok_emb"], 0, tok, out=x)
         if Tb <= ops.LINEAR_ROWS_MAX and self._fused_rows:
-            self._forward_rows(s, x, q, attn, act, pos, slot, lidx, qsl, lens, bt)
+            self._forward_rows(s, x, q, attn, act, tok, pos, slot, lidx, qsl, lens, bt)
             return
+        torch.index_select(W["tok_emb"], 0, tok, out=x)
         ops.rms_norm(h, x, W["layers"][0]["attn_norm"])
         ops.paged_attention_plan(q, self.cache_k[0], lens, qsl, self.block_size, self._ws)
         n_layers = mc.n_layers
@@ -265,7 +265,7 @@ class HipRunner(ModelRunner):
         torch.index_select(h, 0, lidx, out=hsel)
         torch.mm(hsel, W["lm_head"], out=self._logits[:Rb])
 
-    def _forward_rows(self, s: _Shape, x, q, attn, act, pos, slot, lidx, qsl, lens,
+    def _forward_rows(self, s: _Shape, x, q, attn, act, tok, pos, slot, lidx, qsl, lens,
                       bt) -> None:
         """The forward for at most 16 token rows (the decode steps): each
         projection is one launch with its RMSNorm, residual add, SwiGLU or
@@ -275,17 +275,20 @@ class HipRunner(ModelRunner):
         ops.paged_attention_plan(q, self.cache_k[0], lens, qsl, self.block_size, self._ws)
         for li, L in enumerate(W["layers"]):
             kc, vc = self.cache_k[li], self.cache_v[li]
-            ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, x, L["w_qkv"], L["attn_norm"], pos, slot,
-                               self.cos, self.sin, self.H, self.Hkv, self.hd)
+            if li == 0:  # the embedding gather, with x = tok_emb[tok] written out
+                ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, W["tok_emb"], L["w_qkv"],
+                                   L["attn_norm"], pos, slot, self.cos, self.sin, self.H,
+                                   self.Hkv, self.hd, row_index=tok, x_out=x)
+            else:
+                ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, x, L["w_qkv"], L["attn_norm"], pos,
+                                   slot, self.cos, self.sin, self.H, self.Hkv, self.hd)
             ops.paged_attention_run(attn, q, kc, vc, bt, lens, qsl, self.scale, self.block_size,
                                     self._ws)
             ops.linear_rows(x, attn.view(Tb, -1), L["wo"], mode=ops.LINEAR_ACCUMULATE)
             ops.linear_rows(act, x, L["w_gate_up"], L["ffn_norm"], mode=ops.LINEAR_SWIGLU)
             ops.linear_rows(x, act, L["w_down"], mode=ops.LINEAR_ACCUMULATE)
-        hsel = self._hsel[:Rb]
-        torch.index_select(x, 0, lidx, out=hsel)
-        ops.linear_rows(self._logits[:Rb], hsel, W["lm_head"], W["final_norm"],
-                        mode=ops.LINEAR_STORE)
+        ops.linear_rows(self._logits[:Rb], x, W["lm_head"], W["final_norm"],
+                        mode=ops.LINEAR_STORE, row_index=lidx)
 
     def _capture(self, s: _Shape, key) -> None:
         g = torch.cuda.CUDAGraph()

@@ -49,11 +49,12 @@ SIGNATURES = {
     "vl_greedy_verify": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i32,
                                 _c_void_p, _c_void_p, _i32, _c_void_p]),
     "vl_argmax_rows": (_i32, [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p]),
-    "vl_linear_rows": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _f32,
-                              _i32, _i32, _i32, _i32, _c_void_p]),
+    "vl_linear_rows": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64,
+                              _c_void_p, _f32, _i32, _i32, _i32, _i32, _c_void_p]),
     "vl_qkv_rope_cache": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
-                                 _i64, _c_void_p, _f32, _c_void_p, _c_void_p, _c_void_p,
-                                 _c_void_p, _i32, _i32, _i32, _i32, _i32, _c_void_p]),
+                                 _c_void_p, _c_void_p, _i64, _c_void_p, _f32, _c_void_p,
+                                 _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32,
+                                 _c_void_p]),
 }
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -255,35 +256,45 @@ LINEAR_ROWS_MAX = 16
 
 def linear_rows(out: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
                 norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
-                mode: int = LINEAR_STORE) -> None:
+                mode: int = LINEAR_STORE, row_index: Optional[torch.Tensor] = None) -> None:
     """out (=, += or SwiGLU of) f(x) @ weight for at most 16 fp32 rows; f is
-    the RMSNorm times norm_weight when given (see vl_linear_rows)."""
-    rows, k = x.shape
+    the RMSNorm times norm_weight when given; with row_index the input rows
+    are x[row_index] (see vl_linear_rows)."""
+    k = x.shape[1]
+    rows = out.shape[0] if row_index is not None else x.shape[0]
     n = out.shape[1]
+    _need(row_index is None or (row_index.dtype == torch.int32 and row_index.numel() >= rows),
+          "row_index must hold int32 row numbers")
     for t in (out, x, weight) + ((norm_weight,) if norm_weight is not None else ()):
         _need(t.dtype == torch.float32 and t.stride(-1) == 1, "fp32 row-major tensors required")
     _need(out.shape[0] == rows and weight.shape[0] == k, "shape mismatch")
     _need(weight.shape[1] >= (2 * n if mode == LINEAR_SWIGLU else n), "weight too narrow")
     _need(norm_weight is None or norm_weight.numel() == k, "norm weight shape mismatch")
-    _check(lib().vl_linear_rows(_ptr(out), out.stride(0), _ptr(x), x.stride(0), _ptr(weight),
-                                weight.stride(0), _ptr(norm_weight), float(eps), rows, k, n, mode,
-                                _stream()), "vl_linear_rows")
+    _check(lib().vl_linear_rows(_ptr(out), out.stride(0), _ptr(x), x.stride(0), _ptr(row_index),
+                                _ptr(weight), weight.stride(0), _ptr(norm_weight), float(eps),
+                                rows, k, n, mode, _stream()), "vl_linear_rows")
 
 
 def qkv_rope_cache(q_out: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
                    x: torch.Tensor, weight: torch.Tensor, norm_weight: Optional[torch.Tensor],
                    positions: torch.Tensor, slot_mapping: torch.Tensor, cos: torch.Tensor,
                    sin: torch.Tensor, num_heads: int, num_kv_heads: int, head_dim: int,
-                   eps: float = 1e-5) -> None:
-    """QKV projection of <= 16 rows fused with RoPE and the K/V scatter (see
+                   eps: float = 1e-5, row_index: Optional[torch.Tensor] = None,
+                   x_out: Optional[torch.Tensor] = None) -> None:
+    """QKV projection of <= 16 rows fused with RoPE and the K/V scatter; with
+    row_index the rows are x[row_index], copied to x_out when given (see
     vl_qkv_rope_cache)."""
-    rows, k = x.shape
+    k = x.shape[1]
+    rows = q_out.shape[0]
+    _need(row_index is not None or x.shape[0] >= rows, "x has too few rows")
+    _need(x_out is None or (x_out.is_contiguous() and x_out.shape[1] == k), "x_out shape mismatch")
     for t in (q_out, key_cache, value_cache, x, weight, cos, sin):
         _need(t.dtype == torch.float32 and t.stride(-1) == 1, "fp32 row-major tensors required")
     _need(weight.shape[0] == k and positions.numel() >= rows and slot_mapping.numel() >= rows,
           "shape mismatch")
     _check(lib().vl_qkv_rope_cache(_ptr(q_out), _ptr(key_cache), _ptr(value_cache), _ptr(x),
-                                   x.stride(0), _ptr(weight), weight.stride(0), _ptr(norm_weight),
+                                   x.stride(0), _ptr(row_index), _ptr(x_out), _ptr(weight),
+                                   weight.stride(0), _ptr(norm_weight),
                                    float(eps), _ptr(positions), _ptr(slot_mapping), _ptr(cos),
                                    _ptr(sin), rows, k, num_heads, num_kv_heads, head_dim,
                                    _stream()), "vl_qkv_rope_cache")
