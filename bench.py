@@ -149,12 +149,13 @@ def cpu_baseline(torch, b, budget_s=12.0):
 
 def mixed_leg(torch, ops, syn, steps, warmup, profile_only=False):
     """Scatter + plan + one attention launch over 16 prefill chunks and 200
-    decodes; also the prefill chunks alone and the decodes alone."""
+    decodes; also the prefill chunks alone and the decodes alone. profile_only
+    names the one part to run (True: the mixed batch)."""
     out = {}
     full = syn.mixed_8392_seqs(0)
     parts = {"mixed": full, "prefill_only": full[200:], "decode_only": full[:200]}
     for name, seqs in parts.items():
-        if profile_only and name != "mixed":
+        if profile_only and name != (profile_only if isinstance(profile_only, str) else "mixed"):
             continue
         b = syn.build(torch, seqs, seed=2)
         S, T = len(seqs), int(b["q_lens"].sum())
@@ -398,8 +399,8 @@ def main():
     ap.add_argument("--legs", default="decode,mixed,verify,cow,e2e",
                     help="comma-separated legs to run (decode is always run)")
     ap.add_argument("--profile-mode", default=None, metavar="LEG",
-                    help="only the timed launches of one leg (decode, mixed, verify, cow, e2e), "
-                         "for rocprofv3 passes")
+                    help="only the timed launches of one leg (decode, mixed, prefill, verify, cow, "
+                         "e2e), for rocprofv3 passes")
     ap.add_argument("--copy-only", action="store_true",
                     help="only 5 device copies of 1 GiB (calibrates rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE against a kernel of known traffic)")
@@ -427,6 +428,8 @@ def main():
         leg = args.profile_mode
         fn = {"decode": lambda: decode_leg(torch, ops, syn, args.steps, args.warmup, True),
               "mixed": lambda: mixed_leg(torch, ops, syn, args.steps, args.warmup, True),
+              "prefill": lambda: mixed_leg(torch, ops, syn, args.steps, args.warmup,
+                                           "prefill_only"),
               "verify": lambda: verify_leg(torch, ops, syn, args.steps, args.warmup, True),
               "cow": lambda: cow_leg(torch, ops, args.steps, args.warmup),
               "e2e": lambda: e2e_leg(cpu=False)}[leg]

@@ -41,6 +41,9 @@ constexpr int kHdrInts = 64;  // [0] bandwidth-kernel items [1] generic items [2
                               // decode and tile kernels exit)
                               // [16..25] step kernel: work counters of the decode
                               // queue and the 8 tile queues, workgroups finished
+                              // [26..33] 16-row tile kernel: work counters of its 8
+                              // queues; [34..41] the same for the 32-row kernel
+                              // (zeroed by the plan, then by every combine launch)
 constexpr int kPlanThreads = 1024;
 constexpr int kMaxHeadDim = 256;
 constexpr int kSplitMaxQ = 16;  // only sequences with <= this many queries split their context
@@ -75,8 +78,10 @@ struct Layout {
   int32_t* tile_off;    // [S+1] MFMA tile workgroup items
   int32_t* nparts;      // [S]
   int32_t* split_base;  // [S] first partial row, or -1
-  int32_t* wide_off;    // [S+1] 32-row MFMA tile workgroup items
+  int32_t* wide_off;    // [S+1] 32-row MFMA tile workgroup items, by position in wide_seq
   int32_t* cmb_seq;     // [S] split sequences the combine kernel merges
+  int32_t* wide_seq;    // [S] sequences in the order their 32-row items are handed
+                        // out: longest context first, those without such items last
   int4* desc;           // [S + cap_rows] bandwidth-kernel ranges: (sequence, range,
                         // context length, query token); full ranges in sequence
                         // order, then the short last ranges, longest first
@@ -86,7 +91,7 @@ struct Layout {
 };
 
 inline size_t plan_bytes(int S) {
-  size_t b = kHdrInts * 4 + (size_t)(6 * S + 3) * 4;
+  size_t b = kHdrInts * 4 + (size_t)(7 * S + 3) * 4;
   return (b + 255) & ~(size_t)255;
 }
 
@@ -108,6 +113,7 @@ inline Layout make_layout(void* ws, size_t bytes, int S, int D) {
   L.split_base = L.nparts + S;
   L.wide_off = L.split_base + S;
   L.cmb_seq = L.wide_off + S + 1;
+  L.wide_seq = L.cmb_seq + S;
   const size_t pb = plan_bytes(S);
   // descriptors, 8-byte (m, l) pairs and a [rows, D] float array, each
   // 256-byte aligned
@@ -281,20 +287,24 @@ static_assert(kTailBuckets == kPlanThreads, "one tail bucket per plan thread");
 // multi-query partition length P (256), doubling both until the split
 // partials fit the workspace. Then writes per-sequence offsets and the order
 // in which the shorter last ranges are handed out: longest first, after all
-// full ranges, so the kernel ends on its smallest items.
+// full ranges, so the kernel ends on its smallest items. The sequences with
+// 32-row tile items are ordered the same way, by context length, longest
+// first (their row blocks are handed out last block first, so within a
+// sequence too the items come longest first).
 __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H, int Hkv,
     bool fast, bool tile, bool wide, int64_t cap_rows, int target_items, int tile_target,
     int32_t* __restrict__ hdr, int32_t* __restrict__ gen_off,
     int32_t* __restrict__ tile_off, int32_t* __restrict__ nparts,
     int32_t* __restrict__ split_base, int32_t* __restrict__ wide_off,
-    int32_t* __restrict__ cmb_seq, int4* __restrict__ desc, float2* __restrict__ ml) {
+    int32_t* __restrict__ cmb_seq, int32_t* __restrict__ wide_seq, int4* __restrict__ desc,
+    float2* __restrict__ ml) {
   __shared__ unsigned long long need, bw_tokens, tile_keys;
   __shared__ int part_len, range_len;
-  __shared__ int hist[kTailBuckets];
+  __shared__ int hist[kTailBuckets], whist[kTailBuckets];
   const int t = threadIdx.x;
   if (t == 0) part_len = kPart0, bw_tokens = 0, tile_keys = 0;
-  for (int k = t; k < kTailBuckets; k += kPlanThreads) hist[k] = 0;
+  for (int k = t; k < kTailBuckets; k += kPlanThreads) hist[k] = 0, whist[k] = 0;
   __syncthreads();
   // 0. range length from the decode tokens and the target item count; the
   // same for the partition length of the splittable multi-query sequences
@@ -355,6 +365,11 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
                                           : (int)((int64_t)(blocks - 1) * kTailBuckets / rblocks);
     return kTailBuckets - 1 - k;  // ascending key = descending length
   };
+  // sequences with 32-row items by their context in 64-key tiles (up to
+  // kTailBuckets - 2 distinct lengths), descending; the others in the last bucket
+  auto wide_key = [&](int c, bool wd) {
+    return wd ? kTailBuckets - 2 - min(kTailBuckets - 2, cdiv(c, kTileKeys) - 1) : kTailBuckets - 1;
+  };
   int64_t f = 0, g = 0, r = 0, x = 0, tl = 0, wd = 0, cm = 0;
   for (int i = s0; i < s1; ++i) {
     const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
@@ -362,6 +377,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     f += w.full, g += w.gen, r += w.rows, x += w.tile, tl += w.tail, wd += w.wide;
     cm += w.np > 1 && !is_bw(q, c, fast);
     if (w.tail) atomicAdd(&hist[tail_key(c)], 1);
+    atomicAdd(&whist[wide_key(c, w.wide > 0)], 1);
   }
   int sc[7] = {(int)f, (int)g, (int)r, (int)x, (int)tl, (int)wd, (int)cm}, tot[7];
   block_exclusive_scan(sc, tot);
@@ -369,11 +385,11 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
   const int64_t tf = tot[0], tg = tot[1], tr = tot[2], tx = tot[3], ttl = tot[4], twd = tot[5],
                 tcm = tot[6];
   // bucket starts (kTailBuckets == kPlanThreads: one bucket per thread)
-  int hs[1] = {hist[t]}, htot[1];
+  int hs[2] = {hist[t], whist[t]}, htot[2];
   block_exclusive_scan(hs, htot);
-  const int64_t hstart = hs[0];
   __syncthreads();
-  hist[t] = (int)hstart;
+  hist[t] = hs[0];
+  whist[t] = hs[1];
   __syncthreads();
   for (int i = s0; i < s1; ++i) {
     const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
@@ -381,7 +397,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     for (int k = 0; k < w.full; ++k) desc[fo + k] = make_int4(i, k, c, qsl[i]);
     gen_off[i] = (int32_t)go;
     tile_off[i] = (int32_t)xo;
-    wide_off[i] = (int32_t)wo;
+    wide_seq[atomicAdd(&whist[wide_key(c, w.wide > 0)], 1)] = i;
     nparts[i] = w.np;
     split_base[i] = w.np > 1 ? (int32_t)ro : -1;
     if (w.tail) desc[tf + atomicAdd(&hist[tail_key(c)], 1)] = make_int4(i, c / R, c, qsl[i]);
@@ -389,7 +405,26 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     if (w.np > 1 && is_bw(q, c, fast))  // arrival counters start at 0
       for (int k = 0; k < Hkv; ++k)
         reinterpret_cast<int32_t*>(ml + ro + (int64_t)H * w.np + k)[0] = 0;
-    fo += w.full, go += w.gen, ro += w.rows, xo += w.tile, wo += w.wide;
+    fo += w.full, go += w.gen, ro += w.rows, xo += w.tile;
+  }
+  // 32-row item offsets in wide_seq order (every thread reads the positions of
+  // its chunk, written above by any thread of the workgroup)
+  __syncthreads();
+  if (twd == 0) {  // no 32-row items (twd is the same in every thread)
+    for (int p = s0; p < s1; ++p) wide_off[p] = 0;
+  } else {
+    auto wide_items = [&](int i) {
+      return seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, R, H, Hkv, fast, tile, wide).wide;
+    };
+    int64_t mine = 0;
+    for (int p = s0; p < s1; ++p) mine += wide_items(wide_seq[p]);
+    int ws[1] = {(int)mine}, wtot[1];
+    block_exclusive_scan(ws, wtot);
+    wo = ws[0];
+    for (int p = s0; p < s1; ++p) {
+      wide_off[p] = (int32_t)wo;
+      wo += wide_items(wide_seq[p]);
+    }
   }
   if (t == 0) {
     gen_off[S] = (int32_t)tg;
@@ -408,7 +443,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     hdr[10] = (int32_t)twd;
     hdr[11] = (tf + ttl) > 0 && (tx + twd) > 0;
     hdr[12] = (int32_t)tcm;
-    for (int k = 16; k < 26; ++k) hdr[k] = 0;
+    for (int k = 16; k < 42; ++k) hdr[k] = 0;
   }
 }
 
@@ -549,12 +584,16 @@ __device__ __forceinline__ uint4 load16(const void* p) {
   return __builtin_bit_cast(uint4, *reinterpret_cast<const u32x4_t*>(p));
 }
 
-template <typename T, int D>
+// One K/V tile in LDS. RW (rows per wavefront) sets the V^T row stride: the
+// PV operand reads of a wavefront (rows l % RW, 8-byte reads) then spread
+// over all 64 banks.
+template <typename T, int D, int RW>
 struct TileLds;
-template <int D>
-struct TileLds<uint16_t, D> {
+template <int D, int RW>
+struct TileLds<uint16_t, D, RW> {
   static constexpr int kRow = D + 8;           // K row stride (bf16), 16-byte aligned
-  static constexpr int vRow = kTileKeys + 8;   // V^T row stride (bf16), 16-byte aligned
+  static constexpr int vRow = kTileKeys + (RW == 32 ? 4 : 8);  // V^T row stride (bf16),
+                                                              // 8-byte aligned
   static constexpr int kChunks = D / 8;        // 16-byte chunks per head row
   // prefetch units per thread: K (key, chunk); V (4 keys, chunk)
   static constexpr int kUnits = kTileKeys * kChunks / 256;
@@ -562,8 +601,8 @@ struct TileLds<uint16_t, D> {
   uint16_t k[kTileKeys * kRow];
   uint16_t vt[D * vRow];
 };
-template <int D>
-struct TileLds<float, D> {
+template <int D, int RW>
+struct TileLds<float, D, RW> {
   static constexpr int kRow = D + 1;
   static constexpr int vRow = D + 1;
   static constexpr int kChunks = D / 4;        // float4 chunks per head row
@@ -619,6 +658,9 @@ __device__ __forceinline__ int item_tid() {
 
 
 // One workgroup item of the tile kernel (256 threads; the caller's LDS).
+// item_off holds the first item of each sequence, in sequence order, or (32-row
+// items) in the order of item_seq, which names the sequences; there a
+// sequence's row blocks come last block first.
 // RW = rows per wavefront: 16 (v_mfma_f32_16x16x32_bf16 / 16x16x4f32, 64-row
 // workgroups; short-query sequences, which may be split into partitions, and
 // fp32) or 32 (bf16 v_mfma_f32_32x32x16_bf16, 128-row workgroups, for long
@@ -626,8 +668,9 @@ __device__ __forceinline__ int item_tid() {
 // a lane holds row l%32; its S^T values are keys 32t + 8(r/4) + 4(l/32) + r%4
 // (r < 16) and its O^T values dims 32u + 8(r/4) + 4(l/32) + r%4.
 template <typename T, int D, int RW, bool kMixed>
-__device__ __forceinline__ void tile_body(TileLds<T, D>& lds, int it, int P,
+__device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
                                           const int32_t* __restrict__ item_off,
+                                          const int32_t* __restrict__ item_seq,
                                           VL_ATTN_PARAMS(T)) {
   const int tid = item_tid<kMixed>();
   constexpr bool kBf16 = sizeof(T) == 2;
@@ -638,7 +681,7 @@ __device__ __forceinline__ void tile_body(TileLds<T, D>& lds, int it, int P,
   constexpr int kKS = kW ? D / 16 : kBf16 ? D / 32 : D / 4;  // k-steps of the QK^T product
   constexpr int kST = kTileKeys / (kW ? 32 : 16);        // key subtiles per LDS tile
   constexpr int kCV = kW ? 16 : 4;                       // accumulator values per subtile
-  using Lds = TileLds<T, D>;
+  using Lds = TileLds<T, D, RW>;
   using AccT = float __attribute__((ext_vector_type(kCV)));
   static_assert(!kBf16 || (Lds::kUnits * 256 == kTileKeys * Lds::kChunks && Lds::vUnits <= 256),
                 "bf16 tile staging assumes head_dim 64 or 128");
@@ -650,15 +693,16 @@ __device__ __forceinline__ void tile_body(TileLds<T, D>& lds, int it, int P,
   const int64_t slot_stride = (int64_t)Hkv * D;
 
   {
-    const int i = wave_upper_bound_le(item_off, S + 1, it);
+    const int pos = wave_upper_bound_le(item_off, S + 1, it);
+    const int i = kW ? item_seq[pos] : pos;
     const int q_len = qsl[i + 1] - qsl[i];
     const int ctx = seq_lens[i];
     const int np = kW ? 1 : nparts[i];
-    const int local = it - item_off[i];
+    const int local = it - item_off[pos];
     const int part = local % np;
     const int kvh = (local / np) % Hkv;
-    const int rb = (local / np) / Hkv;
     const int nrows = q_len * rep;
+    const int rb = kW ? cdiv(nrows, kRows) - 1 - local / Hkv : (local / np) / Hkv;
     const int kbeg = np > 1 ? part * P : 0;
     const int kend = np > 1 ? min(ctx, kbeg + P) : ctx;
     // keys the block's last row can see bound the tiles the workgroup loads
@@ -721,43 +765,65 @@ __device__ __forceinline__ void tile_body(TileLds<T, D>& lds, int it, int P,
         (uint32_t)(tid / Lds::kChunks) * (uint32_t)slot_stride + (tid % Lds::kChunks) * 8;
     auto prefetch = [&](int k0) {
       if constexpr (kBf16) {
+        // V: four consecutive keys of one 8-dim chunk (one block: block sizes
+        // are powers of two >= 4 here); the key quad varies fastest over the
+        // lanes so the transposed LDS stores hit distinct banks
+        const int kq = tid & (kTileKeys / 4 - 1), c = tid / (kTileKeys / 4);
+        const int kv0 = k0 + 4 * kq;
+        const bool v_lane = Lds::vUnits == 256 || tid < Lds::vUnits;
         if (unit_blocks) {
+          // the units' block ids first (scalar loads, issued together), then
+          // every K and V address from them: V keys kv0 .. kv0 + 3 lie in unit
+          // 4 kq / kUnitKeys, and a V key clamped to the last key lies in the
+          // last unit's block, which is that unit's (a unit past the end reads
+          // the last unit's block, as the K loads do)
           const int klast = (kend_wg - 1) & ~(kUnitKeys - 1);
+          uint32_t blk[Lds::kUnits];
+#pragma unroll
+          for (int r = 0; r < Lds::kUnits; ++r)
+            blk[r] = (uint32_t)table[min(k0 + kUnitKeys * r, klast) >> bs_log2];
+          int64_t boff[Lds::kUnits];
 #pragma unroll
           for (int r = 0; r < Lds::kUnits; ++r) {
             const int kr = min(k0 + kUnitKeys * r, klast);
-            const T* base = kc + (int64_t)((uint64_t)(uint32_t)table[kr >> bs_log2] * blk_elems) + kv_off;
-            pk[r] = load16(base + ((uint32_t)(kr & bs_mask) * (uint32_t)slot_stride + k_thr_off));
+            boff[r] = (int64_t)((uint64_t)blk[r] * blk_elems) + kv_off;
+            pk[r] = load16(kc + boff[r] + ((uint32_t)(kr & bs_mask) * (uint32_t)slot_stride + k_thr_off));
+          }
+          if (v_lane) {
+            const int u = (4 * kq) / kUnitKeys;
+            int64_t vb = boff[0];
+#pragma unroll
+            for (int r = 1; r < Lds::kUnits; ++r) vb = u == r ? boff[r] : vb;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int key = min(kv0 + e, kend_wg - 1);
+              pv[e] = load16(vc + vb + ((uint32_t)(key & bs_mask) * (uint32_t)slot_stride + c * 8));
+            }
           }
         } else {
 #pragma unroll
           for (int r = 0; r < Lds::kUnits; ++r) {
             const int idx = tid + 256 * r;
-            const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
+            const int kk = idx / Lds::kChunks, cc = idx - kk * Lds::kChunks;
             const int key = min(k0 + kk, kend_wg - 1);
-            pk[r] = load16(kc + row_of(key) + c * 8);
+            pk[r] = load16(kc + row_of(key) + cc * 8);
           }
-        }
-        // V: four consecutive keys of one 8-dim chunk (one block: block sizes
-        // are powers of two >= 4 here); the key quad varies fastest over the
-        // lanes so the transposed LDS stores hit distinct banks
-        if (Lds::vUnits == 256 || tid < Lds::vUnits) {
-          const int kq = tid & (kTileKeys / 4 - 1), c = tid / (kTileKeys / 4);
-          const int kv0 = k0 + 4 * kq;
-          if (bs_log2 >= 2) {
-            const int vb = min(kv0, kend_wg - 1);
-            const T* base = vc + (int64_t)((uint64_t)(uint32_t)table[vb >> bs_log2] * blk_elems) +
-                            kv_off + c * 8;
+          if (v_lane) {
+            if (bs_log2 >= 2) {
+              const int vb = min(kv0, kend_wg - 1);
+              const T* base = vc + (int64_t)((uint64_t)(uint32_t)table[vb >> bs_log2] * blk_elems) +
+                              kv_off + c * 8;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int key = min(kv0 + e, kend_wg - 1);
-              pv[e] = load16(base + (uint32_t)(key & bs_mask) * (uint32_t)slot_stride);
-            }
-          } else {
+              for (int e = 0; e < 4; ++e) {
+                const int key = min(kv0 + e, kend_wg - 1);
+                pv[e] = load16(base + (uint32_t)(key & bs_mask) * (uint32_t)slot_stride);
+              }
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int key = min(kv0 + e, kend_wg - 1);
-              pv[e] = load16(vc + row_of(key) + c * 8);
+              for (int e = 0; e < 4; ++e) {
+                const int key = min(kv0 + e, kend_wg - 1);
+                pv[e] = load16(vc + row_of(key) + c * 8);
+              }
             }
           }
         }
@@ -774,13 +840,13 @@ __device__ __forceinline__ void tile_body(TileLds<T, D>& lds, int it, int P,
         }
       }
     };
-    auto stage = [&]() {  // prefetch registers -> LDS
+    auto stage = [&](Lds& b) {  // prefetch registers -> LDS b
       if constexpr (kBf16) {
 #pragma unroll
         for (int r = 0; r < Lds::kUnits; ++r) {
           const int idx = tid + 256 * r;
           const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
-          *reinterpret_cast<uint4*>(&lds.k[kk * Lds::kRow + c * 8]) = pk[r];
+          *reinterpret_cast<uint4*>(&b.k[kk * Lds::kRow + c * 8]) = pk[r];
         }
         if (Lds::vUnits == 256 || tid < Lds::vUnits) {
           const int kq = tid & (kTileKeys / 4 - 1), c = tid / (kTileKeys / 4);
@@ -796,8 +862,8 @@ __device__ __forceinline__ void tile_body(TileLds<T, D>& lds, int it, int P,
             const uint32_t hi01 = __builtin_amdgcn_perm(w[1][m], w[0][m], 0x07060302u);
             const uint32_t hi23 = __builtin_amdgcn_perm(w[3][m], w[2][m], 0x07060302u);
             const int d = c * 8 + 2 * m;
-            *reinterpret_cast<uint2*>(&lds.vt[d * Lds::vRow + 4 * kq]) = make_uint2(lo01, lo23);
-            *reinterpret_cast<uint2*>(&lds.vt[(d + 1) * Lds::vRow + 4 * kq]) = make_uint2(hi01, hi23);
+            *reinterpret_cast<uint2*>(&b.vt[d * Lds::vRow + 4 * kq]) = make_uint2(lo01, lo23);
+            *reinterpret_cast<uint2*>(&b.vt[(d + 1) * Lds::vRow + 4 * kq]) = make_uint2(hi01, hi23);
           }
         }
       } else {
@@ -806,8 +872,8 @@ __device__ __forceinline__ void tile_body(TileLds<T, D>& lds, int it, int P,
           const int idx = tid + 256 * r;
           if (idx < kTileKeys * Lds::kChunks) {
             const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
-            float* kd = &lds.k[kk * Lds::kRow + c * 4];
-            float* vd = &lds.v[kk * Lds::vRow + c * 4];
+            float* kd = &b.k[kk * Lds::kRow + c * 4];
+            float* vd = &b.v[kk * Lds::vRow + c * 4];
             kd[0] = __uint_as_float(pk[r].x), kd[1] = __uint_as_float(pk[r].y);
             kd[2] = __uint_as_float(pk[r].z), kd[3] = __uint_as_float(pk[r].w);
             vd[0] = __uint_as_float(pv[r].x), vd[1] = __uint_as_float(pv[r].y);
@@ -822,15 +888,8 @@ __device__ __forceinline__ void tile_body(TileLds<T, D>& lds, int it, int P,
     };
 
     const int ntile = kend_wg > kbeg ? (kend_wg - kbeg + kTileKeys - 1) / kTileKeys : 0;
-    if (ntile > 0) prefetch(kbeg);
-    for (int ti = 0; ti < ntile; ++ti) {
-      const int k0 = kbeg + ti * kTileKeys;
-      __syncthreads();  // the previous tile (or item) is done with the LDS buffer
-      stage();
-      __syncthreads();
-      if (ti + 1 < ntile) prefetch(k0 + kTileKeys);  // in flight during the compute below
-      if (k0 >= kend_wave) continue;  // every row of this wave is past its causal end
-
+    // one tile of keys k0.. from LDS b into the running softmax and output
+    auto compute = [&](const Lds& b, int k0) {
       // ---- S^T = K Q^T for the key subtiles
       AccT sc[kST];
 #pragma unroll
@@ -841,16 +900,16 @@ __device__ __forceinline__ void tile_body(TileLds<T, D>& lds, int it, int P,
         for (int s = 0; s < kKS; ++s) {
           if constexpr (kW) {
             const uint4 w = *reinterpret_cast<const uint4*>(
-                &lds.k[(32 * t + col) * Lds::kRow + 16 * s + 8 * grp]);
+                &b.k[(32 * t + col) * Lds::kRow + 16 * s + 8 * grp]);
             sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, w),
                                                             qop[s], sc[t], 0, 0, 0);
           } else if constexpr (kBf16) {
             const uint4 w = *reinterpret_cast<const uint4*>(
-                &lds.k[(16 * t + col) * Lds::kRow + 32 * s + 8 * grp]);
+                &b.k[(16 * t + col) * Lds::kRow + 32 * s + 8 * grp]);
             sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, w),
                                                             qop[s], sc[t], 0, 0, 0);
           } else {
-            const float a = lds.k[(16 * t + col) * Lds::kRow + 4 * s + grp];
+            const float a = b.k[(16 * t + col) * Lds::kRow + 4 * s + grp];
             sc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, qop[s], sc[t], 0, 0, 0);
           }
         }
@@ -920,7 +979,7 @@ __device__ __forceinline__ void tile_body(TileLds<T, D>& lds, int it, int P,
             const int kb = 32 * t + 16 * hh + 4 * grp;
 #pragma unroll
             for (int u = 0; u < kDT; ++u) {
-              const uint16_t* vrow = &lds.vt[(32 * u + col) * Lds::vRow + kb];
+              const uint16_t* vrow = &b.vt[(32 * u + col) * Lds::vRow + kb];
               const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
               const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
               const uint4 vw = make_uint4(lo.x, lo.y, hi.x, hi.y);
@@ -939,7 +998,7 @@ __device__ __forceinline__ void tile_body(TileLds<T, D>& lds, int it, int P,
           const bf16x8_t pop = __builtin_bit_cast(bf16x8_t, pw);
 #pragma unroll
           for (int u = 0; u < kDT; ++u) {
-            const uint16_t* vrow = &lds.vt[(16 * u + col) * Lds::vRow + 32 * hh];
+            const uint16_t* vrow = &b.vt[(16 * u + col) * Lds::vRow + 32 * hh];
             const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * grp);
             const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * grp);
             const uint4 vw = make_uint4(lo.x, lo.y, hi.x, hi.y);
@@ -952,13 +1011,22 @@ __device__ __forceinline__ void tile_body(TileLds<T, D>& lds, int it, int P,
         for (int t = 0; t < kST; ++t)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float* vrow = &lds.v[(16 * t + 4 * grp + e) * Lds::vRow];
+            const float* vrow = &b.v[(16 * t + 4 * grp + e) * Lds::vRow];
 #pragma unroll
             for (int u = 0; u < kDT; ++u)
               acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[16 * u + col], pr[t][e], acc[u],
                                                             0, 0, 0);
           }
       }
+    };
+    if (ntile > 0) prefetch(kbeg);
+    for (int ti = 0; ti < ntile; ++ti) {
+      const int k0 = kbeg + ti * kTileKeys;
+      __syncthreads();  // the previous tile (or item) is done with the LDS buffer
+      stage(lds);
+      __syncthreads();
+      if (ti + 1 < ntile) prefetch(k0 + kTileKeys);  // in flight during the compute below
+      if (k0 < kend_wave) compute(lds, k0);  // else every row of the wave is past its end
     }
     // ---- row sums over the lane groups, then write
     float l_row = l_part;
@@ -998,17 +1066,54 @@ __device__ __forceinline__ void tile_body(TileLds<T, D>& lds, int it, int P,
   }
 }
 
-// RW = rows per wavefront (see tile_body). Items are strided over a grid
-// of resident workgroups.
+// The last workgroup to leave a persistent kernel (every claim of every
+// workgroup has returned) zeroes the work counters counters[0..n) and the
+// exit counter counters[n] for the next run.
+__device__ __forceinline__ void leave_and_reset(int32_t* counters, int n) {
+  if (threadIdx.x == 0) {
+    const int prev =
+        __hip_atomic_fetch_add(counters + n, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == (int)gridDim.x - 1) {
+      for (int k = 0; k <= n; ++k)
+        __hip_atomic_store(counters + k, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+constexpr int kXcds = 8;
+
+// RW = rows per wavefront (see tile_body). Persistent workgroups take items
+// from 8 queues, queue x holding the items it with it % 8 == x: workgroup b
+// serves queue b % 8 (workgroups are dispatched round-robin over the 8 XCDs,
+// so that is its XCD), its first item is the queue's (b / 8)-th and the later
+// ones are claimed from the queue's counter (counters[x]), each at the start
+// of the item before, so the atomic's latency is hidden and a workgroup
+// without items leaves at once. Consecutive items are the KV heads of one row
+// block, so with 8 KV heads each XCD's L2 holds the K/V of its own KV head,
+// which the sequence's other row blocks read again; the plan orders the
+// items longest first, so the launch ends on short ones. The counters are
+// zeroed by the plan and by the combine launch that follows every run.
 template <typename T, int D, int RW>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) attend_tile_kernel(
-    VL_ATTN_PARAMS(T), const int32_t* __restrict__ hdr, const int32_t* __restrict__ item_off) {
-  __shared__ TileLds<T, D> lds;
-  const int P = hdr[2];
+    VL_ATTN_PARAMS(T), const int32_t* __restrict__ hdr, const int32_t* __restrict__ item_off,
+    const int32_t* __restrict__ item_seq, int32_t* counters) {
+  __shared__ TileLds<T, D, RW> lds;
+  __shared__ int claim_lds;
   if (hdr[11]) return;  // a mixed batch: the step kernel has these items
+  const int P = hdr[2];
   const int n_items = hdr[RW == 32 ? 10 : 4];
-  for (int it = blockIdx.x; it < n_items; it += gridDim.x)
-    tile_body<T, D, RW, false>(lds, it, P, item_off, VL_ATTN_ARGS);
+  const int xcd = blockIdx.x % kXcds;
+  const int per_queue = ((int)gridDim.x + kXcds - 1 - xcd) / kXcds;  // workgroups serving it
+  int it = (blockIdx.x / kXcds) * kXcds + xcd;
+  while (it < n_items) {
+    int nxt = 0;
+    if (threadIdx.x == 0) nxt = per_queue + atomicAdd(counters + xcd, 1);
+    tile_body<T, D, RW, false>(lds, it, P, item_off, item_seq, VL_ATTN_ARGS);
+    __syncthreads();  // the item is done with the LDS; claim_lds has been read
+    if (threadIdx.x == 0) claim_lds = nxt;
+    __syncthreads();
+    it = claim_lds * kXcds + xcd;
+  }
 }
 
 // ---------------------------------------------------- bandwidth decode -----
@@ -1449,20 +1554,6 @@ __device__ __forceinline__ void decode_body(DecodeLds& s, int it, const DecodeIt
   }
 }
 
-// The last workgroup to leave a persistent kernel (every claim of every
-// workgroup has returned) zeroes the work counters counters[0..n) and the
-// exit counter counters[n] for the next run.
-__device__ __forceinline__ void leave_and_reset(int32_t* counters, int n) {
-  if (threadIdx.x == 0) {
-    const int prev =
-        __hip_atomic_fetch_add(counters + n, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == (int)gridDim.x - 1) {
-      for (int k = 0; k <= n; ++k)
-        __hip_atomic_store(counters + k, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-}
-
 __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
     VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hdr, int32_t* work) {
   __shared__ DecodeLds s;
@@ -1504,21 +1595,20 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
 // the same time; a workgroup whose queues have run dry moves to the others.
 // The two item kinds share the LDS allocation. counters: [0] decode queue,
 // [1 + x] tile queue x, [9] workgroups finished.
-constexpr size_t kStepLds =
-    sizeof(TileLds<uint16_t, kFD>) > sizeof(DecodeLds) ? sizeof(TileLds<uint16_t, kFD>)
-                                                         : sizeof(DecodeLds);
-constexpr int kXcds = 8;
+constexpr size_t kStepLds = std::max({sizeof(TileLds<uint16_t, kFD, 32>),
+                                      sizeof(TileLds<uint16_t, kFD, 16>), sizeof(DecodeLds)});
 #ifndef VL_STEP_TILE_FIRST
 #define VL_STEP_TILE_FIRST 2  // one in this many workgroups starts on the tile queues
 #endif
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 attend_step_bf16_kernel(VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hdr,
-                        const int32_t* __restrict__ wide_off, const int32_t* __restrict__ tile_off,
-                        int32_t* counters, int always) {
+                        const int32_t* __restrict__ wide_off, const int32_t* __restrict__ wide_seq,
+                        const int32_t* __restrict__ tile_off, int32_t* counters, int always) {
   __shared__ __align__(16) unsigned char smem[kStepLds];
   __shared__ int claim_lds;
-  auto& tl = *reinterpret_cast<TileLds<uint16_t, kFD>*>(smem);
+  auto& tl32 = *reinterpret_cast<TileLds<uint16_t, kFD, 32>*>(smem);
+  auto& tl16 = *reinterpret_cast<TileLds<uint16_t, kFD, 16>*>(smem);
   auto& dl = *reinterpret_cast<DecodeLds*>(smem);
   if (!always && !hdr[11]) return;  // not a mixed batch: the decode and tile kernels run it
   const int P = hdr[2];
@@ -1551,9 +1641,9 @@ attend_step_bf16_kernel(VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hd
                                        threadIdx.x & 63, query, q_stride, bt, bt_stride),
                           R, VL_ATTN_ARGS);
       else if (it < n_wide)
-        tile_body<uint16_t, kFD, 32, true>(tl, it, P, wide_off, VL_ATTN_ARGS);
+        tile_body<uint16_t, kFD, 32, true>(tl32, it, P, wide_off, wide_seq, VL_ATTN_ARGS);
       else
-        tile_body<uint16_t, kFD, 16, true>(tl, it - n_wide, P, tile_off, VL_ATTN_ARGS);
+        tile_body<uint16_t, kFD, 16, true>(tl16, it - n_wide, P, tile_off, nullptr, VL_ATTN_ARGS);
       __syncthreads();  // the item is done with the LDS; claim_lds has been read
       if (threadIdx.x == 0) claim_lds = nxt;
       __syncthreads();
@@ -1576,8 +1666,11 @@ __global__ void __launch_bounds__(256) combine_kernel(
     T* __restrict__ out, const int32_t* __restrict__ qsl, int H, int D,
     const int32_t* __restrict__ hdr, const int32_t* __restrict__ cmb_seq,
     const int32_t* __restrict__ nparts, const int32_t* __restrict__ split_base,
-    const float2* __restrict__ ml, const float* __restrict__ po) {
+    const float2* __restrict__ ml, const float* __restrict__ po, int32_t* tile_counters) {
   constexpr int kDk = kMaxHeadDim / 64;
+  // every tile launch of this run has ended: zero their queue counters for the next
+  if (blockIdx.x == 0 && threadIdx.x < 16)
+    __hip_atomic_store(tile_counters + threadIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t items = (int64_t)hdr[12] * H;
   for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
@@ -1697,7 +1790,8 @@ int step_grid() {
   return cached[dev];
 }
 
-// Workgroups the MFMA tile kernel is launched with (it loops over its items).
+// The tile items the plan aims for are kTileItemsPerWg per this many
+// workgroups.
 int tile_grid() { return vl_num_cus() * 4; }
 
 int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
@@ -1711,7 +1805,7 @@ int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
   plan_kernel<<<1, kPlanThreads, 0, st>>>(a.seq_lens, a.qsl, a.S, a.H, a.Hkv, fast, tile, wide,
                                           L.cap_rows, target_items, tile_target, L.hdr,
                                           L.gen_off, L.tile_off, L.nparts, L.split_base,
-                                          L.wide_off, L.cmb_seq, L.desc, L.ml);
+                                          L.wide_off, L.cmb_seq, L.wide_seq, L.desc, L.ml);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
@@ -1722,10 +1816,31 @@ int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
       a.seq_lens, a.qsl, a.S, a.H, a.Hkv, __builtin_ctz(a.bs), sl2, L.desc, L.nparts,          \
       L.split_base, L.ml, L.po
 
+// Workgroups of a tile kernel that are resident at once on the current device
+// (its grid is persistent), cached per device and instantiation.
+template <typename T, int D, int RW>
+int tile_launch_grid() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (!cached[dev]) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attend_tile_kernel<T, D, RW>, 256,
+                                                     0) != hipSuccess ||
+        per_cu <= 0)
+      per_cu = 2;
+    // at most 4 per compute unit: more only add workgroups that find no item
+    // in small batches
+    cached[dev] = std::min(per_cu, 4) * vl_num_cus();
+  }
+  return cached[dev];
+}
+
 template <typename T, int D, int RW>
 int launch_tile_d(const Args& a, const Layout& L, float sl2, hipStream_t st) {
-  attend_tile_kernel<T, D, RW><<<tile_grid(), 256, 0, st>>>(
-      VL_ATTN_LAUNCH_ARGS(T), L.hdr, RW == 32 ? L.wide_off : L.tile_off);
+  attend_tile_kernel<T, D, RW><<<tile_launch_grid<T, D, RW>(), 256, 0, st>>>(
+      VL_ATTN_LAUNCH_ARGS(T), L.hdr, RW == 32 ? L.wide_off : L.tile_off,
+      RW == 32 ? L.wide_seq : nullptr, L.hdr + (RW == 32 ? 34 : 26));
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
@@ -1779,8 +1894,8 @@ int do_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) 
     // bound: the step kernel runs the whole batch.
     const bool step_all = max_q <= 0;
     attend_step_bf16_kernel<<<step_grid(), 256, 0, st>>>(VL_ATTN_LAUNCH_ARGS(uint16_t), L.hdr,
-                                                         L.wide_off, L.tile_off, L.hdr + 16,
-                                                         step_all ? 1 : 0);
+                                                         L.wide_off, L.wide_seq, L.tile_off,
+                                                         L.hdr + 16, step_all ? 1 : 0);
     VL_CHECK_LAUNCH();
     if (!step_all) {
       const int rc = launch_tile<T>(a, L, sl2, max_q, st);
@@ -1797,7 +1912,7 @@ int do_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) 
     VL_CHECK_LAUNCH();
   }
   combine_kernel<T><<<ncu * 8, 256, 0, st>>>((T*)a.out, a.qsl, a.H, a.D, L.hdr, L.cmb_seq,
-                                            L.nparts, L.split_base, L.ml, L.po);
+                                            L.nparts, L.split_base, L.ml, L.po, L.hdr + 26);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
