@@ -266,7 +266,7 @@ __device__ __forceinline__ SeqWork seq_work(int q, int c, int P, int R, int H, i
 }
 
 #ifndef VL_RANGE_MAX
-#define VL_RANGE_MAX 1024
+#define VL_RANGE_MAX 2048
 #endif
 #ifndef VL_ITEMS_PER_WG
 #define VL_ITEMS_PER_WG 4
@@ -1939,7 +1939,7 @@ extern "C" size_t vl_paged_attention_workspace_size(int num_seqs, int num_tokens
   const int64_t rows_tile = parts > 1 ? split_tokens * H * parts : 0;
   // decode ranges: as short as 64 tokens for small batches, at most a few
   // items per resident workgroup (plus one short range per sequence) and at
-  // most 1024 tokens long otherwise
+  // most kRangeMax (2048) tokens long otherwise
   const int64_t rows_fast =
       std::min<int64_t>(S * H * cdiv64(ctx, 64),
                         4 * kItemsPerWg * (int64_t)decode_grid() +
