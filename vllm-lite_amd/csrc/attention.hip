@@ -71,6 +71,10 @@ constexpr int kBV = VL_BV;  // blocks per V load burst
 // 64 keys per LDS tile
 constexpr int kTileRows = 64;
 constexpr int kTileKeys = 64;
+#ifndef VL_PV_LOOK
+#define VL_PV_LOOK 2
+#endif
+constexpr int kPvLook = VL_PV_LOOK;  // 32-row PV product: V^T operands read this many MFMAs ahead
 
 struct Layout {
   int32_t* hdr;
@@ -949,6 +953,26 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
         for (int u = 0; u < kDT; ++u) acc[u] *= alpha;
         m_run = m_new;
       }
+      // the first V^T operands of the 32-row PV product, read now so that
+      // their LDS latency passes during the exponentials
+      constexpr int kPvSteps = kST * 2 * kDT;  // (subtile t, half hh, d tile u)
+      constexpr int kLook = kW ? kPvLook : 1;
+      auto vread = [&](int st) {  // operand of step st: dims 32u + .., keys 32t + 16hh + ..
+        if constexpr (kW) {
+          const int t = st / (2 * kDT), hh = (st / kDT) % 2, u = st % kDT;
+          const uint16_t* vrow = &b.vt[(32 * u + col) * Lds::vRow + 32 * t + 16 * hh + 4 * grp];
+          const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+          return make_uint4(lo.x, lo.y, hi.x, hi.y);
+        } else {
+          return make_uint4(0, 0, 0, 0);
+        }
+      };
+      uint4 vq[kLook];
+      if constexpr (kW) {
+#pragma unroll
+        for (int i = 0; i < kLook; ++i) vq[i] = vread(i);
+      }
       // masked scores are -inf and give 0; a row with nothing unmasked yet
       // keeps m_run = -inf and uses reference 0
       const float neg_ref = m_run == -__builtin_inff() ? 0.f : -m_run;
@@ -965,28 +989,25 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
       // ---- O^T += V^T P^T
       if constexpr (kW) {
         // 16-key k-steps: subtile t, half h covers keys 32t + 16h ..; this
-        // lane's values r = 8h .. 8h+7 are exactly the B operand's k-slots
+        // lane's values r = 8h .. 8h+7 are exactly the B operand's k-slots.
+        // Each V^T operand is read kLook steps before its MFMA.
+        bf16x8_t pop;
 #pragma unroll
-        for (int t = 0; t < kST; ++t)
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
+        for (int st = 0; st < kPvSteps; ++st) {
+          const int t = st / (2 * kDT), hh = (st / kDT) % 2, u = st % kDT;
+          if (u == 0) {
             uint4 pw;
             pw.x = cvt_pk_bf16(pr[t][8 * hh + 0], pr[t][8 * hh + 1]);
             pw.y = cvt_pk_bf16(pr[t][8 * hh + 2], pr[t][8 * hh + 3]);
             pw.z = cvt_pk_bf16(pr[t][8 * hh + 4], pr[t][8 * hh + 5]);
             pw.w = cvt_pk_bf16(pr[t][8 * hh + 6], pr[t][8 * hh + 7]);
-            const bf16x8_t pop = __builtin_bit_cast(bf16x8_t, pw);
-            const int kb = 32 * t + 16 * hh + 4 * grp;
-#pragma unroll
-            for (int u = 0; u < kDT; ++u) {
-              const uint16_t* vrow = &b.vt[(32 * u + col) * Lds::vRow + kb];
-              const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
-              const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
-              const uint4 vw = make_uint4(lo.x, lo.y, hi.x, hi.y);
-              acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vw),
-                                                               pop, acc[u], 0, 0, 0);
-            }
+            pop = __builtin_bit_cast(bf16x8_t, pw);
           }
+          const uint4 vw = vq[st % kLook];
+          if (st + kLook < kPvSteps) vq[st % kLook] = vread(st + kLook);
+          acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vw), pop,
+                                                           acc[u], 0, 0, 0);
+        }
       } else if constexpr (kBf16) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
