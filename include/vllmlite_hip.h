@@ -33,6 +33,9 @@ extern "C" {
 #define VL_LINEAR_STORE 0      /* vl_linear_rows: out = f(x) @ W */
 #define VL_LINEAR_ACCUMULATE 1 /* out += f(x) @ W (the residual add) */
 #define VL_LINEAR_SWIGLU 2     /* out = silu(f(x) @ W[:, :n]) * (f(x) @ W[:, n:2n]) */
+#define VL_LINEAR_TILES16 16   /* flag ORed into the mode: W in 16-column tiles */
+#define VL_WEIGHT_ROWS 0       /* a projection weight [k, n] row-major at a row stride */
+#define VL_WEIGHT_TILES16 1    /* ... as 16-column tiles [ceil(n/16), k, 16], zero past n */
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* vl_last_error(void);
@@ -167,8 +170,11 @@ int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_out, float*
  * x [*, k] (16-byte aligned, row stride a multiple of 4); row r of the
  * input is x[row_index[r]] when row_index != NULL (the gather of the logits
  * rows, runner.py:90), else x[r]. W [k, n] (or [k, 2n]) row-major with row
- * stride weight_stride, out [rows, n]; out must not overlap x. rows <= 16, k
- * a multiple of 16, k <= 1024. fp32 throughout.
+ * stride weight_stride, or, with VL_LINEAR_TILES16 ORed into mode, as
+ * 16-column tiles [ceil(n/16), k, 16] (zero past column n; SwiGLU: the gate
+ * tiles, then the up tiles; weight_stride unused), which loads in whole cache
+ * lines. out [rows, n]; out must not overlap x. rows <= 16, k a multiple of
+ * 16, k <= 1024. fp32 throughout.
  */
 int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_stride,
                    const int32_t* row_index, const float* weight, int64_t weight_stride,
@@ -185,11 +191,13 @@ int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_str
  * Input rows are x[row_index[r]] when row_index != NULL (the embedding
  * gather tok_emb[token_ids], model.py:93), and when x_out != NULL the rows
  * read (before the norm) are also written to x_out [rows, k] (the residual
- * stream). rows <= 16, k a multiple of 16, k <= 1024, head_dim even. fp32.
+ * stream). weight_layout: VL_WEIGHT_ROWS (row stride weight_stride) or
+ * VL_WEIGHT_TILES16 (as for vl_linear_rows). rows <= 16, k a multiple of 16,
+ * k <= 1024, head_dim even. fp32.
  */
 int vl_qkv_rope_cache(float* q_out, float* key_cache, float* value_cache, const float* x,
                       int64_t x_stride, const int32_t* row_index, float* x_out,
-                      const float* weight, int64_t weight_stride,
+                      const float* weight, int64_t weight_stride, int weight_layout,
                       const float* norm_weight, float eps, const int32_t* positions,
                       const int32_t* slot_mapping, const float* cos_table, const float* sin_table,
                       int rows, int k, int num_heads, int num_kv_heads, int head_dim,

@@ -182,3 +182,49 @@ def test_qkv_rope_cache_embedding_gather_and_residual_copy():
     torch.cuda.synchronize()
     assert torch.equal(q1, q2) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
     assert torch.equal(x_out, table[ids.long()])
+
+
+@pytest.mark.parametrize("rows", [1, 16])
+@pytest.mark.parametrize("k,n", [(384, 1152), (384, 261), (1024, 384), (64, 40)])
+@pytest.mark.parametrize("mode", ["store", "accumulate", "swiglu"])
+def test_tiled_weights_same_bits(rows, k, n, mode):
+    """Weights in 16-column tiles ([ceil(n/16), k, 16], zero past n; SwiGLU:
+    gate tiles then up tiles) give the same bits as the row-major weight."""
+    o = _ops()
+    m = {"store": o.LINEAR_STORE, "accumulate": o.LINEAR_ACCUMULATE, "swiglu": o.LINEAR_SWIGLU}[mode]
+    halves = 2 if mode == "swiglu" else 1
+    rng = np.random.default_rng(rows + k + n + halves)
+    x = torch.from_numpy(rng.standard_normal((rows, k)).astype(np.float32)).cuda()
+    w = torch.from_numpy((0.05 * rng.standard_normal((k, halves * n))).astype(np.float32)).cuda()
+    g = torch.from_numpy((1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)).cuda()
+    wt = o.tile16(w, halves)
+    assert wt.shape == (halves * -(-n // 16), k, 16)
+    init = torch.from_numpy(rng.standard_normal((rows, n)).astype(np.float32)).cuda()
+    a, b = init.clone(), init.clone()
+    o.linear_rows(a, x, w, g, mode=m)
+    o.linear_rows(b, x, wt, g, mode=m)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_qkv_rope_cache_tiled_weights_same_bits():
+    o = _ops()
+    H, Hkv, D, k, rows = 8, 4, 48, 384, 13
+    n = (H + 2 * Hkv) * D
+    rng = np.random.default_rng(21)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    x = dev(rng.standard_normal((rows, k)).astype(np.float32))
+    w = dev((0.05 * rng.standard_normal((k, n))).astype(np.float32))
+    g = dev((1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32))
+    pos = dev(rng.integers(0, 64, rows).astype(np.int32))
+    slot = dev(rng.permutation(30)[:rows].astype(np.int32))
+    ang = rng.standard_normal((64, D // 2)).astype(np.float32)
+    cos, sin = dev(np.cos(ang)), dev(np.sin(ang))
+    kc1, vc1 = (torch.zeros((30, Hkv, D), device="cuda") for _ in range(2))
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    q1 = torch.empty((rows, H * D), device="cuda")
+    q2 = torch.empty_like(q1)
+    o.qkv_rope_cache(q1, kc1, vc1, x, w, g, pos, slot, cos, sin, H, Hkv, D)
+    o.qkv_rope_cache(q2, kc2, vc2, x, o.tile16(w), g, pos, slot, cos, sin, H, Hkv, D)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2)

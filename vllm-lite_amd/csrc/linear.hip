@@ -9,6 +9,13 @@
 // are staged in LDS and normalised there; the four partial tiles are summed
 // in a fixed order. hipBLASLt runs these shapes as separate launches of
 // ~7 us each; here a projection and its neighbours are one.
+//
+// Weights come row-major ([k, n] at a row stride) or as 16-column tiles
+// ([ceil(n/16), k, 16], the columns past n zero): a workgroup's 16 columns
+// are then one contiguous k x 64-byte run, which it reads in whole 128-byte
+// lines (row-major, every k row is a separate 64-byte piece). These kernels
+// run on few workgroups, where the number of cache lines each one requests
+// sets the time.
 #include "vl_common.h"
 
 namespace {
@@ -53,10 +60,12 @@ struct RopeCache {
 // rotated by RoPE, q to rc.q_out, k and v to the caches at the row's slot.
 // f(x) = x, or with NORM the RMSNorm of x (as rms_norm_kernel computes it)
 // times norm_w.
-template <int MODE, bool NORM, int KMAX>
+// TILES: the weight is in 16-column tiles (ldw unused; up_off counts
+// elements, the start of the up tiles).
+template <int MODE, bool NORM, int KMAX, bool TILES>
 __global__ void __launch_bounds__(256) linear_rows_kernel(
     float* __restrict__ out, int64_t ldo, const float* __restrict__ x, int64_t ldx,
-    const float* __restrict__ w, int64_t ldw, int up_off, const float* __restrict__ norm_w,
+    const float* __restrict__ w, int64_t ldw, int64_t up_off, const float* __restrict__ norm_w,
     float eps, int M, int K, int N, const RopeCache rc, const int32_t* __restrict__ row_index,
     float* __restrict__ x_out) {
   constexpr int kSlices = MODE == 2 ? 2 : 1;
@@ -82,10 +91,20 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(
   const float colmask = c0 + m < N ? 1.f : 0.f;
 #pragma unroll
   for (int s = 0; s < kSlices; ++s) {
-    const float* src = w + (s ? up_off : 0) + min(c0 + m, N - 1) + (int64_t)(kb + j) * ldw;
+    if constexpr (TILES) {
+      // tile blockIdx.x: element (k, m) at k * 16 + m; a wavefront's 64 lanes
+      // read 4 consecutive k rows, 256 contiguous bytes
+      const float* src = w + (s ? up_off : 0) + (int64_t)blockIdx.x * K * kCols + m +
+                         (int64_t)(kb + j) * kCols;
 #pragma unroll
-    for (int i = 0; i < kSteps; ++i)
-      wb[s][i] = src[(int64_t)(4 * min(i, nsteps - 1)) * ldw] * (i < nsteps ? colmask : 0.f);
+      for (int i = 0; i < kSteps; ++i)
+        wb[s][i] = src[(int64_t)(4 * min(i, nsteps - 1)) * kCols] * (i < nsteps ? colmask : 0.f);
+    } else {
+      const float* src = w + (s ? up_off : 0) + min(c0 + m, N - 1) + (int64_t)(kb + j) * ldw;
+#pragma unroll
+      for (int i = 0; i < kSteps; ++i)
+        wb[s][i] = src[(int64_t)(4 * min(i, nsteps - 1)) * ldw] * (i < nsteps ? colmask : 0.f);
+    }
   }
   // the norm weights of this lane's columns k = lane + 64 i (clamped loads)
   float gw[KMAX / 64];
@@ -220,11 +239,18 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(
 
 template <int MODE, bool NORM, int KMAX>
 int launch(float* out, int64_t ldo, const float* x, int64_t ldx, const float* w, int64_t ldw,
-           int up_off, const float* norm_w, float eps, int M, int K, int N, hipStream_t st,
+           bool tiles, const float* norm_w, float eps, int M, int K, int N, hipStream_t st,
            const int32_t* row_index, const RopeCache& rc = RopeCache{}, float* x_out = nullptr) {
   const int grid = (N + kCols - 1) / kCols;
-  linear_rows_kernel<MODE, NORM, KMAX><<<grid, 256, 0, st>>>(
-      out, ldo, x, ldx, w, ldw, up_off, norm_w, eps, M, K, N, rc, row_index, x_out);
+  if (tiles) {
+    const int64_t up_off = MODE == 2 ? (int64_t)grid * K * kCols : 0;
+    linear_rows_kernel<MODE, NORM, KMAX, true><<<grid, 256, 0, st>>>(
+        out, ldo, x, ldx, w, 0, up_off, norm_w, eps, M, K, N, rc, row_index, x_out);
+  } else {
+    const int64_t up_off = MODE == 2 ? N : 0;
+    linear_rows_kernel<MODE, NORM, KMAX, false><<<grid, 256, 0, st>>>(
+        out, ldo, x, ldx, w, ldw, up_off, norm_w, eps, M, K, N, rc, row_index, x_out);
+  }
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
@@ -236,6 +262,8 @@ extern "C" int vl_linear_rows(float* out, int64_t out_stride, const float* x, in
                               int64_t weight_stride, const float* norm_weight, float eps,
                               int rows, int k, int n, int mode, void* stream) {
   VL_CHECK_ARG(rows >= 0 && rows <= kRowsMax, "rows must be in 0..%d", kRowsMax);
+  const bool tiles = (mode & VL_LINEAR_TILES16) != 0;
+  mode &= ~VL_LINEAR_TILES16;
   VL_CHECK_ARG(mode >= VL_LINEAR_STORE && mode <= VL_LINEAR_SWIGLU, "bad mode %d", mode);
   VL_CHECK_ARG(k > 0 && k % 16 == 0 && k <= 1024, "k must be a multiple of 16, at most 1024");
   VL_CHECK_ARG(n > 0, "n must be positive");
@@ -245,20 +273,17 @@ extern "C" int vl_linear_rows(float* out, int64_t out_stride, const float* x, in
                "x must be 16-byte aligned with a row stride that is a multiple of 4");
   VL_CHECK_ARG(x_stride >= k && out_stride >= n, "row strides too small");
   const int64_t wcols = mode == VL_LINEAR_SWIGLU ? 2 * (int64_t)n : n;
-  VL_CHECK_ARG(weight_stride >= wcols, "weight row stride too small");
+  VL_CHECK_ARG(tiles || weight_stride >= wcols, "weight row stride too small");
   hipStream_t st = (hipStream_t)stream;
   const bool nrm = norm_weight != nullptr;
   // KMAX, the unrolled depth, is the smallest of 384 / 512 / 1024 that holds k
 #define VL_LINEAR_K(MODE, NORM)                                                              \
   (k <= 384 ? launch<MODE, NORM, 384>(out, out_stride, x, x_stride, weight, weight_stride,    \
-                                      MODE == 2 ? n : 0, norm_weight, eps, rows, k, n, st,     \
-                                      row_index)                                               \
+                                      tiles, norm_weight, eps, rows, k, n, st, row_index)      \
    : k <= 512 ? launch<MODE, NORM, 512>(out, out_stride, x, x_stride, weight, weight_stride,  \
-                                        MODE == 2 ? n : 0, norm_weight, eps, rows, k, n, st,   \
-                                        row_index)                                             \
+                                        tiles, norm_weight, eps, rows, k, n, st, row_index)    \
               : launch<MODE, NORM, 1024>(out, out_stride, x, x_stride, weight, weight_stride, \
-                                         MODE == 2 ? n : 0, norm_weight, eps, rows, k, n, st,  \
-                                         row_index))
+                                         tiles, norm_weight, eps, rows, k, n, st, row_index))
   switch (mode) {
     case VL_LINEAR_STORE:
       return nrm ? VL_LINEAR_K(0, true) : VL_LINEAR_K(0, false);
@@ -273,7 +298,8 @@ extern "C" int vl_linear_rows(float* out, int64_t out_stride, const float* x, in
 extern "C" int vl_qkv_rope_cache(float* q_out, float* key_cache, float* value_cache,
                                  const float* x, int64_t x_stride, const int32_t* row_index,
                                  float* x_out, const float* weight,
-                                 int64_t weight_stride, const float* norm_weight, float eps,
+                                 int64_t weight_stride, int weight_layout,
+                                 const float* norm_weight, float eps,
                                  const int32_t* positions, const int32_t* slot_mapping,
                                  const float* cos_table, const float* sin_table, int rows, int k,
                                  int num_heads, int num_kv_heads, int head_dim, void* stream) {
@@ -288,7 +314,10 @@ extern "C" int vl_qkv_rope_cache(float* q_out, float* key_cache, float* value_ca
   VL_CHECK_ARG((((uintptr_t)x) & 15) == 0 && x_stride % 4 == 0 && x_stride >= k,
                "x must be 16-byte aligned with a row stride that is a multiple of 4");
   const int n = (num_heads + 2 * num_kv_heads) * head_dim;
-  VL_CHECK_ARG(weight_stride >= n, "weight row stride too small");
+  VL_CHECK_ARG(weight_layout == VL_WEIGHT_ROWS || weight_layout == VL_WEIGHT_TILES16,
+               "bad weight layout %d", weight_layout);
+  const bool tiles = weight_layout == VL_WEIGHT_TILES16;
+  VL_CHECK_ARG(tiles || weight_stride >= n, "weight row stride too small");
   RopeCache rc;
   rc.q_out = q_out, rc.kc = key_cache, rc.vc = value_cache, rc.positions = positions;
   rc.slots = slot_mapping, rc.cos_t = cos_table, rc.sin_t = sin_table;
@@ -296,8 +325,8 @@ extern "C" int vl_qkv_rope_cache(float* q_out, float* key_cache, float* value_ca
   hipStream_t st = (hipStream_t)stream;
   const bool nrm = norm_weight != nullptr;
 #define VL_QKV(NORM, KM) \
-  launch<3, NORM, KM>(nullptr, 0, x, x_stride, weight, weight_stride, 0, norm_weight, eps, rows, k, \
-                      n, st, row_index, rc, x_out)
+  launch<3, NORM, KM>(nullptr, 0, x, x_stride, weight, weight_stride, tiles, norm_weight, eps, rows, \
+                      k, n, st, row_index, rc, x_out)
   if (k <= 384) return nrm ? VL_QKV(true, 384) : VL_QKV(false, 384);
   if (k <= 512) return nrm ? VL_QKV(true, 512) : VL_QKV(false, 512);
   return nrm ? VL_QKV(true, 1024) : VL_QKV(false, 1024);

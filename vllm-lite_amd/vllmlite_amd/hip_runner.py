@@ -18,7 +18,8 @@ count) for scheduled sequence i, count = min(1 + drafts, tokens)
      gate|up GEMM, SwiGLU, the down GEMM; finally RMSNorm and the tied lm_head
      on the logits rows only. Steps of at most 16 tokens (the decode steps)
      run each projection as one vl_linear_rows launch with the RMSNorm before
-     it and the residual add or SwiGLU after it fused in;
+     it and the residual add or SwiGLU after it fused in (weights in
+     16-column tiles);
   4. one device-to-host copy of the logits rows and a stream synchronisation.
 
 Step 3 is captured once per shape bucket (tokens, sequences and logits rows
@@ -40,7 +41,7 @@ import numpy as np
 import torch
 
 from . import ops
-from .model import model_weights, pack_weights, rope_tables
+from .model import model_weights, pack_weights, rope_tables, tile_weights
 from .runner import ModelRunner
 
 
@@ -87,6 +88,7 @@ class HipRunner(ModelRunner):
             self.stream = torch.cuda.Stream(self.device)
             w = weights if weights is not None else model_weights(mc)
             self.w = pack_weights(mc, w, torch, self.device)
+            tile_weights(self.w, ops.tile16)
             cos, sin = rope_tables(mc.head_dim, mc.max_seq_len)
             self.cos = torch.from_numpy(cos).to(self.device)
             self.sin = torch.from_numpy(sin).to(self.device)
@@ -282,18 +284,18 @@ class HipRunner(ModelRunner):
         for li, L in enumerate(W["layers"]):
             kc, vc = self.cache_k[li], self.cache_v[li]
             if li == 0:  # the embedding gather, with x = tok_emb[tok] written out
-                ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, W["tok_emb"], L["w_qkv"],
+                ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, W["tok_emb"], L["w_qkv_t"],
                                    L["attn_norm"], pos, slot, self.cos, self.sin, self.H,
                                    self.Hkv, self.hd, row_index=tok, x_out=x)
             else:
-                ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, x, L["w_qkv"], L["attn_norm"], pos,
+                ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, x, L["w_qkv_t"], L["attn_norm"], pos,
                                    slot, self.cos, self.sin, self.H, self.Hkv, self.hd)
             ops.paged_attention_run(attn, q, kc, vc, bt, lens, qsl, self.scale, self.block_size,
                                     self._ws)
-            ops.linear_rows(x, attn.view(Tb, -1), L["wo"], mode=ops.LINEAR_ACCUMULATE)
-            ops.linear_rows(act, x, L["w_gate_up"], L["ffn_norm"], mode=ops.LINEAR_SWIGLU)
-            ops.linear_rows(x, act, L["w_down"], mode=ops.LINEAR_ACCUMULATE)
-        ops.linear_rows(self._logits[:Rb], x, W["lm_head"], W["final_norm"],
+            ops.linear_rows(x, attn.view(Tb, -1), L["wo_t"], mode=ops.LINEAR_ACCUMULATE)
+            ops.linear_rows(act, x, L["w_gate_up_t"], L["ffn_norm"], mode=ops.LINEAR_SWIGLU)
+            ops.linear_rows(x, act, L["w_down_t"], mode=ops.LINEAR_ACCUMULATE)
+        ops.linear_rows(self._logits[:Rb], x, W["lm_head_t"], W["final_norm"],
                         mode=ops.LINEAR_STORE, row_index=lidx)
 
     def _capture(self, s: _Shape, key) -> None:

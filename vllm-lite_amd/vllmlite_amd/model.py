@@ -96,3 +96,14 @@ def pack_weights(cfg, w: Dict[str, np.ndarray], torch, device) -> dict:
         })
     return {"tok_emb": dev(w["tok_emb"]), "lm_head": dev(w["lm_head"]),
             "final_norm": dev(w["final_norm"]), "layers": layers}
+
+
+def tile_weights(packed: dict, tile16) -> None:
+    """Add 16-column tiled copies of the projection weights (suffix `_t`) for
+    the decode-step kernels, which read them in whole cache lines."""
+    for L in packed["layers"]:
+        L["w_qkv_t"] = tile16(L["w_qkv"])
+        L["wo_t"] = tile16(L["wo"])
+        L["w_gate_up_t"] = tile16(L["w_gate_up"], 2)
+        L["w_down_t"] = tile16(L["w_down"])
+    packed["lm_head_t"] = tile16(packed["lm_head"])

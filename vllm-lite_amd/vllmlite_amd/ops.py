@@ -52,7 +52,7 @@ SIGNATURES = {
     "vl_linear_rows": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64,
                               _c_void_p, _f32, _i32, _i32, _i32, _i32, _c_void_p]),
     "vl_qkv_rope_cache": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
-                                 _c_void_p, _c_void_p, _i64, _c_void_p, _f32, _c_void_p,
+                                 _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _f32, _c_void_p,
                                  _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32,
                                  _c_void_p]),
 }
@@ -251,7 +251,35 @@ def rms_norm(out: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, eps: floa
 
 
 LINEAR_STORE, LINEAR_ACCUMULATE, LINEAR_SWIGLU = 0, 1, 2
+LINEAR_TILES16 = 16  # mode flag: the weight is in 16-column tiles
+WEIGHT_ROWS, WEIGHT_TILES16 = 0, 1
 LINEAR_ROWS_MAX = 16
+
+
+def tile16(w: torch.Tensor, halves: int = 1) -> torch.Tensor:
+    """A [k, halves * n] weight as 16-column tiles [halves * ceil(n/16), k, 16]
+    (zero past column n; with halves 2, the tiles of w[:, :n] then those of
+    w[:, n:], the SwiGLU gate and up halves)."""
+    k, cols = w.shape
+    n = cols // halves
+    nt = -(-n // 16)
+    parts = []
+    for h in range(halves):
+        p = torch.zeros(k, nt * 16, dtype=w.dtype, device=w.device)
+        p[:, :n] = w[:, h * n:(h + 1) * n]
+        parts.append(p.view(k, nt, 16).permute(1, 0, 2))
+    return torch.cat(parts).contiguous()
+
+
+def _weight_layout(weight: torch.Tensor, k: int, n: int, halves: int):
+    """(tiles?, row stride) of a row-major [k, >= halves*n] or tiled weight."""
+    if weight.dim() == 3:
+        _need(weight.is_contiguous() and weight.shape == (halves * -(-n // 16), k, 16),
+              "tiled weight must be [halves * ceil(n/16), k, 16]")
+        return True, 0
+    _need(weight.shape[0] == k and weight.shape[1] >= halves * n and weight.stride(-1) == 1,
+          "weight shape mismatch")
+    return False, weight.stride(0)
 
 
 def linear_rows(out: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
@@ -267,12 +295,13 @@ def linear_rows(out: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
           "row_index must hold int32 row numbers")
     for t in (out, x, weight) + ((norm_weight,) if norm_weight is not None else ()):
         _need(t.dtype == torch.float32 and t.stride(-1) == 1, "fp32 row-major tensors required")
-    _need(out.shape[0] == rows and weight.shape[0] == k, "shape mismatch")
-    _need(weight.shape[1] >= (2 * n if mode == LINEAR_SWIGLU else n), "weight too narrow")
+    _need(out.shape[0] == rows, "shape mismatch")
+    tiles, wstride = _weight_layout(weight, k, n, 2 if mode == LINEAR_SWIGLU else 1)
     _need(norm_weight is None or norm_weight.numel() == k, "norm weight shape mismatch")
     _check(lib().vl_linear_rows(_ptr(out), out.stride(0), _ptr(x), x.stride(0), _ptr(row_index),
-                                _ptr(weight), weight.stride(0), _ptr(norm_weight), float(eps),
-                                rows, k, n, mode, _stream()), "vl_linear_rows")
+                                _ptr(weight), wstride, _ptr(norm_weight), float(eps), rows, k, n,
+                                mode | (LINEAR_TILES16 if tiles else 0), _stream()),
+           "vl_linear_rows")
 
 
 def qkv_rope_cache(q_out: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
@@ -290,11 +319,12 @@ def qkv_rope_cache(q_out: torch.Tensor, key_cache: torch.Tensor, value_cache: to
     _need(x_out is None or (x_out.is_contiguous() and x_out.shape[1] == k), "x_out shape mismatch")
     for t in (q_out, key_cache, value_cache, x, weight, cos, sin):
         _need(t.dtype == torch.float32 and t.stride(-1) == 1, "fp32 row-major tensors required")
-    _need(weight.shape[0] == k and positions.numel() >= rows and slot_mapping.numel() >= rows,
-          "shape mismatch")
+    _need(positions.numel() >= rows and slot_mapping.numel() >= rows, "shape mismatch")
+    tiles, wstride = _weight_layout(weight, k, (num_heads + 2 * num_kv_heads) * head_dim, 1)
     _check(lib().vl_qkv_rope_cache(_ptr(q_out), _ptr(key_cache), _ptr(value_cache), _ptr(x),
                                    x.stride(0), _ptr(row_index), _ptr(x_out), _ptr(weight),
-                                   weight.stride(0), _ptr(norm_weight),
+                                   wstride, WEIGHT_TILES16 if tiles else WEIGHT_ROWS,
+                                   _ptr(norm_weight),
                                    float(eps), _ptr(positions), _ptr(slot_mapping), _ptr(cos),
                                    _ptr(sin), rows, k, num_heads, num_kv_heads, head_dim,
                                    _stream()), "vl_qkv_rope_cache")
