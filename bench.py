@@ -15,7 +15,9 @@ inputs resident in HBM; the work plan is built once outside the timed region,
 as the runner does once per step for all of a model's layers.
 
 One JSON line:
-  value         algorithmic HBM bytes per step / measured step time (GB/s)
+  value         algorithmic HBM bytes per step / step time (GB/s); the step time
+                is the host clock over `steps` launches issued back to back,
+                between two stream synchronisations
   roofline      the decode launch's average duration from HIP events on the
                 stream it is launched on; achieved = algorithmic bytes / that,
                 against 8 TB/s; traffic = FETCH_SIZE + WRITE_SIZE bytes per
@@ -83,12 +85,17 @@ def decode_leg(torch, ops, syn, steps, warmup, profile_only=False):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    # the launch's own duration: an event pair around each launch
     ev = events(torch, steps)
-    t0 = time.perf_counter()
     for e0, e1 in ev:
         e0.record()
         step()
         e1.record()
+    torch.cuda.synchronize()
+    # the step rate: `steps` launches back to back, host clock around them
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     res = {"kernel_ms": mean_ms(ev), "ms_per_step": wall * 1e3 / steps,
