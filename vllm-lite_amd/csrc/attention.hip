@@ -595,16 +595,27 @@ template <typename T, int D, int RW>
 struct TileLds;
 template <int D, int RW>
 struct TileLds<uint16_t, D, RW> {
-  static constexpr int kRow = D + 8;           // K row stride (bf16), 16-byte aligned
-  static constexpr int vRow = kTileKeys + (RW == 32 ? 4 : 8);  // V^T row stride (bf16),
-                                                              // 8-byte aligned
-  static constexpr int kChunks = D / 8;        // 16-byte chunks per head row
-  // prefetch units per thread: K (key, chunk); V (4 keys, chunk)
+  static constexpr int kRow = D + 8;  // K row stride (bf16), 16-byte aligned
+  // V rows as in the cache (key-major), read transposed by ds_read_b64_tr_b16:
+  // a PV operand read takes 8 bytes of each of 4 (RW 16: 8) keys per 16 dims,
+  // so the row stride in dwords is 16 (RW 16: 8) modulo the 64 banks
+  static constexpr int vRow = 2 * ((D / 2 + 63 - (RW == 32 ? 16 : 8)) / 64 * 64 + (RW == 32 ? 16 : 8));
+  static constexpr int kChunks = D / 8;  // 16-byte chunks per head row
+  // prefetch units per thread (K and V alike): (key, chunk)
   static constexpr int kUnits = kTileKeys * kChunks / 256;
-  static constexpr int vUnits = (kTileKeys / 4) * kChunks;  // threads < vUnits take one
   uint16_t k[kTileKeys * kRow];
-  uint16_t vt[D * vRow];
+  uint16_t v[kTileKeys * vRow];
 };
+
+// 4 bf16 of a PV operand from LDS by the transposing read: lane i of each
+// 16-lane group passes the address of 4 consecutive dims (4 (i % 4) ..) of key
+// i / 4 of a 4-key x 16-dim block and receives dim i of the 4 keys.
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
+  typedef short s16x4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+  const s16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)p);
+  return __builtin_bit_cast(uint2, r);
+}
 template <int D, int RW>
 struct TileLds<float, D, RW> {
   static constexpr int kRow = D + 1;
@@ -687,7 +698,7 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
   constexpr int kCV = kW ? 16 : 4;                       // accumulator values per subtile
   using Lds = TileLds<T, D, RW>;
   using AccT = float __attribute__((ext_vector_type(kCV)));
-  static_assert(!kBf16 || (Lds::kUnits * 256 == kTileKeys * Lds::kChunks && Lds::vUnits <= 256),
+  static_assert(!kBf16 || Lds::kUnits * 256 == kTileKeys * Lds::kChunks,
                 "bf16 tile staging assumes head_dim 64 or 128");
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -756,7 +767,7 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
       return (int64_t)((uint64_t)blk * blk_elems) +
              (int64_t)((key & bs_mask) * (uint32_t)slot_stride) + kv_off;
     };
-    uint4 pk[Lds::kUnits], pv[kBf16 ? 4 : Lds::kUnits];
+    uint4 pk[Lds::kUnits], pv[Lds::kUnits];
     // bf16 staging: K unit r of a tile is keys k0 + kUnitKeys r + threadIdx / kChunks,
     // chunk threadIdx % kChunks; with blocks of >= kUnitKeys slots the unit lies
     // in one block whose id is uniform over the workgroup (tile starts are
@@ -769,66 +780,33 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
         (uint32_t)(tid / Lds::kChunks) * (uint32_t)slot_stride + (tid % Lds::kChunks) * 8;
     auto prefetch = [&](int k0) {
       if constexpr (kBf16) {
-        // V: four consecutive keys of one 8-dim chunk (one block: block sizes
-        // are powers of two >= 4 here); the key quad varies fastest over the
-        // lanes so the transposed LDS stores hit distinct banks
-        const int kq = tid & (kTileKeys / 4 - 1), c = tid / (kTileKeys / 4);
-        const int kv0 = k0 + 4 * kq;
-        const bool v_lane = Lds::vUnits == 256 || tid < Lds::vUnits;
         if (unit_blocks) {
           // the units' block ids first (scalar loads, issued together), then
-          // every K and V address from them: V keys kv0 .. kv0 + 3 lie in unit
-          // 4 kq / kUnitKeys, and a V key clamped to the last key lies in the
-          // last unit's block, which is that unit's (a unit past the end reads
-          // the last unit's block, as the K loads do)
+          // every K and V address from them; V keys past the end re-read the
+          // last key, which lies in the last unit's block, as does a unit
+          // past the end (its K reads stay there too; their scores are masked)
           const int klast = (kend_wg - 1) & ~(kUnitKeys - 1);
           uint32_t blk[Lds::kUnits];
 #pragma unroll
           for (int r = 0; r < Lds::kUnits; ++r)
             blk[r] = (uint32_t)table[min(k0 + kUnitKeys * r, klast) >> bs_log2];
-          int64_t boff[Lds::kUnits];
+          const int tk = tid / Lds::kChunks, tc = (tid % Lds::kChunks) * 8;
 #pragma unroll
           for (int r = 0; r < Lds::kUnits; ++r) {
             const int kr = min(k0 + kUnitKeys * r, klast);
-            boff[r] = (int64_t)((uint64_t)blk[r] * blk_elems) + kv_off;
-            pk[r] = load16(kc + boff[r] + ((uint32_t)(kr & bs_mask) * (uint32_t)slot_stride + k_thr_off));
-          }
-          if (v_lane) {
-            const int u = (4 * kq) / kUnitKeys;
-            int64_t vb = boff[0];
-#pragma unroll
-            for (int r = 1; r < Lds::kUnits; ++r) vb = u == r ? boff[r] : vb;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int key = min(kv0 + e, kend_wg - 1);
-              pv[e] = load16(vc + vb + ((uint32_t)(key & bs_mask) * (uint32_t)slot_stride + c * 8));
-            }
+            const int64_t boff = (int64_t)((uint64_t)blk[r] * blk_elems) + kv_off;
+            pk[r] = load16(kc + boff + ((uint32_t)(kr & bs_mask) * (uint32_t)slot_stride + k_thr_off));
+            const int vkey = min(kr + tk, kend_wg - 1);
+            pv[r] = load16(vc + boff + ((uint32_t)(vkey & bs_mask) * (uint32_t)slot_stride + tc));
           }
         } else {
 #pragma unroll
           for (int r = 0; r < Lds::kUnits; ++r) {
             const int idx = tid + 256 * r;
             const int kk = idx / Lds::kChunks, cc = idx - kk * Lds::kChunks;
-            const int key = min(k0 + kk, kend_wg - 1);
-            pk[r] = load16(kc + row_of(key) + cc * 8);
-          }
-          if (v_lane) {
-            if (bs_log2 >= 2) {
-              const int vb = min(kv0, kend_wg - 1);
-              const T* base = vc + (int64_t)((uint64_t)(uint32_t)table[vb >> bs_log2] * blk_elems) +
-                              kv_off + c * 8;
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const int key = min(kv0 + e, kend_wg - 1);
-                pv[e] = load16(base + (uint32_t)(key & bs_mask) * (uint32_t)slot_stride);
-              }
-            } else {
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const int key = min(kv0 + e, kend_wg - 1);
-                pv[e] = load16(vc + row_of(key) + c * 8);
-              }
-            }
+            const int64_t off = row_of(min(k0 + kk, kend_wg - 1)) + cc * 8;
+            pk[r] = load16(kc + off);
+            pv[r] = load16(vc + off);
           }
         }
       } else {
@@ -851,24 +829,7 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
           const int idx = tid + 256 * r;
           const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
           *reinterpret_cast<uint4*>(&b.k[kk * Lds::kRow + c * 8]) = pk[r];
-        }
-        if (Lds::vUnits == 256 || tid < Lds::vUnits) {
-          const int kq = tid & (kTileKeys / 4 - 1), c = tid / (kTileKeys / 4);
-          const uint32_t w[4][4] = {{pv[0].x, pv[0].y, pv[0].z, pv[0].w},
-                                    {pv[1].x, pv[1].y, pv[1].z, pv[1].w},
-                                    {pv[2].x, pv[2].y, pv[2].z, pv[2].w},
-                                    {pv[3].x, pv[3].y, pv[3].z, pv[3].w}};
-#pragma unroll
-          for (int m = 0; m < 4; ++m) {
-            // dims 8c + 2m (low halves) and 8c + 2m + 1 (high halves) of keys 4kq..4kq+3
-            const uint32_t lo01 = __builtin_amdgcn_perm(w[1][m], w[0][m], 0x05040100u);
-            const uint32_t lo23 = __builtin_amdgcn_perm(w[3][m], w[2][m], 0x05040100u);
-            const uint32_t hi01 = __builtin_amdgcn_perm(w[1][m], w[0][m], 0x07060302u);
-            const uint32_t hi23 = __builtin_amdgcn_perm(w[3][m], w[2][m], 0x07060302u);
-            const int d = c * 8 + 2 * m;
-            *reinterpret_cast<uint2*>(&b.vt[d * Lds::vRow + 4 * kq]) = make_uint2(lo01, lo23);
-            *reinterpret_cast<uint2*>(&b.vt[(d + 1) * Lds::vRow + 4 * kq]) = make_uint2(hi01, hi23);
-          }
+          *reinterpret_cast<uint4*>(&b.v[kk * Lds::vRow + c * 8]) = pv[r];
         }
       } else {
 #pragma unroll
@@ -959,10 +920,14 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
       constexpr int kLook = kW ? kPvLook : 1;
       auto vread = [&](int st) {  // operand of step st: dims 32u + .., keys 32t + 16hh + ..
         if constexpr (kW) {
+          // keys 32t + 16hh + 4 grp + (0..3) and + 8, dims 32u + l % 32 (16-lane
+          // group: dims 32u + 16 (l / 16 % 2) + ..)
           const int t = st / (2 * kDT), hh = (st / kDT) % 2, u = st % kDT;
-          const uint16_t* vrow = &b.vt[(32 * u + col) * Lds::vRow + 32 * t + 16 * hh + 4 * grp];
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 8);
+          const int li = lane & 15;
+          const uint16_t* vp = &b.v[(32 * t + 16 * hh + 4 * grp + (li >> 2)) * Lds::vRow + 32 * u +
+                                    16 * ((lane >> 4) & 1) + 4 * (li & 3)];
+          const uint2 lo = lds_read_tr16(vp);
+          const uint2 hi = lds_read_tr16(vp + 8 * Lds::vRow);
           return make_uint4(lo.x, lo.y, hi.x, hi.y);
         } else {
           return make_uint4(0, 0, 0, 0);
@@ -1019,9 +984,12 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
           const bf16x8_t pop = __builtin_bit_cast(bf16x8_t, pw);
 #pragma unroll
           for (int u = 0; u < kDT; ++u) {
-            const uint16_t* vrow = &b.vt[(16 * u + col) * Lds::vRow + 32 * hh];
-            const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * grp);
-            const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * grp);
+            // keys 32hh + 4 grp + (0..3) and + 16, dims 16u + l % 16
+            const int li = lane & 15;
+            const uint16_t* vp =
+                &b.v[(32 * hh + 4 * grp + (li >> 2)) * Lds::vRow + 16 * u + 4 * (li & 3)];
+            const uint2 lo = lds_read_tr16(vp);
+            const uint2 hi = lds_read_tr16(vp + 16 * Lds::vRow);
             const uint4 vw = make_uint4(lo.x, lo.y, hi.x, hi.y);
             acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, vw), pop,
                                                              acc[u], 0, 0, 0);
