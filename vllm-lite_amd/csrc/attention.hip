@@ -1900,7 +1900,9 @@ int do_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) 
         L.nparts, L.split_base, L.ml, L.po);
     VL_CHECK_LAUNCH();
   }
-  combine_kernel<T><<<ncu * 8, 256, 0, st>>>((T*)a.out, a.qsl, a.H, a.D, L.hdr, L.cmb_seq,
+  // one workgroup per (split sequence, query head) item, at most S * H of them
+  const int cmb_grid = (int)std::min<int64_t>((int64_t)ncu * 8, std::max<int64_t>((int64_t)a.S * a.H, 1));
+  combine_kernel<T><<<cmb_grid, 256, 0, st>>>((T*)a.out, a.qsl, a.H, a.D, L.hdr, L.cmb_seq,
                                             L.nparts, L.split_base, L.ml, L.po, L.hdr + 26);
   VL_CHECK_LAUNCH();
   return VL_OK;
