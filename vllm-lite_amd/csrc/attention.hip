@@ -6,20 +6,24 @@
 // host synchronisation:
 //  plan     one workgroup reads seq_lens / query_start_loc and writes into the
 //           workspace, per sequence, its work-item offsets, its number of
-//           context partitions and where split partials go. The partition
-//           length starts at 256 tokens and doubles until the split partials
-//           fit the workspace, so any workspace >= the minimum is correct.
-//           The plan depends only on the lengths, so one plan serves every
-//           layer of a step.
-//  run      decode sequences of the bf16 / head_dim 128 / 4-query-heads-per-
-//           KV-head / block-16 shape go to the bandwidth kernel (one
-//           wavefront per (sequence, partition, KV head), a 4-wave workgroup
-//           per 4 adjacent KV heads), which merges its own split sequences;
-//           multi-query sequences go to the MFMA tile kernel when the head
-//           dim has an instantiation, else to the generic kernel (one
-//           wavefront per (sequence, query, head, partition)). Their split
-//           sequences are merged by the combine kernel (max-rescaled
-//           log-sum-exp).
+//           context partitions (multi-query) or ranges (decode), where split
+//           partials go, and the order in which items are handed out
+//           (longest first). Partitions start at 64 tokens and ranges at the
+//           smallest power of two that gives a few items per resident
+//           workgroup; both double until the split partials fit the
+//           workspace, so any workspace >= the minimum is correct. The plan
+//           depends only on the lengths, so one plan serves every layer of a
+//           step.
+//  run      single-query sequences of the bf16 / head_dim 128 / 4-query-heads-
+//           per-KV-head / block-16 shape go to the bandwidth kernel (a
+//           workgroup per (range, KV head) item, its 4 wavefronts splitting
+//           the range's blocks), which merges its own split sequences;
+//           multi-query sequences go to the MFMA tile kernels (16- or 32-row
+//           wavefronts) when the head dim has an instantiation, else to the
+//           generic kernel (one wavefront per (sequence, query, head,
+//           partition)); a batch holding both kinds runs in the one step
+//           kernel. Split multi-query sequences are merged by the combine
+//           kernel (max-rescaled log-sum-exp).
 //
 // Softmax runs in the base-2 domain: scores are pre-multiplied by
 // scale * log2(e) and exponentiated with exp2, which is the same function.
@@ -288,8 +292,9 @@ static_assert(kTailBuckets == kPlanThreads, "one tail bucket per plan thread");
 // power of two in 64..kRangeMax that leaves at most target_items (range, KV head)
 // items, i.e. a few per resident workgroup: longer ranges mean fewer split
 // partials to write and merge, shorter ones keep every CU busy) and the
-// multi-query partition length P (256), doubling both until the split
-// partials fit the workspace. Then writes per-sequence offsets and the order
+// multi-query partition length P (the smallest power of two from kPart0 that
+// leaves about tile_target items), doubling both until the split partials fit
+// the workspace. Then writes per-sequence offsets and the order
 // in which the shorter last ranges are handed out: longest first, after all
 // full ranges, so the kernel ends on its smallest items. The sequences with
 // 32-row tile items are ordered the same way, by context length, longest
@@ -1924,7 +1929,7 @@ extern "C" size_t vl_paged_attention_workspace_size(int num_seqs, int num_tokens
   if (num_seqs < 0 || num_tokens < 0 || num_heads <= 0 || head_dim <= 0) return 0;
   const int64_t S = num_seqs, H = num_heads;
   const int64_t ctx = max_context_len > 0 ? max_context_len : 1;
-  // multi-query rows split into partitions of 256 tokens (up to 64)
+  // multi-query rows split into partitions of kPart0 tokens or more (at most 64)
   const int64_t split_tokens = num_tokens < S * kSplitMaxQ ? num_tokens : S * kSplitMaxQ;
   int64_t parts = std::min<int64_t>(std::max<int64_t>(cdiv64(ctx, kPart0), 1), 64);
   const int64_t rows_tile = parts > 1 ? split_tokens * H * parts : 0;
