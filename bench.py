@@ -138,20 +138,32 @@ def cpu_baseline(torch, b, budget_s=12.0):
                      b["vc"][sl].float().cpu().numpy(), np.arange(len(slots))))
     ctx = b["ctx"][sample]
     per_pass = int(ctx.sum()) * 2 * b["Hkv"] * b["D"] * 2 + 2 * len(sample) * b["H"] * b["D"] * 2
-    done_bytes, t0, reps = 0, time.perf_counter(), 0
-    while True:
-        for q, k, v, rs in data:
-            paged_attention(q, k, v, rs, b["Hkv"], b["scale"])
-        reps += 1
-        done_bytes += per_pass
-        if time.perf_counter() - t0 > budget_s or reps >= 50:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": round(done_bytes / dt / 1e9, 3), "unit": "GB/s",
+
+    def rate(budget):
+        done_bytes, t0, reps = 0, time.perf_counter(), 0
+        while True:
+            for q, k, v, rs in data:
+                paged_attention(q, k, v, rs, b["Hkv"], b["scale"])
+            reps += 1
+            done_bytes += per_pass
+            if time.perf_counter() - t0 > budget or reps >= 50:
+                break
+        return done_bytes / (time.perf_counter() - t0) / 1e9, reps
+
+    gbs, reps = rate(budget_s)
+    one = None
+    try:  # the same with one BLAS thread
+        from threadpoolctl import threadpool_limits
+        with threadpool_limits(limits=1):
+            one = round(rate(budget_s / 2)[0], 3)
+    except Exception:  # pragma: no cover
+        pass
+    return {"value": round(gbs, 3), "unit": "GB/s", "value_1_blas_thread": one,
             "cores": int(min(cores, blas_threads)), "kind": "port",
             "sample": f"{len(sample)} of {S} sequences (every 8th), {reps} passes of the oracle's "
                       f"NumPy paged_attention on fp32 copies, bytes counted at the bf16 size; "
-                      f"{cores} visible cores, BLAS threads {blas_threads}"}
+                      f"{cores} visible cores, BLAS threads {blas_threads} (value_1_blas_thread: "
+                      f"one BLAS thread, half the time budget)"}
 
 
 def mixed_leg(torch, ops, syn, steps, warmup, profile_only=False):
@@ -378,6 +390,14 @@ def e2e_leg(repeat=3, cpu=True, shared_prefix=0):
         out["cpu_cores"] = len(os.sched_getaffinity(0))
         out["speedup_vs_cpu_numpy"] = round(toks / wall / cpu_tps, 2)
         out["cpu_streams_identical"] = cpu_best[3] == streams
+        try:  # one pass with one BLAS thread
+            from threadpoolctl import threadpool_limits
+            with threadpool_limits(limits=1):
+                one = run_mix(NumpyRunner(cfg.model, cfg.cache), cfg, shared_prefix)
+            out["cpu_numpy_tok_per_s_1_blas_thread"] = round(one[1] / one[0], 1)
+            out["speedup_vs_cpu_numpy_1_blas_thread"] = round(toks / wall / (one[1] / one[0]), 2)
+        except Exception:  # pragma: no cover
+            pass
     return out
 
 
