@@ -90,6 +90,7 @@ def test_graph_replay_equals_eager_logits():
             return lg, rows
 
         eng.runner.execute = execute
+        eng.device_argmax = False  # every step through execute()
         run(eng, PROMPTS)
         seen.append(logs)
     assert len(seen[0]) == len(seen[1])
@@ -134,6 +135,54 @@ def test_speculation_matches_plain_greedy(k):
     assert e.spec.accepted > 0
 
 
+@pytest.mark.parametrize("k", [0, 4])
+def test_device_argmax_matches_host_argmax(k):
+    """Greedy steps through execute_argmax (argmax on the device, R int32
+    values to the host) give the streams of execute() + np.argmax, with and
+    without draft verification; the device path is the one taken."""
+    rep = PROMPTS + ["abcdefgh abcdefgh abcdefgh abcdefgh abcdefgh abcdefgh"]
+    streams, calls = [], []
+    for dev in (True, False):
+        e = hip_engine()
+        if k:
+            e.spec_k = k
+            e.proposer = NgramProposer(k)
+        e.device_argmax = dev
+        n = [0]
+        real = e.runner.execute_argmax
+
+        def execute_argmax(sched, real=real, n=n):
+            n[0] += 1
+            return real(sched)
+
+        e.runner.execute_argmax = execute_argmax
+        streams.append(run(e, rep, max_tokens=24))
+        calls.append(n[0])
+    assert streams[0] == streams[1]
+    assert calls[0] > 0 and calls[1] == 0
+
+
+def test_device_argmax_ids_equal_numpy_argmax():
+    """execute_argmax returns np.argmax of execute()'s rows for the same step
+    (the forward is deterministic: graph replay is bitwise eager)."""
+    e = hip_engine()
+    got = []
+    real_x, real_a = e.runner.execute, e.runner.execute_argmax
+
+    def execute_argmax(sched):
+        ids, rows = real_a(sched)
+        lg, rows2 = real_x(sched)
+        assert rows == rows2
+        got.append((ids, np.argmax(lg, axis=-1).astype(np.int32)))
+        return ids, rows
+
+    e.runner.execute_argmax = execute_argmax
+    run(e, PROMPTS, max_tokens=8)
+    assert got
+    for ids, want in got:
+        assert np.array_equal(ids, want)
+
+
 def test_copy_on_write_fork_matches_oracle_runner():
     """A forked parent with a partial tail block: the children's first decode
     step writes into the shared block, so the block manager emits CoW pairs;
@@ -158,6 +207,7 @@ def test_copy_on_write_fork_matches_oracle_runner():
             return real(sched)
 
         eng.runner.execute = execute
+        eng.device_argmax = False  # every step through execute()
         while eng.has_work:
             eng.step()
         assert cows, "no copy-on-write pair was scheduled"

@@ -22,7 +22,7 @@ from .runner import ModelRunner, make_runner
 from .sampling import sample
 from .scheduler import Scheduler
 from .sequence import RequestOutput, SamplingParams, Sequence, Status
-from .speculative import NgramProposer, SpecStats, verify
+from .speculative import NgramProposer, SpecStats, accept_greedy, verify
 from .tokenizer import get_tokenizer
 
 
@@ -43,6 +43,8 @@ class LLMEngine:
         if self.cfg.model.vocab_size < self.tokenizer.vocab_size:
             self.cfg.model.vocab_size = self.tokenizer.vocab_size
         self.runner = runner if runner is not None else make_runner(self.cfg)
+        # greedy steps take the argmax on the runner's side when it offers one
+        self.device_argmax = hasattr(self.runner, "execute_argmax")
         self.scheduler = Scheduler(self.cfg.scheduler, self.cfg.cache)
         self.seqs: Dict[str, Sequence] = {}
         self.detok: Dict[str, _Detok] = {}
@@ -113,6 +115,22 @@ class LLMEngine:
     def has_work(self) -> bool:
         return self.scheduler.has_work
 
+    def _argmax_only(self, sched) -> bool:
+        """True when every row the step's sequences read is used by a plain
+        argmax: draft verification, or greedy sampling with no repetition
+        penalty and no min_tokens EOS mask (sampling.sample's first branch)."""
+        eos = self.tokenizer.eos_id
+        for item in sched.scheduled:
+            seq = item.seq
+            if seq.draft_token_ids:
+                continue
+            p = seq.params
+            if p.temperature != 0.0 or p.repetition_penalty != 1.0:
+                return False
+            if eos is not None and len(seq.output_token_ids) < p.min_tokens:
+                return False
+        return True
+
     def step(self) -> List[RequestOutput]:
         sched = self.scheduler.schedule()
         dropped = [self._retired_output(s) for s in self.scheduler.drain_reports()]
@@ -120,7 +138,14 @@ class LLMEngine:
             return dropped
 
         t0 = time.perf_counter()
-        logits, rows = self.runner.execute(sched)
+        # a runner that can take the argmax on its side does so when every
+        # row of the step is consumed by a plain argmax
+        picked = None
+        if self.device_argmax and self._argmax_only(sched):
+            picked, rows = self.runner.execute_argmax(sched)
+            logits = None
+        else:
+            logits, rows = self.runner.execute(sched)
         self.busy_time += time.perf_counter() - t0
         self.total_steps += 1
 
@@ -133,7 +158,10 @@ class LLMEngine:
             drafts = seq.draft_token_ids
             if drafts:
                 drafts = list(drafts)
-                new_tokens, accepted = verify(logits[row0:row0 + count], drafts)
+                if picked is not None:
+                    new_tokens, accepted = accept_greedy(picked[row0:row0 + count], drafts)
+                else:
+                    new_tokens, accepted = verify(logits[row0:row0 + count], drafts)
                 seq.draft_token_ids.clear()
                 self.spec.proposed += len(drafts)
                 self.spec.accepted += accepted
@@ -148,7 +176,9 @@ class LLMEngine:
             if seq.num_computed < seq.num_tokens:
                 continue
 
-            if new_tokens is None:
+            if new_tokens is None and picked is not None:
+                new_tokens = [int(picked[row0 + count - 1])]
+            elif new_tokens is None:
                 # the seen-token list only matters under a repetition penalty
                 seen = seq.token_ids if seq.params.repetition_penalty != 1.0 else ()
                 new_tokens = [sample(logits[row0 + count - 1], seq.params, seen,

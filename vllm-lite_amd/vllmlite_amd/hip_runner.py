@@ -112,20 +112,40 @@ class HipRunner(ModelRunner):
 
     def execute(self, out) -> Tuple[np.ndarray, List[Tuple[int, int]]]:
         with torch.cuda.device(self.device), torch.cuda.stream(self.stream):
-            if out.cow:
-                self._copy_on_write(out.cow)
-            shape, rows, R = self._stage(out)
-            key = (shape.Tb, shape.Sb, shape.Rb)
-            g = self._graphs.get(key)
-            if g is not None:
-                g.replay()
-            else:
-                self._forward(shape)
-                if self.use_graphs:
-                    self._capture(shape, key)
+            rows, R = self._run(out)
             self._logits_host[:R].copy_(self._logits[:R], non_blocking=True)
             self.stream.synchronize()
             return self._logits_host_np[:R].copy(), rows
+
+    def execute_argmax(self, out) -> Tuple[np.ndarray, List[Tuple[int, int]]]:
+        """execute() for a batch whose every logits row is consumed by a plain
+        argmax (greedy sampling with nothing masked or penalised, and greedy
+        draft verification: vllmlite/sampling.py:49,56-57,
+        vllmlite/speculative.py:86-100): returns each row's argmax, ties to the
+        lowest index as np.argmax, computed on the device, so R int32 values
+        cross to the host instead of R x vocab fp32 logits."""
+        with torch.cuda.device(self.device), torch.cuda.stream(self.stream):
+            rows, R = self._run(out)
+            ops.argmax_rows(self._logits[:R], self._ids[:R])
+            self._ids_host[:R].copy_(self._ids[:R], non_blocking=True)
+            self.stream.synchronize()
+            return self._ids_host_np[:R].copy(), rows
+
+    def _run(self, out) -> Tuple[List[Tuple[int, int]], int]:
+        """CoW copies, staging and the forward (graph replay when captured);
+        leaves the logits rows in self._logits[:R]."""
+        if out.cow:
+            self._copy_on_write(out.cow)
+        shape, rows, R = self._stage(out)
+        key = (shape.Tb, shape.Sb, shape.Rb)
+        g = self._graphs.get(key)
+        if g is not None:
+            g.replay()
+        else:
+            self._forward(shape)
+            if self.use_graphs:
+                self._capture(shape, key)
+        return rows, R
 
     # -------------------------------------------------------------- staging --
     def _ensure_capacity(self, T: int, W: int) -> None:
@@ -157,6 +177,9 @@ class HipRunner(ModelRunner):
         self._logits = torch.zeros(cap, mc.vocab_size, **f32)
         self._logits_host = torch.zeros(cap, mc.vocab_size, dtype=torch.float32, pin_memory=True)
         self._logits_host_np = self._logits_host.numpy()
+        self._ids = torch.zeros(cap, dtype=torch.int32, device=dev)
+        self._ids_host = torch.zeros(cap, dtype=torch.int32, pin_memory=True)
+        self._ids_host_np = self._ids_host.numpy()
         ws = ops.paged_attention_workspace_size(cap, cap, H, hd, mc.max_seq_len + 64)
         self._ws = ops.AttentionWorkspace(dev).get(ws)
         self._cap_T = cap
