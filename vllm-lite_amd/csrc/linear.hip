@@ -3,11 +3,11 @@
 // residual add or SwiGLU gate after them fused in (vllmlite/model.py:96-101,
 // 114, 116-117, 119-120).
 //
-// One workgroup computes 16 rows x 16 output columns: the 4 wavefronts split
-// K four ways on v_mfma_f32_16x16x4f32, each loading its weight operands
-// straight into registers (all loads in flight at once) while the rows of x
-// are staged in LDS and normalised there; the four partial tiles are summed
-// in a fixed order. hipBLASLt runs these shapes as separate launches of
+// One workgroup computes 16 rows x 16 output columns: its kLinWaves (8)
+// wavefronts split K into contiguous ranges on v_mfma_f32_16x16x4f32, each
+// loading its weight operands straight into registers (all loads in flight at
+// once) while the rows of x are staged in LDS and normalised there; the
+// partial tiles are summed in wavefront order. hipBLASLt runs these shapes as separate launches of
 // ~7 us each; here a projection and its neighbours are one.
 //
 // Weights come row-major ([k, n] at a row stride) or as 16-column tiles
@@ -22,6 +22,15 @@ namespace {
 
 constexpr int kRowsMax = 16;
 constexpr int kCols = 16;
+#ifndef VL_LIN_WAVES
+#define VL_LIN_WAVES 8
+#endif
+// wavefronts per projection workgroup; they split K, so more of them make the
+// serial MFMA chain of each shorter (the kernel is latency-bound at <= 16
+// rows): 8 measured 7 % faster per TinyLlama decode step than 4, and the same
+// as 16, which spills registers at K = 1024)
+constexpr int kLinWaves = VL_LIN_WAVES;
+static_assert(kLinWaves == 4 || kLinWaves == 8, "4 or 8 wavefronts");
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -63,7 +72,7 @@ struct RopeCache {
 // TILES: the weight is in 16-column tiles (ldw unused; up_off counts
 // elements, the start of the up tiles).
 template <int MODE, bool NORM, int KMAX, bool TILES>
-__global__ void __launch_bounds__(256) linear_rows_kernel(
+__global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
     float* __restrict__ out, int64_t ldo, const float* __restrict__ x, int64_t ldx,
     const float* __restrict__ w, int64_t ldw, int64_t up_off, const float* __restrict__ norm_w,
     float eps, int M, int K, int N, const RopeCache rc, const int32_t* __restrict__ row_index,
@@ -71,20 +80,23 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(
   constexpr int kSlices = MODE == 2 ? 2 : 1;
   constexpr int KP = KMAX + 4;  // xs row stride: rows 4 words apart, so the
                                 // 16 rows x 4 k of an A read hit 64 banks
-  constexpr int kSteps = KMAX / 16;  // 16x16x4 steps per wavefront at K = KMAX
+  constexpr int kSteps = KMAX / (4 * kLinWaves);  // 16x16x4 steps per wavefront at K = KMAX
   __shared__ float xs[kRowsMax * KP];
-  __shared__ float red[kSlices][4][kRowsMax * kCols];
+  __shared__ float red[kSlices][kLinWaves][kRowsMax * kCols];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c0 = blockIdx.x * kCols;
   const int m = lane & 15, j = lane >> 4;
-  const int kb = wave * (K / 4);  // wavefront w takes k in [w K/4, (w+1) K/4)
-  const int nsteps = K / 16;
+  // wavefront w takes the spw steps of 4 k from step w spw (k in [kb, kb + 4
+  // nsteps)); the last wavefronts may have fewer steps, or none
+  const int spw = (K / 4 + kLinWaves - 1) / kLinWaves;
+  const int kb = wave * spw * 4;
+  const int nsteps = max(0, min(spw, K / 4 - wave * spw));
 
   // ---- the B operand straight into registers: step i of wavefront w needs
   // w[kb + 4i + l/16][c0 + l%16] in lane l (columns past the end read 0);
   // every load is issued before any is used
   // (loads outside the shape read a clamped, valid element that is then
-  // multiplied by 0: columns past N, and steps past K / 4 of this wavefront,
+  // multiplied by 0: columns past N, and steps past this wavefront's nsteps,
   // whose A values belong to the next wavefront's range. A select would let
   // the compiler turn each load into a branch that waits for it.)
   float wb[kSlices][kSteps];
@@ -94,16 +106,17 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(
     if constexpr (TILES) {
       // tile blockIdx.x: element (k, m) at k * 16 + m; a wavefront's 64 lanes
       // read 4 consecutive k rows, 256 contiguous bytes
-      const float* src = w + (s ? up_off : 0) + (int64_t)blockIdx.x * K * kCols + m +
-                         (int64_t)(kb + j) * kCols;
+      // (k rows clamped to K - 4 + j < K)
+      const float* src = w + (s ? up_off : 0) + (int64_t)blockIdx.x * K * kCols + m;
 #pragma unroll
       for (int i = 0; i < kSteps; ++i)
-        wb[s][i] = src[(int64_t)(4 * min(i, nsteps - 1)) * kCols] * (i < nsteps ? colmask : 0.f);
+        wb[s][i] = src[(int64_t)min(kb + 4 * i, K - 4) * kCols + j * kCols] *
+                   (i < nsteps ? colmask : 0.f);
     } else {
-      const float* src = w + (s ? up_off : 0) + min(c0 + m, N - 1) + (int64_t)(kb + j) * ldw;
+      const float* src = w + (s ? up_off : 0) + min(c0 + m, N - 1);
 #pragma unroll
       for (int i = 0; i < kSteps; ++i)
-        wb[s][i] = src[(int64_t)(4 * min(i, nsteps - 1)) * ldw] * (i < nsteps ? colmask : 0.f);
+        wb[s][i] = src[(int64_t)(min(kb + 4 * i, K - 4) + j) * ldw] * (i < nsteps ? colmask : 0.f);
     }
   }
   // the norm weights of this lane's columns k = lane + 64 i (clamped loads)
@@ -112,10 +125,10 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(
 #pragma unroll
     for (int i = 0; i < KMAX / 64; ++i) gw[i] = norm_w[min(lane + 64 * i, K - 1)];
   }
-  // ---- x rows to LDS (rows >= M are zero): thread t takes row t / 16 and
-  // float4 columns t % 16 + 16 u; row r is x[row_index[r]] when an index is
-  // given, and workgroup 0 copies the rows it read to x_out when given
-  {
+  // ---- x rows to LDS (rows >= M are zero): thread t < 256 takes row t / 16
+  // and float4 columns t % 16 + 16 u; row r is x[row_index[r]] when an index
+  // is given, and workgroup 0 copies the rows it read to x_out when given
+  if (tid < 16 * kRowsMax) {
     const int r = tid >> 4, q = tid & 15;
     const int kq = K / 4;
     float4 xv[KMAX / 64];
@@ -141,21 +154,24 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(
   __syncthreads();
 
   if constexpr (NORM) {
-    // rows r = wave, wave + 4, ...: the sum of squares over k = lane + 64 i in
-    // increasing i, then the wavefront sum, as rms_norm_kernel
-    // (the 4 rows of a wavefront interleaved; columns past K hold zeros)
-    float ss[4] = {0.f, 0.f, 0.f, 0.f};
+    // rows r = wave, wave + kLinWaves, ...: the sum of squares over k = lane +
+    // 64 i in increasing i, then the wavefront sum, as rms_norm_kernel (the
+    // rows of a wavefront interleaved; columns past K hold zeros)
+    constexpr int kRq = kRowsMax / kLinWaves;
+    float ss[kRq];
+#pragma unroll
+    for (int q = 0; q < kRq; ++q) ss[q] = 0.f;
 #pragma unroll
     for (int i = 0; i < KMAX / 64; ++i)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float a = xs[(wave + 4 * q) * KP + lane + 64 * i];
+      for (int q = 0; q < kRq; ++q) {
+        const float a = xs[(wave + kLinWaves * q) * KP + lane + 64 * i];
         ss[q] += a * a;
       }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kRq; ++q) {
       const float rms = sqrtf(wave_sum(ss[q]) / (float)K + eps);
-      float* row = &xs[(wave + 4 * q) * KP + lane];
+      float* row = &xs[(wave + kLinWaves * q) * KP + lane];
 #pragma unroll
       for (int i = 0; i < KMAX / 64; ++i)
         if (lane + 64 * i < K) row[64 * i] = (row[64 * i] / rms) * gw[i];
@@ -173,8 +189,8 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(
 #pragma unroll
     for (int q = 0; q < kAcc; ++q) acc4[s][q] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
   const float* arow = &xs[m * KP + kb + j];
-  // all A reads first, then the MFMA chain (the reads of steps past K / 4
-  // stay inside the row and meet zero weights)
+  // all A reads first, then the MFMA chain (the reads of steps past this
+  // wavefront's nsteps stay inside the row, below KMAX, and meet zero weights)
   float av[kSteps];
 #pragma unroll
   for (int i = 0; i < kSteps; ++i) av[i] = arow[4 * i];
@@ -200,10 +216,16 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(
 
   const int r = tid / kCols, c = tid - r * kCols;
   if (r >= M || c0 + c >= N) return;
+  // the wavefronts' partial sums in wavefront order
+  auto total = [&](int s, int e) {
+    float t = red[s][0][e];
+#pragma unroll
+    for (int q = 1; q < kLinWaves; ++q) t += red[s][q][e];
+    return t;
+  };
   float v[kSlices];
 #pragma unroll
-  for (int s = 0; s < kSlices; ++s)
-    v[s] = ((red[s][0][tid] + red[s][1][tid]) + red[s][2][tid]) + red[s][3][tid];
+  for (int s = 0; s < kSlices; ++s) v[s] = total(s, tid);
   if constexpr (MODE == 0) {
     out[(int64_t)r * ldo + c0 + c] = v[0];
   } else if constexpr (MODE == 1) {
@@ -215,7 +237,7 @@ __global__ void __launch_bounds__(256) linear_rows_kernel(
     // the pair partner of column c is c ^ 1 in the same tile (head_dim even,
     // tiles 16 columns)
     const int pt = r * kCols + (c ^ 1);
-    const float partner = ((red[0][0][pt] + red[0][1][pt]) + red[0][2][pt]) + red[0][3][pt];
+    const float partner = total(0, pt);
     const int col = c0 + c, qd = rc.nh * rc.hd, kd = rc.nkv * rc.hd;
     const int slot = rc.slots[r];
     if (col < qd + kd) {
@@ -244,11 +266,11 @@ int launch(float* out, int64_t ldo, const float* x, int64_t ldx, const float* w,
   const int grid = (N + kCols - 1) / kCols;
   if (tiles) {
     const int64_t up_off = MODE == 2 ? (int64_t)grid * K * kCols : 0;
-    linear_rows_kernel<MODE, NORM, KMAX, true><<<grid, 256, 0, st>>>(
+    linear_rows_kernel<MODE, NORM, KMAX, true><<<grid, 64 * kLinWaves, 0, st>>>(
         out, ldo, x, ldx, w, 0, up_off, norm_w, eps, M, K, N, rc, row_index, x_out);
   } else {
     const int64_t up_off = MODE == 2 ? N : 0;
-    linear_rows_kernel<MODE, NORM, KMAX, false><<<grid, 256, 0, st>>>(
+    linear_rows_kernel<MODE, NORM, KMAX, false><<<grid, 64 * kLinWaves, 0, st>>>(
         out, ldo, x, ldx, w, ldw, up_off, norm_w, eps, M, K, N, rc, row_index, x_out);
   }
   VL_CHECK_LAUNCH();
