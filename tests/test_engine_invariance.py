@@ -6,8 +6,10 @@ the reference's own, from tests/golden/small_streams.json."""
 import json
 import os
 
+import numpy as np
 import pytest
 
+from oracle.runner import NumpyRunner
 from vllmlite_amd.sequence import SamplingParams
 
 from helpers import PROMPTS, build, run
@@ -180,3 +182,62 @@ def test_fork_shares_blocks_and_copy_on_write_keeps_streams():
     assert all(engine.seqs[k].output_token_ids == want for k in kids)
     a = engine.scheduler.blocks.allocator
     assert a.num_free == a.num_blocks
+
+
+class _ArgmaxRunner(NumpyRunner):
+    """The oracle runner with the argmax entry the HIP runner offers: the same
+    rows, reduced by np.argmax; counts the steps that take it."""
+
+    def __init__(self, *a, **kw):
+        super().__init__(*a, **kw)
+        self.argmax_steps = 0
+
+    def execute_argmax(self, out):
+        logits, rows = self.execute(out)
+        self.argmax_steps += 1
+        return np.argmax(logits, axis=-1).astype(np.int32), rows
+
+
+def _streams(engine, params_list):
+    ids = [engine.add_request(p_, p) for p_, p in params_list]
+    while engine.has_work:
+        engine.step()
+    return [engine.seqs[i].output_token_ids for i in ids]
+
+
+@pytest.mark.parametrize("spec", [0, 3])
+def test_argmax_dispatch_keeps_streams(spec):
+    """Greedy steps through execute_argmax give the streams of execute() +
+    sampling, with and without draft verification."""
+    from vllmlite_amd.speculative import NgramProposer
+    rep = PROMPTS + ["abcdefgh abcdefgh abcdefgh abcdefgh abcdefgh"]
+    p = SamplingParams(max_tokens=16, temperature=0.0, ignore_eos=True)
+    out = []
+    for dev in (True, False):
+        e = build(runner_factory=_ArgmaxRunner)
+        if spec:
+            e.spec_k = spec
+            e.proposer = NgramProposer(spec)
+        e.device_argmax = dev
+        out.append(_streams(e, [(x, p) for x in rep]))
+        assert (e.runner.argmax_steps > 0) == dev
+    assert out[0] == out[1]
+
+
+def test_argmax_dispatch_falls_back_for_sampled_and_masked_rows():
+    """A step holding a sampled, a penalised or an EOS-masked (min_tokens)
+    request reads full logits rows; all-greedy steps take the argmax entry."""
+    e = build(runner_factory=_ArgmaxRunner)
+    assert e.device_argmax
+    greedy = SamplingParams(max_tokens=4, temperature=0.0, ignore_eos=True)
+    _streams(e, [("hello", greedy)])
+    assert e.runner.argmax_steps == e.total_steps
+    for p in (SamplingParams(max_tokens=4, temperature=0.8, seed=1),
+              SamplingParams(max_tokens=4, temperature=0.0, repetition_penalty=1.3),
+              SamplingParams(max_tokens=4, temperature=0.0, min_tokens=8)):
+        e = build(runner_factory=_ArgmaxRunner)
+        ref = build()
+        got = _streams(e, [("hello", greedy), ("the quick brown fox", p)])
+        want = _streams(ref, [("hello", greedy), ("the quick brown fox", p)])
+        assert got == want
+        assert e.runner.argmax_steps == 0
