@@ -35,7 +35,9 @@ extern "C" {
 #define VL_LINEAR_SWIGLU 2     /* out = silu(f(x) @ W[:, :n]) * (f(x) @ W[:, n:2n]) */
 #define VL_LINEAR_TILES16 16   /* flag ORed into the mode: W in 16-column tiles */
 #define VL_WEIGHT_ROWS 0       /* a projection weight [k, n] row-major at a row stride */
-#define VL_WEIGHT_TILES16 1    /* ... as 16-column tiles [ceil(n/16), k, 16], zero past n */
+#define VL_WEIGHT_TILES16 1    /* ... as 16-column tiles [ceil(n/16), k, 16], zero past n;
+                                  inside a tile, element (k, m) with k = 16g + 4s + j
+                                  at flat position 256g + 4(16j + m) + s */
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* vl_last_error(void);
@@ -172,8 +174,9 @@ int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_out, float*
  * rows, runner.py:90), else x[r]. W [k, n] (or [k, 2n]) row-major with row
  * stride weight_stride, or, with VL_LINEAR_TILES16 ORed into mode, as
  * 16-column tiles [ceil(n/16), k, 16] (zero past column n; SwiGLU: the gate
- * tiles, then the up tiles; weight_stride unused), which loads in whole cache
- * lines. out [rows, n]; out must not overlap x. rows <= 16, k a multiple of
+ * tiles, then the up tiles; weight_stride unused; 16-byte aligned; inside a
+ * tile element (k, m), k = 16g + 4s + j, at flat position 256g + 4(16j + m) +
+ * s, so each lane's operands of 4 MFMA steps are one 16-byte load). out [rows, n]; out must not overlap x. rows <= 16, k a multiple of
  * 16, k <= 1024. fp32 throughout.
  */
 int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_stride,

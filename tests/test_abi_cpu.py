@@ -71,3 +71,24 @@ def test_engine_default_backend_is_the_hip_runner():
         pytest.skip("a GPU is visible")
     with pytest.raises(RuntimeError):
         make_runner(EngineConfig())
+
+
+def test_tile16_layout():
+    """Tiled projection weights: element (k, m) of tile t, k = 16 g + 4 s + j,
+    at flat position 256 g + 4 (16 j + m) + s; columns past n zero; with
+    halves 2 the gate tiles precede the up tiles."""
+    import torch
+    from vllmlite_amd.ops import tile16
+    k, n = 48, 20
+    w = torch.arange(k * 2 * n, dtype=torch.float32).reshape(k, 2 * n)
+    t = tile16(w, halves=2)
+    assert t.shape == (4, k, 16)
+    flat = t.reshape(4, -1)
+    for h in range(2):
+        for tt in range(2):
+            for kk in range(k):
+                g, s, j = kk // 16, (kk % 16) // 4, kk % 4
+                for m in range(16):
+                    col = tt * 16 + m
+                    want = w[kk, h * n + col].item() if col < n else 0.0
+                    assert flat[2 * h + tt, 256 * g + 4 * (16 * j + m) + s].item() == want

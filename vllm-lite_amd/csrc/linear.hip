@@ -12,10 +12,12 @@
 //
 // Weights come row-major ([k, n] at a row stride) or as 16-column tiles
 // ([ceil(n/16), k, 16], the columns past n zero): a workgroup's 16 columns
-// are then one contiguous k x 64-byte run, which it reads in whole 128-byte
-// lines (row-major, every k row is a separate 64-byte piece). These kernels
-// run on few workgroups, where the number of cache lines each one requests
-// sets the time.
+// are then one contiguous k x 64-byte run, ordered inside so that a lane's
+// B operands of 4 consecutive MFMA steps are adjacent (element (k, m), k =
+// 16 g + 4 s + j, at 256 g + 4 (16 j + m) + s): a wavefront reads 1 KB per
+// 16-byte load instruction (row-major, every k row is a separate 64-byte
+// piece read 4 bytes per lane). These kernels run on few workgroups, where
+// the number of requests each one issues sets the time.
 #include "vl_common.h"
 
 namespace {
@@ -81,6 +83,7 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
   constexpr int KP = KMAX + 4;  // xs row stride: rows 4 words apart, so the
                                 // 16 rows x 4 k of an A read hit 64 banks
   constexpr int kSteps = KMAX / (4 * kLinWaves);  // 16x16x4 steps per wavefront at K = KMAX
+  static_assert(kSteps % 4 == 0, "whole groups of 4 steps");
   __shared__ float xs[kRowsMax * KP];
   __shared__ float red[kSlices][kLinWaves][kRowsMax * kCols];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -88,7 +91,8 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
   const int m = lane & 15, j = lane >> 4;
   // wavefront w takes the spw steps of 4 k from step w spw (k in [kb, kb + 4
   // nsteps)); the last wavefronts may have fewer steps, or none
-  const int spw = (K / 4 + kLinWaves - 1) / kLinWaves;
+  // (spw is a multiple of 4: the tiled weights hold 4 steps per 16-byte load)
+  const int spw = ((K / 4 + kLinWaves - 1) / kLinWaves + 3) / 4 * 4;
   const int kb = wave * spw * 4;
   const int nsteps = max(0, min(spw, K / 4 - wave * spw));
 
@@ -104,14 +108,22 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
 #pragma unroll
   for (int s = 0; s < kSlices; ++s) {
     if constexpr (TILES) {
-      // tile blockIdx.x: element (k, m) at k * 16 + m; a wavefront's 64 lanes
-      // read 4 consecutive k rows, 256 contiguous bytes
-      // (k rows clamped to K - 4 + j < K)
-      const float* src = w + (s ? up_off : 0) + (int64_t)blockIdx.x * K * kCols + m;
+      // tile blockIdx.x: element (k, m), k = 16 g + 4 s + j, at 256 g + 4 (16 j
+      // + m) + s, so lane l's operands of the 4 steps of group g are one
+      // float4 and a wavefront reads 1 KB per load (groups clamped below K / 16;
+      // kb and nsteps are multiples of 16 and 4)
+      const float4* src = reinterpret_cast<const float4*>(w + (s ? up_off : 0) +
+                                                          (int64_t)blockIdx.x * K * kCols) +
+                          lane;
 #pragma unroll
-      for (int i = 0; i < kSteps; ++i)
-        wb[s][i] = src[(int64_t)min(kb + 4 * i, K - 4) * kCols + j * kCols] *
-                   (i < nsteps ? colmask : 0.f);
+      for (int g = 0; g < kSteps / 4; ++g) {
+        const float4 v = src[(int64_t)min(kb / 16 + g, K / 16 - 1) * 64];
+        const float z = 4 * g < nsteps ? colmask : 0.f;
+        wb[s][4 * g] = v.x * z;
+        wb[s][4 * g + 1] = v.y * z;
+        wb[s][4 * g + 2] = v.z * z;
+        wb[s][4 * g + 3] = v.w * z;
+      }
     } else {
       const float* src = w + (s ? up_off : 0) + min(c0 + m, N - 1);
 #pragma unroll
@@ -296,6 +308,7 @@ extern "C" int vl_linear_rows(float* out, int64_t out_stride, const float* x, in
   VL_CHECK_ARG(x_stride >= k && out_stride >= n, "row strides too small");
   const int64_t wcols = mode == VL_LINEAR_SWIGLU ? 2 * (int64_t)n : n;
   VL_CHECK_ARG(tiles || weight_stride >= wcols, "weight row stride too small");
+  VL_CHECK_ARG(!tiles || (((uintptr_t)weight) & 15) == 0, "tiled weight must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   const bool nrm = norm_weight != nullptr;
   // KMAX, the unrolled depth, is the smallest of 384 / 512 / 1024 that holds k
@@ -340,6 +353,7 @@ extern "C" int vl_qkv_rope_cache(float* q_out, float* key_cache, float* value_ca
                "bad weight layout %d", weight_layout);
   const bool tiles = weight_layout == VL_WEIGHT_TILES16;
   VL_CHECK_ARG(tiles || weight_stride >= n, "weight row stride too small");
+  VL_CHECK_ARG(!tiles || (((uintptr_t)weight) & 15) == 0, "tiled weight must be 16-byte aligned");
   RopeCache rc;
   rc.q_out = q_out, rc.kc = key_cache, rc.vc = value_cache, rc.positions = positions;
   rc.slots = slot_mapping, rc.cos_t = cos_table, rc.sin_t = sin_table;

@@ -257,17 +257,22 @@ LINEAR_ROWS_MAX = 16
 
 
 def tile16(w: torch.Tensor, halves: int = 1) -> torch.Tensor:
-    """A [k, halves * n] weight as 16-column tiles [halves * ceil(n/16), k, 16]
-    (zero past column n; with halves 2, the tiles of w[:, :n] then those of
-    w[:, n:], the SwiGLU gate and up halves)."""
+    """A [k, halves * n] weight (k a multiple of 16) as 16-column tiles
+    [halves * ceil(n/16), k, 16] (zero past column n; with halves 2, the tiles
+    of w[:, :n] then those of w[:, n:], the SwiGLU gate and up halves). Inside
+    a tile, element (k, m) with k = 16 g + 4 s + j sits at flat position
+    256 g + 4 (16 j + m) + s."""
     k, cols = w.shape
+    _need(k % 16 == 0, "k must be a multiple of 16")
     n = cols // halves
     nt = -(-n // 16)
     parts = []
     for h in range(halves):
         p = torch.zeros(k, nt * 16, dtype=w.dtype, device=w.device)
         p[:, :n] = w[:, h * n:(h + 1) * n]
-        parts.append(p.view(k, nt, 16).permute(1, 0, 2))
+        t = p.view(k, nt, 16).permute(1, 0, 2)  # [nt, k, 16]: (k, m)
+        t = t.reshape(nt, k // 16, 4, 4, 16).permute(0, 1, 3, 4, 2)  # (g, s, j, m) -> (g, j, m, s)
+        parts.append(t.reshape(nt, k, 16))
     return torch.cat(parts).contiguous()
 
 
