@@ -12,7 +12,6 @@ Contents, each citing the reference file:line it restates:
   greedy.py     verify / greedy argmax               (vllmlite/speculative.py:86-100,
                                                       vllmlite/sampling.py:56-57)
   dense.py      the textbook dense attention checker (tests/test_attention.py:13-30)
-  workload.py   the bench request generator          (bench/bench.py:35-47)
 
 How each function is pinned (tests/test_oracle_*.py):
   gather_slots / write_kv / CoW: the known answer [12,13,14,15,0,1]
@@ -23,9 +22,11 @@ How each function is pinned (tests/test_oracle_*.py):
   apply_rope / build_rope: position-0 identity and position dependence
       (tests/test_attention.py:65-77), norm preservation, and a 2x2 rotation
       built independently with math.cos/math.sin.
-  rms_norm / silu: closed forms (unit RMS, silu(0)=0, odd-part identity).
+  rms_norm / silu: closed forms (tests/test_oracle_model.py: a known answer,
+      unit RMS, scale invariance, the eps term, silu(0)=0, silu(1), the
+      odd-part identity silu(x) - silu(-x) = x).
   verify: the reference's known answers (tests/test_speculative.py:36-60).
-  workload + scheduler: the published totals 3025/3179 tokens and 260 steps
+  the package's workload generator + the caller side: the published totals 3025/3179 tokens and 260 steps
       (results/mixed_lengths.json:22-23,88) and 14480/3323, 281/280 steps
       (results/shared_prefix.json).
   forward / seeded weights / end-to-end greedy streams: golden fixtures written

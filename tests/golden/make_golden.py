@@ -14,7 +14,20 @@ Outputs (small JSON, committed):
   weights_sha256.json sha256 of every weight tensor for that model config and
                       for the small invariance-test config;
   small_streams.json  greedy streams of the 4 invariance prompts on the small
-                      engine (2 layers, d 64, H4/Hkv2, d_ff 128).
+                      engine (2 layers, d 64, H4/Hkv2, d_ff 128);
+  shared_prefix_streams.json
+                      the 48-request mix behind a 256-token shared system
+                      prompt (bench/bench.py:35-47 with shared_prefix 256,
+                      max_len 768, 768 blocks, prefix cache on): greedy
+                      streams and step count ("plain"), and the same mix with
+                      every request forked once, right after its first token,
+                      through the reference's BlockManager.fork
+                      (vllmlite/block_manager.py:133-137) so that the first
+                      write into each shared partial tail block emits a
+                      copy-on-write pair (block_manager.py:74-85): streams of
+                      parents and children, step count, and the number of CoW
+                      pairs with the prompt lengths whose tails were partial
+                      ("forked").
 """
 
 from __future__ import annotations
@@ -31,9 +44,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, REF)
 
 from vllmlite.config import CacheConfig, EngineConfig, ModelConfig, SchedulerConfig  # noqa: E402
-from vllmlite.engine import LLMEngine  # noqa: E402
+from vllmlite.engine import LLMEngine, _Detok  # noqa: E402
 from vllmlite.model import Layer, TinyLlama  # noqa: E402
-from vllmlite.sequence import SamplingParams  # noqa: E402
+from vllmlite.sequence import SamplingParams, Sequence  # noqa: E402
 from bench.bench import make_workload  # noqa: E402
 
 
@@ -78,6 +91,82 @@ def run_with_margins(engine, reqs):
     return margins
 
 
+def fork_child(engine, parent, child_id):
+    """A running copy of `parent` that shares all of its blocks, partial tail
+    included, made with the reference's own BlockManager.fork. The child
+    joins the running list after its parent's peers; its stream continues
+    from the parent's state."""
+    child = Sequence(child_id, list(parent.prompt_token_ids), parent.params)
+    child.output_token_ids = list(parent.output_token_ids)
+    child.num_computed = parent.num_computed
+    child.status = parent.status
+    engine.scheduler.blocks.fork(parent, child)
+    engine.scheduler.blocks.live_tokens += child.table.num_filled
+    engine.scheduler.running.append(child)
+    engine.seqs[child_id] = child
+    engine.detok[child_id] = _Detok(engine.detok[parent.request_id].text,
+                                    engine.detok[parent.request_id].consumed)
+    engine.rngs[child_id] = np.random.default_rng(parent.params.seed)
+    return child
+
+
+def shared_prefix_runs():
+    mc = ModelConfig(n_layers=6, n_heads=8, n_kv_heads=4, d_model=384, d_ff=1024,
+                     vocab_size=261, max_seq_len=768)
+    reqs = make_workload(48, np.random.default_rng(0), 16, 256, 16, 192, 256)
+    out = {"prompts": {rid: [int(t) for t in ids] for rid, ids, _ in reqs},
+           "max_tokens": {rid: int(p.max_tokens) for rid, _, p in reqs}}
+
+    def engine():
+        return LLMEngine(EngineConfig(
+            model=mc, cache=CacheConfig(block_size=16, num_blocks=768, enable_prefix_caching=True),
+            scheduler=SchedulerConfig(max_seqs=16, max_batched_tokens=1024)))
+
+    eng = engine()
+    for rid, ids, params in reqs:
+        eng.add_request(params=params, request_id=rid, prompt_token_ids=ids)
+    while eng.has_work:
+        eng.step()
+    st = eng.stats()
+    out["plain"] = {"steps": eng.total_steps,
+                    "output_tokens": eng.total_output_tokens,
+                    "prefix_hit_rate": round(st["prefix_hit_rate"], 6),
+                    "streams": {rid: [int(t) for t in eng.seqs[rid].output_token_ids]
+                                for rid, _, _ in reqs}}
+
+    eng = engine()
+    pairs = []
+    real_execute = eng.runner.execute
+
+    def execute(sched):
+        pairs.extend((int(a), int(b)) for a, b in sched.cow)
+        return real_execute(sched)
+
+    eng.runner.execute = execute
+    for rid, ids, params in reqs:
+        eng.add_request(params=params, request_id=rid, prompt_token_ids=ids)
+    forked, partial = set(), []
+    while eng.has_work:
+        eng.step()
+        for seq in list(eng.scheduler.running):
+            rid = seq.request_id
+            if rid in forked or rid.endswith(".c") or len(seq.output_token_ids) != 1:
+                continue
+            forked.add(rid)
+            if seq.table.num_filled % 16:
+                partial.append(rid)
+            fork_child(eng, seq, rid + ".c")
+    out["forked"] = {"steps": eng.total_steps,
+                     "output_tokens": eng.total_output_tokens,
+                     "cow_pairs": len(pairs),
+                     "forked": sorted(forked, key=lambda r: int(r[1:])),
+                     "partial_tails": partial,
+                     "preemptions": eng.scheduler.total_preemptions,
+                     "streams": {rid: [int(t) for t in s.output_token_ids]
+                                 for rid, s in eng.seqs.items()}}
+    return out
+
+
 def main():
     mc = ModelConfig(n_layers=6, n_heads=8, n_kv_heads=4, d_model=384, d_ff=1024,
                      vocab_size=261, max_seq_len=512)
@@ -109,6 +198,12 @@ def main():
     with open(os.path.join(HERE, "small_streams.json"), "w") as f:
         json.dump({"prompts": prompts4, "max_tokens": 20,
                    "streams": [e2.seqs[i].output_token_ids for i in ids]}, f)
+    sp = shared_prefix_runs()
+    with open(os.path.join(HERE, "shared_prefix_streams.json"), "w") as f:
+        json.dump(sp, f)
+    print("shared prefix: plain", sp["plain"]["steps"], "steps,", sp["plain"]["output_tokens"],
+          "tokens; forked", sp["forked"]["steps"], "steps,", sp["forked"]["cow_pairs"], "CoW pairs,",
+          sp["forked"]["preemptions"], "preemptions")
     print("wrote fixtures; cfg0 steps", eng.total_steps,
           "min margin", min(min(v) for v in margins.values() if v))
 

@@ -83,3 +83,50 @@ def test_shared_prefix_step_counts():
     eng, _ = _drive(True, 256)
     st = eng.stats()
     assert (st["steps"], round(st["slot_utilization"], 3), st["prefix_hit_rate"]) == (280, 0.629, 1.0)
+
+
+def _cfg3(prefix_cache=True):
+    from vllmlite_amd.workload import shared_prefix_config
+    cfg = shared_prefix_config(prefix_cache)
+    return LLMEngine(cfg, runner=NumpyRunner(cfg.model, cfg.cache))
+
+
+def test_shared_prefix_mix_matches_reference_streams():
+    """The published shared-prefix configuration (max_len 768, 768 blocks,
+    prefix cache on): 280 steps and the reference's 3323-token streams."""
+    g = _load("shared_prefix_streams.json")
+    eng = _cfg3()
+    reqs = mixed_lengths(0, 48, 256)
+    for rid, ids, p in reqs:
+        assert ids == g["prompts"][rid]
+        eng.add_request(params=p, request_id=rid, prompt_token_ids=ids)
+    while eng.has_work:
+        eng.step()
+    assert eng.total_steps == g["plain"]["steps"] == 280
+    assert eng.total_output_tokens == g["plain"]["output_tokens"] == 3323
+    for rid, _, _ in reqs:
+        assert eng.seqs[rid].output_token_ids == g["plain"]["streams"][rid], rid
+
+
+def test_forked_shared_prefix_mix_matches_reference():
+    """Every request forked once after its first token (BlockManager.fork,
+    vllmlite/block_manager.py:133-137): the reference's step count, copy-on-
+    write pair count (one per partial shared tail) and every stream, parents
+    and children."""
+    from vllmlite_amd.workload import drive_forked
+    g = _load("shared_prefix_streams.json")["forked"]
+    eng = _cfg3()
+    pairs = []
+    execute = eng.runner.execute
+
+    def counting(out):
+        pairs.extend(out.cow)
+        return execute(out)
+
+    eng.runner.execute = counting
+    forked, partial = drive_forked(eng, mixed_lengths(0, 48, 256))
+    assert sorted(forked) == sorted(g["forked"]) and partial == g["partial_tails"]
+    assert len(pairs) == g["cow_pairs"] == len(partial) == 44
+    assert eng.total_steps == g["steps"]
+    assert eng.total_output_tokens == g["output_tokens"]
+    assert {rid: s.output_token_ids for rid, s in eng.seqs.items()} == g["streams"]

@@ -1,8 +1,9 @@
 """GPU parity of every kernel against the oracle, through the C ABI.
 
 Bars: copies and scatters bit-exact; fp32 attention rtol 1e-4 / atol 1e-5
-(the reference's own tolerance, tests/test_attention.py:57); bf16 attention
-rtol/atol 2e-2 against fp32 oracle math on bf16-rounded inputs; argmax and
+(the reference's own tolerance, tests/test_attention.py:57) and every (token,
+head) row within 1e-4 normwise; bf16 attention every row within 2e-2 normwise
+against fp32 oracle math on bf16-rounded inputs (tests/parity.py); argmax and
 greedy acceptance exact.
 """
 
@@ -12,6 +13,7 @@ import pytest
 torch = pytest.importorskip("torch")
 
 from batches import bf16_round, make_batch, oracle_attention  # noqa: E402
+from parity import BF16_ROW_REL, F32_ROW_REL, assert_rows_close  # noqa: E402
 
 pytestmark = pytest.mark.gpu
 
@@ -57,8 +59,9 @@ def check(got, want, dtype):
     assert np.isfinite(got).all()
     if dtype == "f32":
         np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
+        assert_rows_close(got, want, F32_ROW_REL)
     else:
-        np.testing.assert_allclose(got, want, rtol=2e-2, atol=2e-2)
+        assert_rows_close(got, want, BF16_ROW_REL)
 
 
 # -- the reference's grid (tests/test_attention.py:33-57), one sequence per launch
@@ -353,3 +356,77 @@ def test_bandwidth_decode_split_merge_across_repeated_runs():
         out = torch.empty_like(q)
         o.paged_attention_run(out, q, kc, vc, bt, sl, qsl, b["scale"], 16, ws, max_query_len=1)
         check(to_np(out), expected(b, "bf16"), "bf16")
+
+
+# -- closed forms at forced multi-partition splits ----------------------------
+def _plan_header(ws):
+    """The plan's first 16 int32 of the workspace: [2] the tile partition
+    length, [3] the split partial rows written, [7] the decode range length."""
+    torch.cuda.synchronize()
+    return ws[:64].view(torch.int32).cpu().numpy()
+
+
+def _closed_form_batch(seqs, H, Hkv, D, seed, dominant):
+    """Q/K/V of a batch whose exact attention is known without the oracle.
+    dominant=False: every key of a KV head is the same vector, so each query
+    attends uniformly and its output is the mean of V over its causal keys.
+    dominant=True: every query row of KV group g is the same vector u_g and
+    one key per sequence (at 0.6 of the context, inside a middle partition)
+    is 40 u_g / |u_g|, a score ~40 above the N(0,1) others, so the output is
+    that key's V row."""
+    b = make_batch(seqs, H, Hkv, D, 16, seed=seed)
+    rng = np.random.default_rng(seed + 1)
+    rep = H // Hkv
+    kc = b["k_cache"]
+    q = b["q"]
+    star = []
+    for i, t in enumerate(b["tables"]):
+        ctx = int(b["seq_lens"][i])
+        slots = (t[:, None].astype(np.int64) * 16 + np.arange(16)[None, :]).reshape(-1)[:ctx]
+        q0, q1 = b["qsl"][i], b["qsl"][i + 1]
+        if not dominant:
+            kc[slots] = bf16_round(rng.standard_normal((1, Hkv, D)).astype(np.float32))
+            star.append(None)
+        else:
+            u = bf16_round(rng.standard_normal((Hkv, D)).astype(np.float32))
+            q[q0:q1] = np.repeat(u, rep, axis=0)[None]
+            j = int(0.6 * ctx)
+            kc[slots[j]] = bf16_round(40.0 * u / np.linalg.norm(u, axis=1, keepdims=True))
+            star.append(j)
+    for name in ("q", "k_cache", "v_cache"):
+        b[name] = bf16_round(b[name])
+    want = np.zeros_like(b["q"])
+    for i, t in enumerate(b["tables"]):
+        ctx = int(b["seq_lens"][i])
+        slots = (t[:, None].astype(np.int64) * 16 + np.arange(16)[None, :]).reshape(-1)[:ctx]
+        q0, q1 = b["qsl"][i], b["qsl"][i + 1]
+        vv = b["v_cache"][slots].astype(np.float64)              # [ctx, Hkv, D]
+        for j in range(q1 - q0):
+            pos = ctx - (q1 - q0) + j
+            row = vv[star[i]] if dominant else vv[:pos + 1].mean(axis=0)   # [Hkv, D]
+            want[q0 + j] = np.repeat(row, rep, axis=0)
+    return b, want
+
+
+@pytest.mark.parametrize("dominant", [False, True])
+@pytest.mark.parametrize("q_len", [1, 5])
+def test_closed_forms_at_forced_splits(dominant, q_len):
+    """Contexts of 32768 and 8192 keys split into many partitions (the header
+    of the plan shows partition / range lengths far below the context and
+    split rows written), merged by the decode kernel's last arriver (q_len 1)
+    or the combine kernel (q_len 5): uniform attention gives the mean of V,
+    a dominant key gives its V, every row within 2e-2 normwise."""
+    o = ops()
+    seqs = [(q_len, 32768), (q_len, 8192), (q_len, 20000)]
+    b, want = _closed_form_batch(seqs, 32, 8, 128, 60 + q_len, dominant)
+    q = dev(b["q"], torch.bfloat16)
+    kc, vc = dev(b["k_cache"], torch.bfloat16), dev(b["v_cache"], torch.bfloat16)
+    out = torch.empty_like(q)
+    S, T = len(seqs), q.shape[0]
+    ws = o.AttentionWorkspace().get(o.paged_attention_workspace_size(S, T, 32, 128, 32768))
+    o.paged_attention(out, q, kc, vc, dev(b["block_tables"]), dev(b["seq_lens"]), dev(b["qsl"]),
+                      b["scale"], 16, ws, max_query_len=q_len)
+    hdr = _plan_header(ws)
+    split_len = hdr[7] if q_len == 1 else hdr[2]
+    assert hdr[3] > 0 and split_len <= 8192 // 4, f"no forced split: header {hdr[:13]}"
+    assert_rows_close(to_np(out), want, BF16_ROW_REL, f"q_len {q_len} dominant {dominant}")

@@ -112,16 +112,37 @@ def test_chunked_prefill_does_not_change_output(max_batched):
     assert run(hip_engine(max_batched=max_batched), PROMPTS) == small_reference()
 
 
-@pytest.mark.parametrize("max_seqs", [1, 3])
+def test_no_chunked_prefill_matches():
+    assert run(hip_engine(chunked=False, max_batched=4096), PROMPTS) == small_reference()
+
+
+@pytest.mark.parametrize("max_seqs", [1, 2, 3, 8])
 def test_batch_composition_does_not_change_output(max_seqs):
     assert run(hip_engine(max_seqs=max_seqs), PROMPTS) == small_reference()
 
 
-def test_preemption_preserves_output():
-    engine = hip_engine(block_size=4, num_blocks=24, max_seqs=8, prefix_cache=True)
+def test_single_request_matches_batched():
+    from vllmlite_amd.hip_runner import HipRunner
+    cfg = small_cfg()
+    runner = HipRunner(cfg.model, cfg.cache)  # one runner (and its graphs) for every engine
+    solo = [run(LLMEngine(cfg, runner=runner), [p])[0] for p in PROMPTS]
+    assert solo == small_reference()
+
+
+@pytest.mark.parametrize("prefix_cache", [False, True])
+def test_preemption_preserves_output(prefix_cache):
+    engine = hip_engine(block_size=4, num_blocks=24, max_seqs=8, prefix_cache=prefix_cache)
     got = run(engine, PROMPTS, check_counts=True)
     assert engine.scheduler.total_preemptions > 0
     assert got == small_reference()
+
+
+@pytest.mark.parametrize("k", [1, 2, 4, 8])
+def test_speculation_does_not_change_the_output(k):
+    e = hip_engine()
+    e.spec_k = k
+    e.proposer = NgramProposer(k)
+    assert run(e, PROMPTS) == small_reference()
 
 
 @pytest.mark.parametrize("k", [1, 4])
@@ -213,3 +234,53 @@ def test_copy_on_write_fork_matches_oracle_runner():
         assert cows, "no copy-on-write pair was scheduled"
         outs.append([eng.seqs[r].output_token_ids for r in [rid] + kids])
     assert outs[0] == outs[1]
+
+
+def _cfg3_engine(fork_counts=None):
+    from vllmlite_amd.hip_runner import HipRunner
+    from vllmlite_amd.workload import shared_prefix_config
+    cfg = shared_prefix_config(True)
+    eng = LLMEngine(cfg, runner=HipRunner(cfg.model, cfg.cache))
+    if fork_counts is not None:
+        for name in ("execute", "execute_argmax"):
+            real = getattr(eng.runner, name)
+
+            def counting(out, real=real):
+                fork_counts.extend(out.cow)
+                return real(out)
+
+            setattr(eng.runner, name, counting)
+    return eng
+
+
+def test_shared_prefix_mix_matches_reference_streams():
+    """48 requests behind a 256-token system prompt with the prefix cache on
+    (prefill skips the cached blocks): the reference's 280 steps and streams."""
+    g = _gold("shared_prefix_streams.json")
+    eng = _cfg3_engine()
+    reqs = mixed_lengths(0, 48, 256)
+    for rid, ids, p in reqs:
+        eng.add_request(params=p, request_id=rid, prompt_token_ids=ids)
+    while eng.has_work:
+        eng.step()
+    assert eng.total_steps == g["plain"]["steps"] == 280
+    same = sum(eng.seqs[rid].output_token_ids == g["plain"]["streams"][rid] for rid, _, _ in reqs)
+    assert same == 48
+
+
+def test_forked_shared_prefix_copy_on_write_matches_reference():
+    """The same mix with every request forked after its first token: 44
+    copy-on-write pairs (one per partial shared tail, 4 prompts end on a block
+    boundary) run through vl_copy_blocks, and every parent's and child's
+    stream, the step count and the pair count equal the reference's."""
+    from vllmlite_amd.workload import drive_forked
+    g = _gold("shared_prefix_streams.json")["forked"]
+    pairs = []
+    eng = _cfg3_engine(pairs)
+    forked, partial = drive_forked(eng, mixed_lengths(0, 48, 256))
+    assert partial == g["partial_tails"] and len(pairs) == g["cow_pairs"] == 44
+    assert eng.total_steps == g["steps"]
+    got = {rid: s.output_token_ids for rid, s in eng.seqs.items()}
+    assert sorted(got) == sorted(g["streams"])
+    bad = [rid for rid in got if got[rid] != g["streams"][rid]]
+    assert not bad, f"streams differ: {bad[:5]}"

@@ -1,9 +1,10 @@
 """The benchmark workloads at full size on the GPU, checked against the oracle.
 
 Each builds the batch in a 2^17-block pool (8.6 GB of bf16 K/V, unowned slots
-NaN), runs the step through the C ABI and compares sequences with the oracle's
-per-sequence paged_attention (vllmlite/attention.py:59-98) on fp32 copies of
-the same bf16 values; bf16 bar 2e-2. The K/V scatter is checked bit-exact.
+NaN), runs the step through the C ABI and compares EVERY sequence with the
+oracle's per-sequence paged_attention (vllmlite/attention.py:59-98) on fp32
+copies of the same bf16 values, each (token, head) row within 2e-2 normwise
+(tests/parity.py). The K/V scatter is checked bit-exact.
 """
 
 import numpy as np
@@ -11,8 +12,9 @@ import pytest
 
 torch = pytest.importorskip("torch")
 
+from parity import BF16_ROW_REL, assert_rows_close  # noqa: E402
+
 pytestmark = pytest.mark.gpu
-TOL = 2e-2
 
 
 def _mods():
@@ -46,53 +48,48 @@ def _step(ops, syn, b, scatter=True):
     return out
 
 
-def _check(b, out, idx):
-    for i in idx:
+def _check(b, out, idx=None):
+    """Sequences idx (default: all) against the oracle; returns the worst row error."""
+    worst = 0.0
+    for i in (range(len(b["seqs"])) if idx is None else idx):
         q0, q1 = b["qsl_np"][i], b["qsl_np"][i + 1]
         got = out[q0:q1].float().cpu().numpy()
-        assert np.isfinite(got).all(), f"sequence {i}: non-finite output"
-        np.testing.assert_allclose(got, _oracle_rows(b, i), rtol=TOL, atol=TOL,
-                                   err_msg=f"sequence {i} (q={b['q_lens'][i]}, ctx={b['ctx'][i]})")
+        worst = max(worst, assert_rows_close(
+            got, _oracle_rows(b, i), BF16_ROW_REL,
+            f"sequence {i} (q={b['q_lens'][i]}, ctx={b['ctx'][i]})"))
+    return worst
 
 
 def test_mixed_8392_step_scatter_and_attention():
     """16 chunks x 512 tokens after 0-2048 cached tokens plus 200 decodes with
-    128-4096 tokens, one scatter and one attention call: every chunk and 24
-    decodes against the oracle, the scatter bit-exact."""
+    128-4096 tokens, one scatter and one attention call: every sequence
+    against the oracle, the scatter bit-exact."""
     ops, syn = _mods()
     b = syn.build(torch, syn.mixed_8392_seqs(0), seed=2)
     out = _step(ops, syn, b)
     sm = b["slot_mapping"].long()
     assert torch.equal(b["kc"][sm], b["knew"]) and torch.equal(b["vc"][sm], b["vnew"])
-    S = len(b["seqs"])
-    _check(b, out, list(range(200, S)) + list(np.linspace(0, 199, 24).astype(int)))
+    print("worst row error", _check(b, out))
     del b, out
     torch.cuda.empty_cache()
 
 
 def test_verify_64x5_step():
-    """64 sequences x 5 query positions over 1024-32768 cached tokens: the
-    longest, the shortest and 6 more against the oracle."""
+    """64 sequences x 5 query positions over 1024-32768 cached tokens: every
+    sequence against the oracle."""
     ops, syn = _mods()
     b = syn.build(torch, syn.verify_64x5_seqs(0), seed=3)
     out = _step(ops, syn, b)
-    ctx = b["ctx"]
-    idx = sorted({int(np.argmax(ctx)), int(np.argmin(ctx))} |
-                 set(np.linspace(0, len(ctx) - 1, 6).astype(int).tolist()))
-    _check(b, out, idx)
+    print("worst row error", _check(b, out))
     del b, out
     torch.cuda.empty_cache()
 
 
 def test_decode_256_step():
-    """The headline decode batch: the longest, the shortest and 14 more
-    sequences against the oracle."""
+    """The headline decode batch: all 256 sequences against the oracle."""
     ops, syn = _mods()
     b = syn.build(torch, syn.decode_256_seqs(0), seed=0)
     out = _step(ops, syn, b)
-    ctx = b["ctx"]
-    idx = sorted({int(np.argmax(ctx)), int(np.argmin(ctx))} |
-                 set(np.linspace(0, len(ctx) - 1, 14).astype(int).tolist()))
-    _check(b, out, idx)
+    print("worst row error", _check(b, out))
     del b, out
     torch.cuda.empty_cache()

@@ -18,10 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.normpath(os.path.join(HERE, "..", "csrc"))
 INCLUDE = os.path.normpath(os.path.join(HERE, "..", "..", "include"))
 LIB_DIR = os.path.join(HERE, "lib")
-DEFAULT_LIB_PATH = os.path.join(LIB_DIR, "libvllmlite_hip.so")
-# another build of the same sources (e.g. compiled with different -D tuning
-# constants) can be loaded instead by naming it in VLLMLITE_HIP_LIB
-LIB_PATH = os.environ.get("VLLMLITE_HIP_LIB") or DEFAULT_LIB_PATH
+LIB_PATH = os.path.join(LIB_DIR, "libvllmlite_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 HIP_FLAGS = [
@@ -35,7 +32,7 @@ def sources():
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
 
-def build(verbose: bool = False, out: str = DEFAULT_LIB_PATH, defines=()) -> str:
+def build(verbose: bool = False, out: str = LIB_PATH, defines=()) -> str:
     os.makedirs(os.path.dirname(out), exist_ok=True)
     tmp = out + ".tmp"
     cmd = [HIPCC, *HIP_FLAGS, *[f"-D{d}" for d in defines], "-I", INCLUDE, "-I", CSRC,

@@ -106,6 +106,13 @@ class LLMEngine:
         self.rngs[child_id] = np.random.default_rng(parent.params.seed)
         return child_id
 
+    def just_started(self, child_suffix: str):
+        """(request id, KV tokens written) of every running request, in running
+        order, that has emitted exactly one token and is not itself a fork
+        (id ending in child_suffix)."""
+        return [(s.request_id, s.table.num_filled) for s in self.scheduler.running
+                if len(s.output_token_ids) == 1 and not s.request_id.endswith(child_suffix)]
+
     def release(self, request_id: str) -> None:
         self.seqs.pop(request_id, None)
         self.detok.pop(request_id, None)

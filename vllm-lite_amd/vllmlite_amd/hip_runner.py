@@ -52,6 +52,79 @@ def _bucket(n: int, floor: int) -> int:
     return b
 
 
+class Flattened:
+    """One step's ragged batch as plain int lists, in schedule order."""
+
+    __slots__ = ("toks", "pos", "slots", "lidx", "qsl", "lens", "tables", "rows", "T", "S",
+                 "R", "width")
+
+
+def flatten_scheduled(out, block_size: int, max_seq_len: int) -> Flattened:
+    """SchedulerOutput -> Flattened (vllmlite/runner.py:62-100), reading only
+    the fields the reference runner reads: `item.start_pos` and
+    `item.num_tokens` of each scheduled item (scheduler.py:23-30),
+    `seq.token_ids[start:start + n]`, `seq.draft_token_ids` and
+    `seq.table.block_ids` (sequence.py:49-94, block.py:120-156). A sequence
+    object may offer `token_slice(start, stop)` to skip building the whole
+    token list. Sequence i contributes positions start..start+n-1, slots
+    block_ids[p // bs] * bs + p % bs (block.py:154-156) and the last
+    min(1 + drafts, n) token rows as logits rows (runner.py:86-90)."""
+    bs = block_size
+    f = Flattened()
+    toks: List[int] = []
+    pos: List[int] = []
+    slots: List[int] = []
+    lidx: List[int] = []
+    qsl: List[int] = [0]
+    lens: List[int] = []
+    rows: List[Tuple[int, int]] = []
+    tables = []
+    T = R = 0
+    width = 1
+    for item in out.scheduled:
+        seq = item.seq
+        st, n = item.start_pos, item.num_tokens
+        ids = seq.table.block_ids
+        nb = len(ids)
+        end = st + n
+        if end > nb * bs:
+            raise ValueError(f"sequence {seq.request_id}: {end} tokens but only {nb} blocks")
+        if end > max_seq_len:
+            # the reference fails the same way indexing its RoPE table
+            raise IndexError(f"position {end - 1} beyond max_seq_len {max_seq_len}")
+        fast = getattr(seq, "token_slice", None)
+        toks += fast(st, end) if fast is not None else seq.token_ids[st:end]
+        if n == 1:
+            pos.append(st)
+            slots.append(ids[st // bs] * bs + st % bs)
+        else:
+            p = range(st, end)
+            pos += p
+            slots += [ids[q // bs] * bs + q % bs for q in p]
+        c = min(1 + len(seq.draft_token_ids), n)
+        lidx += range(T + n - c, T + n)
+        rows.append((R, c))
+        T += n
+        R += c
+        qsl.append(T)
+        lens.append(end)
+        tables.append(ids)
+        if nb > width:
+            width = nb
+    f.toks, f.pos, f.slots, f.lidx, f.qsl, f.lens = toks, pos, slots, lidx, qsl, lens
+    f.tables, f.rows, f.T, f.S, f.R, f.width = tables, rows, T, len(tables), R, width
+    return f
+
+
+def fused_rows_supported(mc) -> bool:
+    """Steps of <= 16 token rows run the fused projection kernels
+    (vl_linear_rows, vl_qkv_rope_cache), which need d_model and d_ff to be
+    multiples of 16 within their K limits; other shapes take the GEMM path for
+    every step and keep no tiled weight copies."""
+    return (mc.d_model % 16 == 0 and mc.d_ff % 16 == 0 and mc.d_model <= 512
+            and mc.d_ff <= 1024)
+
+
 class _Shape:
     """Offsets of one bucket's int32 record and views of the device buffers."""
 
@@ -88,7 +161,9 @@ class HipRunner(ModelRunner):
             self.stream = torch.cuda.Stream(self.device)
             w = weights if weights is not None else model_weights(mc)
             self.w = pack_weights(mc, w, torch, self.device)
-            tile_weights(self.w, ops.tile16)
+            self._fused_rows = fused_rows_supported(mc)
+            if self._fused_rows:
+                tile_weights(self.w, ops.tile16)
             cos, sin = rope_tables(mc.head_dim, mc.max_seq_len)
             self.cos = torch.from_numpy(cos).to(self.device)
             self.sin = torch.from_numpy(sin).to(self.device)
@@ -170,9 +245,6 @@ class HipRunner(ModelRunner):
         self._attn = torch.zeros(cap, H, hd, **f32)
         self._gu = torch.zeros(cap, 2 * mc.d_ff, **f32)
         self._act = torch.zeros(cap, mc.d_ff, **f32)
-        # the fused small-batch projections cover d_model and d_ff up to their limits
-        self._fused_rows = (mc.d_model % 16 == 0 and mc.d_ff % 16 == 0 and mc.d_model <= 512
-                            and mc.d_ff <= 1024)
         self._hsel = torch.zeros(cap, mc.d_model, **f32)
         self._logits = torch.zeros(cap, mc.vocab_size, **f32)
         self._logits_host = torch.zeros(cap, mc.vocab_size, dtype=torch.float32, pin_memory=True)
@@ -185,71 +257,26 @@ class HipRunner(ModelRunner):
         self._cap_T = cap
 
     def _stage(self, out):
-        """Flatten the scheduled batch into the pinned record and send it.
-
-        Plain Python lists: at decode batch sizes this is about 40% cheaper
-        than building the same record with numpy gathers.
-        """
-        bs = self.block_size
-        max_len = self.model_cfg.max_seq_len
-        sched = out.scheduled
-        S = len(sched)
-        toks: List[int] = []
-        pos: List[int] = []
-        slots: List[int] = []
-        lidx: List[int] = []
-        qsl: List[int] = [0]
-        lens: List[int] = []
-        rows: List[Tuple[int, int]] = []
-        tables = []
-        T = R = 0
-        width = 1
-        for item in sched:
-            seq = item.seq
-            st, n = seq.num_computed, item.num_tokens
-            ids = seq.table.block_ids
-            nb = len(ids)
-            end = st + n
-            if end > nb * bs:
-                raise ValueError(f"sequence {seq.request_id}: {end} tokens but only {nb} blocks")
-            if end > max_len:
-                # the reference fails the same way indexing its RoPE table
-                raise IndexError(f"position {end - 1} beyond max_seq_len {max_len}")
-            toks += seq.token_slice(st, end)
-            if n == 1:
-                pos.append(st)
-                slots.append(ids[st // bs] * bs + st % bs)
-            else:
-                p = range(st, end)
-                pos += p
-                slots += [ids[q // bs] * bs + q % bs for q in p]
-            c = min(1 + len(seq.draft_token_ids), n)
-            lidx += range(T + n - c, T + n)
-            rows.append((R, c))
-            T += n
-            R += c
-            qsl.append(T)
-            lens.append(end)
-            tables.append(ids)
-            if nb > width:
-                width = nb
-        self._ensure_capacity(T, width)
-        shape = _Shape(_bucket(T, 16), _bucket(S, 8), _bucket(R, 8), self.W)
+        """Flatten the scheduled batch into the pinned record and send it."""
+        f = flatten_scheduled(out, self.block_size, self.model_cfg.max_seq_len)
+        self._ensure_capacity(f.T, f.width)
+        shape = _Shape(_bucket(f.T, 16), _bucket(f.S, 8), _bucket(f.R, 8), self.W)
         Tb, Sb, Rb, W = shape.Tb, shape.Sb, shape.Rb, shape.W
+        T, S, R = f.T, f.S, f.R
         bt = [0] * (Sb * W)
-        for i, ids in enumerate(tables):
+        for i, ids in enumerate(f.tables):
             bt[i * W:i * W + len(ids)] = ids
         m = self._meta_np
-        m[shape.tok:shape.tok + Tb] = toks + [0] * (Tb - T)
-        m[shape.pos:shape.pos + Tb] = pos + [0] * (Tb - T)
-        m[shape.slot:shape.slot + Tb] = slots + [-1] * (Tb - T)
-        m[shape.lidx:shape.lidx + Rb] = lidx + [0] * (Rb - R)
-        m[shape.qsl:shape.qsl + Sb + 1] = qsl + [T] * (Sb - S)
-        m[shape.lens:shape.lens + Sb] = lens + [0] * (Sb - S)
+        m[shape.tok:shape.tok + Tb] = f.toks + [0] * (Tb - T)
+        m[shape.pos:shape.pos + Tb] = f.pos + [0] * (Tb - T)
+        m[shape.slot:shape.slot + Tb] = f.slots + [-1] * (Tb - T)
+        m[shape.lidx:shape.lidx + Rb] = f.lidx + [0] * (Rb - R)
+        m[shape.qsl:shape.qsl + Sb + 1] = f.qsl + [T] * (Sb - S)
+        m[shape.lens:shape.lens + Sb] = f.lens + [0] * (Sb - S)
         m[shape.bt:shape.bt + Sb * W] = bt
         n = shape.n_ints
         self._meta[:n].copy_(self._meta_host[:n], non_blocking=True)
-        return shape, rows, R
+        return shape, f.rows, R
 
     # -------------------------------------------------------------- forward --
     def _copy_on_write(self, pairs) -> None:
