@@ -127,6 +127,28 @@ int vl_paged_attention_run(void* out, const void* query, int64_t query_stride,
                            void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * vl_paged_attention without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). It has no counterpart in the reference.
+ * Its workspace is a static device array of VL_NOALLOC_SCRATCH_BYTES bytes,
+ * one per GPU, held until the process ends; the call allocates nothing and
+ * calls no allocating routine. Batches whose plan alone needs more than that
+ * (vl_paged_attention_min_workspace(num_seqs) > VL_NOALLOC_SCRATCH_BYTES) are
+ * rejected with VL_EINVAL; smaller ones run exactly as vl_paged_attention
+ * with a workspace of that size. Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU (two streams, two threads) race and must be
+ * ordered by the caller. Each call rewrites all plan state before reading it.
+ */
+#define VL_NOALLOC_SCRATCH_BYTES (32u << 20)
+int vl_paged_attention_noalloc(void* out, const void* query, int64_t query_stride,
+                               const void* key_cache, const void* value_cache,
+                               const int32_t* block_tables, int block_table_stride,
+                               const int32_t* seq_lens, const int32_t* query_start_loc,
+                               int num_seqs, int num_tokens, int num_heads, int num_kv_heads,
+                               int head_dim, int block_size, float scale, int dtype,
+                               int max_query_len, void* stream);
+
+/*
  * K4a RMSNorm, optionally fused with the residual add that precedes it
  * (vllmlite/model.py:17-19 used at 96, 116, 119):
  *   if residual != NULL: residual[r] += x[r] (x = residual afterwards)

@@ -28,6 +28,7 @@
 // Softmax runs in the base-2 domain: scores are pre-multiplied by
 // scale * log2(e) and exponentiated with exp2, which is the same function.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "vl_common.h"
@@ -1994,4 +1995,58 @@ extern "C" int vl_paged_attention(void* out, const void* query, int64_t query_st
                                 block_table_stride, seq_lens, query_start_loc, num_seqs,
                                 num_tokens, num_heads, num_kv_heads, head_dim, block_size, scale,
                                 dtype, max_query_len, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------- allocation-free call --
+// The workspace of vl_paged_attention_noalloc: a file-scope device array, one
+// copy per GPU, held until the process ends. Host code never passes its name
+// to a kernel (the name is a host-side stand-in); it uses the per-device
+// address hipGetSymbolAddress returns.
+static __device__ __align__(256) unsigned char scratch[VL_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64] = {};
+
+// The current device's copy of `scratch`, looked up once per device.
+int scratch_ptr(void** out) {
+  int dev = 0;
+  VL_CHECK_HIP(hipGetDevice(&dev));
+  VL_CHECK_ARG(dev >= 0 && dev < 64, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    VL_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    VL_CHECK_ARG(p != nullptr && ((uintptr_t)p & 255) == 0, "bad scratch address");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return VL_OK;
+}
+
+}  // namespace
+
+extern "C" int vl_paged_attention_noalloc(void* out, const void* query, int64_t query_stride,
+                                          const void* key_cache, const void* value_cache,
+                                          const int32_t* block_tables, int block_table_stride,
+                                          const int32_t* seq_lens,
+                                          const int32_t* query_start_loc, int num_seqs,
+                                          int num_tokens, int num_heads, int num_kv_heads,
+                                          int head_dim, int block_size, float scale, int dtype,
+                                          int max_query_len, void* stream) {
+  VL_CHECK_ARG(num_seqs >= 0 && fixed_bytes(num_seqs) <= (size_t)VL_NOALLOC_SCRATCH_BYTES,
+               "vl_paged_attention_noalloc: %d sequences need %zu bytes of plan space, more than "
+               "its %zu-byte static scratch; use vl_paged_attention with a workspace",
+               num_seqs, fixed_bytes(num_seqs < 0 ? 0 : num_seqs),
+               (size_t)VL_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = scratch_ptr(&ws);
+  if (rc) return rc;
+  // the plan kernel rewrites every header field and counter the run reads,
+  // so nothing left in the scratch by an earlier call is used
+  return vl_paged_attention(out, query, query_stride, key_cache, value_cache, block_tables,
+                            block_table_stride, seq_lens, query_start_loc, num_seqs, num_tokens,
+                            num_heads, num_kv_heads, head_dim, block_size, scale, dtype,
+                            max_query_len, ws, (size_t)VL_NOALLOC_SCRATCH_BYTES, stream);
 }

@@ -40,6 +40,9 @@ SIGNATURES = {
                                       _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32,
                                       _i32, _i32, _i32, _f32, _i32, _i32, _c_void_p, _size,
                                       _c_void_p]),
+    "vl_paged_attention_noalloc": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,
+                                          _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32,
+                                          _i32, _i32, _i32, _i32, _f32, _i32, _i32, _c_void_p]),
     "vl_rms_norm": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _f32,
                            _c_void_p]),
     "vl_silu_mul": (_i32, [_c_void_p, _c_void_p, _i64, _i32, _c_void_p]),
@@ -235,6 +238,29 @@ def paged_attention_run(out, query, key_cache, value_cache, block_tables, seq_le
                                                     scale, block_size, workspace, max_query_len,
                                                     *dims)),
            "vl_paged_attention_run")
+
+
+NOALLOC_SCRATCH_BYTES = 32 << 20  # VL_NOALLOC_SCRATCH_BYTES
+
+
+def paged_attention_noalloc(out, query, key_cache, value_cache, block_tables, seq_lens,
+                            query_start_loc, scale, block_size, max_query_len: int = 0) -> None:
+    """paged_attention with the library's static per-GPU scratch as the
+    workspace (vl_paged_attention_noalloc): nothing is allocated."""
+    T, H, D = query.shape
+    _need(query.stride(2) == 1 and query.stride(1) == D, "query rows must be [H, D] contiguous")
+    _need(out.shape == (T, H, D) and out.is_contiguous() and out.dtype == query.dtype,
+          "out must be a contiguous [T, H, D] tensor of the query dtype")
+    _need(key_cache.dim() == 3 and key_cache.shape == value_cache.shape, "cache shape mismatch")
+    for t, n in ((block_tables, "block_tables"), (seq_lens, "seq_lens"),
+                 (query_start_loc, "query_start_loc")):
+        _dev_i32(t, n)
+    S = seq_lens.numel()
+    _check(lib().vl_paged_attention_noalloc(
+        _ptr(out), _ptr(query), query.stride(0), _ptr(key_cache), _ptr(value_cache),
+        _ptr(block_tables), block_tables.stride(0), _ptr(seq_lens), _ptr(query_start_loc), S, T,
+        H, key_cache.shape[1], D, block_size, float(scale), _dtype_code(query),
+        int(max_query_len), _stream()), "vl_paged_attention_noalloc")
 
 
 # ------------------------------------------------------------------ K4 -----
