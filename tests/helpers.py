@@ -3,7 +3,7 @@ of the reference: 2 layers, d 64, H4/Hkv2, d_ff 128, max_len 512)."""
 
 from vllmlite_amd.config import CacheConfig, EngineConfig, ModelConfig, SchedulerConfig
 from vllmlite_amd.engine import LLMEngine
-from vllmlite_amd.sequence import SamplingParams
+from vllmlite_amd.request import SamplingParams
 
 from oracle.runner import NumpyRunner
 
@@ -39,7 +39,7 @@ def run(engine, prompts, max_tokens=20, check_counts=False):
     while engine.has_work:
         engine.step()
         if check_counts:
-            assert engine.scheduler.blocks.allocator.check_counts()
+            assert engine.batcher.pool.audit()
     return [engine.seqs[i].output_token_ids for i in ids]
 
 

@@ -133,7 +133,7 @@ def test_single_request_matches_batched():
 def test_preemption_preserves_output(prefix_cache):
     engine = hip_engine(block_size=4, num_blocks=24, max_seqs=8, prefix_cache=prefix_cache)
     got = run(engine, PROMPTS, check_counts=True)
-    assert engine.scheduler.total_preemptions > 0
+    assert engine.batcher.preemptions > 0
     assert got == small_reference()
 
 
@@ -210,7 +210,7 @@ def test_copy_on_write_fork_matches_oracle_runner():
     the HipRunner's logits must match the NumPy oracle runner's."""
     from oracle.runner import NumpyRunner
     from vllmlite_amd.hip_runner import HipRunner
-    from vllmlite_amd.sequence import SamplingParams
+    from vllmlite_amd.request import SamplingParams
 
     cfg = small_cfg(block_size=4)
     outs = []

@@ -4,7 +4,7 @@
 import numpy as np
 import pytest
 
-from vllmlite_amd.sequence import SamplingParams, Sequence
+from vllmlite_amd.request import SamplingParams
 from vllmlite_amd.speculative import NgramProposer, accept_greedy, verify
 from oracle import greedy as oracle_greedy
 
@@ -18,7 +18,8 @@ REPETITIVE = [
 
 
 def seq_with(tokens):
-    return Sequence("t", list(tokens), SamplingParams())
+    from vllmlite_amd.request import Request
+    return Request("t", list(tokens), SamplingParams())
 
 
 def spec_engine(k, **kw):
@@ -93,15 +94,15 @@ def test_speculation_cuts_the_number_of_forward_passes():
 def test_speculation_survives_preemption():
     fast = spec_engine(4, block_size=4, num_blocks=24)
     got = run(fast, PROMPTS, check_counts=True)
-    assert fast.scheduler.total_preemptions > 0
+    assert fast.batcher.preemptions > 0
     assert got == run(build(block_size=4, num_blocks=24), PROMPTS)
 
 
 def test_speculation_frees_every_block():
     fast = spec_engine(4)
     run(fast, REPETITIVE, max_tokens=32)
-    a = fast.scheduler.blocks.allocator
-    assert a.num_free == a.num_blocks
+    pool = fast.batcher.pool
+    assert pool.num_free == pool.num_blocks and pool.audit()
 
 
 def test_speculation_respects_max_tokens():

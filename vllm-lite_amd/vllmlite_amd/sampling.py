@@ -1,58 +1,47 @@
-"""Token sampling from one row of logits. Behaviour follows
-vllmlite/sampling.py:8-64: greedy is argmax with ties to the lowest index,
-after the min_tokens EOS mask and the repetition penalty."""
+"""Choosing the next token from one row of logits.
+
+The rules are the reference's (vllmlite/sampling.py:41-64), in this order:
+EOS masked while fewer than min_tokens were generated; every token already
+seen divided (if positive) or multiplied (if not) by the repetition penalty;
+temperature 0 takes the argmax (ties to the lowest index); otherwise the
+logits are divided by the temperature, cut to the top_k largest (top_k > 0),
+cut to the smallest set of most probable tokens whose probability reaches
+top_p (the token that crosses top_p kept), and one token is drawn from the
+renormalised distribution with the request's own generator (inverse CDF on
+one uniform draw).
+"""
 
 from __future__ import annotations
 
 import numpy as np
 
-from .sequence import SamplingParams
 
-
-def _apply_repetition_penalty(logits: np.ndarray, seen, penalty: float) -> None:
-    if penalty == 1.0 or not seen:
-        return
-    idx = np.unique(np.asarray(seen, dtype=np.int64))
-    vals = logits[idx]
-    logits[idx] = np.where(vals > 0, vals / penalty, vals * penalty)
-
-
-def _top_k(logits: np.ndarray, k: int) -> None:
-    if k <= 0 or k >= logits.size:
-        return
-    cut = np.partition(logits, -k)[-k]
-    logits[logits < cut] = -np.inf
-
-
-def _softmax(x: np.ndarray) -> np.ndarray:
-    e = np.exp(x - x.max())
-    return e / e.sum()
-
-
-def _top_p(logits: np.ndarray, p: float) -> None:
-    if p >= 1.0:
-        return
-    order = np.argsort(-logits)
-    probs = _softmax(logits[order])
-    cum = np.cumsum(probs)
-    # keep up to and including the token whose mass crosses p
-    logits[order[~(cum - probs < p)]] = -np.inf
-
-
-def sample(logits: np.ndarray, params: SamplingParams, seen_tokens, rng: np.random.Generator,
-           num_generated: int = 0, eos_id=None) -> int:
-    if (params.temperature == 0.0 and params.repetition_penalty == 1.0
-            and (eos_id is None or num_generated >= params.min_tokens)):
-        # nothing modifies the row: argmax of the fp32 values (sampling.py:49,56-57)
-        return int(np.argmax(logits if logits.dtype == np.float32 else logits.astype(np.float32)))
-    logits = logits.astype(np.float32, copy=True)
+def choose(row: np.ndarray, params, seen, rng: np.random.Generator, num_generated: int,
+           eos_id) -> int:
+    x = np.array(row, dtype=np.float32)
     if eos_id is not None and num_generated < params.min_tokens:
-        logits[eos_id] = -np.inf
-    _apply_repetition_penalty(logits, seen_tokens, params.repetition_penalty)
-    if params.greedy:
-        return int(np.argmax(logits))
-    logits /= params.temperature
-    _top_k(logits, params.top_k)
-    _top_p(logits, params.top_p)
-    probs = _softmax(logits)
-    return int(rng.choice(probs.size, p=probs))
+        x[eos_id] = -np.inf
+    pen = params.repetition_penalty
+    if pen != 1.0 and len(seen):
+        idx = np.unique(np.asarray(seen, dtype=np.int64))
+        v = x[idx]
+        x[idx] = np.where(v > 0, v / pen, v * pen)
+    if params.temperature == 0.0:
+        return int(np.argmax(x))
+    x /= params.temperature
+    k = params.top_k
+    if 0 < k < x.size:
+        x[x < np.partition(x, x.size - k)[x.size - k]] = -np.inf
+    p = np.exp(x - x.max())
+    p /= p.sum()
+    if params.top_p < 1.0:
+        order = np.argsort(-x, kind="stable")
+        ranked = p[order]
+        before = np.cumsum(ranked) - ranked  # probability mass ranked ahead of each token
+        p = np.zeros_like(p)
+        keep = order[before < params.top_p]
+        p[keep] = ranked[before < params.top_p]
+        p /= p.sum()
+    cdf = np.cumsum(p, dtype=np.float64)
+    i = int(np.searchsorted(cdf, rng.random() * cdf[-1], side="right"))
+    return min(i, x.size - 1)

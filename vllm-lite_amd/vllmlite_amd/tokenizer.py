@@ -1,15 +1,26 @@
-"""Byte-level tokenizer: one token per UTF-8 byte plus BOS/EOS/PAD
-(vllmlite/tokenizer.py:9-59). The HuggingFace tokenizer of the reference
-downloads by name and is not available offline; `get_tokenizer` raises for it."""
+"""Byte-level tokenization: one token per UTF-8 byte, then the specials BOS
+256, EOS 257 and PAD 258 in a 261-entry vocabulary (the ids the reference's
+model and workload use, vllmlite/tokenizer.py:9-22).
+
+Streaming detokenization keeps one incremental UTF-8 decoder per request:
+each step feeds that step's new byte tokens (specials are dropped) and gets
+back the text they complete; a multi-byte character split across steps is
+held inside the decoder until its last byte arrives. The HuggingFace
+tokenizer of the reference loads by model name from the network and is not
+available offline.
+"""
 
 from __future__ import annotations
 
-from typing import List, Tuple
+import codecs
+from typing import List
 
 BOS = 256
 EOS = 257
 PAD = 258
 VOCAB_SIZE = 261
+
+_Utf8 = codecs.getincrementaldecoder("utf-8")
 
 
 class ByteTokenizer:
@@ -20,41 +31,20 @@ class ByteTokenizer:
     name = "byte"
 
     def encode(self, text: str, add_bos: bool = True) -> List[int]:
-        ids = list(text.encode("utf-8"))
-        return [BOS] + ids if add_bos else ids
+        body = list(text.encode("utf-8"))
+        return [BOS, *body] if add_bos else body
 
     def decode(self, ids: List[int]) -> str:
-        return bytes(i for i in ids if i < 256).decode("utf-8", errors="replace")
+        return bytes(t for t in ids if t < 256).decode("utf-8", errors="replace")
 
-    def decode_stream(self, ids: List[int], already: int) -> Tuple[str, int]:
-        """Decode ids[already:], holding back an unfinished multi-byte UTF-8
-        character (tokenizer.py:28-58). Returns (text_delta, new_already)."""
-        tail = ids[already:]
-        raw = bytes(i for i in tail if i < 256)
-        if not raw:
-            return "", len(ids)
-        cut = len(raw)
-        for back in range(1, min(4, len(raw)) + 1):
-            b = raw[-back]
-            if b < 0x80:
-                break
-            if b >= 0xC0:
-                need = 2 if b < 0xE0 else 3 if b < 0xF0 else 4
-                if back < need:
-                    cut = len(raw) - back
-                break
-        text = raw[:cut].decode("utf-8", errors="replace")
-        consumed = used = 0
-        for tid in tail:
-            if consumed >= cut:
-                break
-            if tid < 256:
-                consumed += 1
-            used += 1
-        return text, already + used
+    def stream_decoder(self):
+        """A callable new_ids -> text completed by them."""
+        dec = _Utf8(errors="replace")
+        return lambda new: dec.decode(bytes(t for t in new if t < 256))
 
 
 def get_tokenizer(name=None):
     if not name or name == "byte":
         return ByteTokenizer()
-    raise ValueError(f"tokenizer {name!r} needs a download; only the byte tokenizer is available")
+    raise ValueError(f"tokenizer {name!r} loads from the network; only the byte tokenizer "
+                     "is available")

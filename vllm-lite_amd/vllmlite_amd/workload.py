@@ -12,7 +12,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .sequence import SamplingParams
+from .request import SamplingParams
 
 BOS = 256
 
