@@ -63,8 +63,8 @@ def events(torch, n):
             for _ in range(n)]
 
 
-def mean_ms(ev):
-    return float(np.mean([a.elapsed_time(b) for a, b in ev]))
+def median_ms(ev):
+    return float(np.median([a.elapsed_time(b) for a, b in ev]))
 
 
 def decode_leg(torch, ops, syn, steps, warmup, profile_only=False):
@@ -82,6 +82,10 @@ def decode_leg(torch, ops, syn, steps, warmup, profile_only=False):
         ops.paged_attention_run(out, b["q"], b["kc"], b["vc"], b["bt"], b["seq_lens"], b["qsl"],
                                 b["scale"], syn.BS, ws, max_query_len=1)
 
+    def planned_step():
+        ops.paged_attention_plan(b["q"], b["kc"], b["seq_lens"], b["qsl"], syn.BS, ws)
+        step()
+
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -92,13 +96,21 @@ def decode_leg(torch, ops, syn, steps, warmup, profile_only=False):
         step()
         e1.record()
     torch.cuda.synchronize()
+    # a standalone step: the plan and the run, event pair around both
+    ev_plan = events(torch, steps)
+    for e0, e1 in ev_plan:
+        e0.record()
+        planned_step()
+        e1.record()
+    torch.cuda.synchronize()
     # the step rate: `steps` launches back to back, host clock around them
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    res = {"kernel_ms": mean_ms(ev), "ms_per_step": wall * 1e3 / steps,
+    res = {"kernel_ms": median_ms(ev), "ms_per_step": wall * 1e3 / steps,
+           "plan_and_run_ms": median_ms(ev_plan),
            "bytes": syn.algorithmic_bytes(b, with_scatter=False), "batch": b}
     if not profile_only:
         res["check_rel_err"] = syn.torch_reference_check(
@@ -197,7 +209,7 @@ def mixed_leg(torch, ops, syn, steps, warmup, profile_only=False):
             step()
             e1.record()
         torch.cuda.synchronize()
-        ms = mean_ms(ev)
+        ms = median_ms(ev)
         nbytes, flops = syn.algorithmic_bytes(b), syn.attention_flops(b)
         roof_ms = max(nbytes / (PEAK_HBM_GBS * 1e9), flops / (PEAK_BF16_TFLOPS * 1e12)) * 1e3
         r = {"us": round(ms * 1e3, 1), "tokens": T, "sequences": S, "sum_ctx": int(b["ctx"].sum()),
@@ -260,7 +272,7 @@ def verify_leg(torch, ops, syn, steps, warmup, profile_only=False):
         step()
         e1.record()
     torch.cuda.synchronize()
-    ms = mean_ms(ev)
+    ms = median_ms(ev)
     nbytes = syn.algorithmic_bytes(b) + T * V * 4 + S * (K + 2) * 4 * 2
     flops = syn.attention_flops(b)
     r = {"us": round(ms * 1e3, 1), "sum_ctx": int(b["ctx"].sum()), "algorithmic_bytes": nbytes,
@@ -305,7 +317,7 @@ def cow_leg(torch, ops, steps, warmup):
         ops.copy_blocks(kc, vc, pairs, bs)
         e1.record()
     torch.cuda.synchronize()
-    ms = mean_ms(ev)
+    ms = median_ms(ev)
     nbytes = 48 * L * bs * hkv * hd * 4 * 2 * 2
     ok = True
     for kc, vc in caches:  # every cache has been copied at least once
@@ -333,46 +345,93 @@ def engine_config(prefix_cache=False):
         scheduler=SchedulerConfig(max_seqs=16, max_batched_tokens=1024))
 
 
-def run_mix(runner, cfg, shared_prefix=0):
-    """One pass of the mix: wall from the first add_request until drained
-    (the reference's run_paged, bench/bench.py:74-109)."""
+MIXES = {
+    # name: (shared prefix tokens, fork every request after its first token)
+    "mixed": (0, False),
+    "shared_prefix": (256, False),
+    "shared_prefix_forked": (256, True),
+}
+
+
+def mix_config(name):
+    from vllmlite_amd.workload import shared_prefix_config
+    return engine_config(False) if name == "mixed" else shared_prefix_config(True)
+
+
+def run_mix(runner, cfg, name):
+    """One pass of a mix: wall from the first add_request until drained (the
+    reference's run_paged, bench/bench.py:74-109). Returns (wall, output
+    tokens, steps, streams, copy-on-write pairs)."""
     from vllmlite_amd.engine import LLMEngine
-    from vllmlite_amd.workload import mixed_lengths
-    eng = LLMEngine(cfg, runner=runner)
-    reqs = mixed_lengths(0, 48, shared_prefix)
+    from vllmlite_amd.workload import drive_forked, mixed_lengths
+    shared, fork = MIXES[name]
+    counter = _CowCounter(runner) if fork else runner
+    eng = LLMEngine(cfg, runner=counter)
+    reqs = mixed_lengths(0, 48, shared)
     t0 = time.perf_counter()
-    for rid, ids, p in reqs:
-        eng.add_request(params=p, request_id=rid, prompt_token_ids=ids)
-    while eng.has_work:
-        eng.step()
+    if fork:
+        drive_forked(eng, reqs)
+    else:
+        for rid, ids, p in reqs:
+            eng.add_request(params=p, request_id=rid, prompt_token_ids=ids)
+        while eng.has_work:
+            eng.step()
     wall = time.perf_counter() - t0
-    streams = {rid: list(eng.seqs[rid].output_token_ids) for rid, _, _ in reqs}
-    return wall, eng.total_output_tokens, eng.total_steps, streams
+    streams = {rid: eng.seqs[rid].output_token_ids for rid in eng.seqs}
+    return wall, eng.total_output_tokens, eng.total_steps, streams, counter.pairs if fork else 0
 
 
-def e2e_leg(repeat=3, cpu=True, shared_prefix=0):
-    """Output tok/s of the 48-request mix through HipRunner (one warm-up pass,
-    then best of `repeat`; the runner and its captured graphs persist across
-    passes, each pass gets a fresh engine), and the same mix through the NumPy
-    oracle runner on this host's cores (warm-up on a 4-request mix, best of
-    `repeat`)."""
+class _CowCounter:
+    """A runner wrapper that counts the copy-on-write pairs it is handed."""
+
+    def __init__(self, runner):
+        self.runner = runner
+        self.pairs = 0
+        self.vocab_size = runner.vocab_size
+        if hasattr(runner, "execute_argmax"):
+            self.execute_argmax = self._argmax
+
+    def execute(self, out):
+        self.pairs += len(out.cow)
+        return self.runner.execute(out)
+
+    def _argmax(self, out):
+        self.pairs += len(out.cow)
+        return self.runner.execute_argmax(out)
+
+
+def e2e_leg(name="mixed", repeat=3, cpu=True):
+    """Output tok/s of a mix through HipRunner (one warm-up pass, then best of
+    `repeat`; the runner and its captured graphs persist across passes, each
+    pass gets a fresh engine), the streams checked against the reference's,
+    and the same mix through the NumPy oracle runner on this host's cores
+    (warm-up on a 4-request mix, best of `repeat`)."""
     from vllmlite_amd.hip_runner import HipRunner
-    cfg = engine_config(prefix_cache=shared_prefix > 0)
+    cfg = mix_config(name)
     runner = HipRunner(cfg.model, cfg.cache)
-    run_mix(runner, cfg, shared_prefix)
-    wall, toks, steps, streams = min((run_mix(runner, cfg, shared_prefix) for _ in range(repeat)),
-                                     key=lambda r: r[0])
-    out = {"workload": ("48-request ragged mix" + (f" behind a {shared_prefix}-token shared prefix, "
-                                                   "prefix cache on" if shared_prefix else "") +
-                        " (greedy), TinyLlama 6L d384 H8/Hkv4 d_ff1024 fp32, block 16, 512 blocks, "
+    run_mix(runner, cfg, name)
+    wall, toks, steps, streams, pairs = min(
+        (run_mix(runner, cfg, name) for _ in range(repeat)), key=lambda r: r[0])
+    shared, fork = MIXES[name]
+    out = {"workload": ("48-request ragged mix" +
+                        (f" behind a {shared}-token shared prefix, prefix cache on" if shared
+                         else "") +
+                        (", every request forked once after its first token (copy-on-write of "
+                         "its partial shared tail)" if fork else "") +
+                        f" (greedy), TinyLlama 6L d384 H8/Hkv4 d_ff1024 fp32, block 16, "
+                        f"{cfg.cache.num_blocks} blocks, max_len {cfg.model.max_seq_len}, "
                         "16 seqs, budget 1024"),
            "output_tok_per_s": round(toks / wall, 1), "wall_s": round(wall, 4),
            "steps": steps, "us_per_step": round(wall / steps * 1e6, 1), "output_tokens": toks}
-    if shared_prefix == 0:
-        with open(os.path.join(ROOT, "tests", "golden", "cfg0_streams.json")) as f:
-            gold = json.load(f)["streams"]
-        same = sum(streams[r] == gold[r] for r in gold)
-        out["streams_identical_to_reference"] = f"{same}/{len(gold)}"
+    if fork:
+        out["cow_pairs"] = pairs
+    fixture, key = (("cfg0_streams.json", None) if name == "mixed" else
+                    ("shared_prefix_streams.json", "forked" if fork else "plain"))
+    with open(os.path.join(ROOT, "tests", "golden", fixture)) as f:
+        gold = json.load(f)
+    gold = gold["streams"] if key is None else gold[key]["streams"]
+    same = sum(streams.get(r) == gold[r] for r in gold)
+    out["streams_identical_to_reference"] = f"{same}/{len(gold)}"
     if cpu:
         from oracle.runner import NumpyRunner
         from vllmlite_amd.engine import LLMEngine
@@ -383,7 +442,7 @@ def e2e_leg(repeat=3, cpu=True, shared_prefix=0):
             eng.add_request(params=p, request_id=rid, prompt_token_ids=ids)
         while eng.has_work:
             eng.step()
-        cpu_best = min((run_mix(NumpyRunner(cfg.model, cfg.cache), cfg, shared_prefix)
+        cpu_best = min((run_mix(NumpyRunner(cfg.model, cfg.cache), cfg, name)
                         for _ in range(repeat)), key=lambda r: r[0])
         cpu_tps = cpu_best[1] / cpu_best[0]
         out["cpu_numpy_tok_per_s"] = round(cpu_tps, 1)
@@ -393,7 +452,7 @@ def e2e_leg(repeat=3, cpu=True, shared_prefix=0):
         try:  # one pass with one BLAS thread
             from threadpoolctl import threadpool_limits
             with threadpool_limits(limits=1):
-                one = run_mix(NumpyRunner(cfg.model, cfg.cache), cfg, shared_prefix)
+                one = run_mix(NumpyRunner(cfg.model, cfg.cache), cfg, name)
             out["cpu_numpy_tok_per_s_1_blas_thread"] = round(one[1] / one[0], 1)
             out["speedup_vs_cpu_numpy_1_blas_thread"] = round(toks / wall / (one[1] / one[0]), 2)
         except Exception:  # pragma: no cover
@@ -459,7 +518,7 @@ def main():
                                            "prefill_only"),
               "verify": lambda: verify_leg(torch, ops, syn, args.steps, args.warmup, True),
               "cow": lambda: cow_leg(torch, ops, args.steps, args.warmup),
-              "e2e": lambda: e2e_leg(cpu=False)}[leg]
+              "e2e": lambda: e2e_leg("mixed", cpu=False)}[leg]
         r = fn()
         r.pop("batch", None)
         print(json.dumps({"profile_mode": leg, "result": r}), flush=True)
@@ -491,6 +550,11 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": traffic_from_summary()},
         "kernel_us": round(d["kernel_ms"] * 1e3, 2),
+        "kernel_us_is": "median of per-launch HIP event pairs (the run launch; the plan is "
+                        "built once per step for all layers and timed below)",
+        "plan_and_run_us": round(d["plan_and_run_ms"] * 1e3, 2),
+        "plan_and_run_hbm_frac": round(nbytes / (d["plan_and_run_ms"] * 1e-3) / 1e9
+                                       / PEAK_HBM_GBS, 4),
         "check_rel_err": d["check_rel_err"],
     }
     if not args.no_cpu:
@@ -506,8 +570,9 @@ def main():
     if "cow" in legs:
         extra["copy_on_write"] = cow_leg(torch, ops, 50, 5)
     if "e2e" in legs and not args.no_e2e:
-        line["e2e"] = e2e_leg(cpu=not args.no_cpu)
-        extra["e2e_shared_prefix"] = e2e_leg(cpu=not args.no_cpu, shared_prefix=256)
+        line["e2e"] = e2e_leg("mixed", cpu=not args.no_cpu)
+        extra["e2e_shared_prefix"] = e2e_leg("shared_prefix", cpu=not args.no_cpu)
+        extra["e2e_shared_prefix_forked"] = e2e_leg("shared_prefix_forked", cpu=False)
     line["legs"] = extra
     print(json.dumps(line), flush=True)
 

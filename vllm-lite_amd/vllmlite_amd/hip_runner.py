@@ -35,6 +35,7 @@ The engine calls execute serially, possibly from a different thread each time
 
 from __future__ import annotations
 
+import gc
 from typing import Dict, List, Tuple
 
 import numpy as np
@@ -349,9 +350,19 @@ class HipRunner(ModelRunner):
                         mode=ops.LINEAR_STORE, row_index=lidx)
 
     def _capture(self, s: _Shape, key) -> None:
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, pool=self._pool, stream=self.stream):
-            self._forward(s)
+        # A garbage collection inside the capture could free device or pinned
+        # host memory of unreachable objects (an earlier runner, say); the
+        # stream operations such frees perform are illegal while a capture is
+        # active and abort the process. Collect first, and keep the collector
+        # off until the capture has ended.
+        gc.collect()
+        gc.disable()
+        try:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=self._pool, stream=self.stream):
+                self._forward(s)
+        finally:
+            gc.enable()
         if self._pool is None:
             self._pool = g.pool()
         self._graphs[key] = g
