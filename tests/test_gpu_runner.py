@@ -284,3 +284,39 @@ def test_forked_shared_prefix_copy_on_write_matches_reference():
     assert sorted(got) == sorted(g["streams"])
     bad = [rid for rid in got if got[rid] != g["streams"][rid]]
     assert not bad, f"streams differ: {bad[:5]}"
+
+
+def _logit_trace(runner_factory, cfg, prompts, max_tokens):
+    """Logits of every step (through execute()) of a greedy run."""
+    eng = LLMEngine(cfg, runner=runner_factory(cfg.model, cfg.cache))
+    eng.device_argmax = False
+    logs = []
+    real = eng.runner.execute
+
+    def execute(sched, real=real):
+        lg, rows = real(sched)
+        logs.append((lg.copy(), all(i.num_tokens == 1 for i in sched.scheduled)))
+        return lg, rows
+
+    eng.runner.execute = execute
+    run(eng, prompts, max_tokens=max_tokens)
+    return logs
+
+
+@pytest.mark.parametrize("layers,d_model", [(2, 64), (6, 384)])
+def test_every_step_logits_match_oracle_runner(layers, d_model):
+    """Every step's logits, prefill steps (GEMM path) and single-token decode
+    steps (fused projection kernels) alike, against the NumPy oracle runner's
+    (vllmlite/model.py:80-120): within 2e-4 of each row's largest logit (fp32
+    sums in a different order)."""
+    from oracle.runner import NumpyRunner
+    from vllmlite_amd.hip_runner import HipRunner
+    cfg = small_cfg(layers=layers, d_model=d_model)
+    if d_model == 384:  # the TinyLlama mix's shape
+        cfg.model.n_heads, cfg.model.n_kv_heads, cfg.model.d_ff = 8, 4, 1024
+    got = _logit_trace(HipRunner, cfg, PROMPTS, 12)
+    want = _logit_trace(NumpyRunner, cfg, PROMPTS, 12)
+    assert len(got) == len(want) and sum(dec for _, dec in got) >= 10
+    for (g, dec), (w, _) in zip(got, want):
+        scale = np.abs(w).max(axis=-1, keepdims=True)
+        assert np.all(np.abs(g - w) <= 2e-4 * scale), f"decode step {dec}"
