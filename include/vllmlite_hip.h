@@ -229,6 +229,16 @@ int vl_qkv_rope_cache(float* q_out, float* key_cache, float* value_cache, const 
                       void* stream);
 
 /*
+ * The device side of a step issued before the previous step's tokens reached
+ * the host (no reference counterpart: the reference engine waits for every
+ * step, vllmlite/engine.py:99-181): token_ids[i] < 0 stands for
+ * prev_ids[-token_ids[i] - 1], the id the previous step chose for that row,
+ * and is replaced by it in place (0 if the index is not below num_prev).
+ */
+int vl_resolve_tokens(int32_t* token_ids, int64_t num_tokens, const int32_t* prev_ids,
+                      int64_t num_prev, void* stream);
+
+/*
  * K5 greedy acceptance. Replaces verify (vllmlite/speculative.py:86-100).
  * Sequence i owns logits rows row_start[i] .. row_start[i] + num_drafts[i]
  * (vocab floats each, `row_stride` apart) and drafts[i, 0..num_drafts[i]).

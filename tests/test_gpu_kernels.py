@@ -430,3 +430,22 @@ def test_closed_forms_at_forced_splits(dominant, q_len):
     split_len = hdr[7] if q_len == 1 else hdr[2]
     assert hdr[3] > 0 and split_len <= 8192 // 4, f"no forced split: header {hdr[:13]}"
     assert_rows_close(to_np(out), want, BF16_ROW_REL, f"q_len {q_len} dominant {dominant}")
+
+
+def test_resolve_tokens_takes_previous_step_ids():
+    """vl_resolve_tokens: ids t < 0 become prev[-t - 1]; out-of-range
+    references become 0; others are kept."""
+    o = ops()
+    rng = np.random.default_rng(70)
+    prev = rng.integers(0, 32000, size=37).astype(np.int32)
+    tok = rng.integers(0, 32000, size=300).astype(np.int32)
+    refs = rng.choice(300, size=120, replace=False)
+    tok[refs] = -1 - rng.integers(0, 37, size=120)
+    tok[refs[:3]] = [-38, -1000, -(2 ** 31)]  # past the end of prev
+    want = tok.copy()
+    neg = want < 0
+    idx = -want[neg].astype(np.int64) - 1
+    want[neg] = np.where(idx < 37, prev[np.minimum(idx, 36)], 0)
+    d = dev(tok)
+    o.resolve_tokens(d, dev(prev))
+    assert np.array_equal(to_np(d).astype(np.int64), want.astype(np.int64))

@@ -158,9 +158,10 @@ def test_speculation_matches_plain_greedy(k):
 
 @pytest.mark.parametrize("k", [0, 4])
 def test_device_argmax_matches_host_argmax(k):
-    """Greedy steps through execute_argmax (argmax on the device, R int32
-    values to the host) give the streams of execute() + np.argmax, with and
-    without draft verification; the device path is the one taken."""
+    """Greedy steps through execute_argmax / launch_argmax (argmax on the
+    device, R int32 values to the host) give the streams of execute() +
+    np.argmax, with and without draft verification; the device path is the
+    one taken."""
     rep = PROMPTS + ["abcdefgh abcdefgh abcdefgh abcdefgh abcdefgh abcdefgh"]
     streams, calls = [], []
     for dev in (True, False):
@@ -170,13 +171,14 @@ def test_device_argmax_matches_host_argmax(k):
             e.proposer = NgramProposer(k)
         e.device_argmax = dev
         n = [0]
-        real = e.runner.execute_argmax
+        for name in ("execute_argmax", "launch_argmax"):
+            real = getattr(e.runner, name)
 
-        def execute_argmax(sched, real=real, n=n):
-            n[0] += 1
-            return real(sched)
+            def counted(sched, real=real, n=n):
+                n[0] += 1
+                return real(sched)
 
-        e.runner.execute_argmax = execute_argmax
+            setattr(e.runner, name, counted)
         streams.append(run(e, rep, max_tokens=24))
         calls.append(n[0])
     assert streams[0] == streams[1]
@@ -187,6 +189,7 @@ def test_device_argmax_ids_equal_numpy_argmax():
     """execute_argmax returns np.argmax of execute()'s rows for the same step
     (the forward is deterministic: graph replay is bitwise eager)."""
     e = hip_engine()
+    e.lookahead = False  # every greedy step through execute_argmax
     got = []
     real_x, real_a = e.runner.execute, e.runner.execute_argmax
 
@@ -215,7 +218,7 @@ def test_copy_on_write_fork_matches_oracle_runner():
     cfg = small_cfg(block_size=4)
     outs = []
     for factory in (NumpyRunner, HipRunner):
-        eng = LLMEngine(cfg, runner=factory(cfg.model, cfg.cache))
+        eng = LLMEngine(cfg, runner=factory(cfg.model, cfg.cache), lookahead=False)
         p = SamplingParams(max_tokens=6, temperature=0.0, ignore_eos=True)
         rid = eng.add_request("copy on write please", p)
         eng.step()  # prefill: 20 tokens -> a partial 6th block
@@ -320,3 +323,22 @@ def test_every_step_logits_match_oracle_runner(layers, d_model):
     for (g, dec), (w, _) in zip(got, want):
         scale = np.abs(w).max(axis=-1, keepdims=True)
         assert np.all(np.abs(g - w) <= 2e-4 * scale), f"decode step {dec}"
+
+
+def test_lookahead_across_buffer_growth():
+    from vllmlite_amd.request import SamplingParams
+    """A launched step whose ids are still on their way to the host while the
+    next step grows the runner's buffers (a 2-sequence engine admitting a long
+    prompt after short ones): every stream equals the synchronous engine's."""
+    p = SamplingParams(max_tokens=12, temperature=0.0, ignore_eos=True)
+    prompts = ["hi", "yo", "x" * 150, "a somewhat longer prompt " * 4]
+    got = []
+    for lookahead in (True, False):
+        from vllmlite_amd.hip_runner import HipRunner
+        cfg = small_cfg(max_seqs=2)
+        eng = LLMEngine(cfg, runner=HipRunner(cfg.model, cfg.cache), lookahead=lookahead)
+        ids = [eng.add_request(x, p) for x in prompts]
+        while eng.has_work:
+            eng.step()
+        got.append([eng.seqs[i].output_token_ids for i in ids])
+    assert got[0] == got[1]

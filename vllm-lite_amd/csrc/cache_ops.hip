@@ -91,6 +91,20 @@ __global__ void __launch_bounds__(256) rope_and_cache_kernel(
   }
 }
 
+// Token ids of a step whose inputs include tokens the previous step chose on
+// the device: an id t < 0 stands for prev_ids[-t - 1] (out of range: 0).
+__global__ void __launch_bounds__(256) resolve_tokens_kernel(int32_t* __restrict__ tok, int64_t n,
+                                                             const int32_t* __restrict__ prev,
+                                                             int64_t num_prev) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int32_t t = tok[i];
+  if (t < 0) {
+    const int64_t j = -(int64_t)t - 1;
+    tok[i] = j < num_prev ? prev[j] : 0;
+  }
+}
+
 }  // namespace
 
 extern "C" int vl_reshape_and_cache(const void* key, const void* value, int64_t key_stride,
@@ -179,6 +193,19 @@ extern "C" int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_
   rope_and_cache_kernel<<<grid, 128, 0, (hipStream_t)stream>>>(
       qkv, qkv_stride, q_out, key_cache, value_cache, positions, slot_mapping, cos_table,
       sin_table, num_tokens, num_heads, num_kv_heads, head_dim);
+  VL_CHECK_LAUNCH();
+  return VL_OK;
+}
+
+extern "C" int vl_resolve_tokens(int32_t* token_ids, int64_t num_tokens, const int32_t* prev_ids,
+                                 int64_t num_prev, void* stream) {
+  VL_CHECK_ARG(num_tokens >= 0 && num_prev >= 0, "bad counts");
+  if (num_tokens == 0) return VL_OK;
+  VL_CHECK_ARG(token_ids && (prev_ids || num_prev == 0), "null pointer");
+  const int64_t grid = (num_tokens + 255) / 256;
+  VL_CHECK_ARG(grid < (1ll << 31), "too many tokens");
+  resolve_tokens_kernel<<<(unsigned)grid, 256, 0, (hipStream_t)stream>>>(token_ids, num_tokens,
+                                                                         prev_ids, num_prev);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }

@@ -22,9 +22,25 @@ reasons) the reference fixes:
   4. with speculation on, running requests that are plain-decoding get up to
      k n-gram drafts within the token budget.
 
+Lookahead (on by default, for runners that offer `launch_argmax` /
+`collect`): while a greedy step runs on the device, the host already does
+the next one's bookkeeping. After launching step n the engine applies the
+part of step n's outcome that does not depend on the chosen tokens (K/V
+commits, num_computed, one placeholder token per request that completes,
+max_tokens / max_seq_len stops, which free blocks), schedules and launches
+step n + 1 - a placeholder input token is the negative index of the row whose
+argmax the device holds - and only then waits for step n's ids, writes them
+over the placeholders, decodes text and reports. `step()` therefore returns
+the outputs of the step launched by the call before. Lookahead is used only
+for steps whose outcome cannot depend on token values: every row consumed by
+a plain argmax, no stop strings, EOS and stop ids ignored (`ignore_eos`), no
+speculation; any other step runs synchronously. Streams, step counts and
+stop reasons are those of synchronous stepping.
+
 `fork_request` starts a running copy of a request that shares all of its
 blocks (the reference defines BlockManager.fork but no engine path calls it;
-the copy-on-write workload uses it).
+the copy-on-write workload uses it). Forking happens between synchronous
+steps: drive it with `lookahead = False`.
 """
 
 from __future__ import annotations
@@ -46,7 +62,8 @@ from .tokenizer import get_tokenizer
 
 class LLMEngine:
     def __init__(self, cfg: Optional[EngineConfig] = None, tokenizer: Optional[str] = None,
-                 speculative_tokens: int = 0, runner: Optional[ModelRunner] = None):
+                 speculative_tokens: int = 0, runner: Optional[ModelRunner] = None,
+                 lookahead: bool = True):
         self.cfg = cfg or EngineConfig()
         self.tokenizer = get_tokenizer(tokenizer)
         self.spec_k = speculative_tokens
@@ -56,6 +73,9 @@ class LLMEngine:
             self.cfg.model.vocab_size = self.tokenizer.vocab_size
         self.runner = runner if runner is not None else make_runner(self.cfg)
         self.device_argmax = hasattr(self.runner, "execute_argmax")
+        self.lookahead = lookahead
+        self._inflight = None  # (batch, handle, emitted) of a launched, uncollected step
+        self._next: Optional[StepBatch] = None  # scheduled, to run synchronously
         self.batcher = Batcher(self.cfg.scheduler, self.cfg.cache)
         self.seqs: Dict[str, Request] = {}
         self._ids = itertools.count()
@@ -95,6 +115,9 @@ class LLMEngine:
         """A running copy of a running request, sharing all of its blocks,
         partial tail included; whichever of the two writes that tail first gets
         a copy-on-write pair."""
+        if self._inflight is not None or self._next is not None:
+            raise RuntimeError("fork_request needs synchronous steps: a lookahead step is in "
+                               "flight (construct the engine with lookahead=False)")
         parent = self.seqs[parent_id]
         if parent not in self.batcher.running:
             raise ValueError(f"{parent_id} is not running")
@@ -120,7 +143,7 @@ class LLMEngine:
 
     @property
     def has_work(self) -> bool:
-        return self.batcher.has_work
+        return self._inflight is not None or self._next is not None or self.batcher.has_work
 
     # ----------------------------------------------------------------- step --
     def _argmax_only(self, batch: StepBatch) -> bool:
@@ -136,12 +159,101 @@ class LLMEngine:
                 return False
         return True
 
+    def _lookahead_ok(self, batch: StepBatch) -> bool:
+        if not (self.lookahead and self.device_argmax and self.proposer is None
+                and hasattr(self.runner, "launch_argmax")):
+            return False
+        eos = self.tokenizer.eos_id
+        for item in batch.scheduled:
+            p = item.seq.params
+            if (p.temperature != 0.0 or p.repetition_penalty != 1.0 or p.stop
+                    or item.seq.n_draft):
+                return False
+            if eos is not None and (not p.ignore_eos or item.seq.num_output < p.min_tokens):
+                return False
+        return True
+
+    def _schedule(self) -> StepBatch:
+        if self._next is not None:
+            batch, self._next = self._next, None
+            return batch
+        return self.batcher.schedule()
+
     def step(self) -> List[RequestOutput]:
         b = self.batcher
-        batch = b.schedule()
-        outs = [self._finished_output(r) for r in b.drain_reports()]
-        if not batch.scheduled:
-            return outs
+        if self._inflight is None:
+            batch = self._schedule()
+            outs = [self._finished_output(r) for r in b.drain_reports()]
+            if not batch.scheduled:
+                return outs
+            if not self._lookahead_ok(batch):
+                return outs + self._run_sync(batch)
+            self._inflight = self._advance(self._launch(batch))
+        else:
+            outs = []
+        # step n is on the device and advanced on the host: schedule n + 1
+        nxt = self.batcher.schedule()
+        outs += [self._finished_output(r) for r in b.drain_reports()]
+        following = None
+        if nxt.scheduled and self._lookahead_ok(nxt):
+            following = self._launch(nxt)
+        elif nxt.scheduled:
+            self._next = nxt
+        # step n's tokens replace its placeholders before step n + 1's outcome
+        # is applied (publishing a block reads the tokens in it)
+        outs += self._finish_launched(self._inflight)
+        self._inflight = self._advance(following) if following is not None else None
+        return outs
+
+    def _launch(self, batch: StepBatch):
+        t0 = time.perf_counter()
+        handle = self.runner.launch_argmax(batch)
+        self.busy_time += time.perf_counter() - t0
+        self.total_steps += 1
+        return batch, handle
+
+    def _advance(self, launched):
+        """A launched greedy step's token-independent outcome."""
+        batch, handle = launched
+        rows = handle[0]
+        b = self.batcher
+        emitted = []
+        for item, (row0, count) in zip(batch.scheduled, rows):
+            req = item.seq
+            b.commit(req, item.num_tokens)
+            req.num_computed += item.num_tokens
+            if req.num_computed < len(req.ids):
+                continue  # a prefill chunk or a recompute, not finished yet
+            req.append_token(-1 - (row0 + count - 1))  # the device holds its value
+            self.total_output_tokens += 1
+            p = req.params
+            if req.num_output >= p.max_tokens:
+                req.finish(Status.FINISHED_LENGTH, "length")
+            elif len(req.ids) >= self.cfg.model.max_seq_len:
+                req.finish(Status.FINISHED_LENGTH, "length")
+            if req.status.finished:
+                b.finish(req)
+            emitted.append((req, len(req.ids) - 1, row0 + count - 1))
+        return batch, handle, emitted
+
+    def _finish_launched(self, inflight) -> List[RequestOutput]:
+        """Wait for a launched step's ids; put them in place of the
+        placeholders; report."""
+        _, handle, emitted = inflight
+        t0 = time.perf_counter()
+        picks, _ = self.runner.collect(handle)
+        self.busy_time += time.perf_counter() - t0
+        outs = []
+        for req, pos, row in emitted:
+            tok = int(picks[row])
+            req.ids[pos] = tok
+            # a request preempted since holds its tokens; others also wait for
+            # the next step's placeholder
+            outs.append(self._output(req, [tok], self._detok(req, [tok])))
+        return outs
+
+    def _run_sync(self, batch: StepBatch) -> List[RequestOutput]:
+        b = self.batcher
         t0 = time.perf_counter()
         if self.device_argmax and self._argmax_only(batch):
             picks, rows = self.runner.execute_argmax(batch)
@@ -152,6 +264,7 @@ class LLMEngine:
         self.busy_time += time.perf_counter() - t0
         self.total_steps += 1
         eos = self.tokenizer.eos_id
+        outs = []
         for item, (row0, count) in zip(batch.scheduled, rows):
             req = item.seq
             new = None
@@ -185,18 +298,20 @@ class LLMEngine:
                 if req.status.finished:
                     break
             delta = self._detok(req, emitted)
-            done = req.status.finished
-            if done:
+            if req.status.finished:
                 b.finish(req)
-            outs.append(RequestOutput(
-                request_id=req.request_id, token_ids=req.output_token_ids,
-                new_token_ids=emitted, text_delta=delta, finished=done,
-                finish_reason=finish_reason(req.status), num_prompt_tokens=req.n_prompt,
-                num_output_tokens=req.num_output, cached_prefix_tokens=req.cached_prefix_tokens))
+            outs.append(self._output(req, emitted, delta))
         if self.proposer is not None:
             self.spec.rounds += 1
             self._propose()
         return outs
+
+    def _output(self, req: Request, emitted: List[int], delta: str) -> RequestOutput:
+        return RequestOutput(
+            request_id=req.request_id, token_ids=req.output_token_ids, new_token_ids=emitted,
+            text_delta=delta, finished=req.status.finished,
+            finish_reason=finish_reason(req.status), num_prompt_tokens=req.n_prompt,
+            num_output_tokens=req.num_output, cached_prefix_tokens=req.cached_prefix_tokens)
 
     def _sample(self, req: Request, row: np.ndarray, eos) -> int:
         p = req.params

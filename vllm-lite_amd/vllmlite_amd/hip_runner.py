@@ -173,6 +173,7 @@ class HipRunner(ModelRunner):
             self.cache_k = torch.zeros(shape, dtype=torch.float32, device=self.device)
             self.cache_v = torch.zeros(shape, dtype=torch.float32, device=self.device)
         self.W = max(1, -(-mc.max_seq_len // self.block_size))
+        self._buf = 0  # which of the two pinned staging / id buffers the next launch uses
         self._cap_T = 0
         self._graphs: Dict[Tuple[int, int, int], torch.cuda.CUDAGraph] = {}
         self._pool = None
@@ -200,12 +201,31 @@ class HipRunner(ModelRunner):
         vllmlite/speculative.py:86-100): returns each row's argmax, ties to the
         lowest index as np.argmax, computed on the device, so R int32 values
         cross to the host instead of R x vocab fp32 logits."""
+        return self.collect(self.launch_argmax(out))
+
+    def launch_argmax(self, out):
+        """The first half of execute_argmax: stages the step, enqueues its
+        forward, the argmax and the copy of the ids to the host, and returns
+        at once with a handle for collect(). One launched step may be
+        outstanding while the next is staged and launched; a token id t < 0 in
+        the next step's sequences stands for row -t - 1 of this step's ids
+        (resolved on the device, vl_resolve_tokens)."""
         with torch.cuda.device(self.device), torch.cuda.stream(self.stream):
             rows, R = self._run(out)
+            k = self._buf
             ops.argmax_rows(self._logits[:R], self._ids[:R])
-            self._ids_host[:R].copy_(self._ids[:R], non_blocking=True)
-            self.stream.synchronize()
-            return self._ids_host_np[:R].copy(), rows
+            self._ids_hosts[k][:R].copy_(self._ids[:R], non_blocking=True)
+            self._done[k].record(self.stream)
+            self._buf ^= 1
+            # the handle holds its own buffer and event: a later step that grows
+            # the buffers replaces them while this copy may still be queued
+            return rows, R, self._ids_hosts_np[k], self._done[k]
+
+    def collect(self, handle) -> Tuple[np.ndarray, List[Tuple[int, int]]]:
+        """Waits for a launched step; its ids and rows."""
+        rows, R, host, done = handle
+        done.synchronize()
+        return host[:R].copy(), rows
 
     def _run(self, out) -> Tuple[List[Tuple[int, int]], int]:
         """CoW copies, staging and the forward (graph replay when captured);
@@ -231,13 +251,17 @@ class HipRunner(ModelRunner):
         self.W = max(self.W, W)
         self._graphs.clear()
         self._pool = None
+        old_ids = getattr(self, "_ids", None)
         mc, dev = self.model_cfg, self.device
         H, Hkv, hd = self.H, self.Hkv, self.hd
         f32 = dict(dtype=torch.float32, device=dev)
         n_ints = _Shape(cap, cap, cap, self.W).n_ints
         self._meta = torch.zeros(n_ints, dtype=torch.int32, device=dev)
-        self._meta_host = torch.zeros(n_ints, dtype=torch.int32, pin_memory=True)
-        self._meta_np = self._meta_host.numpy()
+        # two pinned records: a step may be staged while the copy of the one
+        # before is still queued behind the device
+        self._meta_hosts = [torch.zeros(n_ints, dtype=torch.int32, pin_memory=True)
+                            for _ in range(2)]
+        self._meta_nps = [m.numpy() for m in self._meta_hosts]
         self._x = torch.zeros(cap, mc.d_model, **f32)
         self._h = torch.zeros(cap, mc.d_model, **f32)
         self._delta = torch.zeros(cap, mc.d_model, **f32)
@@ -251,8 +275,11 @@ class HipRunner(ModelRunner):
         self._logits_host = torch.zeros(cap, mc.vocab_size, dtype=torch.float32, pin_memory=True)
         self._logits_host_np = self._logits_host.numpy()
         self._ids = torch.zeros(cap, dtype=torch.int32, device=dev)
-        self._ids_host = torch.zeros(cap, dtype=torch.int32, pin_memory=True)
-        self._ids_host_np = self._ids_host.numpy()
+        if old_ids is not None:  # a launched step's ids, still to be read by the next
+            self._ids[:old_ids.numel()].copy_(old_ids)
+        self._ids_hosts = [torch.zeros(cap, dtype=torch.int32, pin_memory=True) for _ in range(2)]
+        self._ids_hosts_np = [h.numpy() for h in self._ids_hosts]
+        self._done = [torch.cuda.Event() for _ in range(2)]
         ws = ops.paged_attention_workspace_size(cap, cap, H, hd, mc.max_seq_len + 64)
         self._ws = ops.AttentionWorkspace(dev).get(ws)
         self._cap_T = cap
@@ -267,7 +294,7 @@ class HipRunner(ModelRunner):
         bt = [0] * (Sb * W)
         for i, ids in enumerate(f.tables):
             bt[i * W:i * W + len(ids)] = ids
-        m = self._meta_np
+        m = self._meta_nps[self._buf]
         m[shape.tok:shape.tok + Tb] = f.toks + [0] * (Tb - T)
         m[shape.pos:shape.pos + Tb] = f.pos + [0] * (Tb - T)
         m[shape.slot:shape.slot + Tb] = f.slots + [-1] * (Tb - T)
@@ -276,7 +303,7 @@ class HipRunner(ModelRunner):
         m[shape.lens:shape.lens + Sb] = f.lens + [0] * (Sb - S)
         m[shape.bt:shape.bt + Sb * W] = bt
         n = shape.n_ints
-        self._meta[:n].copy_(self._meta_host[:n], non_blocking=True)
+        self._meta[:n].copy_(self._meta_hosts[self._buf][:n], non_blocking=True)
         return shape, f.rows, R
 
     # -------------------------------------------------------------- forward --
@@ -295,6 +322,8 @@ class HipRunner(ModelRunner):
         qsl = meta[s.qsl:s.qsl + Sb + 1]
         lens = meta[s.lens:s.lens + Sb]
         bt = meta[s.bt:s.bt + Sb * s.W].view(Sb, s.W)
+        # ids the previous step chose on the device (negative placeholders)
+        ops.resolve_tokens(tok, self._ids)
         x, h, delta = self._x[:Tb], self._h[:Tb], self._delta[:Tb]
         qkv, q, attn = self._qkv[:Tb], self._q[:Tb], self._attn[:Tb]
         gu, act = self._gu[:Tb], self._act[:Tb]

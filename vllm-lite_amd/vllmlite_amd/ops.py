@@ -58,6 +58,7 @@ SIGNATURES = {
                                  _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _f32, _c_void_p,
                                  _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32,
                                  _c_void_p]),
+    "vl_resolve_tokens": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p]),
 }
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -412,3 +413,11 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor) -> None:
     _need(out.numel() == logits.shape[0], "out length")
     _check(lib().vl_argmax_rows(_ptr(logits), logits.stride(0), logits.shape[0], logits.shape[1],
                                 _ptr(out), _stream()), "vl_argmax_rows")
+
+
+def resolve_tokens(token_ids: torch.Tensor, prev_ids: torch.Tensor) -> None:
+    """In place: ids t < 0 become prev_ids[-t - 1] (vl_resolve_tokens)."""
+    _dev_i32(token_ids, "token_ids")
+    _dev_i32(prev_ids, "prev_ids")
+    _check(lib().vl_resolve_tokens(_ptr(token_ids), token_ids.numel(), _ptr(prev_ids),
+                                   prev_ids.numel(), _stream()), "vl_resolve_tokens")

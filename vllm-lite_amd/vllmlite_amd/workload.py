@@ -54,7 +54,9 @@ def drive_forked(engine, reqs, suffix: str = ".c"):
     its blocks, partial tail included (BlockManager.fork,
     vllmlite/block_manager.py:133-137). Whichever of the two writes that tail
     first gets a copy-on-write pair (block_manager.py:74-85). Returns the
-    forked request ids and those whose tail block was partial."""
+    forked request ids and those whose tail block was partial. The engine
+    steps synchronously (the forks happen between steps)."""
+    engine.lookahead = False
     for rid, ids, p in reqs:
         engine.add_request(params=p, request_id=rid, prompt_token_ids=ids)
     forked, partial = set(), []
