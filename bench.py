@@ -80,7 +80,7 @@ def decode_leg(torch, ops, syn, steps, warmup, profile_only=False):
 
     def step():
         ops.paged_attention_run(out, b["q"], b["kc"], b["vc"], b["bt"], b["seq_lens"], b["qsl"],
-                                b["scale"], syn.BS, ws, max_query_len=1)
+                                b["scale"], syn.BS, ws, max_query_len=1, min_query_len=1)
 
     def planned_step():
         ops.paged_attention_plan(b["q"], b["kc"], b["seq_lens"], b["qsl"], syn.BS, ws)
@@ -198,7 +198,8 @@ def mixed_leg(torch, ops, syn, steps, warmup, profile_only=False):
             ops.reshape_and_cache(b["knew"], b["vnew"], b["kc"], b["vc"], b["slot_mapping"])
             ops.paged_attention_plan(b["q"], b["kc"], b["seq_lens"], b["qsl"], syn.BS, ws)
             ops.paged_attention_run(o, b["q"], b["kc"], b["vc"], b["bt"], b["seq_lens"], b["qsl"],
-                                    b["scale"], syn.BS, ws, max_query_len=b["max_q"])
+                                    b["scale"], syn.BS, ws, max_query_len=b["max_q"],
+                                    min_query_len=b["min_q"])
 
         for _ in range(warmup):
             step()
@@ -260,7 +261,7 @@ def verify_leg(torch, ops, syn, steps, warmup, profile_only=False):
         ops.reshape_and_cache(b["knew"], b["vnew"], b["kc"], b["vc"], b["slot_mapping"])
         ops.paged_attention_plan(b["q"], b["kc"], b["seq_lens"], b["qsl"], syn.BS, ws)
         ops.paged_attention_run(o, b["q"], b["kc"], b["vc"], b["bt"], b["seq_lens"], b["qsl"],
-                                b["scale"], syn.BS, ws, max_query_len=5)
+                                b["scale"], syn.BS, ws, max_query_len=5, min_query_len=5)
         ops.greedy_verify(logits, row_start, nd, dr, toks, nacc)
 
     for _ in range(warmup):

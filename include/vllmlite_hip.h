@@ -92,18 +92,22 @@ size_t vl_paged_attention_min_workspace(int num_seqs);
  * sits at position seq_lens[i] - q_len + j and attends keys 0..position
  * (causal; a single query sees the whole context). Head h reads KV head
  * h / (num_heads / num_kv_heads). out [num_tokens, num_heads, head_dim],
- * contiguous, dtype of the query. Accumulation is fp32. max_query_len is the
- * caller's bound on the per-sequence query count (0 = unknown); with 1 the
- * call launches only the decode kernel. A bound that is too small leaves the
- * longer sequences' outputs unwritten (it never reads or writes out of bounds).
+ * contiguous, dtype of the query. Accumulation is fp32. max_query_len and
+ * min_query_len are the caller's bounds on the query count of the sequences
+ * with at least one query (0 = unknown): with max 1 the call launches only the
+ * decode kernel, with min 1 and max > 1 (decodes and multi-query sequences)
+ * only the one-launch step kernel, with min > 1 only the multi-query kernels;
+ * with a bound unknown the kernels decide on the device. Bounds that do not
+ * hold leave some sequences' outputs unwritten (nothing is read or written
+ * out of bounds).
  */
 int vl_paged_attention(void* out, const void* query, int64_t query_stride, const void* key_cache,
                        const void* value_cache, const int32_t* block_tables,
                        int block_table_stride, const int32_t* seq_lens,
                        const int32_t* query_start_loc, int num_seqs, int num_tokens,
                        int num_heads, int num_kv_heads, int head_dim, int block_size,
-                       float scale, int dtype, int max_query_len, void* workspace,
-                       size_t workspace_bytes, void* stream);
+                       float scale, int dtype, int max_query_len, int min_query_len,
+                       void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * The two halves of vl_paged_attention, for callers that run several
@@ -124,7 +128,8 @@ int vl_paged_attention_run(void* out, const void* query, int64_t query_stride,
                            const int32_t* seq_lens, const int32_t* query_start_loc, int num_seqs,
                            int num_tokens, int num_heads, int num_kv_heads, int head_dim,
                            int block_size, float scale, int dtype, int max_query_len,
-                           void* workspace, size_t workspace_bytes, void* stream);
+                           int min_query_len, void* workspace, size_t workspace_bytes,
+                           void* stream);
 
 /*
  * vl_paged_attention without a workspace argument, for callers that cannot
@@ -146,7 +151,7 @@ int vl_paged_attention_noalloc(void* out, const void* query, int64_t query_strid
                                const int32_t* seq_lens, const int32_t* query_start_loc,
                                int num_seqs, int num_tokens, int num_heads, int num_kv_heads,
                                int head_dim, int block_size, float scale, int dtype,
-                               int max_query_len, void* stream);
+                               int max_query_len, int min_query_len, void* stream);
 
 /*
  * K4a RMSNorm, optionally fused with the residual add that precedes it

@@ -33,7 +33,9 @@ def to_np(t):
     return t.float().cpu().numpy()
 
 
-def run_attention(b, dtype, ws_bytes=None, exact_max_q=True):
+def run_attention(b, dtype, ws_bytes=None, exact_max_q=True, exact_min_q=True):
+    """exact_max_q / exact_min_q: pass the batch's true query-count bounds
+    (they choose the launches) or 0 (the kernels decide on the device)."""
     o = ops()
     tdt = torch.float32 if dtype == "f32" else torch.bfloat16
     q = dev(b["q"], tdt)
@@ -43,9 +45,11 @@ def run_attention(b, dtype, ws_bytes=None, exact_max_q=True):
     if ws_bytes is None:
         ws_bytes = o.paged_attention_workspace_size(S, T, b["H"], b["D"], int(b["seq_lens"].max()))
     ws = o.AttentionWorkspace().get(ws_bytes)
-    max_q = int(np.diff(b["qsl"]).max())
+    q_lens = np.diff(b["qsl"])
+    max_q, min_q = int(q_lens.max()), int(q_lens[q_lens > 0].min())
     o.paged_attention(out, q, kc, vc, dev(b["block_tables"]), dev(b["seq_lens"]), dev(b["qsl"]),
-                      b["scale"], b["bs"], ws, max_query_len=max_q if exact_max_q else 0)
+                      b["scale"], b["bs"], ws, max_query_len=max_q if exact_max_q else 0,
+                      min_query_len=min_q if exact_min_q else 0)
     return to_np(out)
 
 
@@ -77,12 +81,30 @@ def test_reference_grid(q_len, H, Hkv, bs, dtype):
 MIXED = [(1, 1), (1, 37), (5, 40), (17, 17), (1, 300), (64, 700), (3, 1025), (1, 16), (9, 33)]
 
 
+@pytest.mark.parametrize("hints", ["both", "max", "none"])
 @pytest.mark.parametrize("shape", [(8, 4, 48), (32, 8, 128), (4, 2, 16), (6, 3, 64)])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_mixed_prefill_decode_one_launch(shape, dtype):
+def test_mixed_prefill_decode_one_launch(shape, dtype, hints):
+    """Decodes and multi-query sequences in one call. With both bounds known
+    the bf16 fast shapes launch the step kernel alone; with only the maximum,
+    the step kernel and the tile kernels (each takes its items from the
+    plan); with neither, the step kernel takes every item."""
     H, Hkv, D = shape
     b = make_batch(MIXED, H, Hkv, D, 16, seed=1)
-    check(run_attention(b, dtype), expected(b, dtype), dtype)
+    got = run_attention(b, dtype, exact_max_q=hints != "none", exact_min_q=hints == "both")
+    check(got, expected(b, dtype), dtype)
+
+
+def test_query_bounds_are_checked():
+    o = ops()
+    b = make_batch([(3, 40)], 4, 4, 64, 16, seed=4)
+    with pytest.raises(RuntimeError, match="query length bounds"):
+        q = dev(b["q"], torch.bfloat16)
+        kc = dev(b["k_cache"], torch.bfloat16)
+        ws = o.AttentionWorkspace().get(o.paged_attention_workspace_size(1, 3, 4, 64, 40))
+        o.paged_attention(torch.empty_like(q), q, kc, kc, dev(b["block_tables"]),
+                          dev(b["seq_lens"]), dev(b["qsl"]), b["scale"], 16, ws,
+                          max_query_len=3, min_query_len=4)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -106,7 +128,7 @@ def test_bad_arguments_raise():
         o.paged_attention(out, q, kc, kc, dev(b["block_tables"]), dev(b["seq_lens"]),
                           dev(b["qsl"][:1]), b["scale"], b["bs"], ws)
     rc = o.lib().vl_paged_attention(None, None, 0, None, None, None, 0, None, None, 1, 1, 6, 4, 8,
-                                    4, 1.0, 0, 0, None, 0, None)
+                                    4, 1.0, 0, 0, 0, None, 0, None)
     assert rc == -1 and b"multiple" in o.lib().vl_last_error()
 
 
@@ -246,7 +268,8 @@ DECODE_CTX = [1, 5, 15, 16, 17, 100, 255, 256, 257, 1000, 4097, 64, 8192]
 def test_bandwidth_decode_path_matches_oracle(exact_max_q):
     """bf16 / D 128 / 32 heads over 8 KV heads / block 16: the bandwidth kernel."""
     b = make_batch([(1, c) for c in DECODE_CTX], 32, 8, 128, 16, seed=11)
-    check(run_attention(b, "bf16", exact_max_q=exact_max_q), expected(b, "bf16"), "bf16")
+    got = run_attention(b, "bf16", exact_max_q=exact_max_q, exact_min_q=exact_max_q)
+    check(got, expected(b, "bf16"), "bf16")
 
 
 def test_bandwidth_decode_chunks_without_split():

@@ -43,7 +43,8 @@ def _step(ops, syn, b, scatter=True):
     if scatter:
         ops.reshape_and_cache(b["knew"], b["vnew"], b["kc"], b["vc"], b["slot_mapping"])
     ops.paged_attention(out, b["q"], b["kc"], b["vc"], b["bt"], b["seq_lens"], b["qsl"],
-                        b["scale"], b["bs"], ws, max_query_len=b["max_q"])
+                        b["scale"], b["bs"], ws, max_query_len=b["max_q"],
+                        min_query_len=b["min_q"])
     torch.cuda.synchronize()
     return out
 

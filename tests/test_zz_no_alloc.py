@@ -27,12 +27,13 @@ def _run_both(b, dtype):
     bt = torch.from_numpy(b["block_tables"]).cuda()
     sl = torch.from_numpy(b["seq_lens"]).cuda()
     qsl = torch.from_numpy(b["qsl"]).cuda()
-    max_q = int(np.diff(b["qsl"]).max())
+    q_lens = np.diff(b["qsl"])
+    max_q, min_q = int(q_lens.max()), int(q_lens[q_lens > 0].min())
     got = torch.full_like(q, float("nan"))
-    ops.paged_attention_noalloc(got, q, kc, vc, bt, sl, qsl, b["scale"], b["bs"], max_q)
+    ops.paged_attention_noalloc(got, q, kc, vc, bt, sl, qsl, b["scale"], b["bs"], max_q, min_q)
     ws = torch.empty(ops.NOALLOC_SCRATCH_BYTES, dtype=torch.uint8, device="cuda")
     ref = torch.full_like(q, float("nan"))
-    ops.paged_attention(ref, q, kc, vc, bt, sl, qsl, b["scale"], b["bs"], ws, max_q)
+    ops.paged_attention(ref, q, kc, vc, bt, sl, qsl, b["scale"], b["bs"], ws, max_q, min_q)
     torch.cuda.synchronize()
     return got.float().cpu().numpy(), ref.float().cpu().numpy()
 
@@ -59,5 +60,5 @@ def test_noalloc_rejects_batches_beyond_its_scratch():
     n = 2_000_000  # its plan alone needs ~88 MB, beyond the 32 MiB scratch
     assert lib.vl_paged_attention_min_workspace(n) > ops.NOALLOC_SCRATCH_BYTES
     rc = lib.vl_paged_attention_noalloc(None, None, 0, None, None, None, 0, None, None, n, n,
-                                        32, 8, 128, 16, 1.0, 1, 1, None)
+                                        32, 8, 128, 16, 1.0, 1, 1, 1, None)
     assert rc == -1 and b"static scratch" in lib.vl_last_error()

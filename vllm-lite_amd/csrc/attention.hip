@@ -594,6 +594,18 @@ __device__ __forceinline__ uint4 load16(const void* p) {
   return __builtin_bit_cast(uint4, *reinterpret_cast<const u32x4_t*>(p));
 }
 
+// The same for the K / V bytes of a tile item: a non-temporal (streaming)
+// load when no other item reads them (a sequence whose rows fit one item:
+// spec-verify and short chunks; measured 950 -> 870 us on the 64 x 5 verify
+// batch), an ordinary one when the sequence's other row blocks re-read them
+// from the cache (long prefill chunks: streaming loads there measured 281 ->
+// 298 us)
+__device__ __forceinline__ uint4 load16_kv(const void* p, bool stream) {
+  if (stream)
+    return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)));
+  return load16(p);
+}
+
 // One K/V tile in LDS. RW (rows per wavefront) sets the V^T row stride: the
 // PV operand reads of a wavefront (rows l % RW, 8-byte reads) then spread
 // over all 64 banks.
@@ -723,6 +735,7 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
     const int part = local % np;
     const int kvh = (local / np) % Hkv;
     const int nrows = q_len * rep;
+    const bool stream_kv = nrows <= kRows;  // no other row block reads this K / V
     const int rb = kW ? cdiv(nrows, kRows) - 1 - local / Hkv : (local / np) / Hkv;
     const int kbeg = np > 1 ? part * P : 0;
     const int kend = np > 1 ? min(ctx, kbeg + P) : ctx;
@@ -801,9 +814,11 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
           for (int r = 0; r < Lds::kUnits; ++r) {
             const int kr = min(k0 + kUnitKeys * r, klast);
             const int64_t boff = (int64_t)((uint64_t)blk[r] * blk_elems) + kv_off;
-            pk[r] = load16(kc + boff + ((uint32_t)(kr & bs_mask) * (uint32_t)slot_stride + k_thr_off));
+            pk[r] = load16_kv(kc + boff + ((uint32_t)(kr & bs_mask) * (uint32_t)slot_stride + k_thr_off),
+                              stream_kv);
             const int vkey = min(kr + tk, kend_wg - 1);
-            pv[r] = load16(vc + boff + ((uint32_t)(vkey & bs_mask) * (uint32_t)slot_stride + tc));
+            pv[r] = load16_kv(vc + boff + ((uint32_t)(vkey & bs_mask) * (uint32_t)slot_stride + tc),
+                              stream_kv);
           }
         } else {
 #pragma unroll
@@ -811,8 +826,8 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
             const int idx = tid + 256 * r;
             const int kk = idx / Lds::kChunks, cc = idx - kk * Lds::kChunks;
             const int64_t off = row_of(min(k0 + kk, kend_wg - 1)) + cc * 8;
-            pk[r] = load16(kc + off);
-            pv[r] = load16(vc + off);
+            pk[r] = load16_kv(kc + off, stream_kv);
+            pv[r] = load16_kv(vc + off, stream_kv);
           }
         }
       } else {
@@ -1268,6 +1283,23 @@ __device__ __forceinline__ DecodeItem decode_fetch(int4 d, int it, int R, int Hk
   return x;
 }
 
+// 16 bytes of K or V for the decode kernel. Each step reads every byte once
+// out of a pool far larger than the caches: non-temporal (streaming) loads
+// measured 222-230 us against 241 us with ordinary loads for the 256-sequence
+// batch (1.29 GB).
+#ifndef VL_DECODE_NT
+#define VL_DECODE_NT 1
+#endif
+__device__ __forceinline__ uint4 load_stream16(const char* p) {
+  if constexpr (VL_DECODE_NT) {
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return *reinterpret_cast<const uint4*>(p);
+  }
+}
+
 // One item (see above) by the 256 threads of a workgroup, from its prologue
 // `cur`; R from the plan header.
 template <bool kMixed>
@@ -1333,7 +1365,7 @@ __device__ __forceinline__ void decode_body(DecodeLds& s, int it, const DecodeIt
           const int bid = __builtin_amdgcn_readlane(my_bid, min(g + u, nblk - 1));
           const char* bp = kbytes + (int64_t)bid * blk_bytes + k_lane;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) kb[u][j] = *reinterpret_cast<const uint4*>(bp + j * 64);
+          for (int j = 0; j < 4; ++j) kb[u][j] = load_stream16(bp + j * 64);
         }
         // all loads of the group go out before any of them is consumed
         asm volatile("" ::: "memory");
@@ -1425,7 +1457,7 @@ __device__ __forceinline__ void decode_body(DecodeLds& s, int it, const DecodeIt
           const int bid = __builtin_amdgcn_readlane(my_bid, min(g + u, nblk - 1));
           const char* bp = vbytes + (int64_t)bid * blk_bytes + v_lane;
 #pragma unroll
-          for (int t = 0; t < 4; ++t) vb[u][t] = *reinterpret_cast<const uint4*>(bp + t * v_tstep);
+          for (int t = 0; t < 4; ++t) vb[u][t] = load_stream16(bp + t * v_tstep);
         }
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
@@ -1871,7 +1903,7 @@ int launch_tile(const Args& a, const Layout& L, float sl2, int max_q, hipStream_
 }
 
 template <typename T>
-int do_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) {
+int do_run(const Args& a, int max_q, int min_q, void* ws, size_t ws_bytes, hipStream_t st) {
   const Layout L = make_layout(ws, ws_bytes, a.S, a.D);
   const float sl2 = a.scale * kLog2e;
   const int ncu = vl_num_cus();
@@ -1883,16 +1915,20 @@ int do_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) 
       VL_CHECK_LAUNCH();
       return VL_OK;
     }
-    // A known bound: the step kernel runs a batch of decodes and multi-query
-    // sequences (the plan's flag, read on the device) and the tile kernels,
-    // which are faster on their own, run one without decodes. An unknown
-    // bound: the step kernel runs the whole batch.
+    // With both bounds known the host knows the batch's kind: decodes and
+    // multi-query sequences together (min 1, max > 1) run in the step kernel
+    // alone; multi-query sequences only (min > 1) in the tile kernels alone.
+    // A bound unknown (0): the step kernel runs a mixed batch and exits on any
+    // other (the plan's flag, read on the device), the tile kernels the reverse.
+    const bool known = max_q > 0 && min_q > 0;
     const bool step_all = max_q <= 0;
-    attend_step_bf16_kernel<<<step_grid(), 256, 0, st>>>(VL_ATTN_LAUNCH_ARGS(uint16_t), L.hdr,
-                                                         L.wide_off, L.wide_seq, L.tile_off,
-                                                         L.hdr + 16, step_all ? 1 : 0);
-    VL_CHECK_LAUNCH();
-    if (!step_all) {
+    if (!known || min_q == 1) {
+      attend_step_bf16_kernel<<<step_grid(), 256, 0, st>>>(VL_ATTN_LAUNCH_ARGS(uint16_t), L.hdr,
+                                                           L.wide_off, L.wide_seq, L.tile_off,
+                                                           L.hdr + 16, step_all ? 1 : 0);
+      VL_CHECK_LAUNCH();
+    }
+    if (!step_all && !(known && min_q == 1)) {
       const int rc = launch_tile<T>(a, L, sl2, max_q, st);
       if (rc) return rc;
     }
@@ -1914,9 +1950,10 @@ int do_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) 
   return VL_OK;
 }
 
-int dispatch_run(const Args& a, int max_q, void* ws, size_t ws_bytes, hipStream_t st) {
-  return a.dtype == VL_DTYPE_F32 ? do_run<float>(a, max_q, ws, ws_bytes, st)
-                                 : do_run<uint16_t>(a, max_q, ws, ws_bytes, st);
+int dispatch_run(const Args& a, int max_q, int min_q, void* ws, size_t ws_bytes,
+                 hipStream_t st) {
+  return a.dtype == VL_DTYPE_F32 ? do_run<float>(a, max_q, min_q, ws, ws_bytes, st)
+                                 : do_run<uint16_t>(a, max_q, min_q, ws, ws_bytes, st);
 }
 
 }  // namespace
@@ -1963,8 +2000,10 @@ extern "C" int vl_paged_attention_run(void* out, const void* query, int64_t quer
                                       const int32_t* seq_lens, const int32_t* query_start_loc,
                                       int num_seqs, int num_tokens, int num_heads,
                                       int num_kv_heads, int head_dim, int block_size, float scale,
-                                      int dtype, int max_query_len, void* workspace,
-                                      size_t workspace_bytes, void* stream) {
+                                      int dtype, int max_query_len, int min_query_len,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+  VL_CHECK_ARG(min_query_len >= 0 && (max_query_len <= 0 || min_query_len <= max_query_len),
+               "bad query length bounds");
   Args a{out, query, query_stride, key_cache, value_cache, block_tables, block_table_stride,
          seq_lens, query_start_loc, num_seqs, num_tokens, num_heads, num_kv_heads, head_dim,
          block_size, scale, dtype};
@@ -1976,7 +2015,8 @@ extern "C" int vl_paged_attention_run(void* out, const void* query, int64_t quer
                      ((uintptr_t)out & 15) == 0 && ((uintptr_t)key_cache & 15) == 0 &&
                      ((uintptr_t)value_cache & 15) == 0,
                  "query, out and caches must be 16-byte aligned (query rows a multiple of 8 elements)");
-  return dispatch_run(a, max_query_len, workspace, workspace_bytes, (hipStream_t)stream);
+  return dispatch_run(a, max_query_len, min_query_len, workspace, workspace_bytes,
+                      (hipStream_t)stream);
 }
 
 extern "C" int vl_paged_attention(void* out, const void* query, int64_t query_stride,
@@ -1985,8 +2025,8 @@ extern "C" int vl_paged_attention(void* out, const void* query, int64_t query_st
                                   const int32_t* seq_lens, const int32_t* query_start_loc,
                                   int num_seqs, int num_tokens, int num_heads, int num_kv_heads,
                                   int head_dim, int block_size, float scale, int dtype,
-                                  int max_query_len, void* workspace, size_t workspace_bytes,
-                                  void* stream) {
+                                  int max_query_len, int min_query_len, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
   int rc = vl_paged_attention_plan(seq_lens, query_start_loc, num_seqs, num_tokens, num_heads,
                                    num_kv_heads, head_dim, block_size, dtype, workspace,
                                    workspace_bytes, stream);
@@ -1994,7 +2034,8 @@ extern "C" int vl_paged_attention(void* out, const void* query, int64_t query_st
   return vl_paged_attention_run(out, query, query_stride, key_cache, value_cache, block_tables,
                                 block_table_stride, seq_lens, query_start_loc, num_seqs,
                                 num_tokens, num_heads, num_kv_heads, head_dim, block_size, scale,
-                                dtype, max_query_len, workspace, workspace_bytes, stream);
+                                dtype, max_query_len, min_query_len, workspace, workspace_bytes,
+                                stream);
 }
 
 // ---------------------------------------------------- allocation-free call --
@@ -2034,7 +2075,7 @@ extern "C" int vl_paged_attention_noalloc(void* out, const void* query, int64_t 
                                           const int32_t* query_start_loc, int num_seqs,
                                           int num_tokens, int num_heads, int num_kv_heads,
                                           int head_dim, int block_size, float scale, int dtype,
-                                          int max_query_len, void* stream) {
+                                          int max_query_len, int min_query_len, void* stream) {
   VL_CHECK_ARG(num_seqs >= 0 && fixed_bytes(num_seqs) <= (size_t)VL_NOALLOC_SCRATCH_BYTES,
                "vl_paged_attention_noalloc: %d sequences need %zu bytes of plan space, more than "
                "its %zu-byte static scratch; use vl_paged_attention with a workspace",
@@ -2048,5 +2089,6 @@ extern "C" int vl_paged_attention_noalloc(void* out, const void* query, int64_t 
   return vl_paged_attention(out, query, query_stride, key_cache, value_cache, block_tables,
                             block_table_stride, seq_lens, query_start_loc, num_seqs, num_tokens,
                             num_heads, num_kv_heads, head_dim, block_size, scale, dtype,
-                            max_query_len, ws, (size_t)VL_NOALLOC_SCRATCH_BYTES, stream);
+                            max_query_len, min_query_len, ws, (size_t)VL_NOALLOC_SCRATCH_BYTES,
+                            stream);
 }

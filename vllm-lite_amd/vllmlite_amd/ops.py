@@ -18,6 +18,7 @@ import torch
 from .build import LIB_PATH
 
 F32, BF16 = 0, 1
+ABI_VERSION = 2  # vl_abi_version() of the library these signatures describe
 _c_void_p = ctypes.c_void_p
 _i32, _i64, _f32, _size = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
 
@@ -33,16 +34,17 @@ SIGNATURES = {
     "vl_paged_attention_min_workspace": (_size, [_i32]),
     "vl_paged_attention": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
                                   _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32,
-                                  _f32, _i32, _i32, _c_void_p, _size, _c_void_p]),
+                                  _f32, _i32, _i32, _i32, _c_void_p, _size, _c_void_p]),
     "vl_paged_attention_plan": (_i32, [_c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32,
                                        _i32, _c_void_p, _size, _c_void_p]),
     "vl_paged_attention_run": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,
                                       _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32,
-                                      _i32, _i32, _i32, _f32, _i32, _i32, _c_void_p, _size,
-                                      _c_void_p]),
+                                      _i32, _i32, _i32, _f32, _i32, _i32, _i32, _c_void_p,
+                                      _size, _c_void_p]),
     "vl_paged_attention_noalloc": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,
                                           _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32,
-                                          _i32, _i32, _i32, _i32, _f32, _i32, _i32, _c_void_p]),
+                                          _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32,
+                                          _c_void_p]),
     "vl_rms_norm": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _f32,
                            _c_void_p]),
     "vl_silu_mul": (_i32, [_c_void_p, _c_void_p, _i64, _i32, _c_void_p]),
@@ -76,6 +78,9 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
+        if handle.vl_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI {handle.vl_abi_version()}, these bindings "
+                               f"need {ABI_VERSION}: rebuild the library")
         _LIB = handle
     return _LIB
 
@@ -190,25 +195,28 @@ def _attn_check(out, query, key_cache, value_cache, block_tables, seq_lens, quer
 
 
 def _attn_args(out, query, key_cache, value_cache, block_tables, seq_lens, query_start_loc,
-               scale, block_size, workspace, max_query_len, T, H, hkv, D, S):
+               scale, block_size, workspace, max_query_len, min_query_len, T, H, hkv, D, S):
     return (_ptr(out), _ptr(query), query.stride(0), _ptr(key_cache), _ptr(value_cache),
             _ptr(block_tables), block_tables.stride(0), _ptr(seq_lens), _ptr(query_start_loc),
             S, T, H, hkv, D, block_size, float(scale), _dtype_code(query), int(max_query_len),
-            _ptr(workspace), workspace.numel() * workspace.element_size(), _stream())
+            int(min_query_len), _ptr(workspace), workspace.numel() * workspace.element_size(), _stream())
 
 
 def paged_attention(out: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
                     value_cache: torch.Tensor, block_tables: torch.Tensor, seq_lens: torch.Tensor,
                     query_start_loc: torch.Tensor, scale: float, block_size: int,
-                    workspace: torch.Tensor, max_query_len: int = 0) -> None:
+                    workspace: torch.Tensor, max_query_len: int = 0,
+                    min_query_len: int = 0) -> None:
     """query [T, H, D] (token rows may be strided), caches [slots, Hkv, D],
     block_tables int32 [S, W], seq_lens int32 [S], query_start_loc int32 [S+1].
-    max_query_len: host-known bound on per-sequence queries (0 = unknown)."""
+    max_query_len / min_query_len: host-known bounds on the query count of
+    the sequences that have queries (0 = unknown); they pick the launches."""
     dims = _attn_check(out, query, key_cache, value_cache, block_tables, seq_lens,
                        query_start_loc, workspace)
     _check(lib().vl_paged_attention(*_attn_args(out, query, key_cache, value_cache, block_tables,
                                                 seq_lens, query_start_loc, scale, block_size,
-                                                workspace, max_query_len, *dims)),
+                                                workspace, max_query_len, min_query_len,
+                                                *dims)),
            "vl_paged_attention")
 
 
@@ -231,13 +239,13 @@ def paged_attention_plan(query: torch.Tensor, key_cache: torch.Tensor, seq_lens:
 
 def paged_attention_run(out, query, key_cache, value_cache, block_tables, seq_lens,
                         query_start_loc, scale, block_size, workspace,
-                        max_query_len: int = 0) -> None:
+                        max_query_len: int = 0, min_query_len: int = 0) -> None:
     dims = _attn_check(out, query, key_cache, value_cache, block_tables, seq_lens,
                        query_start_loc, workspace)
     _check(lib().vl_paged_attention_run(*_attn_args(out, query, key_cache, value_cache,
                                                     block_tables, seq_lens, query_start_loc,
                                                     scale, block_size, workspace, max_query_len,
-                                                    *dims)),
+                                                    min_query_len, *dims)),
            "vl_paged_attention_run")
 
 
@@ -245,7 +253,8 @@ NOALLOC_SCRATCH_BYTES = 32 << 20  # VL_NOALLOC_SCRATCH_BYTES
 
 
 def paged_attention_noalloc(out, query, key_cache, value_cache, block_tables, seq_lens,
-                            query_start_loc, scale, block_size, max_query_len: int = 0) -> None:
+                            query_start_loc, scale, block_size, max_query_len: int = 0,
+                            min_query_len: int = 0) -> None:
     """paged_attention with the library's static per-GPU scratch as the
     workspace (vl_paged_attention_noalloc): nothing is allocated."""
     T, H, D = query.shape
@@ -261,7 +270,7 @@ def paged_attention_noalloc(out, query, key_cache, value_cache, block_tables, se
         _ptr(out), _ptr(query), query.stride(0), _ptr(key_cache), _ptr(value_cache),
         _ptr(block_tables), block_tables.stride(0), _ptr(seq_lens), _ptr(query_start_loc), S, T,
         H, key_cache.shape[1], D, block_size, float(scale), _dtype_code(query),
-        int(max_query_len), _stream()), "vl_paged_attention_noalloc")
+        int(max_query_len), int(min_query_len), _stream()), "vl_paged_attention_noalloc")
 
 
 # ------------------------------------------------------------------ K4 -----

@@ -94,7 +94,7 @@ def build(torch, seqs, seed=0, pool_blocks=POOL, dtype=None, heads=(H, HKV, D), 
         bt=torch.from_numpy(tables).to(device),
         seq_lens=torch.from_numpy(ctx.astype(np.int32)).to(device),
         qsl=torch.from_numpy(qsl).to(device), qsl_np=qsl, scale=1.0 / np.sqrt(hd),
-        max_q=int(q_lens.max()))
+        max_q=int(q_lens.max()), min_q=int(q_lens[q_lens > 0].min()) if (q_lens > 0).any() else 0)
 
 
 def algorithmic_bytes(b, with_scatter=True):
