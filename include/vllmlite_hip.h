@@ -92,14 +92,19 @@ size_t vl_paged_attention_min_workspace(int num_seqs);
  * sits at position seq_lens[i] - q_len + j and attends keys 0..position
  * (causal; a single query sees the whole context). Head h reads KV head
  * h / (num_heads / num_kv_heads). out [num_tokens, num_heads, head_dim],
- * contiguous, dtype of the query. Accumulation is fp32. max_query_len and
- * min_query_len are the caller's bounds on the query count of the sequences
- * with at least one query (0 = unknown): with max 1 the call launches only the
- * decode kernel, with min 1 and max > 1 (decodes and multi-query sequences)
- * only the one-launch step kernel, with min > 1 only the multi-query kernels;
- * with a bound unknown the kernels decide on the device. Bounds that do not
- * hold leave some sequences' outputs unwritten (nothing is read or written
- * out of bounds).
+ * contiguous, dtype of the query. Accumulation is fp32.
+ * Launch hints, each 0 when unknown: max_query_len and min_query_len bound
+ * the query count of the sequences with at least one query, max_context_len
+ * bounds seq_lens. With max_query_len 1 and max_context_len <= 2048, head_dim
+ * 16, 32, 48 or 64, 1, 2, 4 or 8 query heads per KV head and a power-of-two
+ * block size, one short-decode launch runs the call and reads no plan (the
+ * _plan call may be skipped; vl_paged_attention skips it). For bf16,
+ * head_dim 128, 4 query heads per KV head and 16-token blocks: max 1 launches
+ * only the decode kernel, min 1 with max > 1 (decodes and multi-query
+ * sequences) only the one-launch step kernel, min > 1 only the multi-query
+ * kernels; with a bound unknown the kernels decide on the device. Bounds that
+ * do not hold leave some sequences' outputs unwritten (nothing is read or
+ * written out of bounds).
  */
 int vl_paged_attention(void* out, const void* query, int64_t query_stride, const void* key_cache,
                        const void* value_cache, const int32_t* block_tables,
@@ -107,7 +112,8 @@ int vl_paged_attention(void* out, const void* query, int64_t query_stride, const
                        const int32_t* query_start_loc, int num_seqs, int num_tokens,
                        int num_heads, int num_kv_heads, int head_dim, int block_size,
                        float scale, int dtype, int max_query_len, int min_query_len,
-                       void* workspace, size_t workspace_bytes, void* stream);
+                       int max_context_len, void* workspace, size_t workspace_bytes,
+                       void* stream);
 
 /*
  * The two halves of vl_paged_attention, for callers that run several
@@ -128,8 +134,16 @@ int vl_paged_attention_run(void* out, const void* query, int64_t query_stride,
                            const int32_t* seq_lens, const int32_t* query_start_loc, int num_seqs,
                            int num_tokens, int num_heads, int num_kv_heads, int head_dim,
                            int block_size, float scale, int dtype, int max_query_len,
-                           int min_query_len, void* workspace, size_t workspace_bytes,
-                           void* stream);
+                           int min_query_len, int max_context_len, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/*
+ * 1 if a _run call with these shapes and launch hints reads the plan, 0 if it
+ * takes the short-decode kernel, which reads none (its _plan call may then be
+ * skipped). Part of this library's plan/run split; the reference has no plan.
+ */
+int vl_paged_attention_reads_plan(int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                  int max_query_len, int max_context_len);
 
 /*
  * vl_paged_attention without a workspace argument, for callers that cannot
@@ -151,7 +165,8 @@ int vl_paged_attention_noalloc(void* out, const void* query, int64_t query_strid
                                const int32_t* seq_lens, const int32_t* query_start_loc,
                                int num_seqs, int num_tokens, int num_heads, int num_kv_heads,
                                int head_dim, int block_size, float scale, int dtype,
-                               int max_query_len, int min_query_len, void* stream);
+                               int max_query_len, int min_query_len, int max_context_len,
+                               void* stream);
 
 /*
  * K4a RMSNorm, optionally fused with the residual add that precedes it

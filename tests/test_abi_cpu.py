@@ -48,7 +48,29 @@ def test_no_compute_without_gpu_needed_for_queries():
     assert lib.vl_paged_attention_workspace_size(256, 256, 32, 128, 8192) > \
         lib.vl_paged_attention_min_workspace(256)
     lib.vl_abi_version.restype = ctypes.c_int
-    assert lib.vl_abi_version() == 2
+    assert lib.vl_abi_version() == 3
+
+
+def test_reads_plan_names_the_short_decode_shapes():
+    """The host-only rule for which runs read no plan: one query per sequence,
+    a context bound <= 2048, head_dim 16/32/48/64, 1/2/4/8 query heads per KV
+    head, a power-of-two block size; every other case reads the plan."""
+    from vllmlite_amd.build import LIB_PATH
+    lib = ctypes.CDLL(LIB_PATH)
+    f = lib.vl_paged_attention_reads_plan
+    f.restype = ctypes.c_int
+    assert f(8, 4, 48, 16, 1, 512) == 0          # the TinyLlama decode step
+    assert f(8, 1, 64, 1, 1, 2048) == 0
+    assert f(4, 4, 16, 4, 1, 1) == 0
+    assert f(8, 4, 48, 16, 0, 512) == 1          # query bound unknown
+    assert f(8, 4, 48, 16, 2, 512) == 1          # multi-query sequences
+    assert f(8, 4, 48, 16, 1, 0) == 1            # context bound unknown
+    assert f(8, 4, 48, 16, 1, 2049) == 1         # too long for the staged table
+    assert f(32, 8, 128, 16, 1, 512) == 1        # head_dim 128: the bandwidth kernel
+    assert f(12, 4, 48, 16, 1, 512) == 1         # 3 query heads per KV head
+    assert f(8, 4, 48, 12, 1, 512) == 1          # block size not a power of two
+    assert f(8, 3, 48, 16, 1, 512) == 1          # heads not a multiple of KV heads
+    assert f(8, 0, 48, 16, 1, 512) == 1
 
 
 def test_hip_runner_refuses_to_run_without_a_gpu():

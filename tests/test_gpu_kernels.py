@@ -33,9 +33,10 @@ def to_np(t):
     return t.float().cpu().numpy()
 
 
-def run_attention(b, dtype, ws_bytes=None, exact_max_q=True, exact_min_q=True):
-    """exact_max_q / exact_min_q: pass the batch's true query-count bounds
-    (they choose the launches) or 0 (the kernels decide on the device)."""
+def run_attention(b, dtype, ws_bytes=None, exact_max_q=True, exact_min_q=True, ctx_hint=False):
+    """exact_max_q / exact_min_q / ctx_hint: pass the batch's true query-count
+    and context bounds (they choose the launches) or 0 (the kernels decide on
+    the device)."""
     o = ops()
     tdt = torch.float32 if dtype == "f32" else torch.bfloat16
     q = dev(b["q"], tdt)
@@ -49,7 +50,8 @@ def run_attention(b, dtype, ws_bytes=None, exact_max_q=True, exact_min_q=True):
     max_q, min_q = int(q_lens.max()), int(q_lens[q_lens > 0].min())
     o.paged_attention(out, q, kc, vc, dev(b["block_tables"]), dev(b["seq_lens"]), dev(b["qsl"]),
                       b["scale"], b["bs"], ws, max_query_len=max_q if exact_max_q else 0,
-                      min_query_len=min_q if exact_min_q else 0)
+                      min_query_len=min_q if exact_min_q else 0,
+                      max_context_len=int(b["seq_lens"].max()) if ctx_hint else 0)
     return to_np(out)
 
 
@@ -128,7 +130,7 @@ def test_bad_arguments_raise():
         o.paged_attention(out, q, kc, kc, dev(b["block_tables"]), dev(b["seq_lens"]),
                           dev(b["qsl"][:1]), b["scale"], b["bs"], ws)
     rc = o.lib().vl_paged_attention(None, None, 0, None, None, None, 0, None, None, 1, 1, 6, 4, 8,
-                                    4, 1.0, 0, 0, 0, None, 0, None)
+                                    4, 1.0, 0, 0, 0, 0, None, 0, None)
     assert rc == -1 and b"multiple" in o.lib().vl_last_error()
 
 
@@ -270,6 +272,38 @@ def test_bandwidth_decode_path_matches_oracle(exact_max_q):
     b = make_batch([(1, c) for c in DECODE_CTX], 32, 8, 128, 16, seed=11)
     got = run_attention(b, "bf16", exact_max_q=exact_max_q, exact_min_q=exact_max_q)
     check(got, expected(b, "bf16"), "bf16")
+
+
+SHORT_CTX = [1, 5, 63, 64, 65, 255, 256, 257, 700, 2048]
+
+
+@pytest.mark.parametrize("D,H,Hkv", [(16, 4, 4), (32, 8, 4), (48, 8, 4), (64, 8, 2), (64, 8, 1),
+                                     (48, 16, 2)])
+@pytest.mark.parametrize("bs", [1, 16])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_short_decode_kernel(D, H, Hkv, bs, dtype):
+    """Decodes of at most 2048 tokens with head_dim <= 64: the one-workgroup-
+    per-(sequence, KV head) kernel, chosen by the query and context bounds
+    (a sequence without a query in the middle)."""
+    seqs = [(1, c) for c in SHORT_CTX[:5]] + [(0, 30)] + [(1, c) for c in SHORT_CTX[5:]]
+    b = make_batch(seqs, H, Hkv, D, bs, seed=D + H + bs)
+    got = run_attention(b, dtype, ctx_hint=True)
+    check(got, expected(b, dtype), dtype)
+
+
+def test_short_decode_reads_no_plan():
+    """The short-decode run reads nothing from the workspace: a run on a
+    workspace holding no plan (every byte 0xff) gives the oracle's output."""
+    o = ops()
+    b = make_batch([(1, c) for c in (40, 2000, 1)], 8, 4, 48, 16, seed=31)
+    q, kc, vc = dev(b["q"]), dev(b["k_cache"]), dev(b["v_cache"])
+    ws = o.AttentionWorkspace().get(o.paged_attention_workspace_size(3, 3, 8, 48, 2000))
+    ws.fill_(255)
+    out = torch.full_like(q, float("nan"))
+    o.paged_attention_run(out, q, kc, vc, dev(b["block_tables"]), dev(b["seq_lens"]),
+                          dev(b["qsl"]), b["scale"], 16, ws, max_query_len=1, min_query_len=1,
+                          max_context_len=2000)
+    check(to_np(out), expected(b, "f32"), "f32")
 
 
 def test_bandwidth_decode_chunks_without_split():

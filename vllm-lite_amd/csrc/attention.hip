@@ -1607,6 +1607,235 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
   leave_and_reset(work, 1);
 }
 
+// --------------------------------------------------------- short decode --
+
+// Decode batches of short sequences (every sequence at most one query and at
+// most kShortCtx tokens) for head dims up to 64: one workgroup per
+// (sequence, KV head) takes the whole context, so the call needs no plan, no
+// context split and no merge launch. The sequence's block table is staged in
+// LDS first, so that the K and V loads of a 256-key chunk (wavefront w takes
+// keys 64 (4 t + w) + lane of chunk t) are issued together:
+//   QK: lane l holds key l of its wavefront's 64, its K row in registers,
+//       and the dot products with the REP query heads (LDS broadcast reads);
+//   softmax: per head, the wavefront max by DPP row operations (no LDS
+//       round trips), merged online across chunks; each lane keeps the sum of
+//       its own keys' weights until the end; the weights go to the
+//       wavefront's LDS row;
+//   PV: lane l = g NC + c (NC 16-byte chunks per head row, G = 64 / NC key
+//       groups) sums chunk c over keys g, g + G, ... of the chunk, its V
+//       chunks loaded with the K row.
+// At the end the wavefronts' lanes are merged in LDS (max-rescaled), one
+// head at a time, and every (head, dim) written once. Keys past the context
+// re-read the last key (finite values) and get weight 0.
+constexpr int kShortCtx = 2048;
+
+template <typename T, int D, int REP>
+struct ShortLds {
+  static constexpr int kVE = 16 / (int)sizeof(T);  // elements per 16-byte load
+  float q[REP][D];          // query heads, pre-scaled to the log2 domain
+  float p[4][REP][64];      // per wavefront: the chunk's weights
+  float red[4][64][kVE];    // per wavefront and lane: one head's PV sums
+  float m[4][REP], l[4][REP];
+  int32_t tbl[kShortCtx];   // the sequence's block ids
+};
+
+// DPP lane exchange (update_dpp with `old` kept where the row mask excludes
+// the lane).
+#define VL_DPP(old, v, ctrl, rmask)                                                     \
+  __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), ctrl, \
+                                             rmask, 0xF, false))
+
+// Max / sum over the 64 lanes of a wavefront by DPP: within each row of 16
+// (quad xor 1, xor 2, half-row mirror, row mirror), then row 0 into 1 and 2
+// into 3 (row_bcast:15), row 1 into 2 and 3 (row_bcast:31); lane 63 holds the
+// result, which every lane reads back.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, VL_DPP(v, v, 0xB1, 0xF));
+  v = fmaxf(v, VL_DPP(v, v, 0x4E, 0xF));
+  v = fmaxf(v, VL_DPP(v, v, 0x141, 0xF));
+  v = fmaxf(v, VL_DPP(v, v, 0x140, 0xF));
+  v = fmaxf(v, VL_DPP(v, v, 0x142, 0xA));
+  v = fmaxf(v, VL_DPP(v, v, 0x143, 0xC));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += VL_DPP(0.f, v, 0xB1, 0xF);
+  v += VL_DPP(0.f, v, 0x4E, 0xF);
+  v += VL_DPP(0.f, v, 0x141, 0xF);
+  v += VL_DPP(0.f, v, 0x140, 0xF);
+  v += VL_DPP(0.f, v, 0x142, 0xA);
+  v += VL_DPP(0.f, v, 0x143, 0xC);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// A head row of D elements of T as floats (16-byte loads).
+template <typename T, int D>
+__device__ __forceinline__ void load_row(const T* p, float (&r)[D]) {
+  constexpr int VE = 16 / (int)sizeof(T);
+#pragma unroll
+  for (int c = 0; c < D / VE; ++c) {
+    const uint4 v = reinterpret_cast<const uint4*>(p)[c];
+    if constexpr (sizeof(T) == 4) {
+      r[4 * c] = __uint_as_float(v.x), r[4 * c + 1] = __uint_as_float(v.y);
+      r[4 * c + 2] = __uint_as_float(v.z), r[4 * c + 3] = __uint_as_float(v.w);
+    } else {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        r[8 * c + 2 * e] = __uint_as_float(w[e] << 16);
+        r[8 * c + 2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+      }
+    }
+  }
+}
+
+// 16 bytes of T as floats
+template <typename T>
+__device__ __forceinline__ void widen16(const uint4& v, float* r) {
+  if constexpr (sizeof(T) == 4) {
+    r[0] = __uint_as_float(v.x), r[1] = __uint_as_float(v.y);
+    r[2] = __uint_as_float(v.z), r[3] = __uint_as_float(v.w);
+  } else {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      r[2 * e] = __uint_as_float(w[e] << 16);
+      r[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+    }
+  }
+}
+
+template <typename T, int D, int REP>
+__global__ void __launch_bounds__(256) attend_short_decode_kernel(
+    T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const T* kc, const T* vc,
+    const int32_t* __restrict__ bt, int bt_stride, const int32_t* __restrict__ seq_lens,
+    const int32_t* __restrict__ qsl, int Hkv, int bs_log2, float scale_log2) {
+  using Lds = ShortLds<T, D, REP>;
+  constexpr int VE = Lds::kVE;
+  static_assert(D % VE == 0 && D <= 64, "head_dim");
+  constexpr int NC = D / VE;               // 16-byte chunks per head row
+  constexpr int G = 64 / NC;               // PV key groups
+  constexpr int KPL = (64 + G - 1) / G;    // keys per lane in the PV product
+  __shared__ Lds s;
+  const int i = blockIdx.x / Hkv, g = blockIdx.x - (blockIdx.x / Hkv) * Hkv;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int c = seq_lens[i];
+  // a sequence without exactly one query, or longer than the staged table,
+  // is not this kernel's (the bounds the caller stated do not hold)
+  if (qsl[i + 1] - qsl[i] != 1 || c <= 0 || c > kShortCtx) return;
+  const int tok = qsl[i];
+  const int bs_mask = (1 << bs_log2) - 1;
+  const int nblk = (c + bs_mask) >> bs_log2;
+  const int32_t* table = bt + (int64_t)i * bt_stride;
+  for (int b = tid; b < nblk; b += 256) s.tbl[b] = table[b];
+  for (int e = tid; e < REP * D; e += 256) {
+    const int h = e / D, d = e - (e / D) * D;
+    s.q[h][d] = Elem<T>::load(query, (int64_t)tok * q_stride + (int64_t)(g * REP + h) * D + d) *
+                scale_log2;
+  }
+  __syncthreads();
+  const int64_t slot_stride = (int64_t)Hkv * D;
+  const T* kg = kc + (int64_t)g * D;
+  const T* vg = vc + (int64_t)g * D;
+  auto slot_of = [&](int k) {
+    return ((int64_t)s.tbl[k >> bs_log2] << bs_log2) + (k & bs_mask);
+  };
+  const int pg = lane / NC, pc = lane - (lane / NC) * NC;  // PV: key group, chunk
+  float m[REP], lsum[REP], acc[REP][VE];
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+    m[h] = -__builtin_inff(), lsum[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) acc[h][e] = 0.f;
+  }
+  const int nchunk = (c + 255) >> 8;
+  for (int t = 0; t < nchunk; ++t) {
+    const int base = (4 * t + wave) * 64;
+    if (base >= c) break;  // wavefront-uniform; later chunks start later still
+    // every load of the chunk first: the lane's K row and its V chunks
+    float kr[D];
+    load_row<T, D>(kg + slot_of(min(base + lane, c - 1)) * slot_stride, kr);
+    uint4 vraw[KPL];
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      const int kk = min(pg + G * j, 63);  // past the chunk (or lanes past G NC): weight 0
+      vraw[j] = *reinterpret_cast<const uint4*>(vg + slot_of(min(base + kk, c - 1)) * slot_stride +
+                                                pc * VE);
+    }
+    const bool valid = base + lane < c;
+#pragma unroll
+    for (int h = 0; h < REP; ++h) {
+      float a = 0.f;
+#pragma unroll
+      for (int d = 0; d < D; ++d) a += s.q[h][d] * kr[d];
+      const float sc = valid ? a : -__builtin_inff();
+      const float mn = fmaxf(m[h], wave_max_dpp(sc));  // finite: key base is valid
+      const float alpha = exp2_fast(m[h] - mn);
+      const float p = exp2_fast(sc - mn);
+      lsum[h] = lsum[h] * alpha + p;
+#pragma unroll
+      for (int e = 0; e < VE; ++e) acc[h][e] *= alpha;
+      m[h] = mn;
+      s.p[wave][h][lane] = p;
+    }
+    // the weights the wavefront's other lanes wrote above
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      const int kk = pg + G * j;
+      float v[VE];
+      widen16<T>(vraw[j], v);
+#pragma unroll
+      for (int h = 0; h < REP; ++h) {
+        const float w = kk < 64 ? s.p[wave][h][kk] : 0.f;
+#pragma unroll
+        for (int e = 0; e < VE; ++e) acc[h][e] += w * v[e];
+      }
+    }
+    // the weights have been read before the next chunk overwrites them
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+#pragma unroll
+  for (int h = 0; h < REP; ++h) lsum[h] = wave_sum_dpp(lsum[h]);
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < REP; ++h) s.m[wave][h] = m[h], s.l[wave][h] = lsum[h];
+  }
+  const int H = Hkv * REP;
+  // one head at a time: every lane's sums to LDS, then thread d < D adds
+  // dim d over the key groups of each wavefront, max-rescaled across them
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+#pragma unroll
+    for (int e = 0; e < VE; ++e) s.red[wave][lane][e] = acc[h][e];
+    __syncthreads();
+    if (tid < D) {
+      const int d = tid, dc = d / VE, de = d - (d / VE) * VE;
+      float M = -__builtin_inff();
+#pragma unroll
+      for (int w = 0; w < 4; ++w) M = fmaxf(M, s.m[w][h]);
+      float L = 0.f, a = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float mw = s.m[w][h];
+        if (mw == -__builtin_inff()) continue;
+        const float wt = exp2_fast(mw - M);
+        float sw = 0.f;
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) sw += s.red[w][gg * NC + dc][de];
+        L += s.l[w][h] * wt;
+        a += sw * wt;
+      }
+      Elem<T>::store(out, ((int64_t)tok * H + g * REP + h) * D + d, L > 0.f ? a * (1.f / L) : 0.f);
+    }
+    __syncthreads();
+  }
+}
+
 // ------------------------------------------------------------------ step --
 
 // One launch for a whole batch of the bandwidth-kernel shape (bf16, head_dim
@@ -1902,10 +2131,54 @@ int launch_tile(const Args& a, const Layout& L, float sl2, int max_q, hipStream_
   return VL_EINVAL;
 }
 
+// Whether a call takes the short-decode kernel: every sequence a decode
+// (max_q 1) of at most kShortCtx tokens (max_ctx), a power-of-two block size,
+// head_dim 16 / 32 / 48 / 64 and 1, 2, 4 or 8 query heads per KV head.
+inline bool short_decode(const Args& a, int max_q, int max_ctx) {
+  if (a.Hkv <= 0 || a.H <= 0 || a.H % a.Hkv != 0) return false;
+  const int rep = a.H / a.Hkv;
+  return max_q == 1 && max_ctx > 0 && max_ctx <= kShortCtx && a.bs > 0 &&
+         (a.bs & (a.bs - 1)) == 0 && (a.D == 16 || a.D == 32 || a.D == 48 || a.D == 64) &&
+         (rep == 1 || rep == 2 || rep == 4 || rep == 8) && (int64_t)a.S * a.Hkv <= (1 << 30);
+}
+
+template <typename T, int D>
+int launch_short_decode_d(const Args& a, float sl2, hipStream_t st) {
+  const int rep = a.H / a.Hkv;
+  const int grid = a.S * a.Hkv;
+  if (grid == 0) return VL_OK;
+  const int bs_log2 = __builtin_ctz((unsigned)a.bs);
+#define VL_SHORT(REP)                                                                        \
+  attend_short_decode_kernel<T, D, REP><<<grid, 256, 0, st>>>(                               \
+      (T*)a.out, (const T*)a.query, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.bt,        \
+      a.bt_stride, a.seq_lens, a.qsl, a.Hkv, bs_log2, sl2)
+  switch (rep) {
+    case 1: VL_SHORT(1); break;
+    case 2: VL_SHORT(2); break;
+    case 4: VL_SHORT(4); break;
+    default: VL_SHORT(8); break;
+  }
+#undef VL_SHORT
+  VL_CHECK_LAUNCH();
+  return VL_OK;
+}
+
 template <typename T>
-int do_run(const Args& a, int max_q, int min_q, void* ws, size_t ws_bytes, hipStream_t st) {
-  const Layout L = make_layout(ws, ws_bytes, a.S, a.D);
+int launch_short_decode(const Args& a, float sl2, hipStream_t st) {
+  switch (a.D) {
+    case 16: return launch_short_decode_d<T, 16>(a, sl2, st);
+    case 32: return launch_short_decode_d<T, 32>(a, sl2, st);
+    case 48: return launch_short_decode_d<T, 48>(a, sl2, st);
+    default: return launch_short_decode_d<T, 64>(a, sl2, st);
+  }
+}
+
+template <typename T>
+int do_run(const Args& a, int max_q, int min_q, int max_ctx, void* ws, size_t ws_bytes,
+           hipStream_t st) {
   const float sl2 = a.scale * kLog2e;
+  if (short_decode(a, max_q, max_ctx)) return launch_short_decode<T>(a, sl2, st);  // no plan
+  const Layout L = make_layout(ws, ws_bytes, a.S, a.D);
   const int ncu = vl_num_cus();
   const bool fast = fast_shape(a.dtype, a.H, a.Hkv, a.D, a.bs);
   if (fast) {
@@ -1950,10 +2223,10 @@ int do_run(const Args& a, int max_q, int min_q, void* ws, size_t ws_bytes, hipSt
   return VL_OK;
 }
 
-int dispatch_run(const Args& a, int max_q, int min_q, void* ws, size_t ws_bytes,
+int dispatch_run(const Args& a, int max_q, int min_q, int max_ctx, void* ws, size_t ws_bytes,
                  hipStream_t st) {
-  return a.dtype == VL_DTYPE_F32 ? do_run<float>(a, max_q, min_q, ws, ws_bytes, st)
-                                 : do_run<uint16_t>(a, max_q, min_q, ws, ws_bytes, st);
+  return a.dtype == VL_DTYPE_F32 ? do_run<float>(a, max_q, min_q, max_ctx, ws, ws_bytes, st)
+                                 : do_run<uint16_t>(a, max_q, min_q, max_ctx, ws, ws_bytes, st);
 }
 
 }  // namespace
@@ -1982,6 +2255,14 @@ extern "C" size_t vl_paged_attention_workspace_size(int num_seqs, int num_tokens
   return fixed_bytes(num_seqs) + (size_t)rows * row_bytes(head_dim);
 }
 
+extern "C" int vl_paged_attention_reads_plan(int num_heads, int num_kv_heads, int head_dim,
+                                             int block_size, int max_query_len,
+                                             int max_context_len) {
+  Args a{};
+  a.H = num_heads, a.Hkv = num_kv_heads, a.D = head_dim, a.bs = block_size;
+  return short_decode(a, max_query_len, max_context_len) ? 0 : 1;
+}
+
 extern "C" int vl_paged_attention_plan(const int32_t* seq_lens, const int32_t* query_start_loc,
                                        int num_seqs, int num_tokens, int num_heads,
                                        int num_kv_heads, int head_dim, int block_size, int dtype,
@@ -2001,9 +2282,11 @@ extern "C" int vl_paged_attention_run(void* out, const void* query, int64_t quer
                                       int num_seqs, int num_tokens, int num_heads,
                                       int num_kv_heads, int head_dim, int block_size, float scale,
                                       int dtype, int max_query_len, int min_query_len,
-                                      void* workspace, size_t workspace_bytes, void* stream) {
+                                      int max_context_len, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
   VL_CHECK_ARG(min_query_len >= 0 && (max_query_len <= 0 || min_query_len <= max_query_len),
                "bad query length bounds");
+  VL_CHECK_ARG(max_context_len >= 0, "bad context length bound");
   Args a{out, query, query_stride, key_cache, value_cache, block_tables, block_table_stride,
          seq_lens, query_start_loc, num_seqs, num_tokens, num_heads, num_kv_heads, head_dim,
          block_size, scale, dtype};
@@ -2015,8 +2298,11 @@ extern "C" int vl_paged_attention_run(void* out, const void* query, int64_t quer
                      ((uintptr_t)out & 15) == 0 && ((uintptr_t)key_cache & 15) == 0 &&
                      ((uintptr_t)value_cache & 15) == 0,
                  "query, out and caches must be 16-byte aligned (query rows a multiple of 8 elements)");
-  return dispatch_run(a, max_query_len, min_query_len, workspace, workspace_bytes,
-                      (hipStream_t)stream);
+  if (short_decode(a, max_query_len, max_context_len))
+    VL_CHECK_ARG(((uintptr_t)key_cache & 15) == 0 && ((uintptr_t)value_cache & 15) == 0,
+                 "caches must be 16-byte aligned");
+  return dispatch_run(a, max_query_len, min_query_len, max_context_len, workspace,
+                      workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" int vl_paged_attention(void* out, const void* query, int64_t query_stride,
@@ -2025,17 +2311,21 @@ extern "C" int vl_paged_attention(void* out, const void* query, int64_t query_st
                                   const int32_t* seq_lens, const int32_t* query_start_loc,
                                   int num_seqs, int num_tokens, int num_heads, int num_kv_heads,
                                   int head_dim, int block_size, float scale, int dtype,
-                                  int max_query_len, int min_query_len, void* workspace,
-                                  size_t workspace_bytes, void* stream) {
-  int rc = vl_paged_attention_plan(seq_lens, query_start_loc, num_seqs, num_tokens, num_heads,
-                                   num_kv_heads, head_dim, block_size, dtype, workspace,
-                                   workspace_bytes, stream);
-  if (rc) return rc;
+                                  int max_query_len, int min_query_len, int max_context_len,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  Args a{};
+  a.S = num_seqs, a.H = num_heads, a.Hkv = num_kv_heads, a.D = head_dim, a.bs = block_size;
+  if (!short_decode(a, max_query_len, max_context_len)) {  // that kernel reads no plan
+    const int rc = vl_paged_attention_plan(seq_lens, query_start_loc, num_seqs, num_tokens,
+                                           num_heads, num_kv_heads, head_dim, block_size, dtype,
+                                           workspace, workspace_bytes, stream);
+    if (rc) return rc;
+  }
   return vl_paged_attention_run(out, query, query_stride, key_cache, value_cache, block_tables,
                                 block_table_stride, seq_lens, query_start_loc, num_seqs,
                                 num_tokens, num_heads, num_kv_heads, head_dim, block_size, scale,
-                                dtype, max_query_len, min_query_len, workspace, workspace_bytes,
-                                stream);
+                                dtype, max_query_len, min_query_len, max_context_len, workspace,
+                                workspace_bytes, stream);
 }
 
 // ---------------------------------------------------- allocation-free call --
@@ -2075,7 +2365,8 @@ extern "C" int vl_paged_attention_noalloc(void* out, const void* query, int64_t 
                                           const int32_t* query_start_loc, int num_seqs,
                                           int num_tokens, int num_heads, int num_kv_heads,
                                           int head_dim, int block_size, float scale, int dtype,
-                                          int max_query_len, int min_query_len, void* stream) {
+                                          int max_query_len, int min_query_len,
+                                          int max_context_len, void* stream) {
   VL_CHECK_ARG(num_seqs >= 0 && fixed_bytes(num_seqs) <= (size_t)VL_NOALLOC_SCRATCH_BYTES,
                "vl_paged_attention_noalloc: %d sequences need %zu bytes of plan space, more than "
                "its %zu-byte static scratch; use vl_paged_attention with a workspace",
@@ -2089,6 +2380,6 @@ extern "C" int vl_paged_attention_noalloc(void* out, const void* query, int64_t 
   return vl_paged_attention(out, query, query_stride, key_cache, value_cache, block_tables,
                             block_table_stride, seq_lens, query_start_loc, num_seqs, num_tokens,
                             num_heads, num_kv_heads, head_dim, block_size, scale, dtype,
-                            max_query_len, min_query_len, ws, (size_t)VL_NOALLOC_SCRATCH_BYTES,
-                            stream);
+                            max_query_len, min_query_len, max_context_len, ws,
+                            (size_t)VL_NOALLOC_SCRATCH_BYTES, stream);
 }

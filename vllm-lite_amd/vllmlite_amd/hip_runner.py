@@ -57,7 +57,7 @@ class Flattened:
     """One step's ragged batch as plain int lists, in schedule order."""
 
     __slots__ = ("toks", "pos", "slots", "lidx", "qsl", "lens", "tables", "rows", "T", "S",
-                 "R", "width")
+                 "R", "width", "max_q")
 
 
 def flatten_scheduled(out, block_size: int, max_seq_len: int) -> Flattened:
@@ -80,7 +80,7 @@ def flatten_scheduled(out, block_size: int, max_seq_len: int) -> Flattened:
     lens: List[int] = []
     rows: List[Tuple[int, int]] = []
     tables = []
-    T = R = 0
+    T = R = max_q = 0
     width = 1
     for item in out.scheduled:
         seq = item.seq
@@ -112,8 +112,11 @@ def flatten_scheduled(out, block_size: int, max_seq_len: int) -> Flattened:
         tables.append(ids)
         if nb > width:
             width = nb
+        if n > max_q:
+            max_q = n
     f.toks, f.pos, f.slots, f.lidx, f.qsl, f.lens = toks, pos, slots, lidx, qsl, lens
     f.tables, f.rows, f.T, f.S, f.R, f.width = tables, rows, T, len(tables), R, width
+    f.max_q = max_q
     return f
 
 
@@ -129,8 +132,10 @@ def fused_rows_supported(mc) -> bool:
 class _Shape:
     """Offsets of one bucket's int32 record and views of the device buffers."""
 
-    def __init__(self, Tb: int, Sb: int, Rb: int, W: int):
-        self.Tb, self.Sb, self.Rb, self.W = Tb, Sb, Rb, W
+    def __init__(self, Tb: int, Sb: int, Rb: int, W: int, decode: bool = False):
+        # decode: every sequence has one query (its attention takes the
+        # short-decode kernel, which needs no plan)
+        self.Tb, self.Sb, self.Rb, self.W, self.decode = Tb, Sb, Rb, W, decode
         o = 0
         self.tok, o = o, o + Tb
         self.pos, o = o, o + Tb
@@ -175,8 +180,13 @@ class HipRunner(ModelRunner):
         self.W = max(1, -(-mc.max_seq_len // self.block_size))
         self._buf = 0  # which of the two pinned staging / id buffers the next launch uses
         self._cap_T = 0
-        self._graphs: Dict[Tuple[int, int, int], torch.cuda.CUDAGraph] = {}
+        self._graphs: Dict[Tuple[int, int, int, bool], torch.cuda.CUDAGraph] = {}
         self._pool = None
+        # decode-only steps: the attention hints (one query per sequence, at
+        # most max_seq_len tokens, which bounds every position) and whether
+        # they select the short-decode kernel, which needs no plan
+        self._short_decode = not ops.paged_attention_reads_plan(
+            self.H, self.Hkv, self.hd, self.block_size, 1, mc.max_seq_len)
 
     # ------------------------------------------------------------ interface --
     @property
@@ -233,7 +243,7 @@ class HipRunner(ModelRunner):
         if out.cow:
             self._copy_on_write(out.cow)
         shape, rows, R = self._stage(out)
-        key = (shape.Tb, shape.Sb, shape.Rb)
+        key = (shape.Tb, shape.Sb, shape.Rb, shape.decode)
         g = self._graphs.get(key)
         if g is not None:
             g.replay()
@@ -288,7 +298,8 @@ class HipRunner(ModelRunner):
         """Flatten the scheduled batch into the pinned record and send it."""
         f = flatten_scheduled(out, self.block_size, self.model_cfg.max_seq_len)
         self._ensure_capacity(f.T, f.width)
-        shape = _Shape(_bucket(f.T, 16), _bucket(f.S, 8), _bucket(f.R, 8), self.W)
+        shape = _Shape(_bucket(f.T, 16), _bucket(f.S, 8), _bucket(f.R, 8), self.W,
+                       f.max_q == 1 and self._short_decode)
         Tb, Sb, Rb, W = shape.Tb, shape.Sb, shape.Rb, shape.W
         T, S, R = f.T, f.S, f.R
         bt = [0] * (Sb * W)
@@ -333,15 +344,14 @@ class HipRunner(ModelRunner):
             return
         torch.index_select(W["tok_emb"], 0, tok, out=x)
         ops.rms_norm(h, x, W["layers"][0]["attn_norm"])
-        ops.paged_attention_plan(q, self.cache_k[0], lens, qsl, self.block_size, self._ws)
+        self._plan(s, q, lens, qsl)
         n_layers = mc.n_layers
         for li, L in enumerate(W["layers"]):
             kc, vc = self.cache_k[li], self.cache_v[li]
             torch.mm(h, L["w_qkv"], out=qkv)
             ops.rope_and_cache(qkv, q, kc, vc, pos, slot, self.cos, self.sin, self.H, self.Hkv,
                                self.hd)
-            ops.paged_attention_run(attn, q, kc, vc, bt, lens, qsl, self.scale, self.block_size,
-                                    self._ws)
+            self._attend(s, attn, q, kc, vc, bt, lens, qsl)
             torch.mm(attn.view(Tb, -1), L["wo"], out=delta)
             ops.rms_norm(h, delta, L["ffn_norm"], residual=x)
             torch.mm(h, L["w_gate_up"], out=gu)
@@ -353,6 +363,21 @@ class HipRunner(ModelRunner):
         torch.index_select(h, 0, lidx, out=hsel)
         torch.mm(hsel, W["lm_head"], out=self._logits[:Rb])
 
+    def _plan(self, s: _Shape, q, lens, qsl) -> None:
+        """The attention plan of the step, shared by its layers (a decode-only
+        step's short-decode kernel reads none)."""
+        if not s.decode:
+            ops.paged_attention_plan(q, self.cache_k[0], lens, qsl, self.block_size, self._ws)
+
+    def _attend(self, s: _Shape, attn, q, kc, vc, bt, lens, qsl) -> None:
+        if s.decode:
+            ops.paged_attention_run(attn, q, kc, vc, bt, lens, qsl, self.scale, self.block_size,
+                                    self._ws, max_query_len=1, min_query_len=1,
+                                    max_context_len=self.model_cfg.max_seq_len)
+        else:
+            ops.paged_attention_run(attn, q, kc, vc, bt, lens, qsl, self.scale, self.block_size,
+                                    self._ws)
+
     def _forward_rows(self, s: _Shape, x, q, attn, act, tok, pos, slot, lidx, qsl, lens,
                       bt) -> None:
         """The forward for at most 16 token rows (the decode steps): each
@@ -360,7 +385,7 @@ class HipRunner(ModelRunner):
         RoPE + K/V scatter fused in, so a layer is QKV (+ RoPE + cache),
         attention, output (+= residual), gate|up (SwiGLU), down (+= residual)."""
         W, Tb, Rb = self.w, s.Tb, s.Rb
-        ops.paged_attention_plan(q, self.cache_k[0], lens, qsl, self.block_size, self._ws)
+        self._plan(s, q, lens, qsl)
         for li, L in enumerate(W["layers"]):
             kc, vc = self.cache_k[li], self.cache_v[li]
             if li == 0:  # the embedding gather, with x = tok_emb[tok] written out
@@ -370,8 +395,7 @@ class HipRunner(ModelRunner):
             else:
                 ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, x, L["w_qkv_t"], L["attn_norm"], pos,
                                    slot, self.cos, self.sin, self.H, self.Hkv, self.hd)
-            ops.paged_attention_run(attn, q, kc, vc, bt, lens, qsl, self.scale, self.block_size,
-                                    self._ws)
+            self._attend(s, attn, q, kc, vc, bt, lens, qsl)
             ops.linear_rows(x, attn.view(Tb, -1), L["wo_t"], mode=ops.LINEAR_ACCUMULATE)
             ops.linear_rows(act, x, L["w_gate_up_t"], L["ffn_norm"], mode=ops.LINEAR_SWIGLU)
             ops.linear_rows(x, act, L["w_down_t"], mode=ops.LINEAR_ACCUMULATE)

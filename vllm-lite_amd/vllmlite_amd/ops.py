@@ -18,7 +18,7 @@ import torch
 from .build import LIB_PATH
 
 F32, BF16 = 0, 1
-ABI_VERSION = 2  # vl_abi_version() of the library these signatures describe
+ABI_VERSION = 3  # vl_abi_version() of the library these signatures describe
 _c_void_p = ctypes.c_void_p
 _i32, _i64, _f32, _size = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
 
@@ -34,17 +34,18 @@ SIGNATURES = {
     "vl_paged_attention_min_workspace": (_size, [_i32]),
     "vl_paged_attention": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
                                   _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32,
-                                  _f32, _i32, _i32, _i32, _c_void_p, _size, _c_void_p]),
+                                  _f32, _i32, _i32, _i32, _i32, _c_void_p, _size, _c_void_p]),
+    "vl_paged_attention_reads_plan": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "vl_paged_attention_plan": (_i32, [_c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32,
                                        _i32, _c_void_p, _size, _c_void_p]),
     "vl_paged_attention_run": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,
                                       _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32,
-                                      _i32, _i32, _i32, _f32, _i32, _i32, _i32, _c_void_p,
-                                      _size, _c_void_p]),
+                                      _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32,
+                                      _c_void_p, _size, _c_void_p]),
     "vl_paged_attention_noalloc": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,
                                           _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32,
                                           _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32,
-                                          _c_void_p]),
+                                          _i32, _c_void_p]),
     "vl_rms_norm": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _f32,
                            _c_void_p]),
     "vl_silu_mul": (_i32, [_c_void_p, _c_void_p, _i64, _i32, _c_void_p]),
@@ -195,28 +196,30 @@ def _attn_check(out, query, key_cache, value_cache, block_tables, seq_lens, quer
 
 
 def _attn_args(out, query, key_cache, value_cache, block_tables, seq_lens, query_start_loc,
-               scale, block_size, workspace, max_query_len, min_query_len, T, H, hkv, D, S):
+               scale, block_size, workspace, max_query_len, min_query_len, max_context_len,
+               T, H, hkv, D, S):
     return (_ptr(out), _ptr(query), query.stride(0), _ptr(key_cache), _ptr(value_cache),
             _ptr(block_tables), block_tables.stride(0), _ptr(seq_lens), _ptr(query_start_loc),
             S, T, H, hkv, D, block_size, float(scale), _dtype_code(query), int(max_query_len),
-            int(min_query_len), _ptr(workspace), workspace.numel() * workspace.element_size(), _stream())
+            int(min_query_len), int(max_context_len), _ptr(workspace), workspace.numel() * workspace.element_size(), _stream())
 
 
 def paged_attention(out: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
                     value_cache: torch.Tensor, block_tables: torch.Tensor, seq_lens: torch.Tensor,
                     query_start_loc: torch.Tensor, scale: float, block_size: int,
                     workspace: torch.Tensor, max_query_len: int = 0,
-                    min_query_len: int = 0) -> None:
+                    min_query_len: int = 0, max_context_len: int = 0) -> None:
     """query [T, H, D] (token rows may be strided), caches [slots, Hkv, D],
     block_tables int32 [S, W], seq_lens int32 [S], query_start_loc int32 [S+1].
     max_query_len / min_query_len: host-known bounds on the query count of
-    the sequences that have queries (0 = unknown); they pick the launches."""
+    the sequences that have queries, max_context_len on seq_lens (0 =
+    unknown); they pick the launches."""
     dims = _attn_check(out, query, key_cache, value_cache, block_tables, seq_lens,
                        query_start_loc, workspace)
     _check(lib().vl_paged_attention(*_attn_args(out, query, key_cache, value_cache, block_tables,
                                                 seq_lens, query_start_loc, scale, block_size,
                                                 workspace, max_query_len, min_query_len,
-                                                *dims)),
+                                                max_context_len, *dims)),
            "vl_paged_attention")
 
 
@@ -237,15 +240,25 @@ def paged_attention_plan(query: torch.Tensor, key_cache: torch.Tensor, seq_lens:
            "vl_paged_attention_plan")
 
 
+def paged_attention_reads_plan(num_heads: int, num_kv_heads: int, head_dim: int,
+                               block_size: int, max_query_len: int = 0,
+                               max_context_len: int = 0) -> bool:
+    """Whether paged_attention_run with these shapes and hints reads the plan
+    (False: the short-decode kernel, whose plan call may be skipped)."""
+    return bool(lib().vl_paged_attention_reads_plan(num_heads, num_kv_heads, head_dim, block_size,
+                                                    max_query_len, max_context_len))
+
+
 def paged_attention_run(out, query, key_cache, value_cache, block_tables, seq_lens,
                         query_start_loc, scale, block_size, workspace,
-                        max_query_len: int = 0, min_query_len: int = 0) -> None:
+                        max_query_len: int = 0, min_query_len: int = 0,
+                        max_context_len: int = 0) -> None:
     dims = _attn_check(out, query, key_cache, value_cache, block_tables, seq_lens,
                        query_start_loc, workspace)
     _check(lib().vl_paged_attention_run(*_attn_args(out, query, key_cache, value_cache,
                                                     block_tables, seq_lens, query_start_loc,
                                                     scale, block_size, workspace, max_query_len,
-                                                    min_query_len, *dims)),
+                                                    min_query_len, max_context_len, *dims)),
            "vl_paged_attention_run")
 
 
@@ -254,7 +267,7 @@ NOALLOC_SCRATCH_BYTES = 32 << 20  # VL_NOALLOC_SCRATCH_BYTES
 
 def paged_attention_noalloc(out, query, key_cache, value_cache, block_tables, seq_lens,
                             query_start_loc, scale, block_size, max_query_len: int = 0,
-                            min_query_len: int = 0) -> None:
+                            min_query_len: int = 0, max_context_len: int = 0) -> None:
     """paged_attention with the library's static per-GPU scratch as the
     workspace (vl_paged_attention_noalloc): nothing is allocated."""
     T, H, D = query.shape
@@ -270,7 +283,8 @@ def paged_attention_noalloc(out, query, key_cache, value_cache, block_tables, se
         _ptr(out), _ptr(query), query.stride(0), _ptr(key_cache), _ptr(value_cache),
         _ptr(block_tables), block_tables.stride(0), _ptr(seq_lens), _ptr(query_start_loc), S, T,
         H, key_cache.shape[1], D, block_size, float(scale), _dtype_code(query),
-        int(max_query_len), int(min_query_len), _stream()), "vl_paged_attention_noalloc")
+        int(max_query_len), int(min_query_len), int(max_context_len), _stream()),
+        "vl_paged_attention_noalloc")
 
 
 # ------------------------------------------------------------------ K4 -----
