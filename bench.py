@@ -351,12 +351,18 @@ MIXES = {
     "mixed": (0, False),
     "shared_prefix": (256, False),
     "shared_prefix_forked": (256, True),
+    "mixed_bf16_kv": (0, False),  # the 48-request mix over a bf16 K/V cache
 }
 
 
 def mix_config(name):
     from vllmlite_amd.workload import shared_prefix_config
-    return engine_config(False) if name == "mixed" else shared_prefix_config(True)
+    if name.startswith("mixed"):
+        cfg = engine_config(False)
+        if name == "mixed_bf16_kv":
+            cfg.cache.kv_dtype = "bfloat16"
+        return cfg
+    return shared_prefix_config(True)
 
 
 def run_mix(runner, cfg, name):
@@ -419,20 +425,25 @@ def e2e_leg(name="mixed", repeat=3, cpu=True):
                          else "") +
                         (", every request forked once after its first token (copy-on-write of "
                          "its partial shared tail)" if fork else "") +
-                        f" (greedy), TinyLlama 6L d384 H8/Hkv4 d_ff1024 fp32, block 16, "
+                        f" (greedy), TinyLlama 6L d384 H8/Hkv4 d_ff1024 fp32"
+                        f"{', bf16 K/V cache' if cfg.cache.kv_dtype == 'bfloat16' else ''}, "
+                        "block 16, "
                         f"{cfg.cache.num_blocks} blocks, max_len {cfg.model.max_seq_len}, "
                         "16 seqs, budget 1024"),
            "output_tok_per_s": round(toks / wall, 1), "wall_s": round(wall, 4),
            "steps": steps, "us_per_step": round(wall / steps * 1e6, 1), "output_tokens": toks}
     if fork:
         out["cow_pairs"] = pairs
-    fixture, key = (("cfg0_streams.json", None) if name == "mixed" else
+    fixture, key = (("cfg0_streams.json", None) if name.startswith("mixed") else
                     ("shared_prefix_streams.json", "forked" if fork else "plain"))
     with open(os.path.join(ROOT, "tests", "golden", fixture)) as f:
         gold = json.load(f)
     gold = gold["streams"] if key is None else gold[key]["streams"]
     same = sum(streams.get(r) == gold[r] for r in gold)
     out["streams_identical_to_reference"] = f"{same}/{len(gold)}"
+    if cfg.cache.kv_dtype == "bfloat16":
+        out["streams_note"] = ("the reference caches fp32; against the oracle runner with the "
+                               "same bf16 cache the streams are checked by the GPU tests")
     if cpu:
         from oracle.runner import NumpyRunner
         from vllmlite_amd.engine import LLMEngine
@@ -574,6 +585,7 @@ def main():
         line["e2e"] = e2e_leg("mixed", cpu=not args.no_cpu)
         extra["e2e_shared_prefix"] = e2e_leg("shared_prefix", cpu=not args.no_cpu)
         extra["e2e_shared_prefix_forked"] = e2e_leg("shared_prefix_forked", cpu=False)
+        extra["e2e_bf16_kv_cache"] = e2e_leg("mixed_bf16_kv", cpu=False)
     line["legs"] = extra
     print(json.dumps(line), flush=True)
 

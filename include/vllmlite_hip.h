@@ -10,7 +10,9 @@
  *   - the return value is 0 (VL_OK), a negative VL_E* argument error, or a
  *     positive hipError_t; vl_last_error() returns the message of the last
  *     failure on the calling thread. Nothing throws across this boundary.
- *   - dtype is VL_DTYPE_F32 (float) or VL_DTYPE_BF16 (raw bfloat16 bits).
+ *   - dtype is VL_DTYPE_F32 (float) or VL_DTYPE_BF16 (raw bfloat16 bits);
+ *     the paged-attention calls also take VL_DTYPE_F32_BF16KV: fp32 query
+ *     and output over bf16 caches (a bf16 KV cache under an fp32 model).
  *
  * Cache layout is the reference's (vllmlite/runner.py:41-44): one tensor per
  * layer and per K/V of shape [num_slots, num_kv_heads, head_dim], where slot
@@ -30,6 +32,7 @@ extern "C" {
 #define VL_EINVAL (-1)
 #define VL_DTYPE_F32 0
 #define VL_DTYPE_BF16 1
+#define VL_DTYPE_F32_BF16KV 2
 #define VL_LINEAR_STORE 0      /* vl_linear_rows: out = f(x) @ W */
 #define VL_LINEAR_ACCUMULATE 1 /* out += f(x) @ W (the residual add) */
 #define VL_LINEAR_SWIGLU 2     /* out = silu(f(x) @ W[:, :n]) * (f(x) @ W[:, n:2n]) */
@@ -192,12 +195,15 @@ int vl_silu_mul(float* out, const float* gate_up, int64_t rows, int d_ff, void* 
  * and k by cos/sin[positions[t]] (tables [max_pos, head_dim/2], fp32;
  * vllmlite/attention.py:21-37), writes rotated q to q_out [num_tokens,
  * num_heads, head_dim] and rotated k / plain v to the caches at
- * slot_mapping[t] (vllmlite/attention.py:47-49). fp32 only.
+ * slot_mapping[t] (vllmlite/attention.py:47-49). fp32 arithmetic; the caches
+ * hold cache_dtype elements (VL_DTYPE_F32, or VL_DTYPE_BF16: each value
+ * rounded to nearest even when stored).
  */
-int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_out, float* key_cache,
-                      float* value_cache, const int32_t* positions, const int32_t* slot_mapping,
+int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_out, void* key_cache,
+                      void* value_cache, const int32_t* positions, const int32_t* slot_mapping,
                       const float* cos_table, const float* sin_table, int64_t num_tokens,
-                      int num_heads, int num_kv_heads, int head_dim, void* stream);
+                      int num_heads, int num_kv_heads, int head_dim, int cache_dtype,
+                      void* stream);
 
 /*
  * K6 fp32 projections of the TinyLlama forward for at most 16 token rows
@@ -238,15 +244,16 @@ int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_str
  * read (before the norm) are also written to x_out [rows, k] (the residual
  * stream). weight_layout: VL_WEIGHT_ROWS (row stride weight_stride) or
  * VL_WEIGHT_TILES16 (as for vl_linear_rows). rows <= 16, k a multiple of 16,
- * k <= 1024, head_dim even. fp32.
+ * k <= 1024, head_dim even. fp32; the caches hold cache_dtype elements as for
+ * vl_rope_and_cache.
  */
-int vl_qkv_rope_cache(float* q_out, float* key_cache, float* value_cache, const float* x,
+int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cache, const float* x,
                       int64_t x_stride, const int32_t* row_index, float* x_out,
                       const float* weight, int64_t weight_stride, int weight_layout,
                       const float* norm_weight, float eps, const int32_t* positions,
                       const int32_t* slot_mapping, const float* cos_table, const float* sin_table,
                       int rows, int k, int num_heads, int num_kv_heads, int head_dim,
-                      void* stream);
+                      int cache_dtype, void* stream);
 
 /*
  * The device side of a step issued before the previous step's tokens reached

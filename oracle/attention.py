@@ -34,6 +34,17 @@ def gather_slots(block_ids, block_size: int, count: int) -> np.ndarray:
     return (bids[:, None] * block_size + np.arange(block_size, dtype=np.int64)[None, :]).reshape(-1)[:count]
 
 
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    """fp32 -> the nearest bfloat16 (ties to even), returned as fp32: the
+    values a bf16 K/V cache holds. No reference counterpart (the reference
+    caches fp32, attention.py:47-49); pinned in tests/test_oracle_bf16.py by
+    torch's bfloat16 conversion and hand-picked ties. NaN stays NaN."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16).astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(a), a, r).astype(np.float32)
+
+
 def write_kv(cache_k, cache_v, k, v, slots) -> None:
     """attention.py:47-49: scatter rows into the flat [slots, Hkv, D] cache."""
     cache_k[slots] = k

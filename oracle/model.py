@@ -49,9 +49,11 @@ def init_weights(cfg) -> dict:
 
 
 class TinyLlamaOracle:
-    def __init__(self, cfg, weights: dict | None = None):
+    def __init__(self, cfg, weights: dict | None = None, kv_round=None):
         self.cfg = cfg
         self.w = weights if weights is not None else init_weights(cfg)
+        # applied to K/V rows as they are cached (round_bf16 for a bf16 cache)
+        self.kv_round = kv_round if kv_round is not None else (lambda a: a)
         self.cos, self.sin = build_rope(cfg.head_dim, cfg.max_seq_len)
         self.scale = 1.0 / np.sqrt(cfg.head_dim)
         self.layers = [{k: self.w[f"layers.{i}.{k}"] for k in LAYER_KEYS}
@@ -73,7 +75,7 @@ class TinyLlamaOracle:
             attn = np.empty_like(q)
             for start, q_len, wslots, rslots in seq_meta:
                 sl = slice(start, start + q_len)
-                write_kv(ck, cv, k[sl], v[sl], wslots)
+                write_kv(ck, cv, self.kv_round(k[sl]), self.kv_round(v[sl]), wslots)
                 attn[sl] = paged_attention(q[sl], ck, cv, rslots, cfg.n_kv_heads, self.scale)
             x = x + attn.reshape(-1, cfg.n_heads * hd) @ L["wo"]
             h = rms_norm(x, L["ffn_norm"])

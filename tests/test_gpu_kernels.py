@@ -291,6 +291,30 @@ def test_short_decode_kernel(D, H, Hkv, bs, dtype):
     check(got, expected(b, dtype), dtype)
 
 
+@pytest.mark.parametrize("seqs", [[(1, c) for c in SHORT_CTX],
+                                  [(1, 40), (7, 300), (1, 2000), (16, 16), (3, 5000)]])
+@pytest.mark.parametrize("ctx_hint", [True, False])
+def test_fp32_query_over_bf16_cache(seqs, ctx_hint):
+    """VL_DTYPE_F32_BF16KV: fp32 query and output over bf16 caches (decodes
+    by the short-decode kernel when the bounds allow, everything else by the
+    generic kernel and the combine) against the oracle on the bf16 K/V values,
+    at the fp32 tolerance."""
+    o = ops()
+    b = make_batch(seqs, 8, 4, 48, 16, seed=len(seqs) + ctx_hint)
+    q = dev(b["q"])
+    kc, vc = dev(b["k_cache"], torch.bfloat16), dev(b["v_cache"], torch.bfloat16)
+    S, T = len(seqs), b["q"].shape[0]
+    ws = o.AttentionWorkspace().get(o.paged_attention_workspace_size(S, T, 8, 48,
+                                                                     int(b["seq_lens"].max())))
+    out = torch.full_like(q, float("nan"))
+    q_lens = np.diff(b["qsl"])
+    o.paged_attention(out, q, kc, vc, dev(b["block_tables"]), dev(b["seq_lens"]), dev(b["qsl"]),
+                      b["scale"], 16, ws, max_query_len=int(q_lens.max()),
+                      max_context_len=int(b["seq_lens"].max()) if ctx_hint else 0)
+    want = oracle_attention(b, b["q"], bf16_round(b["k_cache"]), bf16_round(b["v_cache"]))
+    check(to_np(out), want, "f32")
+
+
 def test_short_decode_reads_no_plan():
     """The short-decode run reads nothing from the workspace: a run on a
     workspace holding no plan (every byte 0xff) gives the oracle's output."""

@@ -135,6 +135,41 @@ def test_qkv_rope_cache_equals_projection_then_rope(rows, shape):
     assert torch.equal(vc1.nan_to_num(7.0), vc2.nan_to_num(7.0))
 
 
+@pytest.mark.parametrize("rows", [1, 16])
+def test_qkv_rope_cache_bf16_cache_is_the_rounded_fp32_cache(rows):
+    """With bf16 caches both K/V writers (vl_qkv_rope_cache and
+    vl_rope_and_cache) store exactly the fp32 values rounded to nearest even,
+    and q (fp32) is unchanged."""
+    from oracle.attention import round_bf16
+    o = _ops()
+    H, Hkv, D, k = 8, 4, 48, 384
+    n = (H + 2 * Hkv) * D
+    rng = np.random.default_rng(40 + rows)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    x = dev(rng.standard_normal((rows, k)).astype(np.float32))
+    w = dev((0.05 * rng.standard_normal((k, n))).astype(np.float32))
+    g = dev((1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32))
+    pos = dev(rng.integers(0, 64, rows).astype(np.int32))
+    slot = dev(rng.permutation(40)[:rows].astype(np.int32))
+    ang = rng.standard_normal((64, D // 2)).astype(np.float32)
+    cos, sin = dev(np.cos(ang)), dev(np.sin(ang))
+    kf, vf = (torch.zeros((40, Hkv, D), device="cuda") for _ in range(2))
+    kb, vb, kb2, vb2 = (torch.zeros((40, Hkv, D), device="cuda", dtype=torch.bfloat16)
+                        for _ in range(4))
+    qf, qb, qb2 = (torch.empty((rows, H * D), device="cuda") for _ in range(3))
+    o.qkv_rope_cache(qf, kf, vf, x, w, g, pos, slot, cos, sin, H, Hkv, D)
+    o.qkv_rope_cache(qb, kb, vb, x, w, g, pos, slot, cos, sin, H, Hkv, D)
+    qkv = torch.empty((rows, n), device="cuda")
+    o.linear_rows(qkv, x, w, g, mode=o.LINEAR_STORE)
+    o.rope_and_cache(qkv, qb2.view(rows, H, D), kb2, vb2, pos, slot, cos, sin, H, Hkv, D)
+    torch.cuda.synchronize()
+    assert torch.equal(qf, qb) and torch.equal(qf, qb2)
+    for f32, b16, b16b in ((kf, kb, kb2), (vf, vb, vb2)):
+        want = round_bf16(f32.cpu().numpy())
+        assert np.array_equal(b16.float().cpu().numpy(), want)
+        assert np.array_equal(b16b.float().cpu().numpy(), want)
+
+
 def test_row_index_gathers_input_rows():
     """With row_index the input rows are x[row_index] (the logits-row gather,
     vllmlite/runner.py:90): the same bits as gathering first."""

@@ -144,6 +144,7 @@ inline bool fast_shape(int dtype, int H, int Hkv, int D, int bs) {
 // head_dims with an MFMA tile instantiation
 inline bool tile_shape(int dtype, int D, int bs) {
   if (bs <= 0 || (bs & (bs - 1)) != 0) return false;  // block math is shifts and masks
+  if (dtype == VL_DTYPE_F32_BF16KV) return false;      // the generic kernel takes it
   if (dtype == VL_DTYPE_BF16) return D == 64 || D == 128;
   return D == 16 || D == 32 || D == 48 || D == 64 || D == 128;
 }
@@ -459,10 +460,10 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
 
 // ------------------------------------------------------------ generic -----
 
-template <typename T>
+template <typename T, typename TKV>
 __global__ void __launch_bounds__(64) attend_generic_kernel(
-    T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const T* __restrict__ kc,
-    const T* __restrict__ vc, const int32_t* __restrict__ bt, int bt_stride,
+    T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const TKV* __restrict__ kc,
+    const TKV* __restrict__ vc, const int32_t* __restrict__ bt, int bt_stride,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H, int Hkv,
     int D, int bs, float scale_log2, const int32_t* __restrict__ hdr,
     const int32_t* __restrict__ item_off, const int32_t* __restrict__ nparts,
@@ -508,9 +509,9 @@ __global__ void __launch_bounds__(64) attend_generic_kernel(
       if (key < kend) {
         const int64_t slot = (int64_t)table[key / bs] * bs + key % bs;
         row = slot * slot_stride + (int64_t)kvh * D;
-        const T* kr = kc + row;
+        const TKV* kr = kc + row;
         float dot = 0.f;
-        for (int d = 0; d < D; ++d) dot += q_s[d] * Elem<T>::load(kr, d);
+        for (int d = 0; d < D; ++d) dot += q_s[d] * Elem<TKV>::load(kr, d);
         s = dot * scale_log2;
       }
       const float cmax = wave_max(s);
@@ -526,11 +527,11 @@ __global__ void __launch_bounds__(64) attend_generic_kernel(
       for (int r = 0; r < kR; ++r) acc[r] *= alpha;
       for (int jj = 0; jj < nk; ++jj) {
         const float pj = p_s[jj];
-        const T* vr = vc + row_s[jj];
+        const TKV* vr = vc + row_s[jj];
 #pragma unroll
         for (int r = 0; r < kR; ++r) {
           const int d = lane + 64 * r;
-          if (d < D) acc[r] += pj * Elem<T>::load(vr, d);
+          if (d < D) acc[r] += pj * Elem<TKV>::load(vr, d);
         }
       }
       __syncthreads();
@@ -1629,9 +1630,9 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
 // re-read the last key (finite values) and get weight 0.
 constexpr int kShortCtx = 2048;
 
-template <typename T, int D, int REP>
+template <typename TKV, int D, int REP>
 struct ShortLds {
-  static constexpr int kVE = 16 / (int)sizeof(T);  // elements per 16-byte load
+  static constexpr int kVE = 16 / (int)sizeof(TKV);  // cache elements per 16-byte load
   float q[REP][D];          // query heads, pre-scaled to the log2 domain
   float p[4][REP][64];      // per wavefront: the chunk's weights
   float red[4][64][kVE];    // per wavefront and lane: one head's PV sums
@@ -1705,12 +1706,14 @@ __device__ __forceinline__ void widen16(const uint4& v, float* r) {
   }
 }
 
-template <typename T, int D, int REP>
+// T: query and output elements, TKV: cache elements.
+template <typename T, typename TKV, int D, int REP>
 __global__ void __launch_bounds__(256) attend_short_decode_kernel(
-    T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const T* kc, const T* vc,
-    const int32_t* __restrict__ bt, int bt_stride, const int32_t* __restrict__ seq_lens,
-    const int32_t* __restrict__ qsl, int Hkv, int bs_log2, float scale_log2) {
-  using Lds = ShortLds<T, D, REP>;
+    T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const TKV* kc,
+    const TKV* vc, const int32_t* __restrict__ bt, int bt_stride,
+    const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int Hkv, int bs_log2,
+    float scale_log2) {
+  using Lds = ShortLds<TKV, D, REP>;
   constexpr int VE = Lds::kVE;
   static_assert(D % VE == 0 && D <= 64, "head_dim");
   constexpr int NC = D / VE;               // 16-byte chunks per head row
@@ -1735,8 +1738,8 @@ __global__ void __launch_bounds__(256) attend_short_decode_kernel(
   }
   __syncthreads();
   const int64_t slot_stride = (int64_t)Hkv * D;
-  const T* kg = kc + (int64_t)g * D;
-  const T* vg = vc + (int64_t)g * D;
+  const TKV* kg = kc + (int64_t)g * D;
+  const TKV* vg = vc + (int64_t)g * D;
   auto slot_of = [&](int k) {
     return ((int64_t)s.tbl[k >> bs_log2] << bs_log2) + (k & bs_mask);
   };
@@ -1754,7 +1757,7 @@ __global__ void __launch_bounds__(256) attend_short_decode_kernel(
     if (base >= c) break;  // wavefront-uniform; later chunks start later still
     // every load of the chunk first: the lane's K row and its V chunks
     float kr[D];
-    load_row<T, D>(kg + slot_of(min(base + lane, c - 1)) * slot_stride, kr);
+    load_row<TKV, D>(kg + slot_of(min(base + lane, c - 1)) * slot_stride, kr);
     uint4 vraw[KPL];
 #pragma unroll
     for (int j = 0; j < KPL; ++j) {
@@ -1786,7 +1789,7 @@ __global__ void __launch_bounds__(256) attend_short_decode_kernel(
     for (int j = 0; j < KPL; ++j) {
       const int kk = pg + G * j;
       float v[VE];
-      widen16<T>(vraw[j], v);
+      widen16<TKV>(vraw[j], v);
 #pragma unroll
       for (int h = 0; h < REP; ++h) {
         const float w = kk < 64 ? s.p[wave][h][kk] : 0.f;
@@ -1997,7 +2000,9 @@ struct Args {
 };
 
 int check_args(const Args& a, const void* ws, size_t ws_bytes, bool need_kv) {
-  VL_CHECK_ARG(a.dtype == VL_DTYPE_F32 || a.dtype == VL_DTYPE_BF16, "bad dtype %d", a.dtype);
+  VL_CHECK_ARG(a.dtype == VL_DTYPE_F32 || a.dtype == VL_DTYPE_BF16 ||
+                   a.dtype == VL_DTYPE_F32_BF16KV,
+               "bad dtype %d", a.dtype);
   VL_CHECK_ARG(a.S >= 0 && a.T >= 0, "bad batch size");
   VL_CHECK_ARG(a.H > 0 && a.Hkv > 0 && a.H % a.Hkv == 0,
                "num_heads must be a positive multiple of num_kv_heads");
@@ -2142,15 +2147,15 @@ inline bool short_decode(const Args& a, int max_q, int max_ctx) {
          (rep == 1 || rep == 2 || rep == 4 || rep == 8) && (int64_t)a.S * a.Hkv <= (1 << 30);
 }
 
-template <typename T, int D>
+template <typename T, typename TKV, int D>
 int launch_short_decode_d(const Args& a, float sl2, hipStream_t st) {
   const int rep = a.H / a.Hkv;
   const int grid = a.S * a.Hkv;
   if (grid == 0) return VL_OK;
   const int bs_log2 = __builtin_ctz((unsigned)a.bs);
 #define VL_SHORT(REP)                                                                        \
-  attend_short_decode_kernel<T, D, REP><<<grid, 256, 0, st>>>(                               \
-      (T*)a.out, (const T*)a.query, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.bt,        \
+  attend_short_decode_kernel<T, TKV, D, REP><<<grid, 256, 0, st>>>(                          \
+      (T*)a.out, (const T*)a.query, a.q_stride, (const TKV*)a.kc, (const TKV*)a.vc, a.bt,    \
       a.bt_stride, a.seq_lens, a.qsl, a.Hkv, bs_log2, sl2)
   switch (rep) {
     case 1: VL_SHORT(1); break;
@@ -2163,25 +2168,30 @@ int launch_short_decode_d(const Args& a, float sl2, hipStream_t st) {
   return VL_OK;
 }
 
-template <typename T>
+template <typename T, typename TKV>
 int launch_short_decode(const Args& a, float sl2, hipStream_t st) {
   switch (a.D) {
-    case 16: return launch_short_decode_d<T, 16>(a, sl2, st);
-    case 32: return launch_short_decode_d<T, 32>(a, sl2, st);
-    case 48: return launch_short_decode_d<T, 48>(a, sl2, st);
-    default: return launch_short_decode_d<T, 64>(a, sl2, st);
+    case 16: return launch_short_decode_d<T, TKV, 16>(a, sl2, st);
+    case 32: return launch_short_decode_d<T, TKV, 32>(a, sl2, st);
+    case 48: return launch_short_decode_d<T, TKV, 48>(a, sl2, st);
+    default: return launch_short_decode_d<T, TKV, 64>(a, sl2, st);
   }
 }
 
-template <typename T>
+// T: query and output elements, TKV: cache elements (fp32 / fp32, bf16 /
+// bf16, or fp32 / bf16; the fast and tile kernels take one type).
+template <typename T, typename TKV>
 int do_run(const Args& a, int max_q, int min_q, int max_ctx, void* ws, size_t ws_bytes,
            hipStream_t st) {
   const float sl2 = a.scale * kLog2e;
-  if (short_decode(a, max_q, max_ctx)) return launch_short_decode<T>(a, sl2, st);  // no plan
+  if (short_decode(a, max_q, max_ctx)) return launch_short_decode<T, TKV>(a, sl2, st);  // no plan
   const Layout L = make_layout(ws, ws_bytes, a.S, a.D);
   const int ncu = vl_num_cus();
-  const bool fast = fast_shape(a.dtype, a.H, a.Hkv, a.D, a.bs);
-  if (fast) {
+  constexpr bool one_type = std::is_same<T, TKV>::value;
+  const bool fast = one_type && fast_shape(a.dtype, a.H, a.Hkv, a.D, a.bs);
+  if constexpr (!one_type) {
+    // generic kernel below
+  } else if (fast) {
     if (max_q == 1) {  // every sequence is a decode
       attend_decode_bf16_kernel<<<decode_grid(), 256, 0, st>>>(VL_ATTN_LAUNCH_ARGS(uint16_t),
                                                                L.hdr, L.hdr + 8);
@@ -2208,9 +2218,10 @@ int do_run(const Args& a, int max_q, int min_q, int max_ctx, void* ws, size_t ws
   } else if (tile_shape(a.dtype, a.D, a.bs)) {
     int rc = launch_tile<T>(a, L, sl2, max_q, st);
     if (rc) return rc;
-  } else {
-    attend_generic_kernel<T><<<ncu * 16, 64, 0, st>>>(
-        (T*)a.out, (const T*)a.query, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.bt,
+  }
+  if (!one_type || (!fast && !tile_shape(a.dtype, a.D, a.bs))) {
+    attend_generic_kernel<T, TKV><<<ncu * 16, 64, 0, st>>>(
+        (T*)a.out, (const T*)a.query, a.q_stride, (const TKV*)a.kc, (const TKV*)a.vc, a.bt,
         a.bt_stride, a.seq_lens, a.qsl, a.S, a.H, a.Hkv, a.D, a.bs, sl2, L.hdr, L.gen_off,
         L.nparts, L.split_base, L.ml, L.po);
     VL_CHECK_LAUNCH();
@@ -2225,8 +2236,12 @@ int do_run(const Args& a, int max_q, int min_q, int max_ctx, void* ws, size_t ws
 
 int dispatch_run(const Args& a, int max_q, int min_q, int max_ctx, void* ws, size_t ws_bytes,
                  hipStream_t st) {
-  return a.dtype == VL_DTYPE_F32 ? do_run<float>(a, max_q, min_q, max_ctx, ws, ws_bytes, st)
-                                 : do_run<uint16_t>(a, max_q, min_q, max_ctx, ws, ws_bytes, st);
+  switch (a.dtype) {
+    case VL_DTYPE_F32: return do_run<float, float>(a, max_q, min_q, max_ctx, ws, ws_bytes, st);
+    case VL_DTYPE_BF16:
+      return do_run<uint16_t, uint16_t>(a, max_q, min_q, max_ctx, ws, ws_bytes, st);
+    default: return do_run<float, uint16_t>(a, max_q, min_q, max_ctx, ws, ws_bytes, st);
+  }
 }
 
 }  // namespace

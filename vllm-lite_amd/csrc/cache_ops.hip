@@ -54,9 +54,11 @@ __device__ __forceinline__ void rotate_pair(float e, float o, float c, float s, 
   *oo = es + oc;
 }
 
+// TC: cache elements (float, or uint16_t bf16 bits rounded to nearest even)
+template <typename TC>
 __global__ void __launch_bounds__(256) rope_and_cache_kernel(
     const float* __restrict__ qkv, int64_t qkv_stride, float* __restrict__ q_out,
-    float* __restrict__ kc, float* __restrict__ vc, const int32_t* __restrict__ positions,
+    TC* __restrict__ kc, TC* __restrict__ vc, const int32_t* __restrict__ positions,
     const int32_t* __restrict__ slots, const float* __restrict__ cos_t,
     const float* __restrict__ sin_t, int64_t num_tokens, int nh, int nkv, int hd) {
   const int half = hd >> 1;
@@ -75,18 +77,20 @@ __global__ void __launch_bounds__(256) rope_and_cache_kernel(
       const float* src = (i < q_pairs ? row : row + nh * hd) + head * hd + 2 * pr;
       float oe, oo;
       rotate_pair(src[0], src[1], c[pr], s[pr], &oe, &oo);
-      float* dst = (i < q_pairs) ? q_out + t * (int64_t)nh * hd + head * hd + 2 * pr
-                                 : (slot >= 0 ? kc + (int64_t)slot * v_elems + head * hd + 2 * pr
-                                              : nullptr);
-      if (dst) {
+      if (i < q_pairs) {
+        float* dst = q_out + t * (int64_t)nh * hd + head * hd + 2 * pr;
         dst[0] = oe;
         dst[1] = oo;
+      } else if (slot >= 0) {
+        TC* dst = kc + (int64_t)slot * v_elems + head * hd + 2 * pr;
+        Elem<TC>::store(dst, 0, oe);
+        Elem<TC>::store(dst, 1, oo);
       }
     }
     if (slot >= 0) {
       const float* vs = row + (nh + nkv) * hd;
-      float* vd = vc + (int64_t)slot * v_elems;
-      for (int i = threadIdx.x; i < v_elems; i += blockDim.x) vd[i] = vs[i];
+      TC* vd = vc + (int64_t)slot * v_elems;
+      for (int i = threadIdx.x; i < v_elems; i += blockDim.x) Elem<TC>::store(vd, i, vs[i]);
     }
   }
 }
@@ -176,10 +180,12 @@ extern "C" int vl_copy_blocks(void* key_cache, void* value_cache, const int32_t*
 }
 
 extern "C" int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_out,
-                                 float* key_cache, float* value_cache, const int32_t* positions,
+                                 void* key_cache, void* value_cache, const int32_t* positions,
                                  const int32_t* slot_mapping, const float* cos_table,
                                  const float* sin_table, int64_t num_tokens, int num_heads,
-                                 int num_kv_heads, int head_dim, void* stream) {
+                                 int num_kv_heads, int head_dim, int cache_dtype, void* stream) {
+  VL_CHECK_ARG(cache_dtype == VL_DTYPE_F32 || cache_dtype == VL_DTYPE_BF16, "bad cache dtype %d",
+               cache_dtype);
   VL_CHECK_ARG(num_tokens >= 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0 &&
                    head_dim % 2 == 0,
                "bad shape");
@@ -190,9 +196,14 @@ extern "C" int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_
                    cos_table && sin_table,
                "null pointer");
   const int grid = (int)(num_tokens < 65536 ? num_tokens : 65536);
-  rope_and_cache_kernel<<<grid, 128, 0, (hipStream_t)stream>>>(
-      qkv, qkv_stride, q_out, key_cache, value_cache, positions, slot_mapping, cos_table,
-      sin_table, num_tokens, num_heads, num_kv_heads, head_dim);
+  if (cache_dtype == VL_DTYPE_F32)
+    rope_and_cache_kernel<float><<<grid, 128, 0, (hipStream_t)stream>>>(
+        qkv, qkv_stride, q_out, (float*)key_cache, (float*)value_cache, positions, slot_mapping,
+        cos_table, sin_table, num_tokens, num_heads, num_kv_heads, head_dim);
+  else
+    rope_and_cache_kernel<uint16_t><<<grid, 128, 0, (hipStream_t)stream>>>(
+        qkv, qkv_stride, q_out, (uint16_t*)key_cache, (uint16_t*)value_cache, positions,
+        slot_mapping, cos_table, sin_table, num_tokens, num_heads, num_kv_heads, head_dim);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }

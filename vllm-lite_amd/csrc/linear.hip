@@ -57,14 +57,22 @@ __device__ __forceinline__ void rotate_pair_f32(float e, float o, float c, float
 // Where MODE 3 puts the columns [q | k | v] of a fused QKV projection.
 struct RopeCache {
   float* q_out;  // [rows, nh * hd]
-  float* kc;     // [slots, nkv * hd]
-  float* vc;
+  void* kc;      // [slots, nkv * hd], float or (kv_bf16) bf16 bits
+  void* vc;
   const int32_t* positions;
   const int32_t* slots;
   const float* cos_t;  // [max_pos, hd / 2]
   const float* sin_t;
   int nh, nkv, hd;
+  int kv_bf16;   // caches hold bf16, each value rounded to nearest even
 };
+
+__device__ __forceinline__ void store_cache(void* cache, int64_t i, float v, int bf16) {
+  if (bf16)
+    static_cast<uint16_t*>(cache)[i] = f32_to_bf16(v);
+  else
+    static_cast<float*>(cache)[i] = v;
+}
 
 // MODE 0: out = f(x) @ w; 1: out += f(x) @ w; 2: out = silu(f(x) @ w[:, :n]) *
 // (f(x) @ w[:, up_off : up_off + n]); 3: f(x) @ w is a [q | k | v] row: q and k
@@ -264,9 +272,9 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
       if (col < qd)
         rc.q_out[(int64_t)r * qd + col] = val;
       else if (slot >= 0)
-        rc.kc[(int64_t)slot * kd + base] = val;
+        store_cache(rc.kc, (int64_t)slot * kd + base, val, rc.kv_bf16);
     } else if (slot >= 0) {
-      rc.vc[(int64_t)slot * kd + (col - qd - kd)] = v[0];
+      store_cache(rc.vc, (int64_t)slot * kd + (col - qd - kd), v[0], rc.kv_bf16);
     }
   }
 }
@@ -330,14 +338,17 @@ extern "C" int vl_linear_rows(float* out, int64_t out_stride, const float* x, in
 #undef VL_LINEAR_K
 }
 
-extern "C" int vl_qkv_rope_cache(float* q_out, float* key_cache, float* value_cache,
+extern "C" int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cache,
                                  const float* x, int64_t x_stride, const int32_t* row_index,
                                  float* x_out, const float* weight,
                                  int64_t weight_stride, int weight_layout,
                                  const float* norm_weight, float eps,
                                  const int32_t* positions, const int32_t* slot_mapping,
                                  const float* cos_table, const float* sin_table, int rows, int k,
-                                 int num_heads, int num_kv_heads, int head_dim, void* stream) {
+                                 int num_heads, int num_kv_heads, int head_dim, int cache_dtype,
+                                 void* stream) {
+  VL_CHECK_ARG(cache_dtype == VL_DTYPE_F32 || cache_dtype == VL_DTYPE_BF16, "bad cache dtype %d",
+               cache_dtype);
   VL_CHECK_ARG(rows >= 0 && rows <= kRowsMax, "rows must be in 0..%d", kRowsMax);
   VL_CHECK_ARG(k > 0 && k % 16 == 0 && k <= 1024, "k must be a multiple of 16, at most 1024");
   VL_CHECK_ARG(num_heads > 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0,
@@ -358,6 +369,7 @@ extern "C" int vl_qkv_rope_cache(float* q_out, float* key_cache, float* value_ca
   rc.q_out = q_out, rc.kc = key_cache, rc.vc = value_cache, rc.positions = positions;
   rc.slots = slot_mapping, rc.cos_t = cos_table, rc.sin_t = sin_table;
   rc.nh = num_heads, rc.nkv = num_kv_heads, rc.hd = head_dim;
+  rc.kv_bf16 = cache_dtype == VL_DTYPE_BF16;
   hipStream_t st = (hipStream_t)stream;
   const bool nrm = norm_weight != nullptr;
 #define VL_QKV(NORM, KM) \

@@ -43,6 +43,14 @@ class CacheConfig:
     block_size: int = 16
     num_blocks: int = 1024
     enable_prefix_caching: bool = True
+    # element type of the K/V cache: "float32" (the reference's), or
+    # "bfloat16" (half the cache bytes; K/V rounded to nearest even when
+    # written, everything else stays fp32)
+    kv_dtype: str = "float32"
+
+    def __post_init__(self):
+        if self.kv_dtype not in ("float32", "bfloat16"):
+            raise ValueError("kv_dtype must be float32 or bfloat16")
 
     @property
     def max_cached_tokens(self) -> int:

@@ -175,8 +175,10 @@ class HipRunner(ModelRunner):
             self.sin = torch.from_numpy(sin).to(self.device)
             slots = cache_cfg.num_blocks * cache_cfg.block_size
             shape = (mc.n_layers, slots, mc.n_kv_heads, mc.head_dim)
-            self.cache_k = torch.zeros(shape, dtype=torch.float32, device=self.device)
-            self.cache_v = torch.zeros(shape, dtype=torch.float32, device=self.device)
+            kv = torch.bfloat16 if getattr(cache_cfg, "kv_dtype", "float32") == "bfloat16" \
+                else torch.float32
+            self.cache_k = torch.zeros(shape, dtype=kv, device=self.device)
+            self.cache_v = torch.zeros(shape, dtype=kv, device=self.device)
         self.W = max(1, -(-mc.max_seq_len // self.block_size))
         self._buf = 0  # which of the two pinned staging / id buffers the next launch uses
         self._cap_T = 0
@@ -195,7 +197,7 @@ class HipRunner(ModelRunner):
 
     @property
     def cache_bytes(self) -> int:
-        return (self.cache_k.numel() + self.cache_v.numel()) * 4
+        return (self.cache_k.numel() + self.cache_v.numel()) * self.cache_k.element_size()
 
     def execute(self, out) -> Tuple[np.ndarray, List[Tuple[int, int]]]:
         with torch.cuda.device(self.device), torch.cuda.stream(self.stream):

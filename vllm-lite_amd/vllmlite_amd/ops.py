@@ -17,8 +17,8 @@ import torch
 
 from .build import LIB_PATH
 
-F32, BF16 = 0, 1
-ABI_VERSION = 3  # vl_abi_version() of the library these signatures describe
+F32, BF16, F32_BF16KV = 0, 1, 2  # VL_DTYPE_*: F32_BF16KV = fp32 query / out over bf16 caches
+ABI_VERSION = 4  # vl_abi_version() of the library these signatures describe
 _c_void_p = ctypes.c_void_p
 _i32, _i64, _f32, _size = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
 
@@ -50,7 +50,7 @@ SIGNATURES = {
                            _c_void_p]),
     "vl_silu_mul": (_i32, [_c_void_p, _c_void_p, _i64, _i32, _c_void_p]),
     "vl_rope_and_cache": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                                 _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32,
+                                 _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32, _i32,
                                  _c_void_p]),
     "vl_greedy_verify": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i32,
                                 _c_void_p, _c_void_p, _i32, _c_void_p]),
@@ -60,7 +60,7 @@ SIGNATURES = {
     "vl_qkv_rope_cache": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
                                  _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _f32, _c_void_p,
                                  _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32,
-                                 _c_void_p]),
+                                 _i32, _c_void_p]),
     "vl_resolve_tokens": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p]),
 }
 
@@ -106,6 +106,20 @@ def _dtype_code(t: torch.Tensor) -> int:
     if t.dtype == torch.bfloat16:
         return BF16
     raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def _attn_dtype(query: torch.Tensor, cache: torch.Tensor) -> int:
+    """VL_DTYPE_* of an attention call: the query's, or F32_BF16KV for an
+    fp32 query over bf16 caches."""
+    if query.dtype == torch.float32 and cache.dtype == torch.bfloat16:
+        return F32_BF16KV
+    return _dtype_code(query)
+
+
+def _cache_dtype(key_cache: torch.Tensor, value_cache: torch.Tensor) -> int:
+    _need(key_cache.dtype == value_cache.dtype and key_cache.dtype in (torch.float32, torch.bfloat16),
+          "caches must both be fp32 or both bf16")
+    return _dtype_code(key_cache)
 
 
 def _need(cond: bool, msg: str) -> None:
@@ -182,7 +196,10 @@ def _attn_check(out, query, key_cache, value_cache, block_tables, seq_lens, quer
     _need(key_cache.dim() == 3 and key_cache.shape == value_cache.shape and key_cache.shape[2] == D,
           "cache shape mismatch")
     _need(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
-    _need(key_cache.dtype == query.dtype == value_cache.dtype, "dtype mismatch")
+    _need(key_cache.dtype == value_cache.dtype and
+          (key_cache.dtype == query.dtype or
+           (query.dtype == torch.float32 and key_cache.dtype == torch.bfloat16)),
+          "dtype mismatch (caches of the query dtype, or bf16 under an fp32 query)")
     hkv = key_cache.shape[1]
     _need(H % hkv == 0, "num_heads must be a multiple of num_kv_heads")
     for t, n in ((block_tables, "block_tables"), (seq_lens, "seq_lens"),
@@ -200,7 +217,8 @@ def _attn_args(out, query, key_cache, value_cache, block_tables, seq_lens, query
                T, H, hkv, D, S):
     return (_ptr(out), _ptr(query), query.stride(0), _ptr(key_cache), _ptr(value_cache),
             _ptr(block_tables), block_tables.stride(0), _ptr(seq_lens), _ptr(query_start_loc),
-            S, T, H, hkv, D, block_size, float(scale), _dtype_code(query), int(max_query_len),
+            S, T, H, hkv, D, block_size, float(scale), _attn_dtype(query, key_cache),
+            int(max_query_len),
             int(min_query_len), int(max_context_len), _ptr(workspace), workspace.numel() * workspace.element_size(), _stream())
 
 
@@ -235,7 +253,7 @@ def paged_attention_plan(query: torch.Tensor, key_cache: torch.Tensor, seq_lens:
     _need(query_start_loc.numel() == S + 1, "query_start_loc length")
     _need(workspace.is_cuda and workspace.data_ptr() % 256 == 0, "workspace must be 256-aligned")
     _check(lib().vl_paged_attention_plan(_ptr(seq_lens), _ptr(query_start_loc), S, T, H, hkv, D,
-                                         block_size, _dtype_code(query), _ptr(workspace),
+                                         block_size, _attn_dtype(query, key_cache), _ptr(workspace),
                                          workspace.numel() * workspace.element_size(), _stream()),
            "vl_paged_attention_plan")
 
@@ -282,7 +300,7 @@ def paged_attention_noalloc(out, query, key_cache, value_cache, block_tables, se
     _check(lib().vl_paged_attention_noalloc(
         _ptr(out), _ptr(query), query.stride(0), _ptr(key_cache), _ptr(value_cache),
         _ptr(block_tables), block_tables.stride(0), _ptr(seq_lens), _ptr(query_start_loc), S, T,
-        H, key_cache.shape[1], D, block_size, float(scale), _dtype_code(query),
+        H, key_cache.shape[1], D, block_size, float(scale), _attn_dtype(query, key_cache),
         int(max_query_len), int(min_query_len), int(max_context_len), _stream()),
         "vl_paged_attention_noalloc")
 
@@ -372,8 +390,10 @@ def qkv_rope_cache(q_out: torch.Tensor, key_cache: torch.Tensor, value_cache: to
     rows = q_out.shape[0]
     _need(row_index is not None or x.shape[0] >= rows, "x has too few rows")
     _need(x_out is None or (x_out.is_contiguous() and x_out.shape[1] == k), "x_out shape mismatch")
-    for t in (q_out, key_cache, value_cache, x, weight, cos, sin):
+    for t in (q_out, x, weight, cos, sin):
         _need(t.dtype == torch.float32 and t.stride(-1) == 1, "fp32 row-major tensors required")
+    _need(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
+    cdt = _cache_dtype(key_cache, value_cache)
     _need(positions.numel() >= rows and slot_mapping.numel() >= rows, "shape mismatch")
     tiles, wstride = _weight_layout(weight, k, (num_heads + 2 * num_kv_heads) * head_dim, 1)
     _check(lib().vl_qkv_rope_cache(_ptr(q_out), _ptr(key_cache), _ptr(value_cache), _ptr(x),
@@ -381,7 +401,7 @@ def qkv_rope_cache(q_out: torch.Tensor, key_cache: torch.Tensor, value_cache: to
                                    wstride, WEIGHT_TILES16 if tiles else WEIGHT_ROWS,
                                    _ptr(norm_weight),
                                    float(eps), _ptr(positions), _ptr(slot_mapping), _ptr(cos),
-                                   _ptr(sin), rows, k, num_heads, num_kv_heads, head_dim,
+                                   _ptr(sin), rows, k, num_heads, num_kv_heads, head_dim, cdt,
                                    _stream()), "vl_qkv_rope_cache")
 
 
@@ -401,15 +421,17 @@ def rope_and_cache(qkv: torch.Tensor, q_out: torch.Tensor, key_cache: torch.Tens
     _need(qkv.stride(1) == 1 and qkv.shape[1] >= (num_heads + 2 * num_kv_heads) * head_dim,
           "qkv rows must hold q|k|v")
     _need(q_out.shape == (T, num_heads, head_dim) and q_out.is_contiguous(), "q_out shape")
-    _need(key_cache.shape[1:] == (num_kv_heads, head_dim) and key_cache.is_contiguous(),
-          "cache shape")
+    _need(key_cache.shape[1:] == (num_kv_heads, head_dim) and key_cache.is_contiguous() and
+          value_cache.shape == key_cache.shape and value_cache.is_contiguous(), "cache shape")
+    _need(qkv.dtype == q_out.dtype == torch.float32, "qkv and q_out are fp32")
+    cdt = _cache_dtype(key_cache, value_cache)
     _dev_i32(positions, "positions")
     _dev_i32(slot_mapping, "slot_mapping")
     _need(cos.shape == sin.shape and cos.shape[1] == head_dim // 2, "rope table shape")
     _check(lib().vl_rope_and_cache(_ptr(qkv), qkv.stride(0), _ptr(q_out), _ptr(key_cache),
                                    _ptr(value_cache), _ptr(positions), _ptr(slot_mapping),
                                    _ptr(cos), _ptr(sin), T, num_heads, num_kv_heads, head_dim,
-                                   _stream()), "vl_rope_and_cache")
+                                   cdt, _stream()), "vl_rope_and_cache")
 
 
 # ------------------------------------------------------------------ K5 -----
