@@ -601,8 +601,12 @@ __device__ __forceinline__ uint4 load16(const void* p) {
 // batch), an ordinary one when the sequence's other row blocks re-read them
 // from the cache (long prefill chunks: streaming loads there measured 281 ->
 // 298 us)
-__device__ __forceinline__ uint4 load16_kv(const void* p, bool stream) {
-  if (stream)
+// kStream: a non-temporal load (data read once). A compile-time choice: a
+// runtime one puts every load in a branch of its own, and the compiler then
+// cannot issue a tile's loads (and the block-id loads they need) together.
+template <bool kStream>
+__device__ __forceinline__ uint4 load16_kv(const void* p) {
+  if constexpr (kStream)
     return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)));
   return load16(p);
 }
@@ -798,7 +802,9 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
     const bool unit_blocks = (1 << bs_log2) >= kUnitKeys;
     const uint32_t k_thr_off =
         (uint32_t)(tid / Lds::kChunks) * (uint32_t)slot_stride + (tid % Lds::kChunks) * 8;
-    auto prefetch = [&](int k0) {
+    // nt: std::true_type / std::false_type, non-temporal loads or not
+    auto prefetch_as = [&](int k0, auto nt) {
+      constexpr bool kNt = decltype(nt)::value;
       if constexpr (kBf16) {
         if (unit_blocks) {
           // the units' block ids first (scalar loads, issued together), then
@@ -815,11 +821,10 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
           for (int r = 0; r < Lds::kUnits; ++r) {
             const int kr = min(k0 + kUnitKeys * r, klast);
             const int64_t boff = (int64_t)((uint64_t)blk[r] * blk_elems) + kv_off;
-            pk[r] = load16_kv(kc + boff + ((uint32_t)(kr & bs_mask) * (uint32_t)slot_stride + k_thr_off),
-                              stream_kv);
+            pk[r] = load16_kv<kNt>(kc + boff + ((uint32_t)(kr & bs_mask) * (uint32_t)slot_stride +
+                                                k_thr_off));
             const int vkey = min(kr + tk, kend_wg - 1);
-            pv[r] = load16_kv(vc + boff + ((uint32_t)(vkey & bs_mask) * (uint32_t)slot_stride + tc),
-                              stream_kv);
+            pv[r] = load16_kv<kNt>(vc + boff + ((uint32_t)(vkey & bs_mask) * (uint32_t)slot_stride + tc));
           }
         } else {
 #pragma unroll
@@ -827,8 +832,8 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
             const int idx = tid + 256 * r;
             const int kk = idx / Lds::kChunks, cc = idx - kk * Lds::kChunks;
             const int64_t off = row_of(min(k0 + kk, kend_wg - 1)) + cc * 8;
-            pk[r] = load16_kv(kc + off, stream_kv);
-            pv[r] = load16_kv(vc + off, stream_kv);
+            pk[r] = load16_kv<kNt>(kc + off);
+            pv[r] = load16_kv<kNt>(vc + off);
           }
         }
       } else {
@@ -843,6 +848,12 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
           pv[r] = ok ? *reinterpret_cast<const uint4*>(vc + off) : make_uint4(0, 0, 0, 0);
         }
       }
+    };
+    auto prefetch = [&](int k0) {  // one uniform branch per tile, around branch-free loads
+      if (stream_kv)
+        prefetch_as(k0, std::true_type{});
+      else
+        prefetch_as(k0, std::false_type{});
     };
     auto stage = [&](Lds& b) {  // prefetch registers -> LDS b
       if constexpr (kBf16) {
@@ -879,17 +890,43 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
     auto compute = [&](const Lds& b, int k0) {
       // ---- S^T = K Q^T for the key subtiles
       AccT sc[kST];
+      if constexpr (kW) {
+        // every K operand of a subtile read before its MFMAs, the next
+        // subtile's reads paired with them: the LDS latency is paid once per
+        // subtile instead of once per two MFMAs (the compiler's own order
+        // kept two reads in flight)
+        uint4 kw[2][kKS];
 #pragma unroll
-      for (int t = 0; t < kST; ++t) {
+        for (int s = 0; s < kKS; ++s)
+          kw[0][s] = *reinterpret_cast<const uint4*>(&b.k[col * Lds::kRow + 16 * s + 8 * grp]);
+#pragma unroll
+        for (int t = 0; t < kST; ++t) {
+#pragma unroll
+          for (int r = 0; r < kCV; ++r) sc[t][r] = 0.f;
+#pragma unroll
+          for (int s = 0; s < kKS; ++s) {
+            if (t + 1 < kST)
+              kw[(t + 1) & 1][s] = *reinterpret_cast<const uint4*>(
+                  &b.k[(32 * (t + 1) + col) * Lds::kRow + 16 * s + 8 * grp]);
+            sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kw[t & 1][s]),
+                                                            qop[s], sc[t], 0, 0, 0);
+          }
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, kKS, 0);  // subtile 0's reads
+#pragma unroll
+        for (int i = 0; i < kKS * (kST - 1); ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a read of the next subtile
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, kKS, 0);  // the last subtile's MFMAs
+      }
+#pragma unroll
+      for (int t = 0; t < kST && !kW; ++t) {
 #pragma unroll
         for (int r = 0; r < kCV; ++r) sc[t][r] = 0.f;
 #pragma unroll
         for (int s = 0; s < kKS; ++s) {
           if constexpr (kW) {
-            const uint4 w = *reinterpret_cast<const uint4*>(
-                &b.k[(32 * t + col) * Lds::kRow + 16 * s + 8 * grp]);
-            sc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, w),
-                                                            qop[s], sc[t], 0, 0, 0);
           } else if constexpr (kBf16) {
             const uint4 w = *reinterpret_cast<const uint4*>(
                 &b.k[(16 * t + col) * Lds::kRow + 32 * s + 8 * grp]);

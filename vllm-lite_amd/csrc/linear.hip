@@ -113,6 +113,28 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
   // the compiler turn each load into a branch that waits for it.)
   float wb[kSlices][kSteps];
   const float colmask = c0 + m < N ? 1.f : 0.f;
+  // ---- the epilogue's own global reads, issued now so that they arrive with
+  // the weights instead of after the reduction: thread t writes row t / 16,
+  // column c0 + t % 16; the residual it adds to (MODE 1), or its slot and
+  // its RoPE table entries (MODE 3)
+  const int er = tid / kCols, ec = tid - (tid / kCols) * kCols;
+  const bool e_ok = er < M && c0 + ec < N;
+  float e_resid = 0.f, e_cos = 0.f, e_sin = 0.f;
+  int e_slot = -1;
+  if constexpr (MODE == 1) {
+    if (e_ok) e_resid = out[(int64_t)er * ldo + c0 + ec];
+  } else if constexpr (MODE == 3) {
+    if (e_ok) {
+      const int col = c0 + ec, qd = rc.nh * rc.hd, kd = rc.nkv * rc.hd;
+      e_slot = rc.slots[er];
+      if (col < qd + kd) {
+        const int base = col < qd ? col : col - qd;
+        const int64_t tab = (int64_t)rc.positions[er] * (rc.hd >> 1) + ((base % rc.hd) >> 1);
+        e_cos = rc.cos_t[tab];
+        e_sin = rc.sin_t[tab];
+      }
+    }
+  }
 #pragma unroll
   for (int s = 0; s < kSlices; ++s) {
     if constexpr (TILES) {
@@ -234,8 +256,8 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
     for (int i = 0; i < 4; ++i) red[s][wave][(4 * j + i) * kCols + m] = acc[s][i];
   __syncthreads();
 
-  const int r = tid / kCols, c = tid - r * kCols;
-  if (r >= M || c0 + c >= N) return;
+  const int r = er, c = ec;
+  if (!e_ok) return;
   // the wavefronts' partial sums in wavefront order
   auto total = [&](int s, int e) {
     float t = red[s][0][e];
@@ -249,8 +271,7 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
   if constexpr (MODE == 0) {
     out[(int64_t)r * ldo + c0 + c] = v[0];
   } else if constexpr (MODE == 1) {
-    float* dst = out + (int64_t)r * ldo + c0 + c;
-    *dst = *dst + v[0];
+    out[(int64_t)r * ldo + c0 + c] = e_resid + v[0];
   } else if constexpr (MODE == 2) {
     out[(int64_t)r * ldo + c0 + c] = silu_times_f32(v[0], v[1]);
   } else {
@@ -259,15 +280,12 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
     const int pt = r * kCols + (c ^ 1);
     const float partner = total(0, pt);
     const int col = c0 + c, qd = rc.nh * rc.hd, kd = rc.nkv * rc.hd;
-    const int slot = rc.slots[r];
+    const int slot = e_slot;
     if (col < qd + kd) {
       const int base = col < qd ? col : col - qd;
-      const int d = base % rc.hd, half = rc.hd >> 1;
-      const int64_t tab = (int64_t)rc.positions[r] * half + (d >> 1);
-      const bool odd = d & 1;
+      const bool odd = (base % rc.hd) & 1;
       float oe, oo;
-      rotate_pair_f32(odd ? partner : v[0], odd ? v[0] : partner, rc.cos_t[tab], rc.sin_t[tab],
-                      &oe, &oo);
+      rotate_pair_f32(odd ? partner : v[0], odd ? v[0] : partner, e_cos, e_sin, &oe, &oo);
       const float val = odd ? oo : oe;
       if (col < qd)
         rc.q_out[(int64_t)r * qd + col] = val;
