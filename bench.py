@@ -67,23 +67,28 @@ def median_ms(ev):
     return float(np.median([a.elapsed_time(b) for a, b in ev]))
 
 
-def decode_leg(torch, ops, syn, steps, warmup, profile_only=False):
+def decode_leg(torch, ops, syn, steps, warmup, profile_only=False, layout="token"):
+    """layout "head": the same cache as head-major blocks [blocks, Hkv, 16,
+    D] (one KV head's 16 rows of a block are one 4 KB span)."""
     b = syn.build(torch, syn.decode_256_seqs(0))
     # this step's K/V are part of the cached context for the decode-only batch
     b["kc"][b["slot_mapping"].long()] = b["knew"]
     b["vc"][b["slot_mapping"].long()] = b["vnew"]
+    kc, vc = b["kc"], b["vc"]
+    if layout == "head":
+        kc, vc = syn.to_head_major(kc, syn.BS), syn.to_head_major(vc, syn.BS)
     S = len(b["seqs"])
     out = torch.empty_like(b["q"])
     ws = ops.AttentionWorkspace().get(
         ops.paged_attention_workspace_size(S, S, syn.H, syn.D, int(b["ctx"].max())))
-    ops.paged_attention_plan(b["q"], b["kc"], b["seq_lens"], b["qsl"], syn.BS, ws)
+    ops.paged_attention_plan(b["q"], kc, b["seq_lens"], b["qsl"], syn.BS, ws)
 
     def step():
-        ops.paged_attention_run(out, b["q"], b["kc"], b["vc"], b["bt"], b["seq_lens"], b["qsl"],
+        ops.paged_attention_run(out, b["q"], kc, vc, b["bt"], b["seq_lens"], b["qsl"],
                                 b["scale"], syn.BS, ws, max_query_len=1, min_query_len=1)
 
     def planned_step():
-        ops.paged_attention_plan(b["q"], b["kc"], b["seq_lens"], b["qsl"], syn.BS, ws)
+        ops.paged_attention_plan(b["q"], kc, b["seq_lens"], b["qsl"], syn.BS, ws)
         step()
 
     for _ in range(warmup):
@@ -365,6 +370,7 @@ MIXES = {
     "shared_prefix": (256, False),
     "shared_prefix_forked": (256, True),
     "mixed_bf16_kv": (0, False),  # the 48-request mix over a bf16 K/V cache
+    "mixed_head_major": (0, False),  # ... over head-major cache blocks
 }
 
 
@@ -374,6 +380,8 @@ def mix_config(name):
         cfg = engine_config(False)
         if name == "mixed_bf16_kv":
             cfg.cache.kv_dtype = "bfloat16"
+        if name == "mixed_head_major":
+            cfg.cache.kv_layout = "head"
         return cfg
     return shared_prefix_config(True)
 
@@ -439,7 +447,8 @@ def e2e_leg(name="mixed", repeat=3, cpu=True):
                         (", every request forked once after its first token (copy-on-write of "
                          "its partial shared tail)" if fork else "") +
                         f" (greedy), TinyLlama 6L d384 H8/Hkv4 d_ff1024 fp32"
-                        f"{', bf16 K/V cache' if cfg.cache.kv_dtype == 'bfloat16' else ''}, "
+                        f"{', bf16 K/V cache' if cfg.cache.kv_dtype == 'bfloat16' else ''}"
+                        f"{', head-major cache blocks' if cfg.cache.kv_layout == 'head' else ''}, "
                         "block 16, "
                         f"{cfg.cache.num_blocks} blocks, max_len {cfg.model.max_seq_len}, "
                         "16 seqs, budget 1024"),
@@ -588,6 +597,16 @@ def main():
     torch.cuda.empty_cache()
     line["copy_ceiling_gbs"] = round(copy_ceiling(torch), 1)
     extra = {}
+    # the same batch over head-major cache blocks [blocks, Hkv, 16, D]
+    h = decode_leg(torch, ops, syn, args.steps, args.warmup, layout="head")
+    h.pop("batch")
+    extra["decode_head_major"] = {
+        "kernel_us": round(h["kernel_ms"] * 1e3, 2),
+        "hbm_frac": round(nbytes / (h["kernel_ms"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+        "ms_per_step": round(h["ms_per_step"], 4), "check_rel_err": h["check_rel_err"],
+        "layout": "head-major blocks [blocks, Hkv, 16, D]: a KV head's 16 rows are one 4 KB span"}
+    del h
+    torch.cuda.empty_cache()
     if "mixed" in legs:
         extra["mixed_prefill_decode"] = mixed_leg(torch, ops, syn, 20, 3)
     if "verify" in legs:
@@ -599,6 +618,7 @@ def main():
         extra["e2e_shared_prefix"] = e2e_leg("shared_prefix", cpu=not args.no_cpu)
         extra["e2e_shared_prefix_forked"] = e2e_leg("shared_prefix_forked", cpu=False)
         extra["e2e_bf16_kv_cache"] = e2e_leg("mixed_bf16_kv", cpu=False)
+        extra["e2e_head_major_cache"] = e2e_leg("mixed_head_major", cpu=False)
     line["legs"] = extra
     print(json.dumps(line), flush=True)
 

@@ -14,9 +14,14 @@
  *     the paged-attention calls also take VL_DTYPE_F32_BF16KV: fp32 query
  *     and output over bf16 caches (a bf16 KV cache under an fp32 model).
  *
- * Cache layout is the reference's (vllmlite/runner.py:41-44): one tensor per
- * layer and per K/V of shape [num_slots, num_kv_heads, head_dim], where slot
- * = block_id * block_size + offset (vllmlite/block.py:154-156).
+ * Cache layout (kv_layout): VL_KV_TOKEN_MAJOR is the reference's
+ * (vllmlite/runner.py:41-44), one tensor per layer and per K/V of shape
+ * [num_slots, num_kv_heads, head_dim], where slot = block_id * block_size +
+ * offset (vllmlite/block.py:154-156). VL_KV_HEAD_MAJOR stores the same
+ * blocks as [num_blocks, num_kv_heads, block_size, head_dim]: one KV head's
+ * rows of a block are contiguous (block_size must be a power of two). Slots,
+ * block tables and block copies are the same in both; only the order of the
+ * rows inside a block differs.
  */
 #ifndef VLLMLITE_HIP_H
 #define VLLMLITE_HIP_H
@@ -33,6 +38,8 @@ extern "C" {
 #define VL_DTYPE_F32 0
 #define VL_DTYPE_BF16 1
 #define VL_DTYPE_F32_BF16KV 2
+#define VL_KV_TOKEN_MAJOR 0 /* caches [num_slots, num_kv_heads, head_dim] */
+#define VL_KV_HEAD_MAJOR 1  /* caches [num_blocks, num_kv_heads, block_size, head_dim] */
 #define VL_LINEAR_STORE 0      /* vl_linear_rows: out = f(x) @ W */
 #define VL_LINEAR_ACCUMULATE 1 /* out += f(x) @ W (the residual add) */
 #define VL_LINEAR_SWIGLU 2     /* out = silu(f(x) @ W[:, :n]) * (f(x) @ W[:, n:2n]) */
@@ -54,12 +61,13 @@ int vl_abi_version(void);
  *   key_cache[slot_mapping[t]] = key[t]; value_cache[slot_mapping[t]] = value[t]
  * for t < num_tokens. key/value rows are [num_kv_heads, head_dim] contiguous,
  * `key_stride`/`value_stride` elements apart. A negative slot skips the token.
+ * The caches are kv_layout (block_size is read only for VL_KV_HEAD_MAJOR).
  * Bit-exact copy.
  */
 int vl_reshape_and_cache(const void* key, const void* value, int64_t key_stride,
                          int64_t value_stride, void* key_cache, void* value_cache,
                          const int32_t* slot_mapping, int64_t num_tokens, int num_kv_heads,
-                         int head_dim, int dtype, void* stream);
+                         int head_dim, int dtype, int kv_layout, int block_size, void* stream);
 
 /*
  * K3 copy-on-write block copy. Replaces NumpyRunner._do_cow
@@ -94,8 +102,8 @@ size_t vl_paged_attention_min_workspace(int num_seqs);
  * 0..ceil(seq_lens[i]/block_size)). Query j of a sequence with q_len tokens
  * sits at position seq_lens[i] - q_len + j and attends keys 0..position
  * (causal; a single query sees the whole context). Head h reads KV head
- * h / (num_heads / num_kv_heads). out [num_tokens, num_heads, head_dim],
- * contiguous, dtype of the query. Accumulation is fp32.
+ * h / (num_heads / num_kv_heads). The caches are kv_layout. out [num_tokens,
+ * num_heads, head_dim], contiguous, dtype of the query. Accumulation is fp32.
  * Launch hints, each 0 when unknown: max_query_len and min_query_len bound
  * the query count of the sequences with at least one query, max_context_len
  * bounds seq_lens. With max_query_len 1 and max_context_len <= 2048, head_dim
@@ -114,9 +122,9 @@ int vl_paged_attention(void* out, const void* query, int64_t query_stride, const
                        int block_table_stride, const int32_t* seq_lens,
                        const int32_t* query_start_loc, int num_seqs, int num_tokens,
                        int num_heads, int num_kv_heads, int head_dim, int block_size,
-                       float scale, int dtype, int max_query_len, int min_query_len,
-                       int max_context_len, void* workspace, size_t workspace_bytes,
-                       void* stream);
+                       float scale, int dtype, int kv_layout, int max_query_len,
+                       int min_query_len, int max_context_len, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /*
  * The two halves of vl_paged_attention, for callers that run several
@@ -125,7 +133,8 @@ int vl_paged_attention(void* out, const void* query, int64_t query_stride, const
  * workspace; _run performs the attention using the plan currently in that
  * workspace, which must come from a _plan call with the same lengths, head
  * counts, head_dim, block_size, dtype and workspace size (stream-ordered before
- * it). vl_paged_attention is _plan followed by _run.
+ * it; the plan does not depend on kv_layout). vl_paged_attention is _plan
+ * followed by _run.
  */
 int vl_paged_attention_plan(const int32_t* seq_lens, const int32_t* query_start_loc,
                             int num_seqs, int num_tokens, int num_heads, int num_kv_heads,
@@ -136,9 +145,9 @@ int vl_paged_attention_run(void* out, const void* query, int64_t query_stride,
                            const int32_t* block_tables, int block_table_stride,
                            const int32_t* seq_lens, const int32_t* query_start_loc, int num_seqs,
                            int num_tokens, int num_heads, int num_kv_heads, int head_dim,
-                           int block_size, float scale, int dtype, int max_query_len,
-                           int min_query_len, int max_context_len, void* workspace,
-                           size_t workspace_bytes, void* stream);
+                           int block_size, float scale, int dtype, int kv_layout,
+                           int max_query_len, int min_query_len, int max_context_len,
+                           void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * 1 if a _run call with these shapes and launch hints reads the plan, 0 if it
@@ -168,8 +177,8 @@ int vl_paged_attention_noalloc(void* out, const void* query, int64_t query_strid
                                const int32_t* seq_lens, const int32_t* query_start_loc,
                                int num_seqs, int num_tokens, int num_heads, int num_kv_heads,
                                int head_dim, int block_size, float scale, int dtype,
-                               int max_query_len, int min_query_len, int max_context_len,
-                               void* stream);
+                               int kv_layout, int max_query_len, int min_query_len,
+                               int max_context_len, void* stream);
 
 /*
  * K4a RMSNorm, optionally fused with the residual add that precedes it
@@ -197,13 +206,14 @@ int vl_silu_mul(float* out, const float* gate_up, int64_t rows, int d_ff, void* 
  * num_heads, head_dim] and rotated k / plain v to the caches at
  * slot_mapping[t] (vllmlite/attention.py:47-49). fp32 arithmetic; the caches
  * hold cache_dtype elements (VL_DTYPE_F32, or VL_DTYPE_BF16: each value
- * rounded to nearest even when stored).
+ * rounded to nearest even when stored) in kv_layout (block_size is read only
+ * for VL_KV_HEAD_MAJOR).
  */
 int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_out, void* key_cache,
                       void* value_cache, const int32_t* positions, const int32_t* slot_mapping,
                       const float* cos_table, const float* sin_table, int64_t num_tokens,
                       int num_heads, int num_kv_heads, int head_dim, int cache_dtype,
-                      void* stream);
+                      int kv_layout, int block_size, void* stream);
 
 /*
  * K6 fp32 projections of the TinyLlama forward for at most 16 token rows
@@ -244,8 +254,8 @@ int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_str
  * read (before the norm) are also written to x_out [rows, k] (the residual
  * stream). weight_layout: VL_WEIGHT_ROWS (row stride weight_stride) or
  * VL_WEIGHT_TILES16 (as for vl_linear_rows). rows <= 16, k a multiple of 16,
- * k <= 1024, head_dim even. fp32; the caches hold cache_dtype elements as for
- * vl_rope_and_cache.
+ * k <= 1024, head_dim even. fp32; the caches hold cache_dtype elements in
+ * kv_layout as for vl_rope_and_cache.
  */
 int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cache, const float* x,
                       int64_t x_stride, const int32_t* row_index, float* x_out,
@@ -253,7 +263,7 @@ int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cache, const fl
                       const float* norm_weight, float eps, const int32_t* positions,
                       const int32_t* slot_mapping, const float* cos_table, const float* sin_table,
                       int rows, int k, int num_heads, int num_kv_heads, int head_dim,
-                      int cache_dtype, void* stream);
+                      int cache_dtype, int kv_layout, int block_size, void* stream);
 
 /*
  * The device side of a step issued before the previous step's tokens reached

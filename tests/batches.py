@@ -63,3 +63,17 @@ def oracle_attention(b, q=None, ck=None, cv=None):
         slots = gather_slots(t, b["bs"], int(b["seq_lens"][i]))
         out[s0:s1] = paged_attention(q[s0:s1], ck, cv, slots, b["Hkv"], b["scale"])
     return out
+
+
+def head_major(cache: np.ndarray, bs: int) -> np.ndarray:
+    """A token-major cache [slots, Hkv, D] rearranged as head-major blocks
+    [blocks, Hkv, bs, D]: the same values, only the order of the rows inside
+    each block differs (slot = block * bs + offset in both)."""
+    s, hkv, d = cache.shape
+    return np.ascontiguousarray(cache.reshape(s // bs, bs, hkv, d).transpose(0, 2, 1, 3))
+
+
+def token_major(cache: np.ndarray) -> np.ndarray:
+    """The inverse of head_major: [blocks, Hkv, bs, D] -> [slots, Hkv, D]."""
+    nb, hkv, bs, d = cache.shape
+    return np.ascontiguousarray(cache.transpose(0, 2, 1, 3).reshape(nb * bs, hkv, d))

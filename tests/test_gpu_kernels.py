@@ -12,7 +12,7 @@ import pytest
 
 torch = pytest.importorskip("torch")
 
-from batches import bf16_round, make_batch, oracle_attention  # noqa: E402
+from batches import bf16_round, head_major, make_batch, oracle_attention, token_major  # noqa: E402
 from parity import BF16_ROW_REL, F32_ROW_REL, assert_rows_close  # noqa: E402
 
 pytestmark = pytest.mark.gpu
@@ -33,14 +33,23 @@ def to_np(t):
     return t.float().cpu().numpy()
 
 
-def run_attention(b, dtype, ws_bytes=None, exact_max_q=True, exact_min_q=True, ctx_hint=False):
+def caches(b, tdt, layout="token"):
+    """The batch's K/V caches on the device, token-major [slots, Hkv, D] or
+    head-major [blocks, Hkv, bs, D]."""
+    if layout == "head":
+        return tuple(dev(head_major(b[n], b["bs"]), tdt) for n in ("k_cache", "v_cache"))
+    return dev(b["k_cache"], tdt), dev(b["v_cache"], tdt)
+
+
+def run_attention(b, dtype, ws_bytes=None, exact_max_q=True, exact_min_q=True, ctx_hint=False,
+                  layout="token"):
     """exact_max_q / exact_min_q / ctx_hint: pass the batch's true query-count
     and context bounds (they choose the launches) or 0 (the kernels decide on
-    the device)."""
+    the device); layout: the caches token-major or head-major."""
     o = ops()
     tdt = torch.float32 if dtype == "f32" else torch.bfloat16
     q = dev(b["q"], tdt)
-    kc, vc = dev(b["k_cache"], tdt), dev(b["v_cache"], tdt)
+    kc, vc = caches(b, tdt, layout)
     out = torch.empty_like(q)
     S, T = len(b["seq_lens"]), b["q"].shape[0]
     if ws_bytes is None:
@@ -83,17 +92,20 @@ def test_reference_grid(q_len, H, Hkv, bs, dtype):
 MIXED = [(1, 1), (1, 37), (5, 40), (17, 17), (1, 300), (64, 700), (3, 1025), (1, 16), (9, 33)]
 
 
+@pytest.mark.parametrize("layout", ["token", "head"])
 @pytest.mark.parametrize("hints", ["both", "max", "none"])
 @pytest.mark.parametrize("shape", [(8, 4, 48), (32, 8, 128), (4, 2, 16), (6, 3, 64)])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_mixed_prefill_decode_one_launch(shape, dtype, hints):
+def test_mixed_prefill_decode_one_launch(shape, dtype, hints, layout):
     """Decodes and multi-query sequences in one call. With both bounds known
     the bf16 fast shapes launch the step kernel alone; with only the maximum,
     the step kernel and the tile kernels (each takes its items from the
-    plan); with neither, the step kernel takes every item."""
+    plan); with neither, the step kernel takes every item. Both cache
+    layouts."""
     H, Hkv, D = shape
     b = make_batch(MIXED, H, Hkv, D, 16, seed=1)
-    got = run_attention(b, dtype, exact_max_q=hints != "none", exact_min_q=hints == "both")
+    got = run_attention(b, dtype, exact_max_q=hints != "none", exact_min_q=hints == "both",
+                        layout=layout)
     check(got, expected(b, dtype), dtype)
 
 
@@ -109,14 +121,16 @@ def test_query_bounds_are_checked():
                           max_query_len=3, min_query_len=4)
 
 
+@pytest.mark.parametrize("layout", ["token", "head"])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_long_context_split_and_small_workspace(dtype):
+def test_long_context_split_and_small_workspace(dtype, layout):
     b = make_batch([(1, 5000), (4, 3000), (1, 70)], 8, 2, 64, 16, seed=2)
     want = expected(b, dtype)
-    check(run_attention(b, dtype), want, dtype)
+    check(run_attention(b, dtype, layout=layout), want, dtype)
     # a workspace with room for the plan only: no context splitting at all
     o = ops()
-    check(run_attention(b, dtype, ws_bytes=o.lib().vl_paged_attention_min_workspace(3)), want, dtype)
+    check(run_attention(b, dtype, ws_bytes=o.lib().vl_paged_attention_min_workspace(3),
+                        layout=layout), want, dtype)
 
 
 def test_bad_arguments_raise():
@@ -130,16 +144,19 @@ def test_bad_arguments_raise():
         o.paged_attention(out, q, kc, kc, dev(b["block_tables"]), dev(b["seq_lens"]),
                           dev(b["qsl"][:1]), b["scale"], b["bs"], ws)
     rc = o.lib().vl_paged_attention(None, None, 0, None, None, None, 0, None, None, 1, 1, 6, 4, 8,
-                                    4, 1.0, 0, 0, 0, 0, None, 0, None)
+                                    4, 1.0, 0, 0, 0, 0, 0, None, 0, None)
     assert rc == -1 and b"multiple" in o.lib().vl_last_error()
 
 
+@pytest.mark.parametrize("layout", ["token", "head"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_reshape_and_cache_bit_exact(dtype):
+def test_reshape_and_cache_bit_exact(dtype, layout):
+    """The scatter equals oracle.write_kv bit for bit; a head-major cache
+    holds the same rows (head_major of the oracle's token-major cache)."""
     from oracle.attention import write_kv
     o = ops()
     rng = np.random.default_rng(3)
-    T, Hkv, D, slots = 77, 4, 48, 500
+    T, Hkv, D, slots = 77, 4, 48, 512
     qkv = torch.from_numpy(rng.standard_normal((T, (8 + 2 * Hkv) * D)).astype(np.float32)).to(dtype)
     k = qkv[:, 8 * D:(8 + Hkv) * D].view(T, Hkv, D)
     v = qkv[:, (8 + Hkv) * D:].view(T, Hkv, D)
@@ -151,7 +168,11 @@ def test_reshape_and_cache_bit_exact(dtype):
     dqkv = qkv.cuda()
     dk = dqkv[:, 8 * D:(8 + Hkv) * D].view(T, Hkv, D)
     dv = dqkv[:, (8 + Hkv) * D:].view(T, Hkv, D)
-    dkc, dvc = kc.cuda(), vc.cuda()
+    if layout == "head":
+        dkc, dvc = (dev(head_major(x.float().numpy(), 16), dtype) for x in (kc, vc))
+        want_k, want_v = head_major(want_k, 16), head_major(want_v, 16)
+    else:
+        dkc, dvc = kc.cuda(), vc.cuda()
     o.reshape_and_cache(dk, dv, dkc, dvc, dev(slot))
     assert np.array_equal(to_np(dkc), want_k) and np.array_equal(to_np(dvc), want_v)
 
@@ -174,9 +195,16 @@ def test_copy_blocks_bit_exact(dtype):
     srcs = rng.integers(0, 20, size=48)
     dsts = 20 + rng.permutation(80)[:48]
     pairs = [(int(s), int(d)) for s, d in zip(srcs, dsts)]
+    # the same copies on head-major caches [L, blocks, Hkv, 16, D]
+    hk = torch.stack([dev(head_major(x, 16), dtype) for x in r.cache_k])
+    hv = torch.stack([dev(head_major(x, 16), dtype) for x in r.cache_v])
     r.do_cow(pairs)
     o.copy_blocks(dk, dv, dev(np.array(pairs, np.int32)), 16)
     assert np.array_equal(to_np(dk), r.cache_k) and np.array_equal(to_np(dv), r.cache_v)
+    o.copy_blocks(hk, hv, dev(np.array(pairs, np.int32)), 16)
+    for layer in range(3):
+        assert np.array_equal(token_major(to_np(hk[layer])), r.cache_k[layer])
+        assert np.array_equal(token_major(to_np(hv[layer])), r.cache_v[layer])
 
 
 def test_rms_norm_and_residual():
@@ -203,19 +231,23 @@ def test_silu_mul():
     np.testing.assert_allclose(to_np(out), silu(gu[:, :1024]) * gu[:, 1024:], rtol=2e-6, atol=1e-7)
 
 
-def test_rope_and_cache_matches_oracle():
+@pytest.mark.parametrize("layout", ["token", "head"])
+def test_rope_and_cache_matches_oracle(layout):
     from oracle.attention import apply_rope, build_rope
     o = ops()
     rng = np.random.default_rng(7)
     T, H, Hkv, D = 29, 8, 4, 48
     qkv = rng.standard_normal((T, (H + 2 * Hkv) * D)).astype(np.float32)
     pos = rng.integers(0, 512, size=T).astype(np.int32)
-    slots = rng.permutation(300)[:T].astype(np.int32)
+    slots = rng.permutation(304)[:T].astype(np.int32)
     cos, sin = build_rope(D, 512)
-    kc = torch.zeros(300, Hkv, D, device="cuda")
-    vc = torch.zeros(300, Hkv, D, device="cuda")
+    shape = (19, Hkv, 16, D) if layout == "head" else (304, Hkv, D)
+    kc = torch.zeros(shape, device="cuda")
+    vc = torch.zeros(shape, device="cuda")
     qo = torch.empty(T, H, D, device="cuda")
     o.rope_and_cache(dev(qkv), qo, kc, vc, dev(pos), dev(slots), dev(cos), dev(sin), H, Hkv, D)
+    if layout == "head":
+        kc, vc = (torch.from_numpy(token_major(to_np(x))) for x in (kc, vc))
     q = qkv[:, :H * D].reshape(T, H, D)
     k = qkv[:, H * D:(H + Hkv) * D].reshape(T, Hkv, D)
     v = qkv[:, (H + Hkv) * D:].reshape(T, Hkv, D)
@@ -266,11 +298,14 @@ def test_greedy_verify_matches_oracle():
 DECODE_CTX = [1, 5, 15, 16, 17, 100, 255, 256, 257, 1000, 4097, 64, 8192]
 
 
+@pytest.mark.parametrize("layout", ["token", "head"])
 @pytest.mark.parametrize("exact_max_q", [True, False])
-def test_bandwidth_decode_path_matches_oracle(exact_max_q):
-    """bf16 / D 128 / 32 heads over 8 KV heads / block 16: the bandwidth kernel."""
+def test_bandwidth_decode_path_matches_oracle(exact_max_q, layout):
+    """bf16 / D 128 / 32 heads over 8 KV heads / block 16: the bandwidth
+    kernel, both cache layouts."""
     b = make_batch([(1, c) for c in DECODE_CTX], 32, 8, 128, 16, seed=11)
-    got = run_attention(b, "bf16", exact_max_q=exact_max_q, exact_min_q=exact_max_q)
+    got = run_attention(b, "bf16", exact_max_q=exact_max_q, exact_min_q=exact_max_q,
+                        layout=layout)
     check(got, expected(b, "bf16"), "bf16")
 
 
@@ -281,28 +316,30 @@ SHORT_CTX = [1, 5, 63, 64, 65, 255, 256, 257, 700, 2048]
                                      (48, 16, 2)])
 @pytest.mark.parametrize("bs", [1, 16])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_short_decode_kernel(D, H, Hkv, bs, dtype):
+@pytest.mark.parametrize("layout", ["token", "head"])
+def test_short_decode_kernel(D, H, Hkv, bs, dtype, layout):
     """Decodes of at most 2048 tokens with head_dim <= 64: the one-workgroup-
     per-(sequence, KV head) kernel, chosen by the query and context bounds
-    (a sequence without a query in the middle)."""
+    (a sequence without a query in the middle), both cache layouts."""
     seqs = [(1, c) for c in SHORT_CTX[:5]] + [(0, 30)] + [(1, c) for c in SHORT_CTX[5:]]
     b = make_batch(seqs, H, Hkv, D, bs, seed=D + H + bs)
-    got = run_attention(b, dtype, ctx_hint=True)
+    got = run_attention(b, dtype, ctx_hint=True, layout=layout)
     check(got, expected(b, dtype), dtype)
 
 
 @pytest.mark.parametrize("seqs", [[(1, c) for c in SHORT_CTX],
                                   [(1, 40), (7, 300), (1, 2000), (16, 16), (3, 5000)]])
 @pytest.mark.parametrize("ctx_hint", [True, False])
-def test_fp32_query_over_bf16_cache(seqs, ctx_hint):
+@pytest.mark.parametrize("layout", ["token", "head"])
+def test_fp32_query_over_bf16_cache(seqs, ctx_hint, layout):
     """VL_DTYPE_F32_BF16KV: fp32 query and output over bf16 caches (decodes
     by the short-decode kernel when the bounds allow, everything else by the
     generic kernel and the combine) against the oracle on the bf16 K/V values,
-    at the fp32 tolerance."""
+    at the fp32 tolerance; both cache layouts."""
     o = ops()
     b = make_batch(seqs, 8, 4, 48, 16, seed=len(seqs) + ctx_hint)
     q = dev(b["q"])
-    kc, vc = dev(b["k_cache"], torch.bfloat16), dev(b["v_cache"], torch.bfloat16)
+    kc, vc = caches(b, torch.bfloat16, layout)
     S, T = len(seqs), b["q"].shape[0]
     ws = o.AttentionWorkspace().get(o.paged_attention_workspace_size(S, T, 8, 48,
                                                                      int(b["seq_lens"].max())))
@@ -372,7 +409,8 @@ TILE_SHAPES = [("f32", 8, 4, 48), ("f32", 8, 2, 64), ("f32", 4, 4, 16), ("f32", 
 
 @pytest.mark.parametrize("dtype,H,Hkv,D", TILE_SHAPES)
 @pytest.mark.parametrize("bs", [1, 4, 16, 32])
-def test_tile_prefill_chunks_with_prior_context(dtype, H, Hkv, D, bs):
+@pytest.mark.parametrize("layout", ["token", "head"])
+def test_tile_prefill_chunks_with_prior_context(dtype, H, Hkv, D, bs, layout):
     """Chunks that start mid-block after prior context, causal within the chunk,
     plus decodes and a 1-token context, all in one call. Block sizes cover
     every staging path: per-key block lookups (1), per-quad V lookups (4),
@@ -380,20 +418,21 @@ def test_tile_prefill_chunks_with_prior_context(dtype, H, Hkv, D, bs):
     sequence's last block are NaN."""
     seqs = [(37, 37), (100, 133), (1, 90), (64, 64 + 200), (17, 500), (3, 3), (2, 40)]
     b = make_batch(seqs, H, Hkv, D, bs, seed=30 + D + bs)
-    check(run_attention(b, dtype), expected(b, dtype), dtype)
+    check(run_attention(b, dtype, layout=layout), expected(b, dtype), dtype)
 
 
+@pytest.mark.parametrize("layout", ["token", "head"])
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_tile_speculative_verify_rows_split_over_long_context(dtype):
+def test_tile_speculative_verify_rows_split_over_long_context(dtype, layout):
     """5 queries per sequence over long contexts: the context is split into
     partitions and merged; also with no room for partials."""
     seqs = [(5, 3000), (5, 1025), (5, 5), (4, 700), (5, 6001)]
     b = make_batch(seqs, 32, 8, 128, 16, seed=40)
     want = expected(b, dtype)
-    check(run_attention(b, dtype), want, dtype)
+    check(run_attention(b, dtype, layout=layout), want, dtype)
     o = ops()
-    check(run_attention(b, dtype, ws_bytes=o.lib().vl_paged_attention_min_workspace(len(seqs))),
-          want, dtype)
+    check(run_attention(b, dtype, ws_bytes=o.lib().vl_paged_attention_min_workspace(len(seqs)),
+                        layout=layout), want, dtype)
 
 
 def test_tile_fp32_meets_the_reference_tolerance_at_the_tinyllama_shape():

@@ -101,12 +101,14 @@ def test_bad_arguments_raise():
                       torch.zeros((100, 384), device="cuda"))
 
 
+@pytest.mark.parametrize("layout", ["token", "head"])
 @pytest.mark.parametrize("rows", [1, 13, 16])
 @pytest.mark.parametrize("shape", [(8, 4, 48, 384), (4, 2, 16, 64)])
-def test_qkv_rope_cache_equals_projection_then_rope(rows, shape):
+def test_qkv_rope_cache_equals_projection_then_rope(rows, shape, layout):
     """vl_qkv_rope_cache gives the same bits as vl_linear_rows followed by
     vl_rope_and_cache: rotated q, rotated k and v at each row's slot, rows
-    with slot -1 writing q only."""
+    with slot -1 writing q only; with head-major caches (8-slot blocks) both
+    writers put the same rows there."""
     o = _ops()
     H, Hkv, D, k = shape
     n = (H + 2 * Hkv) * D
@@ -121,7 +123,8 @@ def test_qkv_rope_cache_equals_projection_then_rope(rows, shape):
     slot = dev(slots)
     ang = rng.standard_normal((64, D // 2)).astype(np.float32)
     cos, sin = dev(np.cos(ang)), dev(np.sin(ang))
-    kc1, vc1 = (torch.full((40, Hkv, D), float("nan"), device="cuda") for _ in range(2))
+    shape = (5, Hkv, 8, D) if layout == "head" else (40, Hkv, D)
+    kc1, vc1 = (torch.full(shape, float("nan"), device="cuda") for _ in range(2))
     kc2, vc2 = kc1.clone(), vc1.clone()
     q1 = torch.empty((rows, H, D), device="cuda")
     q2 = torch.empty_like(q1)
@@ -133,6 +136,16 @@ def test_qkv_rope_cache_equals_projection_then_rope(rows, shape):
     assert torch.equal(q1, q2)
     assert torch.equal(kc1.nan_to_num(7.0), kc2.nan_to_num(7.0))
     assert torch.equal(vc1.nan_to_num(7.0), vc2.nan_to_num(7.0))
+    if layout == "head":  # row (slot, h) of the head-major cache is rotated k / v of slot's row
+        from oracle.attention import apply_rope
+        kh = kc1.permute(0, 2, 1, 3).reshape(40, Hkv, D).cpu().numpy()
+        vh = vc1.permute(0, 2, 1, 3).reshape(40, Hkv, D).cpu().numpy()
+        ok = slots >= 0
+        qkvn = qkv.cpu().numpy()
+        k_rows = qkvn[:, H * D:(H + Hkv) * D].reshape(rows, Hkv, D)
+        want_k = apply_rope(k_rows, pos.cpu().numpy(), cos.cpu().numpy(), sin.cpu().numpy())
+        np.testing.assert_array_equal(kh[slots[ok]], want_k[ok])
+        np.testing.assert_array_equal(vh[slots[ok]], qkvn[ok, (H + Hkv) * D:].reshape(-1, Hkv, D))
 
 
 @pytest.mark.parametrize("rows", [1, 16])

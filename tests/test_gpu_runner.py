@@ -46,12 +46,15 @@ def small_reference():
     return g["streams"]
 
 
-def test_cfg0_mix_matches_reference_streams():
+@pytest.mark.parametrize("layout", ["token", "head"])
+def test_cfg0_mix_matches_reference_streams(layout):
     """The 48-request ragged mix end to end: 260 steps, 3179 tokens, the
-    reference's greedy streams token for token (near-ties excepted)."""
+    reference's greedy streams token for token (near-ties excepted), with
+    the cache token-major (the reference's layout) or head-major."""
     from vllmlite_amd.hip_runner import HipRunner
     g = _gold("cfg0_streams.json")
     cfg = cfg0_config(False)
+    cfg.cache.kv_layout = layout
     eng = LLMEngine(cfg, runner=HipRunner(cfg.model, cfg.cache))
     reqs = mixed_lengths(0, 48, 0)
     for rid, ids, p in reqs:
@@ -207,15 +210,18 @@ def test_device_argmax_ids_equal_numpy_argmax():
         assert np.array_equal(ids, want)
 
 
-def test_copy_on_write_fork_matches_oracle_runner():
+@pytest.mark.parametrize("layout", ["token", "head"])
+def test_copy_on_write_fork_matches_oracle_runner(layout):
     """A forked parent with a partial tail block: the children's first decode
     step writes into the shared block, so the block manager emits CoW pairs;
-    the HipRunner's logits must match the NumPy oracle runner's."""
+    the HipRunner's streams (either cache layout) must match the NumPy oracle
+    runner's."""
     from oracle.runner import NumpyRunner
     from vllmlite_amd.hip_runner import HipRunner
     from vllmlite_amd.request import SamplingParams
 
     cfg = small_cfg(block_size=4)
+    cfg.cache.kv_layout = layout
     outs = []
     for factory in (NumpyRunner, HipRunner):
         eng = LLMEngine(cfg, runner=factory(cfg.model, cfg.cache), lookahead=False)
@@ -323,6 +329,25 @@ def test_every_step_logits_match_oracle_runner(layers, d_model):
     for (g, dec), (w, _) in zip(got, want):
         scale = np.abs(w).max(axis=-1, keepdims=True)
         assert np.all(np.abs(g - w) <= 2e-4 * scale), f"decode step {dec}"
+
+
+@pytest.mark.parametrize("layers,d_model", [(2, 64), (6, 384)])
+def test_head_major_cache_gives_the_same_logits(layers, d_model):
+    """cache kv_layout "head" ([blocks, Hkv, block_size, D] per layer): every
+    step's logits, prefill and decode, equal those with the token-major cache
+    bit for bit (the kernels read the same values in the same order; only the
+    addresses differ)."""
+    from vllmlite_amd.hip_runner import HipRunner
+    traces = []
+    for layout in ("token", "head"):
+        cfg = small_cfg(layers=layers, d_model=d_model)
+        if d_model == 384:
+            cfg.model.n_heads, cfg.model.n_kv_heads, cfg.model.d_ff = 8, 4, 1024
+        cfg.cache.kv_layout = layout
+        traces.append(_logit_trace(HipRunner, cfg, PROMPTS, 12))
+    assert len(traces[0]) == len(traces[1]) and sum(dec for _, dec in traces[0]) >= 10
+    for (a, _), (b, _) in zip(*traces):
+        assert np.array_equal(a, b)
 
 
 def test_runner_reads_weights_from_npz(tmp_path):

@@ -465,7 +465,7 @@ __global__ void __launch_bounds__(64) attend_generic_kernel(
     T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const TKV* __restrict__ kc,
     const TKV* __restrict__ vc, const int32_t* __restrict__ bt, int bt_stride,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H, int Hkv,
-    int D, int bs, float scale_log2, const int32_t* __restrict__ hdr,
+    int D, int bs, int kv_hm, float scale_log2, const int32_t* __restrict__ hdr,
     const int32_t* __restrict__ item_off, const int32_t* __restrict__ nparts,
     const int32_t* __restrict__ split_base, float2* __restrict__ ml, float* __restrict__ po) {
   __shared__ float q_s[kMaxHeadDim];
@@ -475,7 +475,11 @@ __global__ void __launch_bounds__(64) attend_generic_kernel(
   const int n_items = hdr[1];
   const int P = hdr[2];
   const int rep = H / Hkv;
-  const int64_t slot_stride = (int64_t)Hkv * D;
+  // row of (block b, offset o, KV head h): b * blk + o * row + h * head, for
+  // token-major [slots, Hkv, D] or head-major [blocks, Hkv, bs, D] caches
+  const int64_t blk = (int64_t)bs * Hkv * D;
+  const int64_t row_stride = kv_hm ? D : (int64_t)Hkv * D;
+  const int64_t head_stride = kv_hm ? (int64_t)bs * D : D;
   constexpr int kR = kMaxHeadDim / 64;
   for (int it = blockIdx.x; it < n_items; it += gridDim.x) {
     const int i = wave_upper_bound_le(item_off, S + 1, it);
@@ -507,8 +511,8 @@ __global__ void __launch_bounds__(64) attend_generic_kernel(
       float s = -__builtin_inff();
       int64_t row = 0;
       if (key < kend) {
-        const int64_t slot = (int64_t)table[key / bs] * bs + key % bs;
-        row = slot * slot_stride + (int64_t)kvh * D;
+        row = (int64_t)table[key / bs] * blk + (int64_t)(key % bs) * row_stride +
+              (int64_t)kvh * head_stride;
         const TKV* kr = kc + row;
         float dot = 0.f;
         for (int d = 0; d < D; ++d) dot += q_s[d] * Elem<TKV>::load(kr, d);
@@ -687,12 +691,12 @@ __device__ __forceinline__ int item_tid() {
   T *__restrict__ out, const T *__restrict__ query, int64_t q_stride, const T *kc,          \
       const T *vc, const int32_t *__restrict__ bt, int bt_stride,                           \
       const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ qsl, int S, int H,   \
-      int Hkv, int bs_log2, float scale_log2, const int4 *__restrict__ desc,                 \
+      int Hkv, int bs_log2, int kv_hm, float scale_log2, const int4 *__restrict__ desc,      \
       const int32_t *__restrict__ nparts,                                                    \
       const int32_t *__restrict__ split_base, float2 *ml, float *po
 #define VL_ATTN_ARGS \
-  out, query, q_stride, kc, vc, bt, bt_stride, seq_lens, qsl, S, H, Hkv, bs_log2, scale_log2, \
-      desc, nparts, split_base, ml, po
+  out, query, q_stride, kc, vc, bt, bt_stride, seq_lens, qsl, S, H, Hkv, bs_log2, kv_hm,      \
+      scale_log2, desc, nparts, split_base, ml, po
 
 
 // One workgroup item of the tile kernel (256 threads; the caller's LDS).
@@ -728,7 +732,11 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
   const int col = lane & (RW - 1);  // the lane's row within the wave's rows
   const int grp = lane / RW;        // lane group: which keys / d chunk it holds
   const int rep = H / Hkv;
-  const int64_t slot_stride = (int64_t)Hkv * D;
+  // elements between a KV head's consecutive slots inside a block and
+  // between KV heads: token-major [slots, Hkv, D] or head-major [blocks, Hkv,
+  // bs, D] caches
+  const int64_t slot_stride = kv_hm ? D : (int64_t)Hkv * D;
+  const int64_t head_stride = kv_hm ? (int64_t)D << bs_log2 : D;
 
   {
     const int pos = wave_upper_bound_le(item_off, S + 1, it);
@@ -758,7 +766,7 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
     const int qpos = ctx - q_len + j;
     const int qpos_wave_min = ctx - q_len + row0 / rep;  // earliest query row of the wave
     const int32_t* table = bt + (int64_t)i * bt_stride;
-    const int64_t kv_off = (int64_t)kvh * D;
+    const int64_t kv_off = (int64_t)kvh * head_stride;
 
     // Q^T operand of the QK^T product, kept in registers for the whole item
     typename std::conditional<kBf16, bf16x8_t, float>::type qop[kKS];
@@ -784,7 +792,7 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
     float l_part = 0.f;  // this lane's share of the row sum
 
     // ---- prefetch registers: this thread's share of one tile's K and V
-    const uint32_t blk_elems = (uint32_t)slot_stride << bs_log2;
+    const uint32_t blk_elems = (uint32_t)(Hkv * D) << bs_log2;
     const uint32_t bs_mask = (1u << bs_log2) - 1;
     auto row_of = [&](int key) -> int64_t {  // element offset of key's head row
       const uint32_t blk = (uint32_t)table[key >> bs_log2];
@@ -795,7 +803,7 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
     // bf16 staging: K unit r of a tile is keys k0 + kUnitKeys r + threadIdx / kChunks,
     // chunk threadIdx % kChunks; with blocks of >= kUnitKeys slots the unit lies
     // in one block whose id is uniform over the workgroup (tile starts are
-    // multiples of 64). Keys past the workgroup's end are masked: K reads stay
+    // multiples of 64); in a head-major cache the unit is one contiguous span. Keys past the workgroup's end are masked: K reads stay
     // in the last key's block (finite or not, the score is replaced by -inf);
     // V reads re-read the last key, finite values whose weights are zero.
     constexpr int kUnitKeys = 256 / Lds::kChunks;
@@ -1186,13 +1194,6 @@ __device__ __forceinline__ uint64_t pack2(float lo, float hi) {
 __device__ __forceinline__ float lo_f(uint64_t w) { return __uint_as_float((uint32_t)w); }
 __device__ __forceinline__ float hi_f(uint64_t w) { return __uint_as_float((uint32_t)(w >> 32)); }
 
-// sum over the 4 lanes of a quad, result in every lane (DPP quad_perm)
-__device__ __forceinline__ float quad_sum(float v) {
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
-  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
-  return v;
-}
-
 // Reduce over lanes that share (lane & 3): xor 4, 8, 16, 32.
 __device__ __forceinline__ float stride4_max(float v) {
 #pragma unroll
@@ -1203,6 +1204,43 @@ __device__ __forceinline__ float stride4_sum(float v) {
 #pragma unroll
   for (int o = 4; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
   return v;
+}
+
+// DPP lane exchange (update_dpp with `old` kept where the row mask excludes
+// the lane).
+#define VL_DPP(old, v, ctrl, rmask)                                                     \
+  __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), ctrl, \
+                                             rmask, 0xF, false))
+
+// Transposing sum over each row of 16 lanes: lane c (= lane & 15) holds 16
+// partial values v[0..15]; afterwards it returns the row's total of v[c].
+// Four halving steps pair lanes whose index differs in bit 3, 2, 1, 0 (row
+// mirror 15 - c, half-row mirror, quad mirror, quad swap); each lane adds
+// its partner's copy of the half of the values whose index bit matches its
+// own and keeps that half. 45 VALU instead of 16 separate 4-step sums.
+__device__ __forceinline__ float row_transpose_sum16(const float (&v)[16], int c) {
+  float w[8], x[4], y[2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float lo = v[i] + VL_DPP(0.f, v[i], 0x140, 0xF);
+    const float hi = v[i + 8] + VL_DPP(0.f, v[i + 8], 0x140, 0xF);
+    w[i] = (c & 8) ? hi : lo;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = w[i] + VL_DPP(0.f, w[i], 0x141, 0xF);
+    const float hi = w[i + 4] + VL_DPP(0.f, w[i + 4], 0x141, 0xF);
+    x[i] = (c & 4) ? hi : lo;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float lo = x[i] + VL_DPP(0.f, x[i], 0x1B, 0xF);
+    const float hi = x[i + 2] + VL_DPP(0.f, x[i + 2], 0x1B, 0xF);
+    y[i] = (c & 2) ? hi : lo;
+  }
+  const float lo = y[0] + VL_DPP(0.f, y[0], 0xB1, 0xF);
+  const float hi = y[1] + VL_DPP(0.f, y[1], 0xB1, 0xF);
+  return (c & 1) ? hi : lo;
 }
 
 // One output row's merge of np partitions written by other workgroups
@@ -1264,9 +1302,11 @@ __device__ __forceinline__ float2 merge_partitions(const uint64_t* mlw, const ui
 // ranges. Items are (range, KV head) with the KV heads of a range adjacent;
 // full ranges come first, then the shorter last ranges, longest first.
 // Persistent workgroups claim items from a counter.
-//   QK: lane l reads token l/4 of a block, 16-byte chunks (l&3)+4j of the
-//       head row (j < 4); four v_dot2_f32_bf16 per chunk and query head,
-//       then a quad DPP sum gives every lane of the quad the 4 heads' scores.
+//   QK: load j (j < 4) of a block gives lane l the 16-byte chunk l&15 of
+//       token 4j + (l>>4) (whole 256-byte head rows, four per instruction);
+//       four v_dot2_f32_bf16 per chunk and query head give 16 partial dot
+//       products per lane, which a transposing DPP sum over each 16-lane
+//       row turns into one (token, head) score per lane.
 //   softmax: scores through LDS, per head max over the wavefront's chunk of
 //       up to 16 blocks, exponentials rounded to bf16 (the sum adds the
 //       rounded values).
@@ -1339,22 +1379,30 @@ __device__ __forceinline__ uint4 load_stream16(const char* p) {
 }
 
 // One item (see above) by the 256 threads of a workgroup, from its prologue
-// `cur`; R from the plan header.
+// `cur`; R from the plan header. Load j of a block's K (j < 4) reads tokens
+// 4 j .. 4 j + 3 of the KV head whole (lane l: chunk l % 16 of token 4 j +
+// l / 16): four 256-byte rows per instruction, one contiguous 1 KB span in a
+// head-major cache. The 16 chunks' partial dot products are then summed
+// across each 16-lane row by a transposing DPP sum. (Lanes reading 64 bytes
+// of each of 16 tokens per instruction, completed by a quad sum, measured
+// 229-233 us against 215-221 us for the 256-sequence batch.)
 template <bool kMixed>
 __device__ __forceinline__ void decode_body(DecodeLds& s, int it, const DecodeItem& cur, int R,
                                             VL_ATTN_PARAMS(uint16_t)) {
   const int tid = item_tid<kMixed>();
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int qp = lane & 3, tk = lane >> 2;     // QK mapping
+  const int qp = lane & 3;                    // the head of the lane's scores
   const int vcn = lane & 15, vg = lane >> 4;  // PV mapping
-  // H = Hkv * kFRep (the bandwidth-kernel shape)
-  const int64_t tok_stride = (int64_t)Hkv * kFD;  // elements per cache slot
+  // H = Hkv * kFRep (the bandwidth-kernel shape). Elements between a KV
+  // head's consecutive slots of a block: Hkv * 128 (token-major) or 128
+  // (head-major, where a head's 16 rows are one 4 KB span)
+  const int64_t tok_stride = kv_hm ? kFD : (int64_t)Hkv * kFD;
   float4* pw = s.p[wave];
   uint4* qw = s.q[wave];
   float4* stash = s.acc[wave] + lane;  // stash[64 * k]: conflict-free
   float* pf = reinterpret_cast<float*>(pw);  // [block][token][head] scores, then probabilities
-  const int64_t blk_bytes = (int64_t)kFBs * tok_stride * 2;
+  const int64_t blk_bytes = (int64_t)kFBs * Hkv * kFD * 2;
   const char* kbytes = reinterpret_cast<const char*>(kc);
   const char* vbytes = reinterpret_cast<const char*>(vc);
   {
@@ -1370,9 +1418,10 @@ __device__ __forceinline__ void decode_body(DecodeLds& s, int it, const DecodeIt
     const int wb0 = kbeg / kFBs + wave;  // first block; stride 4
 
     qw[lane] = cur.q;  // query of the 4 heads to LDS: [head][16-byte chunk]
-    const int64_t kv_off = (int64_t)kvh * kFD;
+    const int64_t kv_off = (int64_t)kvh * (kv_hm ? kFBs * kFD : kFD);
     // byte offsets of this lane inside a block (a block is 16 slots x Hkv x 128 bf16)
-    const uint32_t k_lane = (uint32_t)((tk * tok_stride + kv_off) * 2) + qp * 16;
+    const uint32_t k_lane = (uint32_t)(((lane >> 4) * tok_stride + kv_off) * 2) + (lane & 15) * 16;
+    const uint32_t k_jstep = (uint32_t)(4 * tok_stride * 2);
     const uint32_t v_lane = (uint32_t)((vg * tok_stride + kv_off) * 2) + vcn * 16;
     const uint32_t v_tstep = (uint32_t)(4 * tok_stride * 2);
 
@@ -1403,39 +1452,33 @@ __device__ __forceinline__ void decode_body(DecodeLds& s, int it, const DecodeIt
           const int bid = __builtin_amdgcn_readlane(my_bid, min(g + u, nblk - 1));
           const char* bp = kbytes + (int64_t)bid * blk_bytes + k_lane;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) kb[u][j] = load_stream16(bp + j * 64);
+          for (int j = 0; j < 4; ++j) kb[u][j] = load_stream16(bp + j * k_jstep);
         }
         // all loads of the group go out before any of them is consumed
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        // one query head at a time (its 4 chunks from LDS): 16 registers of
-        // query live instead of 64
-        float a4[kBK][kFRep];
+        // lane (tg = lane / 16, c = lane % 16) holds chunk c of tokens 4 j +
+        // tg; partial v[4 j + h] = chunk c of head h's query . chunk c of K,
+        // summed over the row; lane c then holds token 4 (c / 4) + tg of head
+        // c % 4 = qp
+        const int c = lane & 15, tg = lane >> 4;
+        uint4 qh[kFRep];
 #pragma unroll
-        for (int h = 0; h < kFRep; ++h) {
-          uint4 q[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) q[j] = qw[h * 16 + qp + 4 * j];
-#pragma unroll
-          for (int u = 0; u < kBK; ++u) {
-            float d = 0.f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) d = dot8(q[j], kb[u][j], d);
-            a4[u][h] = d;
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
+        for (int h = 0; h < kFRep; ++h) qh[h] = qw[h * 16 + c];
 #pragma unroll
         for (int u = 0; u < kBK; ++u) {
-          float a[kFRep];
+          float v[16];
 #pragma unroll
-          for (int h = 0; h < kFRep; ++h) a[h] = quad_sum(a4[u][h]);
-          const float mine = qp == 0 ? a[0] : qp == 1 ? a[1] : qp == 2 ? a[2] : a[3];
-          const int key = key0 + (g + u) * 4 * kFBs + tk;
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int h = 0; h < kFRep; ++h) v[4 * j + h] = dot8(qh[h], kb[u][j], 0.f);
+          const float sc = row_transpose_sum16(v, c);
+          const int tok16 = 4 * (c >> 2) + tg;
+          const int key = key0 + (g + u) * 4 * kFBs + tok16;
           const bool ok = (g + u < nblk) && key < kend;
-          const float sv = ok ? mine * scale_log2 : -__builtin_inff();
+          const float sv = ok ? sc * scale_log2 : -__builtin_inff();
           cmax = fmaxf(cmax, sv);
-          pf[((g + u) * 16 + tk) * 4 + qp] = sv;
+          pf[((g + u) * 16 + tok16) * 4 + qp] = sv;
         }
       }
       // ---- online softmax update for head qp
@@ -1677,12 +1720,6 @@ struct ShortLds {
   int32_t tbl[kShortCtx];   // the sequence's block ids
 };
 
-// DPP lane exchange (update_dpp with `old` kept where the row mask excludes
-// the lane).
-#define VL_DPP(old, v, ctrl, rmask)                                                     \
-  __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), ctrl, \
-                                             rmask, 0xF, false))
-
 // Max / sum over the 64 lanes of a wavefront by DPP: within each row of 16
 // (quad xor 1, xor 2, half-row mirror, row mirror), then row 0 into 1 and 2
 // into 3 (row_bcast:15), row 1 into 2 and 3 (row_bcast:31); lane 63 holds the
@@ -1749,7 +1786,7 @@ __global__ void __launch_bounds__(256) attend_short_decode_kernel(
     T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const TKV* kc,
     const TKV* vc, const int32_t* __restrict__ bt, int bt_stride,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int Hkv, int bs_log2,
-    float scale_log2) {
+    int kv_hm, float scale_log2) {
   using Lds = ShortLds<TKV, D, REP>;
   constexpr int VE = Lds::kVE;
   static_assert(D % VE == 0 && D <= 64, "head_dim");
@@ -1774,12 +1811,13 @@ __global__ void __launch_bounds__(256) attend_short_decode_kernel(
                 scale_log2;
   }
   __syncthreads();
-  const int64_t slot_stride = (int64_t)Hkv * D;
-  const TKV* kg = kc + (int64_t)g * D;
-  const TKV* vg = vc + (int64_t)g * D;
-  auto slot_of = [&](int k) {
-    return ((int64_t)s.tbl[k >> bs_log2] << bs_log2) + (k & bs_mask);
-  };
+  // row of key k of KV head g: block * blk + offset * row + g * head
+  // (token-major: row Hkv * D, head D; head-major: row D, head bs * D)
+  const int64_t blk = (int64_t)Hkv * D << bs_log2;
+  const int64_t row = kv_hm ? D : (int64_t)Hkv * D;
+  const TKV* kg = kc + (int64_t)g * (kv_hm ? (int64_t)D << bs_log2 : D);
+  const TKV* vg = vc + (kg - kc);
+  auto row_of = [&](int k) { return s.tbl[k >> bs_log2] * blk + (k & bs_mask) * row; };
   const int pg = lane / NC, pc = lane - (lane / NC) * NC;  // PV: key group, chunk
   float m[REP], lsum[REP], acc[REP][VE];
 #pragma unroll
@@ -1794,13 +1832,12 @@ __global__ void __launch_bounds__(256) attend_short_decode_kernel(
     if (base >= c) break;  // wavefront-uniform; later chunks start later still
     // every load of the chunk first: the lane's K row and its V chunks
     float kr[D];
-    load_row<TKV, D>(kg + slot_of(min(base + lane, c - 1)) * slot_stride, kr);
+    load_row<TKV, D>(kg + row_of(min(base + lane, c - 1)), kr);
     uint4 vraw[KPL];
 #pragma unroll
     for (int j = 0; j < KPL; ++j) {
       const int kk = min(pg + G * j, 63);  // past the chunk (or lanes past G NC): weight 0
-      vraw[j] = *reinterpret_cast<const uint4*>(vg + slot_of(min(base + kk, c - 1)) * slot_stride +
-                                                pc * VE);
+      vraw[j] = *reinterpret_cast<const uint4*>(vg + row_of(min(base + kk, c - 1)) + pc * VE);
     }
     const bool valid = base + lane < c;
 #pragma unroll
@@ -2034,6 +2071,7 @@ struct Args {
   int S, T, H, Hkv, D, bs;
   float scale;
   int dtype;
+  int kv_layout;
 };
 
 int check_args(const Args& a, const void* ws, size_t ws_bytes, bool need_kv) {
@@ -2068,7 +2106,10 @@ int decode_grid() {
             hipSuccess ||
         per_cu <= 0)
       per_cu = 2;
-    cached[dev] = per_cu * vl_num_cus();
+    // at most 2 per compute unit: 3 fit (157 VGPRs, 52 KB of LDS) but
+    // measured 225-230 us against 215-221 us for the 256-sequence batch (the
+    // plan then also cuts the contexts into more, shorter ranges)
+    cached[dev] = std::min(per_cu, 2) * vl_num_cus();
   }
   return cached[dev];
 }
@@ -2111,8 +2152,8 @@ int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
 // The VL_ATTN_PARAMS arguments of a launch (inside do_run / launch_tile_d).
 #define VL_ATTN_LAUNCH_ARGS(T)                                                                  \
   (T*)a.out, (const T*)a.query, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.bt, a.bt_stride,  \
-      a.seq_lens, a.qsl, a.S, a.H, a.Hkv, __builtin_ctz(a.bs), sl2, L.desc, L.nparts,          \
-      L.split_base, L.ml, L.po
+      a.seq_lens, a.qsl, a.S, a.H, a.Hkv, __builtin_ctz(a.bs),                                 \
+      a.kv_layout == VL_KV_HEAD_MAJOR ? 1 : 0, sl2, L.desc, L.nparts, L.split_base, L.ml, L.po
 
 // Workgroups of a tile kernel that are resident at once on the current device
 // (its grid is persistent), cached per device and instantiation.
@@ -2193,7 +2234,7 @@ int launch_short_decode_d(const Args& a, float sl2, hipStream_t st) {
 #define VL_SHORT(REP)                                                                        \
   attend_short_decode_kernel<T, TKV, D, REP><<<grid, 256, 0, st>>>(                          \
       (T*)a.out, (const T*)a.query, a.q_stride, (const TKV*)a.kc, (const TKV*)a.vc, a.bt,    \
-      a.bt_stride, a.seq_lens, a.qsl, a.Hkv, bs_log2, sl2)
+      a.bt_stride, a.seq_lens, a.qsl, a.Hkv, bs_log2, a.kv_layout == VL_KV_HEAD_MAJOR ? 1 : 0, sl2)
   switch (rep) {
     case 1: VL_SHORT(1); break;
     case 2: VL_SHORT(2); break;
@@ -2259,7 +2300,8 @@ int do_run(const Args& a, int max_q, int min_q, int max_ctx, void* ws, size_t ws
   if (!one_type || (!fast && !tile_shape(a.dtype, a.D, a.bs))) {
     attend_generic_kernel<T, TKV><<<ncu * 16, 64, 0, st>>>(
         (T*)a.out, (const T*)a.query, a.q_stride, (const TKV*)a.kc, (const TKV*)a.vc, a.bt,
-        a.bt_stride, a.seq_lens, a.qsl, a.S, a.H, a.Hkv, a.D, a.bs, sl2, L.hdr, L.gen_off,
+        a.bt_stride, a.seq_lens, a.qsl, a.S, a.H, a.Hkv, a.D, a.bs,
+        a.kv_layout == VL_KV_HEAD_MAJOR ? 1 : 0, sl2, L.hdr, L.gen_off,
         L.nparts, L.split_base, L.ml, L.po);
     VL_CHECK_LAUNCH();
   }
@@ -2333,15 +2375,18 @@ extern "C" int vl_paged_attention_run(void* out, const void* query, int64_t quer
                                       const int32_t* seq_lens, const int32_t* query_start_loc,
                                       int num_seqs, int num_tokens, int num_heads,
                                       int num_kv_heads, int head_dim, int block_size, float scale,
-                                      int dtype, int max_query_len, int min_query_len,
-                                      int max_context_len, void* workspace,
+                                      int dtype, int kv_layout, int max_query_len,
+                                      int min_query_len, int max_context_len, void* workspace,
                                       size_t workspace_bytes, void* stream) {
   VL_CHECK_ARG(min_query_len >= 0 && (max_query_len <= 0 || min_query_len <= max_query_len),
                "bad query length bounds");
   VL_CHECK_ARG(max_context_len >= 0, "bad context length bound");
   Args a{out, query, query_stride, key_cache, value_cache, block_tables, block_table_stride,
          seq_lens, query_start_loc, num_seqs, num_tokens, num_heads, num_kv_heads, head_dim,
-         block_size, scale, dtype};
+         block_size, scale, dtype, kv_layout};
+  KvGeom geom;
+  if (num_kv_heads > 0 && head_dim > 0)
+    if (int rc = vl_kv_geom(kv_layout, block_size, num_kv_heads, head_dim, &geom)) return rc;
   int rc = check_args(a, workspace, workspace_bytes, true);
   if (rc || a.S == 0 || a.T == 0) return rc;
   if (fast_shape(dtype, num_heads, num_kv_heads, head_dim, block_size) ||
@@ -2363,8 +2408,9 @@ extern "C" int vl_paged_attention(void* out, const void* query, int64_t query_st
                                   const int32_t* seq_lens, const int32_t* query_start_loc,
                                   int num_seqs, int num_tokens, int num_heads, int num_kv_heads,
                                   int head_dim, int block_size, float scale, int dtype,
-                                  int max_query_len, int min_query_len, int max_context_len,
-                                  void* workspace, size_t workspace_bytes, void* stream) {
+                                  int kv_layout, int max_query_len, int min_query_len,
+                                  int max_context_len, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
   Args a{};
   a.S = num_seqs, a.H = num_heads, a.Hkv = num_kv_heads, a.D = head_dim, a.bs = block_size;
   if (!short_decode(a, max_query_len, max_context_len)) {  // that kernel reads no plan
@@ -2376,8 +2422,8 @@ extern "C" int vl_paged_attention(void* out, const void* query, int64_t query_st
   return vl_paged_attention_run(out, query, query_stride, key_cache, value_cache, block_tables,
                                 block_table_stride, seq_lens, query_start_loc, num_seqs,
                                 num_tokens, num_heads, num_kv_heads, head_dim, block_size, scale,
-                                dtype, max_query_len, min_query_len, max_context_len, workspace,
-                                workspace_bytes, stream);
+                                dtype, kv_layout, max_query_len, min_query_len, max_context_len,
+                                workspace, workspace_bytes, stream);
 }
 
 // ---------------------------------------------------- allocation-free call --
@@ -2417,7 +2463,7 @@ extern "C" int vl_paged_attention_noalloc(void* out, const void* query, int64_t 
                                           const int32_t* query_start_loc, int num_seqs,
                                           int num_tokens, int num_heads, int num_kv_heads,
                                           int head_dim, int block_size, float scale, int dtype,
-                                          int max_query_len, int min_query_len,
+                                          int kv_layout, int max_query_len, int min_query_len,
                                           int max_context_len, void* stream) {
   VL_CHECK_ARG(num_seqs >= 0 && fixed_bytes(num_seqs) <= (size_t)VL_NOALLOC_SCRATCH_BYTES,
                "vl_paged_attention_noalloc: %d sequences need %zu bytes of plan space, more than "
@@ -2432,6 +2478,6 @@ extern "C" int vl_paged_attention_noalloc(void* out, const void* query, int64_t 
   return vl_paged_attention(out, query, query_stride, key_cache, value_cache, block_tables,
                             block_table_stride, seq_lens, query_start_loc, num_seqs, num_tokens,
                             num_heads, num_kv_heads, head_dim, block_size, scale, dtype,
-                            max_query_len, min_query_len, max_context_len, ws,
+                            kv_layout, max_query_len, min_query_len, max_context_len, ws,
                             (size_t)VL_NOALLOC_SCRATCH_BYTES, stream);
 }

@@ -1,28 +1,32 @@
 // K1 reshape-and-cache, K3 copy-on-write block copy, K4b RoPE + scatter.
 //
-// All three are pure data movement over the flat per-layer cache
-// [num_slots, num_kv_heads, head_dim]. They are HBM-bound byte copies: each
+// All three are pure data movement over the paged per-layer cache, token-major
+// [num_slots, num_kv_heads, head_dim] or head-major [num_blocks, num_kv_heads,
+// block_size, head_dim] (KvGeom). They are HBM-bound byte copies: each
 // workgroup moves whole rows with the widest aligned vector the operands allow.
 #include "vl_common.h"
 
 namespace {
 
+// A token's row of nvec vectors lands in the cache as segments of seg_vec
+// vectors: one segment at the slot's row (token-major), or one per KV head
+// at that head's row (head-major).
 template <typename V>
 __global__ void __launch_bounds__(256) scatter_rows_kernel(
     const char* __restrict__ key, const char* __restrict__ value, int64_t key_stride_b,
     int64_t value_stride_b, char* __restrict__ kc, char* __restrict__ vc,
-    const int32_t* __restrict__ slots, int64_t num_tokens, int nvec) {
+    const int32_t* __restrict__ slots, int64_t num_tokens, KvGeom g, int es, int seg_vec,
+    int nvec) {
   for (int64_t t = blockIdx.x; t < num_tokens; t += gridDim.x) {
     const int slot = slots[t];
     if (slot < 0) continue;
-    const int64_t row_b = (int64_t)nvec * sizeof(V);
     const V* ks = reinterpret_cast<const V*>(key + t * key_stride_b);
     const V* vs = reinterpret_cast<const V*>(value + t * value_stride_b);
-    V* kd = reinterpret_cast<V*>(kc + (int64_t)slot * row_b);
-    V* vd = reinterpret_cast<V*>(vc + (int64_t)slot * row_b);
     for (int i = threadIdx.x; i < nvec; i += blockDim.x) {
-      kd[i] = ks[i];
-      vd[i] = vs[i];
+      const int seg = i / seg_vec;
+      const int64_t off = g.at(slot, seg) * es + (int64_t)(i - seg * seg_vec) * sizeof(V);
+      *reinterpret_cast<V*>(kc + off) = ks[i];
+      *reinterpret_cast<V*>(vc + off) = vs[i];
     }
   }
 }
@@ -60,7 +64,7 @@ __global__ void __launch_bounds__(256) rope_and_cache_kernel(
     const float* __restrict__ qkv, int64_t qkv_stride, float* __restrict__ q_out,
     TC* __restrict__ kc, TC* __restrict__ vc, const int32_t* __restrict__ positions,
     const int32_t* __restrict__ slots, const float* __restrict__ cos_t,
-    const float* __restrict__ sin_t, int64_t num_tokens, int nh, int nkv, int hd) {
+    const float* __restrict__ sin_t, int64_t num_tokens, int nh, int nkv, int hd, KvGeom g) {
   const int half = hd >> 1;
   const int q_pairs = nh * half;
   const int k_pairs = nkv * half;
@@ -82,15 +86,17 @@ __global__ void __launch_bounds__(256) rope_and_cache_kernel(
         dst[0] = oe;
         dst[1] = oo;
       } else if (slot >= 0) {
-        TC* dst = kc + (int64_t)slot * v_elems + head * hd + 2 * pr;
+        TC* dst = kc + g.at(slot, head) + 2 * pr;
         Elem<TC>::store(dst, 0, oe);
         Elem<TC>::store(dst, 1, oo);
       }
     }
     if (slot >= 0) {
       const float* vs = row + (nh + nkv) * hd;
-      TC* vd = vc + (int64_t)slot * v_elems;
-      for (int i = threadIdx.x; i < v_elems; i += blockDim.x) Elem<TC>::store(vd, i, vs[i]);
+      for (int i = threadIdx.x; i < v_elems; i += blockDim.x) {
+        const int head = i / hd;
+        Elem<TC>::store(vc + g.at(slot, head), i - head * hd, vs[i]);
+      }
     }
   }
 }
@@ -114,9 +120,12 @@ __global__ void __launch_bounds__(256) resolve_tokens_kernel(int32_t* __restrict
 extern "C" int vl_reshape_and_cache(const void* key, const void* value, int64_t key_stride,
                                     int64_t value_stride, void* key_cache, void* value_cache,
                                     const int32_t* slot_mapping, int64_t num_tokens,
-                                    int num_kv_heads, int head_dim, int dtype, void* stream) {
+                                    int num_kv_heads, int head_dim, int dtype, int kv_layout,
+                                    int block_size, void* stream) {
   VL_CHECK_ARG(dtype == VL_DTYPE_F32 || dtype == VL_DTYPE_BF16, "bad dtype %d", dtype);
   VL_CHECK_ARG(num_tokens >= 0 && num_kv_heads > 0 && head_dim > 0, "bad shape");
+  KvGeom g;
+  if (int rc = vl_kv_geom(kv_layout, block_size, num_kv_heads, head_dim, &g)) return rc;
   if (num_tokens == 0) return VL_OK;
   VL_CHECK_ARG(key && value && key_cache && value_cache && slot_mapping, "null pointer");
   const int es = dtype == VL_DTYPE_F32 ? 4 : 2;
@@ -127,26 +136,28 @@ extern "C" int vl_reshape_and_cache(const void* key, const void* value, int64_t 
                "row stride smaller than a row");
   hipStream_t st = (hipStream_t)stream;
   const int grid = (int)(num_tokens < 65536 ? num_tokens : 65536);
+  // a contiguous segment: the whole row (token-major) or one head's D elements
+  const int64_t seg_b = kv_layout == VL_KV_HEAD_MAJOR ? (int64_t)head_dim * es : row_b;
   auto ok = [&](int64_t a) {
-    return row_b % a == 0 && ks_b % a == 0 && vs_b % a == 0 && aligned(key, a) &&
+    return seg_b % a == 0 && ks_b % a == 0 && vs_b % a == 0 && aligned(key, a) &&
            aligned(value, a) && aligned(key_cache, a) && aligned(value_cache, a);
   };
   if (ok(16)) {
     const int nvec = (int)(row_b / 16);
     scatter_rows_kernel<uint4><<<grid, nvec < 256 ? ((nvec + 63) / 64) * 64 : 256, 0, st>>>(
         (const char*)key, (const char*)value, ks_b, vs_b, (char*)key_cache, (char*)value_cache,
-        slot_mapping, num_tokens, nvec);
+        slot_mapping, num_tokens, g, es, (int)(seg_b / 16), nvec);
   } else if (ok(4)) {
     const int nvec = (int)(row_b / 4);
     scatter_rows_kernel<uint32_t><<<grid, 256, 0, st>>>(
         (const char*)key, (const char*)value, ks_b, vs_b, (char*)key_cache, (char*)value_cache,
-        slot_mapping, num_tokens, nvec);
+        slot_mapping, num_tokens, g, es, (int)(seg_b / 4), nvec);
   } else {
     VL_CHECK_ARG(ok(2), "operands not 2-byte aligned");
     const int nvec = (int)(row_b / 2);
     scatter_rows_kernel<uint16_t><<<grid, 256, 0, st>>>(
         (const char*)key, (const char*)value, ks_b, vs_b, (char*)key_cache, (char*)value_cache,
-        slot_mapping, num_tokens, nvec);
+        slot_mapping, num_tokens, g, es, (int)(seg_b / 2), nvec);
   }
   VL_CHECK_LAUNCH();
   return VL_OK;
@@ -183,12 +194,15 @@ extern "C" int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_
                                  void* key_cache, void* value_cache, const int32_t* positions,
                                  const int32_t* slot_mapping, const float* cos_table,
                                  const float* sin_table, int64_t num_tokens, int num_heads,
-                                 int num_kv_heads, int head_dim, int cache_dtype, void* stream) {
+                                 int num_kv_heads, int head_dim, int cache_dtype, int kv_layout,
+                                 int block_size, void* stream) {
   VL_CHECK_ARG(cache_dtype == VL_DTYPE_F32 || cache_dtype == VL_DTYPE_BF16, "bad cache dtype %d",
                cache_dtype);
   VL_CHECK_ARG(num_tokens >= 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0 &&
                    head_dim % 2 == 0,
                "bad shape");
+  KvGeom g;
+  if (int rc = vl_kv_geom(kv_layout, block_size, num_kv_heads, head_dim, &g)) return rc;
   VL_CHECK_ARG(qkv_stride >= (int64_t)(num_heads + 2 * num_kv_heads) * head_dim,
                "qkv row stride too small");
   if (num_tokens == 0) return VL_OK;
@@ -199,11 +213,11 @@ extern "C" int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_
   if (cache_dtype == VL_DTYPE_F32)
     rope_and_cache_kernel<float><<<grid, 128, 0, (hipStream_t)stream>>>(
         qkv, qkv_stride, q_out, (float*)key_cache, (float*)value_cache, positions, slot_mapping,
-        cos_table, sin_table, num_tokens, num_heads, num_kv_heads, head_dim);
+        cos_table, sin_table, num_tokens, num_heads, num_kv_heads, head_dim, g);
   else
     rope_and_cache_kernel<uint16_t><<<grid, 128, 0, (hipStream_t)stream>>>(
         qkv, qkv_stride, q_out, (uint16_t*)key_cache, (uint16_t*)value_cache, positions,
-        slot_mapping, cos_table, sin_table, num_tokens, num_heads, num_kv_heads, head_dim);
+        slot_mapping, cos_table, sin_table, num_tokens, num_heads, num_kv_heads, head_dim, g);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }

@@ -57,8 +57,9 @@ __device__ __forceinline__ void rotate_pair_f32(float e, float o, float c, float
 // Where MODE 3 puts the columns [q | k | v] of a fused QKV projection.
 struct RopeCache {
   float* q_out;  // [rows, nh * hd]
-  void* kc;      // [slots, nkv * hd], float or (kv_bf16) bf16 bits
+  void* kc;      // paged cache (layout geom), float or (kv_bf16) bf16 bits
   void* vc;
+  KvGeom geom;
   const int32_t* positions;
   const int32_t* slots;
   const float* cos_t;  // [max_pos, hd / 2]
@@ -290,9 +291,10 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
       if (col < qd)
         rc.q_out[(int64_t)r * qd + col] = val;
       else if (slot >= 0)
-        store_cache(rc.kc, (int64_t)slot * kd + base, val, rc.kv_bf16);
+        store_cache(rc.kc, rc.geom.at(slot, base / rc.hd) + base % rc.hd, val, rc.kv_bf16);
     } else if (slot >= 0) {
-      store_cache(rc.vc, (int64_t)slot * kd + (col - qd - kd), v[0], rc.kv_bf16);
+      const int vcol = col - qd - kd;
+      store_cache(rc.vc, rc.geom.at(slot, vcol / rc.hd) + vcol % rc.hd, v[0], rc.kv_bf16);
     }
   }
 }
@@ -364,9 +366,12 @@ extern "C" int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cach
                                  const int32_t* positions, const int32_t* slot_mapping,
                                  const float* cos_table, const float* sin_table, int rows, int k,
                                  int num_heads, int num_kv_heads, int head_dim, int cache_dtype,
-                                 void* stream) {
+                                 int kv_layout, int block_size, void* stream) {
   VL_CHECK_ARG(cache_dtype == VL_DTYPE_F32 || cache_dtype == VL_DTYPE_BF16, "bad cache dtype %d",
                cache_dtype);
+  KvGeom geom;
+  if (num_kv_heads > 0 && head_dim > 0)
+    if (int rc = vl_kv_geom(kv_layout, block_size, num_kv_heads, head_dim, &geom)) return rc;
   VL_CHECK_ARG(rows >= 0 && rows <= kRowsMax, "rows must be in 0..%d", kRowsMax);
   VL_CHECK_ARG(k > 0 && k % 16 == 0 && k <= 1024, "k must be a multiple of 16, at most 1024");
   VL_CHECK_ARG(num_heads > 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0,
@@ -388,6 +393,7 @@ extern "C" int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cach
   rc.slots = slot_mapping, rc.cos_t = cos_table, rc.sin_t = sin_table;
   rc.nh = num_heads, rc.nkv = num_kv_heads, rc.hd = head_dim;
   rc.kv_bf16 = cache_dtype == VL_DTYPE_BF16;
+  rc.geom = geom;
   hipStream_t st = (hipStream_t)stream;
   const bool nrm = norm_weight != nullptr;
 #define VL_QKV(NORM, KM) \

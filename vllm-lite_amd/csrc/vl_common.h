@@ -85,3 +85,24 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __host__ __device__ __forceinline__ int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
 __host__ __device__ __forceinline__ int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// ----------------------------------------------------------- cache layout ---
+// A paged K or V cache in one of two layouts: VL_KV_TOKEN_MAJOR, [num_slots,
+// Hkv, D] with slot = block * block_size + offset, or VL_KV_HEAD_MAJOR,
+// [num_blocks, Hkv, block_size, D]. A block spans the same block_size * Hkv
+// * D elements in both, so block copies do not depend on the layout. The row
+// of (slot, KV head h) starts at element
+//   (slot >> bs_log2) * blk + (slot & (2^bs_log2 - 1)) * row + h * head
+// (token-major: bs_log2 0, blk = row = Hkv * D, head = D; head-major: blk =
+// 2^bs_log2 * Hkv * D, row = D, head = 2^bs_log2 * D).
+struct KvGeom {
+  int64_t blk, row, head;
+  int bs_log2;
+  __host__ __device__ __forceinline__ int64_t at(int64_t slot, int h) const {
+    return (slot >> bs_log2) * blk + (slot & ((1ll << bs_log2) - 1)) * row + (int64_t)h * head;
+  }
+};
+
+// Checks kv_layout (and, for head-major, that block_size is a power of two)
+// and fills *g; a VL_EINVAL return carries its message.
+int vl_kv_geom(int kv_layout, int block_size, int num_kv_heads, int head_dim, KvGeom* g);

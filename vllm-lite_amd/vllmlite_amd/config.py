@@ -47,10 +47,18 @@ class CacheConfig:
     # "bfloat16" (half the cache bytes; K/V rounded to nearest even when
     # written, everything else stays fp32)
     kv_dtype: str = "float32"
+    # order of the rows inside a cache block: "token" ([slots, Hkv, D], the
+    # reference's), or "head" ([blocks, Hkv, block_size, D]: each KV head's
+    # rows of a block contiguous; block_size a power of two)
+    kv_layout: str = "token"
 
     def __post_init__(self):
         if self.kv_dtype not in ("float32", "bfloat16"):
             raise ValueError("kv_dtype must be float32 or bfloat16")
+        if self.kv_layout not in ("token", "head"):
+            raise ValueError("kv_layout must be token or head")
+        if self.kv_layout == "head" and self.block_size & (self.block_size - 1):
+            raise ValueError("a head-major cache needs a power-of-two block_size")
 
     @property
     def max_cached_tokens(self) -> int:

@@ -174,7 +174,11 @@ class HipRunner(ModelRunner):
             self.cos = torch.from_numpy(cos).to(self.device)
             self.sin = torch.from_numpy(sin).to(self.device)
             slots = cache_cfg.num_blocks * cache_cfg.block_size
-            shape = (mc.n_layers, slots, mc.n_kv_heads, mc.head_dim)
+            if getattr(cache_cfg, "kv_layout", "token") == "head":
+                shape = (mc.n_layers, cache_cfg.num_blocks, mc.n_kv_heads, cache_cfg.block_size,
+                         mc.head_dim)
+            else:
+                shape = (mc.n_layers, slots, mc.n_kv_heads, mc.head_dim)
             kv = torch.bfloat16 if getattr(cache_cfg, "kv_dtype", "float32") == "bfloat16" \
                 else torch.float32
             self.cache_k = torch.zeros(shape, dtype=kv, device=self.device)

@@ -18,7 +18,10 @@ import torch
 from .build import LIB_PATH
 
 F32, BF16, F32_BF16KV = 0, 1, 2  # VL_DTYPE_*: F32_BF16KV = fp32 query / out over bf16 caches
-ABI_VERSION = 4  # vl_abi_version() of the library these signatures describe
+# VL_KV_*: a per-layer cache tensor [slots, Hkv, D] is token-major (the
+# reference's layout), [blocks, Hkv, block_size, D] head-major
+KV_TOKEN_MAJOR, KV_HEAD_MAJOR = 0, 1
+ABI_VERSION = 5  # vl_abi_version() of the library these signatures describe
 _c_void_p = ctypes.c_void_p
 _i32, _i64, _f32, _size = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
 
@@ -27,31 +30,32 @@ SIGNATURES = {
     "vl_last_error": (ctypes.c_char_p, []),
     "vl_abi_version": (_i32, []),
     "vl_reshape_and_cache": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
-                                    _c_void_p, _i64, _i32, _i32, _i32, _c_void_p]),
+                                    _c_void_p, _i64, _i32, _i32, _i32, _i32, _i32, _c_void_p]),
     "vl_copy_blocks": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i64, _i64, _i32,
                               _c_void_p]),
     "vl_paged_attention_workspace_size": (_size, [_i32, _i32, _i32, _i32, _i32]),
     "vl_paged_attention_min_workspace": (_size, [_i32]),
     "vl_paged_attention": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
                                   _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32,
-                                  _f32, _i32, _i32, _i32, _i32, _c_void_p, _size, _c_void_p]),
+                                  _f32, _i32, _i32, _i32, _i32, _i32, _c_void_p, _size,
+                                  _c_void_p]),
     "vl_paged_attention_reads_plan": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "vl_paged_attention_plan": (_i32, [_c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32,
                                        _i32, _c_void_p, _size, _c_void_p]),
     "vl_paged_attention_run": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,
                                       _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32, _i32,
-                                      _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32,
+                                      _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _i32,
                                       _c_void_p, _size, _c_void_p]),
     "vl_paged_attention_noalloc": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,
                                           _c_void_p, _i32, _c_void_p, _c_void_p, _i32, _i32,
                                           _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32,
-                                          _i32, _c_void_p]),
+                                          _i32, _i32, _c_void_p]),
     "vl_rms_norm": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _f32,
                            _c_void_p]),
     "vl_silu_mul": (_i32, [_c_void_p, _c_void_p, _i64, _i32, _c_void_p]),
     "vl_rope_and_cache": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                  _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32, _i32,
-                                 _c_void_p]),
+                                 _i32, _i32, _c_void_p]),
     "vl_greedy_verify": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i32,
                                 _c_void_p, _c_void_p, _i32, _c_void_p]),
     "vl_argmax_rows": (_i32, [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p]),
@@ -60,7 +64,7 @@ SIGNATURES = {
     "vl_qkv_rope_cache": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
                                  _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _f32, _c_void_p,
                                  _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32,
-                                 _i32, _c_void_p]),
+                                 _i32, _i32, _i32, _c_void_p]),
     "vl_resolve_tokens": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p]),
 }
 
@@ -122,6 +126,16 @@ def _cache_dtype(key_cache: torch.Tensor, value_cache: torch.Tensor) -> int:
     return _dtype_code(key_cache)
 
 
+def kv_layout(cache: torch.Tensor):
+    """(VL_KV_* layout, num_kv_heads, block_size (0: token-major, any),
+    head_dim) of one layer's cache tensor: [slots, Hkv, D] is token-major,
+    [blocks, Hkv, block_size, D] head-major."""
+    if cache.dim() == 3:
+        return KV_TOKEN_MAJOR, cache.shape[1], 0, cache.shape[2]
+    _need(cache.dim() == 4, "a layer's cache is [slots, Hkv, D] or [blocks, Hkv, block_size, D]")
+    return KV_HEAD_MAJOR, cache.shape[1], cache.shape[2], cache.shape[3]
+
+
 def _need(cond: bool, msg: str) -> None:
     if not cond:
         raise ValueError(msg)
@@ -135,10 +149,12 @@ def _dev_i32(t: torch.Tensor, name: str) -> None:
 # ------------------------------------------------------------------ K1 -----
 def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, key_cache: torch.Tensor,
                       value_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
-    """key/value [T, Hkv, D] (rows may be strided), caches [slots, Hkv, D]."""
+    """key/value [T, Hkv, D] (rows may be strided), caches [slots, Hkv, D] or
+    head-major [blocks, Hkv, block_size, D]."""
     T, hkv, d = key.shape
     _need(value.shape == key.shape, "key/value shapes differ")
-    _need(key_cache.shape[1:] == (hkv, d) and value_cache.shape == key_cache.shape,
+    layout, c_hkv, bs, c_d = kv_layout(key_cache)
+    _need((c_hkv, c_d) == (hkv, d) and value_cache.shape == key_cache.shape,
           "cache shape mismatch")
     _need(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
     for t in (key, value):
@@ -148,21 +164,27 @@ def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, key_cache: torch.T
     _need(slot_mapping.numel() == T, "slot_mapping length != tokens")
     _check(lib().vl_reshape_and_cache(_ptr(key), _ptr(value), key.stride(0), value.stride(0),
                                       _ptr(key_cache), _ptr(value_cache), _ptr(slot_mapping), T,
-                                      hkv, d, _dtype_code(key), _stream()),
+                                      hkv, d, _dtype_code(key), layout, bs, _stream()),
            "vl_reshape_and_cache")
 
 
 # ------------------------------------------------------------------ K3 -----
 def copy_blocks(key_cache: torch.Tensor, value_cache: torch.Tensor, block_pairs: torch.Tensor,
                 block_size: int) -> None:
-    """Caches [L, slots, Hkv, D]; block_pairs int32 [n, 2] on the device."""
+    """Caches [L, slots, Hkv, D] or head-major [L, blocks, Hkv, block_size, D]
+    (a block is the same span in both); block_pairs int32 [n, 2] on the
+    device."""
     _need(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
-    _need(key_cache.shape == value_cache.shape and key_cache.dim() == 4, "cache shape mismatch")
+    _need(key_cache.shape == value_cache.shape and key_cache.dim() in (4, 5),
+          "cache shape mismatch")
+    _need(key_cache.dim() == 4 or key_cache.shape[3] == block_size, "block_size mismatch")
     _dev_i32(block_pairs, "block_pairs")
     n = block_pairs.shape[0]
-    L, slots, hkv, d = key_cache.shape
+    L = key_cache.shape[0]
+    layer = key_cache[0].numel()
+    hkv, d = key_cache.shape[2], key_cache.shape[-1]
     _check(lib().vl_copy_blocks(_ptr(key_cache), _ptr(value_cache), _ptr(block_pairs), n, L,
-                                slots * hkv * d, block_size * hkv * d, _dtype_code(key_cache),
+                                layer, block_size * hkv * d, _dtype_code(key_cache),
                                 _stream()),
            "vl_copy_blocks")
 
@@ -193,8 +215,8 @@ def _attn_check(out, query, key_cache, value_cache, block_tables, seq_lens, quer
     _need(query.stride(2) == 1 and query.stride(1) == D, "query rows must be [H, D] contiguous")
     _need(out.shape == (T, H, D) and out.is_contiguous() and out.dtype == query.dtype,
           "out must be a contiguous [T, H, D] tensor of the query dtype")
-    _need(key_cache.dim() == 3 and key_cache.shape == value_cache.shape and key_cache.shape[2] == D,
-          "cache shape mismatch")
+    _need(key_cache.dim() in (3, 4) and key_cache.shape == value_cache.shape and
+          key_cache.shape[-1] == D, "cache shape mismatch")
     _need(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
     _need(key_cache.dtype == value_cache.dtype and
           (key_cache.dtype == query.dtype or
@@ -212,14 +234,22 @@ def _attn_check(out, query, key_cache, value_cache, block_tables, seq_lens, quer
     return T, H, hkv, D, S
 
 
+def _cache_layout(key_cache, block_size):
+    layout, _, bs, _ = kv_layout(key_cache)
+    _need(layout == KV_TOKEN_MAJOR or bs == block_size,
+          "block_size differs from the head-major cache's block dimension")
+    return layout
+
+
 def _attn_args(out, query, key_cache, value_cache, block_tables, seq_lens, query_start_loc,
                scale, block_size, workspace, max_query_len, min_query_len, max_context_len,
                T, H, hkv, D, S):
     return (_ptr(out), _ptr(query), query.stride(0), _ptr(key_cache), _ptr(value_cache),
             _ptr(block_tables), block_tables.stride(0), _ptr(seq_lens), _ptr(query_start_loc),
             S, T, H, hkv, D, block_size, float(scale), _attn_dtype(query, key_cache),
-            int(max_query_len),
-            int(min_query_len), int(max_context_len), _ptr(workspace), workspace.numel() * workspace.element_size(), _stream())
+            _cache_layout(key_cache, block_size), int(max_query_len), int(min_query_len),
+            int(max_context_len), _ptr(workspace), workspace.numel() * workspace.element_size(),
+            _stream())
 
 
 def paged_attention(out: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
@@ -227,8 +257,9 @@ def paged_attention(out: torch.Tensor, query: torch.Tensor, key_cache: torch.Ten
                     query_start_loc: torch.Tensor, scale: float, block_size: int,
                     workspace: torch.Tensor, max_query_len: int = 0,
                     min_query_len: int = 0, max_context_len: int = 0) -> None:
-    """query [T, H, D] (token rows may be strided), caches [slots, Hkv, D],
-    block_tables int32 [S, W], seq_lens int32 [S], query_start_loc int32 [S+1].
+    """query [T, H, D] (token rows may be strided), caches [slots, Hkv, D] or
+    head-major [blocks, Hkv, block_size, D], block_tables int32 [S, W],
+    seq_lens int32 [S], query_start_loc int32 [S+1].
     max_query_len / min_query_len: host-known bounds on the query count of
     the sequences that have queries, max_context_len on seq_lens (0 =
     unknown); they pick the launches."""
@@ -246,7 +277,7 @@ def paged_attention_plan(query: torch.Tensor, key_cache: torch.Tensor, seq_lens:
                          workspace: torch.Tensor) -> None:
     """Plan once per batch; reuse with paged_attention_run for every layer."""
     T, H, D = query.shape
-    hkv = key_cache.shape[-2]
+    hkv = kv_layout(key_cache)[1]
     _dev_i32(seq_lens, "seq_lens")
     _dev_i32(query_start_loc, "query_start_loc")
     S = seq_lens.numel()
@@ -292,7 +323,8 @@ def paged_attention_noalloc(out, query, key_cache, value_cache, block_tables, se
     _need(query.stride(2) == 1 and query.stride(1) == D, "query rows must be [H, D] contiguous")
     _need(out.shape == (T, H, D) and out.is_contiguous() and out.dtype == query.dtype,
           "out must be a contiguous [T, H, D] tensor of the query dtype")
-    _need(key_cache.dim() == 3 and key_cache.shape == value_cache.shape, "cache shape mismatch")
+    _need(key_cache.dim() in (3, 4) and key_cache.shape == value_cache.shape,
+          "cache shape mismatch")
     for t, n in ((block_tables, "block_tables"), (seq_lens, "seq_lens"),
                  (query_start_loc, "query_start_loc")):
         _dev_i32(t, n)
@@ -301,7 +333,8 @@ def paged_attention_noalloc(out, query, key_cache, value_cache, block_tables, se
         _ptr(out), _ptr(query), query.stride(0), _ptr(key_cache), _ptr(value_cache),
         _ptr(block_tables), block_tables.stride(0), _ptr(seq_lens), _ptr(query_start_loc), S, T,
         H, key_cache.shape[1], D, block_size, float(scale), _attn_dtype(query, key_cache),
-        int(max_query_len), int(min_query_len), int(max_context_len), _stream()),
+        _cache_layout(key_cache, block_size), int(max_query_len), int(min_query_len),
+        int(max_context_len), _stream()),
         "vl_paged_attention_noalloc")
 
 
@@ -394,6 +427,9 @@ def qkv_rope_cache(q_out: torch.Tensor, key_cache: torch.Tensor, value_cache: to
         _need(t.dtype == torch.float32 and t.stride(-1) == 1, "fp32 row-major tensors required")
     _need(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
     cdt = _cache_dtype(key_cache, value_cache)
+    layout, c_hkv, bs, c_d = kv_layout(key_cache)
+    _need((c_hkv, c_d) == (num_kv_heads, head_dim) and value_cache.shape == key_cache.shape,
+          "cache shape")
     _need(positions.numel() >= rows and slot_mapping.numel() >= rows, "shape mismatch")
     tiles, wstride = _weight_layout(weight, k, (num_heads + 2 * num_kv_heads) * head_dim, 1)
     _check(lib().vl_qkv_rope_cache(_ptr(q_out), _ptr(key_cache), _ptr(value_cache), _ptr(x),
@@ -402,7 +438,7 @@ def qkv_rope_cache(q_out: torch.Tensor, key_cache: torch.Tensor, value_cache: to
                                    _ptr(norm_weight),
                                    float(eps), _ptr(positions), _ptr(slot_mapping), _ptr(cos),
                                    _ptr(sin), rows, k, num_heads, num_kv_heads, head_dim, cdt,
-                                   _stream()), "vl_qkv_rope_cache")
+                                   layout, bs, _stream()), "vl_qkv_rope_cache")
 
 
 def silu_mul(out: torch.Tensor, gate_up: torch.Tensor) -> None:
@@ -421,7 +457,8 @@ def rope_and_cache(qkv: torch.Tensor, q_out: torch.Tensor, key_cache: torch.Tens
     _need(qkv.stride(1) == 1 and qkv.shape[1] >= (num_heads + 2 * num_kv_heads) * head_dim,
           "qkv rows must hold q|k|v")
     _need(q_out.shape == (T, num_heads, head_dim) and q_out.is_contiguous(), "q_out shape")
-    _need(key_cache.shape[1:] == (num_kv_heads, head_dim) and key_cache.is_contiguous() and
+    layout, c_hkv, bs, c_d = kv_layout(key_cache)
+    _need((c_hkv, c_d) == (num_kv_heads, head_dim) and key_cache.is_contiguous() and
           value_cache.shape == key_cache.shape and value_cache.is_contiguous(), "cache shape")
     _need(qkv.dtype == q_out.dtype == torch.float32, "qkv and q_out are fp32")
     cdt = _cache_dtype(key_cache, value_cache)
@@ -431,7 +468,7 @@ def rope_and_cache(qkv: torch.Tensor, q_out: torch.Tensor, key_cache: torch.Tens
     _check(lib().vl_rope_and_cache(_ptr(qkv), qkv.stride(0), _ptr(q_out), _ptr(key_cache),
                                    _ptr(value_cache), _ptr(positions), _ptr(slot_mapping),
                                    _ptr(cos), _ptr(sin), T, num_heads, num_kv_heads, head_dim,
-                                   cdt, _stream()), "vl_rope_and_cache")
+                                   cdt, layout, bs, _stream()), "vl_rope_and_cache")
 
 
 # ------------------------------------------------------------------ K5 -----

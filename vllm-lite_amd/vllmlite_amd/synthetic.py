@@ -97,6 +97,13 @@ def build(torch, seqs, seed=0, pool_blocks=POOL, dtype=None, heads=(H, HKV, D), 
         max_q=int(q_lens.max()), min_q=int(q_lens[q_lens > 0].min()) if (q_lens > 0).any() else 0)
 
 
+def to_head_major(cache, bs):
+    """A token-major cache [slots, Hkv, D] as a new head-major tensor
+    [blocks, Hkv, bs, D] (the same rows; slot = block * bs + offset)."""
+    s, hkv, d = cache.shape
+    return cache.view(s // bs, bs, hkv, d).permute(0, 2, 1, 3).contiguous()
+
+
 def algorithmic_bytes(b, with_scatter=True):
     """Each K/V element once, Q read and out written once, block-table
     entries and lengths; plus, with the scatter, the new K/V read and
