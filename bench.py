@@ -183,10 +183,11 @@ def cpu_baseline(torch, b, budget_s=12.0):
                       f"one BLAS thread, half the time budget)"}
 
 
-def mixed_leg(torch, ops, syn, steps, warmup, profile_only=False):
+def mixed_leg(torch, ops, syn, steps, warmup, profile_only=False, layout="token"):
     """Scatter + plan + one attention launch over 16 prefill chunks and 200
     decodes; also the prefill chunks alone and the decodes alone. profile_only
-    names the one part to run (True: the mixed batch)."""
+    names the one part to run (True: the mixed batch); layout "head": the
+    caches as head-major blocks."""
     out = {}
     full = syn.mixed_8392_seqs(0)
     parts = {"mixed": full, "prefill_only": full[200:], "decode_only": full[:200]}
@@ -198,11 +199,12 @@ def mixed_leg(torch, ops, syn, steps, warmup, profile_only=False):
         o = torch.empty_like(b["q"])
         ws = ops.AttentionWorkspace().get(
             ops.paged_attention_workspace_size(S, T, syn.H, syn.D, int(b["ctx"].max())))
+        kc, vc = _layout_caches(syn, b, layout)
 
         def step():
-            ops.reshape_and_cache(b["knew"], b["vnew"], b["kc"], b["vc"], b["slot_mapping"])
-            ops.paged_attention_plan(b["q"], b["kc"], b["seq_lens"], b["qsl"], syn.BS, ws)
-            ops.paged_attention_run(o, b["q"], b["kc"], b["vc"], b["bt"], b["seq_lens"], b["qsl"],
+            ops.reshape_and_cache(b["knew"], b["vnew"], kc, vc, b["slot_mapping"])
+            ops.paged_attention_plan(b["q"], kc, b["seq_lens"], b["qsl"], syn.BS, ws)
+            ops.paged_attention_run(o, b["q"], kc, vc, b["bt"], b["seq_lens"], b["qsl"],
                                     b["scale"], syn.BS, ws, max_query_len=b["max_q"],
                                     min_query_len=b["min_q"])
 
@@ -225,10 +227,11 @@ def mixed_leg(torch, ops, syn, steps, warmup, profile_only=False):
              "mfma_frac": round(flops / ms / 1e9 / PEAK_BF16_TFLOPS, 4),
              "roofline_us": round(roof_ms * 1e3, 1), "roofline_frac": round(roof_ms / ms, 4)}
         if not profile_only:
+            _token_major_back(syn, b, kc, vc, layout)
             pick = [int(i) for i in np.linspace(0, S - 1, 6).astype(int)]
             r["check_rel_err"] = syn.torch_reference_check(torch, b, o, pick)
         out[name] = r
-        del b, o, ws
+        del b, o, ws, kc, vc
         torch.cuda.empty_cache()
     out["workload"] = ("16 prefill chunks x 512 tokens with 0-2048 prior context + 200 decodes "
                        "with context 128-4096, H32/Hkv8/D128 bf16, block 16; a step = K/V scatter "
@@ -236,10 +239,27 @@ def mixed_leg(torch, ops, syn, steps, warmup, profile_only=False):
     return out
 
 
-def verify_leg(torch, ops, syn, steps, warmup, profile_only=False):
+def _layout_caches(syn, b, layout):
+    """The batch's caches for the timed steps: the token-major ones, or
+    head-major copies."""
+    if layout == "head":
+        return syn.to_head_major(b["kc"], syn.BS), syn.to_head_major(b["vc"], syn.BS)
+    return b["kc"], b["vc"]
+
+
+def _token_major_back(syn, b, kc, vc, layout):
+    """After head-major steps: the batch's token-major caches with what the
+    steps scattered, for the reference check."""
+    if layout == "head":
+        b["kc"], b["vc"] = syn.to_token_major(kc), syn.to_token_major(vc)
+
+
+def verify_leg(torch, ops, syn, steps, warmup, profile_only=False, layout="token"):
     """64 sequences x 5 query positions over contexts 1024..32768, then
-    greedy acceptance of 4 drafts from fp32 logits [320, 32000]."""
+    greedy acceptance of 4 drafts from fp32 logits [320, 32000]; layout
+    "head": the caches as head-major blocks."""
     b = syn.build(torch, syn.verify_64x5_seqs(0), seed=3)
+    kc, vc = _layout_caches(syn, b, layout)
     S, T = len(b["seqs"]), int(b["q_lens"].sum())
     V, K = 32000, 4
     o = torch.empty_like(b["q"])
@@ -263,9 +283,9 @@ def verify_leg(torch, ops, syn, steps, warmup, profile_only=False):
     nacc = torch.empty((S,), dtype=torch.int32, device="cuda")
 
     def step():
-        ops.reshape_and_cache(b["knew"], b["vnew"], b["kc"], b["vc"], b["slot_mapping"])
-        ops.paged_attention_plan(b["q"], b["kc"], b["seq_lens"], b["qsl"], syn.BS, ws)
-        ops.paged_attention_run(o, b["q"], b["kc"], b["vc"], b["bt"], b["seq_lens"], b["qsl"],
+        ops.reshape_and_cache(b["knew"], b["vnew"], kc, vc, b["slot_mapping"])
+        ops.paged_attention_plan(b["q"], kc, b["seq_lens"], b["qsl"], syn.BS, ws)
+        ops.paged_attention_run(o, b["q"], kc, vc, b["bt"], b["seq_lens"], b["qsl"],
                                 b["scale"], syn.BS, ws, max_query_len=5, min_query_len=5)
         ops.greedy_verify(logits, row_start, nd, dr, toks, nacc)
 
@@ -295,8 +315,9 @@ def verify_leg(torch, ops, syn, steps, warmup, profile_only=False):
             want = [int(picks[s * 5 + r]) for r in range(accept[s] + 1)]
             ok = ok and got_tok[s, :len(want)].tolist() == want and bool((got_tok[s, len(want):] == -1).all())
         r["acceptance_exact"] = ok
+        _token_major_back(syn, b, kc, vc, layout)
         r["check_rel_err"] = syn.torch_reference_check(torch, b, o, [0, 21, 42, 63])
-    del b, o, ws, logits
+    del b, o, ws, logits, kc, vc
     torch.cuda.empty_cache()
     return r
 

@@ -104,6 +104,12 @@ def to_head_major(cache, bs):
     return cache.view(s // bs, bs, hkv, d).permute(0, 2, 1, 3).contiguous()
 
 
+def to_token_major(cache):
+    """The inverse of to_head_major: [blocks, Hkv, bs, D] -> [slots, Hkv, D]."""
+    nb, hkv, bs, d = cache.shape
+    return cache.permute(0, 2, 1, 3).reshape(nb * bs, hkv, d).contiguous()
+
+
 def algorithmic_bytes(b, with_scatter=True):
     """Each K/V element once, Q read and out written once, block-table
     entries and lengths; plus, with the scatter, the new K/V read and
