@@ -392,6 +392,7 @@ MIXES = {
     "shared_prefix_forked": (256, True),
     "mixed_bf16_kv": (0, False),  # the 48-request mix over a bf16 K/V cache
     "mixed_head_major": (0, False),  # ... over head-major cache blocks
+    "mixed_fp8_kv": (0, False),  # ... over an FP8 E4M3 K/V cache
 }
 
 
@@ -403,6 +404,8 @@ def mix_config(name):
             cfg.cache.kv_dtype = "bfloat16"
         if name == "mixed_head_major":
             cfg.cache.kv_layout = "head"
+        if name == "mixed_fp8_kv":
+            cfg.cache.kv_dtype = "float8_e4m3"
         return cfg
     return shared_prefix_config(True)
 
@@ -469,6 +472,7 @@ def e2e_leg(name="mixed", repeat=3, cpu=True):
                          "its partial shared tail)" if fork else "") +
                         f" (greedy), TinyLlama 6L d384 H8/Hkv4 d_ff1024 fp32"
                         f"{', bf16 K/V cache' if cfg.cache.kv_dtype == 'bfloat16' else ''}"
+                        f"{', FP8 E4M3 K/V cache' if cfg.cache.kv_dtype == 'float8_e4m3' else ''}"
                         f"{', head-major cache blocks' if cfg.cache.kv_layout == 'head' else ''}, "
                         "block 16, "
                         f"{cfg.cache.num_blocks} blocks, max_len {cfg.model.max_seq_len}, "
@@ -484,9 +488,9 @@ def e2e_leg(name="mixed", repeat=3, cpu=True):
     gold = gold["streams"] if key is None else gold[key]["streams"]
     same = sum(streams.get(r) == gold[r] for r in gold)
     out["streams_identical_to_reference"] = f"{same}/{len(gold)}"
-    if cfg.cache.kv_dtype == "bfloat16":
+    if cfg.cache.kv_dtype != "float32":
         out["streams_note"] = ("the reference caches fp32; against the oracle runner with the "
-                               "same bf16 cache the streams are checked by the GPU tests")
+                               "same narrow cache the streams are checked by the GPU tests")
     if cpu:
         from oracle.runner import NumpyRunner
         from vllmlite_amd.engine import LLMEngine
@@ -640,6 +644,7 @@ def main():
         extra["e2e_shared_prefix_forked"] = e2e_leg("shared_prefix_forked", cpu=False)
         extra["e2e_bf16_kv_cache"] = e2e_leg("mixed_bf16_kv", cpu=False)
         extra["e2e_head_major_cache"] = e2e_leg("mixed_head_major", cpu=False)
+        extra["e2e_fp8_kv_cache"] = e2e_leg("mixed_fp8_kv", cpu=False)
     line["legs"] = extra
     print(json.dumps(line), flush=True)
 

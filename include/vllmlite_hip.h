@@ -11,8 +11,12 @@
  *     positive hipError_t; vl_last_error() returns the message of the last
  *     failure on the calling thread. Nothing throws across this boundary.
  *   - dtype is VL_DTYPE_F32 (float) or VL_DTYPE_BF16 (raw bfloat16 bits);
- *     the paged-attention calls also take VL_DTYPE_F32_BF16KV: fp32 query
- *     and output over bf16 caches (a bf16 KV cache under an fp32 model).
+ *     the paged-attention calls also take VL_DTYPE_F32_BF16KV and
+ *     VL_DTYPE_F32_FP8KV: fp32 query and output over bf16 or FP8 E4M3
+ *     caches (a narrow KV cache under an fp32 model). FP8 E4M3 is the OCP
+ *     format (4 exponent bits, bias 7, 3 mantissa bits, no infinities, 0x7F
+ *     / 0xFF NaN, largest finite 448); writers round to nearest even and
+ *     saturate finite values beyond 448 to +-448.
  *
  * Cache layout (kv_layout): VL_KV_TOKEN_MAJOR is the reference's
  * (vllmlite/runner.py:41-44), one tensor per layer and per K/V of shape
@@ -38,6 +42,8 @@ extern "C" {
 #define VL_DTYPE_F32 0
 #define VL_DTYPE_BF16 1
 #define VL_DTYPE_F32_BF16KV 2
+#define VL_DTYPE_FP8_E4M3 3   /* cache elements: OCP FP8 E4M3 (e4m3fn) bytes */
+#define VL_DTYPE_F32_FP8KV 4  /* attention: fp32 query and output over FP8 E4M3 caches */
 #define VL_KV_TOKEN_MAJOR 0 /* caches [num_slots, num_kv_heads, head_dim] */
 #define VL_KV_HEAD_MAJOR 1  /* caches [num_blocks, num_kv_heads, block_size, head_dim] */
 #define VL_LINEAR_STORE 0      /* vl_linear_rows: out = f(x) @ W */
@@ -62,7 +68,8 @@ int vl_abi_version(void);
  * for t < num_tokens. key/value rows are [num_kv_heads, head_dim] contiguous,
  * `key_stride`/`value_stride` elements apart. A negative slot skips the token.
  * The caches are kv_layout (block_size is read only for VL_KV_HEAD_MAJOR).
- * Bit-exact copy.
+ * dtype VL_DTYPE_F32, VL_DTYPE_BF16 or VL_DTYPE_FP8_E4M3 (inputs and caches
+ * alike). Bit-exact copy.
  */
 int vl_reshape_and_cache(const void* key, const void* value, int64_t key_stride,
                          int64_t value_stride, void* key_cache, void* value_cache,
@@ -77,7 +84,8 @@ int vl_reshape_and_cache(const void* key, const void* value, int64_t key_stride,
  * the K and the V cache. Pairs are processed in parallel, which equals the
  * reference's in-order loop because no dst is another pair's src and dsts are
  * distinct (fresh blocks, vllmlite/block_manager.py:77-85); the caller must
- * guarantee that. Bit-exact copy.
+ * guarantee that. dtype VL_DTYPE_F32, VL_DTYPE_BF16 or VL_DTYPE_FP8_E4M3.
+ * Bit-exact copy.
  */
 int vl_copy_blocks(void* key_cache, void* value_cache, const int32_t* block_pairs, int num_pairs,
                    int num_layers, int64_t layer_stride, int64_t block_elems, int dtype,
@@ -205,9 +213,10 @@ int vl_silu_mul(float* out, const float* gate_up, int64_t rows, int d_ff, void* 
  * vllmlite/attention.py:21-37), writes rotated q to q_out [num_tokens,
  * num_heads, head_dim] and rotated k / plain v to the caches at
  * slot_mapping[t] (vllmlite/attention.py:47-49). fp32 arithmetic; the caches
- * hold cache_dtype elements (VL_DTYPE_F32, or VL_DTYPE_BF16: each value
- * rounded to nearest even when stored) in kv_layout (block_size is read only
- * for VL_KV_HEAD_MAJOR).
+ * hold cache_dtype elements (VL_DTYPE_F32; VL_DTYPE_BF16 or
+ * VL_DTYPE_FP8_E4M3: each value rounded to nearest even when stored, FP8
+ * saturating at +-448) in kv_layout (block_size is read only for
+ * VL_KV_HEAD_MAJOR).
  */
 int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_out, void* key_cache,
                       void* value_cache, const int32_t* positions, const int32_t* slot_mapping,

@@ -45,6 +45,45 @@ def round_bf16(x: np.ndarray) -> np.ndarray:
     return np.where(np.isnan(a), a, r).astype(np.float32)
 
 
+def fp8_e4m3_decode(codes: np.ndarray) -> np.ndarray:
+    """OCP FP8 E4M3 ("e4m3fn") bytes -> fp32, from the format's definition:
+    sign bit, 4 exponent bits with bias 7, 3 mantissa bits; exponent 0 is
+    subnormal (m * 2^-9); 0x7F / 0xFF are NaN; there are no infinities. No
+    reference counterpart (the reference caches fp32); pinned in
+    tests/test_oracle_fp8.py."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    e, m = (c >> 3) & 15, c & 7
+    mag = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * 2.0 ** (e - 7))
+    mag = np.where((c & 0x7F) == 0x7F, np.nan, mag)
+    return np.where(c & 0x80, -mag, mag).astype(np.float32)
+
+
+_FP8_VALUES = fp8_e4m3_decode(np.arange(0x7F, dtype=np.uint8))  # 0, 2^-9, ..., 448
+
+
+def fp8_e4m3_encode(x: np.ndarray) -> np.ndarray:
+    """fp32 -> OCP FP8 E4M3 bytes, round to nearest with ties to the even
+    code (the one whose mantissa's last bit is 0), saturating: finite values
+    and infinities beyond 448 in magnitude become +-448; NaN becomes 0x7F
+    (0xFF if negative). Found by a search over the 127 non-negative finite
+    values, not by bit manipulation, so it is independent of the kernels'
+    method."""
+    a = np.asarray(x, dtype=np.float32)
+    mag = np.minimum(np.abs(a).astype(np.float64), 448.0)
+    hi = np.searchsorted(_FP8_VALUES, mag, side="left").clip(0, 126)   # first value >= mag
+    lo = np.maximum(hi - 1, 0)
+    d_lo, d_hi = mag - _FP8_VALUES[lo], _FP8_VALUES[hi] - mag
+    pick = np.where(d_lo < d_hi, lo, np.where(d_hi < d_lo, hi, np.where(lo % 2 == 0, lo, hi)))
+    pick = np.where(_FP8_VALUES[hi] == mag, hi, pick)
+    code = pick.astype(np.uint8) | np.where(np.signbit(a), 0x80, 0).astype(np.uint8)
+    return np.where(np.isnan(a), np.where(np.signbit(a), 0xFF, 0x7F), code).astype(np.uint8)
+
+
+def round_fp8_e4m3(x: np.ndarray) -> np.ndarray:
+    """The values an FP8 E4M3 K/V cache holds: fp8_e4m3_encode then decode."""
+    return fp8_e4m3_decode(fp8_e4m3_encode(x))
+
+
 def write_kv(cache_k, cache_v, k, v, slots) -> None:
     """attention.py:47-49: scatter rows into the flat [slots, Hkv, D] cache."""
     cache_k[slots] = k

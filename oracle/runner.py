@@ -5,7 +5,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .attention import gather_slots, round_bf16
+from .attention import gather_slots, round_bf16, round_fp8_e4m3
 from .model import TinyLlamaOracle
 
 
@@ -15,10 +15,11 @@ class NumpyRunner:
     def __init__(self, model_cfg, cache_cfg, weights: dict | None = None):
         self.model_cfg = model_cfg
         self.block_size = cache_cfg.block_size
-        # a bf16 K/V cache (cache_cfg.kv_dtype "bfloat16"): the fp32 cache
-        # arrays hold K/V rounded to bf16 when written
-        bf16 = getattr(cache_cfg, "kv_dtype", "float32") == "bfloat16"
-        self.model = TinyLlamaOracle(model_cfg, weights, round_bf16 if bf16 else None)
+        # a bf16 or FP8 E4M3 K/V cache (cache_cfg.kv_dtype "bfloat16",
+        # "float8_e4m3"): the fp32 cache arrays hold K/V rounded to it when written
+        kv_round = {"bfloat16": round_bf16, "float8_e4m3": round_fp8_e4m3}.get(
+            getattr(cache_cfg, "kv_dtype", "float32"))
+        self.model = TinyLlamaOracle(model_cfg, weights, kv_round)
         shape = (model_cfg.n_layers, cache_cfg.num_blocks * cache_cfg.block_size,
                  model_cfg.n_kv_heads, model_cfg.head_dim)
         self.cache_k = np.zeros(shape, dtype=np.float32)

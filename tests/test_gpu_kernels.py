@@ -149,7 +149,7 @@ def test_bad_arguments_raise():
 
 
 @pytest.mark.parametrize("layout", ["token", "head"])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float8_e4m3fn])
 def test_reshape_and_cache_bit_exact(dtype, layout):
     """The scatter equals oracle.write_kv bit for bit; a head-major cache
     holds the same rows (head_major of the oracle's token-major cache)."""
@@ -162,7 +162,7 @@ def test_reshape_and_cache_bit_exact(dtype, layout):
     v = qkv[:, (8 + Hkv) * D:].view(T, Hkv, D)
     slot = rng.permutation(slots)[:T].astype(np.int32)
     kc = torch.from_numpy(rng.standard_normal((slots, Hkv, D)).astype(np.float32)).to(dtype)
-    vc = kc.clone() * 2
+    vc = (kc.float() * 2).to(dtype)
     want_k, want_v = kc.clone().float().numpy(), vc.clone().float().numpy()
     write_kv(want_k, want_v, k.float().numpy(), v.float().numpy(), slot)
     dqkv = qkv.cuda()
@@ -177,7 +177,7 @@ def test_reshape_and_cache_bit_exact(dtype, layout):
     assert np.array_equal(to_np(dkc), want_k) and np.array_equal(to_np(dvc), want_v)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float8_e4m3fn])
 def test_copy_blocks_bit_exact(dtype):
     from oracle.runner import NumpyRunner
     from vllmlite_amd.config import CacheConfig, ModelConfig
@@ -350,6 +350,77 @@ def test_fp32_query_over_bf16_cache(seqs, ctx_hint, layout):
                       max_context_len=int(b["seq_lens"].max()) if ctx_hint else 0)
     want = oracle_attention(b, b["q"], bf16_round(b["k_cache"]), bf16_round(b["v_cache"]))
     check(to_np(out), want, "f32")
+
+
+@pytest.mark.parametrize("seqs", [[(1, c) for c in SHORT_CTX],
+                                  [(1, 40), (7, 300), (1, 2000), (16, 16), (3, 5000)]])
+@pytest.mark.parametrize("ctx_hint", [True, False])
+@pytest.mark.parametrize("layout", ["token", "head"])
+def test_fp32_query_over_fp8_cache(seqs, ctx_hint, layout):
+    """VL_DTYPE_F32_FP8KV: fp32 query and output over FP8 E4M3 caches (the
+    short-decode kernel when the bounds allow, else the generic kernel and
+    the combine) against the oracle on the FP8 values of K/V, at the fp32
+    tolerance; poisoned slots hold the FP8 NaN code."""
+    from oracle.attention import fp8_e4m3_decode, fp8_e4m3_encode
+    o = ops()
+    b = make_batch(seqs, 8, 4, 48, 16, seed=7 + len(seqs) + ctx_hint)
+    kq, vq = fp8_e4m3_decode(fp8_e4m3_encode(b["k_cache"])), fp8_e4m3_decode(fp8_e4m3_encode(b["v_cache"]))
+    fb = dict(b, k_cache=kq, v_cache=vq)
+
+    def fp8_dev(x):
+        return dev(fp8_e4m3_encode(x)).view(torch.float8_e4m3fn)
+
+    if layout == "head":
+        kc, vc = fp8_dev(head_major(b["k_cache"], 16)), fp8_dev(head_major(b["v_cache"], 16))
+    else:
+        kc, vc = fp8_dev(b["k_cache"]), fp8_dev(b["v_cache"])
+    q = dev(b["q"])
+    S, T = len(seqs), b["q"].shape[0]
+    ws = o.AttentionWorkspace().get(o.paged_attention_workspace_size(S, T, 8, 48,
+                                                                     int(b["seq_lens"].max())))
+    out = torch.full_like(q, float("nan"))
+    q_lens = np.diff(b["qsl"])
+    o.paged_attention(out, q, kc, vc, dev(b["block_tables"]), dev(b["seq_lens"]), dev(b["qsl"]),
+                      b["scale"], 16, ws, max_query_len=int(q_lens.max()),
+                      max_context_len=int(b["seq_lens"].max()) if ctx_hint else 0)
+    check(to_np(out), oracle_attention(fb), "f32")
+
+
+@pytest.mark.parametrize("layout", ["token", "head"])
+def test_fp8_cache_writer_rounds_like_the_oracle(layout):
+    """The RoPE + K/V writer into FP8 E4M3 caches stores the oracle's byte for
+    every value: rotated k (the fp32 rotation is bit-exact with NumPy's), and
+    v rows holding ties between neighbouring FP8 values, values around 448,
+    infinities, tiny and subnormal values."""
+    from oracle.attention import apply_rope, build_rope, fp8_e4m3_decode, fp8_e4m3_encode
+    o = ops()
+    rng = np.random.default_rng(9)
+    T, H, Hkv, D = 32, 8, 4, 48
+    qkv = (rng.standard_normal((T, (H + 2 * Hkv) * D)) * 3).astype(np.float32)
+    pos8 = fp8_e4m3_decode(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)
+    special = np.concatenate([((pos8[:-1] + pos8[1:]) / 2).astype(np.float32),  # every tie
+                              np.array([448, 449, 463.9, 464, 464.1, 1e9, np.inf, 2.0 ** -10,
+                                        3 * 2.0 ** -11, 1e-30, 0.0], np.float32)])
+    special = np.concatenate([special, -special])
+    vpart = qkv[:, (H + Hkv) * D:].reshape(-1)
+    vpart[:special.size] = special
+    qkv[:, (H + Hkv) * D:] = vpart.reshape(T, Hkv * D)
+    pos = rng.integers(0, 512, size=T).astype(np.int32)
+    slots = rng.permutation(320)[:T].astype(np.int32)
+    cos, sin = build_rope(D, 512)
+    shape = (20, Hkv, 16, D) if layout == "head" else (320, Hkv, D)
+    kc = torch.zeros(shape, device="cuda", dtype=torch.float8_e4m3fn)
+    vc = torch.zeros(shape, device="cuda", dtype=torch.float8_e4m3fn)
+    qo = torch.empty(T, H, D, device="cuda")
+    o.rope_and_cache(dev(qkv), qo, kc, vc, dev(pos), dev(slots), dev(cos), dev(sin), H, Hkv, D)
+    torch.cuda.synchronize()
+    kb, vb = (x.view(torch.uint8).cpu().numpy() for x in (kc, vc))
+    if layout == "head":
+        kb, vb = token_major(kb), token_major(vb)
+    k = apply_rope(qkv[:, H * D:(H + Hkv) * D].reshape(T, Hkv, D), pos, cos, sin)
+    v = qkv[:, (H + Hkv) * D:].reshape(T, Hkv, D)
+    assert np.array_equal(kb[slots], fp8_e4m3_encode(k))
+    assert np.array_equal(vb[slots], fp8_e4m3_encode(v))
 
 
 def test_short_decode_reads_no_plan():

@@ -148,12 +148,15 @@ def test_qkv_rope_cache_equals_projection_then_rope(rows, shape, layout):
         np.testing.assert_array_equal(vh[slots[ok]], qkvn[ok, (H + Hkv) * D:].reshape(-1, Hkv, D))
 
 
+@pytest.mark.parametrize("cdt", ["bf16", "fp8"])
 @pytest.mark.parametrize("rows", [1, 16])
-def test_qkv_rope_cache_bf16_cache_is_the_rounded_fp32_cache(rows):
-    """With bf16 caches both K/V writers (vl_qkv_rope_cache and
-    vl_rope_and_cache) store exactly the fp32 values rounded to nearest even,
-    and q (fp32) is unchanged."""
-    from oracle.attention import round_bf16
+def test_qkv_rope_cache_narrow_cache_is_the_rounded_fp32_cache(rows, cdt):
+    """With bf16 or FP8 E4M3 caches both K/V writers (vl_qkv_rope_cache and
+    vl_rope_and_cache) store exactly the fp32 values rounded to nearest even
+    (FP8 saturating), and q (fp32) is unchanged."""
+    from oracle.attention import round_bf16, round_fp8_e4m3
+    narrow = torch.bfloat16 if cdt == "bf16" else torch.float8_e4m3fn
+    rnd = round_bf16 if cdt == "bf16" else round_fp8_e4m3
     o = _ops()
     H, Hkv, D, k = 8, 4, 48, 384
     n = (H + 2 * Hkv) * D
@@ -167,7 +170,7 @@ def test_qkv_rope_cache_bf16_cache_is_the_rounded_fp32_cache(rows):
     ang = rng.standard_normal((64, D // 2)).astype(np.float32)
     cos, sin = dev(np.cos(ang)), dev(np.sin(ang))
     kf, vf = (torch.zeros((40, Hkv, D), device="cuda") for _ in range(2))
-    kb, vb, kb2, vb2 = (torch.zeros((40, Hkv, D), device="cuda", dtype=torch.bfloat16)
+    kb, vb, kb2, vb2 = (torch.zeros((40, Hkv, D), device="cuda", dtype=narrow)
                         for _ in range(4))
     qf, qb, qb2 = (torch.empty((rows, H * D), device="cuda") for _ in range(3))
     o.qkv_rope_cache(qf, kf, vf, x, w, g, pos, slot, cos, sin, H, Hkv, D)
@@ -178,7 +181,7 @@ def test_qkv_rope_cache_bf16_cache_is_the_rounded_fp32_cache(rows):
     torch.cuda.synchronize()
     assert torch.equal(qf, qb) and torch.equal(qf, qb2)
     for f32, b16, b16b in ((kf, kb, kb2), (vf, vb, vb2)):
-        want = round_bf16(f32.cpu().numpy())
+        want = rnd(f32.cpu().numpy())
         assert np.array_equal(b16.float().cpu().numpy(), want)
         assert np.array_equal(b16b.float().cpu().numpy(), want)
 

@@ -144,7 +144,8 @@ inline bool fast_shape(int dtype, int H, int Hkv, int D, int bs) {
 // head_dims with an MFMA tile instantiation
 inline bool tile_shape(int dtype, int D, int bs) {
   if (bs <= 0 || (bs & (bs - 1)) != 0) return false;  // block math is shifts and masks
-  if (dtype == VL_DTYPE_F32_BF16KV) return false;      // the generic kernel takes it
+  if (dtype == VL_DTYPE_F32_BF16KV || dtype == VL_DTYPE_F32_FP8KV)
+    return false;  // narrow caches under an fp32 query: the generic kernel takes them
   if (dtype == VL_DTYPE_BF16) return D == 64 || D == 128;
   return D == 16 || D == 32 || D == 48 || D == 64 || D == 128;
 }
@@ -1743,33 +1744,18 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// A head row of D elements of T as floats (16-byte loads).
-template <typename T, int D>
-__device__ __forceinline__ void load_row(const T* p, float (&r)[D]) {
-  constexpr int VE = 16 / (int)sizeof(T);
-#pragma unroll
-  for (int c = 0; c < D / VE; ++c) {
-    const uint4 v = reinterpret_cast<const uint4*>(p)[c];
-    if constexpr (sizeof(T) == 4) {
-      r[4 * c] = __uint_as_float(v.x), r[4 * c + 1] = __uint_as_float(v.y);
-      r[4 * c + 2] = __uint_as_float(v.z), r[4 * c + 3] = __uint_as_float(v.w);
-    } else {
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        r[8 * c + 2 * e] = __uint_as_float(w[e] << 16);
-        r[8 * c + 2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
-      }
-    }
-  }
-}
-
-// 16 bytes of T as floats
+// 16 bytes of T (fp32, bf16 bits or FP8 E4M3 bytes) as floats
 template <typename T>
 __device__ __forceinline__ void widen16(const uint4& v, float* r) {
   if constexpr (sizeof(T) == 4) {
     r[0] = __uint_as_float(v.x), r[1] = __uint_as_float(v.y);
     r[2] = __uint_as_float(v.z), r[3] = __uint_as_float(v.w);
+  } else if constexpr (sizeof(T) == 1) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) r[4 * e + b] = e4m3_to_f32((w[e] >> (8 * b)) & 0xffu);
   } else {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -1777,6 +1763,17 @@ __device__ __forceinline__ void widen16(const uint4& v, float* r) {
       r[2 * e] = __uint_as_float(w[e] << 16);
       r[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
     }
+  }
+}
+
+// A head row of D elements of T as floats (16-byte loads).
+template <typename T, int D>
+__device__ __forceinline__ void load_row(const T* p, float (&r)[D]) {
+  constexpr int VE = 16 / (int)sizeof(T);
+#pragma unroll
+  for (int c = 0; c < D / VE; ++c) {
+    const uint4 v = reinterpret_cast<const uint4*>(p)[c];
+    widen16<T>(v, r + VE * c);
   }
 }
 
@@ -2076,7 +2073,7 @@ struct Args {
 
 int check_args(const Args& a, const void* ws, size_t ws_bytes, bool need_kv) {
   VL_CHECK_ARG(a.dtype == VL_DTYPE_F32 || a.dtype == VL_DTYPE_BF16 ||
-                   a.dtype == VL_DTYPE_F32_BF16KV,
+                   a.dtype == VL_DTYPE_F32_BF16KV || a.dtype == VL_DTYPE_F32_FP8KV,
                "bad dtype %d", a.dtype);
   VL_CHECK_ARG(a.S >= 0 && a.T >= 0, "bad batch size");
   VL_CHECK_ARG(a.H > 0 && a.Hkv > 0 && a.H % a.Hkv == 0,
@@ -2319,6 +2316,8 @@ int dispatch_run(const Args& a, int max_q, int min_q, int max_ctx, void* ws, siz
     case VL_DTYPE_F32: return do_run<float, float>(a, max_q, min_q, max_ctx, ws, ws_bytes, st);
     case VL_DTYPE_BF16:
       return do_run<uint16_t, uint16_t>(a, max_q, min_q, max_ctx, ws, ws_bytes, st);
+    case VL_DTYPE_F32_FP8KV:
+      return do_run<float, uint8_t>(a, max_q, min_q, max_ctx, ws, ws_bytes, st);
     default: return do_run<float, uint16_t>(a, max_q, min_q, max_ctx, ws, ws_bytes, st);
   }
 }

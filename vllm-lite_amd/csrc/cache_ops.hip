@@ -58,7 +58,8 @@ __device__ __forceinline__ void rotate_pair(float e, float o, float c, float s, 
   *oo = es + oc;
 }
 
-// TC: cache elements (float, or uint16_t bf16 bits rounded to nearest even)
+// TC: cache elements (float; uint16_t bf16 bits or uint8_t FP8 E4M3 bytes,
+// rounded to nearest even)
 template <typename TC>
 __global__ void __launch_bounds__(256) rope_and_cache_kernel(
     const float* __restrict__ qkv, int64_t qkv_stride, float* __restrict__ q_out,
@@ -122,13 +123,13 @@ extern "C" int vl_reshape_and_cache(const void* key, const void* value, int64_t 
                                     const int32_t* slot_mapping, int64_t num_tokens,
                                     int num_kv_heads, int head_dim, int dtype, int kv_layout,
                                     int block_size, void* stream) {
-  VL_CHECK_ARG(dtype == VL_DTYPE_F32 || dtype == VL_DTYPE_BF16, "bad dtype %d", dtype);
+  const int es = vl_cache_elem_bytes(dtype);
+  VL_CHECK_ARG(es > 0, "bad dtype %d", dtype);
   VL_CHECK_ARG(num_tokens >= 0 && num_kv_heads > 0 && head_dim > 0, "bad shape");
   KvGeom g;
   if (int rc = vl_kv_geom(kv_layout, block_size, num_kv_heads, head_dim, &g)) return rc;
   if (num_tokens == 0) return VL_OK;
   VL_CHECK_ARG(key && value && key_cache && value_cache && slot_mapping, "null pointer");
-  const int es = dtype == VL_DTYPE_F32 ? 4 : 2;
   const int64_t row_b = (int64_t)num_kv_heads * head_dim * es;
   const int64_t ks_b = key_stride * es, vs_b = value_stride * es;
   VL_CHECK_ARG(key_stride >= num_kv_heads * (int64_t)head_dim &&
@@ -152,12 +153,15 @@ extern "C" int vl_reshape_and_cache(const void* key, const void* value, int64_t 
     scatter_rows_kernel<uint32_t><<<grid, 256, 0, st>>>(
         (const char*)key, (const char*)value, ks_b, vs_b, (char*)key_cache, (char*)value_cache,
         slot_mapping, num_tokens, g, es, (int)(seg_b / 4), nvec);
-  } else {
-    VL_CHECK_ARG(ok(2), "operands not 2-byte aligned");
+  } else if (ok(2)) {
     const int nvec = (int)(row_b / 2);
     scatter_rows_kernel<uint16_t><<<grid, 256, 0, st>>>(
         (const char*)key, (const char*)value, ks_b, vs_b, (char*)key_cache, (char*)value_cache,
         slot_mapping, num_tokens, g, es, (int)(seg_b / 2), nvec);
+  } else {
+    scatter_rows_kernel<uint8_t><<<grid, 256, 0, st>>>(
+        (const char*)key, (const char*)value, ks_b, vs_b, (char*)key_cache, (char*)value_cache,
+        slot_mapping, num_tokens, g, es, (int)seg_b, (int)row_b);
   }
   VL_CHECK_LAUNCH();
   return VL_OK;
@@ -166,13 +170,13 @@ extern "C" int vl_reshape_and_cache(const void* key, const void* value, int64_t 
 extern "C" int vl_copy_blocks(void* key_cache, void* value_cache, const int32_t* block_pairs,
                               int num_pairs, int num_layers, int64_t layer_stride,
                               int64_t block_elems, int dtype, void* stream) {
-  VL_CHECK_ARG(dtype == VL_DTYPE_F32 || dtype == VL_DTYPE_BF16, "bad dtype %d", dtype);
+  const int es = vl_cache_elem_bytes(dtype);
+  VL_CHECK_ARG(es > 0, "bad dtype %d", dtype);
   VL_CHECK_ARG(num_pairs >= 0 && num_layers > 0 && block_elems > 0 && layer_stride >= 0,
                "bad shape");
   VL_CHECK_ARG(num_layers <= 65535, "too many layers");
   if (num_pairs == 0) return VL_OK;
   VL_CHECK_ARG(key_cache && value_cache && block_pairs, "null pointer");
-  const int es = dtype == VL_DTYPE_F32 ? 4 : 2;
   const int64_t blk_b = block_elems * es, ls_b = layer_stride * es;
   hipStream_t st = (hipStream_t)stream;
   dim3 grid(num_pairs, num_layers, 2);
@@ -182,9 +186,12 @@ extern "C" int vl_copy_blocks(void* key_cache, void* value_cache, const int32_t*
   } else if (blk_b % 4 == 0 && ls_b % 4 == 0 && aligned(key_cache, 4) && aligned(value_cache, 4)) {
     copy_blocks_kernel<uint32_t><<<grid, 256, 0, st>>>((char*)key_cache, (char*)value_cache,
                                                        block_pairs, ls_b, (int)(blk_b / 4));
-  } else {
+  } else if (blk_b % 2 == 0 && ls_b % 2 == 0 && aligned(key_cache, 2) && aligned(value_cache, 2)) {
     copy_blocks_kernel<uint16_t><<<grid, 256, 0, st>>>((char*)key_cache, (char*)value_cache,
                                                        block_pairs, ls_b, (int)(blk_b / 2));
+  } else {
+    copy_blocks_kernel<uint8_t><<<grid, 256, 0, st>>>((char*)key_cache, (char*)value_cache,
+                                                      block_pairs, ls_b, (int)blk_b);
   }
   VL_CHECK_LAUNCH();
   return VL_OK;
@@ -196,8 +203,7 @@ extern "C" int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_
                                  const float* sin_table, int64_t num_tokens, int num_heads,
                                  int num_kv_heads, int head_dim, int cache_dtype, int kv_layout,
                                  int block_size, void* stream) {
-  VL_CHECK_ARG(cache_dtype == VL_DTYPE_F32 || cache_dtype == VL_DTYPE_BF16, "bad cache dtype %d",
-               cache_dtype);
+  VL_CHECK_ARG(vl_cache_elem_bytes(cache_dtype) > 0, "bad cache dtype %d", cache_dtype);
   VL_CHECK_ARG(num_tokens >= 0 && num_heads > 0 && num_kv_heads > 0 && head_dim > 0 &&
                    head_dim % 2 == 0,
                "bad shape");
@@ -214,9 +220,13 @@ extern "C" int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_
     rope_and_cache_kernel<float><<<grid, 128, 0, (hipStream_t)stream>>>(
         qkv, qkv_stride, q_out, (float*)key_cache, (float*)value_cache, positions, slot_mapping,
         cos_table, sin_table, num_tokens, num_heads, num_kv_heads, head_dim, g);
-  else
+  else if (cache_dtype == VL_DTYPE_BF16)
     rope_and_cache_kernel<uint16_t><<<grid, 128, 0, (hipStream_t)stream>>>(
         qkv, qkv_stride, q_out, (uint16_t*)key_cache, (uint16_t*)value_cache, positions,
+        slot_mapping, cos_table, sin_table, num_tokens, num_heads, num_kv_heads, head_dim, g);
+  else
+    rope_and_cache_kernel<uint8_t><<<grid, 128, 0, (hipStream_t)stream>>>(
+        qkv, qkv_stride, q_out, (uint8_t*)key_cache, (uint8_t*)value_cache, positions,
         slot_mapping, cos_table, sin_table, num_tokens, num_heads, num_kv_heads, head_dim, g);
   VL_CHECK_LAUNCH();
   return VL_OK;

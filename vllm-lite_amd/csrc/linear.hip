@@ -57,7 +57,7 @@ __device__ __forceinline__ void rotate_pair_f32(float e, float o, float c, float
 // Where MODE 3 puts the columns [q | k | v] of a fused QKV projection.
 struct RopeCache {
   float* q_out;  // [rows, nh * hd]
-  void* kc;      // paged cache (layout geom), float or (kv_bf16) bf16 bits
+  void* kc;      // paged cache (layout geom) of kv_dtype elements
   void* vc;
   KvGeom geom;
   const int32_t* positions;
@@ -65,12 +65,14 @@ struct RopeCache {
   const float* cos_t;  // [max_pos, hd / 2]
   const float* sin_t;
   int nh, nkv, hd;
-  int kv_bf16;   // caches hold bf16, each value rounded to nearest even
+  int kv_dtype;  // VL_DTYPE_F32, or VL_DTYPE_BF16 / VL_DTYPE_FP8_E4M3 (rounded to nearest even)
 };
 
-__device__ __forceinline__ void store_cache(void* cache, int64_t i, float v, int bf16) {
-  if (bf16)
+__device__ __forceinline__ void store_cache(void* cache, int64_t i, float v, int dtype) {
+  if (dtype == VL_DTYPE_BF16)
     static_cast<uint16_t*>(cache)[i] = f32_to_bf16(v);
+  else if (dtype == VL_DTYPE_FP8_E4M3)
+    static_cast<uint8_t*>(cache)[i] = f32_to_e4m3(v);
   else
     static_cast<float*>(cache)[i] = v;
 }
@@ -291,10 +293,10 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
       if (col < qd)
         rc.q_out[(int64_t)r * qd + col] = val;
       else if (slot >= 0)
-        store_cache(rc.kc, rc.geom.at(slot, base / rc.hd) + base % rc.hd, val, rc.kv_bf16);
+        store_cache(rc.kc, rc.geom.at(slot, base / rc.hd) + base % rc.hd, val, rc.kv_dtype);
     } else if (slot >= 0) {
       const int vcol = col - qd - kd;
-      store_cache(rc.vc, rc.geom.at(slot, vcol / rc.hd) + vcol % rc.hd, v[0], rc.kv_bf16);
+      store_cache(rc.vc, rc.geom.at(slot, vcol / rc.hd) + vcol % rc.hd, v[0], rc.kv_dtype);
     }
   }
 }
@@ -367,8 +369,7 @@ extern "C" int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cach
                                  const float* cos_table, const float* sin_table, int rows, int k,
                                  int num_heads, int num_kv_heads, int head_dim, int cache_dtype,
                                  int kv_layout, int block_size, void* stream) {
-  VL_CHECK_ARG(cache_dtype == VL_DTYPE_F32 || cache_dtype == VL_DTYPE_BF16, "bad cache dtype %d",
-               cache_dtype);
+  VL_CHECK_ARG(vl_cache_elem_bytes(cache_dtype) > 0, "bad cache dtype %d", cache_dtype);
   KvGeom geom;
   if (num_kv_heads > 0 && head_dim > 0)
     if (int rc = vl_kv_geom(kv_layout, block_size, num_kv_heads, head_dim, &geom)) return rc;
@@ -392,7 +393,7 @@ extern "C" int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cach
   rc.q_out = q_out, rc.kc = key_cache, rc.vc = value_cache, rc.positions = positions;
   rc.slots = slot_mapping, rc.cos_t = cos_table, rc.sin_t = sin_table;
   rc.nh = num_heads, rc.nkv = num_kv_heads, rc.hd = head_dim;
-  rc.kv_bf16 = cache_dtype == VL_DTYPE_BF16;
+  rc.kv_dtype = cache_dtype;
   rc.geom = geom;
   hipStream_t st = (hipStream_t)stream;
   const bool nrm = norm_weight != nullptr;

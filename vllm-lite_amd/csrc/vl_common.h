@@ -70,6 +70,50 @@ struct Elem<uint16_t> {
   }
 };
 
+// OCP FP8 E4M3 ("e4m3fn": 4 exponent bits with bias 7, 3 mantissa bits, no
+// infinities, 0x7F / 0xFF NaN, largest finite 448), carried as raw bytes.
+// Stores round to nearest even and saturate: finite values (and infinities)
+// beyond 448 in magnitude become +-448; NaN stays NaN.
+__host__ __device__ __forceinline__ uint8_t f32_to_e4m3(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint8_t)(sign | 0x7fu);  // NaN
+  if (a >= 0x43e00000u) return (uint8_t)(sign | 0x7eu);  // |f| >= 448
+  if (a < 0x3c800000u) {  // below 2^-6: multiples of 2^-9 (8 is 2^-6, the first normal)
+    const float m = __builtin_rintf(__builtin_bit_cast(float, a) * 512.f);
+    return (uint8_t)(sign | (uint32_t)m);
+  }
+  // normal: round the fp32 mantissa to 3 bits (a carry moves the exponent),
+  // then rebias the exponent from 127 to 7
+  const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+  return (uint8_t)(sign | ((r >> 20) - (120u << 3)));
+}
+
+// Exact FP8 E4M3 -> fp32.
+__host__ __device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
+  const uint32_t em = b & 0x7fu;
+  float v = em >= 8u ? __builtin_bit_cast(float, (((em >> 3) + 120u) << 23) | ((em & 7u) << 20))
+                     : (float)em * 0.001953125f;  // subnormal: em * 2^-9
+  if (em == 0x7fu) v = __builtin_nanf("");
+  return (b & 0x80u) ? -v : v;
+}
+
+template <>
+struct Elem<uint8_t> {
+  static __device__ __forceinline__ float load(const uint8_t* p, int64_t i) {
+    return e4m3_to_f32(p[i]);
+  }
+  static __device__ __forceinline__ void store(uint8_t* p, int64_t i, float v) {
+    p[i] = f32_to_e4m3(v);
+  }
+};
+
+// Element bytes of a VL_DTYPE_* cache dtype (0 if not a cache dtype).
+inline int vl_cache_elem_bytes(int dtype) {
+  return dtype == VL_DTYPE_F32 ? 4 : dtype == VL_DTYPE_BF16 ? 2 : dtype == VL_DTYPE_FP8_E4M3 ? 1 : 0;
+}
+
 // ------------------------------------------------------- wave reductions ----
 // 64-lane wavefront reductions through ds_swizzle-free shuffles.
 __device__ __forceinline__ float wave_max(float v) {

@@ -43,9 +43,10 @@ class CacheConfig:
     block_size: int = 16
     num_blocks: int = 1024
     enable_prefix_caching: bool = True
-    # element type of the K/V cache: "float32" (the reference's), or
-    # "bfloat16" (half the cache bytes; K/V rounded to nearest even when
-    # written, everything else stays fp32)
+    # element type of the K/V cache: "float32" (the reference's), "bfloat16"
+    # (half the cache bytes) or "float8_e4m3" (OCP FP8 E4M3, a quarter; values
+    # beyond +-448 saturate); K/V rounded to nearest even when written,
+    # everything else stays fp32
     kv_dtype: str = "float32"
     # order of the rows inside a cache block: "token" ([slots, Hkv, D], the
     # reference's), or "head" ([blocks, Hkv, block_size, D]: each KV head's
@@ -53,8 +54,8 @@ class CacheConfig:
     kv_layout: str = "token"
 
     def __post_init__(self):
-        if self.kv_dtype not in ("float32", "bfloat16"):
-            raise ValueError("kv_dtype must be float32 or bfloat16")
+        if self.kv_dtype not in ("float32", "bfloat16", "float8_e4m3"):
+            raise ValueError("kv_dtype must be float32, bfloat16 or float8_e4m3")
         if self.kv_layout not in ("token", "head"):
             raise ValueError("kv_layout must be token or head")
         if self.kv_layout == "head" and self.block_size & (self.block_size - 1):

@@ -179,8 +179,8 @@ class HipRunner(ModelRunner):
                          mc.head_dim)
             else:
                 shape = (mc.n_layers, slots, mc.n_kv_heads, mc.head_dim)
-            kv = torch.bfloat16 if getattr(cache_cfg, "kv_dtype", "float32") == "bfloat16" \
-                else torch.float32
+            kv = {"bfloat16": torch.bfloat16, "float8_e4m3": torch.float8_e4m3fn}.get(
+                getattr(cache_cfg, "kv_dtype", "float32"), torch.float32)
             self.cache_k = torch.zeros(shape, dtype=kv, device=self.device)
             self.cache_v = torch.zeros(shape, dtype=kv, device=self.device)
         self.W = max(1, -(-mc.max_seq_len // self.block_size))

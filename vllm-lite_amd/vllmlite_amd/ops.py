@@ -17,7 +17,9 @@ import torch
 
 from .build import LIB_PATH
 
-F32, BF16, F32_BF16KV = 0, 1, 2  # VL_DTYPE_*: F32_BF16KV = fp32 query / out over bf16 caches
+# VL_DTYPE_*: F32_BF16KV / F32_FP8KV = fp32 query and out over bf16 / FP8 E4M3
+# caches; FP8_E4M3 = OCP FP8 E4M3 cache elements (torch.float8_e4m3fn)
+F32, BF16, F32_BF16KV, FP8_E4M3, F32_FP8KV = 0, 1, 2, 3, 4
 # VL_KV_*: a per-layer cache tensor [slots, Hkv, D] is token-major (the
 # reference's layout), [blocks, Hkv, block_size, D] head-major
 KV_TOKEN_MAJOR, KV_HEAD_MAJOR = 0, 1
@@ -109,20 +111,25 @@ def _dtype_code(t: torch.Tensor) -> int:
         return F32
     if t.dtype == torch.bfloat16:
         return BF16
+    if t.dtype == torch.float8_e4m3fn:
+        return FP8_E4M3
     raise TypeError(f"unsupported dtype {t.dtype}")
 
 
 def _attn_dtype(query: torch.Tensor, cache: torch.Tensor) -> int:
-    """VL_DTYPE_* of an attention call: the query's, or F32_BF16KV for an
-    fp32 query over bf16 caches."""
+    """VL_DTYPE_* of an attention call: the query's, or F32_BF16KV /
+    F32_FP8KV for an fp32 query over bf16 / FP8 E4M3 caches."""
     if query.dtype == torch.float32 and cache.dtype == torch.bfloat16:
         return F32_BF16KV
+    if query.dtype == torch.float32 and cache.dtype == torch.float8_e4m3fn:
+        return F32_FP8KV
     return _dtype_code(query)
 
 
 def _cache_dtype(key_cache: torch.Tensor, value_cache: torch.Tensor) -> int:
-    _need(key_cache.dtype == value_cache.dtype and key_cache.dtype in (torch.float32, torch.bfloat16),
-          "caches must both be fp32 or both bf16")
+    _need(key_cache.dtype == value_cache.dtype and
+          key_cache.dtype in (torch.float32, torch.bfloat16, torch.float8_e4m3fn),
+          "caches must both be fp32, both bf16 or both float8_e4m3fn")
     return _dtype_code(key_cache)
 
 
@@ -220,8 +227,10 @@ def _attn_check(out, query, key_cache, value_cache, block_tables, seq_lens, quer
     _need(key_cache.is_contiguous() and value_cache.is_contiguous(), "caches must be contiguous")
     _need(key_cache.dtype == value_cache.dtype and
           (key_cache.dtype == query.dtype or
-           (query.dtype == torch.float32 and key_cache.dtype == torch.bfloat16)),
-          "dtype mismatch (caches of the query dtype, or bf16 under an fp32 query)")
+           (query.dtype == torch.float32 and
+            key_cache.dtype in (torch.bfloat16, torch.float8_e4m3fn))),
+          "dtype mismatch (caches of the query dtype, or bf16 / float8_e4m3fn under an "
+          "fp32 query)")
     hkv = key_cache.shape[1]
     _need(H % hkv == 0, "num_heads must be a multiple of num_kv_heads")
     for t, n in ((block_tables, "block_tables"), (seq_lens, "seq_lens"),
