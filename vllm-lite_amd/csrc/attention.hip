@@ -800,19 +800,26 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
       return (int64_t)((uint64_t)blk * blk_elems) +
              (int64_t)((key & bs_mask) * (uint32_t)slot_stride) + kv_off;
     };
+    // 16-row bf16 items of head_dim 128 (short queries: spec-verify, HBM-bound)
+    // keep two tiles' loads in flight; the others one
+    constexpr bool kDeep = kBf16 && RW == 16 && D == 128;
     uint4 pk[Lds::kUnits], pv[Lds::kUnits];
+    uint4 pk2[kDeep ? Lds::kUnits : 1], pv2[kDeep ? Lds::kUnits : 1];
     // bf16 staging: K unit r of a tile is keys k0 + kUnitKeys r + threadIdx / kChunks,
     // chunk threadIdx % kChunks; with blocks of >= kUnitKeys slots the unit lies
     // in one block whose id is uniform over the workgroup (tile starts are
-    // multiples of 64); in a head-major cache the unit is one contiguous span. Keys past the workgroup's end are masked: K reads stay
-    // in the last key's block (finite or not, the score is replaced by -inf);
-    // V reads re-read the last key, finite values whose weights are zero.
+    // multiples of 64); in a head-major cache the unit is one contiguous span.
+    // Keys past the workgroup's end are masked: K reads stay in the last
+    // key's block (finite or not, the score is replaced by -inf); V reads
+    // re-read the last key, finite values whose weights are zero.
     constexpr int kUnitKeys = 256 / Lds::kChunks;
     const bool unit_blocks = (1 << bs_log2) >= kUnitKeys;
     const uint32_t k_thr_off =
         (uint32_t)(tid / Lds::kChunks) * (uint32_t)slot_stride + (tid % Lds::kChunks) * 8;
-    // nt: std::true_type / std::false_type, non-temporal loads or not
-    auto prefetch_as = [&](int k0, auto nt) {
+    // nt: std::true_type / std::false_type, non-temporal loads or not;
+    // (pk, pv): the registers the tile lands in
+    using Regs = uint4[Lds::kUnits];
+    auto prefetch_as = [&](int k0, auto nt, Regs& pk, Regs& pv) {
       constexpr bool kNt = decltype(nt)::value;
       if constexpr (kBf16) {
         if (unit_blocks) {
@@ -858,13 +865,14 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
         }
       }
     };
-    auto prefetch = [&](int k0) {  // one uniform branch per tile, around branch-free loads
+    // one uniform branch per tile, around branch-free loads
+    auto prefetch = [&](int k0, Regs& dk, Regs& dv) {
       if (stream_kv)
-        prefetch_as(k0, std::true_type{});
+        prefetch_as(k0, std::true_type{}, dk, dv);
       else
-        prefetch_as(k0, std::false_type{});
+        prefetch_as(k0, std::false_type{}, dk, dv);
     };
-    auto stage = [&](Lds& b) {  // prefetch registers -> LDS b
+    auto stage = [&](Lds& b, const Regs& pk, const Regs& pv) {  // registers -> LDS b
       if constexpr (kBf16) {
 #pragma unroll
         for (int r = 0; r < Lds::kUnits; ++r) {
@@ -1076,14 +1084,29 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
           }
       }
     };
-    if (ntile > 0) prefetch(kbeg);
-    for (int ti = 0; ti < ntile; ++ti) {
+    // one tile: stage it from registers (pk, pv), refill them with the tile
+    // `ahead` tiles later, compute
+    auto tile_step = [&](int ti, int ahead, Regs& pk, Regs& pv) {
       const int k0 = kbeg + ti * kTileKeys;
       __syncthreads();  // the previous tile (or item) is done with the LDS buffer
-      stage(lds);
+      stage(lds, pk, pv);
       __syncthreads();
-      if (ti + 1 < ntile) prefetch(k0 + kTileKeys);  // in flight during the compute below
+      if (ti + ahead < ntile) prefetch(k0 + ahead * kTileKeys, pk, pv);  // in flight meanwhile
       if (k0 < kend_wave) compute(lds, k0);  // else every row of the wave is past its end
+    };
+    if constexpr (kDeep) {
+      // two tiles in flight (two register sets, the loop unrolled by two so
+      // each set stays in fixed registers): twice the bytes in flight for the
+      // HBM-bound short-query items, within the 2-waves-per-SIMD budget
+      if (ntile > 0) prefetch(kbeg, pk, pv);
+      if (ntile > 1) prefetch(kbeg + kTileKeys, pk2, pv2);
+      for (int ti = 0; ti < ntile; ti += 2) {
+        tile_step(ti, 2, pk, pv);
+        if (ti + 1 < ntile) tile_step(ti + 1, 2, pk2, pv2);
+      }
+    } else {
+      if (ntile > 0) prefetch(kbeg, pk, pv);
+      for (int ti = 0; ti < ntile; ++ti) tile_step(ti, 1, pk, pv);
     }
     // ---- row sums over the lane groups, then write
     float l_row = l_part;
