@@ -801,10 +801,11 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
              (int64_t)((key & bs_mask) * (uint32_t)slot_stride) + kv_off;
     };
     // 16-row bf16 items of head_dim 128 (short queries: spec-verify, HBM-bound)
-    // keep two tiles' loads in flight; the others one
+    // keep three tiles' loads in flight; the others one
     constexpr bool kDeep = kBf16 && RW == 16 && D == 128;
     uint4 pk[Lds::kUnits], pv[Lds::kUnits];
     uint4 pk2[kDeep ? Lds::kUnits : 1], pv2[kDeep ? Lds::kUnits : 1];
+    uint4 pk3[kDeep ? Lds::kUnits : 1], pv3[kDeep ? Lds::kUnits : 1];
     // bf16 staging: K unit r of a tile is keys k0 + kUnitKeys r + threadIdx / kChunks,
     // chunk threadIdx % kChunks; with blocks of >= kUnitKeys slots the unit lies
     // in one block whose id is uniform over the workgroup (tile starts are
@@ -1095,14 +1096,18 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
       if (k0 < kend_wave) compute(lds, k0);  // else every row of the wave is past its end
     };
     if constexpr (kDeep) {
-      // two tiles in flight (two register sets, the loop unrolled by two so
-      // each set stays in fixed registers): twice the bytes in flight for the
-      // HBM-bound short-query items, within the 2-waves-per-SIMD budget
+      // three tiles in flight (three register sets, the loop unrolled by
+      // three so each set stays in fixed registers): three times the bytes in
+      // flight for the HBM-bound short-query items, within the 2-waves-per-
+      // SIMD register budget (242 VGPRs). Verify step: one tile in flight
+      // 857-875 us, two 831-847, three 783-860 (two boxes)
       if (ntile > 0) prefetch(kbeg, pk, pv);
       if (ntile > 1) prefetch(kbeg + kTileKeys, pk2, pv2);
-      for (int ti = 0; ti < ntile; ti += 2) {
-        tile_step(ti, 2, pk, pv);
-        if (ti + 1 < ntile) tile_step(ti + 1, 2, pk2, pv2);
+      if (ntile > 2) prefetch(kbeg + 2 * kTileKeys, pk3, pv3);
+      for (int ti = 0; ti < ntile; ti += 3) {
+        tile_step(ti, 3, pk, pv);
+        if (ti + 1 < ntile) tile_step(ti + 1, 3, pk2, pv2);
+        if (ti + 2 < ntile) tile_step(ti + 2, 3, pk3, pv3);
       }
     } else {
       if (ntile > 0) prefetch(kbeg, pk, pv);
