@@ -69,8 +69,19 @@ constexpr int kFChunk = 16;  // blocks per softmax chunk (256 tokens)
 #ifndef VL_BV
 #define VL_BV 2
 #endif
-constexpr int kBK = VL_BK;  // blocks per K load burst
-constexpr int kBV = VL_BV;  // blocks per V load burst
+constexpr int kBK = VL_BK;  // blocks per K load burst (decode kernel)
+constexpr int kBV = VL_BV;  // blocks per V load burst (decode kernel)
+// The step kernel's decode items: a deeper V burst. A CU there typically
+// holds one decode and one tile workgroup, so a decode workgroup keeps more
+// bytes in flight on its own (the tile body sets the register budget
+// anyway). Mixed step: bursts (K 4, V 2) 569-573 us, (4, 4) 555-564, (8, 2)
+// 577-588, (8, 4) 573-576.
+#ifndef VL_STEP_BK
+#define VL_STEP_BK 4
+#endif
+#ifndef VL_STEP_BV
+#define VL_STEP_BV 4
+#endif
 
 // MFMA tile-kernel shape: 4 wavefronts x 16 (token, head) rows per workgroup,
 // 64 keys per LDS tile
@@ -1415,7 +1426,7 @@ __device__ __forceinline__ uint4 load_stream16(const char* p) {
 // across each 16-lane row by a transposing DPP sum. (Lanes reading 64 bytes
 // of each of 16 tokens per instruction, completed by a quad sum, measured
 // 229-233 us against 215-221 us for the 256-sequence batch.)
-template <bool kMixed>
+template <bool kMixed, int kBK, int kBV>
 __device__ __forceinline__ void decode_body(DecodeLds& s, int it, const DecodeItem& cur, int R,
                                             VL_ATTN_PARAMS(uint16_t)) {
   const int tid = item_tid<kMixed>();
@@ -1707,7 +1718,7 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
   while (it < n_items) {
     int nxt = 0;
     if (threadIdx.x == 0) nxt = (int)gridDim.x + atomicAdd(work, 1);
-    decode_body<false>(
+    decode_body<false, kBK, kBV>(
         s, it, decode_fetch(desc[it / Hkv], it, R, Hkv, wave, lane, query, q_stride, bt, bt_stride),
         R, VL_ATTN_ARGS);
     if (threadIdx.x == 0) next_lds = nxt;
@@ -1994,7 +2005,7 @@ attend_step_bf16_kernel(VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hd
       int nxt = 0;
       if (threadIdx.x == 0) nxt = atomicAdd(counters + qid, 1);  // the next item, claimed early
       if (!tiles)
-        decode_body<true>(dl, it,
+        decode_body<true, VL_STEP_BK, VL_STEP_BV>(dl, it,
                           decode_fetch(desc[it / Hkv], it, R, Hkv, threadIdx.x >> 6,
                                        threadIdx.x & 63, query, q_stride, bt, bt_stride),
                           R, VL_ATTN_ARGS);
