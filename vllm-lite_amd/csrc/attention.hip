@@ -87,6 +87,10 @@ constexpr int kBV = VL_BV;  // blocks per V load burst (decode kernel)
 // 64 keys per LDS tile
 constexpr int kTileRows = 64;
 constexpr int kTileKeys = 64;
+// rows of a 32-row-wavefront (bf16, > 16 queries) item: 8 wavefronts share
+// each staged K/V tile (the 4-wavefront step kernel takes an item in two
+// passes)
+constexpr int kWideRows = 256;
 #ifndef VL_PV_LOOK
 #define VL_PV_LOOK 2
 #endif
@@ -259,7 +263,7 @@ struct SeqWork {
 // shorter); everything else goes to the MFMA tile kernel when the shape has
 // one (one workgroup per 64-row block of (token, head-in-group) rows per KV
 // head and partition of P tokens; sequences with more than kSplitMaxQ
-// queries take 128-row blocks of 32-row wavefronts when `wide`), else to the
+// queries take kWideRows-row blocks of 32-row wavefronts when `wide`), else to the
 // generic kernel.
 __device__ __forceinline__ bool is_bw(int q, int c, bool fast) { return fast && q == 1 && c > 0; }
 
@@ -279,7 +283,7 @@ __device__ __forceinline__ SeqWork seq_work(int q, int c, int P, int R, int H, i
   }
   const bool wd = tl && wide && q > kSplitMaxQ;  // never split (np == 1)
   w.tile = tl && !wd ? (int64_t)w.np * Hkv * cdiv(q * (H / Hkv), kTileRows) : 0;
-  w.wide = wd ? (int64_t)Hkv * cdiv(q * (H / Hkv), 2 * kTileRows) : 0;
+  w.wide = wd ? (int64_t)Hkv * cdiv(q * (H / Hkv), kWideRows) : 0;
   w.gen = (bw || tl) ? 0 : (int64_t)max(q, 0) * H * w.np;
   // a split decode sequence also keeps one arrival counter per KV head in
   // the rows after its partials
@@ -721,8 +725,8 @@ __device__ __forceinline__ int item_tid() {
 // query chunks: each K/V tile read from LDS feeds twice the rows). With RW 32
 // a lane holds row l%32; its S^T values are keys 32t + 8(r/4) + 4(l/32) + r%4
 // (r < 16) and its O^T values dims 32u + 8(r/4) + 4(l/32) + r%4.
-template <typename T, int D, int RW, bool kMixed>
-__device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
+template <typename T, int D, int RW, bool kMixed, int kWv = 4>
+__device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int pass, int P,
                                           const int32_t* __restrict__ item_off,
                                           const int32_t* __restrict__ item_seq,
                                           VL_ATTN_PARAMS(T)) {
@@ -730,7 +734,16 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
   constexpr bool kBf16 = sizeof(T) == 2;
   constexpr bool kW = RW == 32;
   static_assert(RW == 16 || (RW == 32 && kBf16), "32-row wavefronts are bf16 only");
-  constexpr int kRows = 4 * RW;                          // rows per workgroup item
+  constexpr int kRows = kWv * RW;                         // rows per pass (kWv wavefronts)
+  // a 32-row item spans kWideRows rows: one pass of an 8-wavefront
+  // workgroup, or `pass` 0 or 1 of a 4-wavefront one (the step kernel
+  // hands out the two passes as separate items)
+  constexpr int kItemRows = kW ? kWideRows : kRows;
+  static_assert(kItemRows % kRows == 0, "rows per item");
+  // staging: the workgroup's threads as kWv / 4 groups of 256; group hg
+  // stages the 16-key units hg, hg + kWv / 4, ... (wave-uniform)
+  constexpr int kHalves = kWv / 4;
+  const int hg = __builtin_amdgcn_readfirstlane(tid >> 8), tl = tid & 255;
   constexpr int kDT = D / (kW ? 32 : 16);                // d tiles of the output
   constexpr int kKS = kW ? D / 16 : kBf16 ? D / 32 : D / 4;  // k-steps of the QK^T product
   constexpr int kST = kTileKeys / (kW ? 32 : 16);        // key subtiles per LDS tile
@@ -739,6 +752,8 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
   using AccT = float __attribute__((ext_vector_type(kCV)));
   static_assert(!kBf16 || Lds::kUnits * 256 == kTileKeys * Lds::kChunks,
                 "bf16 tile staging assumes head_dim 64 or 128");
+  static_assert(kHalves == 1 || (kBf16 && Lds::kUnits % kHalves == 0),
+                "8-wavefront items are bf16");
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int col = lane & (RW - 1);  // the lane's row within the wave's rows
@@ -760,14 +775,16 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
     const int part = local % np;
     const int kvh = (local / np) % Hkv;
     const int nrows = q_len * rep;
-    const bool stream_kv = nrows <= kRows;  // no other row block reads this K / V
-    const int rb = kW ? cdiv(nrows, kRows) - 1 - local / Hkv : (local / np) / Hkv;
+    const bool stream_kv = nrows <= kRows;  // no other pass or row block reads this K / V
+    const int rb = kW ? cdiv(nrows, kItemRows) - 1 - local / Hkv : (local / np) / Hkv;
+    const int rbase = rb * kItemRows + pass * kRows;  // the pass's first row
+    if (rbase >= nrows) return;
     const int kbeg = np > 1 ? part * P : 0;
     const int kend = np > 1 ? min(ctx, kbeg + P) : ctx;
     // keys the block's last row can see bound the tiles the workgroup loads
-    const int blk_last = min(nrows - 1, rb * kRows + kRows - 1);
+    const int blk_last = min(nrows - 1, rbase + kRows - 1);
     const int kend_wg = min(kend, ctx - q_len + blk_last / rep + 1);
-    const int row0 = rb * kRows + wave * RW;
+    const int row0 = rbase + wave * RW;
     const int wave_last = min(nrows - 1, row0 + RW - 1);
     const int kend_wave = row0 < nrows ? min(kend, ctx - q_len + wave_last / rep + 1) : kbeg;
     const int my_row = row0 + col;
@@ -814,7 +831,7 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
     // 16-row bf16 items of head_dim 128 (short queries: spec-verify, HBM-bound)
     // keep three tiles' loads in flight; the others one
     constexpr bool kDeep = kBf16 && RW == 16 && D == 128;
-    uint4 pk[Lds::kUnits], pv[Lds::kUnits];
+    uint4 pk[Lds::kUnits / kHalves], pv[Lds::kUnits / kHalves];
     uint4 pk2[kDeep ? Lds::kUnits : 1], pv2[kDeep ? Lds::kUnits : 1];
     uint4 pk3[kDeep ? Lds::kUnits : 1], pv3[kDeep ? Lds::kUnits : 1];
     // bf16 staging: K unit r of a tile is keys k0 + kUnitKeys r + threadIdx / kChunks,
@@ -827,10 +844,11 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
     constexpr int kUnitKeys = 256 / Lds::kChunks;
     const bool unit_blocks = (1 << bs_log2) >= kUnitKeys;
     const uint32_t k_thr_off =
-        (uint32_t)(tid / Lds::kChunks) * (uint32_t)slot_stride + (tid % Lds::kChunks) * 8;
+        (uint32_t)(tl / Lds::kChunks) * (uint32_t)slot_stride + (tl % Lds::kChunks) * 8;
     // nt: std::true_type / std::false_type, non-temporal loads or not;
     // (pk, pv): the registers the tile lands in
-    using Regs = uint4[Lds::kUnits];
+    constexpr int kU = Lds::kUnits / kHalves;  // units this thread stages
+    using Regs = uint4[kU];
     auto prefetch_as = [&](int k0, auto nt, Regs& pk, Regs& pv) {
       constexpr bool kNt = decltype(nt)::value;
       if constexpr (kBf16) {
@@ -840,14 +858,14 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
           // last key, which lies in the last unit's block, as does a unit
           // past the end (its K reads stay there too; their scores are masked)
           const int klast = (kend_wg - 1) & ~(kUnitKeys - 1);
-          uint32_t blk[Lds::kUnits];
+          uint32_t blk[kU];
 #pragma unroll
-          for (int r = 0; r < Lds::kUnits; ++r)
-            blk[r] = (uint32_t)table[min(k0 + kUnitKeys * r, klast) >> bs_log2];
-          const int tk = tid / Lds::kChunks, tc = (tid % Lds::kChunks) * 8;
+          for (int r = 0; r < kU; ++r)
+            blk[r] = (uint32_t)table[min(k0 + kUnitKeys * (kHalves * r + hg), klast) >> bs_log2];
+          const int tk = tl / Lds::kChunks, tc = (tl % Lds::kChunks) * 8;
 #pragma unroll
-          for (int r = 0; r < Lds::kUnits; ++r) {
-            const int kr = min(k0 + kUnitKeys * r, klast);
+          for (int r = 0; r < kU; ++r) {
+            const int kr = min(k0 + kUnitKeys * (kHalves * r + hg), klast);
             const int64_t boff = (int64_t)((uint64_t)blk[r] * blk_elems) + kv_off;
             pk[r] = load16_kv<kNt>(kc + boff + ((uint32_t)(kr & bs_mask) * (uint32_t)slot_stride +
                                                 k_thr_off));
@@ -856,8 +874,8 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
           }
         } else {
 #pragma unroll
-          for (int r = 0; r < Lds::kUnits; ++r) {
-            const int idx = tid + 256 * r;
+          for (int r = 0; r < kU; ++r) {
+            const int idx = tl + 256 * (kHalves * r + hg);
             const int kk = idx / Lds::kChunks, cc = idx - kk * Lds::kChunks;
             const int64_t off = row_of(min(k0 + kk, kend_wg - 1)) + cc * 8;
             pk[r] = load16_kv<kNt>(kc + off);
@@ -887,8 +905,8 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int P,
     auto stage = [&](Lds& b, const Regs& pk, const Regs& pv) {  // registers -> LDS b
       if constexpr (kBf16) {
 #pragma unroll
-        for (int r = 0; r < Lds::kUnits; ++r) {
-          const int idx = tid + 256 * r;
+        for (int r = 0; r < kU; ++r) {
+          const int idx = tl + 256 * (kHalves * r + hg);
           const int kk = idx / Lds::kChunks, c = idx - kk * Lds::kChunks;
           *reinterpret_cast<uint4*>(&b.k[kk * Lds::kRow + c * 8]) = pk[r];
           *reinterpret_cast<uint4*>(&b.v[kk * Lds::vRow + c * 8]) = pv[r];
@@ -1189,8 +1207,8 @@ constexpr int kXcds = 8;
 // which the sequence's other row blocks read again; the plan orders the
 // items longest first, so the launch ends on short ones. The counters are
 // zeroed by the plan and by the combine launch that follows every run.
-template <typename T, int D, int RW>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) attend_tile_kernel(
+template <typename T, int D, int RW, int kWv>
+__global__ void __launch_bounds__(64 * kWv) __attribute__((amdgpu_waves_per_eu(2))) attend_tile_kernel(
     VL_ATTN_PARAMS(T), const int32_t* __restrict__ hdr, const int32_t* __restrict__ item_off,
     const int32_t* __restrict__ item_seq, int32_t* counters) {
   __shared__ TileLds<T, D, RW> lds;
@@ -1204,7 +1222,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) a
   while (it < n_items) {
     int nxt = 0;
     if (threadIdx.x == 0) nxt = per_queue + atomicAdd(counters + xcd, 1);
-    tile_body<T, D, RW, false>(lds, it, P, item_off, item_seq, VL_ATTN_ARGS);
+    tile_body<T, D, RW, false, kWv>(lds, it, 0, P, item_off, item_seq, VL_ATTN_ARGS);
     __syncthreads();  // the item is done with the LDS; claim_lds has been read
     if (threadIdx.x == 0) claim_lds = nxt;
     __syncthreads();
@@ -1981,7 +1999,10 @@ attend_step_bf16_kernel(VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hd
   auto& dl = *reinterpret_cast<DecodeLds*>(smem);
   if (!always && !hdr[11]) return;  // not a mixed batch: the decode and tile kernels run it
   const int P = hdr[2];
-  const int n_wide = hdr[10], n_tiles = n_wide + hdr[4], n_dec = hdr[0];
+  // the kWideRows-row items as two items each (pass 0 of every item, then
+  // pass 1: with 8 KV heads n_wide is a multiple of 8, so both passes of an
+  // item fall in its KV head's queue), then the 16-row items
+  const int n_wide = hdr[10], n_tiles = 2 * n_wide + hdr[4], n_dec = hdr[0];
   const int R = hdr[7];
   const int xcd = blockIdx.x % kXcds;
   const bool tiles_first = (blockIdx.x / kXcds) % VL_STEP_TILE_FIRST == 0;
@@ -2009,10 +2030,12 @@ attend_step_bf16_kernel(VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hd
                           decode_fetch(desc[it / Hkv], it, R, Hkv, threadIdx.x >> 6,
                                        threadIdx.x & 63, query, q_stride, bt, bt_stride),
                           R, VL_ATTN_ARGS);
-      else if (it < n_wide)
-        tile_body<uint16_t, kFD, 32, true>(tl32, it, P, wide_off, wide_seq, VL_ATTN_ARGS);
+      else if (it < 2 * n_wide)
+        tile_body<uint16_t, kFD, 32, true>(tl32, it % n_wide, it / n_wide, P, wide_off, wide_seq,
+                                           VL_ATTN_ARGS);
       else
-        tile_body<uint16_t, kFD, 16, true>(tl16, it - n_wide, P, tile_off, nullptr, VL_ATTN_ARGS);
+        tile_body<uint16_t, kFD, 16, true>(tl16, it - 2 * n_wide, 0, P, tile_off, nullptr,
+                                           VL_ATTN_ARGS);
       __syncthreads();  // the item is done with the LDS; claim_lds has been read
       if (threadIdx.x == 0) claim_lds = nxt;
       __syncthreads();
@@ -2193,15 +2216,15 @@ int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
 
 // Workgroups of a tile kernel that are resident at once on the current device
 // (its grid is persistent), cached per device and instantiation.
-template <typename T, int D, int RW>
+template <typename T, int D, int RW, int kWv>
 int tile_launch_grid() {
   static int cached[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
   if (!cached[dev]) {
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attend_tile_kernel<T, D, RW>, 256,
-                                                     0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attend_tile_kernel<T, D, RW, kWv>,
+                                                     64 * kWv, 0) != hipSuccess ||
         per_cu <= 0)
       per_cu = 2;
     // at most 4 per compute unit: more only add workgroups that find no item
@@ -2211,9 +2234,13 @@ int tile_launch_grid() {
   return cached[dev];
 }
 
+// 32-row items (kWideRows rows) by 8-wavefront workgroups: every staged K/V
+// tile serves 256 rows (prefill chunks 278-300 -> 256-274 us against 4
+// wavefronts); 16-row items by 4.
 template <typename T, int D, int RW>
 int launch_tile_d(const Args& a, const Layout& L, float sl2, hipStream_t st) {
-  attend_tile_kernel<T, D, RW><<<tile_launch_grid<T, D, RW>(), 256, 0, st>>>(
+  constexpr int kWv = RW == 32 ? 8 : 4;
+  attend_tile_kernel<T, D, RW, kWv><<<tile_launch_grid<T, D, RW, kWv>(), 64 * kWv, 0, st>>>(
       VL_ATTN_LAUNCH_ARGS(T), L.hdr, RW == 32 ? L.wide_off : L.tile_off,
       RW == 32 ? L.wide_seq : nullptr, L.hdr + (RW == 32 ? 34 : 26));
   VL_CHECK_LAUNCH();
