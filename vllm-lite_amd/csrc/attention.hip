@@ -1010,7 +1010,14 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int pa
 #pragma unroll
         for (int r = 0; r < kCV; ++r) cmax = fmaxf(cmax, sc[t][r]);
       if constexpr (!kW) cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+      if constexpr (kW) {
+        // the row's other lane (l ^ 32) by a lane swap, not an LDS permute
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(cmax), __float_as_uint(cmax),
+                                                         false, false);
+        cmax = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      } else {
+        cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+      }
       const float cm = cmax * scale_log2;
       if (__any(cm > m_run + kLazy)) {
         const float m_new = fmaxf(m_run, cm);
@@ -1054,9 +1061,9 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int pa
 #pragma unroll
         for (int r = 0; r < kCV; ++r) {
           pr[t][r] = exp2_fast(fmaf(sc[t][r], scale_log2, neg_ref));
-          psum += pr[t][r];
+          if constexpr (!kW) psum += pr[t][r];
         }
-      l_part += psum;
+      if constexpr (!kW) l_part += psum;
       // ---- O^T += V^T P^T
       if constexpr (kW) {
         // 16-key k-steps: subtile t, half h covers keys 32t + 16h ..; this
@@ -1073,12 +1080,20 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int pa
             pw.z = cvt_pk_bf16(pr[t][8 * hh + 4], pr[t][8 * hh + 5]);
             pw.w = cvt_pk_bf16(pr[t][8 * hh + 6], pr[t][8 * hh + 7]);
             pop = __builtin_bit_cast(bf16x8_t, pw);
+            // the row sum of the weights as the MFMA uses them (bf16), by
+            // dot products with ones: 4 VALU ops per 8 weights instead of 8
+            const bf16x2_t ones = {(__bf16)1.f, (__bf16)1.f};
+            psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pw.x), ones, psum, false);
+            psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pw.y), ones, psum, false);
+            psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pw.z), ones, psum, false);
+            psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pw.w), ones, psum, false);
           }
           const uint4 vw = vq[st % kLook];
           if (st + kLook < kPvSteps) vq[st % kLook] = vread(st + kLook);
           acc[u] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, vw), pop,
                                                            acc[u], 0, 0, 0);
         }
+        l_part += psum;
       } else if constexpr (kBf16) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
