@@ -715,14 +715,15 @@ __device__ __forceinline__ int item_tid() {
       scale_log2, desc, nparts, split_base, ml, po
 
 
-// One workgroup item of the tile kernel (256 threads; the caller's LDS).
+// One workgroup item of the tile kernel (kWv wavefronts; the caller's LDS).
 // item_off holds the first item of each sequence, in sequence order, or (32-row
 // items) in the order of item_seq, which names the sequences; there a
 // sequence's row blocks come last block first.
 // RW = rows per wavefront: 16 (v_mfma_f32_16x16x32_bf16 / 16x16x4f32, 64-row
-// workgroups; short-query sequences, which may be split into partitions, and
-// fp32) or 32 (bf16 v_mfma_f32_32x32x16_bf16, 128-row workgroups, for long
-// query chunks: each K/V tile read from LDS feeds twice the rows). With RW 32
+// items on 4 wavefronts; short-query sequences, which may be split into
+// partitions, and fp32) or 32 (bf16 v_mfma_f32_32x32x16_bf16, 256-row items,
+// for long query chunks: one pass of 8 wavefronts, or two passes of the step
+// kernel's 4; each K/V tile read from LDS feeds twice the rows). With RW 32
 // a lane holds row l%32; its S^T values are keys 32t + 8(r/4) + 4(l/32) + r%4
 // (r < 16) and its O^T values dims 32u + 8(r/4) + 4(l/32) + r%4.
 template <typename T, int D, int RW, bool kMixed, int kWv = 4>
