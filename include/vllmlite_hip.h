@@ -243,8 +243,10 @@ int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_out, void* 
  * 16-column tiles [ceil(n/16), k, 16] (zero past column n; SwiGLU: the gate
  * tiles, then the up tiles; weight_stride unused; 16-byte aligned; inside a
  * tile element (k, m), k = 16g + 4s + j, at flat position 256g + 4(16j + m) +
- * s, so each lane's operands of 4 MFMA steps are one 16-byte load). out [rows, n]; out must not overlap x. rows <= 16, k a multiple of
- * 16, k <= 1024. fp32 throughout.
+ * s, so each lane's operands of 4 MFMA steps are one 16-byte load). out [rows, n]; out must not overlap x. rows <= 16 * 65535
+ * (a workgroup per 16 rows and 16 columns; built for the <= 16 rows of a
+ * decode step, where one row tile does it), k a multiple of 16, k <= 1024.
+ * fp32 throughout.
  */
 int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_stride,
                    const int32_t* row_index, const float* weight, int64_t weight_stride,
@@ -252,7 +254,7 @@ int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_str
                    void* stream);
 
 /*
- * K6b the QKV projection of a decode step fused with RoPE and the K/V
+ * K6b the QKV projection of a step's rows fused with RoPE and the K/V
  * scatter (vllmlite/model.py:96-103, 109; vllmlite/attention.py:21-37,
  * 47-49): qkv = f(x) @ weight (weight [k, (num_heads + 2 num_kv_heads) *
  * head_dim], f as in vl_linear_rows), then exactly what vl_rope_and_cache
@@ -262,8 +264,8 @@ int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_str
  * gather tok_emb[token_ids], model.py:93), and when x_out != NULL the rows
  * read (before the norm) are also written to x_out [rows, k] (the residual
  * stream). weight_layout: VL_WEIGHT_ROWS (row stride weight_stride) or
- * VL_WEIGHT_TILES16 (as for vl_linear_rows). rows <= 16, k a multiple of 16,
- * k <= 1024, head_dim even. fp32; the caches hold cache_dtype elements in
+ * VL_WEIGHT_TILES16 (as for vl_linear_rows). rows <= 16 * 65535, k a multiple
+ * of 16, k <= 1024, head_dim even. fp32; the caches hold cache_dtype elements in
  * kv_layout as for vl_rope_and_cache.
  */
 int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cache, const float* x,

@@ -1,5 +1,6 @@
-"""vl_linear_rows (K6): the TinyLlama projections for <= 16 token rows with
-RMSNorm / residual / SwiGLU fused, against float64 NumPy of the reference's
+"""vl_linear_rows (K6): the TinyLlama projections (16-row tiles; one tile for
+a decode step's <= 16 rows, several for a prefill step's) with RMSNorm /
+residual / SwiGLU fused, against float64 NumPy of the reference's
 formulas (vllmlite/model.py:17-23, 96-101, 114-120): rms_norm(x, w) =
 x / sqrt(mean(x^2) + 1e-5) * w, silu(x) = x / (1 + exp(-x))."""
 
@@ -29,7 +30,7 @@ def _close(got, want, tol=2e-5):
     np.testing.assert_allclose(got, want, rtol=0, atol=tol * scale)
 
 
-@pytest.mark.parametrize("rows", [1, 7, 16])
+@pytest.mark.parametrize("rows", [1, 7, 16, 17, 100])
 @pytest.mark.parametrize("k,n", [(384, 1152), (384, 384), (384, 261), (1024, 384), (64, 192),
                                  (128, 64), (496, 40)])
 @pytest.mark.parametrize("norm", [False, True])
@@ -52,7 +53,7 @@ def test_store_and_accumulate(rows, k, n, norm):
     _close(acc.cpu().numpy(), res + want)
 
 
-@pytest.mark.parametrize("rows", [1, 16])
+@pytest.mark.parametrize("rows", [1, 16, 33])
 @pytest.mark.parametrize("norm", [False, True])
 @pytest.mark.parametrize("k,dff", [(384, 1024), (64, 128)])
 def test_swiglu(rows, norm, k, dff):
@@ -94,15 +95,18 @@ def test_bad_arguments_raise():
     o = _ops()
     x = torch.zeros((17, 384), device="cuda")
     w = torch.zeros((384, 384), device="cuda")
-    with pytest.raises(RuntimeError):
-        o.linear_rows(torch.zeros((17, 384), device="cuda"), x, w)
+    out = torch.zeros((17, 384), device="cuda")
+    # more rows than 65535 row tiles: refused before any launch
+    rc = o.lib().vl_linear_rows(o._ptr(out), 384, o._ptr(x), 384, None, o._ptr(w), 384, None,
+                                1e-5, o.LINEAR_ROWS_MAX + 1, 384, 384, o.LINEAR_STORE, o._stream())
+    assert rc != 0
     with pytest.raises(RuntimeError):
         o.linear_rows(torch.zeros((4, 384), device="cuda"), torch.zeros((4, 100), device="cuda"),
                       torch.zeros((100, 384), device="cuda"))
 
 
 @pytest.mark.parametrize("layout", ["token", "head"])
-@pytest.mark.parametrize("rows", [1, 13, 16])
+@pytest.mark.parametrize("rows", [1, 13, 16, 37])
 @pytest.mark.parametrize("shape", [(8, 4, 48, 384), (4, 2, 16, 64)])
 def test_qkv_rope_cache_equals_projection_then_rope(rows, shape, layout):
     """vl_qkv_rope_cache gives the same bits as vl_linear_rows followed by

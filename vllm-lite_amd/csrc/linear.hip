@@ -1,7 +1,8 @@
-// K6 fp32 projections of the TinyLlama forward for batches of at most 16
-// token rows (the decode steps), with the RMSNorm before them and the
-// residual add or SwiGLU gate after them fused in (vllmlite/model.py:96-101,
-// 114, 116-117, 119-120).
+// K6 fp32 projections of the TinyLlama forward, with the RMSNorm before them
+// and the residual add or SwiGLU gate after them fused in
+// (vllmlite/model.py:96-101, 114, 116-117, 119-120). Built for few token rows
+// (the decode steps: at most 16, one row tile), and taking any number of rows
+// as 16-row tiles (the prefill steps), each tile re-reading the weights.
 //
 // One workgroup computes 16 rows x 16 output columns: its kLinWaves (8)
 // wavefronts split K into contiguous ranges on v_mfma_f32_16x16x4f32, each
@@ -22,7 +23,8 @@
 
 namespace {
 
-constexpr int kRowsMax = 16;
+constexpr int kRowsMax = 16;                 // rows per workgroup (one row tile)
+constexpr int kRowsLimit = kRowsMax * 65535;  // rows per call (grid y)
 constexpr int kCols = 16;
 #ifndef VL_LIN_WAVES
 #define VL_LIN_WAVES 8
@@ -99,6 +101,19 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
   __shared__ float red[kSlices][kLinWaves][kRowsMax * kCols];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c0 = blockIdx.x * kCols;
+  // row tile blockIdx.y: rows r0 .. r0 + 15 of the M; every row index below
+  // counts from r0
+  const int r0 = blockIdx.y * kRowsMax;
+  M = min(kRowsMax, M - r0);
+  if (row_index)
+    row_index += r0;
+  else
+    x += (int64_t)r0 * ldx;
+  if constexpr (MODE != 3) out += (int64_t)r0 * ldo;
+  if (x_out) x_out += (int64_t)r0 * K;
+  const int32_t* positions = MODE == 3 ? rc.positions + r0 : nullptr;
+  const int32_t* slots = MODE == 3 ? rc.slots + r0 : nullptr;
+  float* q_out = MODE == 3 ? rc.q_out + (int64_t)r0 * rc.nh * rc.hd : nullptr;
   const int m = lane & 15, j = lane >> 4;
   // wavefront w takes the spw steps of 4 k from step w spw (k in [kb, kb + 4
   // nsteps)); the last wavefronts may have fewer steps, or none
@@ -129,10 +144,10 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
   } else if constexpr (MODE == 3) {
     if (e_ok) {
       const int col = c0 + ec, qd = rc.nh * rc.hd, kd = rc.nkv * rc.hd;
-      e_slot = rc.slots[er];
+      e_slot = slots[er];
       if (col < qd + kd) {
         const int base = col < qd ? col : col - qd;
-        const int64_t tab = (int64_t)rc.positions[er] * (rc.hd >> 1) + ((base % rc.hd) >> 1);
+        const int64_t tab = (int64_t)positions[er] * (rc.hd >> 1) + ((base % rc.hd) >> 1);
         e_cos = rc.cos_t[tab];
         e_sin = rc.sin_t[tab];
       }
@@ -291,7 +306,7 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
       rotate_pair_f32(odd ? partner : v[0], odd ? v[0] : partner, e_cos, e_sin, &oe, &oo);
       const float val = odd ? oo : oe;
       if (col < qd)
-        rc.q_out[(int64_t)r * qd + col] = val;
+        q_out[(int64_t)r * qd + col] = val;
       else if (slot >= 0)
         store_cache(rc.kc, rc.geom.at(slot, base / rc.hd) + base % rc.hd, val, rc.kv_dtype);
     } else if (slot >= 0) {
@@ -305,9 +320,10 @@ template <int MODE, bool NORM, int KMAX>
 int launch(float* out, int64_t ldo, const float* x, int64_t ldx, const float* w, int64_t ldw,
            bool tiles, const float* norm_w, float eps, int M, int K, int N, hipStream_t st,
            const int32_t* row_index, const RopeCache& rc = RopeCache{}, float* x_out = nullptr) {
-  const int grid = (N + kCols - 1) / kCols;
+  const int ntile = (N + kCols - 1) / kCols;
+  const dim3 grid(ntile, (M + kRowsMax - 1) / kRowsMax);
   if (tiles) {
-    const int64_t up_off = MODE == 2 ? (int64_t)grid * K * kCols : 0;
+    const int64_t up_off = MODE == 2 ? (int64_t)ntile * K * kCols : 0;
     linear_rows_kernel<MODE, NORM, KMAX, true><<<grid, 64 * kLinWaves, 0, st>>>(
         out, ldo, x, ldx, w, 0, up_off, norm_w, eps, M, K, N, rc, row_index, x_out);
   } else {
@@ -325,7 +341,7 @@ extern "C" int vl_linear_rows(float* out, int64_t out_stride, const float* x, in
                               const int32_t* row_index, const float* weight,
                               int64_t weight_stride, const float* norm_weight, float eps,
                               int rows, int k, int n, int mode, void* stream) {
-  VL_CHECK_ARG(rows >= 0 && rows <= kRowsMax, "rows must be in 0..%d", kRowsMax);
+  VL_CHECK_ARG(rows >= 0 && rows <= kRowsLimit, "rows must be in 0..%d", kRowsLimit);
   const bool tiles = (mode & VL_LINEAR_TILES16) != 0;
   mode &= ~VL_LINEAR_TILES16;
   VL_CHECK_ARG(mode >= VL_LINEAR_STORE && mode <= VL_LINEAR_SWIGLU, "bad mode %d", mode);
@@ -373,7 +389,7 @@ extern "C" int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cach
   KvGeom geom;
   if (num_kv_heads > 0 && head_dim > 0)
     if (int rc = vl_kv_geom(kv_layout, block_size, num_kv_heads, head_dim, &geom)) return rc;
-  VL_CHECK_ARG(rows >= 0 && rows <= kRowsMax, "rows must be in 0..%d", kRowsMax);
+  VL_CHECK_ARG(rows >= 0 && rows <= kRowsLimit, "rows must be in 0..%d", kRowsLimit);
   VL_CHECK_ARG(k > 0 && k % 16 == 0 && k <= 1024, "k must be a multiple of 16, at most 1024");
   VL_CHECK_ARG(num_heads > 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 2 == 0,
                "bad head shape (head_dim even)");

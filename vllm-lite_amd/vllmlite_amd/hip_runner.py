@@ -46,6 +46,12 @@ from .model import model_weights, pack_weights, rope_tables, tile_weights
 from .runner import ModelRunner
 
 
+# steps of at most this many token rows run the fused projection kernels
+# (vl_linear_rows, vl_qkv_rope_cache: 16-row tiles, norm / residual / SwiGLU /
+# RoPE + scatter inside); larger ones hipBLASLt GEMMs and separate launches
+FUSED_ROWS_MAX = 1024
+
+
 def _bucket(n: int, floor: int) -> int:
     b = floor
     while b < n:
@@ -168,6 +174,7 @@ class HipRunner(ModelRunner):
             w = weights if weights is not None else model_weights(mc)
             self.w = pack_weights(mc, w, torch, self.device)
             self._fused_rows = fused_rows_supported(mc)
+            self.fused_rows_max = FUSED_ROWS_MAX
             if self._fused_rows:
                 tile_weights(self.w, ops.tile16)
             cos, sin = rope_tables(mc.head_dim, mc.max_seq_len)
@@ -345,7 +352,7 @@ class HipRunner(ModelRunner):
         qkv, q, attn = self._qkv[:Tb], self._q[:Tb], self._attn[:Tb]
         gu, act = self._gu[:Tb], self._act[:Tb]
         W = self.w
-        if Tb <= ops.LINEAR_ROWS_MAX and self._fused_rows:
+        if Tb <= min(self.fused_rows_max, ops.LINEAR_ROWS_MAX) and self._fused_rows:
             self._forward_rows(s, x, q, attn, act, tok, pos, slot, lidx, qsl, lens, bt)
             return
         torch.index_select(W["tok_emb"], 0, tok, out=x)
@@ -386,10 +393,11 @@ class HipRunner(ModelRunner):
 
     def _forward_rows(self, s: _Shape, x, q, attn, act, tok, pos, slot, lidx, qsl, lens,
                       bt) -> None:
-        """The forward for at most 16 token rows (the decode steps): each
-        projection is one launch with its RMSNorm, residual add, SwiGLU or
-        RoPE + K/V scatter fused in, so a layer is QKV (+ RoPE + cache),
-        attention, output (+= residual), gate|up (SwiGLU), down (+= residual)."""
+        """The forward by the fused projection kernels (every decode step, and
+        prefill steps up to fused_rows_max rows): each projection is one
+        launch with its RMSNorm, residual add, SwiGLU or RoPE + K/V scatter
+        fused in, so a layer is QKV (+ RoPE + cache), attention, output (+=
+        residual), gate|up (SwiGLU), down (+= residual)."""
         W, Tb, Rb = self.w, s.Tb, s.Rb
         self._plan(s, q, lens, qsl)
         for li, L in enumerate(W["layers"]):

@@ -363,7 +363,7 @@ def rms_norm(out: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, eps: floa
 LINEAR_STORE, LINEAR_ACCUMULATE, LINEAR_SWIGLU = 0, 1, 2
 LINEAR_TILES16 = 16  # mode flag: the weight is in 16-column tiles
 WEIGHT_ROWS, WEIGHT_TILES16 = 0, 1
-LINEAR_ROWS_MAX = 16
+LINEAR_ROWS_MAX = 16 * 65535  # rows per vl_linear_rows / vl_qkv_rope_cache call (16-row tiles)
 
 
 def tile16(w: torch.Tensor, halves: int = 1) -> torch.Tensor:
@@ -400,7 +400,7 @@ def _weight_layout(weight: torch.Tensor, k: int, n: int, halves: int):
 def linear_rows(out: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
                 norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
                 mode: int = LINEAR_STORE, row_index: Optional[torch.Tensor] = None) -> None:
-    """out (=, += or SwiGLU of) f(x) @ weight for at most 16 fp32 rows; f is
+    """out (=, += or SwiGLU of) f(x) @ weight for fp32 rows (16-row tiles); f is
     the RMSNorm times norm_weight when given; with row_index the input rows
     are x[row_index] (see vl_linear_rows)."""
     k = x.shape[1]
@@ -425,7 +425,7 @@ def qkv_rope_cache(q_out: torch.Tensor, key_cache: torch.Tensor, value_cache: to
                    sin: torch.Tensor, num_heads: int, num_kv_heads: int, head_dim: int,
                    eps: float = 1e-5, row_index: Optional[torch.Tensor] = None,
                    x_out: Optional[torch.Tensor] = None) -> None:
-    """QKV projection of <= 16 rows fused with RoPE and the K/V scatter; with
+    """QKV projection of a step's rows fused with RoPE and the K/V scatter; with
     row_index the rows are x[row_index], copied to x_out when given (see
     vl_qkv_rope_cache)."""
     k = x.shape[1]
