@@ -299,9 +299,14 @@ int vl_greedy_verify(const float* logits, int64_t row_stride, int vocab, const i
                      const int32_t* num_drafts, const int32_t* drafts, int max_drafts,
                      int32_t* out_tokens, int32_t* num_accepted, int num_seqs, void* stream);
 
-/* Row-wise argmax (ties to the lowest index) of rows x vocab fp32 logits. */
+/*
+ * Row-wise argmax (ties to the lowest index) of rows x vocab fp32 logits into
+ * out[rows], and also into out2 when it is not NULL: a second copy in memory
+ * the host reads (pinned host memory), written by the same launch instead of
+ * a copy behind it. (ABI 6 added out2.)
+ */
 int vl_argmax_rows(const float* logits, int64_t row_stride, int64_t rows, int vocab, int32_t* out,
-                   void* stream);
+                   int32_t* out2, void* stream);
 
 #ifdef __cplusplus
 }

@@ -265,8 +265,13 @@ def test_argmax_rows_numpy_ties_and_nan():
     x[5, :] = -np.inf
     x[6, -1] = 1e30
     out = torch.empty(64, dtype=torch.int32, device="cuda")
-    o.argmax_rows(dev(x), out)
-    assert to_np(out).astype(np.int64).tolist() == np.argmax(x, axis=-1).tolist()
+    host = torch.full((70,), -7, dtype=torch.int32, pin_memory=True)
+    o.argmax_rows(dev(x), out, host_out=host)
+    torch.cuda.synchronize()
+    want = np.argmax(x, axis=-1).tolist()
+    assert to_np(out).astype(np.int64).tolist() == want
+    # the pinned copy written by the same launch; entries past the rows untouched
+    assert host[:64].tolist() == want and host[64:].tolist() == [-7] * 6
 
 
 def test_greedy_verify_matches_oracle():

@@ -82,10 +82,14 @@ __device__ ArgBest block_argmax(const float* __restrict__ row, int vocab) {
 
 __global__ void __launch_bounds__(256) argmax_rows_kernel(const float* __restrict__ logits,
                                                           int64_t stride, int64_t rows, int vocab,
-                                                          int32_t* __restrict__ out) {
+                                                          int32_t* __restrict__ out,
+                                                          int32_t* __restrict__ out2) {
   for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
     const ArgBest b = block_argmax(logits + r * stride, vocab);
-    if (threadIdx.x == 0) out[r] = b.i;
+    if (threadIdx.x == 0) {
+      out[r] = b.i;
+      if (out2) out2[r] = b.i;
+    }
   }
 }
 
@@ -124,12 +128,13 @@ __global__ void verify_accept_kernel(const int32_t* __restrict__ num_drafts,
 }  // namespace
 
 extern "C" int vl_argmax_rows(const float* logits, int64_t row_stride, int64_t rows, int vocab,
-                              int32_t* out, void* stream) {
+                              int32_t* out, int32_t* out2, void* stream) {
   VL_CHECK_ARG(rows >= 0 && vocab > 0 && row_stride >= vocab, "bad shape");
   if (rows == 0) return VL_OK;
   VL_CHECK_ARG(logits && out, "null pointer");
   const int grid = (int)(rows < 65536 ? rows : 65536);
-  argmax_rows_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(logits, row_stride, rows, vocab, out);
+  argmax_rows_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(logits, row_stride, rows, vocab, out,
+                                                            out2);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }

@@ -236,8 +236,9 @@ class HipRunner(ModelRunner):
         with torch.cuda.device(self.device), torch.cuda.stream(self.stream):
             rows, R = self._run(out)
             k = self._buf
-            ops.argmax_rows(self._logits[:R], self._ids[:R])
-            self._ids_hosts[k][:R].copy_(self._ids[:R], non_blocking=True)
+            # the ids to the device buffer (the next step resolves its
+            # placeholders from it) and, by the same launch, to the pinned one
+            ops.argmax_rows(self._logits[:R], self._ids[:R], host_out=self._ids_hosts[k])
             self._done[k].record(self.stream)
             self._buf ^= 1
             # the handle holds its own buffer and event: a later step that grows

@@ -23,7 +23,7 @@ F32, BF16, F32_BF16KV, FP8_E4M3, F32_FP8KV = 0, 1, 2, 3, 4
 # VL_KV_*: a per-layer cache tensor [slots, Hkv, D] is token-major (the
 # reference's layout), [blocks, Hkv, block_size, D] head-major
 KV_TOKEN_MAJOR, KV_HEAD_MAJOR = 0, 1
-ABI_VERSION = 5  # vl_abi_version() of the library these signatures describe
+ABI_VERSION = 6  # vl_abi_version() of the library these signatures describe
 _c_void_p = ctypes.c_void_p
 _i32, _i64, _f32, _size = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
 
@@ -60,7 +60,7 @@ SIGNATURES = {
                                  _i32, _i32, _c_void_p]),
     "vl_greedy_verify": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i32,
                                 _c_void_p, _c_void_p, _i32, _c_void_p]),
-    "vl_argmax_rows": (_i32, [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p]),
+    "vl_argmax_rows": (_i32, [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p, _c_void_p]),
     "vl_linear_rows": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64,
                               _c_void_p, _f32, _i32, _i32, _i32, _i32, _c_void_p]),
     "vl_qkv_rope_cache": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
@@ -498,12 +498,20 @@ def greedy_verify(logits: torch.Tensor, row_start: torch.Tensor, num_drafts: tor
            "vl_greedy_verify")
 
 
-def argmax_rows(logits: torch.Tensor, out: torch.Tensor) -> None:
+def argmax_rows(logits: torch.Tensor, out: torch.Tensor,
+                host_out: Optional[torch.Tensor] = None) -> None:
+    """out[r] = argmax of logits row r (ties to the lowest index); host_out, a
+    pinned int32 CPU tensor of at least as many entries, receives the same ids
+    from the same launch (no copy behind it); read it after the stream has
+    passed the launch."""
     _need(logits.dtype == torch.float32 and logits.stride(1) == 1, "logits must be fp32 rows")
     _dev_i32(out, "out")
     _need(out.numel() == logits.shape[0], "out length")
+    _need(host_out is None or (host_out.dtype == torch.int32 and host_out.is_pinned() and
+                               host_out.is_contiguous() and host_out.numel() >= out.numel()),
+          "host_out must be a pinned contiguous int32 tensor")
     _check(lib().vl_argmax_rows(_ptr(logits), logits.stride(0), logits.shape[0], logits.shape[1],
-                                _ptr(out), _stream()), "vl_argmax_rows")
+                                _ptr(out), _ptr(host_out), _stream()), "vl_argmax_rows")
 
 
 def resolve_tokens(token_ids: torch.Tensor, prev_ids: torch.Tensor) -> None:
