@@ -30,7 +30,7 @@ def _close(got, want, tol=2e-5):
     np.testing.assert_allclose(got, want, rtol=0, atol=tol * scale)
 
 
-@pytest.mark.parametrize("rows", [1, 7, 16, 17, 100])
+@pytest.mark.parametrize("rows", [1, 7, 16, 17, 100, 1024])
 @pytest.mark.parametrize("k,n", [(384, 1152), (384, 384), (384, 261), (1024, 384), (64, 192),
                                  (128, 64), (496, 40)])
 @pytest.mark.parametrize("norm", [False, True])
