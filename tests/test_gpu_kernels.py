@@ -336,17 +336,20 @@ def test_short_decode_kernel(D, H, Hkv, bs, dtype, layout):
                                   [(1, 40), (7, 300), (1, 2000), (16, 16), (3, 5000)]])
 @pytest.mark.parametrize("ctx_hint", [True, False])
 @pytest.mark.parametrize("layout", ["token", "head"])
-def test_fp32_query_over_bf16_cache(seqs, ctx_hint, layout):
+@pytest.mark.parametrize("D", [48, 128, 80])
+def test_fp32_query_over_bf16_cache(seqs, ctx_hint, layout, D):
     """VL_DTYPE_F32_BF16KV: fp32 query and output over bf16 caches (decodes
-    by the short-decode kernel when the bounds allow, everything else by the
-    generic kernel and the combine) against the oracle on the bf16 K/V values,
+    by the short-decode kernel when the bounds allow; the rest by the fp32
+    MFMA tile kernel, which widens the cache elements when it stages them,
+    for head_dims with a tile instantiation (48, 128), else by the generic
+    kernel (80); then the combine) against the oracle on the bf16 K/V values,
     at the fp32 tolerance; both cache layouts."""
     o = ops()
-    b = make_batch(seqs, 8, 4, 48, 16, seed=len(seqs) + ctx_hint)
+    b = make_batch(seqs, 8, 4, D, 16, seed=len(seqs) + ctx_hint + D)
     q = dev(b["q"])
     kc, vc = caches(b, torch.bfloat16, layout)
     S, T = len(seqs), b["q"].shape[0]
-    ws = o.AttentionWorkspace().get(o.paged_attention_workspace_size(S, T, 8, 48,
+    ws = o.AttentionWorkspace().get(o.paged_attention_workspace_size(S, T, 8, D,
                                                                      int(b["seq_lens"].max())))
     out = torch.full_like(q, float("nan"))
     q_lens = np.diff(b["qsl"])
@@ -361,14 +364,17 @@ def test_fp32_query_over_bf16_cache(seqs, ctx_hint, layout):
                                   [(1, 40), (7, 300), (1, 2000), (16, 16), (3, 5000)]])
 @pytest.mark.parametrize("ctx_hint", [True, False])
 @pytest.mark.parametrize("layout", ["token", "head"])
-def test_fp32_query_over_fp8_cache(seqs, ctx_hint, layout):
+@pytest.mark.parametrize("D", [48, 128, 80])
+def test_fp32_query_over_fp8_cache(seqs, ctx_hint, layout, D):
     """VL_DTYPE_F32_FP8KV: fp32 query and output over FP8 E4M3 caches (the
-    short-decode kernel when the bounds allow, else the generic kernel and
-    the combine) against the oracle on the FP8 values of K/V, at the fp32
-    tolerance; poisoned slots hold the FP8 NaN code."""
+    short-decode kernel when the bounds allow; else the fp32 MFMA tile kernel
+    widening the FP8 elements exactly when it stages them (head_dim 48, 128)
+    or the generic kernel (80); then the combine) against the oracle on the
+    FP8 values of K/V, at the fp32 tolerance; poisoned slots hold the FP8 NaN
+    code."""
     from oracle.attention import fp8_e4m3_decode, fp8_e4m3_encode
     o = ops()
-    b = make_batch(seqs, 8, 4, 48, 16, seed=7 + len(seqs) + ctx_hint)
+    b = make_batch(seqs, 8, 4, D, 16, seed=7 + len(seqs) + ctx_hint + D)
     kq, vq = fp8_e4m3_decode(fp8_e4m3_encode(b["k_cache"])), fp8_e4m3_decode(fp8_e4m3_encode(b["v_cache"]))
     fb = dict(b, k_cache=kq, v_cache=vq)
 
@@ -381,7 +387,7 @@ def test_fp32_query_over_fp8_cache(seqs, ctx_hint, layout):
         kc, vc = fp8_dev(b["k_cache"]), fp8_dev(b["v_cache"])
     q = dev(b["q"])
     S, T = len(seqs), b["q"].shape[0]
-    ws = o.AttentionWorkspace().get(o.paged_attention_workspace_size(S, T, 8, 48,
+    ws = o.AttentionWorkspace().get(o.paged_attention_workspace_size(S, T, 8, D,
                                                                      int(b["seq_lens"].max())))
     out = torch.full_like(q, float("nan"))
     q_lens = np.diff(b["qsl"])

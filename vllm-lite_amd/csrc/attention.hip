@@ -159,9 +159,8 @@ inline bool fast_shape(int dtype, int H, int Hkv, int D, int bs) {
 // head_dims with an MFMA tile instantiation
 inline bool tile_shape(int dtype, int D, int bs) {
   if (bs <= 0 || (bs & (bs - 1)) != 0) return false;  // block math is shifts and masks
-  if (dtype == VL_DTYPE_F32_BF16KV || dtype == VL_DTYPE_F32_FP8KV)
-    return false;  // narrow caches under an fp32 query: the generic kernel takes them
   if (dtype == VL_DTYPE_BF16) return D == 64 || D == 128;
+  // fp32, and fp32 queries over bf16 / FP8 E4M3 caches (widened when staged)
   return D == 16 || D == 32 || D == 48 || D == 64 || D == 128;
 }
 
@@ -615,6 +614,21 @@ __device__ __forceinline__ uint4 load16(const void* p) {
   return __builtin_bit_cast(uint4, *reinterpret_cast<const u32x4_t*>(p));
 }
 
+// 4 consecutive cache elements as the bits of 4 fp32 values: fp32 as they
+// are, bf16 and FP8 E4M3 widened (exactly) for the fp32 tile path
+__device__ __forceinline__ uint4 load4_as_f32(const float* p) { return load16(p); }
+__device__ __forceinline__ uint4 load4_as_f32(const uint16_t* p) {
+  const uint2 w = *reinterpret_cast<const uint2*>(p);
+  return make_uint4(w.x << 16, w.x & 0xffff0000u, w.y << 16, w.y & 0xffff0000u);
+}
+__device__ __forceinline__ uint4 load4_as_f32(const uint8_t* p) {
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+  return make_uint4(__float_as_uint(e4m3_to_f32((uint8_t)w)),
+                    __float_as_uint(e4m3_to_f32((uint8_t)(w >> 8))),
+                    __float_as_uint(e4m3_to_f32((uint8_t)(w >> 16))),
+                    __float_as_uint(e4m3_to_f32((uint8_t)(w >> 24))));
+}
+
 // The same for the K / V bytes of a tile item: a non-temporal (streaming)
 // load when no other item reads them (a sequence whose rows fit one item:
 // spec-verify and short chunks; measured 950 -> 870 us on the 64 x 5 verify
@@ -703,9 +717,12 @@ __device__ __forceinline__ int item_tid() {
 // compiler reads the plan's arrays with scalar loads. K/V are not restrict:
 // restrict-qualified loads are treated as invariant and may be scheduled past
 // the compiler barriers that batch them.
-#define VL_ATTN_PARAMS(T)                                                                    \
-  T *__restrict__ out, const T *__restrict__ query, int64_t q_stride, const T *kc,          \
-      const T *vc, const int32_t *__restrict__ bt, int bt_stride,                           \
+#define VL_ATTN_PARAMS(T) VL_ATTN_PARAMS_KV(T, T)
+// (TKV: the cache elements, when they differ from the query's: fp32 queries
+// over bf16 or FP8 E4M3 caches)
+#define VL_ATTN_PARAMS_KV(T, TKV)                                                            \
+  T *__restrict__ out, const T *__restrict__ query, int64_t q_stride, const TKV *kc,        \
+      const TKV *vc, const int32_t *__restrict__ bt, int bt_stride,                         \
       const int32_t *__restrict__ seq_lens, const int32_t *__restrict__ qsl, int S, int H,   \
       int Hkv, int bs_log2, int kv_hm, float scale_log2, const int4 *__restrict__ desc,      \
       const int32_t *__restrict__ nparts,                                                    \
@@ -726,15 +743,17 @@ __device__ __forceinline__ int item_tid() {
 // kernel's 4; each K/V tile read from LDS feeds twice the rows). With RW 32
 // a lane holds row l%32; its S^T values are keys 32t + 8(r/4) + 4(l/32) + r%4
 // (r < 16) and its O^T values dims 32u + 8(r/4) + 4(l/32) + r%4.
-template <typename T, int D, int RW, bool kMixed, int kWv = 4>
+template <typename T, int D, int RW, bool kMixed, int kWv = 4, typename TKV = T>
 __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int pass, int P,
                                           const int32_t* __restrict__ item_off,
                                           const int32_t* __restrict__ item_seq,
-                                          VL_ATTN_PARAMS(T)) {
+                                          VL_ATTN_PARAMS_KV(T, TKV)) {
   const int tid = item_tid<kMixed>();
   constexpr bool kBf16 = sizeof(T) == 2;
   constexpr bool kW = RW == 32;
   static_assert(RW == 16 || (RW == 32 && kBf16), "32-row wavefronts are bf16 only");
+  static_assert(std::is_same<T, TKV>::value || (!kBf16 && RW == 16),
+                "narrow caches under fp32 queries only");
   constexpr int kRows = kWv * RW;                         // rows per pass (kWv wavefronts)
   // a 32-row item spans kWideRows rows: one pass of an 8-wavefront
   // workgroup, or `pass` 0 or 1 of a 4-wavefront one (the step kernel
@@ -891,8 +910,8 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int pa
           const int key = k0 + kk;
           const bool ok = idx < kTileKeys * Lds::kChunks && key < kend_wg;
           const int64_t off = ok ? row_of(key) + c * 4 : 0;
-          pk[r] = ok ? *reinterpret_cast<const uint4*>(kc + off) : make_uint4(0, 0, 0, 0);
-          pv[r] = ok ? *reinterpret_cast<const uint4*>(vc + off) : make_uint4(0, 0, 0, 0);
+          pk[r] = ok ? load4_as_f32(kc + off) : make_uint4(0, 0, 0, 0);
+          pv[r] = ok ? load4_as_f32(vc + off) : make_uint4(0, 0, 0, 0);
         }
       }
     };
@@ -1223,9 +1242,9 @@ constexpr int kXcds = 8;
 // which the sequence's other row blocks read again; the plan orders the
 // items longest first, so the launch ends on short ones. The counters are
 // zeroed by the plan and by the combine launch that follows every run.
-template <typename T, int D, int RW, int kWv>
+template <typename T, int D, int RW, int kWv, typename TKV = T>
 __global__ void __launch_bounds__(64 * kWv) __attribute__((amdgpu_waves_per_eu(2))) attend_tile_kernel(
-    VL_ATTN_PARAMS(T), const int32_t* __restrict__ hdr, const int32_t* __restrict__ item_off,
+    VL_ATTN_PARAMS_KV(T, TKV), const int32_t* __restrict__ hdr, const int32_t* __restrict__ item_off,
     const int32_t* __restrict__ item_seq, int32_t* counters) {
   __shared__ TileLds<T, D, RW> lds;
   __shared__ int claim_lds;
@@ -1238,7 +1257,7 @@ __global__ void __launch_bounds__(64 * kWv) __attribute__((amdgpu_waves_per_eu(2
   while (it < n_items) {
     int nxt = 0;
     if (threadIdx.x == 0) nxt = per_queue + atomicAdd(counters + xcd, 1);
-    tile_body<T, D, RW, false, kWv>(lds, it, 0, P, item_off, item_seq, VL_ATTN_ARGS);
+    tile_body<T, D, RW, false, kWv, TKV>(lds, it, 0, P, item_off, item_seq, VL_ATTN_ARGS);
     __syncthreads();  // the item is done with the LDS; claim_lds has been read
     if (threadIdx.x == 0) claim_lds = nxt;
     __syncthreads();
@@ -2225,21 +2244,23 @@ int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
 }
 
 // The VL_ATTN_PARAMS arguments of a launch (inside do_run / launch_tile_d).
-#define VL_ATTN_LAUNCH_ARGS(T)                                                                  \
-  (T*)a.out, (const T*)a.query, a.q_stride, (const T*)a.kc, (const T*)a.vc, a.bt, a.bt_stride,  \
+#define VL_ATTN_LAUNCH_ARGS(T) VL_ATTN_LAUNCH_ARGS_KV(T, T)
+#define VL_ATTN_LAUNCH_ARGS_KV(T, TKV)                                                          \
+  (T*)a.out, (const T*)a.query, a.q_stride, (const TKV*)a.kc, (const TKV*)a.vc, a.bt,          \
+      a.bt_stride,                                                                              \
       a.seq_lens, a.qsl, a.S, a.H, a.Hkv, __builtin_ctz(a.bs),                                 \
       a.kv_layout == VL_KV_HEAD_MAJOR ? 1 : 0, sl2, L.desc, L.nparts, L.split_base, L.ml, L.po
 
 // Workgroups of a tile kernel that are resident at once on the current device
 // (its grid is persistent), cached per device and instantiation.
-template <typename T, int D, int RW, int kWv>
+template <typename T, int D, int RW, int kWv, typename TKV = T>
 int tile_launch_grid() {
   static int cached[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
   if (!cached[dev]) {
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attend_tile_kernel<T, D, RW, kWv>,
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, attend_tile_kernel<T, D, RW, kWv, TKV>,
                                                      64 * kWv, 0) != hipSuccess ||
         per_cu <= 0)
       per_cu = 2;
@@ -2253,11 +2274,12 @@ int tile_launch_grid() {
 // 32-row items (kWideRows rows) by 8-wavefront workgroups: every staged K/V
 // tile serves 256 rows (prefill chunks 278-300 -> 256-274 us against 4
 // wavefronts); 16-row items by 4.
-template <typename T, int D, int RW>
+template <typename T, int D, int RW, typename TKV = T>
 int launch_tile_d(const Args& a, const Layout& L, float sl2, hipStream_t st) {
   constexpr int kWv = RW == 32 ? 8 : 4;
-  attend_tile_kernel<T, D, RW, kWv><<<tile_launch_grid<T, D, RW, kWv>(), 64 * kWv, 0, st>>>(
-      VL_ATTN_LAUNCH_ARGS(T), L.hdr, RW == 32 ? L.wide_off : L.tile_off,
+  attend_tile_kernel<T, D, RW, kWv, TKV><<<tile_launch_grid<T, D, RW, kWv, TKV>(), 64 * kWv, 0,
+                                           st>>>(
+      VL_ATTN_LAUNCH_ARGS_KV(T, TKV), L.hdr, RW == 32 ? L.wide_off : L.tile_off,
       RW == 32 ? L.wide_seq : nullptr, L.hdr + (RW == 32 ? 34 : 26));
   VL_CHECK_LAUNCH();
   return VL_OK;
@@ -2265,7 +2287,7 @@ int launch_tile_d(const Args& a, const Layout& L, float sl2, hipStream_t st) {
 
 // The 16-row tile kernel always (short-query and fp32 items); for bf16 also
 // the 32-row kernel when a sequence may have more than kSplitMaxQ queries.
-template <typename T>
+template <typename T, typename TKV = T>
 int launch_tile(const Args& a, const Layout& L, float sl2, int max_q, hipStream_t st) {
   const bool wide = sizeof(T) == 2 && (max_q <= 0 || max_q > kSplitMaxQ);
   int rc = VL_OK;
@@ -2282,11 +2304,11 @@ int launch_tile(const Args& a, const Layout& L, float sl2, int max_q, hipStream_
     }
   } else {
     switch (a.D) {
-      case 16: return launch_tile_d<T, 16, 16>(a, L, sl2, st);
-      case 32: return launch_tile_d<T, 32, 16>(a, L, sl2, st);
-      case 48: return launch_tile_d<T, 48, 16>(a, L, sl2, st);
-      case 64: return launch_tile_d<T, 64, 16>(a, L, sl2, st);
-      case 128: return launch_tile_d<T, 128, 16>(a, L, sl2, st);
+      case 16: return launch_tile_d<T, 16, 16, TKV>(a, L, sl2, st);
+      case 32: return launch_tile_d<T, 32, 16, TKV>(a, L, sl2, st);
+      case 48: return launch_tile_d<T, 48, 16, TKV>(a, L, sl2, st);
+      case 64: return launch_tile_d<T, 64, 16, TKV>(a, L, sl2, st);
+      case 128: return launch_tile_d<T, 128, 16, TKV>(a, L, sl2, st);
     }
   }
   VL_CHECK_ARG(false, "no tile kernel for head_dim %d", a.D);
@@ -2347,7 +2369,10 @@ int do_run(const Args& a, int max_q, int min_q, int max_ctx, void* ws, size_t ws
   constexpr bool one_type = std::is_same<T, TKV>::value;
   const bool fast = one_type && fast_shape(a.dtype, a.H, a.Hkv, a.D, a.bs);
   if constexpr (!one_type) {
-    // generic kernel below
+    if (tile_shape(a.dtype, a.D, a.bs)) {
+      const int rc = launch_tile<T, TKV>(a, L, sl2, max_q, st);
+      if (rc) return rc;
+    }
   } else if (fast) {
     if (max_q == 1) {  // every sequence is a decode
       attend_decode_bf16_kernel<<<decode_grid(), 256, 0, st>>>(VL_ATTN_LAUNCH_ARGS(uint16_t),
@@ -2376,7 +2401,7 @@ int do_run(const Args& a, int max_q, int min_q, int max_ctx, void* ws, size_t ws
     int rc = launch_tile<T>(a, L, sl2, max_q, st);
     if (rc) return rc;
   }
-  if (!one_type || (!fast && !tile_shape(a.dtype, a.D, a.bs))) {
+  if (!fast && !tile_shape(a.dtype, a.D, a.bs)) {
     attend_generic_kernel<T, TKV><<<ncu * 16, 64, 0, st>>>(
         (T*)a.out, (const T*)a.query, a.q_stride, (const TKV*)a.kc, (const TKV*)a.vc, a.bt,
         a.bt_stride, a.seq_lens, a.qsl, a.S, a.H, a.Hkv, a.D, a.bs,
