@@ -622,11 +622,10 @@ __device__ __forceinline__ uint4 load4_as_f32(const uint16_t* p) {
   return make_uint4(w.x << 16, w.x & 0xffff0000u, w.y << 16, w.y & 0xffff0000u);
 }
 __device__ __forceinline__ uint4 load4_as_f32(const uint8_t* p) {
-  const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
-  return make_uint4(__float_as_uint(e4m3_to_f32((uint8_t)w)),
-                    __float_as_uint(e4m3_to_f32((uint8_t)(w >> 8))),
-                    __float_as_uint(e4m3_to_f32((uint8_t)(w >> 16))),
-                    __float_as_uint(e4m3_to_f32((uint8_t)(w >> 24))));
+  float r[4];
+  e4m3x4_to_f32(*reinterpret_cast<const uint32_t*>(p), r);
+  return make_uint4(__float_as_uint(r[0]), __float_as_uint(r[1]), __float_as_uint(r[2]),
+                    __float_as_uint(r[3]));
 }
 
 // The same for the K / V bytes of a tile item: a non-temporal (streaming)
@@ -1843,11 +1842,8 @@ __device__ __forceinline__ void widen16(const uint4& v, float* r) {
     r[0] = __uint_as_float(v.x), r[1] = __uint_as_float(v.y);
     r[2] = __uint_as_float(v.z), r[3] = __uint_as_float(v.w);
   } else if constexpr (sizeof(T) == 1) {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) r[4 * e + b] = e4m3_to_f32((w[e] >> (8 * b)) & 0xffu);
+    e4m3x4_to_f32(v.x, r), e4m3x4_to_f32(v.y, r + 4);
+    e4m3x4_to_f32(v.z, r + 8), e4m3x4_to_f32(v.w, r + 12);
   } else {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
