@@ -651,3 +651,29 @@ def test_resolve_tokens_takes_previous_step_ids():
     d = dev(tok)
     o.resolve_tokens(d, dev(prev))
     assert np.array_equal(to_np(d).astype(np.int64), want.astype(np.int64))
+
+
+@pytest.mark.parametrize("D,q_len", [(48, 1), (128, 2), (80, 2)])
+def test_fp8_cache_values_decode_exactly(D, q_len):
+    """Every FP8 E4M3 code (NaN and subnormals included) comes out of the
+    attention as the oracle's decoded value: with a zero query the first query
+    of each sequence sees one key with weight exactly 1, so its output is that
+    key's V row decoded (the short-decode kernel at head_dim 48, the fp32
+    tile kernel at 128, the generic kernel at 80)."""
+    from oracle.attention import fp8_e4m3_decode
+    o = ops()
+    S = -(-256 // D)
+    codes = np.resize(np.arange(256, dtype=np.uint8), S * D).reshape(S, D)
+    kc = np.full((S * 16, 1, D), 0x38, np.uint8)  # every key 1.0
+    vc = np.full((S * 16, 1, D), 0x38, np.uint8)
+    vc[np.arange(S) * 16, 0, :] = codes  # key 0 of sequence s: the codes
+    f8 = lambda a: dev(a).view(torch.float8_e4m3fn)
+    q = torch.zeros((S * q_len, 1, D), dtype=torch.float32, device="cuda")
+    out = torch.full_like(q, 7.0)
+    ws = o.AttentionWorkspace().get(o.paged_attention_workspace_size(S, S * q_len, 1, D, q_len))
+    o.paged_attention(out, q, f8(kc), f8(vc), dev(np.arange(S, dtype=np.int32).reshape(S, 1)),
+                      dev(np.full(S, q_len, np.int32)),
+                      dev(np.arange(S + 1, dtype=np.int32) * q_len), 1.0 / np.sqrt(D), 16, ws,
+                      max_query_len=q_len, min_query_len=q_len, max_context_len=q_len)
+    got = to_np(out).reshape(S, q_len, D)[:, 0, :]
+    np.testing.assert_array_equal(got, fp8_e4m3_decode(codes))

@@ -92,9 +92,9 @@ __host__ __device__ __forceinline__ uint8_t f32_to_e4m3(float f) {
 
 // Four FP8 E4M3 bytes (w, little-endian) to fp32, exactly, by gfx950's
 // conversion instruction (v_cvt_pk_f32_fp8 reads OCP E4M3: exponent bias 7,
-// 0x7f / 0xff NaN, subnormals m * 2^-9; all 256 codes checked on the device
-// against the bit-level decode of the oracle's fp8_e4m3_decode); one
-// instruction per two bytes
+// 0x7f / 0xff NaN, subnormals m * 2^-9; every code of the cache is checked
+// against the oracle's fp8_e4m3_decode through each attention kernel by the
+// GPU tests); one instruction per two bytes
 __device__ __forceinline__ void e4m3x4_to_f32(uint32_t w, float* r) {
   typedef float f32x2_t __attribute__((ext_vector_type(2)));
   const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)w, false);
