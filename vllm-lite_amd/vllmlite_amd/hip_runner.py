@@ -11,16 +11,19 @@ count) for scheduled sequence i, count = min(1 + drafts, tokens)
      [token_ids | positions | slot_mapping | logits_idx | query_start_loc |
      seq_lens | block_tables] (runner.py:62-100, block.py:154-156) and sent
      with a single host-to-device copy from pinned memory;
-  3. the TinyLlama forward (model.py:80-120) runs on the device: embedding
-     gather, then per layer fused RMSNorm(+residual), one QKV GEMM, RoPE fused
-     with the K/V slot scatter, the ragged paged attention (planned once per
-     step, run per layer), the output GEMM, fused RMSNorm(+residual), one
-     gate|up GEMM, SwiGLU, the down GEMM; finally RMSNorm and the tied lm_head
-     on the logits rows only. Steps of at most 16 tokens (the decode steps)
-     run each projection as one vl_linear_rows launch with the RMSNorm before
-     it and the residual add or SwiGLU after it fused in (weights in
-     16-column tiles);
-  4. one device-to-host copy of the logits rows and a stream synchronisation.
+  3. the TinyLlama forward (model.py:80-120) runs on the device. Steps of up
+     to FUSED_ROWS_MAX tokens (every step of the published mixes) run each
+     projection as one vl_linear_rows / vl_qkv_rope_cache launch over 16-row
+     tiles, with the RMSNorm before it and the residual add, SwiGLU, or RoPE
+     and the K/V slot scatter after it fused in (weights in 16-column tiles;
+     layer 0 also gathers the embedding rows), and the ragged paged attention
+     between (planned once per step, run per layer; decode-only steps take
+     the short-decode kernel, no plan); finally RMSNorm and the lm_head on the
+     logits rows only. Larger steps run PyTorch GEMMs with separate RMSNorm,
+     RoPE + scatter and SwiGLU launches;
+  4. one device-to-host copy of the logits rows and a stream synchronisation
+     (execute), or the argmax of each row written to pinned host memory by
+     its launch (execute_argmax / launch_argmax).
 
 Step 3 is captured once per shape bucket (tokens, sequences and logits rows
 each rounded up to a power of two) into a HIP graph and replayed afterwards;
@@ -127,8 +130,8 @@ def flatten_scheduled(out, block_size: int, max_seq_len: int) -> Flattened:
 
 
 def fused_rows_supported(mc) -> bool:
-    """Steps of <= 16 token rows run the fused projection kernels
-    (vl_linear_rows, vl_qkv_rope_cache), which need d_model and d_ff to be
+    """Steps of up to FUSED_ROWS_MAX token rows run the fused projection
+    kernels (vl_linear_rows, vl_qkv_rope_cache), which need d_model and d_ff to be
     multiples of 16 within their K limits; other shapes take the GEMM path for
     every step and keep no tiled weight copies."""
     return (mc.d_model % 16 == 0 and mc.d_ff % 16 == 0 and mc.d_model <= 512
