@@ -244,8 +244,9 @@ int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_out, void* 
  * tiles, then the up tiles; weight_stride unused; 16-byte aligned; inside a
  * tile element (k, m), k = 16g + 4s + j, at flat position 256g + 4(16j + m) +
  * s, so each lane's operands of 4 MFMA steps are one 16-byte load). out [rows, n]; out must not overlap x. rows <= 16 * 65535
- * (a workgroup per 16 rows and 16 columns; built for the <= 16 rows of a
- * decode step, where one row tile does it), k a multiple of 16, k <= 1024.
+ * (a workgroup per 16 columns and 16 rows, or 2 or 4 row tiles in turn on large
+ * grids; built for the <= 16 rows of a decode step, where one row tile does
+ * it), k a multiple of 16, k <= 1024.
  * fp32 throughout.
  */
 int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_stride,

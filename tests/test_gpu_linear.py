@@ -1,5 +1,6 @@
 """vl_linear_rows (K6): the TinyLlama projections (16-row tiles; one tile for
-a decode step's <= 16 rows, several for a prefill step's) with RMSNorm /
+a decode step's <= 16 rows, several for a prefill step's, up to 4 of them one
+after another in a workgroup when the grid is large) with RMSNorm /
 residual / SwiGLU fused, against float64 NumPy of the reference's
 formulas (vllmlite/model.py:17-23, 96-101, 114-120): rms_norm(x, w) =
 x / sqrt(mean(x^2) + 1e-5) * w, silu(x) = x / (1 + exp(-x))."""
@@ -30,7 +31,7 @@ def _close(got, want, tol=2e-5):
     np.testing.assert_allclose(got, want, rtol=0, atol=tol * scale)
 
 
-@pytest.mark.parametrize("rows", [1, 7, 16, 17, 100, 1024])
+@pytest.mark.parametrize("rows", [1, 7, 16, 17, 100, 1000, 1024])
 @pytest.mark.parametrize("k,n", [(384, 1152), (384, 384), (384, 261), (1024, 384), (64, 192),
                                  (128, 64), (496, 40)])
 @pytest.mark.parametrize("norm", [False, True])
@@ -53,7 +54,7 @@ def test_store_and_accumulate(rows, k, n, norm):
     _close(acc.cpu().numpy(), res + want)
 
 
-@pytest.mark.parametrize("rows", [1, 16, 33])
+@pytest.mark.parametrize("rows", [1, 16, 33, 1000])
 @pytest.mark.parametrize("norm", [False, True])
 @pytest.mark.parametrize("k,dff", [(384, 1024), (64, 128)])
 def test_swiglu(rows, norm, k, dff):
@@ -106,7 +107,7 @@ def test_bad_arguments_raise():
 
 
 @pytest.mark.parametrize("layout", ["token", "head"])
-@pytest.mark.parametrize("rows", [1, 13, 16, 37])
+@pytest.mark.parametrize("rows", [1, 13, 16, 37, 700])
 @pytest.mark.parametrize("shape", [(8, 4, 48, 384), (4, 2, 16, 64)])
 def test_qkv_rope_cache_equals_projection_then_rope(rows, shape, layout):
     """vl_qkv_rope_cache gives the same bits as vl_linear_rows followed by
@@ -122,12 +123,13 @@ def test_qkv_rope_cache_equals_projection_then_rope(rows, shape, layout):
     w = dev((0.05 * rng.standard_normal((k, n))).astype(np.float32))
     g = dev((1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32))
     pos = dev(rng.integers(0, 64, rows).astype(np.int32))
-    slots = rng.permutation(40)[:rows].astype(np.int32)
+    nslots = 40 if rows <= 40 else (rows + 7) // 8 * 8
+    slots = rng.permutation(nslots)[:rows].astype(np.int32)
     slots[::5] = -1
     slot = dev(slots)
     ang = rng.standard_normal((64, D // 2)).astype(np.float32)
     cos, sin = dev(np.cos(ang)), dev(np.sin(ang))
-    shape = (5, Hkv, 8, D) if layout == "head" else (40, Hkv, D)
+    shape = (nslots // 8, Hkv, 8, D) if layout == "head" else (nslots, Hkv, D)
     kc1, vc1 = (torch.full(shape, float("nan"), device="cuda") for _ in range(2))
     kc2, vc2 = kc1.clone(), vc1.clone()
     q1 = torch.empty((rows, H, D), device="cuda")
@@ -142,8 +144,8 @@ def test_qkv_rope_cache_equals_projection_then_rope(rows, shape, layout):
     assert torch.equal(vc1.nan_to_num(7.0), vc2.nan_to_num(7.0))
     if layout == "head":  # row (slot, h) of the head-major cache is rotated k / v of slot's row
         from oracle.attention import apply_rope
-        kh = kc1.permute(0, 2, 1, 3).reshape(40, Hkv, D).cpu().numpy()
-        vh = vc1.permute(0, 2, 1, 3).reshape(40, Hkv, D).cpu().numpy()
+        kh = kc1.permute(0, 2, 1, 3).reshape(nslots, Hkv, D).cpu().numpy()
+        vh = vc1.permute(0, 2, 1, 3).reshape(nslots, Hkv, D).cpu().numpy()
         ok = slots >= 0
         qkvn = qkv.cpu().numpy()
         k_rows = qkvn[:, H * D:(H + Hkv) * D].reshape(rows, Hkv, D)
@@ -190,7 +192,8 @@ def test_qkv_rope_cache_narrow_cache_is_the_rounded_fp32_cache(rows, cdt):
         assert np.array_equal(b16b.float().cpu().numpy(), want)
 
 
-def test_row_index_gathers_input_rows():
+@pytest.mark.parametrize("nrows", [9, 1000])
+def test_row_index_gathers_input_rows(nrows):
     """With row_index the input rows are x[row_index] (the logits-row gather,
     vllmlite/runner.py:90): the same bits as gathering first."""
     o = _ops()
@@ -198,8 +201,8 @@ def test_row_index_gathers_input_rows():
     x = torch.from_numpy(rng.standard_normal((40, 384)).astype(np.float32)).cuda()
     w = torch.from_numpy((0.05 * rng.standard_normal((384, 261))).astype(np.float32)).cuda()
     g = torch.from_numpy((1.0 + 0.1 * rng.standard_normal(384)).astype(np.float32)).cuda()
-    idx = torch.from_numpy(rng.integers(0, 40, 9).astype(np.int32)).cuda()
-    got = torch.empty((9, 261), device="cuda")
+    idx = torch.from_numpy(rng.integers(0, 40, nrows).astype(np.int32)).cuda()
+    got = torch.empty((nrows, 261), device="cuda")
     o.linear_rows(got, x, w, g, mode=o.LINEAR_STORE, row_index=idx)
     want = torch.empty_like(got)
     o.linear_rows(want, x[idx.long()].contiguous(), w, g, mode=o.LINEAR_STORE)

@@ -2,7 +2,8 @@
 // and the residual add or SwiGLU gate after them fused in
 // (vllmlite/model.py:96-101, 114, 116-117, 119-120). Built for few token rows
 // (the decode steps: at most 16, one row tile), and taking any number of rows
-// as 16-row tiles (the prefill steps), each tile re-reading the weights.
+// as 16-row tiles (the prefill steps); on large grids a workgroup takes 2 or 4
+// row tiles in turn, so that its weights serve all of them.
 //
 // One workgroup computes 16 rows x 16 output columns: its kLinWaves (8)
 // wavefronts split K into contiguous ranges on v_mfma_f32_16x16x4f32, each
@@ -91,7 +92,7 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
     float* __restrict__ out, int64_t ldo, const float* __restrict__ x, int64_t ldx,
     const float* __restrict__ w, int64_t ldw, int64_t up_off, const float* __restrict__ norm_w,
     float eps, int M, int K, int N, const RopeCache rc, const int32_t* __restrict__ row_index,
-    float* __restrict__ x_out) {
+    float* __restrict__ x_out, int nsub) {
   constexpr int kSlices = MODE == 2 ? 2 : 1;
   constexpr int KP = KMAX + 4;  // xs row stride: rows 4 words apart, so the
                                 // 16 rows x 4 k of an A read hit 64 banks
@@ -101,19 +102,6 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
   __shared__ float red[kSlices][kLinWaves][kRowsMax * kCols];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c0 = blockIdx.x * kCols;
-  // row tile blockIdx.y: rows r0 .. r0 + 15 of the M; every row index below
-  // counts from r0
-  const int r0 = blockIdx.y * kRowsMax;
-  M = min(kRowsMax, M - r0);
-  if (row_index)
-    row_index += r0;
-  else
-    x += (int64_t)r0 * ldx;
-  if constexpr (MODE != 3) out += (int64_t)r0 * ldo;
-  if (x_out) x_out += (int64_t)r0 * K;
-  const int32_t* positions = MODE == 3 ? rc.positions + r0 : nullptr;
-  const int32_t* slots = MODE == 3 ? rc.slots + r0 : nullptr;
-  float* q_out = MODE == 3 ? rc.q_out + (int64_t)r0 * rc.nh * rc.hd : nullptr;
   const int m = lane & 15, j = lane >> 4;
   // wavefront w takes the spw steps of 4 k from step w spw (k in [kb, kb + 4
   // nsteps)); the last wavefronts may have fewer steps, or none
@@ -131,28 +119,6 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
   // the compiler turn each load into a branch that waits for it.)
   float wb[kSlices][kSteps];
   const float colmask = c0 + m < N ? 1.f : 0.f;
-  // ---- the epilogue's own global reads, issued now so that they arrive with
-  // the weights instead of after the reduction: thread t writes row t / 16,
-  // column c0 + t % 16; the residual it adds to (MODE 1), or its slot and
-  // its RoPE table entries (MODE 3)
-  const int er = tid / kCols, ec = tid - (tid / kCols) * kCols;
-  const bool e_ok = er < M && c0 + ec < N;
-  float e_resid = 0.f, e_cos = 0.f, e_sin = 0.f;
-  int e_slot = -1;
-  if constexpr (MODE == 1) {
-    if (e_ok) e_resid = out[(int64_t)er * ldo + c0 + ec];
-  } else if constexpr (MODE == 3) {
-    if (e_ok) {
-      const int col = c0 + ec, qd = rc.nh * rc.hd, kd = rc.nkv * rc.hd;
-      e_slot = slots[er];
-      if (col < qd + kd) {
-        const int base = col < qd ? col : col - qd;
-        const int64_t tab = (int64_t)positions[er] * (rc.hd >> 1) + ((base % rc.hd) >> 1);
-        e_cos = rc.cos_t[tab];
-        e_sin = rc.sin_t[tab];
-      }
-    }
-  }
 #pragma unroll
   for (int s = 0; s < kSlices; ++s) {
     if constexpr (TILES) {
@@ -185,135 +151,192 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
 #pragma unroll
     for (int i = 0; i < KMAX / 64; ++i) gw[i] = norm_w[min(lane + 64 * i, K - 1)];
   }
-  // ---- x rows to LDS (rows >= M are zero): thread t < 256 takes row t / 16
-  // and float4 columns t % 16 + 16 u; row r is x[row_index[r]] when an index
-  // is given, and workgroup 0 copies the rows it read to x_out when given
-  if (tid < 16 * kRowsMax) {
-    const int r = tid >> 4, q = tid & 15;
-    const int kq = K / 4;
-    float4 xv[KMAX / 64];
-    const int rr = min(r, M - 1);
-    const float* xr = x + (int64_t)(row_index ? row_index[rr] : rr) * ldx;
-#pragma unroll
-    for (int u = 0; u < KMAX / 64; ++u) {
-      const int k4 = q + 16 * u;
-      const float z = r < M && k4 < kq ? 1.f : 0.f;  // rows past M, columns past K: 0
-      const float4 v = *reinterpret_cast<const float4*>(xr + 4 * min(k4, kq - 1));
-      xv[u] = make_float4(v.x * z, v.y * z, v.z * z, v.w * z);
+  const int er = tid / kCols, ec = tid - (tid / kCols) * kCols;
+  const int M_all = M;
+  // row tiles blockIdx.y nsub + t (t < nsub), rows r0 .. r0 + 15 each, one
+  // after the other on the weights already in registers; every row index
+  // below counts from the tile's r0. The barriers of each tile also order the
+  // previous tile's LDS reads (its A operands and reduction) before this
+  // tile's writes.
+  for (int t = 0; t < nsub; ++t) {
+    const int r0 = (blockIdx.y * nsub + t) * kRowsMax;
+    if (r0 >= M_all) break;  // uniform over the workgroup
+    M = min(kRowsMax, M_all - r0);
+    const int32_t* row_index_t = row_index ? row_index + r0 : nullptr;
+    const float* x_t = row_index ? x : x + (int64_t)r0 * ldx;
+    float* out_t = MODE != 3 ? out + (int64_t)r0 * ldo : out;
+    float* x_out_t = x_out ? x_out + (int64_t)r0 * K : nullptr;
+    const int32_t* positions = MODE == 3 ? rc.positions + r0 : nullptr;
+    const int32_t* slots = MODE == 3 ? rc.slots + r0 : nullptr;
+    float* q_out = MODE == 3 ? rc.q_out + (int64_t)r0 * rc.nh * rc.hd : nullptr;
+    // ---- the epilogue's own global reads, issued first so that they arrive
+    // with the rows instead of after the reduction: thread t writes row t / 16,
+    // column c0 + t % 16; the residual it adds to (MODE 1), or its slot and
+    // its RoPE table entries (MODE 3)
+    const bool e_ok = er < M && c0 + ec < N;
+    float e_resid = 0.f, e_cos = 0.f, e_sin = 0.f;
+    int e_slot = -1;
+    if constexpr (MODE == 1) {
+      if (e_ok) e_resid = out_t[(int64_t)er * ldo + c0 + ec];
+    } else if constexpr (MODE == 3) {
+      if (e_ok) {
+        const int col = c0 + ec, qd = rc.nh * rc.hd, kd = rc.nkv * rc.hd;
+        e_slot = slots[er];
+        if (col < qd + kd) {
+          const int base = col < qd ? col : col - qd;
+          const int64_t tab = (int64_t)positions[er] * (rc.hd >> 1) + ((base % rc.hd) >> 1);
+          e_cos = rc.cos_t[tab];
+          e_sin = rc.sin_t[tab];
+        }
+      }
     }
+    // ---- x rows to LDS (rows >= M are zero): thread t < 256 takes row t / 16
+    // and float4 columns t % 16 + 16 u; row r is x[row_index[r]] when an index
+    // is given, and workgroup 0 copies the rows it read to x_out when given
+    if (tid < 16 * kRowsMax) {
+      const int r = tid >> 4, q = tid & 15;
+      const int kq = K / 4;
+      float4 xv[KMAX / 64];
+      const int rr = min(r, M - 1);
+      const float* xr = x_t + (int64_t)(row_index_t ? row_index_t[rr] : rr) * ldx;
 #pragma unroll
-    for (int u = 0; u < KMAX / 64; ++u)
-      *reinterpret_cast<float4*>(&xs[r * KP + 4 * (q + 16 * u)]) = xv[u];
-    if (x_out && blockIdx.x == 0 && r < M) {
-#pragma unroll
-      for (int u = 0; u < KMAX / 64; ++u)
-        if (q + 16 * u < kq)
-          *reinterpret_cast<float4*>(x_out + (int64_t)r * K + 4 * (q + 16 * u)) = xv[u];
-    }
-  }
-  __syncthreads();
-
-  if constexpr (NORM) {
-    // rows r = wave, wave + kLinWaves, ...: the sum of squares over k = lane +
-    // 64 i in increasing i, then the wavefront sum, as rms_norm_kernel (the
-    // rows of a wavefront interleaved; columns past K hold zeros)
-    constexpr int kRq = kRowsMax / kLinWaves;
-    float ss[kRq];
-#pragma unroll
-    for (int q = 0; q < kRq; ++q) ss[q] = 0.f;
-#pragma unroll
-    for (int i = 0; i < KMAX / 64; ++i)
-#pragma unroll
-      for (int q = 0; q < kRq; ++q) {
-        const float a = xs[(wave + kLinWaves * q) * KP + lane + 64 * i];
-        ss[q] += a * a;
+      for (int u = 0; u < KMAX / 64; ++u) {
+        const int k4 = q + 16 * u;
+        const float z = r < M && k4 < kq ? 1.f : 0.f;  // rows past M, columns past K: 0
+        const float4 v = *reinterpret_cast<const float4*>(xr + 4 * min(k4, kq - 1));
+        xv[u] = make_float4(v.x * z, v.y * z, v.z * z, v.w * z);
       }
 #pragma unroll
-    for (int q = 0; q < kRq; ++q) {
-      const float rms = sqrtf(wave_sum(ss[q]) / (float)K + eps);
-      float* row = &xs[(wave + kLinWaves * q) * KP + lane];
+      for (int u = 0; u < KMAX / 64; ++u)
+        *reinterpret_cast<float4*>(&xs[r * KP + 4 * (q + 16 * u)]) = xv[u];
+      if (x_out_t && blockIdx.x == 0 && r < M) {
 #pragma unroll
-      for (int i = 0; i < KMAX / 64; ++i)
-        if (lane + 64 * i < K) row[64 * i] = (row[64 * i] / rms) * gw[i];
+        for (int u = 0; u < KMAX / 64; ++u)
+          if (q + 16 * u < kq)
+            *reinterpret_cast<float4*>(x_out_t + (int64_t)r * K + 4 * (q + 16 * u)) = xv[u];
+      }
     }
     __syncthreads();
-  }
 
-  // ---- lane l supplies A[l%16][l/16] and B[l/16][l%16] of each 16x16x4 step
-  // four independent accumulators per slice (steps i % 4), so consecutive
-  // MFMAs do not wait for each other's results
-  constexpr int kAcc = kSteps >= 4 ? 4 : 1;
-  f32x4_t acc4[kSlices][kAcc];
+    if constexpr (NORM) {
+      // rows r = wave, wave + kLinWaves, ...: the sum of squares over k = lane +
+      // 64 i in increasing i, then the wavefront sum, as rms_norm_kernel (the
+      // rows of a wavefront interleaved; columns past K hold zeros)
+      constexpr int kRq = kRowsMax / kLinWaves;
+      float ss[kRq];
 #pragma unroll
-  for (int s = 0; s < kSlices; ++s)
+      for (int q = 0; q < kRq; ++q) ss[q] = 0.f;
 #pragma unroll
-    for (int q = 0; q < kAcc; ++q) acc4[s][q] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-  const float* arow = &xs[m * KP + kb + j];
-  // all A reads first, then the MFMA chain (the reads of steps past this
-  // wavefront's nsteps stay inside the row, below KMAX, and meet zero weights)
-  float av[kSteps];
+      for (int i = 0; i < KMAX / 64; ++i)
 #pragma unroll
-  for (int i = 0; i < kSteps; ++i) av[i] = arow[4 * i];
+        for (int q = 0; q < kRq; ++q) {
+          const float a = xs[(wave + kLinWaves * q) * KP + lane + 64 * i];
+          ss[q] += a * a;
+        }
 #pragma unroll
-  for (int i = 0; i < kSteps; ++i)
+      for (int q = 0; q < kRq; ++q) {
+        const float rms = sqrtf(wave_sum(ss[q]) / (float)K + eps);
+        float* row = &xs[(wave + kLinWaves * q) * KP + lane];
+#pragma unroll
+        for (int i = 0; i < KMAX / 64; ++i)
+          if (lane + 64 * i < K) row[64 * i] = (row[64 * i] / rms) * gw[i];
+      }
+      __syncthreads();
+    }
+
+    // ---- lane l supplies A[l%16][l/16] and B[l/16][l%16] of each 16x16x4 step
+    // four independent accumulators per slice (steps i % 4), so consecutive
+    // MFMAs do not wait for each other's results
+    constexpr int kAcc = kSteps >= 4 ? 4 : 1;
+    f32x4_t acc4[kSlices][kAcc];
 #pragma unroll
     for (int s = 0; s < kSlices; ++s)
-      acc4[s][i % kAcc] =
-          __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], wb[s][i], acc4[s][i % kAcc], 0, 0, 0);
-  f32x4_t acc[kSlices];
 #pragma unroll
-  for (int s = 0; s < kSlices; ++s) {
-    acc[s] = acc4[s][0];
+      for (int q = 0; q < kAcc; ++q) acc4[s][q] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    const float* arow = &xs[m * KP + kb + j];
+    // all A reads first, then the MFMA chain (the reads of steps past this
+    // wavefront's nsteps stay inside the row, below KMAX, and meet zero weights)
+    float av[kSteps];
 #pragma unroll
-    for (int q = 1; q < kAcc; ++q) acc[s] += acc4[s][q];
-  }
-  // C layout: lane l holds rows 4(l/16) + i of column l%16
+    for (int i = 0; i < kSteps; ++i) av[i] = arow[4 * i];
 #pragma unroll
-  for (int s = 0; s < kSlices; ++s)
+    for (int i = 0; i < kSteps; ++i)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[s][wave][(4 * j + i) * kCols + m] = acc[s][i];
-  __syncthreads();
+      for (int s = 0; s < kSlices; ++s)
+        acc4[s][i % kAcc] =
+            __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], wb[s][i], acc4[s][i % kAcc], 0, 0, 0);
+    f32x4_t acc[kSlices];
+#pragma unroll
+    for (int s = 0; s < kSlices; ++s) {
+      acc[s] = acc4[s][0];
+#pragma unroll
+      for (int q = 1; q < kAcc; ++q) acc[s] += acc4[s][q];
+    }
+    // C layout: lane l holds rows 4(l/16) + i of column l%16
+#pragma unroll
+    for (int s = 0; s < kSlices; ++s)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[s][wave][(4 * j + i) * kCols + m] = acc[s][i];
+    __syncthreads();
 
-  const int r = er, c = ec;
-  if (!e_ok) return;
-  // the wavefronts' partial sums in wavefront order
-  auto total = [&](int s, int e) {
-    float t = red[s][0][e];
+    const int r = er, c = ec;
+    if (e_ok) {
+      // the wavefronts' partial sums in wavefront order
+      auto total = [&](int s, int e) {
+        float t = red[s][0][e];
 #pragma unroll
-    for (int q = 1; q < kLinWaves; ++q) t += red[s][q][e];
-    return t;
-  };
-  float v[kSlices];
+        for (int q = 1; q < kLinWaves; ++q) t += red[s][q][e];
+        return t;
+      };
+      float v[kSlices];
 #pragma unroll
-  for (int s = 0; s < kSlices; ++s) v[s] = total(s, tid);
-  if constexpr (MODE == 0) {
-    out[(int64_t)r * ldo + c0 + c] = v[0];
-  } else if constexpr (MODE == 1) {
-    out[(int64_t)r * ldo + c0 + c] = e_resid + v[0];
-  } else if constexpr (MODE == 2) {
-    out[(int64_t)r * ldo + c0 + c] = silu_times_f32(v[0], v[1]);
-  } else {
-    // the pair partner of column c is c ^ 1 in the same tile (head_dim even,
-    // tiles 16 columns)
-    const int pt = r * kCols + (c ^ 1);
-    const float partner = total(0, pt);
-    const int col = c0 + c, qd = rc.nh * rc.hd, kd = rc.nkv * rc.hd;
-    const int slot = e_slot;
-    if (col < qd + kd) {
-      const int base = col < qd ? col : col - qd;
-      const bool odd = (base % rc.hd) & 1;
-      float oe, oo;
-      rotate_pair_f32(odd ? partner : v[0], odd ? v[0] : partner, e_cos, e_sin, &oe, &oo);
-      const float val = odd ? oo : oe;
-      if (col < qd)
-        q_out[(int64_t)r * qd + col] = val;
-      else if (slot >= 0)
-        store_cache(rc.kc, rc.geom.at(slot, base / rc.hd) + base % rc.hd, val, rc.kv_dtype);
-    } else if (slot >= 0) {
-      const int vcol = col - qd - kd;
-      store_cache(rc.vc, rc.geom.at(slot, vcol / rc.hd) + vcol % rc.hd, v[0], rc.kv_dtype);
+      for (int s = 0; s < kSlices; ++s) v[s] = total(s, tid);
+      if constexpr (MODE == 0) {
+        out_t[(int64_t)r * ldo + c0 + c] = v[0];
+      } else if constexpr (MODE == 1) {
+        out_t[(int64_t)r * ldo + c0 + c] = e_resid + v[0];
+      } else if constexpr (MODE == 2) {
+        out_t[(int64_t)r * ldo + c0 + c] = silu_times_f32(v[0], v[1]);
+      } else {
+        // the pair partner of column c is c ^ 1 in the same tile (head_dim even,
+        // tiles 16 columns)
+        const int pt = r * kCols + (c ^ 1);
+        const float partner = total(0, pt);
+        const int col = c0 + c, qd = rc.nh * rc.hd, kd = rc.nkv * rc.hd;
+        const int slot = e_slot;
+        if (col < qd + kd) {
+          const int base = col < qd ? col : col - qd;
+          const bool odd = (base % rc.hd) & 1;
+          float oe, oo;
+          rotate_pair_f32(odd ? partner : v[0], odd ? v[0] : partner, e_cos, e_sin, &oe, &oo);
+          const float val = odd ? oo : oe;
+          if (col < qd)
+            q_out[(int64_t)r * qd + col] = val;
+          else if (slot >= 0)
+            store_cache(rc.kc, rc.geom.at(slot, base / rc.hd) + base % rc.hd, val, rc.kv_dtype);
+        } else if (slot >= 0) {
+          const int vcol = col - qd - kd;
+          store_cache(rc.vc, rc.geom.at(slot, vcol / rc.hd) + vcol % rc.hd, v[0], rc.kv_dtype);
+        }
+      }
     }
   }
+}
+
+#ifndef VL_LIN_SUB_MAX
+#define VL_LIN_SUB_MAX 4
+#endif
+// Row tiles per workgroup: 1 while the grid is at most one round of two
+// workgroups per CU (the kernel is latency-bound there, so tiles run side by
+// side); beyond that doubled, up to VL_LIN_SUB_MAX, while the grid keeps at
+// least that round, so that each workgroup's weight tile serves more rows.
+inline int rows_per_workgroup(int ntile, int row_tiles) {
+  const int64_t round = 2 * (int64_t)vl_num_cus();
+  int nsub = 1;
+  while (nsub < VL_LIN_SUB_MAX &&
+         (int64_t)ntile * ((row_tiles + 2 * nsub - 1) / (2 * nsub)) >= round)
+    nsub *= 2;
+  return nsub;
 }
 
 template <int MODE, bool NORM, int KMAX>
@@ -321,15 +344,17 @@ int launch(float* out, int64_t ldo, const float* x, int64_t ldx, const float* w,
            bool tiles, const float* norm_w, float eps, int M, int K, int N, hipStream_t st,
            const int32_t* row_index, const RopeCache& rc = RopeCache{}, float* x_out = nullptr) {
   const int ntile = (N + kCols - 1) / kCols;
-  const dim3 grid(ntile, (M + kRowsMax - 1) / kRowsMax);
+  const int row_tiles = (M + kRowsMax - 1) / kRowsMax;
+  const int nsub = rows_per_workgroup(ntile, row_tiles);
+  const dim3 grid(ntile, (row_tiles + nsub - 1) / nsub);
   if (tiles) {
     const int64_t up_off = MODE == 2 ? (int64_t)ntile * K * kCols : 0;
     linear_rows_kernel<MODE, NORM, KMAX, true><<<grid, 64 * kLinWaves, 0, st>>>(
-        out, ldo, x, ldx, w, 0, up_off, norm_w, eps, M, K, N, rc, row_index, x_out);
+        out, ldo, x, ldx, w, 0, up_off, norm_w, eps, M, K, N, rc, row_index, x_out, nsub);
   } else {
     const int64_t up_off = MODE == 2 ? N : 0;
     linear_rows_kernel<MODE, NORM, KMAX, false><<<grid, 64 * kLinWaves, 0, st>>>(
-        out, ldo, x, ldx, w, ldw, up_off, norm_w, eps, M, K, N, rc, row_index, x_out);
+        out, ldo, x, ldx, w, ldw, up_off, norm_w, eps, M, K, N, rc, row_index, x_out, nsub);
   }
   VL_CHECK_LAUNCH();
   return VL_OK;
