@@ -109,6 +109,34 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
   const int spw = ((K / 4 + kLinWaves - 1) / kLinWaves + 3) / 4 * 4;
   const int kb = wave * spw * 4;
   const int nsteps = max(0, min(spw, K / 4 - wave * spw));
+  // ---- the epilogue's own global reads for the row tile at r0, issued early
+  // so that they arrive with the weights (tile 0) or the rows instead of
+  // after the reduction: thread t writes row t / 16, column c0 + t % 16; the
+  // residual it adds to (MODE 1), or its slot and its RoPE table entries
+  // (MODE 3)
+  const int er = tid / kCols, ec = tid - (tid / kCols) * kCols;
+  const int M_all = M;  // M is the current tile's row count from here on
+  float e_resid = 0.f, e_cos = 0.f, e_sin = 0.f;
+  int e_slot = -1;
+  auto epilogue_reads = [&](int r0) {
+    const bool ok = er < min(kRowsMax, M_all - r0) && c0 + ec < N;
+    if constexpr (MODE == 1) {
+      if (ok) e_resid = out[(int64_t)(r0 + er) * ldo + c0 + ec];
+    } else if constexpr (MODE == 3) {
+      if (ok) {
+        const int col = c0 + ec, qd = rc.nh * rc.hd, kd = rc.nkv * rc.hd;
+        e_slot = rc.slots[r0 + er];
+        if (col < qd + kd) {
+          const int base = col < qd ? col : col - qd;
+          const int64_t tab =
+              (int64_t)rc.positions[r0 + er] * (rc.hd >> 1) + ((base % rc.hd) >> 1);
+          e_cos = rc.cos_t[tab];
+          e_sin = rc.sin_t[tab];
+        }
+      }
+    }
+  };
+  epilogue_reads(blockIdx.y * nsub * kRowsMax);
 
   // ---- the B operand straight into registers: step i of wavefront w needs
   // w[kb + 4i + l/16][c0 + l%16] in lane l (columns past the end read 0);
@@ -151,8 +179,6 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
 #pragma unroll
     for (int i = 0; i < KMAX / 64; ++i) gw[i] = norm_w[min(lane + 64 * i, K - 1)];
   }
-  const int er = tid / kCols, ec = tid - (tid / kCols) * kCols;
-  const int M_all = M;
   // row tiles blockIdx.y nsub + t (t < nsub), rows r0 .. r0 + 15 each, one
   // after the other on the weights already in registers; every row index
   // below counts from the tile's r0. The barriers of each tile also order the
@@ -166,30 +192,9 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
     const float* x_t = row_index ? x : x + (int64_t)r0 * ldx;
     float* out_t = MODE != 3 ? out + (int64_t)r0 * ldo : out;
     float* x_out_t = x_out ? x_out + (int64_t)r0 * K : nullptr;
-    const int32_t* positions = MODE == 3 ? rc.positions + r0 : nullptr;
-    const int32_t* slots = MODE == 3 ? rc.slots + r0 : nullptr;
     float* q_out = MODE == 3 ? rc.q_out + (int64_t)r0 * rc.nh * rc.hd : nullptr;
-    // ---- the epilogue's own global reads, issued first so that they arrive
-    // with the rows instead of after the reduction: thread t writes row t / 16,
-    // column c0 + t % 16; the residual it adds to (MODE 1), or its slot and
-    // its RoPE table entries (MODE 3)
+    if (t > 0) epilogue_reads(r0);
     const bool e_ok = er < M && c0 + ec < N;
-    float e_resid = 0.f, e_cos = 0.f, e_sin = 0.f;
-    int e_slot = -1;
-    if constexpr (MODE == 1) {
-      if (e_ok) e_resid = out_t[(int64_t)er * ldo + c0 + ec];
-    } else if constexpr (MODE == 3) {
-      if (e_ok) {
-        const int col = c0 + ec, qd = rc.nh * rc.hd, kd = rc.nkv * rc.hd;
-        e_slot = slots[er];
-        if (col < qd + kd) {
-          const int base = col < qd ? col : col - qd;
-          const int64_t tab = (int64_t)positions[er] * (rc.hd >> 1) + ((base % rc.hd) >> 1);
-          e_cos = rc.cos_t[tab];
-          e_sin = rc.sin_t[tab];
-        }
-      }
-    }
     // ---- x rows to LDS (rows >= M are zero): thread t < 256 takes row t / 16
     // and float4 columns t % 16 + 16 u; row r is x[row_index[r]] when an index
     // is given, and workgroup 0 copies the rows it read to x_out when given
