@@ -28,6 +28,15 @@ Outputs (small JSON, committed):
                       parents and children, step count, and the number of CoW
                       pairs with the prompt lengths whose tails were partial
                       ("forked").
+  sampling_choices.json
+                      seeded draws of the reference's sample()
+                      (vllmlite/sampling.py:41-64) on rows of 64 logits taken
+                      from a few values, so that ties are common, under a grid
+                      of temperature / top_k / top_p / repetition penalty /
+                      min_tokens settings: the row, the settings, the seed
+                      and three successive draws from one generator.
+
+`python tests/golden/make_golden.py sampling` writes only the last file.
 """
 
 from __future__ import annotations
@@ -46,6 +55,7 @@ sys.path.insert(0, REF)
 from vllmlite.config import CacheConfig, EngineConfig, ModelConfig, SchedulerConfig  # noqa: E402
 from vllmlite.engine import LLMEngine, _Detok  # noqa: E402
 from vllmlite.model import Layer, TinyLlama  # noqa: E402
+from vllmlite.sampling import sample  # noqa: E402
 from vllmlite.sequence import SamplingParams, Sequence  # noqa: E402
 from bench.bench import make_workload  # noqa: E402
 
@@ -167,7 +177,36 @@ def shared_prefix_runs():
     return out
 
 
+def sampling_cases():
+    rng = np.random.default_rng(7)
+    cases = []
+    for temperature in (0.0, 0.7, 1.0, 1.3):
+        for top_k in (0, 5, 20):
+            for top_p in (1.0, 0.9, 0.5):
+                for pen in (1.0, 1.3):
+                    row = (rng.integers(-4, 5, 64) * 0.5).astype(np.float32)
+                    seen = [int(t) for t in rng.integers(0, 64, 6)]
+                    min_tokens = int(rng.integers(0, 3))
+                    num_generated = int(rng.integers(0, 3))
+                    seed = int(rng.integers(0, 2 ** 31))
+                    params = SamplingParams(temperature=temperature, top_k=top_k, top_p=top_p,
+                                            repetition_penalty=pen, min_tokens=min_tokens,
+                                            seed=seed)
+                    g = np.random.default_rng(seed)
+                    draws = [sample(row, params, seen, g, num_generated, 2) for _ in range(3)]
+                    cases.append({"row": [float(x) for x in row], "temperature": temperature,
+                                  "top_k": top_k, "top_p": top_p, "repetition_penalty": pen,
+                                  "min_tokens": min_tokens, "num_generated": num_generated,
+                                  "eos_id": 2, "seen": seen, "seed": seed,
+                                  "draws": [int(t) for t in draws]})
+    return cases
+
+
 def main():
+    if sys.argv[1:] == ["sampling"]:
+        with open(os.path.join(HERE, "sampling_choices.json"), "w") as f:
+            json.dump({"cases": sampling_cases()}, f)
+        return
     mc = ModelConfig(n_layers=6, n_heads=8, n_kv_heads=4, d_model=384, d_ff=1024,
                      vocab_size=261, max_seq_len=512)
     cc = CacheConfig(block_size=16, num_blocks=512, enable_prefix_caching=False)
@@ -204,6 +243,8 @@ def main():
     print("shared prefix: plain", sp["plain"]["steps"], "steps,", sp["plain"]["output_tokens"],
           "tokens; forked", sp["forked"]["steps"], "steps,", sp["forked"]["cow_pairs"], "CoW pairs,",
           sp["forked"]["preemptions"], "preemptions")
+    with open(os.path.join(HERE, "sampling_choices.json"), "w") as f:
+        json.dump({"cases": sampling_cases()}, f)
     print("wrote fixtures; cfg0 steps", eng.total_steps,
           "min margin", min(min(v) for v in margins.values() if v))
 

@@ -11,6 +11,7 @@ import pytest
 
 from oracle.runner import NumpyRunner
 from vllmlite_amd.request import SamplingParams
+from vllmlite_amd.sampling import choose
 
 from helpers import PROMPTS, build, run
 
@@ -151,6 +152,28 @@ def test_seeded_sampling_is_reproducible():
     while b.has_work:
         b.step()
     assert a.seqs[ra].output_token_ids == b.seqs[rb].output_token_ids
+
+
+def test_sampling_matches_reference_draws():
+    """`choose` against the reference's sample() (vllmlite/sampling.py:41-64):
+    72 rows whose logits take a few values (ties in most rows), over
+    temperature 0/0.7/1/1.3, top_k 0/5/20, top_p 1/0.9/0.5, repetition
+    penalty 1/1.3 and the min_tokens EOS mask; three successive draws from
+    one seeded generator each, written by the reference
+    (tests/golden/make_golden.py)."""
+    with open(os.path.join(os.path.dirname(__file__), "golden", "sampling_choices.json")) as f:
+        cases = json.load(f)["cases"]
+    ties = 0
+    for c in cases:
+        row = np.array(c["row"], np.float32)
+        ties += len(np.unique(row)) < row.size
+        p = SamplingParams(temperature=c["temperature"], top_k=c["top_k"], top_p=c["top_p"],
+                           repetition_penalty=c["repetition_penalty"],
+                           min_tokens=c["min_tokens"], seed=c["seed"])
+        g = np.random.default_rng(c["seed"])
+        got = [choose(row, p, c["seen"], g, c["num_generated"], c["eos_id"]) for _ in range(3)]
+        assert got == c["draws"], c
+    assert ties == len(cases)
 
 
 def test_empty_token_list_rejected():

@@ -146,3 +146,96 @@ def test_fork_refuses_while_a_step_is_in_flight():
     eng.step()
     with pytest.raises(RuntimeError):
         eng.fork_request(rid, "kid")
+
+
+def _reports(outs):
+    """Per request: every token reported, and each finished report's
+    (reason, token_ids)."""
+    toks, fins = {}, {}
+    for o in outs:
+        assert all(t >= 0 for t in o.token_ids), o  # no placeholder leaks out
+        toks.setdefault(o.request_id, []).extend(o.new_token_ids)
+        if o.finished:
+            fins.setdefault(o.request_id, []).append((o.finish_reason, list(o.token_ids)))
+    return toks, fins
+
+
+def _drive_with_abort(lookahead, victim_params, abort_after, check):
+    """Request a (greedy, ignore_eos) runs; request b joins after two steps;
+    b is aborted after `abort_after` more calls; both engines see the same
+    sequence of calls."""
+    cfg = small_cfg()
+    eng = LLMEngine(cfg, runner=_LaunchingRunner(cfg.model, cfg.cache), lookahead=lookahead)
+    greedy = SamplingParams(max_tokens=12, temperature=0.0, ignore_eos=True)
+    outs = []
+    eng.add_request(PROMPTS[0], greedy, request_id="a")
+    outs += eng.step()
+    outs += eng.step()
+    eng.add_request(PROMPTS[1], victim_params, request_id="b")
+    for _ in range(abort_after):
+        outs += eng.step()
+    if lookahead:
+        check(eng)
+    assert eng.abort("b")
+    while eng.has_work:
+        outs += eng.step()
+        assert eng.batcher.pool.audit()
+    return eng, outs
+
+
+def test_abort_of_a_request_held_for_a_synchronous_step():
+    """A sampled request joins while a greedy step is in flight: the next batch
+    is held for a synchronous step; aborting the sampled request before that
+    step drops it from the held batch (its blocks are already free)."""
+    sampled = SamplingParams(max_tokens=12, temperature=0.7, seed=5, ignore_eos=True)
+    runs = [_drive_with_abort(la, sampled, 1, lambda e: e._next is not None and any(
+        i.seq.request_id == "b" for i in e._next.scheduled)) for la in (True, False)]
+    (eng, outs), (ref, ref_outs) = runs
+    assert eng.seqs["a"].output_token_ids == ref.seqs["a"].output_token_ids
+    toks, fins = _reports(outs)
+    rfins = _reports(ref_outs)[1]
+    assert fins["a"] == rfins["a"]
+    assert toks["a"] == eng.seqs["a"].output_token_ids
+    # b never ran under lookahead (its first step was the held one); the
+    # synchronous engine had run its prefill by the same call
+    assert fins["b"] == [("abort", [])] and rfins["b"][0][0] == "abort"
+
+
+@pytest.mark.parametrize("abort_after", [1, 2, 3])
+def test_abort_while_its_step_is_in_flight(abort_after):
+    """Aborting a greedy request whose step is on the device: its in-flight
+    token is reported (as synchronous stepping reported it before the abort),
+    then one finished report with the real ids and reason "abort"."""
+    greedy = SamplingParams(max_tokens=12, temperature=0.0, ignore_eos=True)
+    eng, outs = _drive_with_abort(True, greedy, abort_after, lambda e: e._inflight is not None)
+    ref, ref_outs = _drive_with_abort(False, greedy, abort_after, lambda e: None)
+    toks, fins = _reports(outs)
+    rtoks, rfins = _reports(ref_outs)
+    assert len(fins["b"]) == 1 and fins["b"][0][0] == "abort"
+    assert fins["b"][0][1] == eng.seqs["b"].output_token_ids == toks["b"]
+    assert eng.seqs["a"].output_token_ids == ref.seqs["a"].output_token_ids == toks["a"]
+    assert fins["a"] == rfins["a"]
+    # the looked-ahead engine has one more step of b on the device when the
+    # abort lands; what it reports of b is a prefix of b's greedy stream
+    assert rtoks["b"] == toks["b"][:len(rtoks["b"])]
+
+
+def test_cache_full_retirement_under_lookahead():
+    """A request that outgrows a 4-block cache is retired "cache_full" by the
+    schedule that follows its in-flight step: one finished report, after the
+    in-flight token, with real ids, as synchronous stepping gives."""
+    got = []
+    for lookahead in (True, False):
+        cfg = small_cfg(block_size=4, num_blocks=4)
+        eng = LLMEngine(cfg, runner=_LaunchingRunner(cfg.model, cfg.cache), lookahead=lookahead)
+        eng.add_request(params=SamplingParams(max_tokens=64, temperature=0.0, ignore_eos=True),
+                        request_id="r", prompt_token_ids=[1, 72, 101, 108, 108])
+        outs = []
+        while eng.has_work:
+            outs += eng.step()
+        if lookahead:
+            assert eng.runner.placeholders > 0
+        got.append(_reports(outs))
+    assert got[0] == got[1]
+    fins = got[0][1]["r"]
+    assert len(fins) == 1 and fins[0][0] == "cache_full"

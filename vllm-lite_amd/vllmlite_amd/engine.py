@@ -176,8 +176,20 @@ class LLMEngine:
     def _schedule(self) -> StepBatch:
         if self._next is not None:
             batch, self._next = self._next, None
-            return batch
+            return self._drop_retired(batch)
         return self.batcher.schedule()
+
+    @staticmethod
+    def _drop_retired(batch: StepBatch) -> StepBatch:
+        """A batch held since the previous call loses the requests retired in
+        between (abort): their blocks went back to the pool, and so do the
+        copy-on-write pairs whose destination was one of them."""
+        if all(not item.seq.status.finished for item in batch.scheduled):
+            return batch
+        batch.scheduled = [i for i in batch.scheduled if not i.seq.status.finished]
+        owned = {b for i in batch.scheduled for b in i.seq.table.block_ids}
+        batch.cow = [(s, d) for s, d in batch.cow if d in owned]
+        return batch
 
     def step(self) -> List[RequestOutput]:
         b = self.batcher
@@ -193,7 +205,10 @@ class LLMEngine:
             outs = []
         # step n is on the device and advanced on the host: schedule n + 1
         nxt = self.batcher.schedule()
-        outs += [self._finished_output(r) for r in b.drain_reports()]
+        # requests retired since step n was launched (aborted between calls,
+        # or out of cache in this schedule) may hold one of its placeholders:
+        # they are reported once the ids are in place, after step n's outputs
+        retired = b.drain_reports()
         following = None
         if nxt.scheduled and self._lookahead_ok(nxt):
             following = self._launch(nxt)
@@ -202,6 +217,7 @@ class LLMEngine:
         # step n's tokens replace its placeholders before step n + 1's outcome
         # is applied (publishing a block reads the tokens in it)
         outs += self._finish_launched(self._inflight)
+        outs += [self._finished_output(r) for r in retired]
         self._inflight = self._advance(following) if following is not None else None
         return outs
 
@@ -233,7 +249,10 @@ class LLMEngine:
                 req.finish(Status.FINISHED_LENGTH, "length")
             if req.status.finished:
                 b.finish(req)
-            emitted.append((req, len(req.ids) - 1, row0 + count - 1))
+            # the output reports the request as this step left it: a later
+            # retirement (abort, cache_full) is reported on its own afterwards
+            emitted.append((req, len(req.ids) - 1, row0 + count - 1,
+                            req.status.finished, req.stop_reason))
         return batch, handle, emitted
 
     def _finish_launched(self, inflight) -> List[RequestOutput]:
@@ -244,12 +263,14 @@ class LLMEngine:
         picks, _ = self.runner.collect(handle)
         self.busy_time += time.perf_counter() - t0
         outs = []
-        for req, pos, row in emitted:
+        for req, pos, row, finished, reason in emitted:
             tok = int(picks[row])
             req.ids[pos] = tok
             # a request preempted since holds its tokens; others also wait for
             # the next step's placeholder
-            outs.append(self._output(req, [tok], self._detok(req, [tok])))
+            out = self._output(req, [tok], self._detok(req, [tok]))
+            out.finished, out.finish_reason = finished, reason if finished else None
+            outs.append(out)
         return outs
 
     def _run_sync(self, batch: StepBatch) -> List[RequestOutput]:

@@ -6,14 +6,21 @@ seen divided (if positive) or multiplied (if not) by the repetition penalty;
 temperature 0 takes the argmax (ties to the lowest index); otherwise the
 logits are divided by the temperature, cut to the top_k largest (top_k > 0),
 cut to the smallest set of most probable tokens whose probability reaches
-top_p (the token that crosses top_p kept), and one token is drawn from the
-renormalised distribution with the request's own generator (inverse CDF on
-one uniform draw).
+top_p (the token that crosses top_p kept; ranks from NumPy's default argsort
+of the negated logits, so tied logits rank as the reference ranks them), and
+one token is drawn from the renormalised distribution by the request's own
+generator through `Generator.choice`, which consumes it as the reference's
+draw does: the same seed gives the same tokens.
 """
 
 from __future__ import annotations
 
 import numpy as np
+
+
+def _softmax(x: np.ndarray) -> np.ndarray:
+    e = np.exp(x - x.max())
+    return e / e.sum()
 
 
 def choose(row: np.ndarray, params, seen, rng: np.random.Generator, num_generated: int,
@@ -31,17 +38,10 @@ def choose(row: np.ndarray, params, seen, rng: np.random.Generator, num_generate
     x /= params.temperature
     k = params.top_k
     if 0 < k < x.size:
-        x[x < np.partition(x, x.size - k)[x.size - k]] = -np.inf
-    p = np.exp(x - x.max())
-    p /= p.sum()
+        x[x < np.partition(x, -k)[-k]] = -np.inf
     if params.top_p < 1.0:
-        order = np.argsort(-x, kind="stable")
-        ranked = p[order]
-        before = np.cumsum(ranked) - ranked  # probability mass ranked ahead of each token
-        p = np.zeros_like(p)
-        keep = order[before < params.top_p]
-        p[keep] = ranked[before < params.top_p]
-        p /= p.sum()
-    cdf = np.cumsum(p, dtype=np.float64)
-    i = int(np.searchsorted(cdf, rng.random() * cdf[-1], side="right"))
-    return min(i, x.size - 1)
+        ranked = np.argsort(-x)
+        w = _softmax(x[ranked])
+        # mass ranked strictly ahead of each token; the one crossing top_p stays
+        x[ranked[np.cumsum(w) - w >= params.top_p]] = -np.inf
+    return int(rng.choice(x.size, p=_softmax(x)))
