@@ -309,6 +309,54 @@ int vl_greedy_verify(const float* logits, int64_t row_stride, int vocab, const i
 int vl_argmax_rows(const float* logits, int64_t row_stride, int64_t rows, int vocab, int32_t* out,
                    int32_t* out2, void* stream);
 
+/*
+ * K7 one decode step of the TinyLlama forward in one launch
+ * (vllmlite/model.py:80-120 over the batch vllmlite/runner.py:62-100 builds
+ * when every scheduled sequence pushes one token, then the greedy argmax of
+ * vllmlite/sampling.py:56-57 on each logits row). Row r (r < 16) is sequence
+ * r: token token_ids[r] (t < 0 stands for prev_ids[-t - 1], the id the
+ * previous step chose for its row -t - 1) at positions[r], its K/V written
+ * to slot_mapping[r] (< 0: none) and seq_lens[r] tokens of context through
+ * block_tables[r, :] (r >= num_seqs, or seq_lens[r] == 0: a padding row,
+ * whose outputs are unspecified). Per layer: RMSNorm, QKV, RoPE, the K/V
+ * scatter, paged attention, x += attn @ wo, RMSNorm, SwiGLU, x += act @
+ * w_down; then the final RMSNorm and lm_head: logits [16, vocab], and the
+ * argmax of every row (numpy's rule) into out_ids[16] and out_ids_host[16]
+ * (pinned host memory). out_ids_host[16] is left as the caller set it (0)
+ * when the launch was good, else set to 1 (a wait between the step's phases
+ * ran out) or 2 (the step's workgroups were not all on one XCD): the
+ * results are then invalid. Every result equals what this library's
+ * separate kernels compute for the step (vl_qkv_rope_cache,
+ * vl_paged_attention, vl_linear_rows, vl_argmax_rows).
+ *
+ * layer_weights: device array of n_layers x 6 device addresses: attn_norm
+ * [d], the fused QKV weight, wo, ffn_norm [d], the fused gate|up weight and
+ * w_down, each weight in the 16-column tile layout of VL_WEIGHT_TILES16
+ * ([ceil(n/16), k, 16]; gate|up: the gate tiles, then the up tiles); lm_head
+ * likewise. Caches [n_layers] x layer_stride elements of kv_dtype
+ * (VL_DTYPE_F32, _BF16 or _FP8_E4M3, written rounded to nearest even) in
+ * kv_layout, a layer under 2 GiB. x, q, attn, act: fp32 [16, d], [16, d],
+ * [16, d], [16, d_ff] rows the launch exchanges between its phases; sync:
+ * 128 uint32 words, 128-byte aligned, zero before the first launch (every
+ * launch leaves them so); launches sharing sync words or row buffers must not
+ * overlap. vl_decode_step_supported says which shapes have a kernel (today:
+ * head_dim 16 or 48, 2 query heads per KV head, d_model <= 384 a multiple
+ * of 64, d_ff <= 1024 a multiple of 16, context <= 2048).
+ */
+int vl_decode_step_supported(int d_model, int num_heads, int num_kv_heads, int d_ff, int kv_dtype,
+                             int max_context);
+int vl_decode_step(const void* layer_weights, int n_layers, const float* tok_emb,
+                   const float* final_norm, const float* lm_head, void* key_cache,
+                   void* value_cache, int64_t layer_stride, int kv_dtype, int kv_layout,
+                   const int32_t* token_ids, const int32_t* positions,
+                   const int32_t* slot_mapping, const int32_t* seq_lens,
+                   const int32_t* block_tables, int block_table_stride, int num_seqs,
+                   const int32_t* prev_ids, int num_prev, const float* cos_table,
+                   const float* sin_table, int d_model, int num_heads, int num_kv_heads,
+                   int d_ff, int vocab, int block_size, int max_context, float scale, float eps,
+                   float* x, float* q, float* attn, float* act, float* logits, int32_t* out_ids,
+                   int32_t* out_ids_host, uint32_t* sync, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

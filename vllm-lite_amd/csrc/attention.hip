@@ -688,10 +688,6 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 
-// 2^x by the hardware's v_exp_f32 (about 1 ulp; results below 2^-126 may
-// flush to zero, far below a softmax row sum's fp32 resolution). exp2f adds
-// a range reduction for denormal results that costs six more VALU ops.
-__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Two floats to packed bf16 with the hardware conversion (v_cvt_pk_bf16_f32,
 // round to nearest even, as f32_to_bf16 for every finite value).
@@ -1298,11 +1294,6 @@ __device__ __forceinline__ float stride4_sum(float v) {
   return v;
 }
 
-// DPP lane exchange (update_dpp with `old` kept where the row mask excludes
-// the lane).
-#define VL_DPP(old, v, ctrl, rmask)                                                     \
-  __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), ctrl, \
-                                             rmask, 0xF, false))
 
 // Transposing sum over each row of 16 lanes: lane c (= lane & 15) holds 16
 // partial values v[0..15]; afterwards it returns the row's total of v[c].
@@ -1812,47 +1803,8 @@ struct ShortLds {
   int32_t tbl[kShortCtx];   // the sequence's block ids
 };
 
-// Max / sum over the 64 lanes of a wavefront by DPP: within each row of 16
-// (quad xor 1, xor 2, half-row mirror, row mirror), then row 0 into 1 and 2
-// into 3 (row_bcast:15), row 1 into 2 and 3 (row_bcast:31); lane 63 holds the
-// result, which every lane reads back.
-__device__ __forceinline__ float wave_max_dpp(float v) {
-  v = fmaxf(v, VL_DPP(v, v, 0xB1, 0xF));
-  v = fmaxf(v, VL_DPP(v, v, 0x4E, 0xF));
-  v = fmaxf(v, VL_DPP(v, v, 0x141, 0xF));
-  v = fmaxf(v, VL_DPP(v, v, 0x140, 0xF));
-  v = fmaxf(v, VL_DPP(v, v, 0x142, 0xA));
-  v = fmaxf(v, VL_DPP(v, v, 0x143, 0xC));
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-  v += VL_DPP(0.f, v, 0xB1, 0xF);
-  v += VL_DPP(0.f, v, 0x4E, 0xF);
-  v += VL_DPP(0.f, v, 0x141, 0xF);
-  v += VL_DPP(0.f, v, 0x140, 0xF);
-  v += VL_DPP(0.f, v, 0x142, 0xA);
-  v += VL_DPP(0.f, v, 0x143, 0xC);
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
 
-// 16 bytes of T (fp32, bf16 bits or FP8 E4M3 bytes) as floats
-template <typename T>
-__device__ __forceinline__ void widen16(const uint4& v, float* r) {
-  if constexpr (sizeof(T) == 4) {
-    r[0] = __uint_as_float(v.x), r[1] = __uint_as_float(v.y);
-    r[2] = __uint_as_float(v.z), r[3] = __uint_as_float(v.w);
-  } else if constexpr (sizeof(T) == 1) {
-    e4m3x4_to_f32(v.x, r), e4m3x4_to_f32(v.y, r + 4);
-    e4m3x4_to_f32(v.z, r + 8), e4m3x4_to_f32(v.w, r + 12);
-  } else {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      r[2 * e] = __uint_as_float(w[e] << 16);
-      r[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
-    }
-  }
-}
+
 
 // A head row of D elements of T as floats (16-byte loads).
 template <typename T, int D>
@@ -1929,12 +1881,12 @@ __global__ void __launch_bounds__(256) attend_short_decode_kernel(
     for (int h = 0; h < REP; ++h) {
       float a = 0.f;
 #pragma unroll
-      for (int d = 0; d < D; ++d) a += s.q[h][d] * kr[d];
+      for (int d = 0; d < D; ++d) a = __builtin_fmaf(s.q[h][d], kr[d], a);
       const float sc = valid ? a : -__builtin_inff();
       const float mn = fmaxf(m[h], wave_max_dpp(sc));  // finite: key base is valid
       const float alpha = exp2_fast(m[h] - mn);
       const float p = exp2_fast(sc - mn);
-      lsum[h] = lsum[h] * alpha + p;
+      lsum[h] = __builtin_fmaf(lsum[h], alpha, p);
 #pragma unroll
       for (int e = 0; e < VE; ++e) acc[h][e] *= alpha;
       m[h] = mn;
@@ -1953,7 +1905,7 @@ __global__ void __launch_bounds__(256) attend_short_decode_kernel(
       for (int h = 0; h < REP; ++h) {
         const float w = kk < 64 ? s.p[wave][h][kk] : 0.f;
 #pragma unroll
-        for (int e = 0; e < VE; ++e) acc[h][e] += w * v[e];
+        for (int e = 0; e < VE; ++e) acc[h][e] = __builtin_fmaf(w, v[e], acc[h][e]);
       }
     }
     // the weights have been read before the next chunk overwrites them
@@ -1989,8 +1941,8 @@ __global__ void __launch_bounds__(256) attend_short_decode_kernel(
         float sw = 0.f;
 #pragma unroll
         for (int gg = 0; gg < G; ++gg) sw += s.red[w][gg * NC + dc][de];
-        L += s.l[w][h] * wt;
-        a += sw * wt;
+        L = __builtin_fmaf(s.l[w][h], wt, L);
+        a = __builtin_fmaf(sw, wt, a);
       }
       Elem<T>::store(out, ((int64_t)tok * H + g * REP + h) * D + d, L > 0.f ? a * (1.f / L) : 0.f);
     }

@@ -1,0 +1,940 @@
+// K7 one TinyLlama decode step in one launch, on the compute units of one XCD
+// (vllmlite/model.py:80-120 over the batch vllmlite/runner.py:62-100 builds
+// when every scheduled sequence pushes one token): the embedding gather, per
+// layer RMSNorm + QKV + RoPE + K/V scatter, paged attention over each
+// sequence's context, x += attn @ wo, RMSNorm + gate|up + SwiGLU,
+// x += act @ w_down; then the final RMSNorm, lm_head and the argmax of every
+// row, written to device memory and to the caller's pinned host buffer.
+//
+// Why one XCD. A decode step of the 6-layer model is ~30 small dependent
+// phases. As separate launches each costs 4-7 us, mostly the launch and the
+// cache maintenance between kernels; a persistent grid spread over all 8 XCDs
+// pays as much per phase, since data and barriers must then pass through
+// memory beyond the XCDs' own L2 caches. Workgroups are dispatched to the XCDs
+// round-robin (workgroup b runs on XCD (s + b) % 8, s where the dispatcher's
+// rotation stands when the launch begins), so a grid of 8 * NW workgroups of
+// which only those with b % 8 == 0 stay puts NW workgroups on one XCD,
+// where they share one L2: a barrier and the exchange of a phase's results
+// (16 rows of 384 floats) then cost ~1.7 us.
+//
+// Protocol between the workgroups of the launch:
+//   * results a later phase reads are written with ordinary stores (the L1 is
+//     write-through) and each writer waits for its stores (s_waitcnt) before
+//     it arrives at the barrier;
+//   * the barrier: one L2 atomic add per workgroup on an arrival counter; the
+//     last arriver (it sees the count reach epoch * NW) stores the epoch to a
+//     release word on another cache line; the others poll that word;
+//   * every read of data written in this launch by another workgroup
+//     (exchange rows, this step's K/V, the logits) and every poll is a
+//     device-scope load, which misses the CU's L1 (whose lines may predate the
+//     write) and is served by the L2; read-only inputs (weights, the step's
+//     record, earlier K/V) take ordinary loads;
+//   * the returning atomics execute in the XCD's L2 (the L1 executes none).
+// Every participant checks that it runs on the XCD of workgroup 0 (hardware
+// register XCC_ID; workgroup 0 publishes its own before the first barrier);
+// every wait is bounded (a wait that runs out stops waiting). Either failure
+// is reported in host_ids[16] (0 when the launch was good) and the results
+// are then not to be used. The last workgroup to leave resets the counters,
+// so consecutive launches on one stream reuse the sync words without a
+// memset.
+//
+// Arithmetic: the same operations in the same order as the separate kernels
+// of this library (vl_qkv_rope_cache, the short-decode attention,
+// vl_linear_rows, vl_argmax_rows): 16 x 16 projection tiles on
+// v_mfma_f32_16x16x4f32 with K split over 8 wavefronts and their partial
+// tiles summed in wavefront order, RMSNorm over k = lane + 64 i then across
+// the wavefront, RoPE / SwiGLU rounded as numpy rounds them, and per
+// (sequence, KV head) attention by 4 wavefronts over 256-key chunks.
+#include "vl_common.h"
+
+namespace {
+
+constexpr int kXcds = 8;
+constexpr int kThreads = 1024;   // 16 wavefronts: two projection tiles at once
+constexpr int kRows = 16;        // token rows (= sequences) of a step
+constexpr int kCols = 16;        // columns of a projection tile
+constexpr int kTileWaves = 8;    // wavefronts that split a tile's K
+constexpr int kUnits = 2;        // tiles (and attention items) per workgroup at once
+constexpr int kMaxCtx = 2048;    // context per sequence (its block table staged in LDS)
+constexpr int kSc1 = 16;         // buffer-load cache policy: device scope (misses the L1)
+
+// sync words (uint32), each on its own 128-byte line
+enum : int { kArrive = 0, kRelease = 32, kExit = 64, kLmDone = 96, kXcc = 112, kSyncWords = 128 };
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------ exchange ----
+__device__ __forceinline__ unsigned l2_add(unsigned* p, unsigned v) {
+  unsigned r;
+  asm volatile("global_atomic_add %0, %1, %2, off sc0\n\ts_waitcnt vmcnt(0)"
+               : "=v"(r)
+               : "v"(p), "v"(v)
+               : "memory");
+  return r;
+}
+__device__ __forceinline__ void l2_store(unsigned* p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ unsigned dev_load(const unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float dev_loadf(const float* p) {
+  return __uint_as_float(dev_load(reinterpret_cast<const unsigned*>(p)));
+}
+__device__ __forceinline__ void stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// A buffer of `bytes` bytes at p, for device-scope 16-byte loads.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ uint4 ld16_dev(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, kSc1);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// threadIdx.x through an opaque move: values derived from it are recomputed
+// where they are used instead of being hoisted out of the layer loop and held
+// (or spilled) for the whole launch
+__device__ __forceinline__ int otid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
+struct Sync {
+  unsigned* w;
+  int NW;
+  unsigned epoch;
+  unsigned limit;
+  bool bad;  // thread 0: a wait ran out
+};
+
+// Grid barrier among the NW workgroups of the XCD (see the protocol above).
+__device__ __forceinline__ void grid_sync(Sync& s) {
+  stores_done();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    ++s.epoch;
+    const unsigned prev = l2_add(s.w + kArrive, 1u);
+    if (prev + 1 == s.epoch * (unsigned)s.NW) {
+      l2_store(s.w + kRelease, s.epoch);
+    } else if (!s.bad) {
+      unsigned spins = 0;
+      while (dev_load(s.w + kRelease) < s.epoch) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins > s.limit) {
+          s.bad = true;
+          break;
+        }
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// ------------------------------------------------------------- params ----
+struct StepLayer {
+  const float* attn_norm;  // [d]
+  const float* qkv;        // 16-column tiles [ceil(nqkv / 16), d, 16]
+  const float* wo;         // [d / 16, d, 16]
+  const float* ffn_norm;   // [d]
+  const float* gate_up;    // [2 dff / 16, d, 16]: the gate tiles, then the up tiles
+  const float* down;       // [d / 16, dff, 16]
+};
+
+struct StepParams {
+  const StepLayer* layers;
+  int n_layers;
+  const float* tok_emb;     // [vocab, d]
+  const float* final_norm;  // [d]
+  const float* lm_head;     // [ceil(vocab / 16), d, 16]
+  void* kc;                 // [n_layers] x layer_stride cache elements
+  void* vc;
+  int64_t layer_stride;
+  KvGeom geom;
+  const int32_t* tokens;     // [16]: < 0 stands for prev_ids[-t - 1]
+  const int32_t* positions;  // [16]
+  const int32_t* slots;      // [16], -1: no cache write
+  const int32_t* seq_lens;   // [n_seqs]
+  const int32_t* bt;         // [n_seqs, bt_stride]
+  int bt_stride, n_seqs;
+  const int32_t* prev_ids;
+  int n_prev;
+  const float* cos_t;  // [max_pos, hd / 2]
+  const float* sin_t;
+  float* x;       // [16, d]
+  float* q;       // [16, H hd]
+  float* attn;    // [16, H hd]
+  float* act;     // [16, dff]
+  float* logits;  // [16, vocab]
+  int32_t* ids;       // [16]
+  int32_t* host_ids;  // [17] pinned host memory: ids, then the launch's status
+  unsigned* sync;     // kSyncWords words, zero before the first launch
+  int d, dff, H, Hkv, vocab;
+  int bs_log2;  // log2 of the block size (block tables)
+  float scale_log2, eps;
+  unsigned spin_limit;
+};
+
+// -------------------------------------------------- projection tiles ----
+// The weights of tile `tile` that wavefront tw (of the tile's 8) multiplies:
+// steps of 4 k from step tw * spw, in registers, 0 past K and past N columns.
+// Tiled element (k, m), k = 16 g + 4 s + j, sits at 256 g + 4 (16 j + m) + s,
+// so a lane's operands of 4 steps are one float4.
+__device__ __forceinline__ int steps_per_wave(int K) {
+  return ((K / 4 + kTileWaves - 1) / kTileWaves + 3) / 4 * 4;
+}
+
+template <int KMAX, int NS>
+struct TileW {
+  float v[NS][KMAX / 32];
+};
+
+template <int KMAX, int NS>
+__device__ __forceinline__ void load_tile(TileW<KMAX, NS>& wb, const float* w, int64_t up_off,
+                                          int tile, int K, int N, bool valid) {
+  const int t_ = otid();
+  const int lane = t_ & 63, tw = (t_ >> 6) & (kTileWaves - 1);
+  const int m = lane & 15;
+  const int spw = steps_per_wave(K), kb = tw * spw * 4;
+  const int nsteps = max(0, min(spw, K / 4 - tw * spw));
+  const float colmask = valid && tile * kCols + m < N ? 1.f : 0.f;
+  const int t = valid ? tile : 0;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const float4* src =
+        reinterpret_cast<const float4*>(w + (s ? up_off : 0) + (int64_t)t * K * kCols) + lane;
+#pragma unroll
+    for (int g = 0; g < KMAX / 128; ++g) {
+      const float4 v = src[(int64_t)min(kb / 16 + g, K / 16 - 1) * 64];
+      const float z = 4 * g < nsteps ? colmask : 0.f;
+      wb.v[s][4 * g] = v.x * z;
+      wb.v[s][4 * g + 1] = v.y * z;
+      wb.v[s][4 * g + 2] = v.z * z;
+      wb.v[s][4 * g + 3] = v.w * z;
+    }
+  }
+}
+
+// The RMSNorm weights a lane applies (k = lane + 64 i).
+template <int KMAX>
+__device__ __forceinline__ void load_norm(float (&gw)[KMAX / 64], const float* w, int K) {
+  const int lane = otid() & 63;
+#pragma unroll
+  for (int i = 0; i < KMAX / 64; ++i) gw[i] = w[min(lane + 64 * i, K - 1)];
+}
+
+// 16 rows of K floats to LDS (row pitch KP), zero past K, from an exchange
+// buffer [16, K] (device-scope loads); every load of a thread is issued
+// before the first LDS store.
+template <int KMAX, int KP>
+__device__ __forceinline__ void stage_rows(float* xs, const float* src, int K) {
+  constexpr int kQ = KMAX / 4;  // float4 per row
+  constexpr int kPer = (kRows * kQ + kThreads - 1) / kThreads;
+  const int tid = otid();
+  const __amdgpu_buffer_rsrc_t r = rsrc(src, (uint32_t)(kRows * K * 4));
+  float4 v[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int e = tid + u * kThreads;
+    const int row = e / kQ, c4 = e - row * kQ;
+    v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (row < kRows && 4 * c4 < K) {
+      const uint4 w = ld16_dev(r, (uint32_t)(row * K + 4 * c4) * 4u);
+      v[u] = make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z),
+                         __uint_as_float(w.w));
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int e = tid + u * kThreads;
+    const int row = e / kQ, c4 = e - row * kQ;
+    if (row < kRows) *reinterpret_cast<float4*>(&xs[row * KP + 4 * c4]) = v[u];
+  }
+}
+
+// The embedding rows tok_emb[token] of the 16 tokens to LDS, as stage_rows
+// (token t < 0 stands for prev[-t - 1], the id the previous step chose for
+// its row -t - 1; ordinary loads: the table and ids are not written in this
+// launch). With x_out, the rows are also written there: the residual stream
+// starts as the embeddings.
+template <int KMAX, int KP>
+__device__ __forceinline__ void stage_embeddings(float* xs, const float* tok_emb, int K,
+                                                 const int32_t* tokens, const int32_t* prev,
+                                                 int n_prev, int vocab, float* x_out) {
+  constexpr int kQ = KMAX / 4;
+  constexpr int kPer = (kRows * kQ + kThreads - 1) / kThreads;
+  const int tid = otid();
+  float4 v[kPer];
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int e = tid + u * kThreads;
+    const int row = e / kQ, c4 = e - row * kQ;
+    v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (row < kRows && 4 * c4 < K) {
+      int t = tokens[row];
+      if (t < 0) t = prev[min(-t - 1, n_prev - 1)];
+      t = min(max(t, 0), vocab - 1);
+      v[u] = *reinterpret_cast<const float4*>(tok_emb + (int64_t)t * K + 4 * c4);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int e = tid + u * kThreads;
+    const int row = e / kQ, c4 = e - row * kQ;
+    if (row < kRows) {
+      *reinterpret_cast<float4*>(&xs[row * KP + 4 * c4]) = v[u];
+      if (x_out && 4 * c4 < K)
+        *reinterpret_cast<float4*>(x_out + (int64_t)row * K + 4 * c4) = v[u];
+    }
+  }
+}
+
+// RMSNorm of the 16 staged rows in place, wavefront w on row w: the sum of
+// squares over k = lane + 64 i in increasing i, the wavefront sum, then
+// (x / rms) * g, as rms_norm_kernel computes it.
+template <int KMAX, int KP>
+__device__ __forceinline__ void norm_rows(float* xs, const float (&gw)[KMAX / 64], int K,
+                                          float eps) {
+  const int t_ = otid();
+  const int lane = t_ & 63, wave = t_ >> 6;
+  float* row = &xs[wave * KP + lane];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < KMAX / 64; ++i) {
+    const float a = row[64 * i];
+    ss += a * a;
+  }
+  const float rms = sqrtf(wave_sum(ss) / (float)K + eps);
+#pragma unroll
+  for (int i = 0; i < KMAX / 64; ++i)
+    if (lane + 64 * i < K) row[64 * i] = (row[64 * i] / rms) * gw[i];
+}
+
+// The tile's products for the unit's 8 wavefronts, summed over them in
+// order: thread t < 256 of the unit gets row t / 16, column t % 16 of each
+// slice in out[s]. The staged rows are read as A (every read below KMAX,
+// columns past K zero); red holds [NS][8][256] floats of this unit.
+template <int KMAX, int NS, int KP>
+__device__ __forceinline__ void tile_mma(const float* xs, const TileW<KMAX, NS>& wb, float* red,
+                                         int K, float (&out)[NS]) {
+  constexpr int kSteps = KMAX / 32;
+  constexpr int kAcc = kSteps >= 4 ? 4 : 1;
+  const int t_ = otid();
+  const int lane = t_ & 63, tw = (t_ >> 6) & (kTileWaves - 1);
+  const int m = lane & 15, j = lane >> 4;
+  const int kb = tw * steps_per_wave(K) * 4;
+  f32x4_t acc4[NS][kAcc];
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int q = 0; q < kAcc; ++q) acc4[s][q] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+  const float* arow = &xs[m * KP + kb + j];
+  float av[kSteps];
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i) av[i] = arow[4 * i];
+#pragma unroll
+  for (int i = 0; i < kSteps; ++i)
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      acc4[s][i % kAcc] =
+          __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], wb.v[s][i], acc4[s][i % kAcc], 0, 0, 0);
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    f32x4_t a = acc4[s][0];
+#pragma unroll
+    for (int q = 1; q < kAcc; ++q) a += acc4[s][q];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[(s * kTileWaves + tw) * 256 + (4 * j + i) * kCols + m] = a[i];
+  }
+  __syncthreads();
+  const int t = otid() & 511;
+  if (t < 256) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      float v = red[s * kTileWaves * 256 + t];
+#pragma unroll
+      for (int w = 1; w < kTileWaves; ++w) v += red[(s * kTileWaves + w) * 256 + t];
+      out[s] = v;
+    }
+  }
+}
+
+// the sum of one element of the partial tiles (the RoPE pair partner)
+__device__ __forceinline__ float tile_total(const float* red, int e) {
+  float v = red[e];
+#pragma unroll
+  for (int w = 1; w < kTileWaves; ++w) v += red[w * 256 + e];
+  return v;
+}
+
+__device__ __forceinline__ float silu_times(float g, float u) {
+#pragma clang fp contract(off)
+  const float s = g / (1.0f + expf(-g));
+  return s * u;
+}
+
+__device__ __forceinline__ void rotate_pair(float e, float o, float c, float s, float* oe,
+                                            float* oo) {
+#pragma clang fp contract(off)
+  float ec = e * c, os = o * s, es = e * s, oc = o * c;
+  *oe = ec - os;
+  *oo = es + oc;
+}
+
+template <typename TKV>
+__device__ __forceinline__ void store_kv(TKV* cache, int64_t i, float v) {
+  Elem<TKV>::store(cache, i, v);
+}
+
+// ------------------------------------------------------------ attention ----
+// One (sequence, KV head) item by 4 wavefronts (256 threads), exactly as
+// the short-decode kernel of this library computes it: the block table in
+// LDS; chunks of 256 keys, wavefront w taking keys 64 (4 t + w) + lane; QK
+// with lane = key against the LDS query heads; a base-2 online softmax per
+// wavefront (DPP max), each lane keeping the sum of its own keys' weights;
+// PV with lane = (key group, 16-byte chunk); the wavefronts merged in LDS,
+// max-rescaled, one head at a time.
+template <typename TKV, int D, int REP>
+struct AttnLds {
+  static constexpr int kVE = 16 / (int)sizeof(TKV);
+  float q[REP][D];
+  float p[4][REP][64];
+  float red[4][64][kVE];
+  float m[4][REP], l[4][REP];
+  int32_t tbl[kMaxCtx];
+};
+
+// ---------------------------------------------------------------- kernel --
+template <typename TKV, int KD, int KF, int D, int REP>
+struct StepLds {
+  static constexpr int KPD = KD + 4, KPF = KF + 4;  // staged row pitches
+  float xs[kRows * KPF];
+  float red[kUnits][2][kTileWaves * 256];
+  AttnLds<TKV, D, REP> at[kUnits];
+  int flag;
+};
+
+template <typename TKV, int KD, int KF, int D, int REP>
+__global__ void __launch_bounds__(kThreads) decode_step_kernel(const StepParams p) {
+  using L = StepLds<TKV, KD, KF, D, REP>;
+  constexpr int KPD = L::KPD, KPF = L::KPF;
+  constexpr int VE = AttnLds<TKV, D, REP>::kVE;
+  static_assert(D % VE == 0 && D <= 64, "head_dim");
+  constexpr int NC = D / VE;             // 16-byte chunks per head row
+  constexpr int G = 64 / NC;             // PV key groups
+  constexpr int KPL = (64 + G - 1) / G;  // keys per lane in the PV product
+  __shared__ L s;
+
+  if (blockIdx.x % kXcds) return;  // workgroups of the other XCDs leave at once
+  const int u = blockIdx.x / kXcds, NW = gridDim.x / kXcds;
+  // a phase's thread coordinates (recomputed per phase from an opaque
+  // thread index): wavefront, tile unit (waves 0-7 and 8-15), thread in the
+  // unit, and the (row, column) of the tile element it finishes
+#define VL_IDS                                                        \
+  const int tid = otid(), lane = tid & 63, wave = tid >> 6;           \
+  const int unit = wave >> 3, ut = tid & 511;                         \
+  const int er = ut / kCols, ec = ut % kCols;                         \
+  (void)lane, (void)er, (void)ec
+  Sync sy{p.sync, NW, 0u, p.spin_limit, false};
+  int status = 0;
+  unsigned xcc = 0;
+  if (threadIdx.x == 0) {
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= 0xf;
+    if (u == 0) l2_store(p.sync + kXcc, xcc + 1);  // read after the first barrier
+  }
+
+  const int d = p.d, dff = p.dff, H = p.H, Hkv = p.Hkv;
+  const int qd = H * D, kd = Hkv * D, nqkv = qd + 2 * kd;
+  const int n_qkv = cdiv(nqkv, kCols), n_d = d / kCols, n_ff = dff / kCols;
+  const int n_lm = cdiv(p.vocab, kCols);
+  const int per_pass = kUnits * NW;  // tiles of one pass over the workgroups
+  const int bs_log2 = p.bs_log2;
+
+  for (int l = 0; l < p.n_layers; ++l) {
+    const StepLayer& W = p.layers[l];
+    TKV* kc = static_cast<TKV*>(p.kc) + (int64_t)l * p.layer_stride;
+    TKV* vc = static_cast<TKV*>(p.vc) + (int64_t)l * p.layer_stride;
+    // ------------------------------------------ A: RMSNorm, QKV, RoPE ----
+    {
+      VL_IDS;
+      TileW<KD, 1> wb;
+      float gw[KD / 64];
+      const int tile0 = kUnits * u + unit;
+      load_tile(wb, W.qkv, 0, tile0, d, nqkv, tile0 < n_qkv);
+      load_norm<KD>(gw, W.attn_norm, d);
+      if (l > 0) grid_sync(sy);
+      for (int base = 0; base < n_qkv; base += per_pass) {
+        const int tile = base + tile0;
+        const bool valid = tile < n_qkv;
+        if (base > 0) load_tile(wb, W.qkv, 0, tile, d, nqkv, valid);
+        // epilogue inputs of this thread's element
+        const int col = tile * kCols + ec;
+        int slot = -1;
+        float cs = 0.f, sn = 0.f;
+        if (valid && ut < 256 && col < qd + kd) {
+          const int bcol = col < qd ? col : col - qd;
+          const int64_t tab = (int64_t)p.positions[er] * (D >> 1) + ((bcol % D) >> 1);
+          cs = p.cos_t[tab];
+          sn = p.sin_t[tab];
+        }
+        if (valid && ut < 256) slot = p.slots[er];
+        if (base == 0) {
+          if (l == 0)
+            stage_embeddings<KD, KPD>(s.xs, p.tok_emb, d, p.tokens, p.prev_ids, p.n_prev,
+                                      p.vocab, u == 0 ? p.x : nullptr);
+          else
+            stage_rows<KD, KPD>(s.xs, p.x, d);
+          __syncthreads();
+          norm_rows<KD, KPD>(s.xs, gw, d, p.eps);
+          __syncthreads();
+        }
+        float v[1];
+        tile_mma<KD, 1, KPD>(s.xs, wb, &s.red[unit][0][0], d, v);
+        if (valid && ut < 256 && col < nqkv) {
+          if (col < qd + kd) {
+            const float partner = tile_total(&s.red[unit][0][0], ut ^ 1);
+            const int bcol = col < qd ? col : col - qd;
+            const bool odd = (bcol % D) & 1;
+            float oe, oo;
+            rotate_pair(odd ? partner : v[0], odd ? v[0] : partner, cs, sn, &oe, &oo);
+            const float val = odd ? oo : oe;
+            if (col < qd)
+              p.q[(int64_t)er * qd + col] = val;
+            else if (slot >= 0)
+              store_kv(kc, p.geom.at(slot, bcol / D) + bcol % D, val);
+          } else if (slot >= 0) {
+            const int vcol = col - qd - kd;
+            store_kv(vc, p.geom.at(slot, vcol / D) + vcol % D, v[0]);
+          }
+        }
+        __syncthreads();
+      }
+    }
+    // ------------------------------------------------------ B: attention ----
+    // item = sequence * Hkv + KV head; unit `unit` of workgroup u takes items
+    // kUnits u + unit (+ per_pass ...); waves 8..15 have none and only meet
+    // the barriers
+    {
+      VL_IDS;
+      AttnLds<TKV, D, REP>& a = s.at[(tid >> 8) & 1];
+      const int at = tid & 255, aw = (tid >> 6) & 3;  // thread / wavefront in the item
+      const bool lower = tid < 256 * kUnits;
+      const int n_items = p.n_seqs * Hkv;
+      const int item0 = kUnits * u + (tid >> 8);
+      // the table of the first item, staged while the QKV phase finishes
+      {
+        const int i = item0 / Hkv;
+        const int c = lower && item0 < n_items ? p.seq_lens[i] : 0;
+        if (c > 0 && c <= kMaxCtx) {
+          const int nblk = (c + (1 << bs_log2) - 1) >> bs_log2;
+          const int32_t* table = p.bt + (int64_t)i * p.bt_stride;
+          for (int b = at; b < nblk; b += 256) a.tbl[b] = table[b];
+        }
+      }
+      grid_sync(sy);
+      if (l == 0 && threadIdx.x == 0 && dev_load(p.sync + kXcc) != xcc + 1) status = 2;
+      for (int base = 0; base < n_items; base += per_pass) {
+        const int item = base + item0;
+        const int i = item / Hkv, g = item - (item / Hkv) * Hkv;
+        const int c = lower && item < n_items ? p.seq_lens[i] : 0;
+        const bool act = c > 0 && c <= kMaxCtx;
+        if (act && base > 0) {
+          const int nblk = (c + (1 << bs_log2) - 1) >> bs_log2;
+          const int32_t* table = p.bt + (int64_t)i * p.bt_stride;
+          for (int b = at; b < nblk; b += 256) a.tbl[b] = table[b];
+        }
+        if (act) {
+          for (int e = at; e < REP * D; e += 256) {
+            const int h = e / D, dd = e - (e / D) * D;
+            a.q[h][dd] = dev_loadf(p.q + (int64_t)i * qd + (g * REP + h) * D + dd) * p.scale_log2;
+          }
+        }
+        __syncthreads();
+        float mrun[REP], lsum[REP], acc[REP][VE];
+#pragma unroll
+        for (int h = 0; h < REP; ++h) {
+          mrun[h] = -__builtin_inff(), lsum[h] = 0.f;
+#pragma unroll
+          for (int e = 0; e < VE; ++e) acc[h][e] = 0.f;
+        }
+        if (act) {
+          const int bs_mask = (1 << bs_log2) - 1;
+          const uint32_t lbytes = (uint32_t)(p.layer_stride * (int64_t)sizeof(TKV));
+          const __amdgpu_buffer_rsrc_t rk = rsrc(kc, lbytes), rv = rsrc(vc, lbytes);
+          // the row of key k of KV head g (either cache layout)
+          auto row_of = [&](int k) {
+            return p.geom.at(((int64_t)a.tbl[k >> bs_log2] << bs_log2) + (k & bs_mask), g);
+          };
+          const int pg = lane / NC, pc = lane - (lane / NC) * NC;
+          const int nchunk = (c + 255) >> 8;
+          for (int t = 0; t < nchunk; ++t) {
+            const int cb = (4 * t + aw) * 64;
+            if (cb >= c) break;  // wavefront-uniform
+            float kr[D];
+            {
+              const uint32_t o = (uint32_t)(row_of(min(cb + lane, c - 1)) * (int64_t)sizeof(TKV));
+#pragma unroll
+              for (int cc = 0; cc < D / VE; ++cc) widen16<TKV>(ld16_dev(rk, o + 16 * cc), kr + VE * cc);
+            }
+            uint4 vraw[KPL];
+#pragma unroll
+            for (int jj = 0; jj < KPL; ++jj) {
+              const int kk = min(pg + G * jj, 63);
+              vraw[jj] = ld16_dev(
+                  rv, (uint32_t)((row_of(min(cb + kk, c - 1)) + pc * VE) * (int64_t)sizeof(TKV)));
+            }
+            const bool valid = cb + lane < c;
+#pragma unroll
+            for (int h = 0; h < REP; ++h) {
+              float dot = 0.f;
+#pragma unroll
+              for (int dd = 0; dd < D; ++dd) dot = __builtin_fmaf(a.q[h][dd], kr[dd], dot);
+              const float sc = valid ? dot : -__builtin_inff();
+              const float mn = fmaxf(mrun[h], wave_max_dpp(sc));
+              const float alpha = exp2_fast(mrun[h] - mn);
+              const float pr = exp2_fast(sc - mn);
+              lsum[h] = __builtin_fmaf(lsum[h], alpha, pr);
+#pragma unroll
+              for (int e = 0; e < VE; ++e) acc[h][e] *= alpha;
+              mrun[h] = mn;
+              a.p[aw][h][lane] = pr;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int jj = 0; jj < KPL; ++jj) {
+              const int kk = pg + G * jj;
+              float vv[VE];
+              widen16<TKV>(vraw[jj], vv);
+#pragma unroll
+              for (int h = 0; h < REP; ++h) {
+                const float w = kk < 64 ? a.p[aw][h][kk] : 0.f;
+#pragma unroll
+                for (int e = 0; e < VE; ++e) acc[h][e] = __builtin_fmaf(w, vv[e], acc[h][e]);
+              }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          }
+#pragma unroll
+          for (int h = 0; h < REP; ++h) lsum[h] = wave_sum_dpp(lsum[h]);
+          if (lane == 0) {
+#pragma unroll
+            for (int h = 0; h < REP; ++h) a.m[aw][h] = mrun[h], a.l[aw][h] = lsum[h];
+          }
+        }
+#pragma unroll
+        for (int h = 0; h < REP; ++h) {
+          if (act) {
+#pragma unroll
+            for (int e = 0; e < VE; ++e) a.red[aw][lane][e] = acc[h][e];
+          }
+          __syncthreads();
+          if (act && at < D) {
+            const int dd = at, dc = dd / VE, de = dd - (dd / VE) * VE;
+            float M = -__builtin_inff();
+#pragma unroll
+            for (int w = 0; w < 4; ++w) M = fmaxf(M, a.m[w][h]);
+            float Ls = 0.f, av = 0.f;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              const float mw = a.m[w][h];
+              if (mw == -__builtin_inff()) continue;
+              const float wt = exp2_fast(mw - M);
+              float sw = 0.f;
+#pragma unroll
+              for (int gg = 0; gg < G; ++gg) sw += a.red[w][gg * NC + dc][de];
+              Ls = __builtin_fmaf(a.l[w][h], wt, Ls);
+              av = __builtin_fmaf(sw, wt, av);
+            }
+            p.attn[((int64_t)i * H + g * REP + h) * D + dd] = Ls > 0.f ? av * (1.f / Ls) : 0.f;
+          }
+          __syncthreads();
+        }
+      }
+    }
+    // --------------------------------------------------- W: wo + residual ----
+    {
+      VL_IDS;
+      TileW<KD, 1> wb;
+      const int tile0 = kUnits * u + unit;
+      load_tile(wb, W.wo, 0, tile0, d, d, tile0 < n_d);
+      // the residual element: x was last written two barriers ago
+      float xres = 0.f;
+      if (tile0 < n_d && ut < 256) xres = dev_loadf(p.x + (int64_t)er * d + tile0 * kCols + ec);
+      grid_sync(sy);
+      for (int base = 0; base < n_d; base += per_pass) {
+        const int tile = base + tile0;
+        const bool valid = tile < n_d;
+        if (base > 0) {
+          load_tile(wb, W.wo, 0, tile, d, d, valid);
+          if (valid && ut < 256) xres = dev_loadf(p.x + (int64_t)er * d + tile * kCols + ec);
+        }
+        if (base == 0) {
+          stage_rows<KD, KPD>(s.xs, p.attn, d);
+          __syncthreads();
+        }
+        float v[1];
+        tile_mma<KD, 1, KPD>(s.xs, wb, &s.red[unit][0][0], d, v);
+        if (valid && ut < 256) p.x[(int64_t)er * d + tile * kCols + ec] = xres + v[0];
+        __syncthreads();
+      }
+    }
+    // --------------------------------- C: RMSNorm, gate|up, SwiGLU ----
+    {
+      VL_IDS;
+      TileW<KD, 2> wb;
+      float gw[KD / 64];
+      const int tile0 = kUnits * u + unit;
+      const int64_t up_off = (int64_t)n_ff * d * kCols;
+      load_tile(wb, W.gate_up, up_off, tile0, d, dff, tile0 < n_ff);
+      load_norm<KD>(gw, W.ffn_norm, d);
+      grid_sync(sy);
+      for (int base = 0; base < n_ff; base += per_pass) {
+        const int tile = base + tile0;
+        const bool valid = tile < n_ff;
+        if (base > 0) load_tile(wb, W.gate_up, up_off, tile, d, dff, valid);
+        if (base == 0) {
+          stage_rows<KD, KPD>(s.xs, p.x, d);
+          __syncthreads();
+          norm_rows<KD, KPD>(s.xs, gw, d, p.eps);
+          __syncthreads();
+        }
+        float v[2];
+        tile_mma<KD, 2, KPD>(s.xs, wb, &s.red[unit][0][0], d, v);
+        if (valid && ut < 256)
+          p.act[(int64_t)er * dff + tile * kCols + ec] = silu_times(v[0], v[1]);
+        __syncthreads();
+      }
+    }
+    // ------------------------------------------- D: down + residual ----
+    {
+      VL_IDS;
+      TileW<KF, 1> wb;
+      const int tile0 = kUnits * u + unit;
+      load_tile(wb, W.down, 0, tile0, dff, d, tile0 < n_d);
+      // x was last written by the W phase, a barrier ago
+      float xres = 0.f;
+      if (tile0 < n_d && ut < 256) xres = dev_loadf(p.x + (int64_t)er * d + tile0 * kCols + ec);
+      grid_sync(sy);
+      for (int base = 0; base < n_d; base += per_pass) {
+        const int tile = base + tile0;
+        const bool valid = tile < n_d;
+        if (base > 0) {
+          load_tile(wb, W.down, 0, tile, dff, d, valid);
+          if (valid && ut < 256) xres = dev_loadf(p.x + (int64_t)er * d + tile * kCols + ec);
+        }
+        if (base == 0) {
+          stage_rows<KF, KPF>(s.xs, p.act, dff);
+          __syncthreads();
+        }
+        float v[1];
+        tile_mma<KF, 1, KPF>(s.xs, wb, &s.red[unit][0][0], dff, v);
+        if (valid && ut < 256) p.x[(int64_t)er * d + tile * kCols + ec] = xres + v[0];
+        __syncthreads();
+      }
+    }
+  }
+  // ------------------------------------ L: final RMSNorm, lm_head ----
+  {
+    VL_IDS;
+    TileW<KD, 1> wb;
+    float gw[KD / 64];
+    const int tile0 = kUnits * u + unit;
+    load_tile(wb, p.lm_head, 0, tile0, d, p.vocab, tile0 < n_lm);
+    load_norm<KD>(gw, p.final_norm, d);
+    grid_sync(sy);
+    const bool has_tile = kUnits * u < n_lm;  // workgroup-uniform
+    for (int base = 0; base < n_lm; base += per_pass) {
+      const int tile = base + tile0;
+      const bool valid = tile < n_lm;
+      if (base > 0) load_tile(wb, p.lm_head, 0, tile, d, p.vocab, valid);
+      if (base == 0) {
+        stage_rows<KD, KPD>(s.xs, p.x, d);
+        __syncthreads();
+        norm_rows<KD, KPD>(s.xs, gw, d, p.eps);
+        __syncthreads();
+      }
+      float v[1];
+      tile_mma<KD, 1, KPD>(s.xs, wb, &s.red[unit][0][0], d, v);
+      const int col = tile * kCols + ec;
+      if (valid && ut < 256 && col < p.vocab) p.logits[(int64_t)er * p.vocab + col] = v[0];
+      __syncthreads();
+    }
+    // the last workgroup with lm_head tiles to finish takes every row's argmax
+    stores_done();
+    __syncthreads();
+    if (tid == 0) {
+      s.flag = 0;
+      if (has_tile) {
+        const unsigned n_wg = (unsigned)min(NW, cdiv(n_lm, kUnits));
+        s.flag = l2_add(p.sync + kLmDone, 1u) + 1 == n_wg;
+      }
+    }
+    __syncthreads();
+    if (s.flag) {
+      // wavefront r takes row r: numpy's rule, the lowest index of the
+      // maximum, a NaN beating every number (its first index)
+      constexpr int kNone = 0x7fffffff;
+      const int r = wave;
+      const float* row = p.logits + (int64_t)r * p.vocab;
+      float bv = -__builtin_inff();
+      int bi = kNone, ni = kNone;
+      for (int c = lane; c < p.vocab; c += 64) {
+        const float e = dev_loadf(row + c);
+        if (e > bv) bv = e, bi = c;
+        if (e != e && ni == kNone) ni = c;
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
+        ni = min(ni, __shfl_xor(ni, o, 64));
+      }
+      if (lane == 0) {
+        const int id = ni != kNone ? ni : (bi == kNone ? 0 : bi);
+        p.ids[r] = id;
+        p.host_ids[r] = id;
+      }
+    }
+  }
+  // ------------------------------------------------------------- exit ----
+  stores_done();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    if (sy.bad) status = 1;
+    if (status) p.host_ids[kRows] = status;
+    if (l2_add(p.sync + kExit, 1u) + 1 == (unsigned)NW) {  // everyone is past every barrier
+      l2_store(p.sync + kArrive, 0u);
+      l2_store(p.sync + kRelease, 0u);
+      l2_store(p.sync + kLmDone, 0u);
+      l2_store(p.sync + kXcc, 0u);
+      l2_store(p.sync + kExit, 0u);
+    }
+  }
+#undef VL_IDS
+}
+
+template <typename TKV, int KD, int KF, int D, int REP>
+int launch(const StepParams& prm, int nw, hipStream_t st) {
+  decode_step_kernel<TKV, KD, KF, D, REP><<<nw * kXcds, kThreads, 0, st>>>(prm);
+  VL_CHECK_LAUNCH();
+  return VL_OK;
+}
+
+}  // namespace
+
+extern "C" int vl_decode_step_supported(int d_model, int num_heads, int num_kv_heads, int d_ff,
+                                        int kv_dtype, int max_context) {
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads || d_model <= 0 ||
+      d_model % num_heads)
+    return 0;
+  const int hd = d_model / num_heads, rep = num_heads / num_kv_heads;
+  const bool dt = kv_dtype == VL_DTYPE_F32 || kv_dtype == VL_DTYPE_BF16 ||
+                  kv_dtype == VL_DTYPE_FP8_E4M3;
+  return dt && rep == 2 && (hd == 48 || hd == 16) && d_model % 64 == 0 && d_model <= 384 &&
+         d_ff % 16 == 0 && d_ff <= 1024 && max_context > 0 && max_context <= kMaxCtx;
+}
+
+extern "C" int vl_decode_step(const void* layer_weights, int n_layers, const float* tok_emb,
+                              const float* final_norm, const float* lm_head, void* key_cache,
+                              void* value_cache, int64_t layer_stride, int kv_dtype,
+                              int kv_layout, const int32_t* token_ids, const int32_t* positions,
+                              const int32_t* slot_mapping, const int32_t* seq_lens,
+                              const int32_t* block_tables, int block_table_stride, int num_seqs,
+                              const int32_t* prev_ids, int num_prev, const float* cos_table,
+                              const float* sin_table, int d_model, int num_heads,
+                              int num_kv_heads, int d_ff, int vocab, int block_size,
+                              int max_context, float scale, float eps, float* x, float* q,
+                              float* attn, float* act, float* logits, int32_t* out_ids,
+                              int32_t* out_ids_host, uint32_t* sync, void* stream) {
+  VL_CHECK_ARG(vl_decode_step_supported(d_model, num_heads, num_kv_heads, d_ff, kv_dtype,
+                                        max_context),
+               "decode step: shape not supported (d_model %d, heads %d / %d, d_ff %d, kv "
+               "dtype %d, context %d)",
+               d_model, num_heads, num_kv_heads, d_ff, kv_dtype, max_context);
+  VL_CHECK_ARG(n_layers > 0 && vocab > 0 && num_seqs >= 0 && num_seqs <= kRows &&
+                   block_size > 0 && (block_size & (block_size - 1)) == 0 &&
+                   block_table_stride >= (max_context + block_size - 1) / block_size &&
+                   num_prev > 0,
+               "decode step: bad layer count, vocab, sequence count (<= %d), block size, table "
+               "stride or prev_ids length",
+               kRows);
+  VL_CHECK_ARG(layer_weights && tok_emb && final_norm && lm_head && key_cache && value_cache &&
+                   token_ids && positions && slot_mapping && (seq_lens || !num_seqs) &&
+                   (block_tables || !num_seqs) && prev_ids && cos_table && sin_table && x && q &&
+                   attn && act && logits && out_ids && out_ids_host && sync,
+               "decode step: null pointer");
+  const int es = vl_cache_elem_bytes(kv_dtype);
+  VL_CHECK_ARG(layer_stride > 0 && layer_stride * es <= 0x7fffffff,
+               "decode step: a layer of the cache must be under 2 GiB");
+  VL_CHECK_ARG((((uintptr_t)key_cache | (uintptr_t)value_cache | (uintptr_t)tok_emb |
+                 (uintptr_t)lm_head | (uintptr_t)x | (uintptr_t)attn | (uintptr_t)act) & 15) == 0 &&
+                   ((uintptr_t)sync & 127) == 0 && (layer_stride * es) % 16 == 0,
+               "decode step: caches, embeddings, lm_head and row buffers 16-byte aligned, sync "
+               "words 128-byte aligned");
+  const int hd = d_model / num_heads;
+  StepParams p{};
+  p.layers = static_cast<const StepLayer*>(layer_weights);
+  p.n_layers = n_layers;
+  p.tok_emb = tok_emb;
+  p.final_norm = final_norm;
+  p.lm_head = lm_head;
+  p.kc = key_cache;
+  p.vc = value_cache;
+  p.layer_stride = layer_stride;
+  int rc = vl_kv_geom(kv_layout, block_size, num_kv_heads, hd, &p.geom);
+  if (rc) return rc;
+  p.tokens = token_ids;
+  p.positions = positions;
+  p.slots = slot_mapping;
+  p.seq_lens = seq_lens;
+  p.bt = block_tables;
+  p.bt_stride = block_table_stride;
+  p.n_seqs = num_seqs;
+  p.prev_ids = prev_ids;
+  p.n_prev = num_prev;
+  p.cos_t = cos_table;
+  p.sin_t = sin_table;
+  p.x = x;
+  p.q = q;
+  p.attn = attn;
+  p.act = act;
+  p.logits = logits;
+  p.ids = out_ids;
+  p.host_ids = out_ids_host;
+  p.sync = sync;
+  p.d = d_model;
+  p.dff = d_ff;
+  p.H = num_heads;
+  p.Hkv = num_kv_heads;
+  p.vocab = vocab;
+  p.bs_log2 = __builtin_ctz((unsigned)block_size);
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.eps = eps;
+  p.spin_limit = 1u << 18;
+  const int nw = vl_num_cus() / kXcds;
+  VL_CHECK_ARG(nw >= 1, "decode step: fewer than 8 compute units");
+  hipStream_t st = (hipStream_t)stream;
+#define VL_STEP_LAUNCH(T, Dh)                                        \
+  if (hd == Dh) return launch<T, 384, 1024, Dh, 2>(p, nw, st);
+  if (kv_dtype == VL_DTYPE_F32) {
+    VL_STEP_LAUNCH(float, 48)
+    VL_STEP_LAUNCH(float, 16)
+  } else if (kv_dtype == VL_DTYPE_BF16) {
+    VL_STEP_LAUNCH(uint16_t, 48)
+    VL_STEP_LAUNCH(uint16_t, 16)
+  } else {
+    VL_STEP_LAUNCH(uint8_t, 48)
+    VL_STEP_LAUNCH(uint8_t, 16)
+  }
+#undef VL_STEP_LAUNCH
+  VL_CHECK_ARG(false, "decode step: no kernel for head_dim %d", hd);
+}

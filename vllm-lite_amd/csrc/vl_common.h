@@ -153,3 +153,57 @@ struct KvGeom {
 // Checks kv_layout (and, for head-major, that block_size is a power of two)
 // and fills *g; a VL_EINVAL return carries its message.
 int vl_kv_geom(int kv_layout, int block_size, int num_kv_heads, int head_dim, KvGeom* g);
+
+// ------------------------------------------------- shared device helpers ----
+// 2^x by the hardware's v_exp_f32 (about 1 ulp; results below 2^-126 may
+// flush to zero, far below a softmax row sum's fp32 resolution). exp2f adds
+// a range reduction for denormal results that costs six more VALU ops.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// DPP lane exchange (update_dpp with `old` kept where the row mask excludes
+// the lane).
+#define VL_DPP(old, v, ctrl, rmask)                                                     \
+  __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), ctrl, \
+                                             rmask, 0xF, false))
+
+// Max / sum over the 64 lanes of a wavefront by DPP: within each row of 16
+// (quad xor 1, xor 2, half-row mirror, row mirror), then row 0 into 1 and 2
+// into 3 (row_bcast:15), row 1 into 2 and 3 (row_bcast:31); lane 63 holds the
+// result, which every lane reads back.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, VL_DPP(v, v, 0xB1, 0xF));
+  v = fmaxf(v, VL_DPP(v, v, 0x4E, 0xF));
+  v = fmaxf(v, VL_DPP(v, v, 0x141, 0xF));
+  v = fmaxf(v, VL_DPP(v, v, 0x140, 0xF));
+  v = fmaxf(v, VL_DPP(v, v, 0x142, 0xA));
+  v = fmaxf(v, VL_DPP(v, v, 0x143, 0xC));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += VL_DPP(0.f, v, 0xB1, 0xF);
+  v += VL_DPP(0.f, v, 0x4E, 0xF);
+  v += VL_DPP(0.f, v, 0x141, 0xF);
+  v += VL_DPP(0.f, v, 0x140, 0xF);
+  v += VL_DPP(0.f, v, 0x142, 0xA);
+  v += VL_DPP(0.f, v, 0x143, 0xC);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// 16 bytes of T (fp32, bf16 bits or FP8 E4M3 bytes) as floats
+template <typename T>
+__device__ __forceinline__ void widen16(const uint4& v, float* r) {
+  if constexpr (sizeof(T) == 4) {
+    r[0] = __uint_as_float(v.x), r[1] = __uint_as_float(v.y);
+    r[2] = __uint_as_float(v.z), r[3] = __uint_as_float(v.w);
+  } else if constexpr (sizeof(T) == 1) {
+    e4m3x4_to_f32(v.x, r), e4m3x4_to_f32(v.y, r + 4);
+    e4m3x4_to_f32(v.z, r + 8), e4m3x4_to_f32(v.w, r + 12);
+  } else {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      r[2 * e] = __uint_as_float(w[e] << 16);
+      r[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+    }
+  }
+}

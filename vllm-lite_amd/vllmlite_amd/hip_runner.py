@@ -25,7 +25,14 @@ count) for scheduled sequence i, count = min(1 + drafts, tokens)
      (execute), or the argmax of each row written to pinned host memory by
      its launch (execute_argmax / launch_argmax).
 
-Step 3 is captured once per shape bucket (tokens, sequences and logits rows
+A decode step of at most 16 sequences (every sequence one query token)
+whose model shape has a one-launch kernel (ops.decode_step_supported) runs
+instead as ONE launch, vl_decode_step, on the compute units of one XCD: the
+whole forward, the logits rows and the argmax of each row, written to device
+memory and to the pinned host buffer of the step (one_launch_decode = False
+keeps every step on the separate kernels).
+
+Step 3 is otherwise captured once per shape bucket (tokens, sequences and logits rows
 each rounded up to a power of two) into a HIP graph and replayed afterwards;
 padded tokens belong to no sequence, carry slot -1 (no cache write) and
 position 0, padded sequences have no tokens and no context, and the rows they
@@ -158,7 +165,7 @@ class _Shape:
 
 class HipRunner(ModelRunner):
     def __init__(self, model_cfg, cache_cfg, weights: Dict[str, np.ndarray] = None,
-                 device=None, use_graphs: bool = True):
+                 device=None, use_graphs: bool = True, one_launch_decode: bool = True):
         if not torch.cuda.is_available():
             raise RuntimeError("HipRunner needs a visible MI355X (torch.cuda.is_available() is False)")
         ops.lib()  # fail now, loudly, if the gfx950 library is not built
@@ -193,6 +200,14 @@ class HipRunner(ModelRunner):
                 getattr(cache_cfg, "kv_dtype", "float32"), torch.float32)
             self.cache_k = torch.zeros(shape, dtype=kv, device=self.device)
             self.cache_v = torch.zeros(shape, dtype=kv, device=self.device)
+            # decode steps of <= 16 sequences as one launch, where a kernel exists
+            self._step = None
+            self.one_launch_steps = 0
+            if (one_launch_decode and self._fused_rows and ops.decode_step_supported(
+                    mc.d_model, mc.n_heads, mc.n_kv_heads, mc.d_ff, kv, mc.max_seq_len)):
+                self._step = ops.DecodeStep(self.w, self.device)
+                self._exec_ids_host = torch.zeros(ops.DECODE_STEP_ROWS + 1, dtype=torch.int32,
+                                                  pin_memory=True)
         self.W = max(1, -(-mc.max_seq_len // self.block_size))
         self._buf = 0  # which of the two pinned staging / id buffers the next launch uses
         self._cap_T = 0
@@ -215,9 +230,11 @@ class HipRunner(ModelRunner):
 
     def execute(self, out) -> Tuple[np.ndarray, List[Tuple[int, int]]]:
         with torch.cuda.device(self.device), torch.cuda.stream(self.stream):
-            rows, R = self._run(out)
+            rows, R, one = self._run(out, -1)
             self._logits_host[:R].copy_(self._logits[:R], non_blocking=True)
             self.stream.synchronize()
+            if one:
+                self._check_step(self._exec_ids_host.numpy())
             return self._logits_host_np[:R].copy(), rows
 
     def execute_argmax(self, out) -> Tuple[np.ndarray, List[Tuple[int, int]]]:
@@ -237,29 +254,49 @@ class HipRunner(ModelRunner):
         the next step's sequences stands for row -t - 1 of this step's ids
         (resolved on the device, vl_resolve_tokens)."""
         with torch.cuda.device(self.device), torch.cuda.stream(self.stream):
-            rows, R = self._run(out)
             k = self._buf
-            # the ids to the device buffer (the next step resolves its
-            # placeholders from it) and, by the same launch, to the pinned one
-            ops.argmax_rows(self._logits[:R], self._ids[:R], host_out=self._ids_hosts[k])
+            rows, R, one = self._run(out, k)
+            if not one:
+                # the ids to the device buffer (the next step resolves its
+                # placeholders from it) and, by the same launch, to the pinned one
+                ops.argmax_rows(self._logits[:R], self._ids[:R], host_out=self._ids_hosts[k])
             self._done[k].record(self.stream)
             self._buf ^= 1
             # the handle holds its own buffer and event: a later step that grows
             # the buffers replaces them while this copy may still be queued
-            return rows, R, self._ids_hosts_np[k], self._done[k]
+            return rows, R, self._ids_hosts_np[k], self._done[k], one
 
     def collect(self, handle) -> Tuple[np.ndarray, List[Tuple[int, int]]]:
         """Waits for a launched step; its ids and rows."""
-        rows, R, host, done = handle
+        rows, R, host, done, one = handle
         done.synchronize()
+        if one:
+            self._check_step(host)
         return host[:R].copy(), rows
 
-    def _run(self, out) -> Tuple[List[Tuple[int, int]], int]:
+    @staticmethod
+    def _check_step(host: np.ndarray) -> None:
+        status = int(host[ops.DECODE_STEP_ROWS])
+        if status:
+            why = {1: "a wait between its phases ran out",
+                   2: "its workgroups were not all on one XCD"}.get(status, f"status {status}")
+            raise RuntimeError(f"one-launch decode step failed: {why}; its results are invalid "
+                               "(construct HipRunner with one_launch_decode=False)")
+
+    def _run(self, out, host_k=None) -> Tuple[List[Tuple[int, int]], int, bool]:
         """CoW copies, staging and the forward (graph replay when captured);
-        leaves the logits rows in self._logits[:R]."""
+        leaves the logits rows in self._logits[:R]. A decode step that the
+        one-launch kernel takes also leaves the ids in self._ids and in a
+        pinned host buffer (host_k: that of launch_argmax's buffer k, or -1
+        for execute's own); the flag says so."""
         if out.cow:
             self._copy_on_write(out.cow)
         shape, rows, R = self._stage(out)
+        if (host_k is not None and self._step is not None and shape.decode and
+                shape.Tb == ops.DECODE_STEP_ROWS and shape.Sb <= ops.DECODE_STEP_ROWS):
+            self._decode_step(shape, self._exec_ids_host if host_k < 0 else self._ids_hosts[host_k])
+            self.one_launch_steps += 1
+            return rows, R, True
         key = (shape.Tb, shape.Sb, shape.Rb, shape.decode)
         g = self._graphs.get(key)
         if g is not None:
@@ -268,7 +305,20 @@ class HipRunner(ModelRunner):
             self._forward(shape)
             if self.use_graphs:
                 self._capture(shape, key)
-        return rows, R
+        return rows, R, False
+
+    def _decode_step(self, s: "_Shape", host: torch.Tensor) -> None:
+        """The step as one vl_decode_step launch (rows = sequences)."""
+        meta, n = self._meta, ops.DECODE_STEP_ROWS
+        host.numpy()[n] = 0  # the launch's status word
+        mc = self.model_cfg
+        ops.decode_step(self._step, self.w["tok_emb"], self.w["final_norm"], self.w["lm_head_t"],
+                        self.cache_k, self.cache_v, meta[s.tok:s.tok + n], meta[s.pos:s.pos + n],
+                        meta[s.slot:s.slot + n], meta[s.lens:s.lens + s.Sb],
+                        meta[s.bt:s.bt + s.Sb * s.W].view(s.Sb, s.W), self._ids, self.cos,
+                        self.sin, self.H, self.Hkv, self.block_size, mc.max_seq_len, self.scale,
+                        1e-5, self._x, self._q, self._attn, self._act, self._logits, self._ids,
+                        host)
 
     # -------------------------------------------------------------- staging --
     def _ensure_capacity(self, T: int, W: int) -> None:

@@ -23,7 +23,7 @@ F32, BF16, F32_BF16KV, FP8_E4M3, F32_FP8KV = 0, 1, 2, 3, 4
 # VL_KV_*: a per-layer cache tensor [slots, Hkv, D] is token-major (the
 # reference's layout), [blocks, Hkv, block_size, D] head-major
 KV_TOKEN_MAJOR, KV_HEAD_MAJOR = 0, 1
-ABI_VERSION = 6  # vl_abi_version() of the library these signatures describe
+ABI_VERSION = 7  # vl_abi_version() of the library these signatures describe
 _c_void_p = ctypes.c_void_p
 _i32, _i64, _f32, _size = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
 
@@ -68,6 +68,13 @@ SIGNATURES = {
                                  _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32,
                                  _i32, _i32, _i32, _c_void_p]),
     "vl_resolve_tokens": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p]),
+    "vl_decode_step_supported": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "vl_decode_step": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                              _c_void_p, _i64, _i32, _i32, _c_void_p, _c_void_p, _c_void_p,
+                              _c_void_p, _c_void_p, _i32, _i32, _c_void_p, _i32, _c_void_p,
+                              _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _f32,
+                              _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                              _c_void_p, _c_void_p, _c_void_p]),
 }
 
 _LIB: Optional[ctypes.CDLL] = None
@@ -520,3 +527,78 @@ def resolve_tokens(token_ids: torch.Tensor, prev_ids: torch.Tensor) -> None:
     _dev_i32(prev_ids, "prev_ids")
     _check(lib().vl_resolve_tokens(_ptr(token_ids), token_ids.numel(), _ptr(prev_ids),
                                    prev_ids.numel(), _stream()), "vl_resolve_tokens")
+
+
+# ------------------------------------------------------------------ K7 -----
+DECODE_STEP_ROWS = 16  # token rows (= sequences) of one vl_decode_step launch
+
+
+def decode_step_supported(d_model: int, num_heads: int, num_kv_heads: int, d_ff: int,
+                          kv_dtype: torch.dtype, max_context: int) -> bool:
+    code = {torch.float32: F32, torch.bfloat16: BF16, torch.float8_e4m3fn: FP8_E4M3}.get(kv_dtype)
+    if code is None:
+        return False
+    return bool(lib().vl_decode_step_supported(d_model, num_heads, num_kv_heads, d_ff, code,
+                                               max_context))
+
+
+class DecodeStep:
+    """What vl_decode_step keeps between launches: the device table of each
+    layer's weight addresses (attn_norm, tiled QKV, tiled wo, ffn_norm, tiled
+    gate|up, tiled w_down) and the launch's sync words (zero-filled here; every
+    launch leaves them zero)."""
+
+    FIELDS = ("attn_norm", "w_qkv_t", "wo_t", "ffn_norm", "w_gate_up_t", "w_down_t")
+
+    def __init__(self, packed: dict, device):
+        self.layers = packed["layers"]
+        ptrs = [L[f].data_ptr() for L in self.layers for f in self.FIELDS]
+        self.table = torch.tensor(ptrs, dtype=torch.int64, device=device)
+        self.sync = torch.zeros(128, dtype=torch.int32, device=device)
+        _need(self.sync.data_ptr() % 128 == 0, "sync words must be 128-byte aligned")
+
+
+def decode_step(ds: DecodeStep, tok_emb, final_norm, lm_head_t, key_cache, value_cache,
+                token_ids, positions, slot_mapping, seq_lens, block_tables, prev_ids,
+                cos, sin, num_heads: int, num_kv_heads: int, block_size: int, max_context: int,
+                scale: float, eps: float, x, q, attn, act, logits, out_ids, out_ids_host) -> None:
+    """One decode step of the model in one launch (vl_decode_step): rows are
+    the first 16 of token_ids / positions / slot_mapping; sequences the rows of
+    seq_lens / block_tables [num_seqs <= 16, W]; the argmax ids land in
+    out_ids[:16] and the pinned out_ids_host[:16]; the caller zeroes
+    out_ids_host[16], which is non-zero afterwards if the launch failed."""
+    n_layers = len(ds.layers)
+    R = DECODE_STEP_ROWS
+    _need(key_cache.shape == value_cache.shape and key_cache.shape[0] == n_layers and
+          key_cache.is_contiguous() and value_cache.is_contiguous(),
+          "caches must be contiguous [n_layers, ...]")
+    cdt = _cache_dtype(key_cache, value_cache)
+    layout, hkv, bs, hd = kv_layout(key_cache[0])
+    _need(hkv == num_kv_heads and (bs in (0, block_size)), "cache shape")
+    d = x.shape[1]
+    d_ff = act.shape[1]
+    vocab = logits.shape[1]
+    for t, n in ((token_ids, "token_ids"), (positions, "positions"),
+                 (slot_mapping, "slot_mapping"), (seq_lens, "seq_lens"),
+                 (block_tables, "block_tables"), (prev_ids, "prev_ids"), (out_ids, "out_ids")):
+        _dev_i32(t, n)
+    _need(token_ids.numel() >= R and positions.numel() >= R and slot_mapping.numel() >= R and
+          out_ids.numel() >= R, "16 rows of tokens, positions, slots and ids")
+    _need(block_tables.dim() == 2 and block_tables.stride(1) == 1 and
+          block_tables.shape[0] == seq_lens.numel() <= R, "block_tables [num_seqs, W]")
+    for t in (x, q, attn, act, logits, tok_emb, final_norm, lm_head_t, cos, sin):
+        _need(t.dtype == torch.float32 and t.is_contiguous(), "fp32 contiguous tensors")
+    _need(x.shape[0] >= R and q.numel() >= R * d and attn.numel() >= R * d and
+          act.shape[0] >= R and logits.shape[0] >= R and tok_emb.shape[1] == d,
+          "row buffers of at least 16 rows")
+    _need(out_ids_host.dtype == torch.int32 and out_ids_host.is_pinned() and
+          out_ids_host.is_contiguous() and out_ids_host.numel() > R,
+          "out_ids_host must be a pinned int32 tensor of at least 17 entries")
+    _check(lib().vl_decode_step(
+        _ptr(ds.table), n_layers, _ptr(tok_emb), _ptr(final_norm), _ptr(lm_head_t),
+        _ptr(key_cache), _ptr(value_cache), key_cache[0].numel(), cdt, layout, _ptr(token_ids),
+        _ptr(positions), _ptr(slot_mapping), _ptr(seq_lens), _ptr(block_tables),
+        block_tables.stride(0), seq_lens.numel(), _ptr(prev_ids), prev_ids.numel(), _ptr(cos),
+        _ptr(sin), d, num_heads, num_kv_heads, d_ff, vocab, block_size, max_context,
+        float(scale), float(eps), _ptr(x), _ptr(q), _ptr(attn), _ptr(act), _ptr(logits),
+        _ptr(out_ids), _ptr(out_ids_host), _ptr(ds.sync), _stream()), "vl_decode_step")
