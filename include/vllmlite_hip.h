@@ -329,11 +329,12 @@ int vl_argmax_rows(const float* logits, int64_t row_stride, int64_t rows, int vo
  * separate kernels compute for the step (vl_qkv_rope_cache,
  * vl_paged_attention, vl_linear_rows, vl_argmax_rows).
  *
- * layer_weights: device array of n_layers x 6 device addresses: attn_norm
- * [d], the fused QKV weight, wo, ffn_norm [d], the fused gate|up weight and
- * w_down, each weight in the 16-column tile layout of VL_WEIGHT_TILES16
- * ([ceil(n/16), k, 16]; gate|up: the gate tiles, then the up tiles); lm_head
- * likewise. Caches [n_layers] x layer_stride elements of kv_dtype
+ * layer_weights: 6 device addresses (a host array), each the first of
+ * n_layers buffers of its kind laid out layer_strides[k] floats apart: the
+ * attn_norm [d], the fused QKV weight, wo, ffn_norm [d], the fused gate|up
+ * weight and w_down, each weight in the 16-column tile layout of
+ * VL_WEIGHT_TILES16 ([ceil(n/16), k, 16]; gate|up: the gate tiles, then the
+ * up tiles); lm_head likewise. Caches [n_layers] x layer_stride elements of kv_dtype
  * (VL_DTYPE_F32, _BF16 or _FP8_E4M3, written rounded to nearest even) in
  * kv_layout, a layer under 2 GiB. x, q, attn, act: fp32 [16, d], [16, d],
  * [16, d], [16, d_ff] rows the launch exchanges between its phases; sync:
@@ -345,7 +346,8 @@ int vl_argmax_rows(const float* logits, int64_t row_stride, int64_t rows, int vo
  */
 int vl_decode_step_supported(int d_model, int num_heads, int num_kv_heads, int d_ff, int kv_dtype,
                              int max_context);
-int vl_decode_step(const void* layer_weights, int n_layers, const float* tok_emb,
+int vl_decode_step(const void* const* layer_weights, const int64_t* layer_strides, int n_layers,
+                   const float* tok_emb,
                    const float* final_norm, const float* lm_head, void* key_cache,
                    void* value_cache, int64_t layer_stride, int kv_dtype, int kv_layout,
                    const int32_t* token_ids, const int32_t* positions,

@@ -33,7 +33,7 @@ class _Twin:
 
     def __init__(self, cfg):
         from vllmlite_amd.hip_runner import HipRunner
-        self.a = HipRunner(cfg.model, cfg.cache)
+        self.a = HipRunner(cfg.model, cfg.cache, one_launch_decode=True)
         self.b = HipRunner(cfg.model, cfg.cache, one_launch_decode=False)
         assert self.a._step is not None, "no one-launch kernel for this shape"
         self.vocab_size = self.a.vocab_size
@@ -117,7 +117,7 @@ def test_one_launch_steps_in_the_lookahead_engine():
     from vllmlite_amd.hip_runner import HipRunner
     g = json.load(open(os.path.join(GOLD, "cfg0_streams.json")))
     cfg = cfg0_config(False)
-    runner = HipRunner(cfg.model, cfg.cache)
+    runner = HipRunner(cfg.model, cfg.cache, one_launch_decode=True)
     eng = LLMEngine(cfg, runner=runner)
     for rid, ids, p in mixed_lengths(0, 48, 0):
         eng.add_request(params=p, request_id=rid, prompt_token_ids=ids)

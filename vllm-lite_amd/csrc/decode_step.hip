@@ -24,11 +24,14 @@
 //   * the barrier: one L2 atomic add per workgroup on an arrival counter; the
 //     last arriver (it sees the count reach epoch * NW) stores the epoch to a
 //     release word on another cache line; the others poll that word;
-//   * every read of data written in this launch by another workgroup
-//     (exchange rows, this step's K/V, the logits) and every poll is a
-//     device-scope load, which misses the CU's L1 (whose lines may predate the
-//     write) and is served by the L2; read-only inputs (weights, the step's
-//     record, earlier K/V) take ordinary loads;
+//   * every read of a buffer that is rewritten during the launch (the
+//     exchange rows x, q, attn, act, rewritten every layer, and the logits)
+//     and every poll is a device-scope load, which misses the CU's L1 (whose
+//     lines may be older than the write) and is served by the L2. The paged
+//     K/V takes ordinary loads: the lines of a layer's cache are read only in
+//     that layer's attention phase, after the barrier that follows their
+//     writes, so no L1 holds an older copy (the L1 starts each launch empty);
+//     so do the read-only inputs (weights, the step's record);
 //   * the returning atomics execute in the XCD's L2 (the L1 executes none).
 // Every participant checks that it runs on the XCD of workgroup 0 (hardware
 // register XCC_ID; workgroup 0 publishes its own before the first barrier);
@@ -46,15 +49,15 @@
 // the wavefront, RoPE / SwiGLU rounded as numpy rounds them, and per
 // (sequence, KV head) attention by 4 wavefronts over 256-key chunks.
 #include "vl_common.h"
+#include "decode_item.h"
 
 namespace {
 
 constexpr int kXcds = 8;
-constexpr int kThreads = 1024;   // 16 wavefronts: two projection tiles at once
+constexpr int kThreads = 512;    // 8 wavefronts: 256 VGPRs each, one workgroup per CU
 constexpr int kRows = 16;        // token rows (= sequences) of a step
 constexpr int kCols = 16;        // columns of a projection tile
 constexpr int kTileWaves = 8;    // wavefronts that split a tile's K
-constexpr int kUnits = 2;        // tiles (and attention items) per workgroup at once
 constexpr int kMaxCtx = 2048;    // context per sequence (its block table staged in LDS)
 constexpr int kSc1 = 16;         // buffer-load cache policy: device scope (misses the L1)
 
@@ -112,8 +115,10 @@ struct Sync {
 };
 
 // Grid barrier among the NW workgroups of the XCD (see the protocol above).
+// Every thread has waited for its stores of the phase before (stores_done at
+// the end of each phase); the loads a workgroup issues for the next phase
+// stay in flight across the barrier.
 __device__ __forceinline__ void grid_sync(Sync& s) {
-  stores_done();
   __syncthreads();
   if (threadIdx.x == 0) {
     ++s.epoch;
@@ -135,17 +140,23 @@ __device__ __forceinline__ void grid_sync(Sync& s) {
 }
 
 // ------------------------------------------------------------- params ----
-struct StepLayer {
-  const float* attn_norm;  // [d]
-  const float* qkv;        // 16-column tiles [ceil(nqkv / 16), d, 16]
-  const float* wo;         // [d / 16, d, 16]
-  const float* ffn_norm;   // [d]
-  const float* gate_up;    // [2 dff / 16, d, 16]: the gate tiles, then the up tiles
-  const float* down;       // [d / 16, dff, 16]
+// The weights of every layer: one buffer per kind, layer l at l * stride
+// elements (so a phase finds its weights by arithmetic, with no dependent
+// load of a pointer). Weights are 16-column tiles [ceil(n / 16), k, 16].
+enum : int { kAttnNorm, kQkv, kWo, kFfnNorm, kGateUp, kDown, kWeightKinds };
+//   kAttnNorm [d]; kQkv [ceil(nqkv / 16), d, 16]; kWo [d / 16, d, 16];
+//   kFfnNorm [d]; kGateUp [2 dff / 16, d, 16] (the gate tiles, then the up
+//   tiles); kDown [d / 16, dff, 16]
+struct StepWeights {
+  const float* base[kWeightKinds];
+  int64_t stride[kWeightKinds];
+  __device__ __forceinline__ const float* at(int kind, int l) const {
+    return base[kind] + (int64_t)l * stride[kind];
+  }
 };
 
 struct StepParams {
-  const StepLayer* layers;
+  StepWeights w;
   int n_layers;
   const float* tok_emb;     // [vocab, d]
   const float* final_norm;  // [d]
@@ -179,42 +190,41 @@ struct StepParams {
 };
 
 // -------------------------------------------------- projection tiles ----
-// The weights of tile `tile` that wavefront tw (of the tile's 8) multiplies:
-// steps of 4 k from step tw * spw, in registers, 0 past K and past N columns.
-// Tiled element (k, m), k = 16 g + 4 s + j, sits at 256 g + 4 (16 j + m) + s,
-// so a lane's operands of 4 steps are one float4.
+// A workgroup computes NT 16 x 16 tiles of a projection at once (tile
+// u + j NW, j < NT), each with NS slices (SwiGLU: the gate and up tiles).
+// Its 8 wavefronts split K: wavefront w takes the steps of 4 k from step
+// w spw, for every tile and slice, its weights in registers (0 past K and
+// past N columns). Tiled element (k, m), k = 16 g + 4 s + j, sits at 256 g +
+// 4 (16 j + m) + s, so a lane's operands of 4 steps are one float4.
 __device__ __forceinline__ int steps_per_wave(int K) {
   return ((K / 4 + kTileWaves - 1) / kTileWaves + 3) / 4 * 4;
 }
 
-template <int KMAX, int NS>
+template <int KMAX, int NSL>
 struct TileW {
-  float v[NS][KMAX / 32];
+  float v[NSL][KMAX / 32];
 };
 
-template <int KMAX, int NS>
-__device__ __forceinline__ void load_tile(TileW<KMAX, NS>& wb, const float* w, int64_t up_off,
-                                          int tile, int K, int N, bool valid) {
+// Slice sl of wb: tile `tile` of w (+ off), or zeros when not valid.
+template <int KMAX, int NSL>
+__device__ __forceinline__ void load_slice(TileW<KMAX, NSL>& wb, int sl, const float* w,
+                                           int64_t off, int tile, int K, int N, bool valid) {
   const int t_ = otid();
-  const int lane = t_ & 63, tw = (t_ >> 6) & (kTileWaves - 1);
+  const int lane = t_ & 63, tw = t_ >> 6;
   const int m = lane & 15;
   const int spw = steps_per_wave(K), kb = tw * spw * 4;
   const int nsteps = max(0, min(spw, K / 4 - tw * spw));
   const float colmask = valid && tile * kCols + m < N ? 1.f : 0.f;
-  const int t = valid ? tile : 0;
+  const float4* src =
+      reinterpret_cast<const float4*>(w + off + (int64_t)(valid ? tile : 0) * K * kCols) + lane;
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const float4* src =
-        reinterpret_cast<const float4*>(w + (s ? up_off : 0) + (int64_t)t * K * kCols) + lane;
-#pragma unroll
-    for (int g = 0; g < KMAX / 128; ++g) {
-      const float4 v = src[(int64_t)min(kb / 16 + g, K / 16 - 1) * 64];
-      const float z = 4 * g < nsteps ? colmask : 0.f;
-      wb.v[s][4 * g] = v.x * z;
-      wb.v[s][4 * g + 1] = v.y * z;
-      wb.v[s][4 * g + 2] = v.z * z;
-      wb.v[s][4 * g + 3] = v.w * z;
-    }
+  for (int g = 0; g < KMAX / 128; ++g) {
+    const float4 v = src[(int64_t)min(kb / 16 + g, K / 16 - 1) * 64];
+    const float z = 4 * g < nsteps ? colmask : 0.f;
+    wb.v[sl][4 * g] = v.x * z;
+    wb.v[sl][4 * g + 1] = v.y * z;
+    wb.v[sl][4 * g + 2] = v.z * z;
+    wb.v[sl][4 * g + 3] = v.w * z;
   }
 }
 
@@ -292,43 +302,46 @@ __device__ __forceinline__ void stage_embeddings(float* xs, const float* tok_emb
   }
 }
 
-// RMSNorm of the 16 staged rows in place, wavefront w on row w: the sum of
-// squares over k = lane + 64 i in increasing i, the wavefront sum, then
-// (x / rms) * g, as rms_norm_kernel computes it.
+// RMSNorm of the 16 staged rows in place, wavefront w on rows w and w + 8:
+// the sum of squares over k = lane + 64 i in increasing i, the wavefront sum,
+// then (x / rms) * g, as rms_norm_kernel computes it.
 template <int KMAX, int KP>
 __device__ __forceinline__ void norm_rows(float* xs, const float (&gw)[KMAX / 64], int K,
                                           float eps) {
   const int t_ = otid();
   const int lane = t_ & 63, wave = t_ >> 6;
-  float* row = &xs[wave * KP + lane];
-  float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < KMAX / 64; ++i) {
-    const float a = row[64 * i];
-    ss += a * a;
+  for (int rr = 0; rr < kRows / kTileWaves; ++rr) {
+    float* row = &xs[(wave + kTileWaves * rr) * KP + lane];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < KMAX / 64; ++i) {
+      const float a = row[64 * i];
+      ss += a * a;
+    }
+    const float rms = sqrtf(wave_sum(ss) / (float)K + eps);
+#pragma unroll
+    for (int i = 0; i < KMAX / 64; ++i)
+      if (lane + 64 * i < K) row[64 * i] = (row[64 * i] / rms) * gw[i];
   }
-  const float rms = sqrtf(wave_sum(ss) / (float)K + eps);
-#pragma unroll
-  for (int i = 0; i < KMAX / 64; ++i)
-    if (lane + 64 * i < K) row[64 * i] = (row[64 * i] / rms) * gw[i];
 }
 
-// The tile's products for the unit's 8 wavefronts, summed over them in
-// order: thread t < 256 of the unit gets row t / 16, column t % 16 of each
-// slice in out[s]. The staged rows are read as A (every read below KMAX,
-// columns past K zero); red holds [NS][8][256] floats of this unit.
-template <int KMAX, int NS, int KP>
-__device__ __forceinline__ void tile_mma(const float* xs, const TileW<KMAX, NS>& wb, float* red,
-                                         int K, float (&out)[NS]) {
+// The products of every slice, each summed over the 8 wavefronts in order:
+// thread t < 256 NT gets row (t % 256) / 16, column t % 16 of slices j NS +
+// s of tile j = t / 256 in out[s]. red holds [NSL][8][256] floats.
+template <int KMAX, int NT, int NS, int KP>
+__device__ __forceinline__ void tile_mma(const float* xs, const TileW<KMAX, NT * NS>& wb,
+                                         float* red, int K, float (&out)[NS]) {
+  constexpr int NSL = NT * NS;
   constexpr int kSteps = KMAX / 32;
   constexpr int kAcc = kSteps >= 4 ? 4 : 1;
   const int t_ = otid();
-  const int lane = t_ & 63, tw = (t_ >> 6) & (kTileWaves - 1);
+  const int lane = t_ & 63, tw = t_ >> 6;
   const int m = lane & 15, j = lane >> 4;
   const int kb = tw * steps_per_wave(K) * 4;
-  f32x4_t acc4[NS][kAcc];
+  f32x4_t acc4[NSL][kAcc];
 #pragma unroll
-  for (int s = 0; s < NS; ++s)
+  for (int s = 0; s < NSL; ++s)
 #pragma unroll
     for (int q = 0; q < kAcc; ++q) acc4[s][q] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
   const float* arow = &xs[m * KP + kb + j];
@@ -338,11 +351,11 @@ __device__ __forceinline__ void tile_mma(const float* xs, const TileW<KMAX, NS>&
 #pragma unroll
   for (int i = 0; i < kSteps; ++i)
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
+    for (int s = 0; s < NSL; ++s)
       acc4[s][i % kAcc] =
           __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], wb.v[s][i], acc4[s][i % kAcc], 0, 0, 0);
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
+  for (int s = 0; s < NSL; ++s) {
     f32x4_t a = acc4[s][0];
 #pragma unroll
     for (int q = 1; q < kAcc; ++q) a += acc4[s][q];
@@ -350,23 +363,25 @@ __device__ __forceinline__ void tile_mma(const float* xs, const TileW<KMAX, NS>&
     for (int i = 0; i < 4; ++i) red[(s * kTileWaves + tw) * 256 + (4 * j + i) * kCols + m] = a[i];
   }
   __syncthreads();
-  const int t = otid() & 511;
-  if (t < 256) {
+  if (t_ < 256 * NT) {
+    const int tj = t_ >> 8, e = t_ & 255;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      float v = red[s * kTileWaves * 256 + t];
+      const float* r = red + (tj * NS + s) * kTileWaves * 256;
+      float v = r[e];
 #pragma unroll
-      for (int w = 1; w < kTileWaves; ++w) v += red[(s * kTileWaves + w) * 256 + t];
+      for (int w = 1; w < kTileWaves; ++w) v += r[w * 256 + e];
       out[s] = v;
     }
   }
 }
 
-// the sum of one element of the partial tiles (the RoPE pair partner)
-__device__ __forceinline__ float tile_total(const float* red, int e) {
-  float v = red[e];
+// one element of slice sl summed over the wavefronts (the RoPE pair partner)
+__device__ __forceinline__ float tile_total(const float* red, int sl, int e) {
+  const float* r = red + sl * kTileWaves * 256;
+  float v = r[e];
 #pragma unroll
-  for (int w = 1; w < kTileWaves; ++w) v += red[w * 256 + e];
+  for (int w = 1; w < kTileWaves; ++w) v += r[w * 256 + e];
   return v;
 }
 
@@ -384,60 +399,56 @@ __device__ __forceinline__ void rotate_pair(float e, float o, float c, float s, 
   *oo = es + oc;
 }
 
-template <typename TKV>
-__device__ __forceinline__ void store_kv(TKV* cache, int64_t i, float v) {
-  Elem<TKV>::store(cache, i, v);
+// ------------------------------------------------------------ attention ----
+// A workgroup takes one sequence and NH of its KV heads: one decode item
+// (decode_item.h, as the short-decode kernel runs it) per head, run by the
+// same 8 wavefronts chunk by chunk, both heads' loads in flight together.
+// The sequence's block table is staged once per launch (it is the same in
+// every layer); the heads' first chunk of K/V is loaded before the barrier
+// that precedes the attention phase (this step's key, written by the QKV
+// phase, after it).
+
+// The block table of sequence i (c keys) into tbl.
+__device__ __forceinline__ void stage_table(int32_t* tbl, const StepParams& p, int i, int c) {
+  if (i >= p.n_seqs || c <= 0 || c > kMaxCtx) return;
+  const int nblk = (c + (1 << p.bs_log2) - 1) >> p.bs_log2;
+  const int32_t* table = p.bt + (int64_t)i * p.bt_stride;
+  for (int b = otid(); b < nblk; b += kThreads) tbl[b] = table[b];
 }
 
-// ------------------------------------------------------------ attention ----
-// One (sequence, KV head) item by 4 wavefronts (256 threads), exactly as
-// the short-decode kernel of this library computes it: the block table in
-// LDS; chunks of 256 keys, wavefront w taking keys 64 (4 t + w) + lane; QK
-// with lane = key against the LDS query heads; a base-2 online softmax per
-// wavefront (DPP max), each lane keeping the sum of its own keys' weights;
-// PV with lane = (key group, 16-byte chunk); the wavefronts merged in LDS,
-// max-rescaled, one head at a time.
-template <typename TKV, int D, int REP>
-struct AttnLds {
-  static constexpr int kVE = 16 / (int)sizeof(TKV);
-  float q[REP][D];
-  float p[4][REP][64];
-  float red[4][64][kVE];
-  float m[4][REP], l[4][REP];
-  int32_t tbl[kMaxCtx];
-};
-
 // ---------------------------------------------------------------- kernel --
-template <typename TKV, int KD, int KF, int D, int REP>
+template <typename TKV, int KD, int KF, int D, int REP, int NH>
 struct StepLds {
   static constexpr int KPD = KD + 4, KPF = KF + 4;  // staged row pitches
-  float xs[kRows * KPF];
-  float red[kUnits][2][kTileWaves * 256];
-  AttnLds<TKV, D, REP> at[kUnits];
+  struct Proj {
+    float xs[kRows * KPF];
+    float red[4][kTileWaves * 256];  // slices of the tiles of one pass
+  };
+  union {  // the projection phases' rows and partial tiles, or the attention items
+    Proj pj;
+    vl_item::Lds<TKV, D, REP> at[NH];
+  };
+  int32_t tbl[kMaxCtx];  // the sequence's block table, kept across phases
   int flag;
 };
 
-template <typename TKV, int KD, int KF, int D, int REP>
+template <typename TKV, int KD, int KF, int D, int REP, int NH>
 __global__ void __launch_bounds__(kThreads) decode_step_kernel(const StepParams p) {
-  using L = StepLds<TKV, KD, KF, D, REP>;
+  using L = StepLds<TKV, KD, KF, D, REP, NH>;
+  namespace it = vl_item;
   constexpr int KPD = L::KPD, KPF = L::KPF;
-  constexpr int VE = AttnLds<TKV, D, REP>::kVE;
-  static_assert(D % VE == 0 && D <= 64, "head_dim");
-  constexpr int NC = D / VE;             // 16-byte chunks per head row
-  constexpr int G = 64 / NC;             // PV key groups
-  constexpr int KPL = (64 + G - 1) / G;  // keys per lane in the PV product
+  static_assert(it::kMaxCtx == kMaxCtx && kThreads == it::kThreads, "item layout");
   __shared__ L s;
 
   if (blockIdx.x % kXcds) return;  // workgroups of the other XCDs leave at once
   const int u = blockIdx.x / kXcds, NW = gridDim.x / kXcds;
   // a phase's thread coordinates (recomputed per phase from an opaque
-  // thread index): wavefront, tile unit (waves 0-7 and 8-15), thread in the
-  // unit, and the (row, column) of the tile element it finishes
-#define VL_IDS                                                        \
-  const int tid = otid(), lane = tid & 63, wave = tid >> 6;           \
-  const int unit = wave >> 3, ut = tid & 511;                         \
-  const int er = ut / kCols, ec = ut % kCols;                         \
-  (void)lane, (void)er, (void)ec
+  // thread index): lane, wavefront, and the (row, column) of the tile
+  // element a thread finishes (tile t / 256 of the pass)
+#define VL_IDS                                                    \
+  const int tid = otid(), lane = tid & 63, wave = tid >> 6;       \
+  const int ej = tid >> 8, er = (tid & 255) / kCols, ec = tid % kCols; \
+  (void)lane, (void)wave, (void)ej, (void)er, (void)ec
   Sync sy{p.sync, NW, 0u, p.spin_limit, false};
   int status = 0;
   unsigned xcc = 0;
@@ -451,52 +462,66 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(const StepParams 
   const int qd = H * D, kd = Hkv * D, nqkv = qd + 2 * kd;
   const int n_qkv = cdiv(nqkv, kCols), n_d = d / kCols, n_ff = dff / kCols;
   const int n_lm = cdiv(p.vocab, kCols);
-  const int per_pass = kUnits * NW;  // tiles of one pass over the workgroups
   const int bs_log2 = p.bs_log2;
+  // attention: workgroup u takes sequence u / (Hkv / NH), KV heads from
+  // NH (u % (Hkv / NH)); a pass covers NW such units
+  const int hpu = Hkv / NH;  // units per sequence
+  const int n_units = p.n_seqs * hpu;
+  int c_first;  // the context of this workgroup's first unit
+  {
+    const int i = u / hpu;
+    c_first = u < n_units ? p.seq_lens[i] : 0;
+    stage_table(s.tbl, p, i, c_first);
+  }
 
   for (int l = 0; l < p.n_layers; ++l) {
-    const StepLayer& W = p.layers[l];
     TKV* kc = static_cast<TKV*>(p.kc) + (int64_t)l * p.layer_stride;
     TKV* vc = static_cast<TKV*>(p.vc) + (int64_t)l * p.layer_stride;
     // ------------------------------------------ A: RMSNorm, QKV, RoPE ----
     {
       VL_IDS;
-      TileW<KD, 1> wb;
+      constexpr int NT = 2;
+      const float* wq = p.w.at(kQkv, l);
+      TileW<KD, NT> wb;
       float gw[KD / 64];
-      const int tile0 = kUnits * u + unit;
-      load_tile(wb, W.qkv, 0, tile0, d, nqkv, tile0 < n_qkv);
-      load_norm<KD>(gw, W.attn_norm, d);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) load_slice(wb, j, wq, 0, u + j * NW, d, nqkv, u + j * NW < n_qkv);
+      load_norm<KD>(gw, p.w.at(kAttnNorm, l), d);
       if (l > 0) grid_sync(sy);
-      for (int base = 0; base < n_qkv; base += per_pass) {
-        const int tile = base + tile0;
-        const bool valid = tile < n_qkv;
-        if (base > 0) load_tile(wb, W.qkv, 0, tile, d, nqkv, valid);
+      for (int base = 0; base < n_qkv; base += NT * NW) {
+        if (base > 0) {
+#pragma unroll
+          for (int j = 0; j < NT; ++j)
+            load_slice(wb, j, wq, 0, base + u + j * NW, d, nqkv, base + u + j * NW < n_qkv);
+        }
+        const int tile = base + u + ej * NW;
+        const bool valid = ej < NT && tile < n_qkv;
         // epilogue inputs of this thread's element
         const int col = tile * kCols + ec;
         int slot = -1;
         float cs = 0.f, sn = 0.f;
-        if (valid && ut < 256 && col < qd + kd) {
+        if (valid && col < qd + kd) {
           const int bcol = col < qd ? col : col - qd;
           const int64_t tab = (int64_t)p.positions[er] * (D >> 1) + ((bcol % D) >> 1);
           cs = p.cos_t[tab];
           sn = p.sin_t[tab];
         }
-        if (valid && ut < 256) slot = p.slots[er];
+        if (valid) slot = p.slots[er];
         if (base == 0) {
           if (l == 0)
-            stage_embeddings<KD, KPD>(s.xs, p.tok_emb, d, p.tokens, p.prev_ids, p.n_prev,
+            stage_embeddings<KD, KPD>(s.pj.xs, p.tok_emb, d, p.tokens, p.prev_ids, p.n_prev,
                                       p.vocab, u == 0 ? p.x : nullptr);
           else
-            stage_rows<KD, KPD>(s.xs, p.x, d);
+            stage_rows<KD, KPD>(s.pj.xs, p.x, d);
           __syncthreads();
-          norm_rows<KD, KPD>(s.xs, gw, d, p.eps);
+          norm_rows<KD, KPD>(s.pj.xs, gw, d, p.eps);
           __syncthreads();
         }
         float v[1];
-        tile_mma<KD, 1, KPD>(s.xs, wb, &s.red[unit][0][0], d, v);
-        if (valid && ut < 256 && col < nqkv) {
+        tile_mma<KD, NT, 1, KPD>(s.pj.xs, wb, &s.pj.red[0][0], d, v);
+        if (valid && col < nqkv) {
           if (col < qd + kd) {
-            const float partner = tile_total(&s.red[unit][0][0], ut ^ 1);
+            const float partner = tile_total(&s.pj.red[0][0], ej, (tid & 255) ^ 1);
             const int bcol = col < qd ? col : col - qd;
             const bool odd = (bcol % D) & 1;
             float oe, oo;
@@ -505,240 +530,193 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(const StepParams 
             if (col < qd)
               p.q[(int64_t)er * qd + col] = val;
             else if (slot >= 0)
-              store_kv(kc, p.geom.at(slot, bcol / D) + bcol % D, val);
+              Elem<TKV>::store(kc, p.geom.at(slot, bcol / D) + bcol % D, val);
           } else if (slot >= 0) {
             const int vcol = col - qd - kd;
-            store_kv(vc, p.geom.at(slot, vcol / D) + vcol % D, v[0]);
+            Elem<TKV>::store(vc, p.geom.at(slot, vcol / D) + vcol % D, v[0]);
           }
         }
         __syncthreads();
       }
+      stores_done();
     }
     // ------------------------------------------------------ B: attention ----
-    // item = sequence * Hkv + KV head; unit `unit` of workgroup u takes items
-    // kUnits u + unit (+ per_pass ...); waves 8..15 have none and only meet
-    // the barriers
     {
       VL_IDS;
-      AttnLds<TKV, D, REP>& a = s.at[(tid >> 8) & 1];
-      const int at = tid & 255, aw = (tid >> 6) & 3;  // thread / wavefront in the item
-      const bool lower = tid < 256 * kUnits;
-      const int n_items = p.n_seqs * Hkv;
-      const int item0 = kUnits * u + (tid >> 8);
-      // the table of the first item, staged while the QKV phase finishes
-      {
-        const int i = item0 / Hkv;
-        const int c = lower && item0 < n_items ? p.seq_lens[i] : 0;
-        if (c > 0 && c <= kMaxCtx) {
-          const int nblk = (c + (1 << bs_log2) - 1) >> bs_log2;
-          const int32_t* table = p.bt + (int64_t)i * p.bt_stride;
-          for (int b = at; b < nblk; b += 256) a.tbl[b] = table[b];
-        }
+      it::Src<TKV> src[NH];
+      const __amdgpu_buffer_rsrc_t rk = it::cache_rsrc(kc, p.layer_stride * (int64_t)sizeof(TKV));
+      const __amdgpu_buffer_rsrc_t rv = it::cache_rsrc(vc, p.layer_stride * (int64_t)sizeof(TKV));
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        src[h].tbl = s.tbl;
+        src[h].kc = kc;
+        src[h].vc = vc;
+        src[h].geom = p.geom;
+        src[h].bs_log2 = bs_log2;
+        src[h].rk = rk;
+        src[h].rv = rv;
+        src[h].g = (u % hpu) * NH + h;
+        src[h].c = c_first;
       }
+      bool act = u < n_units && c_first > 0 && c_first <= kMaxCtx;
+      // the first chunk of the first unit's first head, but for this step's
+      // key (the other heads' right after the barrier: registers)
+      it::Regs<TKV, D, REP> r[NH];
+      if (act) it::issue<true>(r[0], src[0], 0, wave, lane, c_first - 1, true);
       grid_sync(sy);
       if (l == 0 && threadIdx.x == 0 && dev_load(p.sync + kXcc) != xcc + 1) status = 2;
-      for (int base = 0; base < n_items; base += per_pass) {
-        const int item = base + item0;
-        const int i = item / Hkv, g = item - (item / Hkv) * Hkv;
-        const int c = lower && item < n_items ? p.seq_lens[i] : 0;
-        const bool act = c > 0 && c <= kMaxCtx;
-        if (act && base > 0) {
-          const int nblk = (c + (1 << bs_log2) - 1) >> bs_log2;
-          const int32_t* table = p.bt + (int64_t)i * p.bt_stride;
-          for (int b = at; b < nblk; b += 256) a.tbl[b] = table[b];
+#pragma unroll
+      for (int h = 1; h < NH; ++h)
+        if (act) it::issue<true>(r[h], src[h], 0, wave, lane, c_first - 1, false);
+      for (int base = 0; base < n_units; base += NW) {
+        const int unit = base + u;
+        const int i = unit / hpu;
+        if (base > 0) {
+          const int c = unit < n_units ? p.seq_lens[i] : 0;
+#pragma unroll
+          for (int h = 0; h < NH; ++h) src[h].c = c, src[h].g = (unit % hpu) * NH + h;
+          act = unit < n_units && c > 0 && c <= kMaxCtx;
+          __syncthreads();  // the previous unit is done with the table
+          stage_table(s.tbl, p, i, c);
         }
+        const int c = src[0].c;
         if (act) {
-          for (int e = at; e < REP * D; e += 256) {
-            const int h = e / D, dd = e - (e / D) * D;
-            a.q[h][dd] = dev_loadf(p.q + (int64_t)i * qd + (g * REP + h) * D + dd) * p.scale_log2;
-          }
+#pragma unroll
+          for (int h = 0; h < NH; ++h)
+            for (int e = tid; e < REP * D; e += kThreads) {
+              const int hh = e / D, dd = e - (e / D) * D;
+              s.at[h].q[hh][dd] =
+                  dev_loadf(p.q + (int64_t)i * qd + (src[h].g * REP + hh) * D + dd) *
+                  p.scale_log2;
+            }
         }
         __syncthreads();
-        float mrun[REP], lsum[REP], acc[REP][VE];
+        it::State<it::Shape<TKV, D, REP>::VE, REP> st[NH];
 #pragma unroll
-        for (int h = 0; h < REP; ++h) {
-          mrun[h] = -__builtin_inff(), lsum[h] = 0.f;
-#pragma unroll
-          for (int e = 0; e < VE; ++e) acc[h][e] = 0.f;
-        }
+        for (int h = 0; h < NH; ++h) st[h].init();
         if (act) {
-          const int bs_mask = (1 << bs_log2) - 1;
-          const uint32_t lbytes = (uint32_t)(p.layer_stride * (int64_t)sizeof(TKV));
-          const __amdgpu_buffer_rsrc_t rk = rsrc(kc, lbytes), rv = rsrc(vc, lbytes);
-          // the row of key k of KV head g (either cache layout)
-          auto row_of = [&](int k) {
-            return p.geom.at(((int64_t)a.tbl[k >> bs_log2] << bs_log2) + (k & bs_mask), g);
-          };
-          const int pg = lane / NC, pc = lane - (lane / NC) * NC;
-          const int nchunk = (c + 255) >> 8;
+          const int nchunk = (c + it::kChunk - 1) / it::kChunk;
           for (int t = 0; t < nchunk; ++t) {
-            const int cb = (4 * t + aw) * 64;
-            if (cb >= c) break;  // wavefront-uniform
-            float kr[D];
-            {
-              const uint32_t o = (uint32_t)(row_of(min(cb + lane, c - 1)) * (int64_t)sizeof(TKV));
 #pragma unroll
-              for (int cc = 0; cc < D / VE; ++cc) widen16<TKV>(ld16_dev(rk, o + 16 * cc), kr + VE * cc);
+            for (int h = 0; h < NH; ++h) {
+              if (t == 0 && base == 0 && h == 0)
+                it::load_fresh<true>(r[h], src[h], 0, wave, lane, c - 1);
+              else if (!(t == 0 && base == 0))
+                it::issue<true>(r[h], src[h], t, wave, lane, c - 1, false);
             }
-            uint4 vraw[KPL];
 #pragma unroll
-            for (int jj = 0; jj < KPL; ++jj) {
-              const int kk = min(pg + G * jj, 63);
-              vraw[jj] = ld16_dev(
-                  rv, (uint32_t)((row_of(min(cb + kk, c - 1)) + pc * VE) * (int64_t)sizeof(TKV)));
-            }
-            const bool valid = cb + lane < c;
-#pragma unroll
-            for (int h = 0; h < REP; ++h) {
-              float dot = 0.f;
-#pragma unroll
-              for (int dd = 0; dd < D; ++dd) dot = __builtin_fmaf(a.q[h][dd], kr[dd], dot);
-              const float sc = valid ? dot : -__builtin_inff();
-              const float mn = fmaxf(mrun[h], wave_max_dpp(sc));
-              const float alpha = exp2_fast(mrun[h] - mn);
-              const float pr = exp2_fast(sc - mn);
-              lsum[h] = __builtin_fmaf(lsum[h], alpha, pr);
-#pragma unroll
-              for (int e = 0; e < VE; ++e) acc[h][e] *= alpha;
-              mrun[h] = mn;
-              a.p[aw][h][lane] = pr;
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-            for (int jj = 0; jj < KPL; ++jj) {
-              const int kk = pg + G * jj;
-              float vv[VE];
-              widen16<TKV>(vraw[jj], vv);
-#pragma unroll
-              for (int h = 0; h < REP; ++h) {
-                const float w = kk < 64 ? a.p[aw][h][kk] : 0.f;
-#pragma unroll
-                for (int e = 0; e < VE; ++e) acc[h][e] = __builtin_fmaf(w, vv[e], acc[h][e]);
-              }
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-          }
-#pragma unroll
-          for (int h = 0; h < REP; ++h) lsum[h] = wave_sum_dpp(lsum[h]);
-          if (lane == 0) {
-#pragma unroll
-            for (int h = 0; h < REP; ++h) a.m[aw][h] = mrun[h], a.l[aw][h] = lsum[h];
+            for (int h = 0; h < NH; ++h) it::compute(st[h], r[h], s.at[h], c, t, wave, lane);
           }
         }
 #pragma unroll
-        for (int h = 0; h < REP; ++h) {
-          if (act) {
-#pragma unroll
-            for (int e = 0; e < VE; ++e) a.red[aw][lane][e] = acc[h][e];
-          }
-          __syncthreads();
-          if (act && at < D) {
-            const int dd = at, dc = dd / VE, de = dd - (dd / VE) * VE;
-            float M = -__builtin_inff();
-#pragma unroll
-            for (int w = 0; w < 4; ++w) M = fmaxf(M, a.m[w][h]);
-            float Ls = 0.f, av = 0.f;
-#pragma unroll
-            for (int w = 0; w < 4; ++w) {
-              const float mw = a.m[w][h];
-              if (mw == -__builtin_inff()) continue;
-              const float wt = exp2_fast(mw - M);
-              float sw = 0.f;
-#pragma unroll
-              for (int gg = 0; gg < G; ++gg) sw += a.red[w][gg * NC + dc][de];
-              Ls = __builtin_fmaf(a.l[w][h], wt, Ls);
-              av = __builtin_fmaf(sw, wt, av);
-            }
-            p.attn[((int64_t)i * H + g * REP + h) * D + dd] = Ls > 0.f ? av * (1.f / Ls) : 0.f;
-          }
-          __syncthreads();
+        for (int h = 0; h < NH; ++h) {
+          const int g = src[h].g;
+          it::finish(st[h], s.at[h], act, tid, wave, lane, [&](int hh, int dd, float v) {
+            p.attn[((int64_t)i * H + g * REP + hh) * D + dd] = v;
+          });
         }
       }
+      if (n_units > NW) {  // the next layer starts again with the first unit
+        __syncthreads();
+        stage_table(s.tbl, p, u / hpu, c_first);
+      }
+      stores_done();
     }
     // --------------------------------------------------- W: wo + residual ----
     {
       VL_IDS;
+      const float* ww = p.w.at(kWo, l);
       TileW<KD, 1> wb;
-      const int tile0 = kUnits * u + unit;
-      load_tile(wb, W.wo, 0, tile0, d, d, tile0 < n_d);
+      load_slice(wb, 0, ww, 0, u, d, d, u < n_d);
       // the residual element: x was last written two barriers ago
       float xres = 0.f;
-      if (tile0 < n_d && ut < 256) xres = dev_loadf(p.x + (int64_t)er * d + tile0 * kCols + ec);
+      if (ej == 0 && u < n_d) xres = dev_loadf(p.x + (int64_t)er * d + u * kCols + ec);
       grid_sync(sy);
-      for (int base = 0; base < n_d; base += per_pass) {
-        const int tile = base + tile0;
-        const bool valid = tile < n_d;
+      for (int base = 0; base < n_d; base += NW) {
+        const int tile = base + u;
+        const bool valid = ej == 0 && tile < n_d;
         if (base > 0) {
-          load_tile(wb, W.wo, 0, tile, d, d, valid);
-          if (valid && ut < 256) xres = dev_loadf(p.x + (int64_t)er * d + tile * kCols + ec);
+          load_slice(wb, 0, ww, 0, tile, d, d, tile < n_d);
+          if (valid) xres = dev_loadf(p.x + (int64_t)er * d + tile * kCols + ec);
         }
         if (base == 0) {
-          stage_rows<KD, KPD>(s.xs, p.attn, d);
+          stage_rows<KD, KPD>(s.pj.xs, p.attn, d);
           __syncthreads();
         }
         float v[1];
-        tile_mma<KD, 1, KPD>(s.xs, wb, &s.red[unit][0][0], d, v);
-        if (valid && ut < 256) p.x[(int64_t)er * d + tile * kCols + ec] = xres + v[0];
+        tile_mma<KD, 1, 1, KPD>(s.pj.xs, wb, &s.pj.red[0][0], d, v);
+        if (valid) p.x[(int64_t)er * d + tile * kCols + ec] = xres + v[0];
         __syncthreads();
       }
+      stores_done();
     }
     // --------------------------------- C: RMSNorm, gate|up, SwiGLU ----
     {
       VL_IDS;
-      TileW<KD, 2> wb;
-      float gw[KD / 64];
-      const int tile0 = kUnits * u + unit;
+      constexpr int NT = 2;
+      const float* wg = p.w.at(kGateUp, l);
       const int64_t up_off = (int64_t)n_ff * d * kCols;
-      load_tile(wb, W.gate_up, up_off, tile0, d, dff, tile0 < n_ff);
-      load_norm<KD>(gw, W.ffn_norm, d);
+      TileW<KD, 2 * NT> wb;
+      float gw[KD / 64];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int t = u + j * NW;
+        load_slice(wb, 2 * j, wg, 0, t, d, dff, t < n_ff);
+        load_slice(wb, 2 * j + 1, wg, up_off, t, d, dff, t < n_ff);
+      }
+      load_norm<KD>(gw, p.w.at(kFfnNorm, l), d);
       grid_sync(sy);
-      for (int base = 0; base < n_ff; base += per_pass) {
-        const int tile = base + tile0;
-        const bool valid = tile < n_ff;
-        if (base > 0) load_tile(wb, W.gate_up, up_off, tile, d, dff, valid);
+      for (int base = 0; base < n_ff; base += NT * NW) {
+        if (base > 0) {
+#pragma unroll
+          for (int j = 0; j < NT; ++j) {
+            const int t = base + u + j * NW;
+            load_slice(wb, 2 * j, wg, 0, t, d, dff, t < n_ff);
+            load_slice(wb, 2 * j + 1, wg, up_off, t, d, dff, t < n_ff);
+          }
+        }
+        const int tile = base + u + ej * NW;
+        const bool valid = ej < NT && tile < n_ff;
         if (base == 0) {
-          stage_rows<KD, KPD>(s.xs, p.x, d);
+          stage_rows<KD, KPD>(s.pj.xs, p.x, d);
           __syncthreads();
-          norm_rows<KD, KPD>(s.xs, gw, d, p.eps);
+          norm_rows<KD, KPD>(s.pj.xs, gw, d, p.eps);
           __syncthreads();
         }
         float v[2];
-        tile_mma<KD, 2, KPD>(s.xs, wb, &s.red[unit][0][0], d, v);
-        if (valid && ut < 256)
-          p.act[(int64_t)er * dff + tile * kCols + ec] = silu_times(v[0], v[1]);
+        tile_mma<KD, NT, 2, KPD>(s.pj.xs, wb, &s.pj.red[0][0], d, v);
+        if (valid) p.act[(int64_t)er * dff + tile * kCols + ec] = silu_times(v[0], v[1]);
         __syncthreads();
       }
+      stores_done();
     }
     // ------------------------------------------- D: down + residual ----
     {
       VL_IDS;
+      const float* wd = p.w.at(kDown, l);
       TileW<KF, 1> wb;
-      const int tile0 = kUnits * u + unit;
-      load_tile(wb, W.down, 0, tile0, dff, d, tile0 < n_d);
+      load_slice(wb, 0, wd, 0, u, dff, d, u < n_d);
       // x was last written by the W phase, a barrier ago
       float xres = 0.f;
-      if (tile0 < n_d && ut < 256) xres = dev_loadf(p.x + (int64_t)er * d + tile0 * kCols + ec);
+      if (ej == 0 && u < n_d) xres = dev_loadf(p.x + (int64_t)er * d + u * kCols + ec);
       grid_sync(sy);
-      for (int base = 0; base < n_d; base += per_pass) {
-        const int tile = base + tile0;
-        const bool valid = tile < n_d;
+      for (int base = 0; base < n_d; base += NW) {
+        const int tile = base + u;
+        const bool valid = ej == 0 && tile < n_d;
         if (base > 0) {
-          load_tile(wb, W.down, 0, tile, dff, d, valid);
-          if (valid && ut < 256) xres = dev_loadf(p.x + (int64_t)er * d + tile * kCols + ec);
+          load_slice(wb, 0, wd, 0, tile, dff, d, tile < n_d);
+          if (valid) xres = dev_loadf(p.x + (int64_t)er * d + tile * kCols + ec);
         }
         if (base == 0) {
-          stage_rows<KF, KPF>(s.xs, p.act, dff);
+          stage_rows<KF, KPF>(s.pj.xs, p.act, dff);
           __syncthreads();
         }
         float v[1];
-        tile_mma<KF, 1, KPF>(s.xs, wb, &s.red[unit][0][0], dff, v);
-        if (valid && ut < 256) p.x[(int64_t)er * d + tile * kCols + ec] = xres + v[0];
+        tile_mma<KF, 1, 1, KPF>(s.pj.xs, wb, &s.pj.red[0][0], dff, v);
+        if (valid) p.x[(int64_t)er * d + tile * kCols + ec] = xres + v[0];
         __syncthreads();
       }
+      stores_done();
     }
   }
   // ------------------------------------ L: final RMSNorm, lm_head ----
@@ -746,25 +724,24 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(const StepParams 
     VL_IDS;
     TileW<KD, 1> wb;
     float gw[KD / 64];
-    const int tile0 = kUnits * u + unit;
-    load_tile(wb, p.lm_head, 0, tile0, d, p.vocab, tile0 < n_lm);
+    load_slice(wb, 0, p.lm_head, 0, u, d, p.vocab, u < n_lm);
     load_norm<KD>(gw, p.final_norm, d);
     grid_sync(sy);
-    const bool has_tile = kUnits * u < n_lm;  // workgroup-uniform
-    for (int base = 0; base < n_lm; base += per_pass) {
-      const int tile = base + tile0;
-      const bool valid = tile < n_lm;
-      if (base > 0) load_tile(wb, p.lm_head, 0, tile, d, p.vocab, valid);
+    const bool has_tile = u < n_lm;  // workgroup-uniform
+    for (int base = 0; base < n_lm; base += NW) {
+      const int tile = base + u;
+      if (base > 0) load_slice(wb, 0, p.lm_head, 0, tile, d, p.vocab, tile < n_lm);
       if (base == 0) {
-        stage_rows<KD, KPD>(s.xs, p.x, d);
+        stage_rows<KD, KPD>(s.pj.xs, p.x, d);
         __syncthreads();
-        norm_rows<KD, KPD>(s.xs, gw, d, p.eps);
+        norm_rows<KD, KPD>(s.pj.xs, gw, d, p.eps);
         __syncthreads();
       }
       float v[1];
-      tile_mma<KD, 1, KPD>(s.xs, wb, &s.red[unit][0][0], d, v);
+      tile_mma<KD, 1, 1, KPD>(s.pj.xs, wb, &s.pj.red[0][0], d, v);
       const int col = tile * kCols + ec;
-      if (valid && ut < 256 && col < p.vocab) p.logits[(int64_t)er * p.vocab + col] = v[0];
+      if (ej == 0 && tile < n_lm && col < p.vocab)
+        p.logits[(int64_t)er * p.vocab + col] = v[0];
       __syncthreads();
     }
     // the last workgroup with lm_head tiles to finish takes every row's argmax
@@ -773,35 +750,38 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(const StepParams 
     if (tid == 0) {
       s.flag = 0;
       if (has_tile) {
-        const unsigned n_wg = (unsigned)min(NW, cdiv(n_lm, kUnits));
+        const unsigned n_wg = (unsigned)min(NW, n_lm);
         s.flag = l2_add(p.sync + kLmDone, 1u) + 1 == n_wg;
       }
     }
     __syncthreads();
     if (s.flag) {
-      // wavefront r takes row r: numpy's rule, the lowest index of the
-      // maximum, a NaN beating every number (its first index)
+      // wavefront w takes rows w and w + 8: numpy's rule, the lowest index of
+      // the maximum, a NaN beating every number (its first index)
       constexpr int kNone = 0x7fffffff;
-      const int r = wave;
-      const float* row = p.logits + (int64_t)r * p.vocab;
-      float bv = -__builtin_inff();
-      int bi = kNone, ni = kNone;
-      for (int c = lane; c < p.vocab; c += 64) {
-        const float e = dev_loadf(row + c);
-        if (e > bv) bv = e, bi = c;
-        if (e != e && ni == kNone) ni = c;
-      }
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
-        ni = min(ni, __shfl_xor(ni, o, 64));
-      }
-      if (lane == 0) {
-        const int id = ni != kNone ? ni : (bi == kNone ? 0 : bi);
-        p.ids[r] = id;
-        p.host_ids[r] = id;
+      for (int rr = 0; rr < kRows / kTileWaves; ++rr) {
+        const int r = wave + kTileWaves * rr;
+        const float* row = p.logits + (int64_t)r * p.vocab;
+        float bv = -__builtin_inff();
+        int bi = kNone, ni = kNone;
+        for (int c = lane; c < p.vocab; c += 64) {
+          const float e = dev_loadf(row + c);
+          if (e > bv) bv = e, bi = c;
+          if (e != e && ni == kNone) ni = c;
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+          const float ov = __shfl_xor(bv, o, 64);
+          const int oi = __shfl_xor(bi, o, 64);
+          if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
+          ni = min(ni, __shfl_xor(ni, o, 64));
+        }
+        if (lane == 0) {
+          const int id = ni != kNone ? ni : (bi == kNone ? 0 : bi);
+          p.ids[r] = id;
+          p.host_ids[r] = id;
+        }
       }
     }
   }
@@ -822,9 +802,9 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(const StepParams 
 #undef VL_IDS
 }
 
-template <typename TKV, int KD, int KF, int D, int REP>
+template <typename TKV, int KD, int KF, int D, int REP, int NH>
 int launch(const StepParams& prm, int nw, hipStream_t st) {
-  decode_step_kernel<TKV, KD, KF, D, REP><<<nw * kXcds, kThreads, 0, st>>>(prm);
+  decode_step_kernel<TKV, KD, KF, D, REP, NH><<<nw * kXcds, kThreads, 0, st>>>(prm);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
@@ -843,7 +823,8 @@ extern "C" int vl_decode_step_supported(int d_model, int num_heads, int num_kv_h
          d_ff % 16 == 0 && d_ff <= 1024 && max_context > 0 && max_context <= kMaxCtx;
 }
 
-extern "C" int vl_decode_step(const void* layer_weights, int n_layers, const float* tok_emb,
+extern "C" int vl_decode_step(const void* const* layer_weights, const int64_t* layer_strides,
+                              int n_layers, const float* tok_emb,
                               const float* final_norm, const float* lm_head, void* key_cache,
                               void* value_cache, int64_t layer_stride, int kv_dtype,
                               int kv_layout, const int32_t* token_ids, const int32_t* positions,
@@ -867,7 +848,7 @@ extern "C" int vl_decode_step(const void* layer_weights, int n_layers, const flo
                "decode step: bad layer count, vocab, sequence count (<= %d), block size, table "
                "stride or prev_ids length",
                kRows);
-  VL_CHECK_ARG(layer_weights && tok_emb && final_norm && lm_head && key_cache && value_cache &&
+  VL_CHECK_ARG(layer_weights && layer_strides && tok_emb && final_norm && lm_head && key_cache && value_cache &&
                    token_ids && positions && slot_mapping && (seq_lens || !num_seqs) &&
                    (block_tables || !num_seqs) && prev_ids && cos_table && sin_table && x && q &&
                    attn && act && logits && out_ids && out_ids_host && sync,
@@ -882,7 +863,13 @@ extern "C" int vl_decode_step(const void* layer_weights, int n_layers, const flo
                "words 128-byte aligned");
   const int hd = d_model / num_heads;
   StepParams p{};
-  p.layers = static_cast<const StepLayer*>(layer_weights);
+  for (int k = 0; k < kWeightKinds; ++k) {
+    VL_CHECK_ARG(layer_weights[k] && (((uintptr_t)layer_weights[k]) & 15) == 0 &&
+                     (k == kAttnNorm || k == kFfnNorm || layer_strides[k] % 4 == 0),
+                 "decode step: weight buffer %d null or misaligned", k);
+    p.w.base[k] = static_cast<const float*>(layer_weights[k]);
+    p.w.stride[k] = layer_strides[k];
+  }
   p.n_layers = n_layers;
   p.tok_emb = tok_emb;
   p.final_norm = final_norm;
@@ -923,8 +910,10 @@ extern "C" int vl_decode_step(const void* layer_weights, int n_layers, const flo
   const int nw = vl_num_cus() / kXcds;
   VL_CHECK_ARG(nw >= 1, "decode step: fewer than 8 compute units");
   hipStream_t st = (hipStream_t)stream;
-#define VL_STEP_LAUNCH(T, Dh)                                        \
-  if (hd == Dh) return launch<T, 384, 1024, Dh, 2>(p, nw, st);
+#define VL_STEP_LAUNCH(T, Dh)                                                     \
+  if (hd == Dh)                                                                   \
+    return num_kv_heads % 2 ? launch<T, 384, 1024, Dh, 2, 1>(p, nw, st)           \
+                            : launch<T, 384, 1024, Dh, 2, 2>(p, nw, st);
   if (kv_dtype == VL_DTYPE_F32) {
     VL_STEP_LAUNCH(float, 48)
     VL_STEP_LAUNCH(float, 16)

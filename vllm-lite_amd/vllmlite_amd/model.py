@@ -98,12 +98,23 @@ def pack_weights(cfg, w: Dict[str, np.ndarray], torch, device) -> dict:
             "final_norm": dev(w["final_norm"]), "layers": layers}
 
 
-def tile_weights(packed: dict, tile16) -> None:
+def tile_weights(packed: dict, tile16, torch) -> None:
     """Add 16-column tiled copies of the projection weights (suffix `_t`) for
-    the decode-step kernels, which read them in whole cache lines."""
-    for L in packed["layers"]:
+    the decode-step kernels, which read them in whole cache lines. Each kind
+    (the norm weights and the tiled projections) is then stacked into one
+    [n_layers, ...] buffer (packed["stacked"]), and the per-layer entries
+    become views of it: the one-launch decode step finds a layer's weights at
+    a fixed stride from the first."""
+    layers = packed["layers"]
+    for L in layers:
         L["w_qkv_t"] = tile16(L["w_qkv"])
         L["wo_t"] = tile16(L["wo"])
         L["w_gate_up_t"] = tile16(L["w_gate_up"], 2)
         L["w_down_t"] = tile16(L["w_down"])
     packed["lm_head_t"] = tile16(packed["lm_head"])
+    packed["stacked"] = {}
+    for key in ("attn_norm", "w_qkv_t", "wo_t", "ffn_norm", "w_gate_up_t", "w_down_t"):
+        all_ = torch.stack([L[key] for L in layers]).contiguous()
+        packed["stacked"][key] = all_
+        for i, L in enumerate(layers):
+            L[key] = all_[i]

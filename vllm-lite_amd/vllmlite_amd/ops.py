@@ -69,7 +69,7 @@ SIGNATURES = {
                                  _i32, _i32, _i32, _c_void_p]),
     "vl_resolve_tokens": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p]),
     "vl_decode_step_supported": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32]),
-    "vl_decode_step": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+    "vl_decode_step": (_i32, [_c_void_p, _c_void_p, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                               _c_void_p, _i64, _i32, _i32, _c_void_p, _c_void_p, _c_void_p,
                               _c_void_p, _c_void_p, _i32, _i32, _c_void_p, _i32, _c_void_p,
                               _c_void_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _f32,
@@ -543,17 +543,24 @@ def decode_step_supported(d_model: int, num_heads: int, num_kv_heads: int, d_ff:
 
 
 class DecodeStep:
-    """What vl_decode_step keeps between launches: the device table of each
-    layer's weight addresses (attn_norm, tiled QKV, tiled wo, ffn_norm, tiled
-    gate|up, tiled w_down) and the launch's sync words (zero-filled here; every
-    launch leaves them zero)."""
+    """What vl_decode_step keeps between launches: the 6 weight buffers of
+    the layers (attn_norm, tiled QKV, tiled wo, ffn_norm, tiled gate|up,
+    tiled w_down, each [n_layers, ...] with a fixed layer stride, as
+    model.tile_weights stacks them) as a host array of addresses and strides,
+    and the launch's sync words (zero-filled here; every launch leaves them
+    zero)."""
 
     FIELDS = ("attn_norm", "w_qkv_t", "wo_t", "ffn_norm", "w_gate_up_t", "w_down_t")
 
     def __init__(self, packed: dict, device):
-        self.layers = packed["layers"]
-        ptrs = [L[f].data_ptr() for L in self.layers for f in self.FIELDS]
-        self.table = torch.tensor(ptrs, dtype=torch.int64, device=device)
+        self.n_layers = len(packed["layers"])
+        bufs = [packed["stacked"][f] for f in self.FIELDS]
+        for b in bufs:
+            _need(b.is_contiguous() and b.shape[0] == self.n_layers and b.dtype == torch.float32,
+                  "stacked fp32 weights [n_layers, ...]")
+        self._bufs = bufs
+        self.addrs = (ctypes.c_void_p * 6)(*[b.data_ptr() for b in bufs])
+        self.strides = (ctypes.c_int64 * 6)(*[b[0].numel() for b in bufs])
         self.sync = torch.zeros(128, dtype=torch.int32, device=device)
         _need(self.sync.data_ptr() % 128 == 0, "sync words must be 128-byte aligned")
 
@@ -567,7 +574,7 @@ def decode_step(ds: DecodeStep, tok_emb, final_norm, lm_head_t, key_cache, value
     seq_lens / block_tables [num_seqs <= 16, W]; the argmax ids land in
     out_ids[:16] and the pinned out_ids_host[:16]; the caller zeroes
     out_ids_host[16], which is non-zero afterwards if the launch failed."""
-    n_layers = len(ds.layers)
+    n_layers = ds.n_layers
     R = DECODE_STEP_ROWS
     _need(key_cache.shape == value_cache.shape and key_cache.shape[0] == n_layers and
           key_cache.is_contiguous() and value_cache.is_contiguous(),
@@ -595,7 +602,7 @@ def decode_step(ds: DecodeStep, tok_emb, final_norm, lm_head_t, key_cache, value
           out_ids_host.is_contiguous() and out_ids_host.numel() > R,
           "out_ids_host must be a pinned int32 tensor of at least 17 entries")
     _check(lib().vl_decode_step(
-        _ptr(ds.table), n_layers, _ptr(tok_emb), _ptr(final_norm), _ptr(lm_head_t),
+        ds.addrs, ds.strides, n_layers, _ptr(tok_emb), _ptr(final_norm), _ptr(lm_head_t),
         _ptr(key_cache), _ptr(value_cache), key_cache[0].numel(), cdt, layout, _ptr(token_ids),
         _ptr(positions), _ptr(slot_mapping), _ptr(seq_lens), _ptr(block_tables),
         block_tables.stride(0), seq_lens.numel(), _ptr(prev_ids), prev_ids.numel(), _ptr(cos),
