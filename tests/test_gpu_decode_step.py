@@ -4,10 +4,12 @@ the argmax of every row, vllmlite/sampling.py:56-57) against the same steps
 on this library's separate kernels, and end to end against the reference.
 
 Both runners see the same scheduled batches (the engine drives the first and
-the second is handed each batch too), so their caches evolve identically; the
-one-launch kernel performs the separate kernels' operations in the same
-order, so every decode step's logits must be equal bit for bit, and its ids
-equal the host argmax of those logits."""
+the second is handed each batch too), so their caches evolve identically.
+The projections are the same operations in the same order; the attention
+sums in another order, so every decode step's logits must agree within 1e-5
+of the row's largest logit (1e-3 with a bf16 or FP8 cache), and the ids equal the host argmax of the
+separate kernels' logits wherever that row's top-1 / top-2 margin exceeds
+1e-4 (a near-tie may go either way)."""
 
 import json
 import os
@@ -31,8 +33,9 @@ class _Twin:
     """execute() / execute_argmax() on the one-launch runner, each batch also
     run through a runner without it; every result compared."""
 
-    def __init__(self, cfg):
+    def __init__(self, cfg, tol=1e-5):
         from vllmlite_amd.hip_runner import HipRunner
+        self.tol = tol
         self.a = HipRunner(cfg.model, cfg.cache, one_launch_decode=True)
         self.b = HipRunner(cfg.model, cfg.cache, one_launch_decode=False)
         assert self.a._step is not None, "no one-launch kernel for this shape"
@@ -46,7 +49,8 @@ class _Twin:
         assert rows == rows_b
         if self.a.one_launch_steps > n0:
             self.decode_steps += 1
-            assert np.array_equal(la, lb), np.abs(la - lb).max()
+            scale = np.abs(lb).max(axis=-1, keepdims=True)
+            assert np.all(np.abs(la - lb) <= self.tol * scale), np.abs(la - lb).max()
         return la, rows
 
     def execute_argmax(self, out):
@@ -55,12 +59,15 @@ class _Twin:
         lb, _ = self.b.execute(out)
         if self.a.one_launch_steps > n0:
             self.decode_steps += 1
-        assert np.array_equal(ia, np.argmax(lb, axis=-1).astype(ia.dtype))
+        want = np.argmax(lb, axis=-1)
+        top2 = np.sort(lb, axis=-1)[:, -2:]
+        clear = top2[:, 1] - top2[:, 0] > 1e-4
+        assert np.array_equal(ia[clear], want[clear])
         return ia, rows
 
 
-def _drive(cfg, reqs, argmax):
-    twin = _Twin(cfg)
+def _drive(cfg, reqs, argmax, tol=1e-5):
+    twin = _Twin(cfg, tol)
     eng = LLMEngine(cfg, runner=twin, lookahead=False)
     eng.device_argmax = argmax
     for rid, ids, p in reqs:
@@ -73,7 +80,7 @@ def _drive(cfg, reqs, argmax):
 @pytest.mark.parametrize("layout", ["token", "head"])
 def test_cfg0_mix_decode_steps_equal_separate_kernels(layout):
     """The 48-request TinyLlama mix (6 layers, d 384, H8/Hkv4, d_ff 1024):
-    228 decode steps in one launch each, logits bitwise those of the separate
+    228 decode steps in one launch each, logits those of the separate
     kernels, streams the reference's."""
     g = json.load(open(os.path.join(GOLD, "cfg0_streams.json")))
     cfg = cfg0_config(False)
@@ -94,10 +101,13 @@ def test_cfg0_mix_device_argmax_ids():
 @pytest.mark.parametrize("kv_dtype", ["bfloat16", "float8_e4m3"])
 def test_narrow_cache_decode_steps_equal_separate_kernels(kv_dtype):
     """bf16 and FP8 E4M3 caches: the one-launch kernel rounds the K/V it
-    writes as the separate kernels do, and reads the cache the same way."""
+    writes as the separate kernels do, and widens the cache the same way.
+    Bar 1e-3 of the row's largest logit, as for the narrow caches against the
+    oracle runner: K/V computed from inputs ~1e-6 apart can round one cache
+    step apart."""
     cfg = cfg0_config(False)
     cfg.cache.kv_dtype = kv_dtype
-    _, twin = _drive(cfg, mixed_lengths(0, 48, 0)[:24], argmax=False)
+    _, twin = _drive(cfg, mixed_lengths(0, 48, 0)[:24], argmax=False, tol=1e-3)
     assert twin.decode_steps >= 100
 
 

@@ -32,7 +32,6 @@
 #include <type_traits>
 
 #include "vl_common.h"
-#include "decode_item.h"
 
 namespace {
 
@@ -1777,64 +1776,178 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
 // Decode batches of short sequences (every sequence at most one query and at
 // most kShortCtx tokens) for head dims up to 64: one workgroup per
 // (sequence, KV head) takes the whole context, so the call needs no plan, no
-// context split and no merge launch. The sequence's block table and the
-// query heads are staged in LDS first; the item itself is vl_item's
-// 8-wavefront decode item (decode_item.h): 256-key chunks, two lanes per key
-// for QK (half a row each), a per-wavefront online softmax by DPP, PV on
-// 16-byte V chunks, the wavefronts merged in LDS at the end. The one-launch
-// decode step runs the same item code, so the two compute the same values.
-constexpr int kShortCtx = vl_item::kMaxCtx;
+// context split and no merge launch. The sequence's block table is staged in
+// LDS first, so that the K and V loads of a 256-key chunk (wavefront w takes
+// keys 64 (4 t + w) + lane of chunk t) are issued together:
+//   QK: lane l holds key l of its wavefront's 64, its K row in registers,
+//       and the dot products with the REP query heads (LDS broadcast reads);
+//   softmax: per head, the wavefront max by DPP row operations (no LDS
+//       round trips), merged online across chunks; each lane keeps the sum of
+//       its own keys' weights until the end; the weights go to the
+//       wavefront's LDS row;
+//   PV: lane l = g NC + c (NC 16-byte chunks per head row, G = 64 / NC key
+//       groups) sums chunk c over keys g, g + G, ... of the chunk, its V
+//       chunks loaded with the K row.
+// At the end the wavefronts' lanes are merged in LDS (max-rescaled), one
+// head at a time, and every (head, dim) written once. Keys past the context
+// re-read the last key (finite values) and get weight 0.
+constexpr int kShortCtx = 2048;
+
+template <typename TKV, int D, int REP>
+struct ShortLds {
+  static constexpr int kVE = 16 / (int)sizeof(TKV);  // cache elements per 16-byte load
+  float q[REP][D];          // query heads, pre-scaled to the log2 domain
+  float p[4][REP][64];      // per wavefront: the chunk's weights
+  float red[4][64][kVE];    // per wavefront and lane: one head's PV sums
+  float m[4][REP], l[4][REP];
+  int32_t tbl[kShortCtx];   // the sequence's block ids
+};
+
+
+
+
+// A head row of D elements of T as floats (16-byte loads).
+template <typename T, int D>
+__device__ __forceinline__ void load_row(const T* p, float (&r)[D]) {
+  constexpr int VE = 16 / (int)sizeof(T);
+#pragma unroll
+  for (int c = 0; c < D / VE; ++c) {
+    const uint4 v = reinterpret_cast<const uint4*>(p)[c];
+    widen16<T>(v, r + VE * c);
+  }
+}
 
 // T: query and output elements, TKV: cache elements.
 template <typename T, typename TKV, int D, int REP>
-__global__ void __launch_bounds__(vl_item::kThreads) attend_short_decode_kernel(
+__global__ void __launch_bounds__(256) attend_short_decode_kernel(
     T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const TKV* kc,
     const TKV* vc, const int32_t* __restrict__ bt, int bt_stride,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int Hkv, int bs_log2,
     int kv_hm, float scale_log2) {
-  namespace it = vl_item;
-  __shared__ it::Lds<TKV, D, REP> s;
-  __shared__ int32_t tbl[it::kMaxCtx];
+  using Lds = ShortLds<TKV, D, REP>;
+  constexpr int VE = Lds::kVE;
+  static_assert(D % VE == 0 && D <= 64, "head_dim");
+  constexpr int NC = D / VE;               // 16-byte chunks per head row
+  constexpr int G = 64 / NC;               // PV key groups
+  constexpr int KPL = (64 + G - 1) / G;    // keys per lane in the PV product
+  __shared__ Lds s;
   const int i = blockIdx.x / Hkv, g = blockIdx.x - (blockIdx.x / Hkv) * Hkv;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int c = seq_lens[i];
   // a sequence without exactly one query, or longer than the staged table,
   // is not this kernel's (the bounds the caller stated do not hold)
-  if (qsl[i + 1] - qsl[i] != 1 || c <= 0 || c > it::kMaxCtx) return;
+  if (qsl[i + 1] - qsl[i] != 1 || c <= 0 || c > kShortCtx) return;
   const int tok = qsl[i];
-  const int nblk = (c + (1 << bs_log2) - 1) >> bs_log2;
+  const int bs_mask = (1 << bs_log2) - 1;
+  const int nblk = (c + bs_mask) >> bs_log2;
   const int32_t* table = bt + (int64_t)i * bt_stride;
-  for (int b = tid; b < nblk; b += it::kThreads) tbl[b] = table[b];
-  for (int e = tid; e < REP * D; e += it::kThreads) {
+  for (int b = tid; b < nblk; b += 256) s.tbl[b] = table[b];
+  for (int e = tid; e < REP * D; e += 256) {
     const int h = e / D, d = e - (e / D) * D;
     s.q[h][d] = Elem<T>::load(query, (int64_t)tok * q_stride + (int64_t)(g * REP + h) * D + d) *
                 scale_log2;
   }
   __syncthreads();
-  it::Src<TKV> a;
-  a.tbl = tbl;
-  a.kc = kc;
-  a.vc = vc;
-  a.geom.bs_log2 = kv_hm ? bs_log2 : 0;
-  a.geom.head = kv_hm ? (int64_t)D << bs_log2 : D;
-  a.geom.row = kv_hm ? D : (int64_t)Hkv * D;
-  a.geom.blk = kv_hm ? (int64_t)Hkv * D << bs_log2 : (int64_t)Hkv * D;
-  a.g = g;
-  a.c = c;
-  a.bs_log2 = bs_log2;
-  a.rk = a.rv = it::cache_rsrc(kc, 0);  // no device-scope loads here
-  it::State<it::Shape<TKV, D, REP>::VE, REP> st;
-  st.init();
-  const int nchunk = (c + it::kChunk - 1) / it::kChunk;
+  // row of key k of KV head g: block * blk + offset * row + g * head
+  // (token-major: row Hkv * D, head D; head-major: row D, head bs * D)
+  const int64_t blk = (int64_t)Hkv * D << bs_log2;
+  const int64_t row = kv_hm ? D : (int64_t)Hkv * D;
+  const TKV* kg = kc + (int64_t)g * (kv_hm ? (int64_t)D << bs_log2 : D);
+  const TKV* vg = vc + (kg - kc);
+  auto row_of = [&](int k) { return s.tbl[k >> bs_log2] * blk + (k & bs_mask) * row; };
+  const int pg = lane / NC, pc = lane - (lane / NC) * NC;  // PV: key group, chunk
+  float m[REP], lsum[REP], acc[REP][VE];
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+    m[h] = -__builtin_inff(), lsum[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) acc[h][e] = 0.f;
+  }
+  const int nchunk = (c + 255) >> 8;
   for (int t = 0; t < nchunk; ++t) {
-    it::Regs<TKV, D, REP> r;
-    it::issue<false>(r, a, t, w, lane, -1, false);
-    it::compute(st, r, s, c, t, w, lane);
+    const int base = (4 * t + wave) * 64;
+    if (base >= c) break;  // wavefront-uniform; later chunks start later still
+    // every load of the chunk first: the lane's K row and its V chunks
+    float kr[D];
+    load_row<TKV, D>(kg + row_of(min(base + lane, c - 1)), kr);
+    uint4 vraw[KPL];
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      const int kk = min(pg + G * j, 63);  // past the chunk (or lanes past G NC): weight 0
+      vraw[j] = *reinterpret_cast<const uint4*>(vg + row_of(min(base + kk, c - 1)) + pc * VE);
+    }
+    const bool valid = base + lane < c;
+#pragma unroll
+    for (int h = 0; h < REP; ++h) {
+      float a = 0.f;
+#pragma unroll
+      for (int d = 0; d < D; ++d) a = __builtin_fmaf(s.q[h][d], kr[d], a);
+      const float sc = valid ? a : -__builtin_inff();
+      const float mn = fmaxf(m[h], wave_max_dpp(sc));  // finite: key base is valid
+      const float alpha = exp2_fast(m[h] - mn);
+      const float p = exp2_fast(sc - mn);
+      lsum[h] = __builtin_fmaf(lsum[h], alpha, p);
+#pragma unroll
+      for (int e = 0; e < VE; ++e) acc[h][e] *= alpha;
+      m[h] = mn;
+      s.p[wave][h][lane] = p;
+    }
+    // the weights the wavefront's other lanes wrote above
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int j = 0; j < KPL; ++j) {
+      const int kk = pg + G * j;
+      float v[VE];
+      widen16<TKV>(vraw[j], v);
+#pragma unroll
+      for (int h = 0; h < REP; ++h) {
+        const float w = kk < 64 ? s.p[wave][h][kk] : 0.f;
+#pragma unroll
+        for (int e = 0; e < VE; ++e) acc[h][e] = __builtin_fmaf(w, v[e], acc[h][e]);
+      }
+    }
+    // the weights have been read before the next chunk overwrites them
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+#pragma unroll
+  for (int h = 0; h < REP; ++h) lsum[h] = wave_sum_dpp(lsum[h]);
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < REP; ++h) s.m[wave][h] = m[h], s.l[wave][h] = lsum[h];
   }
   const int H = Hkv * REP;
-  it::finish(st, s, true, tid, w, lane, [&](int h, int d, float v) {
-    Elem<T>::store(out, ((int64_t)tok * H + g * REP + h) * D + d, v);
-  });
+  // one head at a time: every lane's sums to LDS, then thread d < D adds
+  // dim d over the key groups of each wavefront, max-rescaled across them
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+#pragma unroll
+    for (int e = 0; e < VE; ++e) s.red[wave][lane][e] = acc[h][e];
+    __syncthreads();
+    if (tid < D) {
+      const int d = tid, dc = d / VE, de = d - (d / VE) * VE;
+      float M = -__builtin_inff();
+#pragma unroll
+      for (int w = 0; w < 4; ++w) M = fmaxf(M, s.m[w][h]);
+      float L = 0.f, a = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float mw = s.m[w][h];
+        if (mw == -__builtin_inff()) continue;
+        const float wt = exp2_fast(mw - M);
+        float sw = 0.f;
+#pragma unroll
+        for (int gg = 0; gg < G; ++gg) sw += s.red[w][gg * NC + dc][de];
+        L = __builtin_fmaf(s.l[w][h], wt, L);
+        a = __builtin_fmaf(sw, wt, a);
+      }
+      Elem<T>::store(out, ((int64_t)tok * H + g * REP + h) * D + d, L > 0.f ? a * (1.f / L) : 0.f);
+    }
+    __syncthreads();
+  }
 }
 
 // ------------------------------------------------------------------ step --
@@ -2168,7 +2281,7 @@ int launch_short_decode_d(const Args& a, float sl2, hipStream_t st) {
   if (grid == 0) return VL_OK;
   const int bs_log2 = __builtin_ctz((unsigned)a.bs);
 #define VL_SHORT(REP)                                                                        \
-  attend_short_decode_kernel<T, TKV, D, REP><<<grid, vl_item::kThreads, 0, st>>>(             \
+  attend_short_decode_kernel<T, TKV, D, REP><<<grid, 256, 0, st>>>(                          \
       (T*)a.out, (const T*)a.query, a.q_stride, (const TKV*)a.kc, (const TKV*)a.vc, a.bt,    \
       a.bt_stride, a.seq_lens, a.qsl, a.Hkv, bs_log2, a.kv_layout == VL_KV_HEAD_MAJOR ? 1 : 0, sl2)
   switch (rep) {

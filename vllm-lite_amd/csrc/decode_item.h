@@ -1,11 +1,9 @@
-// One decode attention item: the REP query heads of one token of a sequence
-// over its c keys in one KV head of a paged cache (vllmlite/attention.py:59-98
-// for a sequence with one query: no causal mask, softmax over every key),
-// computed by 8 wavefronts. The short-decode kernel runs one item per
-// workgroup; the one-launch decode step runs two per workgroup, and issues a
-// chunk's loads before the barrier that precedes its attention phase. Both
-// call these functions, so both compute every output with the same
-// operations in the same order.
+// One decode attention item of the one-launch decode step: the REP query
+// heads of one token of a sequence over its c keys in one KV head of a paged
+// cache (vllmlite/attention.py:59-98 for a sequence with one query: no
+// causal mask, softmax over every key), computed by 8 wavefronts; the step
+// runs one item per KV head of its sequence, and issues a chunk's loads
+// before the barrier that precedes its attention phase.
 //
 // Keys come in chunks of 256: wavefront w of chunk t takes keys 32 (8 t + w)
 // + kk, kk < 32. QK: lanes kk and kk + 32 each hold half of key kk's row

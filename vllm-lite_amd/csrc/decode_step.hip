@@ -41,13 +41,14 @@
 // so consecutive launches on one stream reuse the sync words without a
 // memset.
 //
-// Arithmetic: the same operations in the same order as the separate kernels
-// of this library (vl_qkv_rope_cache, the short-decode attention,
-// vl_linear_rows, vl_argmax_rows): 16 x 16 projection tiles on
-// v_mfma_f32_16x16x4f32 with K split over 8 wavefronts and their partial
-// tiles summed in wavefront order, RMSNorm over k = lane + 64 i then across
-// the wavefront, RoPE / SwiGLU rounded as numpy rounds them, and per
-// (sequence, KV head) attention by 4 wavefronts over 256-key chunks.
+// Arithmetic: the projections perform the same operations in the same order
+// as this library's separate kernels (vl_qkv_rope_cache, vl_linear_rows):
+// 16 x 16 tiles on v_mfma_f32_16x16x4f32 with K split over 8 wavefronts and
+// their partial tiles summed in wavefront order, RMSNorm over k = lane + 64 i
+// then across the wavefront, RoPE / SwiGLU rounded as numpy rounds them; the
+// attention is decode_item.h's 8-wavefront item (the short-decode kernel
+// sums in another order, so logits agree to ~1e-6, not bit for bit); the
+// argmax follows numpy's rule as vl_argmax_rows does.
 #include "vl_common.h"
 #include "decode_item.h"
 

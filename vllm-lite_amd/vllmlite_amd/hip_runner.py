@@ -30,9 +30,9 @@ With one_launch_decode = True, a decode step of at most 16 sequences
 (ops.decode_step_supported) runs instead as ONE launch, vl_decode_step, on
 the compute units of one XCD: the whole forward, the logits rows and the
 argmax of each row, written to device memory and to the pinned host buffer of
-the step. It computes the same values as the separate kernels, bit for bit;
-it is off by default because on the 48-request mix it takes longer per step
-(268 against 202 us).
+the step. Its logits agree with the separate kernels' to ~1e-6 (the
+attention sums in another order); it is off by default because on the
+48-request mix it takes longer per step (268 against 202 us).
 
 Step 3 is otherwise captured once per shape bucket (tokens, sequences and logits rows
 each rounded up to a power of two) into a HIP graph and replayed afterwards;
