@@ -502,3 +502,43 @@ def test_lookahead_across_buffer_growth():
             eng.step()
         got.append([eng.seqs[i].output_token_ids for i in ids])
     assert got[0] == got[1]
+
+
+def test_steps_from_rotating_worker_threads():
+    """The reference's async engine calls engine.step through
+    run_in_executor (vllmlite/async_engine.py:38-53), so each step may run on
+    another thread. Three single-thread executors take the steps of the
+    48-request mix in turn: with the lookahead, a step launched on one thread
+    is collected on the next. First with a fresh runner (its graphs captured
+    on worker threads), then again with the same runner from other workers
+    (graphs captured on one thread, replayed on others). Streams equal the
+    reference's both times."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    from vllmlite_amd.hip_runner import HipRunner
+    g = _gold("cfg0_streams.json")
+    cfg = cfg0_config(False)
+    runner = HipRunner(cfg.model, cfg.cache)
+    for rotation in range(2):
+        pools = [ThreadPoolExecutor(max_workers=1) for _ in range(3)]
+        try:
+            threads = set()
+            eng = LLMEngine(cfg, runner=runner)
+            for rid, ids, p in mixed_lengths(0, 48, 0):
+                eng.add_request(params=p, request_id=rid, prompt_token_ids=ids)
+            k = 0
+
+            def step():
+                import threading
+                threads.add(threading.get_ident())
+                return eng.step()
+
+            while eng.has_work:
+                pools[(k + rotation) % 3].submit(step).result()
+                k += 1
+            assert len(threads) == 3 and eng.total_steps == g["steps"]
+            for rid, want in g["streams"].items():
+                assert eng.seqs[rid].output_token_ids == want, (rotation, rid)
+        finally:
+            for p in pools:
+                p.shutdown()
