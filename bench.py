@@ -433,6 +433,59 @@ def run_mix(runner, cfg, name):
     return wall, eng.total_output_tokens, eng.total_steps, streams, counter.pairs if fork else 0
 
 
+class _ZeroRunner:
+    """A runner that computes nothing (zero logits): with greedy, ignore_eos
+    requests the schedule does not depend on the tokens, so it replays the
+    mix's batches for mix_floor."""
+
+    def __init__(self, vocab):
+        self.vocab_size = vocab
+        self.batches = []
+
+    def execute(self, out):
+        rows, R = [], 0
+        for item in out.scheduled:
+            c = min(1 + len(item.seq.draft_token_ids), item.num_tokens)
+            rows.append((R, c))
+            R += c
+        self.batches.append([(item.start_pos, item.num_tokens) for item in out.scheduled])
+        return np.zeros((R, self.vocab_size), np.float32), rows
+
+
+def mix_floor(cfg, name):
+    """The device floor of a mix at 8 TB/s: per step, every weight once (the
+    layers' projections and norms, lm_head, the embedding rows of the step's
+    tokens) plus every K/V element the step's attention reads (each
+    sequence's context, all layers) and writes (its new tokens), summed over
+    the mix's steps."""
+    from vllmlite_amd.engine import LLMEngine
+    from vllmlite_amd.workload import drive_forked, mixed_lengths
+    mc = cfg.model
+    shared, fork = MIXES[name]
+    zr = _ZeroRunner(mc.vocab_size)
+    eng = LLMEngine(cfg, runner=zr)
+    reqs = mixed_lengths(0, 48, shared)
+    if fork:
+        drive_forked(eng, reqs)
+    else:
+        for rid, ids, p in reqs:
+            eng.add_request(params=p, request_id=rid, prompt_token_ids=ids)
+        while eng.has_work:
+            eng.step()
+    d, hd, f = mc.d_model, mc.head_dim, mc.d_ff
+    per_layer = (d * (mc.n_heads + 2 * mc.n_kv_heads) * hd + mc.n_heads * hd * d
+                 + 2 * d * f + f * d + 2 * d) * 4
+    weights = mc.n_layers * per_layer + (d * mc.vocab_size + d) * 4
+    es = {"bfloat16": 2, "float8_e4m3": 1}.get(cfg.cache.kv_dtype, 4)
+    row = mc.n_kv_heads * hd * es * 2 * mc.n_layers  # K and V of one token, every layer
+    total = 0
+    for b in zr.batches:
+        toks = sum(n for _, n in b)
+        total += weights + toks * d * 4 + sum((st + n) * row + n * row for st, n in b)
+    return {"steps": len(zr.batches), "bytes_per_step": round(total / len(zr.batches)),
+            "floor_us_per_step": round(total / len(zr.batches) / PEAK_HBM_GBS / 1e3, 2)}
+
+
 class _CowCounter:
     """A runner wrapper that counts the copy-on-write pairs it is handed."""
 
@@ -479,6 +532,16 @@ def e2e_leg(name="mixed", repeat=3, cpu=True):
                         "16 seqs, budget 1024"),
            "output_tok_per_s": round(toks / wall, 1), "wall_s": round(wall, 4),
            "steps": steps, "us_per_step": round(wall / steps * 1e6, 1), "output_tokens": toks}
+    fl = mix_floor(cfg, name)
+    out["roofline"] = {
+        "bound": "hbm (weights + K/V per step at 8 TB/s; the steps are launch- and "
+                 "latency-bound far above it)",
+        "floor_us_per_step": fl["floor_us_per_step"], "bytes_per_step": fl["bytes_per_step"],
+        "frac": round(fl["floor_us_per_step"] / (wall / steps * 1e6), 4),
+        "device_launches_per_decode_step": 6 * 5 + 4,
+        "launches_are": "per layer QKV+RoPE+scatter, attention, wo+residual, "
+                        "norm+gate|up+SwiGLU, down+residual; then lm_head, the argmax, the "
+                        "placeholder resolve and the step record's host-to-device copy"}
     if fork:
         out["cow_pairs"] = pairs
     fixture, key = (("cfg0_streams.json", None) if name.startswith("mixed") else
