@@ -1,0 +1,96 @@
+"""A CPU replay of the work-claiming protocol of the persistent attention
+kernels (attend_step_bf16_kernel and leave_and_reset, csrc/attention.hip):
+workgroups as coroutines that interleave their atomic operations in random
+orders. Each kernel's counters are touched only by atomic operations on
+single words, so any interleaving of those operations is a possible
+execution; the replay checks, over many random ones and back-to-back
+launches of different shapes:
+
+  * every item of every queue is run exactly once and no item index at or
+    past its queue's length reaches an item body (the bodies index the plan's
+    arrays with it);
+  * the counters are all zero again when a launch ends (the last workgroup to
+    leave resets them), so the next launch starts from zero without a memset.
+"""
+
+import random
+
+XCDS = 8
+
+
+def step_workgroup(b, grid, n_dec, n_tiles, ctr, ran, tile_first_every=2):
+    """attend_step_bf16_kernel's claim loop for workgroup b; yields at every
+    atomic operation on the counters (ctr[0] decode queue, ctr[1 + x] tile
+    queue x, ctr[9] workgroups finished)."""
+    xcd = b % XCDS
+    tiles_first = (b // XCDS) % tile_first_every == 0
+    for v in range(XCDS + 1):
+        if tiles_first:
+            qid = 1 + (xcd + v) % XCDS if v < XCDS else 0
+        else:
+            qid = 0 if v == 0 else 1 + (xcd + v - 1) % XCDS
+        tiles = qid != 0
+        stride, base = (XCDS, qid - 1) if tiles else (1, 0)
+        n = n_tiles if tiles else n_dec
+        yield
+        seen = ctr[qid]  # an atomic load
+        if seen * stride + base >= n:
+            continue
+        yield
+        claim = ctr[qid]
+        ctr[qid] += 1  # atomicAdd
+        it = claim * stride + base
+        while it < n:
+            yield
+            nxt = ctr[qid]
+            ctr[qid] += 1  # the next item, claimed before this one runs
+            assert 0 <= it < n
+            ran.append((qid == 0, it))
+            it = nxt * stride + base
+    # leave_and_reset(counters, 9)
+    yield
+    prev = ctr[9]
+    ctr[9] += 1
+    if prev == grid - 1:
+        for k in range(10):
+            yield
+            ctr[k] = 0
+
+
+def run_launch(rng, grid, n_dec, n_tiles, ctr):
+    ran = []
+    live = [step_workgroup(b, grid, n_dec, n_tiles, ctr, ran) for b in range(grid)]
+    while live:
+        g = rng.choice(live)
+        try:
+            next(g)
+        except StopIteration:
+            live.remove(g)
+    return ran
+
+
+def test_every_item_runs_once_and_counters_return_to_zero():
+    rng = random.Random(0)
+    ctr = [0] * 10
+    for trial in range(300):
+        grid = rng.choice([1, 2, 8, 9, 16, 24, 64])
+        n_dec = rng.choice([0, 1, 5, 8, 40, 200])
+        n_tiles = rng.choice([0, 1, 7, 8, 16, 33, 96])
+        ran = run_launch(rng, grid, n_dec, n_tiles, ctr)
+        dec = sorted(it for d, it in ran if d)
+        til = sorted(it for d, it in ran if not d)
+        assert dec == list(range(n_dec)), (trial, grid, n_dec)
+        assert til == list(range(n_tiles)), (trial, grid, n_tiles)
+        assert ctr == [0] * 10, (trial, ctr)
+
+
+def test_a_launch_without_its_reset_would_skip_items():
+    """The check above has teeth: counters left non-zero by a launch that did
+    not reset them make the next launch skip items (never run one twice or
+    past its queue: the claim bound holds against any start value)."""
+    rng = random.Random(1)
+    ctr = [0] * 10
+    ctr[0] = 3  # a stale decode counter
+    ran = run_launch(rng, 8, 10, 0, ctr)
+    dec = sorted(it for d, it in ran if d)
+    assert dec == list(range(3, 10))
