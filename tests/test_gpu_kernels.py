@@ -457,6 +457,37 @@ def test_bandwidth_decode_chunks_without_split():
     check(got, expected(b, "bf16"), "bf16")
 
 
+def many_sequences(S, seed):
+    """S sequences, mostly decodes: a run of equal contexts (one tail-range
+    bucket for all of them), contexts of 1..130 keys (split into 64-key
+    ranges when the decode tokens are few), and every tenth sequence a
+    multi-query chunk of 2..20 queries."""
+    rng = np.random.default_rng(seed)
+    seqs = [(1, 77)] * (S // 4)
+    for i in range(S - len(seqs)):
+        if i % 10 == 9:
+            q = int(rng.integers(2, 21))
+            seqs.append((q, q + int(rng.integers(0, 60))))
+        else:
+            seqs.append((1, int(rng.integers(1, 131))))
+    order = rng.permutation(S)
+    return [seqs[i] for i in order]
+
+
+@pytest.mark.parametrize("small_ws", [False, True])
+@pytest.mark.parametrize("S", [300, 1100])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_plans_over_many_sequences(S, dtype, small_ws):
+    """The plan with several sequences per plan thread: from registers (300)
+    and re-read from memory (1100, above what a plan thread caches); with the
+    smallest workspace the plan doubles its range and partition lengths
+    until nothing splits."""
+    o = ops()
+    b = make_batch(many_sequences(S, seed=S), 16, 4, 128, 16, seed=S)
+    ws = o.lib().vl_paged_attention_min_workspace(S) if small_ws else None
+    check(run_attention(b, dtype, ws_bytes=ws), expected(b, dtype), dtype)
+
+
 def test_bandwidth_decode_with_16_kv_heads():
     b = make_batch([(1, c) for c in (33, 600)], 64, 16, 128, 16, seed=13)
     check(run_attention(b, "bf16"), expected(b, "bf16"), "bf16")

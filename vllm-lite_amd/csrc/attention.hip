@@ -49,7 +49,7 @@ constexpr int kHdrInts = 64;  // [0] bandwidth-kernel items [1] generic items [2
                               // [26..33] 16-row tile kernel: work counters of its 8
                               // queues; [34..41] the same for the 32-row kernel
                               // (zeroed by the plan, then by every combine launch)
-constexpr int kPlanThreads = 1024;
+constexpr int kPlanThreads = 256;
 constexpr int kMaxHeadDim = 256;
 constexpr int kSplitMaxQ = 16;  // only sequences with <= this many queries split their context
 #ifndef VL_PART0
@@ -303,7 +303,94 @@ constexpr int kItemsPerWg = VL_ITEMS_PER_WG;  // decode items aimed for per resi
 #endif
 constexpr int kTileItemsPerWg = VL_TILE_ITEMS_PER_WG;  // split tile items aimed for per workgroup
 constexpr int kTailBuckets = 1024;
-static_assert(kTailBuckets == kPlanThreads, "one tail bucket per plan thread");
+constexpr int kPlanBuckets = kTailBuckets / kPlanThreads;  // buckets owned by each plan thread
+constexpr int kPlanRegSeqs = 4;  // sequences a plan thread keeps in registers (S <= 1024)
+static_assert(kTailBuckets % kPlanThreads == 0, "whole tail buckets per plan thread");
+
+// Sums of N 64-bit values over the plan workgroup. red is this call's own LDS
+// slot (a later call that reuses it must come after a barrier that follows
+// every thread's reads here); every thread gets the totals.
+template <int N>
+__device__ __forceinline__ void plan_sum(unsigned long long (&v)[N],
+                                         unsigned long long (*red)[N]) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < N; ++k)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v[k] += __shfl_xor(v[k], o, 64);
+  if (lane == 0)
+#pragma unroll
+    for (int k = 0; k < N; ++k) red[w][k] = v[k];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < N; ++k) {
+    unsigned long long s = 0;
+#pragma unroll
+    for (int j = 0; j < kPlanThreads / 64; ++j) s += red[j][k];
+    v[k] = s;
+  }
+}
+
+// A thread's contiguous chunk [s0, s1) of the sequences, with the query
+// counts and context lengths in registers when the chunk has at most
+// kPlanRegSeqs of them (kCached), else read again from global memory.
+template <bool kCached>
+struct PlanChunk {
+  int s0, s1;
+  int q[kPlanRegSeqs], c[kPlanRegSeqs];
+  __device__ __forceinline__ PlanChunk(const int32_t* __restrict__ qsl,
+                                       const int32_t* __restrict__ seq_lens, int S) {
+    const int chunk = (S + kPlanThreads - 1) / kPlanThreads;
+    s0 = min(S, (int)threadIdx.x * chunk);
+    s1 = min(S, s0 + chunk);
+    if constexpr (kCached) {
+#pragma unroll
+      for (int j = 0; j < kPlanRegSeqs; ++j) {
+        const bool in = s0 + j < s1;
+        q[j] = in ? qsl[s0 + j + 1] - qsl[s0 + j] : 0;
+        c[j] = in ? seq_lens[s0 + j] : 0;
+      }
+    }
+  }
+  // f(i, q, c) for every sequence of the chunk, in order
+  template <typename F>
+  __device__ __forceinline__ void each(const int32_t* __restrict__ qsl,
+                                       const int32_t* __restrict__ seq_lens, F&& f) const {
+    if constexpr (kCached) {
+#pragma unroll
+      for (int j = 0; j < kPlanRegSeqs; ++j)
+        if (s0 + j < s1) f(s0 + j, q[j], c[j]);
+    } else {
+      for (int i = s0; i < s1; ++i) f(i, qsl[i + 1] - qsl[i], seq_lens[i]);
+    }
+  }
+};
+
+// Adds 1 to h[key] for every active lane, the lanes whose key is `hot` (the
+// bucket most sequences share) with one atomic per wavefront: same-address
+// LDS atomics run one after another. With want_pos, returns the old count
+// plus the lane's rank among the wavefront's hot lanes (its slot).
+template <bool want_pos>
+__device__ __forceinline__ int bucket_add(int* h, int key, int hot) {
+  const bool is_hot = key == hot;
+  const uint64_t m = __ballot(is_hot);
+  int pos = 0;
+  if (is_hot) {
+    const int leader = __ffsll((unsigned long long)m) - 1;
+    const int lane = threadIdx.x & 63;
+    int base = 0;
+    if (lane == leader) base = atomicAdd(&h[hot], __popcll(m));
+    if constexpr (want_pos) {
+      base = __shfl(base, leader, 64);
+      pos = base + __popcll(m & ((1ull << lane) - 1));
+    }
+  } else if constexpr (want_pos) {
+    pos = atomicAdd(&h[key], 1);
+  } else {
+    atomicAdd(&h[key], 1);
+  }
+  return pos;
+}
 
 // One workgroup. Chooses the bandwidth kernel's range length R (the smallest
 // power of two in 64..kRangeMax that leaves at most target_items (range, KV head)
@@ -316,7 +403,10 @@ static_assert(kTailBuckets == kPlanThreads, "one tail bucket per plan thread");
 // full ranges, so the kernel ends on its smallest items. The sequences with
 // 32-row tile items are ordered the same way, by context length, longest
 // first (their row blocks are handed out last block first, so within a
-// sequence too the items come longest first).
+// sequence too the items come longest first). Every thread owns a contiguous
+// chunk of the sequences and kPlanBuckets consecutive buckets of each
+// histogram; sums are wavefront reductions, not same-address atomics.
+template <bool kCached>
 __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int S, int H, int Hkv,
     bool fast, bool tile, bool wide, int64_t cap_rows, int target_items, int tile_target,
@@ -325,64 +415,46 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     int32_t* __restrict__ split_base, int32_t* __restrict__ wide_off,
     int32_t* __restrict__ cmb_seq, int32_t* __restrict__ wide_seq, int4* __restrict__ desc,
     float2* __restrict__ ml) {
-  __shared__ unsigned long long need, bw_tokens, tile_keys;
-  __shared__ int part_len, range_len;
+  constexpr int kWaves = kPlanThreads / 64;
+  __shared__ unsigned long long red0[kWaves][2], red1[2][kWaves][1];
   __shared__ int hist[kTailBuckets], whist[kTailBuckets];
   const int t = threadIdx.x;
-  if (t == 0) part_len = kPart0, bw_tokens = 0, tile_keys = 0;
-  for (int k = t; k < kTailBuckets; k += kPlanThreads) hist[k] = 0, whist[k] = 0;
-  __syncthreads();
+  const PlanChunk<kCached> ch(qsl, seq_lens, S);
+#pragma unroll
+  for (int k = 0; k < kPlanBuckets; ++k) hist[t * kPlanBuckets + k] = 0, whist[t * kPlanBuckets + k] = 0;
   // 0. range length from the decode tokens and the target item count; the
   // same for the partition length of the splittable multi-query sequences
   // (at most kSplitMaxQ queries), counted in (KV head, 64-row block) units
+  int R = 64, P = kPart0;
   {
-    unsigned long long mine = 0, mine_t = 0;
     const int rep = H / Hkv;
-    for (int i = t; i < S; i += kPlanThreads) {
-      const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
-      if (is_bw(q, c, fast)) {
-        mine += (unsigned long long)c;
-      } else if (tile && q > 0 && q <= kSplitMaxQ && c > 0) {
-        mine_t += (unsigned long long)c * cdiv(q * rep, kTileRows);
-      }
-    }
-    if (mine) atomicAdd(&bw_tokens, mine);
-    if (mine_t) atomicAdd(&tile_keys, mine_t);
-    __syncthreads();
-    if (t == 0) {
-      int R = 64;
-      while (R < kRangeMax && bw_tokens * (unsigned long long)Hkv >
-                             (unsigned long long)max(target_items, 1) * (unsigned long long)R)
-        R *= 2;
-      range_len = R;
-      int P = kPart0;
-      while (P < (1 << 20) && tile_keys * (unsigned long long)Hkv >
-                                  (unsigned long long)max(tile_target, 1) * (unsigned long long)P)
-        P *= 2;
-      part_len = P;
-    }
-    __syncthreads();
+    unsigned long long v[2] = {0, 0};
+    ch.each(qsl, seq_lens, [&](int, int q, int c) {
+      if (is_bw(q, c, fast))
+        v[0] += (unsigned long long)c;
+      else if (tile && q > 0 && q <= kSplitMaxQ && c > 0)
+        v[1] += (unsigned long long)c * cdiv(q * rep, kTileRows);
+    });
+    plan_sum(v, red0);  // its barrier also orders the histogram clearing
+    while (R < kRangeMax && v[0] * (unsigned long long)Hkv >
+                                (unsigned long long)max(target_items, 1) * (unsigned long long)R)
+      R *= 2;
+    while (P < (1 << 20) && v[1] * (unsigned long long)Hkv >
+                                (unsigned long long)max(tile_target, 1) * (unsigned long long)P)
+      P *= 2;
   }
-  // 1. double P and R until the split partials fit
-  for (;;) {
-    if (t == 0) need = 0;
-    __syncthreads();
-    const int P = part_len, R = range_len;
-    unsigned long long mine = 0;
-    for (int i = t; i < S; i += kPlanThreads)
-      mine += seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, R, H, Hkv, fast, tile, wide).rows;
-    if (mine) atomicAdd(&need, mine);
-    __syncthreads();
-    const bool fits = need <= (unsigned long long)cap_rows || (P >= (1 << 29) && R >= (1 << 29));
-    __syncthreads();
-    if (fits) break;
-    if (t == 0) part_len = min(P * 2, 1 << 29), range_len = min(R * 2, 1 << 29);
-    __syncthreads();
+  // 1. double P and R until the split partials fit (every thread holds the
+  // same sums, so all take the same branch)
+  for (int it = 0;; ++it) {
+    unsigned long long need[1] = {0};
+    ch.each(qsl, seq_lens, [&](int, int q, int c) {
+      need[0] += seq_work(q, c, P, R, H, Hkv, fast, tile, wide).rows;
+    });
+    plan_sum(need, red1[it & 1]);
+    if (need[0] <= (unsigned long long)cap_rows || (P >= (1 << 29) && R >= (1 << 29))) break;
+    P = min(P * 2, 1 << 29), R = min(R * 2, 1 << 29);
   }
-  const int P = part_len, R = range_len;
-  // 2. offsets; every thread owns a contiguous chunk of sequences
-  const int chunk = (S + kPlanThreads - 1) / kPlanThreads;
-  const int s0 = min(S, t * chunk), s1 = min(S, s0 + chunk);
+  // 2. offsets
   // tail ranges are bucketed by their length in blocks, longest first
   const int rblocks = R / kFBs;
   auto tail_key = [&](int c) {
@@ -397,57 +469,71 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     return wd ? kTailBuckets - 2 - min(kTailBuckets - 2, cdiv(c, kTileKeys) - 1) : kTailBuckets - 1;
   };
   int64_t f = 0, g = 0, r = 0, x = 0, tl = 0, wd = 0, cm = 0;
-  for (int i = s0; i < s1; ++i) {
-    const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
+  ch.each(qsl, seq_lens, [&](int, int q, int c) {
     const SeqWork w = seq_work(q, c, P, R, H, Hkv, fast, tile, wide);
     f += w.full, g += w.gen, r += w.rows, x += w.tile, tl += w.tail, wd += w.wide;
     cm += w.np > 1 && !is_bw(q, c, fast);
-    if (w.tail) atomicAdd(&hist[tail_key(c)], 1);
-    atomicAdd(&whist[wide_key(c, w.wide > 0)], 1);
+    if (w.tail) {  // contexts are often alike: the wavefront's first key aggregated
+      const int key = tail_key(c);
+      bucket_add<false>(hist, key, __builtin_amdgcn_readfirstlane(key));
+    }
+    bucket_add<false>(whist, wide_key(c, w.wide > 0), kTailBuckets - 1);
+  });
+  __syncthreads();
+  // the thread's buckets: their counts, summed, join the same scan as the
+  // per-sequence counts; the starts within the thread's buckets follow
+  int hb[kPlanBuckets], wb[kPlanBuckets], hsum = 0, wsum = 0;
+#pragma unroll
+  for (int k = 0; k < kPlanBuckets; ++k) {
+    hb[k] = hsum, wb[k] = wsum;
+    hsum += hist[t * kPlanBuckets + k], wsum += whist[t * kPlanBuckets + k];
   }
-  int sc[7] = {(int)f, (int)g, (int)r, (int)x, (int)tl, (int)wd, (int)cm}, tot[7];
+  int sc[9] = {(int)f, (int)g, (int)r, (int)x, (int)tl, (int)wd, (int)cm, hsum, wsum}, tot[9];
   block_exclusive_scan(sc, tot);
   int64_t fo = sc[0], go = sc[1], ro = sc[2], xo = sc[3], wo = sc[5], co = sc[6];
   const int64_t tf = tot[0], tg = tot[1], tr = tot[2], tx = tot[3], ttl = tot[4], twd = tot[5],
                 tcm = tot[6];
-  // bucket starts (kTailBuckets == kPlanThreads: one bucket per thread)
-  int hs[2] = {hist[t], whist[t]}, htot[2];
-  block_exclusive_scan(hs, htot);
+  // bucket starts (block_exclusive_scan ends on a barrier: the counts above
+  // have been read by every thread)
+#pragma unroll
+  for (int k = 0; k < kPlanBuckets; ++k)
+    hist[t * kPlanBuckets + k] = sc[7] + hb[k], whist[t * kPlanBuckets + k] = sc[8] + wb[k];
   __syncthreads();
-  hist[t] = hs[0];
-  whist[t] = hs[1];
-  __syncthreads();
-  for (int i = s0; i < s1; ++i) {
-    const int q = qsl[i + 1] - qsl[i], c = seq_lens[i];
+  ch.each(qsl, seq_lens, [&](int i, int q, int c) {
     const SeqWork w = seq_work(q, c, P, R, H, Hkv, fast, tile, wide);
-    for (int k = 0; k < w.full; ++k) desc[fo + k] = make_int4(i, k, c, qsl[i]);
+    const int qs = qsl[i];
+    for (int k = 0; k < w.full; ++k) desc[fo + k] = make_int4(i, k, c, qs);
     gen_off[i] = (int32_t)go;
     tile_off[i] = (int32_t)xo;
-    wide_seq[atomicAdd(&whist[wide_key(c, w.wide > 0)], 1)] = i;
+    wide_seq[bucket_add<true>(whist, wide_key(c, w.wide > 0), kTailBuckets - 1)] = i;
     nparts[i] = w.np;
     split_base[i] = w.np > 1 ? (int32_t)ro : -1;
-    if (w.tail) desc[tf + atomicAdd(&hist[tail_key(c)], 1)] = make_int4(i, c / R, c, qsl[i]);
+    if (w.tail) {
+      const int key = tail_key(c);
+      desc[tf + bucket_add<true>(hist, key, __builtin_amdgcn_readfirstlane(key))] =
+          make_int4(i, c / R, c, qs);
+    }
     if (w.np > 1 && !is_bw(q, c, fast)) cmb_seq[co++] = i;
     if (w.np > 1 && is_bw(q, c, fast))  // arrival counters start at 0
       for (int k = 0; k < Hkv; ++k)
         reinterpret_cast<int32_t*>(ml + ro + (int64_t)H * w.np + k)[0] = 0;
     fo += w.full, go += w.gen, ro += w.rows, xo += w.tile;
-  }
+  });
   // 32-row item offsets in wide_seq order (every thread reads the positions of
   // its chunk, written above by any thread of the workgroup)
   __syncthreads();
   if (twd == 0) {  // no 32-row items (twd is the same in every thread)
-    for (int p = s0; p < s1; ++p) wide_off[p] = 0;
+    for (int p = ch.s0; p < ch.s1; ++p) wide_off[p] = 0;
   } else {
     auto wide_items = [&](int i) {
       return seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, R, H, Hkv, fast, tile, wide).wide;
     };
     int64_t mine = 0;
-    for (int p = s0; p < s1; ++p) mine += wide_items(wide_seq[p]);
+    for (int p = ch.s0; p < ch.s1; ++p) mine += wide_items(wide_seq[p]);
     int ws[1] = {(int)mine}, wtot[1];
     block_exclusive_scan(ws, wtot);
     wo = ws[0];
-    for (int p = s0; p < s1; ++p) {
+    for (int p = ch.s0; p < ch.s1; ++p) {
       wide_off[p] = (int32_t)wo;
       wo += wide_items(wide_seq[p]);
     }
@@ -2183,10 +2269,11 @@ int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
   const int target_items = fast ? kItemsPerWg * decode_grid() : 0;
   const int tile_target = kTileItemsPerWg * tile_grid();
   const bool wide = tile && a.dtype == VL_DTYPE_BF16;
-  plan_kernel<<<1, kPlanThreads, 0, st>>>(a.seq_lens, a.qsl, a.S, a.H, a.Hkv, fast, tile, wide,
-                                          L.cap_rows, target_items, tile_target, L.hdr,
-                                          L.gen_off, L.tile_off, L.nparts, L.split_base,
-                                          L.wide_off, L.cmb_seq, L.wide_seq, L.desc, L.ml);
+  auto* plan = a.S <= kPlanThreads * kPlanRegSeqs ? plan_kernel<true> : plan_kernel<false>;
+  plan<<<1, kPlanThreads, 0, st>>>(a.seq_lens, a.qsl, a.S, a.H, a.Hkv, fast, tile, wide,
+                                   L.cap_rows, target_items, tile_target, L.hdr, L.gen_off,
+                                   L.tile_off, L.nparts, L.split_base, L.wide_off, L.cmb_seq,
+                                   L.wide_seq, L.desc, L.ml);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
