@@ -1860,11 +1860,13 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
 // --------------------------------------------------------- short decode --
 
 // Decode batches of short sequences (every sequence at most one query and at
-// most kShortCtx tokens) for head dims up to 64: one workgroup per
-// (sequence, KV head) takes the whole context, so the call needs no plan, no
-// context split and no merge launch. The sequence's block table is staged in
-// LDS first, so that the K and V loads of a 256-key chunk (wavefront w takes
-// keys 64 (4 t + w) + lane of chunk t) are issued together:
+// most kShortCtx tokens) for head dims up to 64: one workgroup of NW
+// wavefronts per (sequence, KV head) takes the whole context, so the call
+// needs no plan, no context split and no merge launch. The sequence's block
+// table is staged in LDS first, so that the K and V loads of a 64 NW-key
+// chunk (wavefront w takes keys 64 (NW t + w) + lane of chunk t) are issued
+// together; with 8 wavefronts a context of up to 512 keys is one chunk, one
+// round trip to memory:
 //   QK: lane l holds key l of its wavefront's 64, its K row in registers,
 //       and the dot products with the REP query heads (LDS broadcast reads);
 //   softmax: per head, the wavefront max by DPP row operations (no LDS
@@ -1874,18 +1876,20 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
 //   PV: lane l = g NC + c (NC 16-byte chunks per head row, G = 64 / NC key
 //       groups) sums chunk c over keys g, g + G, ... of the chunk, its V
 //       chunks loaded with the K row.
-// At the end the wavefronts' lanes are merged in LDS (max-rescaled), one
-// head at a time, and every (head, dim) written once. Keys past the context
-// re-read the last key (finite values) and get weight 0.
+// At the end each wavefront sums its key groups through its own LDS rows;
+// after one workgroup barrier, thread (head, dim) merges the wavefronts
+// (max-rescaled) and writes that element once. Keys past the context re-read
+// the last key (finite values) and get weight 0.
 constexpr int kShortCtx = 2048;
+constexpr int kShortWaves = 8;  // wavefronts per short-decode workgroup
 
-template <typename TKV, int D, int REP>
+template <typename TKV, int D, int REP, int NW>
 struct ShortLds {
   static constexpr int kVE = 16 / (int)sizeof(TKV);  // cache elements per 16-byte load
   float q[REP][D];          // query heads, pre-scaled to the log2 domain
-  float p[4][REP][64];      // per wavefront: the chunk's weights
-  float red[4][64][kVE];    // per wavefront and lane: one head's PV sums
-  float m[4][REP], l[4][REP];
+  float p[NW][REP][64];     // per wavefront: the chunk's weights
+  float red[NW][64][kVE];   // per wavefront and lane: one head's PV sums
+  float m[NW][REP], l[NW][REP];
   int32_t tbl[kShortCtx];   // the sequence's block ids
 };
 
@@ -1903,15 +1907,16 @@ __device__ __forceinline__ void load_row(const T* p, float (&r)[D]) {
   }
 }
 
-// T: query and output elements, TKV: cache elements.
-template <typename T, typename TKV, int D, int REP>
-__global__ void __launch_bounds__(256) attend_short_decode_kernel(
+// T: query and output elements, TKV: cache elements; NW wavefronts.
+template <typename T, typename TKV, int D, int REP, int NW>
+__global__ void __launch_bounds__(64 * NW) attend_short_decode_kernel(
     T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const TKV* kc,
     const TKV* vc, const int32_t* __restrict__ bt, int bt_stride,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int Hkv, int bs_log2,
     int kv_hm, float scale_log2) {
-  using Lds = ShortLds<TKV, D, REP>;
+  using Lds = ShortLds<TKV, D, REP, NW>;
   constexpr int VE = Lds::kVE;
+  constexpr int kThreads = 64 * NW;
   static_assert(D % VE == 0 && D <= 64, "head_dim");
   constexpr int NC = D / VE;               // 16-byte chunks per head row
   constexpr int G = 64 / NC;               // PV key groups
@@ -1919,6 +1924,10 @@ __global__ void __launch_bounds__(256) attend_short_decode_kernel(
   __shared__ Lds s;
   const int i = blockIdx.x / Hkv, g = blockIdx.x - (blockIdx.x / Hkv) * Hkv;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  // the first kThreads entries of the sequence's block-table row (it has
+  // bt_stride of them) are loaded with its length, not after it
+  const int32_t* table = bt + (int64_t)i * bt_stride;
+  const int32_t tbl0 = tid < bt_stride ? table[tid] : 0;
   const int c = seq_lens[i];
   // a sequence without exactly one query, or longer than the staged table,
   // is not this kernel's (the bounds the caller stated do not hold)
@@ -1926,9 +1935,9 @@ __global__ void __launch_bounds__(256) attend_short_decode_kernel(
   const int tok = qsl[i];
   const int bs_mask = (1 << bs_log2) - 1;
   const int nblk = (c + bs_mask) >> bs_log2;
-  const int32_t* table = bt + (int64_t)i * bt_stride;
-  for (int b = tid; b < nblk; b += 256) s.tbl[b] = table[b];
-  for (int e = tid; e < REP * D; e += 256) {
+  if (tid < nblk) s.tbl[tid] = tbl0;
+  for (int b = tid + kThreads; b < nblk; b += kThreads) s.tbl[b] = table[b];
+  for (int e = tid; e < REP * D; e += kThreads) {
     const int h = e / D, d = e - (e / D) * D;
     s.q[h][d] = Elem<T>::load(query, (int64_t)tok * q_stride + (int64_t)(g * REP + h) * D + d) *
                 scale_log2;
@@ -1949,9 +1958,9 @@ __global__ void __launch_bounds__(256) attend_short_decode_kernel(
 #pragma unroll
     for (int e = 0; e < VE; ++e) acc[h][e] = 0.f;
   }
-  const int nchunk = (c + 255) >> 8;
+  const int nchunk = (c + kThreads - 1) / kThreads;
   for (int t = 0; t < nchunk; ++t) {
-    const int base = (4 * t + wave) * 64;
+    const int base = (NW * t + wave) * 64;
     if (base >= c) break;  // wavefront-uniform; later chunks start later still
     // every load of the chunk first: the lane's K row and its V chunks
     float kr[D];
@@ -2005,34 +2014,45 @@ __global__ void __launch_bounds__(256) attend_short_decode_kernel(
 #pragma unroll
     for (int h = 0; h < REP; ++h) s.m[wave][h] = m[h], s.l[wave][h] = lsum[h];
   }
-  const int H = Hkv * REP;
-  // one head at a time: every lane's sums to LDS, then thread d < D adds
-  // dim d over the key groups of each wavefront, max-rescaled across them
+  // each wavefront sums its key groups, one head at a time through its own
+  // LDS rows (no workgroup barrier): lane d < D adds dim d over the groups in
+  // order into the wavefront's weight row of head h, free after the loop
 #pragma unroll
   for (int h = 0; h < REP; ++h) {
 #pragma unroll
     for (int e = 0; e < VE; ++e) s.red[wave][lane][e] = acc[h][e];
-    __syncthreads();
-    if (tid < D) {
-      const int d = tid, dc = d / VE, de = d - (d / VE) * VE;
-      float M = -__builtin_inff();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < D) {
+      const int dc = lane / VE, de = lane - (lane / VE) * VE;
+      float sw = 0.f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) M = fmaxf(M, s.m[w][h]);
-      float L = 0.f, a = 0.f;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float mw = s.m[w][h];
-        if (mw == -__builtin_inff()) continue;
-        const float wt = exp2_fast(mw - M);
-        float sw = 0.f;
-#pragma unroll
-        for (int gg = 0; gg < G; ++gg) sw += s.red[w][gg * NC + dc][de];
-        L = __builtin_fmaf(s.l[w][h], wt, L);
-        a = __builtin_fmaf(sw, wt, a);
-      }
-      Elem<T>::store(out, ((int64_t)tok * H + g * REP + h) * D + d, L > 0.f ? a * (1.f / L) : 0.f);
+      for (int gg = 0; gg < G; ++gg) sw += s.red[wave][gg * NC + dc][de];
+      s.p[wave][h][lane] = sw;
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  __syncthreads();
+  // thread (h, d) merges the wavefronts' sums, max-rescaled, in wavefront order
+  const int H = Hkv * REP;
+  for (int e = tid; e < REP * D; e += kThreads) {
+    const int h = e / D, d = e - (e / D) * D;
+    float M = -__builtin_inff();
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, s.m[w][h]);
+    float L = 0.f, a = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float mw = s.m[w][h];
+      if (mw == -__builtin_inff()) continue;
+      const float wt = exp2_fast(mw - M);
+      L = __builtin_fmaf(s.l[w][h], wt, L);
+      a = __builtin_fmaf(s.p[w][h][d], wt, a);
+    }
+    Elem<T>::store(out, ((int64_t)tok * H + g * REP + h) * D + d, L > 0.f ? a * (1.f / L) : 0.f);
   }
 }
 
@@ -2368,7 +2388,7 @@ int launch_short_decode_d(const Args& a, float sl2, hipStream_t st) {
   if (grid == 0) return VL_OK;
   const int bs_log2 = __builtin_ctz((unsigned)a.bs);
 #define VL_SHORT(REP)                                                                        \
-  attend_short_decode_kernel<T, TKV, D, REP><<<grid, 256, 0, st>>>(                          \
+  attend_short_decode_kernel<T, TKV, D, REP, kShortWaves><<<grid, 64 * kShortWaves, 0, st>>>( \
       (T*)a.out, (const T*)a.query, a.q_stride, (const TKV*)a.kc, (const TKV*)a.vc, a.bt,    \
       a.bt_stride, a.seq_lens, a.qsl, a.Hkv, bs_log2, a.kv_layout == VL_KV_HEAD_MAJOR ? 1 : 0, sl2)
   switch (rep) {
