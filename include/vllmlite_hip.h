@@ -52,7 +52,7 @@ extern "C" {
 #define VL_LINEAR_TILES16 16   /* flag ORed into the mode: W in 16-column tiles */
 #define VL_WEIGHT_ROWS 0       /* a projection weight [k, n] row-major at a row stride */
 #define VL_WEIGHT_TILES16 1    /* ... as 16-column tiles [ceil(n/16), k, 16], zero past n;
-                                  inside a tile, element (k, m) with k = 16g + 4s + j
+                                  inside a tile, element (k, m) with k = 16g + 4j + s
                                   at flat position 256g + 4(16j + m) + s */
 
 /* Message of the last failed call on this thread ("" if none). */
@@ -242,8 +242,9 @@ int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_out, void* 
  * stride weight_stride, or, with VL_LINEAR_TILES16 ORed into mode, as
  * 16-column tiles [ceil(n/16), k, 16] (zero past column n; SwiGLU: the gate
  * tiles, then the up tiles; weight_stride unused; 16-byte aligned; inside a
- * tile element (k, m), k = 16g + 4s + j, at flat position 256g + 4(16j + m) +
- * s, so each lane's operands of 4 MFMA steps are one 16-byte load). out [rows, n]; out must not overlap x. rows <= 16 * 65535
+ * tile element (k, m), k = 16g + 4j + s, at flat position 256g + 4(16j + m) +
+ * s, so each lane's operands of 4 MFMA steps are one 16-byte load, as are
+ * the x elements they meet; norm_weight, when given, 16-byte aligned). out [rows, n]; out must not overlap x. rows <= 16 * 65535
  * (a workgroup per 16 columns and 16 rows, or 2 or 4 row tiles in turn on large
  * grids; built for the <= 16 rows of a decode step, where one row tile does
  * it), k a multiple of 16, k <= 1024.
@@ -262,7 +263,10 @@ int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_str
  * does with that row: rotated q to q_out [rows, num_heads * head_dim],
  * rotated k and plain v to the caches at slot_mapping[r] (skipped when < 0).
  * Input rows are x[row_index[r]] when row_index != NULL (the embedding
- * gather tok_emb[token_ids], model.py:93), and when x_out != NULL the rows
+ * gather tok_emb[token_ids], model.py:93); an index -(1 + i) < 0 stands for
+ * prev_ids[i] (0 when i >= num_prev), the id the previous step chose for its
+ * row i, as vl_resolve_tokens would replace it (prev_ids may be NULL when
+ * num_prev is 0). When x_out != NULL the rows
  * read (before the norm) are also written to x_out [rows, k] (the residual
  * stream). weight_layout: VL_WEIGHT_ROWS (row stride weight_stride) or
  * VL_WEIGHT_TILES16 (as for vl_linear_rows). rows <= 16 * 65535, k a multiple
@@ -270,7 +274,8 @@ int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_str
  * kv_layout as for vl_rope_and_cache.
  */
 int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cache, const float* x,
-                      int64_t x_stride, const int32_t* row_index, float* x_out,
+                      int64_t x_stride, const int32_t* row_index, const int32_t* prev_ids,
+                      int64_t num_prev, float* x_out,
                       const float* weight, int64_t weight_stride, int weight_layout,
                       const float* norm_weight, float eps, const int32_t* positions,
                       const int32_t* slot_mapping, const float* cos_table, const float* sin_table,
@@ -358,6 +363,26 @@ int vl_decode_step(const void* const* layer_weights, const int64_t* layer_stride
                    int d_ff, int vocab, int block_size, int max_context, float scale, float eps,
                    float* x, float* q, float* attn, float* act, float* logits, int32_t* out_ids,
                    int32_t* out_ids_host, uint32_t* sync, void* stream);
+
+/*
+ * A submission thread for captured step graphs (no counterpart in the
+ * reference: its engine steps synchronously, vllmlite/engine.py:99-181; the
+ * callers are runners that overlap host work with a step in flight).
+ * vl_launcher_create starts a thread that launches graph executables on
+ * `stream` (of `device`), in submission order; vl_launcher_submit queues
+ * hipGraphLaunch(graph_exec) (skipped when NULL) followed by
+ * hipEventRecord(event) (skipped when NULL) and returns at once with a
+ * ticket (1, 2, ...); vl_launcher_wait returns once the calls of that ticket
+ * and every earlier one have returned, with 0 or the first hipError_t any of
+ * them gave (the work itself may still be running on the device: wait on
+ * the event for that). vl_launcher_destroy launches what is queued, then
+ * stops the thread. The graph executables, events and stream must outlive
+ * their submissions.
+ */
+int vl_launcher_create(int device, void* stream, void** launcher);
+int vl_launcher_submit(void* launcher, void* graph_exec, void* event, uint64_t* ticket);
+int vl_launcher_wait(void* launcher, uint64_t ticket);
+int vl_launcher_destroy(void* launcher);
 
 #ifdef __cplusplus
 }

@@ -48,7 +48,7 @@ def test_no_compute_without_gpu_needed_for_queries():
     assert lib.vl_paged_attention_workspace_size(256, 256, 32, 128, 8192) > \
         lib.vl_paged_attention_min_workspace(256)
     lib.vl_abi_version.restype = ctypes.c_int
-    assert lib.vl_abi_version() == 7
+    assert lib.vl_abi_version() == 9
 
 
 def test_reads_plan_names_the_short_decode_shapes():
@@ -96,7 +96,7 @@ def test_engine_default_backend_is_the_hip_runner():
 
 
 def test_tile16_layout():
-    """Tiled projection weights: element (k, m) of tile t, k = 16 g + 4 s + j,
+    """Tiled projection weights: element (k, m) of tile t, k = 16 g + 4 j + s,
     at flat position 256 g + 4 (16 j + m) + s; columns past n zero; with
     halves 2 the gate tiles precede the up tiles."""
     import torch
@@ -109,7 +109,7 @@ def test_tile16_layout():
     for h in range(2):
         for tt in range(2):
             for kk in range(k):
-                g, s, j = kk // 16, (kk % 16) // 4, kk % 4
+                g, j, s = kk // 16, (kk % 16) // 4, kk % 4
                 for m in range(16):
                     col = tt * 16 + m
                     want = w[kk, h * n + col].item() if col < n else 0.0

@@ -75,12 +75,14 @@ def test_swiglu(rows, norm, k, dff):
     _close(out.cpu().numpy(), want)
 
 
-def test_norm_prologue_matches_rms_norm_kernel():
-    """The fused RMSNorm gives the same bits as vl_rms_norm: with an identity
-    weight the projection returns the normalised rows themselves."""
+@pytest.mark.parametrize("k", [384, 1024, 48])
+def test_norm_as_row_scale_matches_rms_norm_kernel(k):
+    """The fused RMSNorm is applied as ((x * g) @ W) / rms(x): with an identity
+    weight the projection returns (x * g) / rms, which differs from
+    vl_rms_norm's (x / rms) * g by the order of two roundings only (a few
+    ulps), and the scale is exactly 1 / rms of the row's own elements."""
     o = _ops()
-    rng = np.random.default_rng(3)
-    k = 384
+    rng = np.random.default_rng(3 + k)
     x = torch.from_numpy(rng.standard_normal((16, k)).astype(np.float32)).cuda()
     g = torch.from_numpy((1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)).cuda()
     eye = torch.eye(k, device="cuda")
@@ -89,7 +91,7 @@ def test_norm_prologue_matches_rms_norm_kernel():
     ref = torch.empty_like(x)
     o.rms_norm(ref, x, g)
     torch.cuda.synchronize()
-    assert torch.equal(got, ref)
+    np.testing.assert_allclose(got.cpu().numpy(), ref.cpu().numpy(), rtol=4e-7, atol=0)
 
 
 def test_bad_arguments_raise():
@@ -240,6 +242,52 @@ def test_qkv_rope_cache_embedding_gather_and_residual_copy():
     torch.cuda.synchronize()
     assert torch.equal(q1, q2) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
     assert torch.equal(x_out, table[ids.long()])
+
+
+def test_qkv_rope_cache_resolves_placeholder_tokens():
+    """A token id -(1 + i) < 0 in row_index stands for prev_ids[i] (the id the
+    previous step chose for its row i; 0 when i >= num_prev), as
+    vl_resolve_tokens would replace it first: the same bits as resolving on
+    the device and then gathering."""
+    o = _ops()
+    H, Hkv, D, k, rows = 8, 4, 48, 384, 16
+    n = (H + 2 * Hkv) * D
+    rng = np.random.default_rng(31)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    table = dev(rng.standard_normal((261, k)).astype(np.float32))
+    prev = dev(rng.integers(0, 261, 12).astype(np.int32))
+    ids_np = rng.integers(0, 261, rows).astype(np.int32)
+    ids_np[[0, 3, 4, 9, 15]] = [-1, -12, -5, -13, -40]  # -13, -40: past num_prev -> id 0
+    ids = dev(ids_np)
+    w = dev(o.tile16(torch.from_numpy((0.05 * rng.standard_normal((k, n))).astype(np.float32)))
+            .numpy())
+    g = dev(np.ones(k, np.float32))
+    pos = dev(rng.integers(0, 64, rows).astype(np.int32))
+    slot = dev(rng.permutation(40)[:rows].astype(np.int32))
+    ang = rng.standard_normal((64, D // 2)).astype(np.float32)
+    cos, sin = dev(np.cos(ang)), dev(np.sin(ang))
+    kc1, vc1 = (torch.zeros((40, Hkv, D), device="cuda") for _ in range(2))
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    q1 = torch.empty((rows, H * D), device="cuda")
+    q2 = torch.empty_like(q1)
+    x1 = torch.full((rows, k), float("nan"), device="cuda")
+    x2 = torch.full((rows, k), float("nan"), device="cuda")
+    o.qkv_rope_cache(q1, kc1, vc1, table, w, g, pos, slot, cos, sin, H, Hkv, D, row_index=ids,
+                     x_out=x1, prev_ids=prev)
+    resolved = ids.clone()
+    o.resolve_tokens(resolved, prev)
+    o.qkv_rope_cache(q2, kc2, vc2, table, w, g, pos, slot, cos, sin, H, Hkv, D,
+                     row_index=resolved, x_out=x2)
+    torch.cuda.synchronize()
+    want_ids = np.where(ids_np >= 0, ids_np, 0)
+    p = prev.cpu().numpy()
+    for r, t in enumerate(ids_np):
+        if t < 0 and -t - 1 < 12:
+            want_ids[r] = p[-t - 1]
+    assert np.array_equal(resolved.cpu().numpy(), want_ids)
+    assert torch.equal(q1, q2) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    assert torch.equal(x1, table[torch.from_numpy(want_ids).long().cuda()])
+    assert torch.equal(ids.cpu(), torch.from_numpy(ids_np))  # row_index is only read
 
 
 @pytest.mark.parametrize("rows", [1, 16])

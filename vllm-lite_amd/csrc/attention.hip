@@ -1886,11 +1886,18 @@ constexpr int kShortWaves = 8;  // wavefronts per short-decode workgroup
 template <typename TKV, int D, int REP, int NW>
 struct ShortLds {
   static constexpr int kVE = 16 / (int)sizeof(TKV);  // cache elements per 16-byte load
+  static constexpr int kNC = D / kVE;                 // 16-byte chunks per head row
+  // K rows staged key-major, a row padded to an odd number of 16-byte chunks
+  // (the 64 lanes' reads of their own rows then meet no bank conflicts),
+  // where the wavefronts' rows fit beside the rest (all but fp32 head_dim 64)
+  static constexpr int kNCP = kNC + 1 + (kNC & 1);
+  static constexpr bool kStageK = (size_t)NW * 64 * kNCP * 16 <= 110 * 1024;
   float q[REP][D];          // query heads, pre-scaled to the log2 domain
   float p[NW][REP][64];     // per wavefront: the chunk's weights
   float red[NW][64][kVE];   // per wavefront and lane: one head's PV sums
   float m[NW][REP], l[NW][REP];
   int32_t tbl[kShortCtx];   // the sequence's block ids
+  uint4 k[kStageK ? NW : 1][kStageK ? 64 : 1][kStageK ? kNCP : 1];  // per wavefront: its keys' K rows
 };
 
 
@@ -1962,14 +1969,34 @@ __global__ void __launch_bounds__(64 * NW) attend_short_decode_kernel(
   for (int t = 0; t < nchunk; ++t) {
     const int base = (NW * t + wave) * 64;
     if (base >= c) break;  // wavefront-uniform; later chunks start later still
-    // every load of the chunk first: the lane's K row and its V chunks
-    float kr[D];
-    load_row<TKV, D>(kg + row_of(min(base + lane, c - 1)), kr);
-    uint4 vraw[KPL];
+    // every load of the chunk first. K and V alike: lane (pg, pc) loads
+    // 16-byte chunk pc of keys pg + G j, so each load instruction reads G
+    // whole rows (a lane per key reads one chunk of 64 rows, 64 cache lines,
+    // per instruction: the address work of those loads set the kernel's time)
+    uint4 kraw[Lds::kStageK ? KPL : 1], vraw[KPL];
 #pragma unroll
     for (int j = 0; j < KPL; ++j) {
       const int kk = min(pg + G * j, 63);  // past the chunk (or lanes past G NC): weight 0
-      vraw[j] = *reinterpret_cast<const uint4*>(vg + row_of(min(base + kk, c - 1)) + pc * VE);
+      const int64_t ro = row_of(min(base + kk, c - 1)) + pc * VE;
+      if constexpr (Lds::kStageK) kraw[j] = *reinterpret_cast<const uint4*>(kg + ro);
+      vraw[j] = *reinterpret_cast<const uint4*>(vg + ro);
+    }
+    // the lane's key row: through the wavefront's LDS rows, or (fp32 head_dim
+    // 64, whose rows do not fit) straight from the cache
+    float kr[D];
+    if constexpr (Lds::kStageK) {
+#pragma unroll
+      for (int j = 0; j < KPL; ++j) {
+        const int kk = pg + G * j;
+        if (pg < G && kk < 64) s.k[wave][kk][pc] = kraw[j];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) widen16<TKV>(s.k[wave][lane][cc], kr + VE * cc);
+    } else {
+      load_row<TKV, D>(kg + row_of(min(base + lane, c - 1)), kr);
     }
     const bool valid = base + lane < c;
 #pragma unroll

@@ -195,7 +195,7 @@ struct StepParams {
 // u + j NW, j < NT), each with NS slices (SwiGLU: the gate and up tiles).
 // Its 8 wavefronts split K: wavefront w takes the steps of 4 k from step
 // w spw, for every tile and slice, its weights in registers (0 past K and
-// past N columns). Tiled element (k, m), k = 16 g + 4 s + j, sits at 256 g +
+// past N columns). Tiled element (k, m), k = 16 g + 4 j + s, sits at 256 g +
 // 4 (16 j + m) + s, so a lane's operands of 4 steps are one float4.
 __device__ __forceinline__ int steps_per_wave(int K) {
   return ((K / 4 + kTileWaves - 1) / kTileWaves + 3) / 4 * 4;
@@ -345,10 +345,11 @@ __device__ __forceinline__ void tile_mma(const float* xs, const TileW<KMAX, NT *
   for (int s = 0; s < NSL; ++s)
 #pragma unroll
     for (int q = 0; q < kAcc; ++q) acc4[s][q] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-  const float* arow = &xs[m * KP + kb + j];
+  // step i = 4 g + s meets k = kb + 16 g + 4 j + s (the tile order)
+  const float* arow = &xs[m * KP + kb + 4 * j];
   float av[kSteps];
 #pragma unroll
-  for (int i = 0; i < kSteps; ++i) av[i] = arow[4 * i];
+  for (int i = 0; i < kSteps; ++i) av[i] = arow[16 * (i / 4) + (i % 4)];
 #pragma unroll
   for (int i = 0; i < kSteps; ++i)
 #pragma unroll

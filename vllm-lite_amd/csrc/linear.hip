@@ -7,19 +7,21 @@
 //
 // One workgroup computes 16 rows x 16 output columns: its kLinWaves (8)
 // wavefronts split K into contiguous ranges on v_mfma_f32_16x16x4f32, each
-// loading its weight operands straight into registers (all loads in flight at
-// once) while the rows of x are staged in LDS and normalised there; the
-// partial tiles are summed in wavefront order. hipBLASLt runs these shapes as separate launches of
-// ~7 us each; here a projection and its neighbours are one.
+// loading its rows of x and its weights straight into operand registers (all
+// loads in flight at once, no LDS stage); the RMSNorm is applied as a per-row
+// scale after the product, so the partial tiles and sums of squares meet in
+// LDS behind one barrier and are summed in wavefront order. These kernels run
+// on few workgroups at <= 16 rows, where the dependent phases of a workgroup
+// (not the bytes) set the time: an empty kernel in a graph takes 1.9 us, one
+// that loads 40 KB per workgroup 2.3 us.
 //
 // Weights come row-major ([k, n] at a row stride) or as 16-column tiles
 // ([ceil(n/16), k, 16], the columns past n zero): a workgroup's 16 columns
 // are then one contiguous k x 64-byte run, ordered inside so that a lane's
-// B operands of 4 consecutive MFMA steps are adjacent (element (k, m), k =
-// 16 g + 4 s + j, at 256 g + 4 (16 j + m) + s): a wavefront reads 1 KB per
-// 16-byte load instruction (row-major, every k row is a separate 64-byte
-// piece read 4 bytes per lane). These kernels run on few workgroups, where
-// the number of requests each one issues sets the time.
+// B operands of the 4 MFMA steps of a 16-k group are adjacent (element (k,
+// m), k = 16 g + 4 j + s, at 256 g + 4 (16 j + m) + s): a wavefront reads 1 KB
+// per 16-byte load instruction, and the same lane's A operands, x[m][16 g + 4
+// j + s], are one float4 of the row.
 #include "vl_common.h"
 
 namespace {
@@ -27,15 +29,13 @@ namespace {
 constexpr int kRowsMax = 16;                 // rows per workgroup (one row tile)
 constexpr int kRowsLimit = kRowsMax * 65535;  // rows per call (grid y)
 constexpr int kCols = 16;
-#ifndef VL_LIN_WAVES
-#define VL_LIN_WAVES 8
-#endif
 // wavefronts per projection workgroup; they split K, so more of them make the
 // serial MFMA chain of each shorter (the kernel is latency-bound at <= 16
 // rows): 8 measured 7 % faster per TinyLlama decode step than 4, and the same
-// as 16, which spills registers at K = 1024)
-constexpr int kLinWaves = VL_LIN_WAVES;
-static_assert(kLinWaves == 4 || kLinWaves == 8, "4 or 8 wavefronts");
+// as 16, which spills registers at K = 1024
+constexpr int kLinWaves = 8;
+// row tiles a workgroup takes at most (see rows_per_workgroup)
+constexpr int kSubMax = 4;
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -83,219 +83,224 @@ __device__ __forceinline__ void store_cache(void* cache, int64_t i, float v, int
 // MODE 0: out = f(x) @ w; 1: out += f(x) @ w; 2: out = silu(f(x) @ w[:, :n]) *
 // (f(x) @ w[:, up_off : up_off + n]); 3: f(x) @ w is a [q | k | v] row: q and k
 // rotated by RoPE, q to rc.q_out, k and v to the caches at the row's slot.
-// f(x) = x, or with NORM the RMSNorm of x (as rms_norm_kernel computes it)
-// times norm_w.
+// f(x) = x, or with NORM the RMSNorm of x times norm_w, applied as
+// ((x * norm_w) @ w) / rms(x): the per-row scale 1 / rms commutes with the
+// product, so no wavefront waits for another's rows before its MFMAs.
 // TILES: the weight is in 16-column tiles (ldw unused; up_off counts
 // elements, the start of the up tiles).
+//
+// Lane l = 16 j + m of wavefront w holds, for each 16-k group g of the
+// wavefront's contiguous k range, x[row m][16 g + 4 j .. +3] (one float4
+// straight from global memory: no LDS stage) and the weights w[16 g + 4 j +
+// s][c0 + m], s = 0..3 (one float4 of a tile); step s of group g is then one
+// v_mfma_f32_16x16x4f32 with A = x[m][16 g + 4 j + s], B = w[16 g + 4 j +
+// s][c0 + m]. The 8 wavefronts' partial 16 x 16 tiles (and, with NORM, each
+// lane's sum of x^2 over its k) meet in LDS behind the kernel's one barrier
+// and are summed in wavefront order, so every run gives the same bits.
 template <int MODE, bool NORM, int KMAX, bool TILES>
 __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
     float* __restrict__ out, int64_t ldo, const float* __restrict__ x, int64_t ldx,
     const float* __restrict__ w, int64_t ldw, int64_t up_off, const float* __restrict__ norm_w,
     float eps, int M, int K, int N, const RopeCache rc, const int32_t* __restrict__ row_index,
-    float* __restrict__ x_out, int nsub) {
+    const int32_t* __restrict__ prev_ids, int64_t num_prev, float* __restrict__ x_out,
+    int nsub, int rt) {
   constexpr int kSlices = MODE == 2 ? 2 : 1;
-  constexpr int KP = KMAX + 4;  // xs row stride: rows 4 words apart, so the
-                                // 16 rows x 4 k of an A read hit 64 banks
-  constexpr int kSteps = KMAX / (4 * kLinWaves);  // 16x16x4 steps per wavefront at K = KMAX
-  static_assert(kSteps % 4 == 0, "whole groups of 4 steps");
-  __shared__ float xs[kRowsMax * KP];
+  constexpr int kGroups = KMAX / (16 * kLinWaves);  // 16-k groups per wavefront at K = KMAX
+  static_assert(kGroups >= 1 && KMAX % (16 * kLinWaves) == 0, "whole 16-k groups");
   __shared__ float red[kSlices][kLinWaves][kRowsMax * kCols];
+  __shared__ float4 ssq[kRowsMax][kLinWaves];  // row m: the 4 lanes j of each wavefront
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // rt rows per row tile (4 or 16); lanes of rows past the tile's end load
+  // nothing and feed zeros to the MFMAs
   const int c0 = blockIdx.x * kCols;
   const int m = lane & 15, j = lane >> 4;
-  // wavefront w takes the spw steps of 4 k from step w spw (k in [kb, kb + 4
-  // nsteps)); the last wavefronts may have fewer steps, or none
-  // (spw is a multiple of 4: the tiled weights hold 4 steps per 16-byte load)
-  const int spw = ((K / 4 + kLinWaves - 1) / kLinWaves + 3) / 4 * 4;
-  const int kb = wave * spw * 4;
-  const int nsteps = max(0, min(spw, K / 4 - wave * spw));
-  // ---- the epilogue's own global reads for the row tile at r0, issued early
-  // so that they arrive with the weights (tile 0) or the rows instead of
-  // after the reduction: thread t writes row t / 16, column c0 + t % 16; the
-  // residual it adds to (MODE 1), or its slot and its RoPE table entries
-  // (MODE 3)
-  const int er = tid / kCols, ec = tid - (tid / kCols) * kCols;
+  // wavefront w takes the gn 16-k groups from group gb (the last wavefronts may
+  // have fewer, or none); loads past them read a clamped, valid group whose
+  // weights are then multiplied by 0 (a select would let the compiler turn
+  // each load into a branch that waits for it)
+  const int ng = K / 16;
+  const int gpw = (ng + kLinWaves - 1) / kLinWaves;
+  const int gb = wave * gpw;
+  const int gn = max(0, min(gpw, ng - gb));
+  // ---- the loads of a row tile at r0, in an order that keeps dependent
+  // loads from waiting for independent ones (vector loads complete in issue
+  // order, so waiting for a load waits for every load issued before it):
+  // first the index loads (lane m: its input row; epilogue thread t: its
+  // row's slot and position), then the weights (once, for every tile), then
+  // x at the indexed rows, then the epilogue's reads (the residual, or the
+  // RoPE table entries at the position).
+  // Input rows: x[r0 + m], or x[row_index[r0 + m]] where an index -(1 + i) <
+  // 0 stands for prev_ids[i], the id the previous step chose for its row i (0
+  // when i is not below num_prev). Lanes of rows past the tile's end read its
+  // last row again (the same addresses: no extra traffic); their results are
+  // never stored. Every load is unconditional: a load in a branch whose
+  // other side sets zeros makes the compiler wait for it where the two meet.
   const int M_all = M;  // M is the current tile's row count from here on
-  float e_resid = 0.f, e_cos = 0.f, e_sin = 0.f;
-  int e_slot = -1;
-  auto epilogue_reads = [&](int r0) {
-    const bool ok = er < min(kRowsMax, M_all - r0) && c0 + ec < N;
-    if constexpr (MODE == 1) {
-      if (ok) e_resid = out[(int64_t)(r0 + er) * ldo + c0 + ec];
-    } else if constexpr (MODE == 3) {
-      if (ok) {
-        const int col = c0 + ec, qd = rc.nh * rc.hd, kd = rc.nkv * rc.hd;
+  const int er = tid / kCols, ec = tid - (tid / kCols) * kCols;
+  const bool e_col = c0 + ec < N;
+  int in_row = 0, e_pos = 0, e_slot = -1;
+  auto index_reads = [&](int r0, int Mt) {
+    if (row_index) in_row = row_index[r0 + min(m, Mt - 1)];
+    if constexpr (MODE == 3) {
+      if (er < Mt && e_col) {
         e_slot = rc.slots[r0 + er];
-        if (col < qd + kd) {
-          const int base = col < qd ? col : col - qd;
-          const int64_t tab =
-              (int64_t)rc.positions[r0 + er] * (rc.hd >> 1) + ((base % rc.hd) >> 1);
-          e_cos = rc.cos_t[tab];
-          e_sin = rc.sin_t[tab];
-        }
+        e_pos = rc.positions[r0 + er];
       }
     }
   };
-  epilogue_reads(blockIdx.y * nsub * kRowsMax);
+  auto load_x = [&](float4 (&xv)[kGroups], int r0, int Mt) {
+    int64_t row = r0 + min(m, Mt - 1);
+    if (row_index) {
+      row = in_row;
+      if (prev_ids && num_prev > 0) {
+        const int64_t i = -row - 1;
+        const int64_t pv = prev_ids[min(max(i, (int64_t)0), num_prev - 1)];
+        row = row >= 0 ? row : (i < num_prev ? pv : 0);
+      } else {
+        row = max(row, (int64_t)0);
+      }
+    }
+    const float* xr = x + row * ldx;
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g)
+      xv[g] = *reinterpret_cast<const float4*>(xr + 16 * min(gb + g, ng - 1) + 4 * j);
+  };
+  // thread t writes row t / 16, column c0 + t % 16
+  float e_resid = 0.f, e_cos = 0.f, e_sin = 0.f;
+  auto epilogue_reads = [&](int r0) {
+    const bool ok = er < min(rt, M_all - r0) && e_col;
+    if constexpr (MODE == 1) {
+      if (ok) e_resid = out[(int64_t)(r0 + er) * ldo + c0 + ec];
+    } else if constexpr (MODE == 3) {
+      const int col = c0 + ec, qd = rc.nh * rc.hd, kd = rc.nkv * rc.hd;
+      if (ok && col < qd + kd) {
+        const int base = col < qd ? col : col - qd;
+        const int64_t tab = (int64_t)e_pos * (rc.hd >> 1) + ((base % rc.hd) >> 1);
+        e_cos = rc.cos_t[tab];
+        e_sin = rc.sin_t[tab];
+      }
+    }
+  };
 
-  // ---- the B operand straight into registers: step i of wavefront w needs
-  // w[kb + 4i + l/16][c0 + l%16] in lane l (columns past the end read 0);
-  // every load is issued before any is used
-  // (loads outside the shape read a clamped, valid element that is then
-  // multiplied by 0: columns past N, and steps past this wavefront's nsteps,
-  // whose A values belong to the next wavefront's range. A select would let
-  // the compiler turn each load into a branch that waits for it.)
-  float wb[kSlices][kSteps];
+  // ---- loads of the first row tile
+  const int r00 = blockIdx.y * nsub * rt;
+  index_reads(r00, min(rt, M_all - r00));
+  // the B operands: lane (m, j), group g, step s needs w[16 (gb + g) + 4 j +
+  // s][c0 + m]; in a tile that is one float4 at 256 (gb + g) + 4 (16 j + m)
+  float4 wv[kSlices][kGroups];
   const float colmask = c0 + m < N ? 1.f : 0.f;
 #pragma unroll
   for (int s = 0; s < kSlices; ++s) {
-    if constexpr (TILES) {
-      // tile blockIdx.x: element (k, m), k = 16 g + 4 s + j, at 256 g + 4 (16 j
-      // + m) + s, so lane l's operands of the 4 steps of group g are one
-      // float4 and a wavefront reads 1 KB per load (groups clamped below K / 16;
-      // kb and nsteps are multiples of 16 and 4)
-      const float4* src = reinterpret_cast<const float4*>(w + (s ? up_off : 0) +
-                                                          (int64_t)blockIdx.x * K * kCols) +
-                          lane;
 #pragma unroll
-      for (int g = 0; g < kSteps / 4; ++g) {
-        const float4 v = src[(int64_t)min(kb / 16 + g, K / 16 - 1) * 64];
-        const float z = 4 * g < nsteps ? colmask : 0.f;
-        wb[s][4 * g] = v.x * z;
-        wb[s][4 * g + 1] = v.y * z;
-        wb[s][4 * g + 2] = v.z * z;
-        wb[s][4 * g + 3] = v.w * z;
+    for (int g = 0; g < kGroups; ++g) {
+      const int gg = min(gb + g, ng - 1);
+      float4 v;
+      if constexpr (TILES) {
+        v = reinterpret_cast<const float4*>(w + (s ? up_off : 0) +
+                                            (int64_t)blockIdx.x * K * kCols)[gg * 64 + lane];
+      } else {
+        const float* src = w + (s ? up_off : 0) + min(c0 + m, N - 1) + (16 * gg + 4 * j) * ldw;
+        v = make_float4(src[0], src[ldw], src[2 * ldw], src[3 * ldw]);
       }
-    } else {
-      const float* src = w + (s ? up_off : 0) + min(c0 + m, N - 1);
-#pragma unroll
-      for (int i = 0; i < kSteps; ++i)
-        wb[s][i] = src[(int64_t)(min(kb + 4 * i, K - 4) + j) * ldw] * (i < nsteps ? colmask : 0.f);
+      const float z = g < gn ? colmask : 0.f;
+      wv[s][g] = make_float4(v.x * z, v.y * z, v.z * z, v.w * z);
     }
   }
-  // the norm weights of this lane's columns k = lane + 64 i (clamped loads)
-  float gw[KMAX / 64];
+  // the norm weights of the same k (16-byte aligned, checked by the host)
+  float4 gq[NORM ? kGroups : 1];
   if constexpr (NORM) {
 #pragma unroll
-    for (int i = 0; i < KMAX / 64; ++i) gw[i] = norm_w[min(lane + 64 * i, K - 1)];
+    for (int g = 0; g < kGroups; ++g)
+      gq[g] = *reinterpret_cast<const float4*>(norm_w + 16 * min(gb + g, ng - 1) + 4 * j);
   }
+  float4 xv[kGroups];
+  load_x(xv, r00, min(rt, M_all - r00));
+  epilogue_reads(r00);
+
   // row tiles blockIdx.y nsub + t (t < nsub), rows r0 .. r0 + 15 each, one
   // after the other on the weights already in registers; every row index
-  // below counts from the tile's r0. The barriers of each tile also order the
-  // previous tile's LDS reads (its A operands and reduction) before this
-  // tile's writes.
+  // below counts from the tile's r0
   for (int t = 0; t < nsub; ++t) {
-    const int r0 = (blockIdx.y * nsub + t) * kRowsMax;
+    const int r0 = (blockIdx.y * nsub + t) * rt;
     if (r0 >= M_all) break;  // uniform over the workgroup
-    M = min(kRowsMax, M_all - r0);
-    const int32_t* row_index_t = row_index ? row_index + r0 : nullptr;
-    const float* x_t = row_index ? x : x + (int64_t)r0 * ldx;
+    M = min(rt, M_all - r0);
+    if (t > 0) {
+      index_reads(r0, M);
+      load_x(xv, r0, M);
+      epilogue_reads(r0);
+      __syncthreads();  // the previous tile's reads of red / ssq are done
+    }
     float* out_t = MODE != 3 ? out + (int64_t)r0 * ldo : out;
-    float* x_out_t = x_out ? x_out + (int64_t)r0 * K : nullptr;
     float* q_out = MODE == 3 ? rc.q_out + (int64_t)r0 * rc.nh * rc.hd : nullptr;
-    if (t > 0) epilogue_reads(r0);
-    const bool e_ok = er < M && c0 + ec < N;
-    // ---- x rows to LDS (rows >= M are zero): thread t < 256 takes row t / 16
-    // and float4 columns t % 16 + 16 u; row r is x[row_index[r]] when an index
-    // is given, and workgroup 0 copies the rows it read to x_out when given
-    if (tid < 16 * kRowsMax) {
-      const int r = tid >> 4, q = tid & 15;
-      const int kq = K / 4;
-      float4 xv[KMAX / 64];
-      const int rr = min(r, M - 1);
-      const float* xr = x_t + (int64_t)(row_index_t ? row_index_t[rr] : rr) * ldx;
+    // layer 0 writes the rows it gathered (workgroup 0 of each row tile)
+    if (x_out && blockIdx.x == 0 && m < M) {
 #pragma unroll
-      for (int u = 0; u < KMAX / 64; ++u) {
-        const int k4 = q + 16 * u;
-        const float z = r < M && k4 < kq ? 1.f : 0.f;  // rows past M, columns past K: 0
-        const float4 v = *reinterpret_cast<const float4*>(xr + 4 * min(k4, kq - 1));
-        xv[u] = make_float4(v.x * z, v.y * z, v.z * z, v.w * z);
-      }
-#pragma unroll
-      for (int u = 0; u < KMAX / 64; ++u)
-        *reinterpret_cast<float4*>(&xs[r * KP + 4 * (q + 16 * u)]) = xv[u];
-      if (x_out_t && blockIdx.x == 0 && r < M) {
-#pragma unroll
-        for (int u = 0; u < KMAX / 64; ++u)
-          if (q + 16 * u < kq)
-            *reinterpret_cast<float4*>(x_out_t + (int64_t)r * K + 4 * (q + 16 * u)) = xv[u];
-      }
+      for (int g = 0; g < kGroups; ++g)
+        if (g < gn)
+          *reinterpret_cast<float4*>(x_out + (int64_t)(r0 + m) * K + 16 * (gb + g) + 4 * j) = xv[g];
     }
-    __syncthreads();
-
-    if constexpr (NORM) {
-      // rows r = wave, wave + kLinWaves, ...: the sum of squares over k = lane +
-      // 64 i in increasing i, then the wavefront sum, as rms_norm_kernel (the
-      // rows of a wavefront interleaved; columns past K hold zeros)
-      constexpr int kRq = kRowsMax / kLinWaves;
-      float ss[kRq];
-#pragma unroll
-      for (int q = 0; q < kRq; ++q) ss[q] = 0.f;
-#pragma unroll
-      for (int i = 0; i < KMAX / 64; ++i)
-#pragma unroll
-        for (int q = 0; q < kRq; ++q) {
-          const float a = xs[(wave + kLinWaves * q) * KP + lane + 64 * i];
-          ss[q] += a * a;
-        }
-#pragma unroll
-      for (int q = 0; q < kRq; ++q) {
-        const float rms = sqrtf(wave_sum(ss[q]) / (float)K + eps);
-        float* row = &xs[(wave + kLinWaves * q) * KP + lane];
-#pragma unroll
-        for (int i = 0; i < KMAX / 64; ++i)
-          if (lane + 64 * i < K) row[64 * i] = (row[64 * i] / rms) * gw[i];
-      }
-      __syncthreads();
-    }
-
-    // ---- lane l supplies A[l%16][l/16] and B[l/16][l%16] of each 16x16x4 step
-    // four independent accumulators per slice (steps i % 4), so consecutive
-    // MFMAs do not wait for each other's results
-    constexpr int kAcc = kSteps >= 4 ? 4 : 1;
-    f32x4_t acc4[kSlices][kAcc];
+    // ---- sum of squares of this lane's x (in k order), x * norm_w, and the
+    // MFMA chain: four accumulators per slice (step s of every group), so
+    // consecutive MFMAs do not wait for each other's results
+    float ss = 0.f;
+    f32x4_t acc4[kSlices][4];
 #pragma unroll
     for (int s = 0; s < kSlices; ++s)
 #pragma unroll
-      for (int q = 0; q < kAcc; ++q) acc4[s][q] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    const float* arow = &xs[m * KP + kb + j];
-    // all A reads first, then the MFMA chain (the reads of steps past this
-    // wavefront's nsteps stay inside the row, below KMAX, and meet zero weights)
-    float av[kSteps];
+      for (int q = 0; q < 4; ++q) acc4[s][q] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < kSteps; ++i) av[i] = arow[4 * i];
+    for (int g = 0; g < kGroups; ++g) {
+      float a[4] = {xv[g].x, xv[g].y, xv[g].z, xv[g].w};
+      if constexpr (NORM) {
+        const float b[4] = {gq[g].x, gq[g].y, gq[g].z, gq[g].w};
+        float sg = 0.f;
 #pragma unroll
-    for (int i = 0; i < kSteps; ++i)
+        for (int s = 0; s < 4; ++s) sg += a[s] * a[s];
+        ss += g < gn ? sg : 0.f;
 #pragma unroll
-      for (int s = 0; s < kSlices; ++s)
-        acc4[s][i % kAcc] =
-            __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], wb[s][i], acc4[s][i % kAcc], 0, 0, 0);
-    f32x4_t acc[kSlices];
+        for (int s = 0; s < 4; ++s) a[s] *= b[s];
+      }
 #pragma unroll
-    for (int s = 0; s < kSlices; ++s) {
-      acc[s] = acc4[s][0];
+      for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int q = 1; q < kAcc; ++q) acc[s] += acc4[s][q];
+        for (int sl = 0; sl < kSlices; ++sl) {
+          const float bw = s == 0 ? wv[sl][g].x : s == 1 ? wv[sl][g].y : s == 2 ? wv[sl][g].z : wv[sl][g].w;
+          acc4[sl][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bw, acc4[sl][s], 0, 0, 0);
+        }
     }
     // C layout: lane l holds rows 4(l/16) + i of column l%16
 #pragma unroll
-    for (int s = 0; s < kSlices; ++s)
+    for (int sl = 0; sl < kSlices; ++sl) {
+      const f32x4_t acc = ((acc4[sl][0] + acc4[sl][1]) + acc4[sl][2]) + acc4[sl][3];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) red[s][wave][(4 * j + i) * kCols + m] = acc[s][i];
+      for (int i = 0; i < 4; ++i) red[sl][wave][(4 * j + i) * kCols + m] = acc[i];
+    }
+    if constexpr (NORM) reinterpret_cast<float*>(&ssq[m][wave])[j] = ss;
     __syncthreads();
 
     const int r = er, c = ec;
-    if (e_ok) {
+    if (er < M && e_col) {
       // the wavefronts' partial sums in wavefront order
       auto total = [&](int s, int e) {
-        float t = red[s][0][e];
+        float v = red[s][0][e];
 #pragma unroll
-        for (int q = 1; q < kLinWaves; ++q) t += red[s][q][e];
-        return t;
+        for (int q = 1; q < kLinWaves; ++q) v += red[s][q][e];
+        return v;
       };
+      float rms = 1.f;
+      if constexpr (NORM) {
+        // sum of x^2 over the row: wavefronts in order, the 4 lanes of each in order
+        float s2 = 0.f;
+#pragma unroll
+        for (int q = 0; q < kLinWaves; ++q) {
+          const float4 p = ssq[r][q];
+          s2 += ((p.x + p.y) + p.z) + p.w;
+        }
+        rms = sqrtf(s2 / (float)K + eps);
+      }
       float v[kSlices];
 #pragma unroll
-      for (int s = 0; s < kSlices; ++s) v[s] = total(s, tid);
+      for (int s = 0; s < kSlices; ++s) v[s] = NORM ? total(s, tid) / rms : total(s, tid);
       if constexpr (MODE == 0) {
         out_t[(int64_t)r * ldo + c0 + c] = v[0];
       } else if constexpr (MODE == 1) {
@@ -306,7 +311,7 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
         // the pair partner of column c is c ^ 1 in the same tile (head_dim even,
         // tiles 16 columns)
         const int pt = r * kCols + (c ^ 1);
-        const float partner = total(0, pt);
+        const float partner = NORM ? total(0, pt) / rms : total(0, pt);
         const int col = c0 + c, qd = rc.nh * rc.hd, kd = rc.nkv * rc.hd;
         const int slot = e_slot;
         if (col < qd + kd) {
@@ -328,38 +333,53 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
   }
 }
 
-#ifndef VL_LIN_SUB_MAX
-#define VL_LIN_SUB_MAX 4
-#endif
 // Row tiles per workgroup: 1 while the grid is at most one round of two
 // workgroups per CU (the kernel is latency-bound there, so tiles run side by
-// side); beyond that doubled, up to VL_LIN_SUB_MAX, while the grid keeps at
+// side); beyond that doubled, up to kSubMax, while the grid keeps at
 // least that round, so that each workgroup's weight tile serves more rows.
 inline int rows_per_workgroup(int ntile, int row_tiles) {
   const int64_t round = 2 * (int64_t)vl_num_cus();
   int nsub = 1;
-  while (nsub < VL_LIN_SUB_MAX &&
+  while (nsub < kSubMax &&
          (int64_t)ntile * ((row_tiles + 2 * nsub - 1) / (2 * nsub)) >= round)
     nsub *= 2;
   return nsub;
 }
 
+// Rows per row tile. A step of at most 16 rows (a decode step) runs as row
+// tiles of 4, a workgroup per (16 columns, 4 rows), while that grid stays
+// within one round of two workgroups per CU: a workgroup then loads a quarter
+// of the rows of x, and the last of its wavefronts to receive its operands,
+// which sets the time, waits less (measured per TinyLlama decode layer, 16
+// rows: QKV 3.55 -> 3.16 us, gate|up 3.65 -> 3.32, down 4.16 -> 3.24; rows of
+// 8, or 8 columns per workgroup, were slower). Larger steps use 16-row tiles,
+// several per workgroup on large grids (rows_per_workgroup).
+inline int row_tile(int M, int N) {
+  const int64_t ntile = (N + kCols - 1) / kCols;
+  if (M <= kRowsMax && ntile * ((M + 3) / 4) <= 2 * (int64_t)vl_num_cus()) return 4;
+  return kRowsMax;
+}
+
 template <int MODE, bool NORM, int KMAX>
 int launch(float* out, int64_t ldo, const float* x, int64_t ldx, const float* w, int64_t ldw,
            bool tiles, const float* norm_w, float eps, int M, int K, int N, hipStream_t st,
-           const int32_t* row_index, const RopeCache& rc = RopeCache{}, float* x_out = nullptr) {
+           const int32_t* row_index, const RopeCache& rc = RopeCache{}, float* x_out = nullptr,
+           const int32_t* prev_ids = nullptr, int64_t num_prev = 0) {
   const int ntile = (N + kCols - 1) / kCols;
-  const int row_tiles = (M + kRowsMax - 1) / kRowsMax;
-  const int nsub = rows_per_workgroup(ntile, row_tiles);
+  const int rt = row_tile(M, N);
+  const int row_tiles = (M + rt - 1) / rt;
+  const int nsub = rt == kRowsMax ? rows_per_workgroup(ntile, row_tiles) : 1;
   const dim3 grid(ntile, (row_tiles + nsub - 1) / nsub);
   if (tiles) {
     const int64_t up_off = MODE == 2 ? (int64_t)ntile * K * kCols : 0;
     linear_rows_kernel<MODE, NORM, KMAX, true><<<grid, 64 * kLinWaves, 0, st>>>(
-        out, ldo, x, ldx, w, 0, up_off, norm_w, eps, M, K, N, rc, row_index, x_out, nsub);
+        out, ldo, x, ldx, w, 0, up_off, norm_w, eps, M, K, N, rc, row_index, prev_ids, num_prev,
+        x_out, nsub, rt);
   } else {
     const int64_t up_off = MODE == 2 ? N : 0;
     linear_rows_kernel<MODE, NORM, KMAX, false><<<grid, 64 * kLinWaves, 0, st>>>(
-        out, ldo, x, ldx, w, ldw, up_off, norm_w, eps, M, K, N, rc, row_index, x_out, nsub);
+        out, ldo, x, ldx, w, ldw, up_off, norm_w, eps, M, K, N, rc, row_index, prev_ids,
+        num_prev, x_out, nsub, rt);
   }
   VL_CHECK_LAUNCH();
   return VL_OK;
@@ -385,6 +405,7 @@ extern "C" int vl_linear_rows(float* out, int64_t out_stride, const float* x, in
   const int64_t wcols = mode == VL_LINEAR_SWIGLU ? 2 * (int64_t)n : n;
   VL_CHECK_ARG(tiles || weight_stride >= wcols, "weight row stride too small");
   VL_CHECK_ARG(!tiles || (((uintptr_t)weight) & 15) == 0, "tiled weight must be 16-byte aligned");
+  VL_CHECK_ARG((((uintptr_t)norm_weight) & 15) == 0, "norm weight must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   const bool nrm = norm_weight != nullptr;
   // KMAX, the unrolled depth, is the smallest of 384 / 512 / 1024 that holds k
@@ -408,6 +429,7 @@ extern "C" int vl_linear_rows(float* out, int64_t out_stride, const float* x, in
 
 extern "C" int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cache,
                                  const float* x, int64_t x_stride, const int32_t* row_index,
+                                 const int32_t* prev_ids, int64_t num_prev,
                                  float* x_out, const float* weight,
                                  int64_t weight_stride, int weight_layout,
                                  const float* norm_weight, float eps,
@@ -435,6 +457,9 @@ extern "C" int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cach
   const bool tiles = weight_layout == VL_WEIGHT_TILES16;
   VL_CHECK_ARG(tiles || weight_stride >= n, "weight row stride too small");
   VL_CHECK_ARG(!tiles || (((uintptr_t)weight) & 15) == 0, "tiled weight must be 16-byte aligned");
+  VL_CHECK_ARG((((uintptr_t)norm_weight) & 15) == 0, "norm weight must be 16-byte aligned");
+  VL_CHECK_ARG(num_prev >= 0 && (num_prev == 0 || (prev_ids && row_index)),
+               "prev_ids needs row_index (and num_prev > 0 needs prev_ids)");
   RopeCache rc;
   rc.q_out = q_out, rc.kc = key_cache, rc.vc = value_cache, rc.positions = positions;
   rc.slots = slot_mapping, rc.cos_t = cos_table, rc.sin_t = sin_table;
@@ -445,7 +470,7 @@ extern "C" int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cach
   const bool nrm = norm_weight != nullptr;
 #define VL_QKV(NORM, KM) \
   launch<3, NORM, KM>(nullptr, 0, x, x_stride, weight, weight_stride, tiles, norm_weight, eps, rows, \
-                      k, n, st, row_index, rc, x_out)
+                      k, n, st, row_index, rc, x_out, prev_ids, num_prev)
   if (k <= 384) return nrm ? VL_QKV(true, 384) : VL_QKV(false, 384);
   if (k <= 512) return nrm ? VL_QKV(true, 512) : VL_QKV(false, 512);
   return nrm ? VL_QKV(true, 1024) : VL_QKV(false, 1024);

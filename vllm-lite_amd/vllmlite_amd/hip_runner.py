@@ -213,13 +213,30 @@ class HipRunner(ModelRunner):
         self.W = max(1, -(-mc.max_seq_len // self.block_size))
         self._buf = 0  # which of the two pinned staging / id buffers the next launch uses
         self._cap_T = 0
-        self._graphs: Dict[Tuple[int, int, int, bool], torch.cuda.CUDAGraph] = {}
+        self._graphs: Dict[Tuple[int, int, int, bool, int], torch.cuda.CUDAGraph] = {}
+        self._graph_exec: Dict[Tuple[int, int, int, bool, int], int] = {}  # raw exec handles
+        self._dev_index = (self.device.index if self.device.index is not None
+                           else torch.cuda.current_device())
+        self._stream_h = self.stream.cuda_stream
+        # captured steps are launched from the library's submission thread
+        # (hipGraphLaunch costs the caller ~1 us per node); anything this
+        # thread enqueues on the stream itself drains it first
+        self._launcher = ops.Launcher(self._dev_index, self._stream_h)
         self._pool = None
         # decode-only steps: the attention hints (one query per sequence, at
         # most max_seq_len tokens, which bounds every position) and whether
         # they select the short-decode kernel, which needs no plan
         self._short_decode = not ops.paged_attention_reads_plan(
             self.H, self.Hkv, self.hd, self.block_size, 1, mc.max_seq_len)
+
+    def __del__(self):
+        # the submission thread may still hold launches of this runner's graphs
+        launcher = getattr(self, "_launcher", None)
+        if launcher is not None:
+            try:
+                launcher.drain()
+            finally:
+                launcher.close()
 
     # ------------------------------------------------------------ interface --
     @property
@@ -232,7 +249,9 @@ class HipRunner(ModelRunner):
 
     def execute(self, out) -> Tuple[np.ndarray, List[Tuple[int, int]]]:
         with torch.cuda.device(self.device), torch.cuda.stream(self.stream):
-            rows, R, one = self._run(out, -1)
+            rows, R, one, ge = self._run(out, self._buf, exec_ids=True)
+            if ge is not None:
+                self._launcher.wait(self._launcher.submit(ge))
             self._logits_host[:R].copy_(self._logits[:R], non_blocking=True)
             self.stream.synchronize()
             if one:
@@ -254,24 +273,31 @@ class HipRunner(ModelRunner):
         at once with a handle for collect(). One launched step may be
         outstanding while the next is staged and launched; a token id t < 0 in
         the next step's sequences stands for row -t - 1 of this step's ids
-        (resolved on the device, vl_resolve_tokens)."""
-        with torch.cuda.device(self.device), torch.cuda.stream(self.stream):
-            k = self._buf
-            rows, R, one = self._run(out, k)
-            if not one:
-                # the ids to the device buffer (the next step resolves its
-                # placeholders from it) and, by the same launch, to the pinned one
-                ops.argmax_rows(self._logits[:R], self._ids[:R], host_out=self._ids_hosts[k])
-            self._done[k].record(self.stream)
-            self._buf ^= 1
-            # the handle holds its own buffer and event: a later step that grows
-            # the buffers replaces them while this copy may still be queued
-            return rows, R, self._ids_hosts_np[k], self._done[k], one
+        (resolved on the device by the first layer's embedding gather).
+        A step whose graph is captured costs the host its staging and one
+        graph launch: the graph holds the record's host-to-device copy, the
+        forward and the argmax (which writes the ids to the device buffer the
+        next step reads and to the pinned one collect() reads)."""
+        k = self._buf
+        rows, R, one, ge = self._run(out, k)
+        done = self._done[k]
+        if ge is not None:
+            ticket = self._launcher.submit(ge, done.cuda_event)
+        else:
+            ticket = 0
+            ops.hip_check(ops.hip_runtime().hipEventRecord(done.cuda_event, self._stream_h),
+                          "hipEventRecord")
+        self._buf ^= 1
+        # the handle holds its own buffer and event: a later step that grows
+        # the buffers replaces them while this copy may still be queued
+        return rows, R, self._ids_hosts_np[k], (done, ticket), one
 
     def collect(self, handle) -> Tuple[np.ndarray, List[Tuple[int, int]]]:
         """Waits for a launched step; its ids and rows."""
-        rows, R, host, done, one = handle
-        done.synchronize()
+        rows, R, host, (done, ticket), one = handle
+        self._launcher.wait(ticket)
+        ops.hip_check(ops.hip_runtime().hipEventSynchronize(done.cuda_event),
+                      "hipEventSynchronize")
         if one:
             self._check_step(host)
         return host[:R].copy(), rows
@@ -285,29 +311,42 @@ class HipRunner(ModelRunner):
             raise RuntimeError(f"one-launch decode step failed: {why}; its results are invalid "
                                "(construct HipRunner with one_launch_decode=False)")
 
-    def _run(self, out, host_k=None) -> Tuple[List[Tuple[int, int]], int, bool]:
-        """CoW copies, staging and the forward (graph replay when captured);
-        leaves the logits rows in self._logits[:R]. A decode step that the
-        one-launch kernel takes also leaves the ids in self._ids and in a
-        pinned host buffer (host_k: that of launch_argmax's buffer k, or -1
-        for execute's own); the flag says so."""
+    def _run(self, out, k: int, exec_ids: bool = False):
+        """CoW copies, staging into pinned record k and the forward; leaves
+        the logits rows in self._logits[:R] and their argmax in self._ids and
+        in pinned buffer k. Returns (rows, R, one, graph): a captured step is
+        not launched here but its graph executable returned, for the caller
+        to submit (it holds the record's copy, the forward and the argmax);
+        anything else is enqueued here, on the runner's stream, once earlier
+        submissions have been launched. A decode step that the one-launch
+        kernel takes leaves the ids in self._ids and in pinned buffer k (or,
+        exec_ids, execute()'s own); `one` says so. Selects the runner's
+        device itself: the engine may call from any thread."""
+        ops.hip_check(ops.hip_runtime().hipSetDevice(self._dev_index), "hipSetDevice")
         if out.cow:
-            self._copy_on_write(out.cow)
-        shape, rows, R = self._stage(out)
-        if (host_k is not None and self._step is not None and shape.decode and
+            self._launcher.drain()
+            with torch.cuda.device(self.device), torch.cuda.stream(self.stream):
+                self._copy_on_write(out.cow)
+        shape, rows, R = self._stage(out, k)
+        if (self._step is not None and shape.decode and
                 shape.Tb == ops.DECODE_STEP_ROWS and shape.Sb <= ops.DECODE_STEP_ROWS):
-            self._decode_step(shape, self._exec_ids_host if host_k < 0 else self._ids_hosts[host_k])
+            self._launcher.drain()
+            with torch.cuda.device(self.device), torch.cuda.stream(self.stream):
+                self._meta[:shape.n_ints].copy_(self._meta_hosts[k][:shape.n_ints],
+                                                non_blocking=True)
+                self._decode_step(shape, self._exec_ids_host if exec_ids else self._ids_hosts[k])
             self.one_launch_steps += 1
-            return rows, R, True
-        key = (shape.Tb, shape.Sb, shape.Rb, shape.decode)
-        g = self._graphs.get(key)
-        if g is not None:
-            g.replay()
-        else:
-            self._forward(shape)
+            return rows, R, True, None
+        key = (shape.Tb, shape.Sb, shape.Rb, shape.decode, k)
+        ge = self._graph_exec.get(key)
+        if ge is not None:
+            return rows, R, False, ge
+        self._launcher.drain()
+        with torch.cuda.device(self.device), torch.cuda.stream(self.stream):
+            self._forward(shape, k)
             if self.use_graphs:
-                self._capture(shape, key)
-        return rows, R, False
+                self._capture(shape, key, k)
+        return rows, R, False, None
 
     def _decode_step(self, s: "_Shape", host: torch.Tensor) -> None:
         """The step as one vl_decode_step launch (rows = sequences)."""
@@ -329,6 +368,7 @@ class HipRunner(ModelRunner):
         cap = _bucket(max(T, self._cap_T), 64)
         self.W = max(self.W, W)
         self._graphs.clear()
+        self._graph_exec.clear()
         self._pool = None
         old_ids = getattr(self, "_ids", None)
         mc, dev = self.model_cfg, self.device
@@ -358,15 +398,22 @@ class HipRunner(ModelRunner):
             self._ids[:old_ids.numel()].copy_(old_ids)
         self._ids_hosts = [torch.zeros(cap, dtype=torch.int32, pin_memory=True) for _ in range(2)]
         self._ids_hosts_np = [h.numpy() for h in self._ids_hosts]
-        self._done = [torch.cuda.Event() for _ in range(2)]
+        with torch.cuda.device(dev):
+            self._done = [torch.cuda.Event() for _ in range(2)]
+            for e in self._done:  # created on the runner's device (torch creates events lazily)
+                e.record(self.stream)
         ws = ops.paged_attention_workspace_size(cap, cap, H, hd, mc.max_seq_len + 64)
         self._ws = ops.AttentionWorkspace(dev).get(ws)
         self._cap_T = cap
 
-    def _stage(self, out):
-        """Flatten the scheduled batch into the pinned record and send it."""
+    def _stage(self, out, k: int):
+        """Flatten the scheduled batch into pinned record k (the forward
+        copies it to the device)."""
         f = flatten_scheduled(out, self.block_size, self.model_cfg.max_seq_len)
-        self._ensure_capacity(f.T, f.width)
+        if f.T > self._cap_T or f.width > self.W:
+            self._launcher.drain()  # the ids of a step in flight are copied over
+            with torch.cuda.device(self.device), torch.cuda.stream(self.stream):
+                self._ensure_capacity(f.T, f.width)
         shape = _Shape(_bucket(f.T, 16), _bucket(f.S, 8), _bucket(f.R, 8), self.W,
                        f.max_q == 1 and self._short_decode)
         Tb, Sb, Rb, W = shape.Tb, shape.Sb, shape.Rb, shape.W
@@ -374,7 +421,7 @@ class HipRunner(ModelRunner):
         bt = [0] * (Sb * W)
         for i, ids in enumerate(f.tables):
             bt[i * W:i * W + len(ids)] = ids
-        m = self._meta_nps[self._buf]
+        m = self._meta_nps[k]
         m[shape.tok:shape.tok + Tb] = f.toks + [0] * (Tb - T)
         m[shape.pos:shape.pos + Tb] = f.pos + [0] * (Tb - T)
         m[shape.slot:shape.slot + Tb] = f.slots + [-1] * (Tb - T)
@@ -382,8 +429,6 @@ class HipRunner(ModelRunner):
         m[shape.qsl:shape.qsl + Sb + 1] = f.qsl + [T] * (Sb - S)
         m[shape.lens:shape.lens + Sb] = f.lens + [0] * (Sb - S)
         m[shape.bt:shape.bt + Sb * W] = bt
-        n = shape.n_ints
-        self._meta[:n].copy_(self._meta_hosts[self._buf][:n], non_blocking=True)
         return shape, f.rows, R
 
     # -------------------------------------------------------------- forward --
@@ -391,7 +436,16 @@ class HipRunner(ModelRunner):
         p = torch.tensor(pairs, dtype=torch.int32).reshape(-1, 2).to(self.device, non_blocking=False)
         ops.copy_blocks(self.cache_k, self.cache_v, p, self.block_size)
 
-    def _forward(self, s: _Shape) -> None:
+    def _forward(self, s: _Shape, k: int) -> None:
+        """Pinned record k to the device, the forward, and the argmax of the
+        bucket's Rb logits rows into self._ids and pinned buffer k (rows past
+        the step's R are the padded rows' and never read)."""
+        n = s.n_ints
+        self._meta[:n].copy_(self._meta_hosts[k][:n], non_blocking=True)
+        self._forward_body(s)
+        ops.argmax_rows(self._logits[:s.Rb], self._ids[:s.Rb], host_out=self._ids_hosts[k])
+
+    def _forward_body(self, s: _Shape) -> None:
         mc = self.model_cfg
         Tb, Sb, Rb = s.Tb, s.Sb, s.Rb
         meta = self._meta
@@ -402,8 +456,6 @@ class HipRunner(ModelRunner):
         qsl = meta[s.qsl:s.qsl + Sb + 1]
         lens = meta[s.lens:s.lens + Sb]
         bt = meta[s.bt:s.bt + Sb * s.W].view(Sb, s.W)
-        # ids the previous step chose on the device (negative placeholders)
-        ops.resolve_tokens(tok, self._ids)
         x, h, delta = self._x[:Tb], self._h[:Tb], self._delta[:Tb]
         qkv, q, attn = self._qkv[:Tb], self._q[:Tb], self._attn[:Tb]
         gu, act = self._gu[:Tb], self._act[:Tb]
@@ -411,6 +463,8 @@ class HipRunner(ModelRunner):
         if Tb <= min(self.fused_rows_max, ops.LINEAR_ROWS_MAX) and self._fused_rows:
             self._forward_rows(s, x, q, attn, act, tok, pos, slot, lidx, qsl, lens, bt)
             return
+        # ids the previous step chose on the device (negative placeholders)
+        ops.resolve_tokens(tok, self._ids)
         torch.index_select(W["tok_emb"], 0, tok, out=x)
         ops.rms_norm(h, x, W["layers"][0]["attn_norm"])
         self._plan(s, q, lens, qsl)
@@ -458,10 +512,13 @@ class HipRunner(ModelRunner):
         self._plan(s, q, lens, qsl)
         for li, L in enumerate(W["layers"]):
             kc, vc = self.cache_k[li], self.cache_v[li]
-            if li == 0:  # the embedding gather, with x = tok_emb[tok] written out
+            if li == 0:  # the embedding gather, with x = tok_emb[tok] written out; a
+                # placeholder token -(1 + r) is the id the previous step chose
+                # for its row r, read from the device here
                 ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, W["tok_emb"], L["w_qkv_t"],
                                    L["attn_norm"], pos, slot, self.cos, self.sin, self.H,
-                                   self.Hkv, self.hd, row_index=tok, x_out=x)
+                                   self.Hkv, self.hd, row_index=tok, x_out=x,
+                                   prev_ids=self._ids)
             else:
                 ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, x, L["w_qkv_t"], L["attn_norm"], pos,
                                    slot, self.cos, self.sin, self.H, self.Hkv, self.hd)
@@ -472,7 +529,7 @@ class HipRunner(ModelRunner):
         ops.linear_rows(self._logits[:Rb], x, W["lm_head_t"], W["final_norm"],
                         mode=ops.LINEAR_STORE, row_index=lidx)
 
-    def _capture(self, s: _Shape, key) -> None:
+    def _capture(self, s: _Shape, key, k: int) -> None:
         # A garbage collection inside the capture could free device or pinned
         # host memory of unreachable objects (an earlier runner, say); the
         # stream operations such frees perform are illegal while a capture is
@@ -483,9 +540,10 @@ class HipRunner(ModelRunner):
         try:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g, pool=self._pool, stream=self.stream):
-                self._forward(s)
+                self._forward(s, k)
         finally:
             gc.enable()
         if self._pool is None:
             self._pool = g.pool()
         self._graphs[key] = g
+        self._graph_exec[key] = g.raw_cuda_graph_exec()

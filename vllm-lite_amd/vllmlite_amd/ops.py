@@ -23,7 +23,7 @@ F32, BF16, F32_BF16KV, FP8_E4M3, F32_FP8KV = 0, 1, 2, 3, 4
 # VL_KV_*: a per-layer cache tensor [slots, Hkv, D] is token-major (the
 # reference's layout), [blocks, Hkv, block_size, D] head-major
 KV_TOKEN_MAJOR, KV_HEAD_MAJOR = 0, 1
-ABI_VERSION = 7  # vl_abi_version() of the library these signatures describe
+ABI_VERSION = 9  # vl_abi_version() of the library these signatures describe
 _c_void_p = ctypes.c_void_p
 _i32, _i64, _f32, _size = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
 
@@ -31,6 +31,10 @@ _i32, _i64, _f32, _size = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c
 SIGNATURES = {
     "vl_last_error": (ctypes.c_char_p, []),
     "vl_abi_version": (_i32, []),
+    "vl_launcher_create": (_i32, [_i32, _c_void_p, ctypes.POINTER(_c_void_p)]),
+    "vl_launcher_submit": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.POINTER(ctypes.c_uint64)]),
+    "vl_launcher_wait": (_i32, [_c_void_p, ctypes.c_uint64]),
+    "vl_launcher_destroy": (_i32, [_c_void_p]),
     "vl_reshape_and_cache": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
                                     _c_void_p, _i64, _i32, _i32, _i32, _i32, _i32, _c_void_p]),
     "vl_copy_blocks": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i64, _i64, _i32,
@@ -64,6 +68,7 @@ SIGNATURES = {
     "vl_linear_rows": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64,
                               _c_void_p, _f32, _i32, _i32, _i32, _i32, _c_void_p]),
     "vl_qkv_rope_cache": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
+                                 _c_void_p, _i64,
                                  _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _f32, _c_void_p,
                                  _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32,
                                  _i32, _i32, _i32, _c_void_p]),
@@ -97,6 +102,74 @@ def lib() -> ctypes.CDLL:
                                f"need {ABI_VERSION}: rebuild the library")
         _LIB = handle
     return _LIB
+
+
+_HIP = None
+
+
+def hip_runtime():
+    """The HIP runtime library torch has loaded, for the per-step launch path
+    of HipRunner (hipGraphLaunch of a captured step, hipEventRecord /
+    hipEventSynchronize, hipSetDevice) without torch's per-call overhead."""
+    global _HIP
+    if _HIP is None:
+        h = ctypes.CDLL("libamdhip64.so")
+        for name, args in (("hipGraphLaunch", [_c_void_p, _c_void_p]),
+                           ("hipEventRecord", [_c_void_p, _c_void_p]),
+                           ("hipEventSynchronize", [_c_void_p]),
+                           ("hipSetDevice", [_i32]),
+                           ("hipGetErrorString", [_i32])):
+            fn = getattr(h, name)
+            fn.argtypes = args
+            fn.restype = _i32
+        h.hipGetErrorString.restype = ctypes.c_char_p
+        _HIP = h
+    return _HIP
+
+
+class Launcher:
+    """vl_launcher_*: graph launches (and event records) submitted to a host
+    thread of the library's, in order, on one stream."""
+
+    def __init__(self, device: int, stream_handle: int):
+        h = _c_void_p()
+        _check(lib().vl_launcher_create(device, _c_void_p(stream_handle), ctypes.byref(h)),
+               "vl_launcher_create")
+        self._h = h
+        self._t = ctypes.c_uint64()
+        self.last = 0  # the last ticket handed out
+
+    def submit(self, graph_exec: int, event: int = 0) -> int:
+        _check(lib().vl_launcher_submit(self._h, _c_void_p(graph_exec), _c_void_p(event),
+                                        ctypes.byref(self._t)), "vl_launcher_submit")
+        self.last = self._t.value
+        return self.last
+
+    def wait(self, ticket: int) -> None:
+        if ticket:
+            _check(lib().vl_launcher_wait(self._h, ticket), "vl_launcher_wait")
+
+    def drain(self) -> None:
+        """Until every submission's calls have returned (before the caller
+        itself enqueues work on the same stream)."""
+        self.wait(self.last)
+
+    def close(self) -> None:
+        if self._h is not None and _LIB is not None:
+            lib().vl_launcher_destroy(self._h)
+        self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def hip_check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = hip_runtime().hipGetErrorString(rc).decode(errors="replace")
+        raise RuntimeError(f"{what} failed (hipError {rc}): {msg}")
 
 
 def _check(rc: int, what: str) -> None:
@@ -377,7 +450,7 @@ def tile16(w: torch.Tensor, halves: int = 1) -> torch.Tensor:
     """A [k, halves * n] weight (k a multiple of 16) as 16-column tiles
     [halves * ceil(n/16), k, 16] (zero past column n; with halves 2, the tiles
     of w[:, :n] then those of w[:, n:], the SwiGLU gate and up halves). Inside
-    a tile, element (k, m) with k = 16 g + 4 s + j sits at flat position
+    a tile, element (k, m) with k = 16 g + 4 j + s sits at flat position
     256 g + 4 (16 j + m) + s."""
     k, cols = w.shape
     _need(k % 16 == 0, "k must be a multiple of 16")
@@ -388,7 +461,7 @@ def tile16(w: torch.Tensor, halves: int = 1) -> torch.Tensor:
         p = torch.zeros(k, nt * 16, dtype=w.dtype, device=w.device)
         p[:, :n] = w[:, h * n:(h + 1) * n]
         t = p.view(k, nt, 16).permute(1, 0, 2)  # [nt, k, 16]: (k, m)
-        t = t.reshape(nt, k // 16, 4, 4, 16).permute(0, 1, 3, 4, 2)  # (g, s, j, m) -> (g, j, m, s)
+        t = t.reshape(nt, k // 16, 4, 4, 16).permute(0, 1, 2, 4, 3)  # (g, j, s, m) -> (g, j, m, s)
         parts.append(t.reshape(nt, k, 16))
     return torch.cat(parts).contiguous()
 
@@ -431,10 +504,12 @@ def qkv_rope_cache(q_out: torch.Tensor, key_cache: torch.Tensor, value_cache: to
                    positions: torch.Tensor, slot_mapping: torch.Tensor, cos: torch.Tensor,
                    sin: torch.Tensor, num_heads: int, num_kv_heads: int, head_dim: int,
                    eps: float = 1e-5, row_index: Optional[torch.Tensor] = None,
-                   x_out: Optional[torch.Tensor] = None) -> None:
+                   x_out: Optional[torch.Tensor] = None,
+                   prev_ids: Optional[torch.Tensor] = None) -> None:
     """QKV projection of a step's rows fused with RoPE and the K/V scatter; with
-    row_index the rows are x[row_index], copied to x_out when given (see
-    vl_qkv_rope_cache)."""
+    row_index the rows are x[row_index] (an index -(1 + i) < 0 stands for
+    prev_ids[i], the previous step's id of its row i), copied to x_out when
+    given (see vl_qkv_rope_cache)."""
     k = x.shape[1]
     rows = q_out.shape[0]
     _need(row_index is not None or x.shape[0] >= rows, "x has too few rows")
@@ -448,8 +523,12 @@ def qkv_rope_cache(q_out: torch.Tensor, key_cache: torch.Tensor, value_cache: to
           "cache shape")
     _need(positions.numel() >= rows and slot_mapping.numel() >= rows, "shape mismatch")
     tiles, wstride = _weight_layout(weight, k, (num_heads + 2 * num_kv_heads) * head_dim, 1)
+    _need(prev_ids is None or (row_index is not None and prev_ids.dtype == torch.int32),
+          "prev_ids needs row_index and must hold int32 ids")
     _check(lib().vl_qkv_rope_cache(_ptr(q_out), _ptr(key_cache), _ptr(value_cache), _ptr(x),
-                                   x.stride(0), _ptr(row_index), _ptr(x_out), _ptr(weight),
+                                   x.stride(0), _ptr(row_index), _ptr(prev_ids),
+                                   prev_ids.numel() if prev_ids is not None else 0,
+                                   _ptr(x_out), _ptr(weight),
                                    wstride, WEIGHT_TILES16 if tiles else WEIGHT_ROWS,
                                    _ptr(norm_weight),
                                    float(eps), _ptr(positions), _ptr(slot_mapping), _ptr(cos),
