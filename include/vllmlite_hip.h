@@ -283,6 +283,15 @@ int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cache, const fl
                       int cache_dtype, int kv_layout, int block_size, void* stream);
 
 /*
+ * A copy of n int32 words by one kernel (no counterpart in the reference,
+ * which has no device): src may be pinned host memory (hipHostMalloc), read
+ * by the kernel over the bus. A step graph's host-to-device copy of its
+ * staging record, as a memcpy node, costs ~12 us more per step than this
+ * kernel node.
+ */
+int vl_copy_words(int32_t* dst, const int32_t* src, int64_t n, void* stream);
+
+/*
  * The device side of a step issued before the previous step's tokens reached
  * the host (no reference counterpart: the reference engine waits for every
  * step, vllmlite/engine.py:99-181): token_ids[i] < 0 stands for
@@ -383,6 +392,13 @@ int vl_launcher_create(int device, void* stream, void** launcher);
 int vl_launcher_submit(void* launcher, void* graph_exec, void* event, uint64_t* ticket);
 int vl_launcher_wait(void* launcher, uint64_t ticket);
 int vl_launcher_destroy(void* launcher);
+/*
+ * Host side: spins until values[0..n) (pinned host memory a kernel writes,
+ * the caller having set it negative) are all >= 0, or timeout_us passes
+ * (then VL_EINVAL). A step's token ids arrive this way without an event
+ * record behind the step's graph (which costs the device 3-4.5 us).
+ */
+int vl_host_wait_nonneg(const int32_t* values, int64_t n, int64_t timeout_us);
 
 #ifdef __cplusplus
 }

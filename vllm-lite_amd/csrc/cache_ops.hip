@@ -232,6 +232,27 @@ extern "C" int vl_rope_and_cache(const float* qkv, int64_t qkv_stride, float* q_
   return VL_OK;
 }
 
+// One workgroup copies n int32 words; src may be pinned host memory, read
+// over the bus by the kernel itself (16-byte loads when both ends allow).
+__global__ void __launch_bounds__(256) copy_words_kernel(int32_t* __restrict__ dst,
+                                                         const int32_t* __restrict__ src,
+                                                         int64_t n) {
+  const bool vec = ((((uintptr_t)dst) | ((uintptr_t)src)) & 15) == 0;
+  const int64_t n4 = vec ? n / 4 : 0;
+  for (int64_t i = threadIdx.x; i < n4; i += 256)
+    reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+  for (int64_t i = n4 * 4 + threadIdx.x; i < n; i += 256) dst[i] = src[i];
+}
+
+extern "C" int vl_copy_words(int32_t* dst, const int32_t* src, int64_t n, void* stream) {
+  VL_CHECK_ARG(n >= 0, "bad count");
+  if (n == 0) return VL_OK;
+  VL_CHECK_ARG(dst && src, "null pointer");
+  copy_words_kernel<<<1, 256, 0, (hipStream_t)stream>>>(dst, src, n);
+  VL_CHECK_LAUNCH();
+  return VL_OK;
+}
+
 extern "C" int vl_resolve_tokens(int32_t* token_ids, int64_t num_tokens, const int32_t* prev_ids,
                                  int64_t num_prev, void* stream) {
   VL_CHECK_ARG(num_tokens >= 0 && num_prev >= 0, "bad counts");

@@ -114,6 +114,23 @@ extern "C" int vl_launcher_wait(void* launcher, uint64_t ticket) {
   return VL_OK;
 }
 
+extern "C" int vl_host_wait_nonneg(const int32_t* values, int64_t n, int64_t timeout_us) {
+  VL_CHECK_ARG(n >= 0 && (values || n == 0), "bad arguments");
+  const volatile int32_t* v = values;
+  const auto t0 = std::chrono::steady_clock::now();
+  int64_t i = 0;
+  for (;;) {
+    while (i < n && v[i] >= 0) ++i;
+    if (i == n) return VL_OK;
+    if (std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(timeout_us)) {
+      vl_set_error("value %lld of %lld still negative after %lld us", (long long)i,
+                   (long long)n, (long long)timeout_us);
+      return VL_EINVAL;
+    }
+    __builtin_ia32_pause();
+  }
+}
+
 extern "C" int vl_launcher_destroy(void* launcher) {
   if (!launcher) return VL_OK;
   Launcher* l = static_cast<Launcher*>(launcher);

@@ -165,6 +165,106 @@ class _Shape:
         self.n_ints = o
 
 
+class RecordStager:
+    """Writes a step's ragged batch into an int32 record (the layout of
+    _Shape) that alternates between `nbuf` host buffers, with the same
+    contents flatten_scheduled gives, in fewer host operations: the per-token
+    and per-sequence segments as one list converted once, and the block
+    tables incrementally. A block-table row is rewritten only when its
+    sequence's table is another list than the one this buffer last held at
+    that row (a different or re-admitted sequence), or the table shrank;
+    when it grew, only the new entries are written. Entries past a row's
+    table are never read (its length bounds every read), so they are left
+    as they are. A step with copy-on-write pairs (block ids replaced inside a
+    table) and any change of the record's layout rewrite every row. Converting
+    the whole table region each step (Sb x W ints, 512 for the 48-request mix)
+    cost 10-18 us of host time per step."""
+
+    def __init__(self, nbuf: int = 2):
+        self._rows = [[] for _ in range(nbuf)]  # per buffer: [table list, entries written]
+        self._layout = [None] * nbuf            # per buffer: (bt offset, W) of its rows
+
+    def reset(self) -> None:
+        """The host buffers were replaced: nothing in them is known."""
+        for k in range(len(self._rows)):
+            self._rows[k] = []
+            self._layout[k] = None
+
+    def stage(self, out, m: np.ndarray, k: int, block_size: int, max_seq_len: int, W: int,
+              short_decode: bool, cap_T: int):
+        """Record of `out` into m (buffer k, sized for cap_T tokens and W
+        blocks per table). Returns (shape, rows, R, T, width); shape is None,
+        and nothing is written, when the step needs more room."""
+        bs = block_size
+        toks: List[int] = []
+        pos: List[int] = []
+        slots: List[int] = []
+        lidx: List[int] = []
+        qsl: List[int] = [0]
+        lens: List[int] = []
+        rows: List[Tuple[int, int]] = []
+        tables = []
+        T = R = max_q = 0
+        width = 1
+        for item in out.scheduled:
+            seq = item.seq
+            st, n = item.start_pos, item.num_tokens
+            ids = seq.table.block_ids
+            nb = len(ids)
+            end = st + n
+            if end > nb * bs:
+                raise ValueError(f"sequence {seq.request_id}: {end} tokens but only {nb} blocks")
+            if end > max_seq_len:
+                raise IndexError(f"position {end - 1} beyond max_seq_len {max_seq_len}")
+            fast = getattr(seq, "token_slice", None)
+            toks += fast(st, end) if fast is not None else seq.token_ids[st:end]
+            if n == 1:
+                pos.append(st)
+                slots.append(ids[st // bs] * bs + st % bs)
+            else:
+                pos += range(st, end)
+                slots += [ids[q // bs] * bs + q % bs for q in range(st, end)]
+            c = min(1 + len(seq.draft_token_ids), n)
+            lidx += range(T + n - c, T + n)
+            rows.append((R, c))
+            T += n
+            R += c
+            qsl.append(T)
+            lens.append(end)
+            tables.append(ids)
+            if nb > width:
+                width = nb
+            if n > max_q:
+                max_q = n
+        S = len(tables)
+        if width > W or T > cap_T:
+            return None, rows, R, T, width  # the caller grows the buffers and stages again
+        shape = _Shape(_bucket(T, 16), _bucket(S, 8), _bucket(R, 8), W,
+                       max_q == 1 and short_decode)
+        Tb, Sb, Rb = shape.Tb, shape.Sb, shape.Rb
+        head = (toks + [0] * (Tb - T) + pos + [0] * (Tb - T) + slots + [-1] * (Tb - T) +
+                lidx + [0] * (Rb - R) + qsl + [T] * (Sb - S) + lens + [0] * (Sb - S))
+        m[:shape.bt] = head
+        known = self._rows[k]
+        if getattr(out, "cow", None) or self._layout[k] != (shape.bt, W):
+            self._layout[k] = (shape.bt, W)
+            known = self._rows[k] = []
+        while len(known) < S:
+            known.append([None, 0])
+        base = shape.bt
+        for i, ids in enumerate(tables):
+            kr = known[i]
+            nb = len(ids)
+            if kr[0] is ids and kr[1] <= nb:
+                if kr[1] < nb:
+                    m[base + i * W + kr[1]:base + i * W + nb] = ids[kr[1]:]
+            else:
+                m[base + i * W:base + i * W + nb] = ids
+                kr[0] = ids
+            kr[1] = nb
+        return shape, rows, R, T, width
+
+
 class HipRunner(ModelRunner):
     def __init__(self, model_cfg, cache_cfg, weights: Dict[str, np.ndarray] = None,
                  device=None, use_graphs: bool = True, one_launch_decode: bool = False):
@@ -212,6 +312,7 @@ class HipRunner(ModelRunner):
                                                   pin_memory=True)
         self.W = max(1, -(-mc.max_seq_len // self.block_size))
         self._buf = 0  # which of the two pinned staging / id buffers the next launch uses
+        self._stager = RecordStager(2)
         self._cap_T = 0
         self._graphs: Dict[Tuple[int, int, int, bool, int], torch.cuda.CUDAGraph] = {}
         self._graph_exec: Dict[Tuple[int, int, int, bool, int], int] = {}  # raw exec handles
@@ -235,8 +336,9 @@ class HipRunner(ModelRunner):
         if launcher is not None:
             try:
                 launcher.drain()
-            finally:
                 launcher.close()
+            except Exception:  # interpreter shutdown: the library may be gone
+                pass
 
     # ------------------------------------------------------------ interface --
     @property
@@ -280,9 +382,14 @@ class HipRunner(ModelRunner):
         next step reads and to the pinned one collect() reads)."""
         k = self._buf
         rows, R, one, ge = self._run(out, k)
+        host = self._ids_hosts_np[k]
         done = self._done[k]
         if ge is not None:
-            ticket = self._launcher.submit(ge, done.cuda_event)
+            # a captured step: its argmax writes the ids into the pinned buffer,
+            # which collect() watches (set negative first: the argmax writes
+            # every row once, ids are >= 0), so no event follows the graph
+            host[:R] = -1
+            ticket, done = self._launcher.submit(ge), None
         else:
             ticket = 0
             ops.hip_check(ops.hip_runtime().hipEventRecord(done.cuda_event, self._stream_h),
@@ -290,14 +397,17 @@ class HipRunner(ModelRunner):
         self._buf ^= 1
         # the handle holds its own buffer and event: a later step that grows
         # the buffers replaces them while this copy may still be queued
-        return rows, R, self._ids_hosts_np[k], (done, ticket), one
+        return rows, R, host, (done, ticket), one
 
     def collect(self, handle) -> Tuple[np.ndarray, List[Tuple[int, int]]]:
         """Waits for a launched step; its ids and rows."""
         rows, R, host, (done, ticket), one = handle
         self._launcher.wait(ticket)
-        ops.hip_check(ops.hip_runtime().hipEventSynchronize(done.cuda_event),
-                      "hipEventSynchronize")
+        if done is None:
+            ops.host_wait_nonneg(host[:R])
+        else:
+            ops.hip_check(ops.hip_runtime().hipEventSynchronize(done.cuda_event),
+                          "hipEventSynchronize")
         if one:
             self._check_step(host)
         return host[:R].copy(), rows
@@ -381,6 +491,7 @@ class HipRunner(ModelRunner):
         self._meta_hosts = [torch.zeros(n_ints, dtype=torch.int32, pin_memory=True)
                             for _ in range(2)]
         self._meta_nps = [m.numpy() for m in self._meta_hosts]
+        self._stager.reset()
         self._x = torch.zeros(cap, mc.d_model, **f32)
         self._h = torch.zeros(cap, mc.d_model, **f32)
         self._delta = torch.zeros(cap, mc.d_model, **f32)
@@ -407,29 +518,23 @@ class HipRunner(ModelRunner):
         self._cap_T = cap
 
     def _stage(self, out, k: int):
-        """Flatten the scheduled batch into pinned record k (the forward
+        """The scheduled batch into pinned record k (RecordStager; the forward
         copies it to the device)."""
-        f = flatten_scheduled(out, self.block_size, self.model_cfg.max_seq_len)
-        if f.T > self._cap_T or f.width > self.W:
+        mc = self.model_cfg
+        for _ in range(2):
+            if self._cap_T > 0:
+                shape, rows, R, T, width = self._stager.stage(
+                    out, self._meta_nps[k], k, self.block_size, mc.max_seq_len, self.W,
+                    self._short_decode, self._cap_T)
+                if shape is not None:
+                    return shape, rows, R
+            else:  # no buffers yet
+                f = flatten_scheduled(out, self.block_size, mc.max_seq_len)
+                T, width = f.T, f.width
             self._launcher.drain()  # the ids of a step in flight are copied over
             with torch.cuda.device(self.device), torch.cuda.stream(self.stream):
-                self._ensure_capacity(f.T, f.width)
-        shape = _Shape(_bucket(f.T, 16), _bucket(f.S, 8), _bucket(f.R, 8), self.W,
-                       f.max_q == 1 and self._short_decode)
-        Tb, Sb, Rb, W = shape.Tb, shape.Sb, shape.Rb, shape.W
-        T, S, R = f.T, f.S, f.R
-        bt = [0] * (Sb * W)
-        for i, ids in enumerate(f.tables):
-            bt[i * W:i * W + len(ids)] = ids
-        m = self._meta_nps[k]
-        m[shape.tok:shape.tok + Tb] = f.toks + [0] * (Tb - T)
-        m[shape.pos:shape.pos + Tb] = f.pos + [0] * (Tb - T)
-        m[shape.slot:shape.slot + Tb] = f.slots + [-1] * (Tb - T)
-        m[shape.lidx:shape.lidx + Rb] = f.lidx + [0] * (Rb - R)
-        m[shape.qsl:shape.qsl + Sb + 1] = f.qsl + [T] * (Sb - S)
-        m[shape.lens:shape.lens + Sb] = f.lens + [0] * (Sb - S)
-        m[shape.bt:shape.bt + Sb * W] = bt
-        return shape, f.rows, R
+                self._ensure_capacity(T, width)
+        raise RuntimeError("staging buffers did not grow to the step")
 
     # -------------------------------------------------------------- forward --
     def _copy_on_write(self, pairs) -> None:
@@ -441,7 +546,9 @@ class HipRunner(ModelRunner):
         bucket's Rb logits rows into self._ids and pinned buffer k (rows past
         the step's R are the padded rows' and never read)."""
         n = s.n_ints
-        self._meta[:n].copy_(self._meta_hosts[k][:n], non_blocking=True)
+        # read from the pinned record by a kernel: as a graph's memcpy node
+        # this copy cost ~12 us more per step
+        ops.copy_words(self._meta[:n], self._meta_hosts[k][:n])
         self._forward_body(s)
         ops.argmax_rows(self._logits[:s.Rb], self._ids[:s.Rb], host_out=self._ids_hosts[k])
 

@@ -13,6 +13,7 @@ import ctypes
 import os
 from typing import Optional
 
+import numpy as np
 import torch
 
 from .build import LIB_PATH
@@ -35,6 +36,7 @@ SIGNATURES = {
     "vl_launcher_submit": (_i32, [_c_void_p, _c_void_p, _c_void_p, ctypes.POINTER(ctypes.c_uint64)]),
     "vl_launcher_wait": (_i32, [_c_void_p, ctypes.c_uint64]),
     "vl_launcher_destroy": (_i32, [_c_void_p]),
+    "vl_host_wait_nonneg": (_i32, [_c_void_p, _i64, _i64]),
     "vl_reshape_and_cache": (_i32, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p,
                                     _c_void_p, _i64, _i32, _i32, _i32, _i32, _i32, _c_void_p]),
     "vl_copy_blocks": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i64, _i64, _i32,
@@ -73,6 +75,7 @@ SIGNATURES = {
                                  _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32,
                                  _i32, _i32, _i32, _c_void_p]),
     "vl_resolve_tokens": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p]),
+    "vl_copy_words": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p]),
     "vl_decode_step_supported": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "vl_decode_step": (_i32, [_c_void_p, _c_void_p, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                               _c_void_p, _i64, _i32, _i32, _c_void_p, _c_void_p, _c_void_p,
@@ -164,6 +167,14 @@ class Launcher:
             self.close()
         except Exception:
             pass
+
+
+def host_wait_nonneg(values: np.ndarray, timeout_s: float = 30.0) -> None:
+    """Until every entry of a pinned int32 host array is >= 0 (written by a
+    kernel after the caller set them negative); raises after timeout_s."""
+    _need(values.dtype == np.int32 and values.flags.c_contiguous, "contiguous int32 array")
+    _check(lib().vl_host_wait_nonneg(values.ctypes.data, values.size, int(timeout_s * 1e6)),
+           "vl_host_wait_nonneg")
 
 
 def hip_check(rc: int, what: str) -> None:
@@ -598,6 +609,14 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor,
           "host_out must be a pinned contiguous int32 tensor")
     _check(lib().vl_argmax_rows(_ptr(logits), logits.stride(0), logits.shape[0], logits.shape[1],
                                 _ptr(out), _ptr(host_out), _stream()), "vl_argmax_rows")
+
+
+def copy_words(dst: torch.Tensor, src: torch.Tensor) -> None:
+    """dst[:] = src (int32, src may be pinned host memory) by one kernel
+    (vl_copy_words)."""
+    _need(dst.dtype == torch.int32 and src.dtype == torch.int32 and dst.is_contiguous() and
+          src.is_contiguous() and dst.numel() == src.numel(), "int32 tensors of one size required")
+    _check(lib().vl_copy_words(_ptr(dst), _ptr(src), dst.numel(), _stream()), "vl_copy_words")
 
 
 def resolve_tokens(token_ids: torch.Tensor, prev_ids: torch.Tensor) -> None:

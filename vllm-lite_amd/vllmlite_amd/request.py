@@ -31,16 +31,21 @@ class Status(enum.Enum):
 
     @property
     def finished(self) -> bool:
-        return self in _FINISHED
+        return self._finished
 
 
-_FINISHED = frozenset((Status.FINISHED_STOP, Status.FINISHED_LENGTH, Status.ABORTED))
+# per member, as plain attributes: the engine asks these of every running
+# request every step, and an Enum member's hash is a Python-level call
 _REASONS = {Status.FINISHED_STOP: "stop", Status.FINISHED_LENGTH: "length",
             Status.ABORTED: "abort"}
+for _s in Status:
+    _s._finished = _s in _REASONS
+    _s._reason = _REASONS.get(_s)
+del _s
 
 
 def finish_reason(status: Status) -> Optional[str]:
-    return _REASONS.get(status)
+    return status._reason
 
 
 @dataclass

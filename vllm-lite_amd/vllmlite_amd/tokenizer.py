@@ -21,6 +21,7 @@ PAD = 258
 VOCAB_SIZE = 261
 
 _Utf8 = codecs.getincrementaldecoder("utf-8")
+_BYTE = [bytes((i,)) for i in range(256)]
 
 
 class ByteTokenizer:
@@ -40,7 +41,13 @@ class ByteTokenizer:
     def stream_decoder(self):
         """A callable new_ids -> text completed by them."""
         dec = _Utf8(errors="replace")
-        return lambda new: dec.decode(bytes(t for t in new if t < 256))
+
+        def feed(new: List[int]) -> str:
+            if len(new) == 1:  # a decode step's one token
+                t = new[0]
+                return dec.decode(_BYTE[t]) if 0 <= t < 256 else ""
+            return dec.decode(bytes(t for t in new if t < 256))
+        return feed
 
 
 def get_tokenizer(name=None):
