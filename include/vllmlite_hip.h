@@ -256,6 +256,21 @@ int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_str
                    void* stream);
 
 /*
+ * vl_linear_rows in VL_LINEAR_SWIGLU mode over tiled weights, with the input
+ * rows x[r] + x_parts[r, 0] + ... + x_parts[r, num_parts - 1] (x_parts
+ * [rows, num_parts, k] fp32, summed in that order; num_parts 1, 2, 4 or 8;
+ * k <= 512): the residual add of vllmlite/model.py:114 (x + attn @ wo, wo's
+ * product arriving as one partial row per KV head from
+ * vl_decode_attention_wo) fused into the RMSNorm + gate|up + SwiGLU of
+ * model.py:116-117. When x_out != NULL (not x) the summed rows are written
+ * there too [rows, k], the residual the down projection adds to.
+ */
+int vl_linear_rows_parts(float* out, int64_t out_stride, const float* x, int64_t x_stride,
+                         const float* x_parts, int num_parts, float* x_out, const float* weight,
+                         const float* norm_weight, float eps, int rows, int k, int n,
+                         void* stream);
+
+/*
  * K6b the QKV projection of a step's rows fused with RoPE and the K/V
  * scatter (vllmlite/model.py:96-103, 109; vllmlite/attention.py:21-37,
  * 47-49): qkv = f(x) @ weight (weight [k, (num_heads + 2 num_kv_heads) *
@@ -281,6 +296,28 @@ int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cache, const fl
                       const int32_t* slot_mapping, const float* cos_table, const float* sin_table,
                       int rows, int k, int num_heads, int num_kv_heads, int head_dim,
                       int cache_dtype, int kv_layout, int block_size, void* stream);
+
+/*
+ * K2 for a decode batch (every sequence one query; the short-decode kernel's
+ * shapes: fp32 queries over fp32 / bf16 / FP8 E4M3 caches, dtype
+ * VL_DTYPE_F32 / _F32_BF16KV / _F32_FP8KV, head_dim 16 / 32 / 48 / 64, 1 / 2 /
+ * 4 / 8 query heads per KV head, power-of-two blocks, 0 < max_context_len <=
+ * 2048) fused with the output projection (vllmlite/attention.py:59-98 then
+ * model.py:114's attn @ wo): instead of the attention rows, parts[s, g, :] =
+ * (sequence s's outputs of the query heads of KV head g, as one row of
+ * heads-per-group x head_dim) @ wo[those rows, 0 .. d_model), wo row-major
+ * [num_heads * head_dim, d_model], d_model <= 512. Summed over g (in order)
+ * and added to the residual, they are model.py:114's x + attn @ wo
+ * (vl_linear_rows_parts does that in the next projection's prologue).
+ * Arguments otherwise as vl_paged_attention_run.
+ */
+int vl_decode_attention_wo(float* parts, const float* query, int64_t query_stride,
+                           const void* key_cache, const void* value_cache,
+                           const int32_t* block_tables, int block_table_stride,
+                           const int32_t* seq_lens, const int32_t* query_start_loc, int num_seqs,
+                           int num_heads, int num_kv_heads, int head_dim, int block_size,
+                           float scale, int dtype, int kv_layout, int max_context_len,
+                           const float* wo, int d_model, void* stream);
 
 /*
  * A copy of n int32 words by one kernel (no counterpart in the reference,

@@ -708,3 +708,61 @@ def test_fp8_cache_values_decode_exactly(D, q_len):
                       max_query_len=q_len, min_query_len=q_len, max_context_len=q_len)
     got = to_np(out).reshape(S, q_len, D)[:, 0, :]
     np.testing.assert_array_equal(got, fp8_e4m3_decode(codes))
+
+
+@pytest.mark.parametrize("cache", ["f32", "bf16", "fp8"])
+@pytest.mark.parametrize("D,H,Hkv,dm", [(48, 8, 4, 384), (16, 4, 2, 64), (64, 8, 1, 512),
+                                        (32, 16, 2, 96)])
+@pytest.mark.parametrize("layout", ["token", "head"])
+def test_decode_attention_wo_equals_attention_then_wo(cache, D, H, Hkv, dm, layout):
+    """vl_decode_attention_wo: parts[s, g] = (sequence s's attention outputs of
+    KV head g's query heads) @ those rows of wo, and their sum over g is
+    attn @ wo (vllmlite/model.py:114), against float64 products of the
+    oracle's attention rows (a sequence without a query in the middle keeps
+    its parts unwritten)."""
+    o = ops()
+    seqs = [(1, c) for c in SHORT_CTX[:4]] + [(0, 30)] + [(1, c) for c in SHORT_CTX[4:7]]
+    from oracle.attention import fp8_e4m3_decode, fp8_e4m3_encode
+    b = make_batch(seqs, H, Hkv, D, 16, seed=D + H + dm)
+    if cache == "fp8":
+        def fp8_dev(x):
+            return dev(fp8_e4m3_encode(x)).view(torch.float8_e4m3fn)
+        hm = (lambda x: head_major(x, 16)) if layout == "head" else (lambda x: x)
+        kc, vc = fp8_dev(hm(b["k_cache"])), fp8_dev(hm(b["v_cache"]))
+        ck = lambda a: fp8_e4m3_decode(fp8_e4m3_encode(a))  # noqa: E731
+    else:
+        kc, vc = caches(b, torch.float32 if cache == "f32" else torch.bfloat16, layout)
+        ck = (lambda a: a) if cache == "f32" else bf16_round
+    rng = np.random.default_rng(dm + Hkv)
+    wo = (rng.standard_normal((H * D, dm)) / np.sqrt(H * D)).astype(np.float32)
+    S = len(seqs)
+    parts = torch.full((S, Hkv, dm), float("nan"), device="cuda")
+    o.decode_attention_wo(parts, dev(b["q"]), kc, vc, dev(b["block_tables"]), dev(b["seq_lens"]),
+                          dev(b["qsl"]), b["scale"], 16, dev(wo), int(b["seq_lens"].max()))
+    torch.cuda.synchronize()
+    att = oracle_attention(b, b["q"], ck(b["k_cache"]), ck(b["v_cache"])).astype(np.float64)
+    got = parts.cpu().numpy().astype(np.float64)
+    rep = H // Hkv
+    for i, (q, _) in enumerate(seqs):
+        if q == 0:
+            assert np.isnan(got[i]).all()
+            continue
+        t = b["qsl"][i]
+        for g in range(Hkv):
+            rows = att[t, g * rep:(g + 1) * rep].reshape(-1)
+            want = rows @ wo[g * rep * D:(g + 1) * rep * D].astype(np.float64)
+            err = np.abs(got[i, g] - want).max() / max(1e-3, np.abs(want).max())
+            assert err < 2e-5, (i, g, err)
+        total = att[t].reshape(-1) @ wo.astype(np.float64)
+        np.testing.assert_allclose(got[i].sum(0), total, rtol=0, atol=2e-5 * np.abs(total).max())
+
+
+def test_decode_attention_wo_refuses_other_batches():
+    o = ops()
+    b = make_batch([(1, 40), (1, 3000)], 8, 4, 48, 16, seed=3)
+    parts = torch.zeros((2, 4, 384), device="cuda")
+    wo = torch.zeros((384, 384), device="cuda")
+    with pytest.raises(RuntimeError):  # a context beyond the short-decode bound
+        o.decode_attention_wo(parts, dev(b["q"]), dev(b["k_cache"]), dev(b["v_cache"]),
+                              dev(b["block_tables"]), dev(b["seq_lens"]), dev(b["qsl"]),
+                              b["scale"], 16, wo, 3000)

@@ -334,3 +334,33 @@ def test_qkv_rope_cache_tiled_weights_same_bits():
     o.qkv_rope_cache(q2, kc2, vc2, x, o.tile16(w), g, pos, slot, cos, sin, H, Hkv, D)
     torch.cuda.synchronize()
     assert torch.equal(q1, q2) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+
+
+@pytest.mark.parametrize("rows", [1, 4, 7, 16, 33])
+@pytest.mark.parametrize("k,n,P", [(384, 1024, 4), (512, 256, 8), (64, 128, 1), (128, 48, 2)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_linear_rows_parts_equals_summed_input(rows, k, n, P, norm):
+    """vl_linear_rows_parts: the SwiGLU projection of x + parts[:, 0] + ... +
+    parts[:, P - 1] (summed in that order) gives the same bits as
+    vl_linear_rows over the rows summed beforehand in that order, and x_out
+    receives those summed rows."""
+    o = _ops()
+    rng = np.random.default_rng(rows * 31 + k + P + norm)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    parts = (0.3 * rng.standard_normal((rows, P, k))).astype(np.float32)
+    w = (0.05 * rng.standard_normal((k, 2 * n))).astype(np.float32)
+    g = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    summed = x.copy()
+    for p in range(P):
+        summed = summed + parts[:, p]
+    wt = o.tile16(torch.from_numpy(w), 2).cuda()
+    dx, dp, dg = (torch.from_numpy(a).cuda() for a in (x, parts, g))
+    got = torch.full((rows, n), float("nan"), device="cuda")
+    x_out = torch.full((rows, k), float("nan"), device="cuda")
+    o.linear_rows_parts(got, dx, dp, wt, dg if norm else None, x_out=x_out)
+    want = torch.full((rows, n), float("nan"), device="cuda")
+    o.linear_rows(want, torch.from_numpy(summed).cuda(), wt, dg if norm else None,
+                  mode=o.LINEAR_SWIGLU)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert np.array_equal(x_out.cpu().numpy(), summed)

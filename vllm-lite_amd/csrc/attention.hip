@@ -1898,6 +1898,7 @@ struct ShortLds {
   float m[NW][REP], l[NW][REP];
   int32_t tbl[kShortCtx];   // the sequence's block ids
   uint4 k[kStageK ? NW : 1][kStageK ? 64 : 1][kStageK ? kNCP : 1];  // per wavefront: its keys' K rows
+  float o[REP * D];         // with wo: the workgroup's merged output rows
 };
 
 
@@ -1915,12 +1916,20 @@ __device__ __forceinline__ void load_row(const T* p, float (&r)[D]) {
 }
 
 // T: query and output elements, TKV: cache elements; NW wavefronts.
+// With wo (fp32 T only): instead of its REP output rows the workgroup writes
+// parts[i, g, :] = (its REP x D outputs, as one row) @ wo[g REP D .. (g + 1)
+// REP D, 0 .. wo_n) (row-major, wo_n columns): the output projection of
+// vllmlite/model.py:114 split by KV head, whose wo_n-wide partial rows the
+// next projection adds to its input in KV-head order. Thread t < wo_n takes
+// column t; its REP D weights are loaded when the key chunks are done, so
+// they arrive during the merge of the wavefronts.
 template <typename T, typename TKV, int D, int REP, int NW>
 __global__ void __launch_bounds__(64 * NW) attend_short_decode_kernel(
     T* __restrict__ out, const T* __restrict__ query, int64_t q_stride, const TKV* kc,
     const TKV* vc, const int32_t* __restrict__ bt, int bt_stride,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int Hkv, int bs_log2,
-    int kv_hm, float scale_log2) {
+    int kv_hm, float scale_log2, const float* __restrict__ wo, int wo_n,
+    float* __restrict__ parts) {
   using Lds = ShortLds<TKV, D, REP, NW>;
   constexpr int VE = Lds::kVE;
   constexpr int kThreads = 64 * NW;
@@ -2035,6 +2044,15 @@ __global__ void __launch_bounds__(64 * NW) attend_short_decode_kernel(
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
+  // with wo: this thread's column of the workgroup's wo rows, in flight
+  // during the merge below
+  float wcol[REP * D];
+  const bool wo_col = wo != nullptr && tid < wo_n;
+  if (wo_col) {
+    const float* wc = wo + (int64_t)g * REP * D * wo_n + tid;
+#pragma unroll
+    for (int k = 0; k < REP * D; ++k) wcol[k] = wc[(int64_t)k * wo_n];
+  }
 #pragma unroll
   for (int h = 0; h < REP; ++h) lsum[h] = wave_sum_dpp(lsum[h]);
   if (lane == 0) {
@@ -2079,7 +2097,21 @@ __global__ void __launch_bounds__(64 * NW) attend_short_decode_kernel(
       L = __builtin_fmaf(s.l[w][h], wt, L);
       a = __builtin_fmaf(s.p[w][h][d], wt, a);
     }
-    Elem<T>::store(out, ((int64_t)tok * H + g * REP + h) * D + d, L > 0.f ? a * (1.f / L) : 0.f);
+    const float o = L > 0.f ? a * (1.f / L) : 0.f;
+    if (wo)
+      s.o[e] = o;
+    else
+      Elem<T>::store(out, ((int64_t)tok * H + g * REP + h) * D + d, o);
+  }
+  if (wo) {
+    __syncthreads();
+    if (wo_col) {
+      // four independent chains (k = 4 u + c), added in order at the end
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < REP * D; ++k) acc[k & 3] = __builtin_fmaf(s.o[k], wcol[k], acc[k & 3]);
+      parts[((int64_t)i * Hkv + g) * wo_n + tid] = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+    }
   }
 }
 
@@ -2409,7 +2441,8 @@ inline bool short_decode(const Args& a, int max_q, int max_ctx) {
 }
 
 template <typename T, typename TKV, int D>
-int launch_short_decode_d(const Args& a, float sl2, hipStream_t st) {
+int launch_short_decode_d(const Args& a, float sl2, hipStream_t st, const float* wo = nullptr,
+                          int wo_n = 0, float* parts = nullptr) {
   const int rep = a.H / a.Hkv;
   const int grid = a.S * a.Hkv;
   if (grid == 0) return VL_OK;
@@ -2417,7 +2450,8 @@ int launch_short_decode_d(const Args& a, float sl2, hipStream_t st) {
 #define VL_SHORT(REP)                                                                        \
   attend_short_decode_kernel<T, TKV, D, REP, kShortWaves><<<grid, 64 * kShortWaves, 0, st>>>( \
       (T*)a.out, (const T*)a.query, a.q_stride, (const TKV*)a.kc, (const TKV*)a.vc, a.bt,    \
-      a.bt_stride, a.seq_lens, a.qsl, a.Hkv, bs_log2, a.kv_layout == VL_KV_HEAD_MAJOR ? 1 : 0, sl2)
+      a.bt_stride, a.seq_lens, a.qsl, a.Hkv, bs_log2, a.kv_layout == VL_KV_HEAD_MAJOR ? 1 : 0, sl2, \
+      wo, wo_n, parts)
   switch (rep) {
     case 1: VL_SHORT(1); break;
     case 2: VL_SHORT(2); break;
@@ -2430,12 +2464,13 @@ int launch_short_decode_d(const Args& a, float sl2, hipStream_t st) {
 }
 
 template <typename T, typename TKV>
-int launch_short_decode(const Args& a, float sl2, hipStream_t st) {
+int launch_short_decode(const Args& a, float sl2, hipStream_t st, const float* wo = nullptr,
+                        int wo_n = 0, float* parts = nullptr) {
   switch (a.D) {
-    case 16: return launch_short_decode_d<T, TKV, 16>(a, sl2, st);
-    case 32: return launch_short_decode_d<T, TKV, 32>(a, sl2, st);
-    case 48: return launch_short_decode_d<T, TKV, 48>(a, sl2, st);
-    default: return launch_short_decode_d<T, TKV, 64>(a, sl2, st);
+    case 16: return launch_short_decode_d<T, TKV, 16>(a, sl2, st, wo, wo_n, parts);
+    case 32: return launch_short_decode_d<T, TKV, 32>(a, sl2, st, wo, wo_n, parts);
+    case 48: return launch_short_decode_d<T, TKV, 48>(a, sl2, st, wo, wo_n, parts);
+    default: return launch_short_decode_d<T, TKV, 64>(a, sl2, st, wo, wo_n, parts);
   }
 }
 
@@ -2588,6 +2623,45 @@ extern "C" int vl_paged_attention_run(void* out, const void* query, int64_t quer
                  "caches must be 16-byte aligned");
   return dispatch_run(a, max_query_len, min_query_len, max_context_len, workspace,
                       workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int vl_decode_attention_wo(float* parts, const float* query, int64_t query_stride,
+                                      const void* key_cache, const void* value_cache,
+                                      const int32_t* block_tables, int block_table_stride,
+                                      const int32_t* seq_lens, const int32_t* query_start_loc,
+                                      int num_seqs, int num_heads, int num_kv_heads, int head_dim,
+                                      int block_size, float scale, int dtype, int kv_layout,
+                                      int max_context_len, const float* wo, int d_model,
+                                      void* stream) {
+  Args a{parts, query, query_stride, key_cache, value_cache, block_tables, block_table_stride,
+         seq_lens, query_start_loc, num_seqs, num_seqs, num_heads, num_kv_heads, head_dim,
+         block_size, scale, dtype, kv_layout};
+  VL_CHECK_ARG(dtype == VL_DTYPE_F32 || dtype == VL_DTYPE_F32_BF16KV || dtype == VL_DTYPE_F32_FP8KV,
+               "fp32 queries required (dtype %d)", dtype);
+  VL_CHECK_ARG(num_seqs >= 0 && num_kv_heads > 0 && num_heads > 0 && num_heads % num_kv_heads == 0,
+               "bad head counts");
+  VL_CHECK_ARG(short_decode(a, 1, max_context_len),
+               "not a short-decode batch (head_dim 16/32/48/64, 1/2/4/8 query heads per KV head, "
+               "power-of-two blocks, 0 < max_context_len <= %d)", kShortCtx);
+  VL_CHECK_ARG(d_model > 0 && d_model <= 64 * kShortWaves, "d_model must be in 1..%d",
+               64 * kShortWaves);
+  VL_CHECK_ARG(query_stride >= (int64_t)num_heads * head_dim, "query row stride too small");
+  KvGeom geom;
+  if (int rc = vl_kv_geom(kv_layout, block_size, num_kv_heads, head_dim, &geom)) return rc;
+  if (num_seqs == 0) return VL_OK;
+  VL_CHECK_ARG(parts && query && key_cache && value_cache && block_tables && seq_lens &&
+                   query_start_loc && wo,
+               "null pointer");
+  VL_CHECK_ARG(((uintptr_t)key_cache & 15) == 0 && ((uintptr_t)value_cache & 15) == 0,
+               "caches must be 16-byte aligned");
+  const float sl2 = scale * kLog2e;
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case VL_DTYPE_F32: return launch_short_decode<float, float>(a, sl2, st, wo, d_model, parts);
+    case VL_DTYPE_F32_BF16KV:
+      return launch_short_decode<float, uint16_t>(a, sl2, st, wo, d_model, parts);
+    default: return launch_short_decode<float, uint8_t>(a, sl2, st, wo, d_model, parts);
+  }
 }
 
 extern "C" int vl_paged_attention(void* out, const void* query, int64_t query_stride,

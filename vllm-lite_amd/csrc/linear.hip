@@ -97,13 +97,15 @@ __device__ __forceinline__ void store_cache(void* cache, int64_t i, float v, int
 // s][c0 + m]. The 8 wavefronts' partial 16 x 16 tiles (and, with NORM, each
 // lane's sum of x^2 over its k) meet in LDS behind the kernel's one barrier
 // and are summed in wavefront order, so every run gives the same bits.
-template <int MODE, bool NORM, int KMAX, bool TILES>
+// NP > 0: the input rows are x[r] + x_parts[r, 0] + ... + x_parts[r, NP - 1]
+// (rows of K, summed in that order; vl_linear_rows_parts).
+template <int MODE, bool NORM, int KMAX, bool TILES, int NP = 0>
 __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
     float* __restrict__ out, int64_t ldo, const float* __restrict__ x, int64_t ldx,
     const float* __restrict__ w, int64_t ldw, int64_t up_off, const float* __restrict__ norm_w,
     float eps, int M, int K, int N, const RopeCache rc, const int32_t* __restrict__ row_index,
     const int32_t* __restrict__ prev_ids, int64_t num_prev, float* __restrict__ x_out,
-    int nsub, int rt) {
+    int nsub, int rt, const float* __restrict__ x_parts = nullptr) {
   constexpr int kSlices = MODE == 2 ? 2 : 1;
   constexpr int kGroups = KMAX / (16 * kLinWaves);  // 16-k groups per wavefront at K = KMAX
   static_assert(kGroups >= 1 && KMAX % (16 * kLinWaves) == 0, "whole 16-k groups");
@@ -164,6 +166,25 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
 #pragma unroll
     for (int g = 0; g < kGroups; ++g)
       xv[g] = *reinterpret_cast<const float4*>(xr + 16 * min(gb + g, ng - 1) + 4 * j);
+    if constexpr (NP > 0) {
+      float4 pv[NP][kGroups];  // every load issued before the first add
+      const float* pr = x_parts + row * NP * K;
+#pragma unroll
+      for (int q = 0; q < NP; ++q)
+#pragma unroll
+        for (int g = 0; g < kGroups; ++g)
+          pv[q][g] =
+              *reinterpret_cast<const float4*>(pr + (int64_t)q * K + 16 * min(gb + g, ng - 1) + 4 * j);
+#pragma unroll
+      for (int g = 0; g < kGroups; ++g)
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+          xv[g].x += pv[q][g].x;
+          xv[g].y += pv[q][g].y;
+          xv[g].z += pv[q][g].z;
+          xv[g].w += pv[q][g].w;
+        }
+    }
   };
   // thread t writes row t / 16, column c0 + t % 16
   float e_resid = 0.f, e_cos = 0.f, e_sin = 0.f;
@@ -360,11 +381,12 @@ inline int row_tile(int M, int N) {
   return kRowsMax;
 }
 
-template <int MODE, bool NORM, int KMAX>
+template <int MODE, bool NORM, int KMAX, int NP = 0>
 int launch(float* out, int64_t ldo, const float* x, int64_t ldx, const float* w, int64_t ldw,
            bool tiles, const float* norm_w, float eps, int M, int K, int N, hipStream_t st,
            const int32_t* row_index, const RopeCache& rc = RopeCache{}, float* x_out = nullptr,
-           const int32_t* prev_ids = nullptr, int64_t num_prev = 0) {
+           const int32_t* prev_ids = nullptr, int64_t num_prev = 0,
+           const float* x_parts = nullptr) {
   const int ntile = (N + kCols - 1) / kCols;
   const int rt = row_tile(M, N);
   const int row_tiles = (M + rt - 1) / rt;
@@ -372,10 +394,10 @@ int launch(float* out, int64_t ldo, const float* x, int64_t ldx, const float* w,
   const dim3 grid(ntile, (row_tiles + nsub - 1) / nsub);
   if (tiles) {
     const int64_t up_off = MODE == 2 ? (int64_t)ntile * K * kCols : 0;
-    linear_rows_kernel<MODE, NORM, KMAX, true><<<grid, 64 * kLinWaves, 0, st>>>(
+    linear_rows_kernel<MODE, NORM, KMAX, true, NP><<<grid, 64 * kLinWaves, 0, st>>>(
         out, ldo, x, ldx, w, 0, up_off, norm_w, eps, M, K, N, rc, row_index, prev_ids, num_prev,
-        x_out, nsub, rt);
-  } else {
+        x_out, nsub, rt, x_parts);
+  } else if constexpr (NP == 0) {
     const int64_t up_off = MODE == 2 ? N : 0;
     linear_rows_kernel<MODE, NORM, KMAX, false><<<grid, 64 * kLinWaves, 0, st>>>(
         out, ldo, x, ldx, w, ldw, up_off, norm_w, eps, M, K, N, rc, row_index, prev_ids,
@@ -383,6 +405,22 @@ int launch(float* out, int64_t ldo, const float* x, int64_t ldx, const float* w,
   }
   VL_CHECK_LAUNCH();
   return VL_OK;
+}
+
+template <int NP>
+int launch_parts(float* out, int64_t ldo, const float* x, int64_t ldx, const float* x_parts,
+                 float* x_out, const float* w, const float* norm_w, float eps, int M, int K, int N,
+                 hipStream_t st) {
+  const bool nrm = norm_w != nullptr;
+  if (K <= 384)
+    return nrm ? launch<2, true, 384, NP>(out, ldo, x, ldx, w, 0, true, norm_w, eps, M, K, N, st,
+                                          nullptr, RopeCache{}, x_out, nullptr, 0, x_parts)
+               : launch<2, false, 384, NP>(out, ldo, x, ldx, w, 0, true, norm_w, eps, M, K, N, st,
+                                           nullptr, RopeCache{}, x_out, nullptr, 0, x_parts);
+  return nrm ? launch<2, true, 512, NP>(out, ldo, x, ldx, w, 0, true, norm_w, eps, M, K, N, st,
+                                        nullptr, RopeCache{}, x_out, nullptr, 0, x_parts)
+             : launch<2, false, 512, NP>(out, ldo, x, ldx, w, 0, true, norm_w, eps, M, K, N, st,
+                                         nullptr, RopeCache{}, x_out, nullptr, 0, x_parts);
 }
 
 }  // namespace
@@ -475,4 +513,32 @@ extern "C" int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cach
   if (k <= 512) return nrm ? VL_QKV(true, 512) : VL_QKV(false, 512);
   return nrm ? VL_QKV(true, 1024) : VL_QKV(false, 1024);
 #undef VL_QKV
+}
+
+extern "C" int vl_linear_rows_parts(float* out, int64_t out_stride, const float* x,
+                                    int64_t x_stride, const float* x_parts, int num_parts,
+                                    float* x_out, const float* weight, const float* norm_weight,
+                                    float eps, int rows, int k, int n, void* stream) {
+  VL_CHECK_ARG(rows >= 0 && rows <= kRowsLimit, "rows must be in 0..%d", kRowsLimit);
+  VL_CHECK_ARG(k > 0 && k % 16 == 0 && k <= 512, "k must be a multiple of 16, at most 512");
+  VL_CHECK_ARG(n > 0, "n must be positive");
+  VL_CHECK_ARG(num_parts == 1 || num_parts == 2 || num_parts == 4 || num_parts == 8,
+               "num_parts must be 1, 2, 4 or 8");
+  if (rows == 0) return VL_OK;
+  VL_CHECK_ARG(out && x && x_parts && weight, "null pointer");
+  VL_CHECK_ARG((((uintptr_t)x) & 15) == 0 && x_stride % 4 == 0 && x_stride >= k,
+               "x must be 16-byte aligned with a row stride that is a multiple of 4");
+  VL_CHECK_ARG((((uintptr_t)x_parts) & 15) == 0 && (!x_out || (((uintptr_t)x_out) & 15) == 0),
+               "x_parts and x_out must be 16-byte aligned");
+  VL_CHECK_ARG(out_stride >= n, "row stride too small");
+  VL_CHECK_ARG((((uintptr_t)weight) & 15) == 0, "tiled weight must be 16-byte aligned");
+  VL_CHECK_ARG((((uintptr_t)norm_weight) & 15) == 0, "norm weight must be 16-byte aligned");
+  VL_CHECK_ARG(x_out != x, "x_out must not be x (other workgroups still read x)");
+  hipStream_t st = (hipStream_t)stream;
+  switch (num_parts) {
+    case 1: return launch_parts<1>(out, out_stride, x, x_stride, x_parts, x_out, weight, norm_weight, eps, rows, k, n, st);
+    case 2: return launch_parts<2>(out, out_stride, x, x_stride, x_parts, x_out, weight, norm_weight, eps, rows, k, n, st);
+    case 4: return launch_parts<4>(out, out_stride, x, x_stride, x_parts, x_out, weight, norm_weight, eps, rows, k, n, st);
+    default: return launch_parts<8>(out, out_stride, x, x_stride, x_parts, x_out, weight, norm_weight, eps, rows, k, n, st);
+  }
 }

@@ -267,7 +267,8 @@ class RecordStager:
 
 class HipRunner(ModelRunner):
     def __init__(self, model_cfg, cache_cfg, weights: Dict[str, np.ndarray] = None,
-                 device=None, use_graphs: bool = True, one_launch_decode: bool = False):
+                 device=None, use_graphs: bool = True, one_launch_decode: bool = False,
+                 fused_wo: bool = True):
         if not torch.cuda.is_available():
             raise RuntimeError("HipRunner needs a visible MI355X (torch.cuda.is_available() is False)")
         ops.lib()  # fail now, loudly, if the gfx950 library is not built
@@ -329,6 +330,9 @@ class HipRunner(ModelRunner):
         # they select the short-decode kernel, which needs no plan
         self._short_decode = not ops.paged_attention_reads_plan(
             self.H, self.Hkv, self.hd, self.block_size, 1, mc.max_seq_len)
+        # decode steps with wo inside the attention launch (vl_decode_attention_wo)
+        self._fused_wo = (self._short_decode and self._fused_rows and self.Hkv in (1, 2, 4, 8)
+                          and mc.d_model <= 512 and fused_wo)
 
     def __del__(self):
         # the submission thread may still hold launches of this runner's graphs
@@ -500,6 +504,8 @@ class HipRunner(ModelRunner):
         self._attn = torch.zeros(cap, H, hd, **f32)
         self._gu = torch.zeros(cap, 2 * mc.d_ff, **f32)
         self._act = torch.zeros(cap, mc.d_ff, **f32)
+        # decode steps: wo's product as one partial row per (sequence, KV head)
+        self._parts = torch.zeros(cap, self.Hkv, mc.d_model, **f32)
         self._hsel = torch.zeros(cap, mc.d_model, **f32)
         self._logits = torch.zeros(cap, mc.vocab_size, **f32)
         self._logits_host = torch.zeros(cap, mc.vocab_size, dtype=torch.float32, pin_memory=True)
@@ -614,8 +620,14 @@ class HipRunner(ModelRunner):
         prefill steps up to fused_rows_max rows): each projection is one
         launch with its RMSNorm, residual add, SwiGLU or RoPE + K/V scatter
         fused in, so a layer is QKV (+ RoPE + cache), attention, output (+=
-        residual), gate|up (SwiGLU), down (+= residual)."""
+        residual), gate|up (SwiGLU), down (+= residual). A decode step of the
+        short-decode shape has its output projection inside the attention
+        launch (one partial row per KV head) and the residual add in gate|up's
+        prologue: four launches per layer."""
         W, Tb, Rb = self.w, s.Tb, s.Rb
+        if s.decode and self._fused_wo:
+            self._forward_decode_wo(s, x, q, act, tok, pos, slot, lidx, qsl, lens, bt)
+            return
         self._plan(s, q, lens, qsl)
         for li, L in enumerate(W["layers"]):
             kc, vc = self.cache_k[li], self.cache_v[li]
@@ -634,6 +646,36 @@ class HipRunner(ModelRunner):
             ops.linear_rows(act, x, L["w_gate_up_t"], L["ffn_norm"], mode=ops.LINEAR_SWIGLU)
             ops.linear_rows(x, act, L["w_down_t"], mode=ops.LINEAR_ACCUMULATE)
         ops.linear_rows(self._logits[:Rb], x, W["lm_head_t"], W["final_norm"],
+                        mode=ops.LINEAR_STORE, row_index=lidx)
+
+    def _forward_decode_wo(self, s: _Shape, x, q, act, tok, pos, slot, lidx, qsl, lens,
+                           bt) -> None:
+        """A decode step in four launches per layer: QKV (+ RoPE + cache);
+        attention with wo (vl_decode_attention_wo: parts[s, g] = the outputs
+        of KV head g's query heads @ their rows of wo); gate|up over x + the
+        parts summed in KV-head order, which also writes that sum, the
+        residual, to the other of two row buffers; down added to it there.
+        The two buffers swap roles every layer."""
+        W, Tb, Rb, Sb = self.w, s.Tb, s.Rb, s.Sb
+        xa, xb = x, self._h[:Tb]
+        parts = self._parts[:Tb]
+        mc = self.model_cfg
+        for li, L in enumerate(W["layers"]):
+            kc, vc = self.cache_k[li], self.cache_v[li]
+            if li == 0:
+                ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, W["tok_emb"], L["w_qkv_t"],
+                                   L["attn_norm"], pos, slot, self.cos, self.sin, self.H,
+                                   self.Hkv, self.hd, row_index=tok, x_out=xa,
+                                   prev_ids=self._ids)
+            else:
+                ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, xa, L["w_qkv_t"], L["attn_norm"], pos,
+                                   slot, self.cos, self.sin, self.H, self.Hkv, self.hd)
+            ops.decode_attention_wo(parts, q, kc, vc, bt, lens, qsl, self.scale,
+                                    self.block_size, L["wo"], mc.max_seq_len)
+            ops.linear_rows_parts(act, xa, parts, L["w_gate_up_t"], L["ffn_norm"], x_out=xb)
+            ops.linear_rows(xb, act, L["w_down_t"], mode=ops.LINEAR_ACCUMULATE)
+            xa, xb = xb, xa
+        ops.linear_rows(self._logits[:Rb], xa, W["lm_head_t"], W["final_norm"],
                         mode=ops.LINEAR_STORE, row_index=lidx)
 
     def _capture(self, s: _Shape, key, k: int) -> None:

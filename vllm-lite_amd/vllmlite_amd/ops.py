@@ -24,7 +24,7 @@ F32, BF16, F32_BF16KV, FP8_E4M3, F32_FP8KV = 0, 1, 2, 3, 4
 # VL_KV_*: a per-layer cache tensor [slots, Hkv, D] is token-major (the
 # reference's layout), [blocks, Hkv, block_size, D] head-major
 KV_TOKEN_MAJOR, KV_HEAD_MAJOR = 0, 1
-ABI_VERSION = 9  # vl_abi_version() of the library these signatures describe
+ABI_VERSION = 10  # vl_abi_version() of the library these signatures describe
 _c_void_p = ctypes.c_void_p
 _i32, _i64, _f32, _size = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
 
@@ -76,6 +76,11 @@ SIGNATURES = {
                                  _i32, _i32, _i32, _c_void_p]),
     "vl_resolve_tokens": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p]),
     "vl_copy_words": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p]),
+    "vl_linear_rows_parts": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i32, _c_void_p,
+                                    _c_void_p, _c_void_p, _f32, _i32, _i32, _i32, _c_void_p]),
+    "vl_decode_attention_wo": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
+                                      _i32, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32,
+                                      _f32, _i32, _i32, _i32, _c_void_p, _i32, _c_void_p]),
     "vl_decode_step_supported": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "vl_decode_step": (_i32, [_c_void_p, _c_void_p, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                               _c_void_p, _i64, _i32, _i32, _c_void_p, _c_void_p, _c_void_p,
@@ -609,6 +614,59 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor,
           "host_out must be a pinned contiguous int32 tensor")
     _check(lib().vl_argmax_rows(_ptr(logits), logits.stride(0), logits.shape[0], logits.shape[1],
                                 _ptr(out), _ptr(host_out), _stream()), "vl_argmax_rows")
+
+
+def linear_rows_parts(out: torch.Tensor, x: torch.Tensor, x_parts: torch.Tensor,
+                      weight: torch.Tensor, norm_weight: Optional[torch.Tensor] = None,
+                      eps: float = 1e-5, x_out: Optional[torch.Tensor] = None) -> None:
+    """out = SwiGLU(f(x + sum_p x_parts[:, p]) @ weight) with f the RMSNorm
+    times norm_weight when given; weight in 16-column tiles (gate tiles then up
+    tiles); x_parts [rows, P, k]; the summed rows also to x_out when given
+    (vl_linear_rows_parts)."""
+    rows, k = x.shape
+    n = out.shape[1]
+    _need(x_parts.dim() == 3 and x_parts.shape[0] >= rows and x_parts.shape[2] == k and
+          x_parts.is_contiguous(), "x_parts must be [rows, P, k] contiguous")
+    for t in (out, x, x_parts, weight) + tuple(t for t in (norm_weight, x_out) if t is not None):
+        _need(t.dtype == torch.float32 and t.stride(-1) == 1, "fp32 row-major tensors required")
+    _need(x_out is None or (x_out.is_contiguous() and x_out.shape[1] == k), "x_out shape")
+    tiles, _ = _weight_layout(weight, k, n, 2)
+    _need(tiles, "weight must be in 16-column tiles")
+    _check(lib().vl_linear_rows_parts(_ptr(out), out.stride(0), _ptr(x), x.stride(0),
+                                      _ptr(x_parts), x_parts.shape[1], _ptr(x_out), _ptr(weight),
+                                      _ptr(norm_weight), float(eps), out.shape[0], k, n,
+                                      _stream()), "vl_linear_rows_parts")
+
+
+def decode_attention_wo(parts: torch.Tensor, query: torch.Tensor, key_cache: torch.Tensor,
+                        value_cache: torch.Tensor, block_tables: torch.Tensor,
+                        seq_lens: torch.Tensor, query_start_loc: torch.Tensor, scale: float,
+                        block_size: int, wo: torch.Tensor, max_context_len: int) -> None:
+    """parts[s, g, :] = (decode attention output of sequence s, KV head g's
+    query heads) @ wo[those rows] (vl_decode_attention_wo); query [T, H, D]
+    fp32 (sequence s's token at row query_start_loc[s]), S = seq_lens.numel()
+    sequences, wo [H * D, d_model] row-major fp32, parts [S, Hkv, d_model]."""
+    _, H, D = query.shape
+    S = seq_lens.numel()
+    _need(query_start_loc.numel() == S + 1, "query_start_loc must have S + 1 entries")
+    layout, Hkv, bs, cd = kv_layout(key_cache)
+    _need(cd == D and bs in (0, block_size), "cache shape")
+    _need(query.dtype == torch.float32 and query.stride(-1) == 1 and query.stride(1) == D,
+          "query must be fp32 [S, H, D] rows")
+    _need(parts.dtype == torch.float32 and parts.is_contiguous() and
+          parts.shape[0] >= S and parts.shape[1] == Hkv and parts.shape[2] == wo.shape[1],
+          "parts must be [S, Hkv, d_model] fp32")
+    _need(wo.dtype == torch.float32 and wo.is_contiguous() and wo.shape[0] == H * D, "wo shape")
+    _need(block_tables.dtype == torch.int32 and block_tables.stride(-1) == 1, "int32 block tables")
+    cdt = _cache_dtype(key_cache, value_cache)
+    dtype = {BF16: F32_BF16KV, FP8_E4M3: F32_FP8KV}.get(cdt, F32)
+    _check(lib().vl_decode_attention_wo(_ptr(parts), _ptr(query), query.stride(0),
+                                        _ptr(key_cache), _ptr(value_cache), _ptr(block_tables),
+                                        block_tables.stride(0), _ptr(seq_lens),
+                                        _ptr(query_start_loc), S, H, Hkv, D, block_size,
+                                        float(scale), dtype, layout, int(max_context_len),
+                                        _ptr(wo), wo.shape[1], _stream()),
+           "vl_decode_attention_wo")
 
 
 def copy_words(dst: torch.Tensor, src: torch.Tensor) -> None:
