@@ -256,6 +256,23 @@ int vl_linear_rows(float* out, int64_t out_stride, const float* x, int64_t x_str
                    void* stream);
 
 /*
+ * vl_linear_rows in VL_LINEAR_STORE mode over tiled weights (the lm_head of
+ * vllmlite/model.py:119-120 on the gathered rows, runner.py:90) that also
+ * writes each row's argmax over its n logits to ids[rows], and to host_ids
+ * when it is not NULL (pinned host memory the host polls): greedy sampling,
+ * sampling.py:56-57, with numpy's rule (the lowest index among equal
+ * maxima, -0 equal to +0, the first NaN beating every number), as
+ * vl_argmax_rows computes it, in the same launch. scratch: 8 (rows + 1)
+ * bytes, 8-byte aligned, zero before the first call; every call leaves it
+ * zero again (calls that overlap on one scratch race). ids are written by
+ * the launch's last workgroup after every logit is stored.
+ */
+int vl_linear_rows_argmax(float* out, int64_t out_stride, const float* x, int64_t x_stride,
+                          const int32_t* row_index, const float* weight, const float* norm_weight,
+                          float eps, int rows, int k, int n, int32_t* ids, int32_t* host_ids,
+                          void* scratch, int64_t scratch_bytes, void* stream);
+
+/*
  * vl_linear_rows in VL_LINEAR_SWIGLU mode over tiled weights, with the input
  * rows x[r] + x_parts[r, 0] + ... + x_parts[r, num_parts - 1] (x_parts
  * [rows, num_parts, k] fp32, summed in that order; num_parts 1, 2, 4 or 8;

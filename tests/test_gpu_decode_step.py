@@ -4,7 +4,10 @@ the argmax of every row, vllmlite/sampling.py:56-57) against the same steps
 on this library's separate kernels, and end to end against the reference.
 
 Both runners see the same scheduled batches (the engine drives the first and
-the second is handed each batch too), so their caches evolve identically.
+the second is handed each batch too), and before each step the second's
+caches are set to the first's, so every comparison is of one step from the
+same cache (a narrow cache's rounding, once it differs, would otherwise carry
+into every later step).
 The projections are the same operations in the same order; the attention
 sums in another order, so every decode step's logits must agree within 1e-5
 of the row's largest logit (1e-3 with a bf16 or FP8 cache), and the ids equal the host argmax of the
@@ -42,8 +45,15 @@ class _Twin:
         self.vocab_size = self.a.vocab_size
         self.decode_steps = 0
 
+    def _same_caches(self):
+        torch.cuda.synchronize()
+        self.b.cache_k.copy_(self.a.cache_k)
+        self.b.cache_v.copy_(self.a.cache_v)
+        torch.cuda.synchronize()
+
     def execute(self, out):
         n0 = self.a.one_launch_steps
+        self._same_caches()
         la, rows = self.a.execute(out)
         lb, rows_b = self.b.execute(out)
         assert rows == rows_b
@@ -55,6 +65,7 @@ class _Twin:
 
     def execute_argmax(self, out):
         n0 = self.a.one_launch_steps
+        self._same_caches()
         ia, rows = self.a.execute_argmax(out)
         lb, _ = self.b.execute(out)
         if self.a.one_launch_steps > n0:

@@ -757,6 +757,28 @@ def test_decode_attention_wo_equals_attention_then_wo(cache, D, H, Hkv, dm, layo
         np.testing.assert_allclose(got[i].sum(0), total, rtol=0, atol=2e-5 * np.abs(total).max())
 
 
+@pytest.mark.parametrize("D,H,Hkv,dm", [(48, 8, 4, 384), (64, 8, 1, 512)])
+def test_decode_attention_wo_same_bits_for_any_column_split(D, H, Hkv, dm):
+    """A batch of few (sequence, KV head) items splits each item's wo columns
+    over 4 workgroups, a large batch keeps them in one; the column sums are
+    ((S0 + S1) + S2) + S3 over the same k quarters either way, so the first 8
+    sequences' parts are the same bits alone (32 items or 8) as within 72."""
+    o = ops()
+    rng = np.random.default_rng(D + dm)
+    seqs = [(1, int(c)) for c in rng.integers(1, 400, 72)]
+    b = make_batch(seqs, H, Hkv, D, 16, seed=dm)
+    kc, vc = caches(b, torch.float32)
+    wo = dev((rng.standard_normal((H * D, dm)) / np.sqrt(H * D)).astype(np.float32))
+    q, bt, lens, qsl = dev(b["q"]), dev(b["block_tables"]), dev(b["seq_lens"]), dev(b["qsl"])
+    big = torch.full((72, Hkv, dm), float("nan"), device="cuda")
+    o.decode_attention_wo(big, q, kc, vc, bt, lens, qsl, b["scale"], 16, wo, 400)
+    small = torch.full((8, Hkv, dm), float("nan"), device="cuda")
+    o.decode_attention_wo(small, q, kc, vc, bt[:8], lens[:8], qsl[:9], b["scale"], 16, wo, 400)
+    torch.cuda.synchronize()
+    assert torch.isfinite(big).all()
+    assert torch.equal(big[:8], small)
+
+
 def test_decode_attention_wo_refuses_other_batches():
     o = ops()
     b = make_batch([(1, 40), (1, 3000)], 8, 4, 48, 16, seed=3)

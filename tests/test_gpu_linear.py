@@ -364,3 +364,86 @@ def test_linear_rows_parts_equals_summed_input(rows, k, n, P, norm):
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     assert np.array_equal(x_out.cpu().numpy(), summed)
+
+
+def _argmax_call(o, x, wt, g, rows, n, scratch, row_index=None, host=None):
+    out = torch.full((rows, n), float("nan"), device="cuda")
+    ids = torch.full((rows,), -7, dtype=torch.int32, device="cuda")
+    o.linear_rows_argmax(out, x, wt, g, ids, scratch, host_ids=host, row_index=row_index)
+    return out, ids
+
+
+@pytest.mark.parametrize("rows", [1, 5, 16, 17, 48, 300])
+@pytest.mark.parametrize("k,n", [(384, 261), (1024, 384), (64, 40)])
+def test_linear_rows_argmax_is_store_then_argmax(rows, k, n):
+    """vl_linear_rows_argmax: the logits of vl_linear_rows (same bits) and each
+    row's argmax over them from the same launch, exactly np.argmax's, in the
+    device ids and the pinned host copy; the scratch is zero again after every
+    call, so calls in a row need no clearing."""
+    o = _ops()
+    rng = np.random.default_rng(rows + k + n)
+    scratch = torch.zeros(rows + 1, dtype=torch.int64, device="cuda")
+    host = torch.full((rows,), -1, dtype=torch.int32, pin_memory=True)
+    g = torch.from_numpy((1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)).cuda()
+    for it in range(3):
+        src = torch.from_numpy(rng.standard_normal((rows + 9, k)).astype(np.float32)).cuda()
+        w = torch.from_numpy((0.05 * rng.standard_normal((k, n))).astype(np.float32)).cuda()
+        lidx = torch.from_numpy(rng.integers(0, rows + 9, rows).astype(np.int32)).cuda()
+        want = torch.full((rows, n), float("nan"), device="cuda")
+        o.linear_rows(want, src, w, g, mode=o.LINEAR_STORE, row_index=lidx)
+        out, ids = _argmax_call(o, src, o.tile16(w, 1), g, rows, n, scratch, lidx, host)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), it
+        want_ids = np.argmax(out.cpu().numpy(), axis=1)
+        assert np.array_equal(ids.cpu().numpy(), want_ids), it
+        assert np.array_equal(host.numpy(), want_ids), it
+        assert int(scratch.abs().sum()) == 0, it
+
+
+def test_linear_rows_argmax_ties_nan_and_infinities():
+    """numpy's rule on crafted rows: x = e_0 (no norm) and a weight that is
+    zero but for row 0 make logit c = w[0, c]. Equal maxima go to the lowest
+    column, a NaN beats +inf (the first NaN wins), +inf beats every number,
+    and a row of -inf gives column 0; the 100 columns span 7 tiles (7
+    workgroups fold into each row's key)."""
+    o = _ops()
+    n, k = 100, 64
+    patterns = [
+        ({3: 5.0, 40: 5.0, 90: 5.0}, 3),            # a tie across tiles
+        ({70: 2.0, 20: 2.0, 21: 2.0}, 20),
+        ({10: np.inf, 80: np.nan, 95: np.nan}, 80),  # the first NaN
+        ({55: np.inf, 60: 1e38, 99: np.inf}, 55),    # the first +inf
+        ("neg_inf", 0),                               # every logit -inf
+        ({0: -1.0, 99: -0.5}, 99),                   # the others -3
+    ]
+    scratch = torch.zeros(2, dtype=torch.int64, device="cuda")
+    x = np.zeros((1, k), np.float32)
+    x[0, 0] = 1.0
+    for spec, want in patterns:
+        w = np.zeros((k, n), np.float32)
+        if spec == "neg_inf":
+            w[0] = -np.inf
+        else:
+            w[0] = -3.0
+            for c, v in spec.items():
+                w[0, c] = v
+        assert int(np.argmax(w[0])) == want  # the rule the test states is numpy's
+        out, ids = _argmax_call(o, torch.from_numpy(x).cuda(),
+                                o.tile16(torch.from_numpy(w).cuda(), 1), None, 1, n, scratch)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy()[0], w[0])  # logit c = w[0, c]
+        assert int(ids.cpu()[0]) == want, spec
+        assert int(scratch.abs().sum()) == 0
+
+
+def test_linear_rows_argmax_bad_arguments_raise():
+    o = _ops()
+    x = torch.zeros((4, 64), device="cuda")
+    wt = o.tile16(torch.zeros((64, 40), device="cuda"), 1)
+    out = torch.zeros((4, 40), device="cuda")
+    ids = torch.zeros(4, dtype=torch.int32, device="cuda")
+    with pytest.raises(RuntimeError):  # scratch too small (needs rows + 1 words)
+        o.linear_rows_argmax(out, x, wt, None, ids, torch.zeros(4, dtype=torch.int64, device="cuda"))
+    with pytest.raises(ValueError):  # row-major weight (refused before the call)
+        o.linear_rows_argmax(out, x, torch.zeros((64, 40), device="cuda"), None, ids,
+                             torch.zeros(5, dtype=torch.int64, device="cuda"))

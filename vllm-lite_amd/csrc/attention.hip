@@ -1929,7 +1929,7 @@ __global__ void __launch_bounds__(64 * NW) attend_short_decode_kernel(
     const TKV* vc, const int32_t* __restrict__ bt, int bt_stride,
     const int32_t* __restrict__ seq_lens, const int32_t* __restrict__ qsl, int Hkv, int bs_log2,
     int kv_hm, float scale_log2, const float* __restrict__ wo, int wo_n,
-    float* __restrict__ parts) {
+    float* __restrict__ parts, int n_items, int ncg) {
   using Lds = ShortLds<TKV, D, REP, NW>;
   constexpr int VE = Lds::kVE;
   constexpr int kThreads = 64 * NW;
@@ -1938,7 +1938,18 @@ __global__ void __launch_bounds__(64 * NW) attend_short_decode_kernel(
   constexpr int G = 64 / NC;               // PV key groups
   constexpr int KPL = (64 + G - 1) / G;    // keys per lane in the PV product
   __shared__ Lds s;
-  const int i = blockIdx.x / Hkv, g = blockIdx.x - (blockIdx.x / Hkv) * Hkv;
+  // item (sequence i, KV head g); with wo split over ncg column groups, the
+  // ncg workgroups of an item are b = 8 (ncg (item / 8) + cg) + item % 8, so
+  // they run on one XCD (workgroups go to the XCDs round-robin) and its L2
+  // serves the three that read the item's K/V after the first
+  int item = blockIdx.x, cg = 0;
+  if (ncg > 1) {
+    const int r = blockIdx.x >> 3;
+    item = (r / ncg) * 8 + (blockIdx.x & 7);
+    cg = r - (r / ncg) * ncg;
+  }
+  if (item >= n_items) return;  // the grid's rounding to whole groups of 8 items
+  const int i = item / Hkv, g = item - (item / Hkv) * Hkv;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   // the first kThreads entries of the sequence's block-table row (it has
   // bt_stride of them) are loaded with its length, not after it
@@ -2044,14 +2055,28 @@ __global__ void __launch_bounds__(64 * NW) attend_short_decode_kernel(
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
-  // with wo: this thread's column of the workgroup's wo rows, in flight
-  // during the merge below
+  // with wo: the weights of this thread's products, in flight during the
+  // merge below. Column sums are ((S0 + S1) + S2) + S3 over the quarters k =
+  // KQ q .. KQ (q + 1) - 1 of the REP D rows, each S_q one chain in k order,
+  // however the columns are split: with one column group, thread t < wo_n
+  // takes column t whole; with ncg groups of cols = wo_n / ncg, thread t <
+  // 4 cols takes quarter t / cols of column cg cols + t % cols.
+  constexpr int KQ = REP * D / 4;
+  static_assert(REP * D % 4 == 0, "whole quarters");
   float wcol[REP * D];
-  const bool wo_col = wo != nullptr && tid < wo_n;
+  const int cols = wo_n / ncg;
+  const int wq = ncg > 1 ? tid / max(cols, 1) : 0;  // the thread's quarter (split columns)
+  const int wc_col = ncg > 1 ? cg * cols + (tid - wq * cols) : tid;
+  const bool wo_col = wo != nullptr && (ncg > 1 ? tid < 4 * cols : tid < wo_n);
   if (wo_col) {
-    const float* wc = wo + (int64_t)g * REP * D * wo_n + tid;
+    const float* wc = wo + (int64_t)g * REP * D * wo_n + wc_col;
+    if (ncg > 1) {
 #pragma unroll
-    for (int k = 0; k < REP * D; ++k) wcol[k] = wc[(int64_t)k * wo_n];
+      for (int k = 0; k < KQ; ++k) wcol[k] = wc[(int64_t)(wq * KQ + k) * wo_n];
+    } else {
+#pragma unroll
+      for (int k = 0; k < REP * D; ++k) wcol[k] = wc[(int64_t)k * wo_n];
+    }
   }
 #pragma unroll
   for (int h = 0; h < REP; ++h) lsum[h] = wave_sum_dpp(lsum[h]);
@@ -2105,12 +2130,28 @@ __global__ void __launch_bounds__(64 * NW) attend_short_decode_kernel(
   }
   if (wo) {
     __syncthreads();
-    if (wo_col) {
-      // four independent chains (k = 4 u + c), added in order at the end
-      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float* prow = parts + ((int64_t)i * Hkv + g) * wo_n;
+    if (ncg == 1) {
+      if (wo_col) {
+        float sq[4] = {0.f, 0.f, 0.f, 0.f};  // four independent chains
 #pragma unroll
-      for (int k = 0; k < REP * D; ++k) acc[k & 3] = __builtin_fmaf(s.o[k], wcol[k], acc[k & 3]);
-      parts[((int64_t)i * Hkv + g) * wo_n + tid] = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+        for (int k = 0; k < REP * D; ++k)
+          sq[k / KQ] = __builtin_fmaf(s.o[k], wcol[k], sq[k / KQ]);
+        prow[tid] = ((sq[0] + sq[1]) + sq[2]) + sq[3];
+      }
+    } else {
+      // the quarters meet in LDS (the PV sums' rows, free since the merge)
+      float* sq = reinterpret_cast<float*>(s.red);
+      if (wo_col) {
+        float a = 0.f;
+#pragma unroll
+        for (int k = 0; k < KQ; ++k) a = __builtin_fmaf(s.o[wq * KQ + k], wcol[k], a);
+        sq[tid] = a;  // = sq[wq cols + column]
+      }
+      __syncthreads();
+      if (tid < cols)
+        prow[cg * cols + tid] =
+            ((sq[tid] + sq[cols + tid]) + sq[2 * cols + tid]) + sq[3 * cols + tid];
     }
   }
 }
@@ -2440,18 +2481,30 @@ inline bool short_decode(const Args& a, int max_q, int max_ctx) {
          (rep == 1 || rep == 2 || rep == 4 || rep == 8) && (int64_t)a.S * a.Hkv <= (1 << 30);
 }
 
+// Column groups of the fused output projection: 4 where the items (sequence,
+// KV head) are few enough that 4 workgroups each still fit one round of the
+// chip and a group's quarters fit one thread each, else 1. A workgroup's wo
+// slice (REP D rows of wo_n floats, 147 KB at TinyLlama's 2 x 48 x 384) then
+// streams through 4 compute units' L1s instead of one.
+inline int wo_column_groups(int items, int wo_n) {
+  if (wo_n % 4 == 0 && wo_n <= 64 * kShortWaves && (int64_t)items * 4 <= vl_num_cus()) return 4;
+  return 1;
+}
+
 template <typename T, typename TKV, int D>
 int launch_short_decode_d(const Args& a, float sl2, hipStream_t st, const float* wo = nullptr,
                           int wo_n = 0, float* parts = nullptr) {
   const int rep = a.H / a.Hkv;
-  const int grid = a.S * a.Hkv;
-  if (grid == 0) return VL_OK;
+  const int items = a.S * a.Hkv;
+  if (items == 0) return VL_OK;
+  const int ncg = wo ? wo_column_groups(items, wo_n) : 1;
+  const int grid = ncg > 1 ? (items + 7) / 8 * 8 * ncg : items;
   const int bs_log2 = __builtin_ctz((unsigned)a.bs);
 #define VL_SHORT(REP)                                                                        \
   attend_short_decode_kernel<T, TKV, D, REP, kShortWaves><<<grid, 64 * kShortWaves, 0, st>>>( \
       (T*)a.out, (const T*)a.query, a.q_stride, (const TKV*)a.kc, (const TKV*)a.vc, a.bt,    \
       a.bt_stride, a.seq_lens, a.qsl, a.Hkv, bs_log2, a.kv_layout == VL_KV_HEAD_MAJOR ? 1 : 0, sl2, \
-      wo, wo_n, parts)
+      wo, wo_n, parts, items, ncg)
   switch (rep) {
     case 1: VL_SHORT(1); break;
     case 2: VL_SHORT(2); break;

@@ -71,6 +71,29 @@ struct RopeCache {
   int kv_dtype;  // VL_DTYPE_F32, or VL_DTYPE_BF16 / VL_DTYPE_FP8_E4M3 (rounded to nearest even)
 };
 
+// Where MODE 4 puts each row's argmax (vl_linear_rows_argmax). Every
+// workgroup folds its tiles' columns into keys[row] with one 64-bit atomic
+// max per row and then arrives at count; the last to arrive turns the keys
+// into ids and clears keys and count for the next launch.
+struct ArgmaxOut {
+  unsigned long long* keys;  // [rows], zero before and after a launch
+  unsigned* count;           // zero before and after a launch
+  int32_t* ids;
+  int32_t* host_ids;  // a second copy (pinned host memory), or null
+};
+
+// A key whose unsigned order is numpy's argmax order: the high word orders
+// the values (every NaN above +inf, -0 as +0), the low word prefers the
+// lower column among equal values.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int col) {
+  const unsigned b = __float_as_uint(v);
+  const unsigned o = v != v ? 0xFFFFFFFFu
+                     : v == 0.f ? 0x80000000u
+                     : (b & 0x80000000u) ? ~b
+                                         : (b | 0x80000000u);
+  return ((unsigned long long)o << 32) | (0xFFFFFFFFu - (unsigned)col);
+}
+
 __device__ __forceinline__ void store_cache(void* cache, int64_t i, float v, int dtype) {
   if (dtype == VL_DTYPE_BF16)
     static_cast<uint16_t*>(cache)[i] = f32_to_bf16(v);
@@ -80,7 +103,7 @@ __device__ __forceinline__ void store_cache(void* cache, int64_t i, float v, int
     static_cast<float*>(cache)[i] = v;
 }
 
-// MODE 0: out = f(x) @ w; 1: out += f(x) @ w; 2: out = silu(f(x) @ w[:, :n]) *
+// MODE 0: out = f(x) @ w (4: and each row's argmax to am); 1: out += f(x) @ w; 2: out = silu(f(x) @ w[:, :n]) *
 // (f(x) @ w[:, up_off : up_off + n]); 3: f(x) @ w is a [q | k | v] row: q and k
 // rotated by RoPE, q to rc.q_out, k and v to the caches at the row's slot.
 // f(x) = x, or with NORM the RMSNorm of x times norm_w, applied as
@@ -105,7 +128,8 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
     const float* __restrict__ w, int64_t ldw, int64_t up_off, const float* __restrict__ norm_w,
     float eps, int M, int K, int N, const RopeCache rc, const int32_t* __restrict__ row_index,
     const int32_t* __restrict__ prev_ids, int64_t num_prev, float* __restrict__ x_out,
-    int nsub, int rt, const float* __restrict__ x_parts = nullptr) {
+    int nsub, int rt, const float* __restrict__ x_parts = nullptr,
+    const ArgmaxOut am = ArgmaxOut{}) {
   constexpr int kSlices = MODE == 2 ? 2 : 1;
   constexpr int kGroups = KMAX / (16 * kLinWaves);  // 16-k groups per wavefront at K = KMAX
   static_assert(kGroups >= 1 && KMAX % (16 * kLinWaves) == 0, "whole 16-k groups");
@@ -300,6 +324,7 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
     __syncthreads();
 
     const int r = er, c = ec;
+    unsigned long long e_key = 0;  // MODE 4: this thread's (value, column) key
     if (er < M && e_col) {
       // the wavefronts' partial sums in wavefront order
       auto total = [&](int s, int e) {
@@ -322,8 +347,9 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
       float v[kSlices];
 #pragma unroll
       for (int s = 0; s < kSlices; ++s) v[s] = NORM ? total(s, tid) / rms : total(s, tid);
-      if constexpr (MODE == 0) {
+      if constexpr (MODE == 0 || MODE == 4) {
         out_t[(int64_t)r * ldo + c0 + c] = v[0];
+        if constexpr (MODE == 4) e_key = argmax_key(v[0], c0 + c);
       } else if constexpr (MODE == 1) {
         out_t[(int64_t)r * ldo + c0 + c] = e_resid + v[0];
       } else if constexpr (MODE == 2) {
@@ -350,6 +376,40 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
           store_cache(rc.vc, rc.geom.at(slot, vcol / rc.hd) + vcol % rc.hd, v[0], rc.kv_dtype);
         }
       }
+    }
+    if constexpr (MODE == 4) {
+      // the largest key of each row's 16 threads (lanes 16 u .. 16 u + 15 of
+      // a wavefront), one atomic max per row; waves past the tile's 16 rows
+      // hold none
+      if (tid < kRowsMax * kCols) {
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) {
+          const unsigned long long other = __shfl_xor(e_key, o, 64);
+          e_key = other > e_key ? other : e_key;
+        }
+        if (ec == 0 && e_key != 0)
+          __hip_atomic_fetch_max(am.keys + r0 + er, e_key, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  if constexpr (MODE == 4) {
+    __shared__ int last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's atomics have completed
+    __syncthreads();
+    if (tid == 0)
+      last = __hip_atomic_fetch_add(am.count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             gridDim.x * gridDim.y - 1;
+    __syncthreads();
+    if (last) {  // every workgroup's maxima are in: the ids, and the keys cleared
+      for (int r = tid; r < M_all; r += 64 * kLinWaves) {
+        const unsigned long long k =
+            __hip_atomic_exchange(am.keys + r, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int32_t id = (int32_t)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull));
+        am.ids[r] = id;
+        if (am.host_ids) am.host_ids[r] = id;
+      }
+      if (tid == 0) __hip_atomic_store(am.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -386,7 +446,7 @@ int launch(float* out, int64_t ldo, const float* x, int64_t ldx, const float* w,
            bool tiles, const float* norm_w, float eps, int M, int K, int N, hipStream_t st,
            const int32_t* row_index, const RopeCache& rc = RopeCache{}, float* x_out = nullptr,
            const int32_t* prev_ids = nullptr, int64_t num_prev = 0,
-           const float* x_parts = nullptr) {
+           const float* x_parts = nullptr, const ArgmaxOut& am = ArgmaxOut{}) {
   const int ntile = (N + kCols - 1) / kCols;
   const int rt = row_tile(M, N);
   const int row_tiles = (M + rt - 1) / rt;
@@ -396,8 +456,8 @@ int launch(float* out, int64_t ldo, const float* x, int64_t ldx, const float* w,
     const int64_t up_off = MODE == 2 ? (int64_t)ntile * K * kCols : 0;
     linear_rows_kernel<MODE, NORM, KMAX, true, NP><<<grid, 64 * kLinWaves, 0, st>>>(
         out, ldo, x, ldx, w, 0, up_off, norm_w, eps, M, K, N, rc, row_index, prev_ids, num_prev,
-        x_out, nsub, rt, x_parts);
-  } else if constexpr (NP == 0) {
+        x_out, nsub, rt, x_parts, am);
+  } else if constexpr (NP == 0 && MODE != 4) {
     const int64_t up_off = MODE == 2 ? N : 0;
     linear_rows_kernel<MODE, NORM, KMAX, false><<<grid, 64 * kLinWaves, 0, st>>>(
         out, ldo, x, ldx, w, ldw, up_off, norm_w, eps, M, K, N, rc, row_index, prev_ids,
@@ -541,4 +601,37 @@ extern "C" int vl_linear_rows_parts(float* out, int64_t out_stride, const float*
     case 4: return launch_parts<4>(out, out_stride, x, x_stride, x_parts, x_out, weight, norm_weight, eps, rows, k, n, st);
     default: return launch_parts<8>(out, out_stride, x, x_stride, x_parts, x_out, weight, norm_weight, eps, rows, k, n, st);
   }
+}
+
+extern "C" int vl_linear_rows_argmax(float* out, int64_t out_stride, const float* x,
+                                     int64_t x_stride, const int32_t* row_index,
+                                     const float* weight, const float* norm_weight, float eps,
+                                     int rows, int k, int n, int32_t* ids, int32_t* host_ids,
+                                     void* scratch, int64_t scratch_bytes, void* stream) {
+  VL_CHECK_ARG(rows >= 0 && rows <= kRowsLimit, "rows must be in 0..%d", kRowsLimit);
+  VL_CHECK_ARG(k > 0 && k % 16 == 0 && k <= 1024, "k must be a multiple of 16, at most 1024");
+  VL_CHECK_ARG(n > 0, "n must be positive");
+  if (rows == 0) return VL_OK;
+  VL_CHECK_ARG(out && x && weight && ids && scratch, "null pointer");
+  VL_CHECK_ARG((((uintptr_t)x) & 15) == 0 && x_stride % 4 == 0 && x_stride >= k,
+               "x must be 16-byte aligned with a row stride that is a multiple of 4");
+  VL_CHECK_ARG(out_stride >= n, "row stride too small");
+  VL_CHECK_ARG((((uintptr_t)weight) & 15) == 0, "tiled weight must be 16-byte aligned");
+  VL_CHECK_ARG((((uintptr_t)norm_weight) & 15) == 0, "norm weight must be 16-byte aligned");
+  VL_CHECK_ARG((((uintptr_t)scratch) & 7) == 0 && scratch_bytes >= 8 * ((int64_t)rows + 1),
+               "scratch must be 8-byte aligned and hold rows + 1 8-byte words");
+  ArgmaxOut am;
+  am.keys = static_cast<unsigned long long*>(scratch);
+  am.count = reinterpret_cast<unsigned*>(am.keys + rows);
+  am.ids = ids;
+  am.host_ids = host_ids;
+  hipStream_t st = (hipStream_t)stream;
+  const bool nrm = norm_weight != nullptr;
+#define VL_ARGMAX(NORM, KM)                                                                     \
+  launch<4, NORM, KM>(out, out_stride, x, x_stride, weight, 0, true, norm_weight, eps, rows, k, n, \
+                      st, row_index, RopeCache{}, nullptr, nullptr, 0, nullptr, am)
+  if (k <= 384) return nrm ? VL_ARGMAX(true, 384) : VL_ARGMAX(false, 384);
+  if (k <= 512) return nrm ? VL_ARGMAX(true, 512) : VL_ARGMAX(false, 512);
+  return nrm ? VL_ARGMAX(true, 1024) : VL_ARGMAX(false, 1024);
+#undef VL_ARGMAX
 }

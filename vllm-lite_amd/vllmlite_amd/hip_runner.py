@@ -511,6 +511,8 @@ class HipRunner(ModelRunner):
         self._logits_host = torch.zeros(cap, mc.vocab_size, dtype=torch.float32, pin_memory=True)
         self._logits_host_np = self._logits_host.numpy()
         self._ids = torch.zeros(cap, dtype=torch.int32, device=dev)
+        # the lm_head launch's argmax keys and arrival count (left zero by each launch)
+        self._am_scratch = torch.zeros(cap + 1, dtype=torch.int64, device=dev)
         if old_ids is not None:  # a launched step's ids, still to be read by the next
             self._ids[:old_ids.numel()].copy_(old_ids)
         self._ids_hosts = [torch.zeros(cap, dtype=torch.int32, pin_memory=True) for _ in range(2)]
@@ -555,10 +557,12 @@ class HipRunner(ModelRunner):
         # read from the pinned record by a kernel: as a graph's memcpy node
         # this copy cost ~12 us more per step
         ops.copy_words(self._meta[:n], self._meta_hosts[k][:n])
-        self._forward_body(s)
-        ops.argmax_rows(self._logits[:s.Rb], self._ids[:s.Rb], host_out=self._ids_hosts[k])
+        if not self._forward_body(s, self._ids_hosts[k]):
+            ops.argmax_rows(self._logits[:s.Rb], self._ids[:s.Rb], host_out=self._ids_hosts[k])
 
-    def _forward_body(self, s: _Shape) -> None:
+    def _forward_body(self, s: _Shape, ids_host: torch.Tensor) -> bool:
+        """The forward of staged shape s into self._logits[:Rb]; True when its
+        lm_head launch also wrote the rows' argmax (to self._ids and ids_host)."""
         mc = self.model_cfg
         Tb, Sb, Rb = s.Tb, s.Sb, s.Rb
         meta = self._meta
@@ -574,8 +578,8 @@ class HipRunner(ModelRunner):
         gu, act = self._gu[:Tb], self._act[:Tb]
         W = self.w
         if Tb <= min(self.fused_rows_max, ops.LINEAR_ROWS_MAX) and self._fused_rows:
-            self._forward_rows(s, x, q, attn, act, tok, pos, slot, lidx, qsl, lens, bt)
-            return
+            self._forward_rows(s, x, q, attn, act, tok, pos, slot, lidx, qsl, lens, bt, ids_host)
+            return True
         # ids the previous step chose on the device (negative placeholders)
         ops.resolve_tokens(tok, self._ids)
         torch.index_select(W["tok_emb"], 0, tok, out=x)
@@ -598,6 +602,7 @@ class HipRunner(ModelRunner):
         hsel = self._hsel[:Rb]
         torch.index_select(h, 0, lidx, out=hsel)
         torch.mm(hsel, W["lm_head"], out=self._logits[:Rb])
+        return False
 
     def _plan(self, s: _Shape, q, lens, qsl) -> None:
         """The attention plan of the step, shared by its layers (a decode-only
@@ -614,8 +619,16 @@ class HipRunner(ModelRunner):
             ops.paged_attention_run(attn, q, kc, vc, bt, lens, qsl, self.scale, self.block_size,
                                     self._ws)
 
+    def _lm_head(self, s: _Shape, x, lidx, ids_host) -> None:
+        """The final RMSNorm and lm_head of the logits rows x[lidx] with their
+        argmax (vl_linear_rows_argmax: ids from the same launch)."""
+        W, Rb = self.w, s.Rb
+        ops.linear_rows_argmax(self._logits[:Rb], x, W["lm_head_t"], W["final_norm"],
+                               self._ids[:Rb], self._am_scratch, host_ids=ids_host,
+                               row_index=lidx)
+
     def _forward_rows(self, s: _Shape, x, q, attn, act, tok, pos, slot, lidx, qsl, lens,
-                      bt) -> None:
+                      bt, ids_host) -> None:
         """The forward by the fused projection kernels (every decode step, and
         prefill steps up to fused_rows_max rows): each projection is one
         launch with its RMSNorm, residual add, SwiGLU or RoPE + K/V scatter
@@ -626,7 +639,7 @@ class HipRunner(ModelRunner):
         prologue: four launches per layer."""
         W, Tb, Rb = self.w, s.Tb, s.Rb
         if s.decode and self._fused_wo:
-            self._forward_decode_wo(s, x, q, act, tok, pos, slot, lidx, qsl, lens, bt)
+            self._forward_decode_wo(s, x, q, act, tok, pos, slot, lidx, qsl, lens, bt, ids_host)
             return
         self._plan(s, q, lens, qsl)
         for li, L in enumerate(W["layers"]):
@@ -645,11 +658,10 @@ class HipRunner(ModelRunner):
             ops.linear_rows(x, attn.view(Tb, -1), L["wo_t"], mode=ops.LINEAR_ACCUMULATE)
             ops.linear_rows(act, x, L["w_gate_up_t"], L["ffn_norm"], mode=ops.LINEAR_SWIGLU)
             ops.linear_rows(x, act, L["w_down_t"], mode=ops.LINEAR_ACCUMULATE)
-        ops.linear_rows(self._logits[:Rb], x, W["lm_head_t"], W["final_norm"],
-                        mode=ops.LINEAR_STORE, row_index=lidx)
+        self._lm_head(s, x, lidx, ids_host)
 
     def _forward_decode_wo(self, s: _Shape, x, q, act, tok, pos, slot, lidx, qsl, lens,
-                           bt) -> None:
+                           bt, ids_host) -> None:
         """A decode step in four launches per layer: QKV (+ RoPE + cache);
         attention with wo (vl_decode_attention_wo: parts[s, g] = the outputs
         of KV head g's query heads @ their rows of wo); gate|up over x + the
@@ -675,8 +687,7 @@ class HipRunner(ModelRunner):
             ops.linear_rows_parts(act, xa, parts, L["w_gate_up_t"], L["ffn_norm"], x_out=xb)
             ops.linear_rows(xb, act, L["w_down_t"], mode=ops.LINEAR_ACCUMULATE)
             xa, xb = xb, xa
-        ops.linear_rows(self._logits[:Rb], xa, W["lm_head_t"], W["final_norm"],
-                        mode=ops.LINEAR_STORE, row_index=lidx)
+        self._lm_head(s, xa, lidx, ids_host)
 
     def _capture(self, s: _Shape, key, k: int) -> None:
         # A garbage collection inside the capture could free device or pinned

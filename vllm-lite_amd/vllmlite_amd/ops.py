@@ -24,7 +24,7 @@ F32, BF16, F32_BF16KV, FP8_E4M3, F32_FP8KV = 0, 1, 2, 3, 4
 # VL_KV_*: a per-layer cache tensor [slots, Hkv, D] is token-major (the
 # reference's layout), [blocks, Hkv, block_size, D] head-major
 KV_TOKEN_MAJOR, KV_HEAD_MAJOR = 0, 1
-ABI_VERSION = 10  # vl_abi_version() of the library these signatures describe
+ABI_VERSION = 11  # vl_abi_version() of the library these signatures describe
 _c_void_p = ctypes.c_void_p
 _i32, _i64, _f32, _size = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
 
@@ -76,6 +76,9 @@ SIGNATURES = {
                                  _i32, _i32, _i32, _c_void_p]),
     "vl_resolve_tokens": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p]),
     "vl_copy_words": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p]),
+    "vl_linear_rows_argmax": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p,
+                                     _c_void_p, _f32, _i32, _i32, _i32, _c_void_p, _c_void_p,
+                                     _c_void_p, _i64, _c_void_p]),
     "vl_linear_rows_parts": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i32, _c_void_p,
                                     _c_void_p, _c_void_p, _f32, _i32, _i32, _i32, _c_void_p]),
     "vl_decode_attention_wo": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
@@ -614,6 +617,39 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor,
           "host_out must be a pinned contiguous int32 tensor")
     _check(lib().vl_argmax_rows(_ptr(logits), logits.stride(0), logits.shape[0], logits.shape[1],
                                 _ptr(out), _ptr(host_out), _stream()), "vl_argmax_rows")
+
+
+def linear_rows_argmax(out: torch.Tensor, x: torch.Tensor, weight: torch.Tensor,
+                       norm_weight: Optional[torch.Tensor], ids: torch.Tensor,
+                       scratch: torch.Tensor, host_ids: Optional[torch.Tensor] = None,
+                       row_index: Optional[torch.Tensor] = None, eps: float = 1e-5) -> None:
+    """out = f(x[row_index]) @ weight (tiled; f the RMSNorm times norm_weight
+    when given) and ids[r] = argmax of out row r (numpy's rule), also into
+    host_ids (pinned) when given, from one launch. scratch: int64 [>= rows +
+    1], zero before the first call and left zero by every call (see
+    vl_linear_rows_argmax)."""
+    k = x.shape[1]
+    rows, n = out.shape
+    _need(row_index is None or (row_index.dtype == torch.int32 and row_index.numel() >= rows),
+          "row_index must hold int32 row numbers")
+    for t in (out, x, weight) + ((norm_weight,) if norm_weight is not None else ()):
+        _need(t.dtype == torch.float32 and t.stride(-1) == 1, "fp32 row-major tensors required")
+    _need(row_index is not None or x.shape[0] >= rows, "x has too few rows")
+    tiles, _ = _weight_layout(weight, k, n, 1)
+    _need(tiles, "weight must be in 16-column tiles")
+    _need(norm_weight is None or norm_weight.numel() == k, "norm weight shape mismatch")
+    _dev_i32(ids, "ids")
+    _need(ids.numel() >= rows, "ids length")
+    _need(scratch.dtype == torch.int64 and scratch.is_cuda and scratch.is_contiguous(),
+          "scratch must be a contiguous int64 device tensor")
+    _need(host_ids is None or (host_ids.dtype == torch.int32 and host_ids.is_pinned() and
+                               host_ids.is_contiguous() and host_ids.numel() >= rows),
+          "host_ids must be a pinned contiguous int32 tensor")
+    _check(lib().vl_linear_rows_argmax(_ptr(out), out.stride(0), _ptr(x), x.stride(0),
+                                       _ptr(row_index), _ptr(weight), _ptr(norm_weight),
+                                       float(eps), rows, k, n, _ptr(ids), _ptr(host_ids),
+                                       _ptr(scratch), scratch.numel() * 8, _stream()),
+           "vl_linear_rows_argmax")
 
 
 def linear_rows_parts(out: torch.Tensor, x: torch.Tensor, x_parts: torch.Tensor,
