@@ -505,6 +505,10 @@ class _CowCounter:
         return self.runner.execute_argmax(out)
 
 
+def mc_layers(cfg):
+    return cfg.model.n_layers
+
+
 def e2e_leg(name="mixed", repeat=3, cpu=True):
     """Output tok/s of a mix through HipRunner (one warm-up pass, then best of
     `repeat`; the runner and its captured graphs persist across passes, each
@@ -538,10 +542,14 @@ def e2e_leg(name="mixed", repeat=3, cpu=True):
                  "latency-bound far above it)",
         "floor_us_per_step": fl["floor_us_per_step"], "bytes_per_step": fl["bytes_per_step"],
         "frac": round(fl["floor_us_per_step"] / (wall / steps * 1e6), 4),
-        "device_launches_per_decode_step": 6 * 5 + 4,
-        "launches_are": "per layer QKV+RoPE+scatter, attention, wo+residual, "
-                        "norm+gate|up+SwiGLU, down+residual; then lm_head, the argmax, the "
-                        "placeholder resolve and the step record's host-to-device copy"}
+        "device_launches_per_decode_step": (mc_layers(cfg) * (4 if runner._fused_wo else 5)
+                                            + 2),
+        "launches_are": ("per layer QKV+RoPE+scatter (layer 0 also gathers the embeddings and "
+                         "resolves the previous step's ids), attention"
+                         + (" with wo (one partial row per KV head), residual+norm+gate|up+SwiGLU"
+                            if runner._fused_wo else ", wo+residual, norm+gate|up+SwiGLU")
+                         + ", down+residual; then lm_head with each row's argmax, and the step "
+                           "record's copy from pinned host memory")}
     if fork:
         out["cow_pairs"] = pairs
     fixture, key = (("cfg0_streams.json", None) if name.startswith("mixed") else

@@ -52,10 +52,7 @@ constexpr int kHdrInts = 64;  // [0] bandwidth-kernel items [1] generic items [2
 constexpr int kPlanThreads = 256;
 constexpr int kMaxHeadDim = 256;
 constexpr int kSplitMaxQ = 16;  // only sequences with <= this many queries split their context
-#ifndef VL_PART0
-#define VL_PART0 64
-#endif
-constexpr int kPart0 = VL_PART0;  // first partition length tried by the planner
+constexpr int kPart0 = 64;  // first partition length tried by the planner
 constexpr float kLog2e = 1.4426950408889634f;
 
 // bandwidth-kernel shape
@@ -63,25 +60,15 @@ constexpr int kFD = 128;   // head_dim
 constexpr int kFRep = 4;   // query heads per KV head
 constexpr int kFBs = 16;   // block size
 constexpr int kFChunk = 16;  // blocks per softmax chunk (256 tokens)
-#ifndef VL_BK
-#define VL_BK 4
-#endif
-#ifndef VL_BV
-#define VL_BV 2
-#endif
-constexpr int kBK = VL_BK;  // blocks per K load burst (decode kernel)
-constexpr int kBV = VL_BV;  // blocks per V load burst (decode kernel)
+constexpr int kBK = 4;  // blocks per K load burst (decode kernel)
+constexpr int kBV = 2;  // blocks per V load burst (decode kernel)
 // The step kernel's decode items: a deeper V burst. A CU there typically
 // holds one decode and one tile workgroup, so a decode workgroup keeps more
 // bytes in flight on its own (the tile body sets the register budget
 // anyway). Mixed step: bursts (K 4, V 2) 569-573 us, (4, 4) 555-564, (8, 2)
 // 577-588, (8, 4) 573-576.
-#ifndef VL_STEP_BK
-#define VL_STEP_BK 4
-#endif
-#ifndef VL_STEP_BV
-#define VL_STEP_BV 4
-#endif
+constexpr int kStepBK = 4;  // blocks per K load burst (step kernel's decode items)
+constexpr int kStepBV = 4;  // blocks per V load burst (step kernel's decode items)
 
 // MFMA tile-kernel shape: 4 wavefronts x 16 (token, head) rows per workgroup,
 // 64 keys per LDS tile
@@ -91,10 +78,7 @@ constexpr int kTileKeys = 64;
 // each staged K/V tile (the 4-wavefront step kernel takes an item in two
 // passes)
 constexpr int kWideRows = 256;
-#ifndef VL_PV_LOOK
-#define VL_PV_LOOK 2
-#endif
-constexpr int kPvLook = VL_PV_LOOK;  // 32-row PV product: V^T operands read this many MFMAs ahead
+constexpr int kPvLook = 2;  // 32-row PV product: V^T operands read this many MFMAs ahead
 
 struct Layout {
   int32_t* hdr;
@@ -290,18 +274,9 @@ __device__ __forceinline__ SeqWork seq_work(int q, int c, int P, int R, int H, i
   return w;
 }
 
-#ifndef VL_RANGE_MAX
-#define VL_RANGE_MAX 2048
-#endif
-#ifndef VL_ITEMS_PER_WG
-#define VL_ITEMS_PER_WG 4
-#endif
-constexpr int kRangeMax = VL_RANGE_MAX;       // longest decode range the planner starts with
-constexpr int kItemsPerWg = VL_ITEMS_PER_WG;  // decode items aimed for per resident workgroup
-#ifndef VL_TILE_ITEMS_PER_WG
-#define VL_TILE_ITEMS_PER_WG 4
-#endif
-constexpr int kTileItemsPerWg = VL_TILE_ITEMS_PER_WG;  // split tile items aimed for per workgroup
+constexpr int kRangeMax = 2048;       // longest decode range the planner starts with
+constexpr int kItemsPerWg = 4;  // decode items aimed for per resident workgroup
+constexpr int kTileItemsPerWg = 4;  // split tile items aimed for per workgroup
 constexpr int kTailBuckets = 1024;
 constexpr int kPlanBuckets = kTailBuckets / kPlanThreads;  // buckets owned by each plan thread
 constexpr int kPlanRegSeqs = 4;  // sequences a plan thread keeps in registers (S <= 1024)
@@ -1312,6 +1287,16 @@ __device__ __forceinline__ void leave_and_reset(int32_t* counters, int n) {
 
 constexpr int kXcds = 8;
 
+// The item index of claim c of a persistent kernel's queue (items base,
+// base + stride, ...), or n (none: the claimer stops) when it falls outside
+// the n items. Computed in 64 bits, so that no counter value, whatever it
+// held, gives an index that wraps to a negative int and passes an `it < n`
+// test into an item body.
+__device__ __forceinline__ int claimed_item(int64_t c, int stride, int base, int n) {
+  const int64_t it = c * stride + base;
+  return c < 0 || it >= n ? n : (int)it;
+}
+
 // RW = rows per wavefront (see tile_body). Persistent workgroups take items
 // from 8 queues, queue x holding the items it with it % 8 == x: workgroup b
 // serves queue b % 8 (workgroups are dispatched round-robin over the 8 XCDs,
@@ -1337,12 +1322,13 @@ __global__ void __launch_bounds__(64 * kWv) __attribute__((amdgpu_waves_per_eu(2
   int it = (blockIdx.x / kXcds) * kXcds + xcd;
   while (it < n_items) {
     int nxt = 0;
-    if (threadIdx.x == 0) nxt = per_queue + atomicAdd(counters + xcd, 1);
+    if (threadIdx.x == 0)
+      nxt = claimed_item(per_queue + (int64_t)atomicAdd(counters + xcd, 1), kXcds, xcd, n_items);
     tile_body<T, D, RW, false, kWv, TKV>(lds, it, 0, P, item_off, item_seq, VL_ATTN_ARGS);
     __syncthreads();  // the item is done with the LDS; claim_lds has been read
     if (threadIdx.x == 0) claim_lds = nxt;
     __syncthreads();
-    it = claim_lds * kXcds + xcd;
+    it = claim_lds;
   }
 }
 
@@ -1534,17 +1520,10 @@ __device__ __forceinline__ DecodeItem decode_fetch(int4 d, int it, int R, int Hk
 // out of a pool far larger than the caches: non-temporal (streaming) loads
 // measured 222-230 us against 241 us with ordinary loads for the 256-sequence
 // batch (1.29 GB).
-#ifndef VL_DECODE_NT
-#define VL_DECODE_NT 1
-#endif
 __device__ __forceinline__ uint4 load_stream16(const char* p) {
-  if constexpr (VL_DECODE_NT) {
-    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-    return make_uint4(v.x, v.y, v.z, v.w);
-  } else {
-    return *reinterpret_cast<const uint4*>(p);
-  }
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 // One item (see above) by the 256 threads of a workgroup, from its prologue
@@ -1846,7 +1825,8 @@ __global__ void __launch_bounds__(256) attend_decode_bf16_kernel(
   int it = blockIdx.x;
   while (it < n_items) {
     int nxt = 0;
-    if (threadIdx.x == 0) nxt = (int)gridDim.x + atomicAdd(work, 1);
+    if (threadIdx.x == 0)
+      nxt = claimed_item((int64_t)gridDim.x + atomicAdd(work, 1), 1, 0, n_items);
     decode_body<false, kBK, kBV>(
         s, it, decode_fetch(desc[it / Hkv], it, R, Hkv, wave, lane, query, q_stride, bt, bt_stride),
         R, VL_ATTN_ARGS);
@@ -2173,9 +2153,7 @@ __global__ void __launch_bounds__(64 * NW) attend_short_decode_kernel(
 // [1 + x] tile queue x, [9] workgroups finished.
 constexpr size_t kStepLds = std::max({sizeof(TileLds<uint16_t, kFD, 32>),
                                       sizeof(TileLds<uint16_t, kFD, 16>), sizeof(DecodeLds)});
-#ifndef VL_STEP_TILE_FIRST
-#define VL_STEP_TILE_FIRST 2  // one in this many workgroups starts on the tile queues
-#endif
+constexpr int kStepTileFirst = 2;  // one in this many workgroups starts on the tile queues
 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 attend_step_bf16_kernel(VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hdr,
@@ -2194,7 +2172,7 @@ attend_step_bf16_kernel(VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hd
   const int n_wide = hdr[10], n_tiles = 2 * n_wide + hdr[4], n_dec = hdr[0];
   const int R = hdr[7];
   const int xcd = blockIdx.x % kXcds;
-  const bool tiles_first = (blockIdx.x / kXcds) % VL_STEP_TILE_FIRST == 0;
+  const bool tiles_first = (blockIdx.x / kXcds) % kStepTileFirst == 0;
   for (int v = 0; v <= kXcds; ++v) {  // the decode queue and the 8 tile queues, in turn
     const int qid = tiles_first ? (v < kXcds ? 1 + (xcd + v) % kXcds : 0)
                                 : (v == 0 ? 0 : 1 + (xcd + v - 1) % kXcds);
@@ -2206,16 +2184,19 @@ attend_step_bf16_kernel(VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hd
       // a queue seen empty is skipped without an atomic; one thread decides,
       // so the whole workgroup takes the same branch around the barriers
       const int seen = __hip_atomic_load(counters + qid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      claim_lds = seen * stride + base >= n ? -1 : atomicAdd(counters + qid, 1);
+      claim_lds = claimed_item(seen, stride, base, n) >= n
+                      ? -1
+                      : claimed_item(atomicAdd(counters + qid, 1), stride, base, n);
     }
     __syncthreads();
     if (claim_lds < 0) continue;
-    int it = claim_lds * stride + base;
+    int it = claim_lds;
     while (it < n) {
       int nxt = 0;
-      if (threadIdx.x == 0) nxt = atomicAdd(counters + qid, 1);  // the next item, claimed early
+      if (threadIdx.x == 0)  // the next item, claimed early
+        nxt = claimed_item(atomicAdd(counters + qid, 1), stride, base, n);
       if (!tiles)
-        decode_body<true, VL_STEP_BK, VL_STEP_BV>(dl, it,
+        decode_body<true, kStepBK, kStepBV>(dl, it,
                           decode_fetch(desc[it / Hkv], it, R, Hkv, threadIdx.x >> 6,
                                        threadIdx.x & 63, query, q_stride, bt, bt_stride),
                           R, VL_ATTN_ARGS);
@@ -2228,7 +2209,7 @@ attend_step_bf16_kernel(VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hd
       __syncthreads();  // the item is done with the LDS; claim_lds has been read
       if (threadIdx.x == 0) claim_lds = nxt;
       __syncthreads();
-      it = claim_lds * stride + base;
+      it = claim_lds;
     }
   }
   leave_and_reset(counters, kXcds + 1);
