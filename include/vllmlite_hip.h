@@ -362,11 +362,16 @@ int vl_resolve_tokens(int32_t* token_ids, int64_t num_tokens, const int32_t* pre
  * picked[r] = argmax(row r), ties to the lowest index (numpy's argmax). Writes
  * out_tokens[i, 0..max_drafts] = picked while it equals the draft, then the
  * first mismatch (or, all matched, the bonus row's pick); unused entries -1;
- * num_accepted[i] = drafts accepted. Integer outputs are exact.
+ * num_accepted[i] = drafts accepted. Integer outputs are exact. One launch
+ * (ABI 12: before, a pick and an acceptance launch): scratch holds 8 *
+ * num_seqs * (max_drafts + 1) + 4 * num_seqs bytes, 8-byte aligned, zero
+ * before the first call; every call leaves it zero again (calls that overlap
+ * on one scratch race).
  */
 int vl_greedy_verify(const float* logits, int64_t row_stride, int vocab, const int32_t* row_start,
                      const int32_t* num_drafts, const int32_t* drafts, int max_drafts,
-                     int32_t* out_tokens, int32_t* num_accepted, int num_seqs, void* stream);
+                     int32_t* out_tokens, int32_t* num_accepted, int num_seqs, void* scratch,
+                     int64_t scratch_bytes, void* stream);
 
 /*
  * Row-wise argmax (ties to the lowest index) of rows x vocab fp32 logits into

@@ -300,6 +300,62 @@ def test_greedy_verify_matches_oracle():
         assert got[s, :len(toks)].tolist() == toks and (got[s, len(toks):] == -1).all()
 
 
+@pytest.mark.parametrize("V,stride", [(1003, 1003), (1003, 1004), (32000, 32000), (9, 12)])
+def test_greedy_verify_edge_rows(V, stride):
+    """vl_greedy_verify (one workgroup per sequence, rows two at a time, the
+    scan ending at the first mismatch) against the oracle's verify: ties to
+    the lowest index, NaN rows (the first NaN wins), rows of -inf, a vocab
+    that is not a multiple of 4, rows that are not 16-byte aligned (odd
+    stride: the scalar path), no drafts, every draft accepted (the bonus
+    row), and max_drafts above every sequence's drafts."""
+    from oracle.greedy import verify
+    o = ops()
+    rng = np.random.default_rng(V + stride)
+    S, K = 24, 6
+    nd = np.array([rng.integers(0, K) for _ in range(S)], np.int32)
+    nd[:3] = [0, K - 1, 1]
+    rows = nd + 1
+    row_start = np.zeros(S, np.int32)
+    row_start[1:] = np.cumsum(rows)[:-1]
+    R = int(rows.sum())
+    buf = np.full((R, stride), 7.0, np.float32)  # the padding past V is never a candidate
+    lg = rng.standard_normal((R, V)).astype(np.float32)
+    for r in range(R):
+        kind = r % 5
+        if kind == 1:  # a tie: the lowest index wins
+            c = rng.integers(0, V, 2)
+            lg[r, c] = lg[r].max() + 1.0
+        elif kind == 2:  # NaNs: the first one wins
+            c = np.sort(rng.integers(0, V, 2))
+            lg[r, c] = np.nan
+        elif kind == 3:
+            lg[r] = -np.inf
+    buf[:, :V] = lg
+    drafts = np.zeros((S, K), np.int32)
+    for s in range(S):
+        acc = nd[s] if s % 3 == 1 else int(rng.integers(0, nd[s] + 1))
+        for r in range(nd[s]):
+            best = int(np.argmax(lg[row_start[s] + r]))
+            drafts[s, r] = best if r < acc else (best + 1) % V
+    flat = torch.from_numpy(buf.reshape(-1)).cuda()
+    logits = flat.as_strided((R, V), (stride, 1))
+    scratch = torch.zeros(S * (K + 1) + S, dtype=torch.int64, device="cuda")
+    for _ in range(2):  # the scratch is left zero: a second call needs no clearing
+        out = torch.full((S, K + 1), 99, dtype=torch.int32, device="cuda")
+        nacc = torch.full((S,), 99, dtype=torch.int32, device="cuda")
+        o.greedy_verify(logits, dev(row_start), dev(nd), dev(drafts), out, nacc, scratch=scratch)
+        torch.cuda.synchronize()
+        assert int(scratch.abs().sum()) == 0
+    got, got_acc = to_np(out).astype(np.int64), to_np(nacc).astype(np.int64)
+    full = 0
+    for s in range(S):
+        toks, acc = verify(lg[row_start[s]:row_start[s] + rows[s]], list(drafts[s, :nd[s]]))
+        full += acc == nd[s] and nd[s] > 0
+        assert got_acc[s] == acc, s
+        assert got[s, :len(toks)].tolist() == toks and (got[s, len(toks):] == -1).all(), s
+    assert full >= 3
+
+
 DECODE_CTX = [1, 5, 15, 16, 17, 100, 255, 256, 257, 1000, 4097, 64, 8192]
 
 

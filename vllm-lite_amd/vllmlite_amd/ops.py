@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from typing import Optional
+from typing import Dict, Optional
 
 import numpy as np
 import torch
@@ -24,7 +24,7 @@ F32, BF16, F32_BF16KV, FP8_E4M3, F32_FP8KV = 0, 1, 2, 3, 4
 # VL_KV_*: a per-layer cache tensor [slots, Hkv, D] is token-major (the
 # reference's layout), [blocks, Hkv, block_size, D] head-major
 KV_TOKEN_MAJOR, KV_HEAD_MAJOR = 0, 1
-ABI_VERSION = 11  # vl_abi_version() of the library these signatures describe
+ABI_VERSION = 12  # vl_abi_version() of the library these signatures describe
 _c_void_p = ctypes.c_void_p
 _i32, _i64, _f32, _size = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
 
@@ -65,7 +65,7 @@ SIGNATURES = {
                                  _c_void_p, _c_void_p, _c_void_p, _i64, _i32, _i32, _i32, _i32,
                                  _i32, _i32, _c_void_p]),
     "vl_greedy_verify": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p, _c_void_p, _i32,
-                                _c_void_p, _c_void_p, _i32, _c_void_p]),
+                                _c_void_p, _c_void_p, _i32, _c_void_p, _i64, _c_void_p]),
     "vl_argmax_rows": (_i32, [_c_void_p, _i64, _i64, _i32, _c_void_p, _c_void_p, _c_void_p]),
     "vl_linear_rows": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64,
                               _c_void_p, _f32, _i32, _i32, _i32, _i32, _c_void_p]),
@@ -586,10 +586,16 @@ def rope_and_cache(qkv: torch.Tensor, q_out: torch.Tensor, key_cache: torch.Tens
 
 
 # ------------------------------------------------------------------ K5 -----
+_verify_scratch: Dict[int, torch.Tensor] = {}  # per stream: left zero by every call
+
+
 def greedy_verify(logits: torch.Tensor, row_start: torch.Tensor, num_drafts: torch.Tensor,
                   drafts: torch.Tensor, out_tokens: torch.Tensor,
-                  num_accepted: torch.Tensor) -> None:
-    """logits fp32 [R, V]; drafts int32 [S, K]; out_tokens int32 [S, K+1]."""
+                  num_accepted: torch.Tensor, scratch: Optional[torch.Tensor] = None) -> None:
+    """logits fp32 [R, V]; drafts int32 [S, K]; out_tokens int32 [S, K+1].
+    scratch: int64 device tensor of at least S (K + 1) + ceil(S / 2) entries,
+    zero before the first call (every call leaves it zero); by default one
+    kept per stream (calls on one stream run in order, so they share it)."""
     _need(logits.dtype == torch.float32 and logits.stride(1) == 1, "logits must be fp32 rows")
     S, K = drafts.shape
     for t, n in ((row_start, "row_start"), (num_drafts, "num_drafts"), (drafts, "drafts"),
@@ -597,9 +603,19 @@ def greedy_verify(logits: torch.Tensor, row_start: torch.Tensor, num_drafts: tor
         _dev_i32(t, n)
     _need(out_tokens.shape == (S, K + 1) and num_accepted.numel() == S and
           row_start.numel() == S and num_drafts.numel() == S, "shape mismatch")
+    words = S * (K + 1) + (S + 1) // 2
+    if scratch is None:
+        key = torch.cuda.current_stream(logits.device).cuda_stream
+        scratch = _verify_scratch.get(key)
+        if scratch is None or scratch.numel() < words or scratch.device != logits.device:
+            scratch = torch.zeros(max(words, 1024), dtype=torch.int64, device=logits.device)
+            _verify_scratch[key] = scratch
+    _need(scratch.dtype == torch.int64 and scratch.is_cuda and scratch.is_contiguous() and
+          scratch.numel() >= words, "scratch must be a contiguous int64 device tensor")
     _check(lib().vl_greedy_verify(_ptr(logits), logits.stride(0), logits.shape[1],
                                   _ptr(row_start), _ptr(num_drafts), _ptr(drafts), K,
-                                  _ptr(out_tokens), _ptr(num_accepted), S, _stream()),
+                                  _ptr(out_tokens), _ptr(num_accepted), S, _ptr(scratch),
+                                  scratch.numel() * 8, _stream()),
            "vl_greedy_verify")
 
 
