@@ -303,7 +303,13 @@ int vl_linear_rows_parts(float* out, int64_t out_stride, const float* x, int64_t
  * stream). weight_layout: VL_WEIGHT_ROWS (row stride weight_stride) or
  * VL_WEIGHT_TILES16 (as for vl_linear_rows). rows <= 16 * 65535, k a multiple
  * of 16, k <= 1024, head_dim even. fp32; the caches hold cache_dtype elements in
- * kv_layout as for vl_rope_and_cache.
+ * kv_layout as for vl_rope_and_cache. When record_words > 0 the launch also
+ * copies record_src[0 .. record_words) to record_dst (ABI 13; no reference
+ * counterpart): a step's int32 record from pinned host memory to the device
+ * in the step's first launch, instead of a copy launch before it.
+ * row_index, positions and slot_mapping may then point into record_src (they
+ * are read from there); record_dst must not overlap anything the launch
+ * reads, and holds the copy once the launch has ended.
  */
 int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cache, const float* x,
                       int64_t x_stride, const int32_t* row_index, const int32_t* prev_ids,
@@ -312,7 +318,8 @@ int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cache, const fl
                       const float* norm_weight, float eps, const int32_t* positions,
                       const int32_t* slot_mapping, const float* cos_table, const float* sin_table,
                       int rows, int k, int num_heads, int num_kv_heads, int head_dim,
-                      int cache_dtype, int kv_layout, int block_size, void* stream);
+                      int cache_dtype, int kv_layout, int block_size, const int32_t* record_src,
+                      int32_t* record_dst, int64_t record_words, void* stream);
 
 /*
  * K2 for a decode batch (every sequence one query; the short-decode kernel's

@@ -48,7 +48,7 @@ def test_no_compute_without_gpu_needed_for_queries():
     assert lib.vl_paged_attention_workspace_size(256, 256, 32, 128, 8192) > \
         lib.vl_paged_attention_min_workspace(256)
     lib.vl_abi_version.restype = ctypes.c_int
-    assert lib.vl_abi_version() == 12
+    assert lib.vl_abi_version() == 13
 
 
 def test_reads_plan_names_the_short_decode_shapes():

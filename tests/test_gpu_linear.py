@@ -447,3 +447,46 @@ def test_linear_rows_argmax_bad_arguments_raise():
     with pytest.raises(ValueError):  # row-major weight (refused before the call)
         o.linear_rows_argmax(out, x, torch.zeros((64, 40), device="cuda"), None, ids,
                              torch.zeros(5, dtype=torch.int64, device="cuda"))
+
+
+@pytest.mark.parametrize("rows,extra", [(16, 700), (5, 0), (1, 100_000)])
+def test_qkv_rope_cache_reads_and_copies_a_pinned_record(rows, extra):
+    """vl_qkv_rope_cache with a record: its token / position / slot indices
+    read from pinned host memory (views of the record) give the same bits as
+    the same indices on the device, and the launch copies the whole record to
+    the device (a record longer than the launch's threads too: 100K words
+    against one row's 48 x 512)."""
+    o = _ops()
+    H, Hkv, D, k = 8, 4, 48, 384
+    n = (H + 2 * Hkv) * D
+    rng = np.random.default_rng(rows + extra)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    table = dev(rng.standard_normal((261, k)).astype(np.float32))
+    prev = dev(rng.integers(0, 261, 12).astype(np.int32))
+    w = dev(o.tile16(torch.from_numpy((0.05 * rng.standard_normal((k, n))).astype(np.float32)))
+            .numpy())
+    g = dev((1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32))
+    ang = rng.standard_normal((64, D // 2)).astype(np.float32)
+    cos, sin = dev(np.cos(ang)), dev(np.sin(ang))
+    # the record: tokens (some placeholders), positions, slots, then other words
+    toks = rng.integers(0, 261, rows).astype(np.int32)
+    toks[::3] = -1 - rng.integers(0, 12, len(toks[::3]))
+    rec = np.concatenate([toks, rng.integers(0, 64, rows).astype(np.int32),
+                          rng.permutation(40)[:rows].astype(np.int32),
+                          rng.integers(-5, 5, extra).astype(np.int32)])
+    host = torch.from_numpy(rec).pin_memory()
+    drec = dev(rec)
+    dst = torch.full((rec.size,), -99, dtype=torch.int32, device="cuda")
+    out = []
+    for src, record in ((drec, None), (host, (host, dst))):
+        kc, vc = (torch.zeros((40, Hkv, D), device="cuda") for _ in range(2))
+        q = torch.empty((rows, H * D), device="cuda")
+        x = torch.full((rows, k), float("nan"), device="cuda")
+        o.qkv_rope_cache(q, kc, vc, table, w, g, src[rows:2 * rows], src[2 * rows:3 * rows],
+                         cos, sin, H, Hkv, D, row_index=src[:rows], x_out=x, prev_ids=prev,
+                         record=record)
+        out.append((q, kc, vc, x))
+    torch.cuda.synchronize()
+    for a, b in zip(*out):
+        assert torch.equal(a, b)
+    assert torch.equal(dst.cpu(), torch.from_numpy(rec))

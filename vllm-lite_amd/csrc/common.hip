@@ -15,7 +15,7 @@ void vl_set_error(const char* fmt, ...) {
 
 extern "C" const char* vl_last_error(void) { return g_err; }
 
-extern "C" int vl_abi_version(void) { return 12; }
+extern "C" int vl_abi_version(void) { return 13; }
 
 int vl_num_cus() {
   static int cached[64] = {0};

@@ -69,6 +69,11 @@ struct RopeCache {
   const float* sin_t;
   int nh, nkv, hd;
   int kv_dtype;  // VL_DTYPE_F32, or VL_DTYPE_BF16 / VL_DTYPE_FP8_E4M3 (rounded to nearest even)
+  // a record copied by the same launch (rec_n words from rec_src to rec_dst),
+  // or none (rec_n 0)
+  const int32_t* rec_src;
+  int32_t* rec_dst;
+  int64_t rec_n;
 };
 
 // Where MODE 4 puts each row's argmax (vl_linear_rows_argmax). Every
@@ -230,6 +235,15 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
   // ---- loads of the first row tile
   const int r00 = blockIdx.y * nsub * rt;
   index_reads(r00, min(rt, M_all - r00));
+  // MODE 3 with a record: thread g of the grid copies word g (loaded here,
+  // after the index reads, which may read the record's source too; stored at
+  // the end) and, in records longer than the grid, words g + grid, ...
+  const int64_t rec_g =
+      ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * (64 * kLinWaves) + tid;
+  int32_t rec_word = 0;
+  if constexpr (MODE == 3) {
+    if (rc.rec_n > 0) rec_word = rc.rec_src[min(rec_g, rc.rec_n - 1)];
+  }
   // the B operands: lane (m, j), group g, step s needs w[16 (gb + g) + 4 j +
   // s][c0 + m]; in a tile that is one float4 at 256 (gb + g) + 4 (16 j + m)
   float4 wv[kSlices][kGroups];
@@ -412,6 +426,14 @@ __global__ void __launch_bounds__(64 * kLinWaves) linear_rows_kernel(
       if (tid == 0) __hip_atomic_store(am.count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+  if constexpr (MODE == 3) {
+    if (rc.rec_n > 0) {
+      if (rec_g < rc.rec_n) rc.rec_dst[rec_g] = rec_word;
+      const int64_t grid_threads = (int64_t)gridDim.x * gridDim.y * (64 * kLinWaves);
+      for (int64_t w = rec_g + grid_threads; w < rc.rec_n; w += grid_threads)
+        rc.rec_dst[w] = rc.rec_src[w];
+    }
+  }
 }
 
 // Row tiles per workgroup: 1 while the grid is at most one round of two
@@ -534,7 +556,8 @@ extern "C" int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cach
                                  const int32_t* positions, const int32_t* slot_mapping,
                                  const float* cos_table, const float* sin_table, int rows, int k,
                                  int num_heads, int num_kv_heads, int head_dim, int cache_dtype,
-                                 int kv_layout, int block_size, void* stream) {
+                                 int kv_layout, int block_size, const int32_t* record_src,
+                                 int32_t* record_dst, int64_t record_words, void* stream) {
   VL_CHECK_ARG(vl_cache_elem_bytes(cache_dtype) > 0, "bad cache dtype %d", cache_dtype);
   KvGeom geom;
   if (num_kv_heads > 0 && head_dim > 0)
@@ -558,12 +581,15 @@ extern "C" int vl_qkv_rope_cache(float* q_out, void* key_cache, void* value_cach
   VL_CHECK_ARG((((uintptr_t)norm_weight) & 15) == 0, "norm weight must be 16-byte aligned");
   VL_CHECK_ARG(num_prev >= 0 && (num_prev == 0 || (prev_ids && row_index)),
                "prev_ids needs row_index (and num_prev > 0 needs prev_ids)");
+  VL_CHECK_ARG(record_words >= 0 && (record_words == 0 || (record_src && record_dst)),
+               "a record needs its source and destination");
   RopeCache rc;
   rc.q_out = q_out, rc.kc = key_cache, rc.vc = value_cache, rc.positions = positions;
   rc.slots = slot_mapping, rc.cos_t = cos_table, rc.sin_t = sin_table;
   rc.nh = num_heads, rc.nkv = num_kv_heads, rc.hd = head_dim;
   rc.kv_dtype = cache_dtype;
   rc.geom = geom;
+  rc.rec_src = record_src, rc.rec_dst = record_dst, rc.rec_n = record_words;
   hipStream_t st = (hipStream_t)stream;
   const bool nrm = norm_weight != nullptr;
 #define VL_QKV(NORM, KM) \

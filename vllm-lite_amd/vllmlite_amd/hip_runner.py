@@ -554,15 +554,23 @@ class HipRunner(ModelRunner):
         bucket's Rb logits rows into self._ids and pinned buffer k (rows past
         the step's R are the padded rows' and never read)."""
         n = s.n_ints
-        # read from the pinned record by a kernel: as a graph's memcpy node
-        # this copy cost ~12 us more per step
-        ops.copy_words(self._meta[:n], self._meta_hosts[k][:n])
-        if not self._forward_body(s, self._ids_hosts[k]):
+        if not self._rows_path(s):
+            # read from the pinned record by a kernel: as a graph's memcpy node
+            # this copy cost ~12 us more per step
+            ops.copy_words(self._meta[:n], self._meta_hosts[k][:n])
+        if not self._forward_body(s, self._ids_hosts[k], self._meta_hosts[k]):
             ops.argmax_rows(self._logits[:s.Rb], self._ids[:s.Rb], host_out=self._ids_hosts[k])
 
-    def _forward_body(self, s: _Shape, ids_host: torch.Tensor) -> bool:
+    def _rows_path(self, s: _Shape) -> bool:
+        """Whether shape s runs on the fused projection kernels (whose first
+        launch also copies the step's record to the device)."""
+        return s.Tb <= min(self.fused_rows_max, ops.LINEAR_ROWS_MAX) and self._fused_rows
+
+    def _forward_body(self, s: _Shape, ids_host: torch.Tensor, rec_host: torch.Tensor) -> bool:
         """The forward of staged shape s into self._logits[:Rb]; True when its
-        lm_head launch also wrote the rows' argmax (to self._ids and ids_host)."""
+        lm_head launch also wrote the rows' argmax (to self._ids and ids_host).
+        rec_host: the pinned record the step was staged into (on the fused
+        path layer 0 reads its indices there and copies it to the device)."""
         mc = self.model_cfg
         Tb, Sb, Rb = s.Tb, s.Sb, s.Rb
         meta = self._meta
@@ -577,8 +585,8 @@ class HipRunner(ModelRunner):
         qkv, q, attn = self._qkv[:Tb], self._q[:Tb], self._attn[:Tb]
         gu, act = self._gu[:Tb], self._act[:Tb]
         W = self.w
-        if Tb <= min(self.fused_rows_max, ops.LINEAR_ROWS_MAX) and self._fused_rows:
-            self._forward_rows(s, x, q, attn, act, tok, pos, slot, lidx, qsl, lens, bt, ids_host)
+        if self._rows_path(s):
+            self._forward_rows(s, x, q, attn, act, lidx, qsl, lens, bt, ids_host, rec_host)
             return True
         # ids the previous step chose on the device (negative placeholders)
         ops.resolve_tokens(tok, self._ids)
@@ -627,8 +635,22 @@ class HipRunner(ModelRunner):
                                self._ids[:Rb], self._am_scratch, host_ids=ids_host,
                                row_index=lidx)
 
-    def _forward_rows(self, s: _Shape, x, q, attn, act, tok, pos, slot, lidx, qsl, lens,
-                      bt, ids_host) -> None:
+    def _layer0_qkv(self, s: _Shape, x_out, q, rec_host) -> None:
+        """Layer 0's QKV + RoPE + scatter with the embedding gather (x =
+        tok_emb[tok] written to x_out; a placeholder token -(1 + r) is the id
+        the previous step chose for its row r, read from the device), its
+        token / position / slot indices read from the pinned record, which the
+        same launch copies to the device for the step's later launches."""
+        W, Tb, n = self.w, s.Tb, s.n_ints
+        L = W["layers"][0]
+        ops.qkv_rope_cache(q.view(Tb, -1), self.cache_k[0], self.cache_v[0], W["tok_emb"],
+                           L["w_qkv_t"], L["attn_norm"], rec_host[s.pos:s.pos + Tb],
+                           rec_host[s.slot:s.slot + Tb], self.cos, self.sin, self.H, self.Hkv,
+                           self.hd, row_index=rec_host[s.tok:s.tok + Tb], x_out=x_out,
+                           prev_ids=self._ids, record=(rec_host[:n], self._meta[:n]))
+
+    def _forward_rows(self, s: _Shape, x, q, attn, act, lidx, qsl, lens, bt, ids_host,
+                      rec_host) -> None:
         """The forward by the fused projection kernels (every decode step, and
         prefill steps up to fused_rows_max rows): each projection is one
         launch with its RMSNorm, residual add, SwiGLU or RoPE + K/V scatter
@@ -639,18 +661,15 @@ class HipRunner(ModelRunner):
         prologue: four launches per layer."""
         W, Tb, Rb = self.w, s.Tb, s.Rb
         if s.decode and self._fused_wo:
-            self._forward_decode_wo(s, x, q, act, tok, pos, slot, lidx, qsl, lens, bt, ids_host)
+            self._forward_decode_wo(s, x, q, act, lidx, qsl, lens, bt, ids_host, rec_host)
             return
-        self._plan(s, q, lens, qsl)
+        pos = self._meta[s.pos:s.pos + Tb]
+        slot = self._meta[s.slot:s.slot + Tb]
         for li, L in enumerate(W["layers"]):
             kc, vc = self.cache_k[li], self.cache_v[li]
-            if li == 0:  # the embedding gather, with x = tok_emb[tok] written out; a
-                # placeholder token -(1 + r) is the id the previous step chose
-                # for its row r, read from the device here
-                ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, W["tok_emb"], L["w_qkv_t"],
-                                   L["attn_norm"], pos, slot, self.cos, self.sin, self.H,
-                                   self.Hkv, self.hd, row_index=tok, x_out=x,
-                                   prev_ids=self._ids)
+            if li == 0:
+                self._layer0_qkv(s, x, q, rec_host)
+                self._plan(s, q, lens, qsl)  # reads the record's device copy
             else:
                 ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, x, L["w_qkv_t"], L["attn_norm"], pos,
                                    slot, self.cos, self.sin, self.H, self.Hkv, self.hd)
@@ -660,8 +679,8 @@ class HipRunner(ModelRunner):
             ops.linear_rows(x, act, L["w_down_t"], mode=ops.LINEAR_ACCUMULATE)
         self._lm_head(s, x, lidx, ids_host)
 
-    def _forward_decode_wo(self, s: _Shape, x, q, act, tok, pos, slot, lidx, qsl, lens,
-                           bt, ids_host) -> None:
+    def _forward_decode_wo(self, s: _Shape, x, q, act, lidx, qsl, lens, bt, ids_host,
+                           rec_host) -> None:
         """A decode step in four launches per layer: QKV (+ RoPE + cache);
         attention with wo (vl_decode_attention_wo: parts[s, g] = the outputs
         of KV head g's query heads @ their rows of wo); gate|up over x + the
@@ -672,13 +691,12 @@ class HipRunner(ModelRunner):
         xa, xb = x, self._h[:Tb]
         parts = self._parts[:Tb]
         mc = self.model_cfg
+        pos = self._meta[s.pos:s.pos + Tb]
+        slot = self._meta[s.slot:s.slot + Tb]
         for li, L in enumerate(W["layers"]):
             kc, vc = self.cache_k[li], self.cache_v[li]
             if li == 0:
-                ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, W["tok_emb"], L["w_qkv_t"],
-                                   L["attn_norm"], pos, slot, self.cos, self.sin, self.H,
-                                   self.Hkv, self.hd, row_index=tok, x_out=xa,
-                                   prev_ids=self._ids)
+                self._layer0_qkv(s, xa, q, rec_host)
             else:
                 ops.qkv_rope_cache(q.view(Tb, -1), kc, vc, xa, L["w_qkv_t"], L["attn_norm"], pos,
                                    slot, self.cos, self.sin, self.H, self.Hkv, self.hd)

@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from typing import Dict, Optional
+from typing import Dict, Optional, Tuple
 
 import numpy as np
 import torch
@@ -24,7 +24,7 @@ F32, BF16, F32_BF16KV, FP8_E4M3, F32_FP8KV = 0, 1, 2, 3, 4
 # VL_KV_*: a per-layer cache tensor [slots, Hkv, D] is token-major (the
 # reference's layout), [blocks, Hkv, block_size, D] head-major
 KV_TOKEN_MAJOR, KV_HEAD_MAJOR = 0, 1
-ABI_VERSION = 12  # vl_abi_version() of the library these signatures describe
+ABI_VERSION = 13  # vl_abi_version() of the library these signatures describe
 _c_void_p = ctypes.c_void_p
 _i32, _i64, _f32, _size = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t
 
@@ -73,7 +73,7 @@ SIGNATURES = {
                                  _c_void_p, _i64,
                                  _c_void_p, _c_void_p, _i64, _i32, _c_void_p, _f32, _c_void_p,
                                  _c_void_p, _c_void_p, _c_void_p, _i32, _i32, _i32, _i32, _i32,
-                                 _i32, _i32, _i32, _c_void_p]),
+                                 _i32, _i32, _i32, _c_void_p, _c_void_p, _i64, _c_void_p]),
     "vl_resolve_tokens": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p]),
     "vl_copy_words": (_i32, [_c_void_p, _c_void_p, _i64, _c_void_p]),
     "vl_linear_rows_argmax": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p,
@@ -524,11 +524,14 @@ def qkv_rope_cache(q_out: torch.Tensor, key_cache: torch.Tensor, value_cache: to
                    sin: torch.Tensor, num_heads: int, num_kv_heads: int, head_dim: int,
                    eps: float = 1e-5, row_index: Optional[torch.Tensor] = None,
                    x_out: Optional[torch.Tensor] = None,
-                   prev_ids: Optional[torch.Tensor] = None) -> None:
+                   prev_ids: Optional[torch.Tensor] = None,
+                   record: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> None:
     """QKV projection of a step's rows fused with RoPE and the K/V scatter; with
     row_index the rows are x[row_index] (an index -(1 + i) < 0 stands for
     prev_ids[i], the previous step's id of its row i), copied to x_out when
-    given (see vl_qkv_rope_cache)."""
+    given; record = (src, dst): int32 words the same launch copies from src
+    (pinned host memory, which row_index / positions / slot_mapping may view)
+    to dst (see vl_qkv_rope_cache)."""
     k = x.shape[1]
     rows = q_out.shape[0]
     _need(row_index is not None or x.shape[0] >= rows, "x has too few rows")
@@ -544,6 +547,14 @@ def qkv_rope_cache(q_out: torch.Tensor, key_cache: torch.Tensor, value_cache: to
     tiles, wstride = _weight_layout(weight, k, (num_heads + 2 * num_kv_heads) * head_dim, 1)
     _need(prev_ids is None or (row_index is not None and prev_ids.dtype == torch.int32),
           "prev_ids needs row_index and must hold int32 ids")
+    rsrc, rdst, nrec = None, None, 0
+    if record is not None:
+        rsrc, rdst = record
+        _need(rsrc.dtype == rdst.dtype == torch.int32 and rsrc.is_contiguous() and
+              rdst.is_contiguous() and rsrc.numel() == rdst.numel() and
+              (rsrc.is_pinned() or rsrc.is_cuda) and rdst.is_cuda,
+              "record: contiguous int32 source (pinned or device) and device destination")
+        nrec = rsrc.numel()
     _check(lib().vl_qkv_rope_cache(_ptr(q_out), _ptr(key_cache), _ptr(value_cache), _ptr(x),
                                    x.stride(0), _ptr(row_index), _ptr(prev_ids),
                                    prev_ids.numel() if prev_ids is not None else 0,
@@ -552,7 +563,8 @@ def qkv_rope_cache(q_out: torch.Tensor, key_cache: torch.Tensor, value_cache: to
                                    _ptr(norm_weight),
                                    float(eps), _ptr(positions), _ptr(slot_mapping), _ptr(cos),
                                    _ptr(sin), rows, k, num_heads, num_kv_heads, head_dim, cdt,
-                                   layout, bs, _stream()), "vl_qkv_rope_cache")
+                                   layout, bs, _ptr(rsrc), _ptr(rdst), nrec, _stream()),
+           "vl_qkv_rope_cache")
 
 
 def silu_mul(out: torch.Tensor, gate_up: torch.Tensor) -> None:
