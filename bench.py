@@ -543,13 +543,13 @@ def e2e_leg(name="mixed", repeat=3, cpu=True):
         "floor_us_per_step": fl["floor_us_per_step"], "bytes_per_step": fl["bytes_per_step"],
         "frac": round(fl["floor_us_per_step"] / (wall / steps * 1e6), 4),
         "device_launches_per_decode_step": (mc_layers(cfg) * (4 if runner._fused_wo else 5)
-                                            + 2),
-        "launches_are": ("per layer QKV+RoPE+scatter (layer 0 also gathers the embeddings and "
-                         "resolves the previous step's ids), attention"
+                                            + 1),
+        "launches_are": ("per layer QKV+RoPE+scatter (layer 0 also gathers the embeddings, "
+                         "resolves the previous step's ids, reads its indices from the step's "
+                         "pinned record and copies the record to the device), attention"
                          + (" with wo (one partial row per KV head), residual+norm+gate|up+SwiGLU"
                             if runner._fused_wo else ", wo+residual, norm+gate|up+SwiGLU")
-                         + ", down+residual; then lm_head with each row's argmax, and the step "
-                           "record's copy from pinned host memory")}
+                         + ", down+residual; then lm_head with each row's argmax")}
     if fork:
         out["cow_pairs"] = pairs
     fixture, key = (("cfg0_streams.json", None) if name.startswith("mixed") else
