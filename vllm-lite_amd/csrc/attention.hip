@@ -2223,6 +2223,8 @@ attend_step_bf16_kernel(VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hd
 // sum) and weight (64 partitions at a time); the output dims lane + 64k are
 // then summed over the partitions with the weights read lane by lane, so the
 // partial loads are independent of each other.
+constexpr int kCombineFew = 8;  // partitions whose loads a combine row issues at once
+
 template <typename T>
 __global__ void __launch_bounds__(256) combine_kernel(
     T* __restrict__ out, const int32_t* __restrict__ qsl, int H, int D,
@@ -2242,6 +2244,55 @@ __global__ void __launch_bounds__(256) combine_kernel(
     const int q = qsl[i + 1] - qsl[i];
     for (int j = wave; j < q; j += 4) {
       const int64_t row0 = (int64_t)split_base[i] + (int64_t)(j * H + h) * np;
+      if (np <= kCombineFew) {
+        // every load of the row issued at once (the partials do not depend on
+        // the maximum); the arithmetic is the general loop's below, in the
+        // same order, so the output has the same bits
+        const float2 v = ml[row0 + min(lane, np - 1)];
+        float xs[kCombineFew][kDk];
+#pragma unroll
+        for (int u = 0; u < kCombineFew; ++u)
+#pragma unroll
+          for (int e = 0; e < kDk; ++e)
+            xs[u][e] = po[(row0 + min(u, np - 1)) * D + min(lane + 64 * e, D - 1)];
+        float M = lane < np ? v.x : -__builtin_inff();
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+        float L = 0.f, w = 0.f, acc[kDk];
+#pragma unroll
+        for (int e = 0; e < kDk; ++e) acc[e] = 0.f;
+        if (lane < np) {
+          w = v.x == -__builtin_inff() ? 0.f : exp2_fast(v.x - M);
+          L += v.y * w;
+        }
+        auto wt = [&](int u) {
+          return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), u));
+        };
+#pragma unroll
+        for (int u = 0; u + 4 <= kCombineFew; u += 4) {
+          if (u + 4 > np) break;  // uniform
+#pragma unroll
+          for (int e = 0; e < kDk; ++e)
+            if (lane + 64 * e < D)
+              acc[e] += xs[u][e] * wt(u) + xs[u + 1][e] * wt(u + 1) + xs[u + 2][e] * wt(u + 2) +
+                        xs[u + 3][e] * wt(u + 3);
+        }
+#pragma unroll
+        for (int u = 0; u < kCombineFew; ++u) {
+          if (u < (np & ~3) || u >= np) continue;  // uniform
+#pragma unroll
+          for (int e = 0; e < kDk; ++e)
+            if (lane + 64 * e < D) acc[e] += xs[u][e] * wt(u);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        T* dst = out + ((int64_t)(qsl[i] + j) * H + h) * D;
+#pragma unroll
+        for (int e = 0; e < kDk; ++e)
+          if (lane + 64 * e < D) Elem<T>::store(dst, lane + 64 * e, acc[e] * inv);
+        continue;
+      }
       float M = -__builtin_inff();
       for (int p = lane; p < np; p += 64) M = fmaxf(M, ml[row0 + p].x);
 #pragma unroll
