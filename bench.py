@@ -509,6 +509,34 @@ def mc_layers(cfg):
     return cfg.model.n_layers
 
 
+def launch_floor_us(n, reps=50):
+    """The time per replay of a HIP graph of n dependent launches that each
+    copy one int32 word with one workgroup (the least a launch does), replayed
+    back to back: the floor, on this GPU, of a step made of n dependent
+    launches, whatever the kernels compute."""
+    import torch
+    from vllmlite_amd import ops
+    a = torch.zeros(1, dtype=torch.int32, device="cuda")
+    b = torch.zeros_like(a)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for i in range(n):
+            ops.copy_words(b if i % 2 else a, a if i % 2 else b)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(n):
+                ops.copy_words(b if i % 2 else a, a if i % 2 else b)
+        g.replay()
+        s.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            g.replay()
+        e1.record(s)
+        e1.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
 def e2e_leg(name="mixed", repeat=3, cpu=True):
     """Output tok/s of a mix through HipRunner (one warm-up pass, then best of
     `repeat`; the runner and its captured graphs persist across passes, each
@@ -537,13 +565,19 @@ def e2e_leg(name="mixed", repeat=3, cpu=True):
            "output_tok_per_s": round(toks / wall, 1), "wall_s": round(wall, 4),
            "steps": steps, "us_per_step": round(wall / steps * 1e6, 1), "output_tokens": toks}
     fl = mix_floor(cfg, name)
+    n_launch = mc_layers(cfg) * (4 if runner._fused_wo else 5) + 1
+    lf = launch_floor_us(n_launch)
     out["roofline"] = {
         "bound": "hbm (weights + K/V per step at 8 TB/s; the steps are launch- and "
                  "latency-bound far above it)",
         "floor_us_per_step": fl["floor_us_per_step"], "bytes_per_step": fl["bytes_per_step"],
         "frac": round(fl["floor_us_per_step"] / (wall / steps * 1e6), 4),
-        "device_launches_per_decode_step": (mc_layers(cfg) * (4 if runner._fused_wo else 5)
-                                            + 1),
+        "device_launches_per_decode_step": n_launch,
+        "launch_floor_us_per_step": round(lf, 1),
+        "launch_floor_frac": round(lf / (wall / steps * 1e6), 4),
+        "launch_floor_is": ("a graph of that many dependent one-workgroup launches (each copying "
+                            "one word) replayed back to back on this GPU: the floor of the "
+                            "decode step's launch structure, whatever the kernels compute"),
         "launches_are": ("per layer QKV+RoPE+scatter (layer 0 also gathers the embeddings, "
                          "resolves the previous step's ids, reads its indices from the step's "
                          "pinned record and copies the record to the device), attention"
