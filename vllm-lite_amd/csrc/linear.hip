@@ -108,9 +108,10 @@ __device__ __forceinline__ void store_cache(void* cache, int64_t i, float v, int
     static_cast<float*>(cache)[i] = v;
 }
 
-// MODE 0: out = f(x) @ w (4: and each row's argmax to am); 1: out += f(x) @ w; 2: out = silu(f(x) @ w[:, :n]) *
-// (f(x) @ w[:, up_off : up_off + n]); 3: f(x) @ w is a [q | k | v] row: q and k
-// rotated by RoPE, q to rc.q_out, k and v to the caches at the row's slot.
+// MODE 0: out = f(x) @ w (4: and each row's argmax to am); 1: out += f(x) @
+// w; 2: out = silu(f(x) @ w[:, :n]) * (f(x) @ w[:, up_off : up_off + n]); 3:
+// f(x) @ w is a [q | k | v] row: q and k rotated by RoPE, q to rc.q_out, k and
+// v to the caches at the row's slot (and rc's record copied, when it has one).
 // f(x) = x, or with NORM the RMSNorm of x times norm_w, applied as
 // ((x * norm_w) @ w) / rms(x): the per-row scale 1 / rms commutes with the
 // product, so no wavefront waits for another's rows before its MFMAs.
