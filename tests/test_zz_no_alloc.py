@@ -57,7 +57,7 @@ def test_noalloc_matches_workspace_call_twice(dtype):
 def test_noalloc_rejects_batches_beyond_its_scratch():
     from vllmlite_amd import ops
     lib = ops.lib()
-    n = 2_000_000  # its plan alone needs ~88 MB, beyond the 32 MiB scratch
+    n = 2_000_000  # its plan alone needs ~112 MB, beyond the 32 MiB scratch
     assert lib.vl_paged_attention_min_workspace(n) > ops.NOALLOC_SCRATCH_BYTES
     rc = lib.vl_paged_attention_noalloc(None, None, 0, None, None, None, 0, None, None, n, n,
                                         32, 8, 128, 16, 1.0, 1, 0, 1, 1, 0, None)

@@ -83,7 +83,12 @@ constexpr int kPvLook = 2;  // 32-row PV product: V^T operands read this many MF
 struct Layout {
   int32_t* hdr;
   int32_t* gen_off;     // [S+1] generic wavefront items
-  int32_t* tile_off;    // [S+1] MFMA tile workgroup items
+  int32_t* tile_off;    // [S+1] 16-row MFMA tile items of every partition but the last
+                        // (all P keys long), in sequence order
+  int32_t* tail_seq;    // [S] sequences in the order their last partitions' 16-row
+                        // items are handed out (after all of the above): longest first
+  int32_t* tail_off;    // [S+1] those items, by position in tail_seq (right after
+                        // tail_seq: the kernels find it at tail_seq + S)
   int32_t* nparts;      // [S]
   int32_t* split_base;  // [S] first partial row, or -1
   int32_t* wide_off;    // [S+1] 32-row MFMA tile workgroup items, by position in wide_seq
@@ -99,7 +104,7 @@ struct Layout {
 };
 
 inline size_t plan_bytes(int S) {
-  size_t b = kHdrInts * 4 + (size_t)(7 * S + 3) * 4;
+  size_t b = kHdrInts * 4 + (size_t)(10 * S + 4) * 4;
   return (b + 255) & ~(size_t)255;
 }
 
@@ -122,6 +127,8 @@ inline Layout make_layout(void* ws, size_t bytes, int S, int D) {
   L.wide_off = L.split_base + S;
   L.cmb_seq = L.wide_off + S + 1;
   L.wide_seq = L.cmb_seq + S;
+  L.tail_seq = L.wide_seq + S;
+  L.tail_off = L.tail_seq + S;
   const size_t pb = plan_bytes(S);
   // descriptors, 8-byte (m, l) pairs and a [rows, D] float array, each
   // 256-byte aligned
@@ -388,15 +395,17 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     int32_t* __restrict__ hdr, int32_t* __restrict__ gen_off,
     int32_t* __restrict__ tile_off, int32_t* __restrict__ nparts,
     int32_t* __restrict__ split_base, int32_t* __restrict__ wide_off,
-    int32_t* __restrict__ cmb_seq, int32_t* __restrict__ wide_seq, int4* __restrict__ desc,
+    int32_t* __restrict__ cmb_seq, int32_t* __restrict__ wide_seq,
+    int32_t* __restrict__ tail_seq, int32_t* __restrict__ tail_off, int4* __restrict__ desc,
     float2* __restrict__ ml) {
   constexpr int kWaves = kPlanThreads / 64;
   __shared__ unsigned long long red0[kWaves][2], red1[2][kWaves][1];
-  __shared__ int hist[kTailBuckets], whist[kTailBuckets];
+  __shared__ int hist[kTailBuckets], whist[kTailBuckets], thist[kTailBuckets];
   const int t = threadIdx.x;
   const PlanChunk<kCached> ch(qsl, seq_lens, S);
 #pragma unroll
-  for (int k = 0; k < kPlanBuckets; ++k) hist[t * kPlanBuckets + k] = 0, whist[t * kPlanBuckets + k] = 0;
+  for (int k = 0; k < kPlanBuckets; ++k)
+    hist[t * kPlanBuckets + k] = 0, whist[t * kPlanBuckets + k] = 0, thist[t * kPlanBuckets + k] = 0;
   // 0. range length from the decode tokens and the target item count; the
   // same for the partition length of the splittable multi-query sequences
   // (at most kSplitMaxQ queries), counted in (KV head, 64-row block) units
@@ -443,36 +452,58 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
   auto wide_key = [&](int c, bool wd) {
     return wd ? kTailBuckets - 2 - min(kTailBuckets - 2, cdiv(c, kTileKeys) - 1) : kTailBuckets - 1;
   };
-  int64_t f = 0, g = 0, r = 0, x = 0, tl = 0, wd = 0, cm = 0;
+  // 16-row tile items come from two lists. bf16 items (HBM-bound, long
+  // partitions): the first holds those of every partition but a sequence's
+  // last (each P keys long), in sequence order; the second the last
+  // partitions' items, sequences ordered by that partition's length in 64-key
+  // tiles, descending (sequences without such items in the last bucket), so
+  // that a launch ends on its shortest items. fp32 items (short contexts,
+  // tiny items): the first list holds them all, in sequence order.
+  auto split_items = [&](const SeqWork& w) -> int64_t {
+    return !wide ? w.tile : w.tile > 0 ? w.tile / w.np * (w.np - 1) : 0;
+  };
+  auto last_key = [&](int c, const SeqWork& w) {
+    if (w.tile == 0 || !wide) return kTailBuckets - 1;
+    const int64_t last = (int64_t)c - (int64_t)(w.np - 1) * P;  // 1 .. P keys (all of c unsplit)
+    return kTailBuckets - 2 - (int)min<int64_t>(kTailBuckets - 2, cdiv64(last, kTileKeys) - 1);
+  };
+  int64_t f = 0, g = 0, r = 0, x = 0, xs = 0, tl = 0, wd = 0, cm = 0;
   ch.each(qsl, seq_lens, [&](int, int q, int c) {
     const SeqWork w = seq_work(q, c, P, R, H, Hkv, fast, tile, wide);
     f += w.full, g += w.gen, r += w.rows, x += w.tile, tl += w.tail, wd += w.wide;
+    xs += split_items(w);
     cm += w.np > 1 && !is_bw(q, c, fast);
     if (w.tail) {  // contexts are often alike: the wavefront's first key aggregated
       const int key = tail_key(c);
       bucket_add<false>(hist, key, __builtin_amdgcn_readfirstlane(key));
     }
     bucket_add<false>(whist, wide_key(c, w.wide > 0), kTailBuckets - 1);
+    if (wide) bucket_add<false>(thist, last_key(c, w), kTailBuckets - 1);
   });
   __syncthreads();
   // the thread's buckets: their counts, summed, join the same scan as the
   // per-sequence counts; the starts within the thread's buckets follow
-  int hb[kPlanBuckets], wb[kPlanBuckets], hsum = 0, wsum = 0;
+  int hb[kPlanBuckets], wb[kPlanBuckets], lb[kPlanBuckets], hsum = 0, wsum = 0, lsum = 0;
 #pragma unroll
   for (int k = 0; k < kPlanBuckets; ++k) {
-    hb[k] = hsum, wb[k] = wsum;
+    hb[k] = hsum, wb[k] = wsum, lb[k] = lsum;
     hsum += hist[t * kPlanBuckets + k], wsum += whist[t * kPlanBuckets + k];
+    lsum += thist[t * kPlanBuckets + k];
   }
-  int sc[9] = {(int)f, (int)g, (int)r, (int)x, (int)tl, (int)wd, (int)cm, hsum, wsum}, tot[9];
+  int sc[11] = {(int)f,  (int)g,    (int)r, (int)xs,  (int)tl, (int)wd,
+                (int)cm, hsum,      wsum,   (int)x,   lsum},
+      tot[11];
   block_exclusive_scan(sc, tot);
   int64_t fo = sc[0], go = sc[1], ro = sc[2], xo = sc[3], wo = sc[5], co = sc[6];
-  const int64_t tf = tot[0], tg = tot[1], tr = tot[2], tx = tot[3], ttl = tot[4], twd = tot[5],
-                tcm = tot[6];
+  const int64_t tf = tot[0], tg = tot[1], tr = tot[2], txs = tot[3], ttl = tot[4], twd = tot[5],
+                tcm = tot[6], tx = tot[9];
   // bucket starts (block_exclusive_scan ends on a barrier: the counts above
   // have been read by every thread)
 #pragma unroll
-  for (int k = 0; k < kPlanBuckets; ++k)
+  for (int k = 0; k < kPlanBuckets; ++k) {
     hist[t * kPlanBuckets + k] = sc[7] + hb[k], whist[t * kPlanBuckets + k] = sc[8] + wb[k];
+    thist[t * kPlanBuckets + k] = sc[10] + lb[k];
+  }
   __syncthreads();
   ch.each(qsl, seq_lens, [&](int i, int q, int c) {
     const SeqWork w = seq_work(q, c, P, R, H, Hkv, fast, tile, wide);
@@ -481,6 +512,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     gen_off[i] = (int32_t)go;
     tile_off[i] = (int32_t)xo;
     wide_seq[bucket_add<true>(whist, wide_key(c, w.wide > 0), kTailBuckets - 1)] = i;
+    if (wide) tail_seq[bucket_add<true>(thist, last_key(c, w), kTailBuckets - 1)] = i;
     nparts[i] = w.np;
     split_base[i] = w.np > 1 ? (int32_t)ro : -1;
     if (w.tail) {
@@ -492,7 +524,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     if (w.np > 1 && is_bw(q, c, fast))  // arrival counters start at 0
       for (int k = 0; k < Hkv; ++k)
         reinterpret_cast<int32_t*>(ml + ro + (int64_t)H * w.np + k)[0] = 0;
-    fo += w.full, go += w.gen, ro += w.rows, xo += w.tile;
+    fo += w.full, go += w.gen, ro += w.rows, xo += split_items(w);
   });
   // 32-row item offsets in wide_seq order (every thread reads the positions of
   // its chunk, written above by any thread of the workgroup)
@@ -513,9 +545,28 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
       wo += wide_items(wide_seq[p]);
     }
   }
+  // the second list's 16-row item offsets in tail_seq order
+  if (!wide || tx == 0) {  // none (wide and tx are the same in every thread)
+    for (int p = ch.s0; p < ch.s1; ++p) tail_off[p] = 0;
+  } else {
+    auto last_items = [&](int i) {
+      const SeqWork w = seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, R, H, Hkv, fast, tile, wide);
+      return w.tile - split_items(w);
+    };
+    int64_t mine = 0;
+    for (int p = ch.s0; p < ch.s1; ++p) mine += last_items(tail_seq[p]);
+    int ls[1] = {(int)mine}, ltot[1];
+    block_exclusive_scan(ls, ltot);
+    int64_t lo = ls[0];
+    for (int p = ch.s0; p < ch.s1; ++p) {
+      tail_off[p] = (int32_t)lo;
+      lo += last_items(tail_seq[p]);
+    }
+  }
   if (t == 0) {
     gen_off[S] = (int32_t)tg;
-    tile_off[S] = (int32_t)tx;
+    tile_off[S] = (int32_t)txs;
+    tail_off[S] = (int32_t)(tx - txs);
     wide_off[S] = (int32_t)twd;
     hdr[0] = (int32_t)((tf + ttl) * Hkv);
     hdr[1] = (int32_t)tg;
@@ -842,17 +893,35 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int pa
   const int64_t head_stride = kv_hm ? (int64_t)D << bs_log2 : D;
 
   {
-    const int pos = wave_upper_bound_le(item_off, S + 1, it);
-    const int i = kW ? item_seq[pos] : pos;
-    const int q_len = qsl[i + 1] - qsl[i];
+    // the item's sequence i, context partition, KV head and row block: 32-row
+    // items by the sequence's position in item_seq (item_off in that order);
+    // 16-row items from a first list, item_off (sequence order, item_off[S]
+    // items): partitions 0 .. ns - 1 of sequence i, for ns its items there
+    // over its KV heads and row blocks (every partition, or all but the
+    // last), then from a second list in the order of item_seq (tail_seq),
+    // whose offsets follow it: the last partitions
+    int i, part, kvh, rb_local, q_len;
+    const bool first = !kW && it < item_off[S];
+    if (kW || !first) {
+      const int32_t* off = kW ? item_off : item_seq + S;
+      const int t = kW ? it : it - item_off[S];
+      const int pos = wave_upper_bound_le(off, S + 1, t);
+      i = item_seq[pos];
+      q_len = qsl[i + 1] - qsl[i];
+      const int local = t - off[pos];
+      part = kW ? 0 : nparts[i] - 1, kvh = local % Hkv, rb_local = local / Hkv;
+    } else {
+      i = wave_upper_bound_le(item_off, S + 1, it);
+      q_len = qsl[i + 1] - qsl[i];
+      const int local = it - item_off[i];
+      const int ns = (item_off[i + 1] - item_off[i]) / (Hkv * cdiv(q_len * rep, kItemRows));
+      part = local % ns, kvh = (local / ns) % Hkv, rb_local = (local / ns) / Hkv;
+    }
     const int ctx = seq_lens[i];
     const int np = kW ? 1 : nparts[i];
-    const int local = it - item_off[pos];
-    const int part = local % np;
-    const int kvh = (local / np) % Hkv;
     const int nrows = q_len * rep;
     const bool stream_kv = nrows <= kRows;  // no other pass or row block reads this K / V
-    const int rb = kW ? cdiv(nrows, kItemRows) - 1 - local / Hkv : (local / np) / Hkv;
+    const int rb = kW ? cdiv(nrows, kItemRows) - 1 - rb_local : rb_local;
     const int rbase = rb * kItemRows + pass * kRows;  // the pass's first row
     if (rbase >= nrows) return;
     const int kbeg = np > 1 ? part * P : 0;
@@ -2158,7 +2227,8 @@ constexpr int kStepTileFirst = 2;  // one in this many workgroups starts on the 
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 attend_step_bf16_kernel(VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hdr,
                         const int32_t* __restrict__ wide_off, const int32_t* __restrict__ wide_seq,
-                        const int32_t* __restrict__ tile_off, int32_t* counters, int always) {
+                        const int32_t* __restrict__ tile_off, const int32_t* __restrict__ tail_seq,
+                        int32_t* counters, int always) {
   __shared__ __align__(16) unsigned char smem[kStepLds];
   __shared__ int claim_lds;
   auto& tl32 = *reinterpret_cast<TileLds<uint16_t, kFD, 32>*>(smem);
@@ -2204,7 +2274,7 @@ attend_step_bf16_kernel(VL_ATTN_PARAMS(uint16_t), const int32_t* __restrict__ hd
         tile_body<uint16_t, kFD, 32, true>(tl32, it % n_wide, it / n_wide, P, wide_off, wide_seq,
                                            VL_ATTN_ARGS);
       else
-        tile_body<uint16_t, kFD, 16, true>(tl16, it - 2 * n_wide, 0, P, tile_off, nullptr,
+        tile_body<uint16_t, kFD, 16, true>(tl16, it - 2 * n_wide, 0, P, tile_off, tail_seq,
                                            VL_ATTN_ARGS);
       __syncthreads();  // the item is done with the LDS; claim_lds has been read
       if (threadIdx.x == 0) claim_lds = nxt;
@@ -2425,7 +2495,7 @@ int do_plan(const Args& a, void* ws, size_t ws_bytes, hipStream_t st) {
   plan<<<1, kPlanThreads, 0, st>>>(a.seq_lens, a.qsl, a.S, a.H, a.Hkv, fast, tile, wide,
                                    L.cap_rows, target_items, tile_target, L.hdr, L.gen_off,
                                    L.tile_off, L.nparts, L.split_base, L.wide_off, L.cmb_seq,
-                                   L.wide_seq, L.desc, L.ml);
+                                   L.wide_seq, L.tail_seq, L.tail_off, L.desc, L.ml);
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
@@ -2467,7 +2537,7 @@ int launch_tile_d(const Args& a, const Layout& L, float sl2, hipStream_t st) {
   attend_tile_kernel<T, D, RW, kWv, TKV><<<tile_launch_grid<T, D, RW, kWv, TKV>(), 64 * kWv, 0,
                                            st>>>(
       VL_ATTN_LAUNCH_ARGS_KV(T, TKV), L.hdr, RW == 32 ? L.wide_off : L.tile_off,
-      RW == 32 ? L.wide_seq : nullptr, L.hdr + (RW == 32 ? 34 : 26));
+      RW == 32 ? L.wide_seq : L.tail_seq, L.hdr + (RW == 32 ? 34 : 26));
   VL_CHECK_LAUNCH();
   return VL_OK;
 }
@@ -2592,7 +2662,7 @@ int do_run(const Args& a, int max_q, int min_q, int max_ctx, void* ws, size_t ws
     if (!known || min_q == 1) {
       attend_step_bf16_kernel<<<step_grid(), 256, 0, st>>>(VL_ATTN_LAUNCH_ARGS(uint16_t), L.hdr,
                                                            L.wide_off, L.wide_seq, L.tile_off,
-                                                           L.hdr + 16, step_all ? 1 : 0);
+                                                           L.tail_seq, L.hdr + 16, step_all ? 1 : 0);
       VL_CHECK_LAUNCH();
     }
     if (!step_all && !(known && min_q == 1)) {
