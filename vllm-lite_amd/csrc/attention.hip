@@ -285,6 +285,7 @@ constexpr int kRangeMax = 2048;       // longest decode range the planner starts
 constexpr int kItemsPerWg = 4;  // decode items aimed for per resident workgroup
 constexpr int kTileItemsPerWg = 4;  // split tile items aimed for per workgroup
 constexpr int kTailBuckets = 1024;
+constexpr int kPlanLdsSeqs = 2048;  // batches the plan keeps per-sequence counts of in LDS
 constexpr int kPlanBuckets = kTailBuckets / kPlanThreads;  // buckets owned by each plan thread
 constexpr int kPlanRegSeqs = 4;  // sequences a plan thread keeps in registers (S <= 1024)
 static_assert(kTailBuckets % kPlanThreads == 0, "whole tail buckets per plan thread");
@@ -401,6 +402,10 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
   constexpr int kWaves = kPlanThreads / 64;
   __shared__ unsigned long long red0[kWaves][2], red1[2][kWaves][1];
   __shared__ int hist[kTailBuckets], whist[kTailBuckets], thist[kTailBuckets];
+  // with at most kPlanLdsSeqs sequences, the item counts of the 32-row list
+  // and of the second 16-row list by position, so that their offsets need no
+  // global reads
+  __shared__ int wcnt[kPlanLdsSeqs], tcnt[kPlanLdsSeqs];
   const int t = threadIdx.x;
   const PlanChunk<kCached> ch(qsl, seq_lens, S);
 #pragma unroll
@@ -410,6 +415,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
   // same for the partition length of the splittable multi-query sequences
   // (at most kSplitMaxQ queries), counted in (KV head, 64-row block) units
   int R = 64, P = kPart0;
+  bool lpt;  // the 16-row items in two lists, the last partitions longest first
   {
     const int rep = H / Hkv;
     unsigned long long v[2] = {0, 0};
@@ -426,6 +432,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     while (P < (1 << 20) && v[1] * (unsigned long long)Hkv >
                                 (unsigned long long)max(tile_target, 1) * (unsigned long long)P)
       P *= 2;
+    lpt = wide && v[1] > 0;  // bf16 16-row items (short queries over split contexts)
   }
   // 1. double P and R until the split partials fit (every thread holds the
   // same sums, so all take the same branch)
@@ -452,18 +459,19 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
   auto wide_key = [&](int c, bool wd) {
     return wd ? kTailBuckets - 2 - min(kTailBuckets - 2, cdiv(c, kTileKeys) - 1) : kTailBuckets - 1;
   };
-  // 16-row tile items come from two lists. bf16 items (HBM-bound, long
-  // partitions): the first holds those of every partition but a sequence's
-  // last (each P keys long), in sequence order; the second the last
-  // partitions' items, sequences ordered by that partition's length in 64-key
-  // tiles, descending (sequences without such items in the last bucket), so
-  // that a launch ends on its shortest items. fp32 items (short contexts,
-  // tiny items): the first list holds them all, in sequence order.
+  // 16-row tile items come from two lists. bf16 items over split contexts
+  // (lpt: HBM-bound, partitions of up to P keys): the first holds those of
+  // every partition but a sequence's last (each P keys long), in sequence
+  // order; the second the last partitions' items, sequences ordered by that
+  // partition's length in 64-key tiles, descending (sequences without such
+  // items in the last bucket), so that a launch ends on its shortest items.
+  // Otherwise (fp32 items: short contexts, tiny items) the first list holds
+  // them all, in sequence order.
   auto split_items = [&](const SeqWork& w) -> int64_t {
-    return !wide ? w.tile : w.tile > 0 ? w.tile / w.np * (w.np - 1) : 0;
+    return !lpt ? w.tile : w.tile > 0 ? w.tile / w.np * (w.np - 1) : 0;
   };
   auto last_key = [&](int c, const SeqWork& w) {
-    if (w.tile == 0 || !wide) return kTailBuckets - 1;
+    if (w.tile == 0 || !lpt) return kTailBuckets - 1;
     const int64_t last = (int64_t)c - (int64_t)(w.np - 1) * P;  // 1 .. P keys (all of c unsplit)
     return kTailBuckets - 2 - (int)min<int64_t>(kTailBuckets - 2, cdiv64(last, kTileKeys) - 1);
   };
@@ -478,7 +486,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
       bucket_add<false>(hist, key, __builtin_amdgcn_readfirstlane(key));
     }
     bucket_add<false>(whist, wide_key(c, w.wide > 0), kTailBuckets - 1);
-    if (wide) bucket_add<false>(thist, last_key(c, w), kTailBuckets - 1);
+    if (lpt) bucket_add<false>(thist, last_key(c, w), kTailBuckets - 1);
   });
   __syncthreads();
   // the thread's buckets: their counts, summed, join the same scan as the
@@ -494,7 +502,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
                 (int)cm, hsum,      wsum,   (int)x,   lsum},
       tot[11];
   block_exclusive_scan(sc, tot);
-  int64_t fo = sc[0], go = sc[1], ro = sc[2], xo = sc[3], wo = sc[5], co = sc[6];
+  int64_t fo = sc[0], go = sc[1], ro = sc[2], xo = sc[3], co = sc[6];
   const int64_t tf = tot[0], tg = tot[1], tr = tot[2], txs = tot[3], ttl = tot[4], twd = tot[5],
                 tcm = tot[6], tx = tot[9];
   // bucket starts (block_exclusive_scan ends on a barrier: the counts above
@@ -511,8 +519,16 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     for (int k = 0; k < w.full; ++k) desc[fo + k] = make_int4(i, k, c, qs);
     gen_off[i] = (int32_t)go;
     tile_off[i] = (int32_t)xo;
-    wide_seq[bucket_add<true>(whist, wide_key(c, w.wide > 0), kTailBuckets - 1)] = i;
-    if (wide) tail_seq[bucket_add<true>(thist, last_key(c, w), kTailBuckets - 1)] = i;
+    {
+      const int p = bucket_add<true>(whist, wide_key(c, w.wide > 0), kTailBuckets - 1);
+      wide_seq[p] = i;
+      if (S <= kPlanLdsSeqs) wcnt[p] = (int)w.wide;
+    }
+    if (lpt) {
+      const int p = bucket_add<true>(thist, last_key(c, w), kTailBuckets - 1);
+      tail_seq[p] = i;
+      if (S <= kPlanLdsSeqs) tcnt[p] = (int)(w.tile - split_items(w));
+    }
     nparts[i] = w.np;
     split_base[i] = w.np > 1 ? (int32_t)ro : -1;
     if (w.tail) {
@@ -526,41 +542,36 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
         reinterpret_cast<int32_t*>(ml + ro + (int64_t)H * w.np + k)[0] = 0;
     fo += w.full, go += w.gen, ro += w.rows, xo += split_items(w);
   });
-  // 32-row item offsets in wide_seq order (every thread reads the positions of
-  // its chunk, written above by any thread of the workgroup)
+  // 32-row item offsets in wide_seq order and the second 16-row list's in
+  // tail_seq order (every thread reads the positions of its chunk, written
+  // above by any thread of the workgroup)
   __syncthreads();
-  if (twd == 0) {  // no 32-row items (twd is the same in every thread)
-    for (int p = ch.s0; p < ch.s1; ++p) wide_off[p] = 0;
-  } else {
-    auto wide_items = [&](int i) {
+  {
+    const bool do_w = twd > 0, do_t = lpt && tx > 0;  // the same in every thread
+    auto wide_items = [&](int p) -> int64_t {
+      if (S <= kPlanLdsSeqs) return wcnt[p];
+      const int i = wide_seq[p];
       return seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, R, H, Hkv, fast, tile, wide).wide;
     };
-    int64_t mine = 0;
-    for (int p = ch.s0; p < ch.s1; ++p) mine += wide_items(wide_seq[p]);
-    int ws[1] = {(int)mine}, wtot[1];
-    block_exclusive_scan(ws, wtot);
-    wo = ws[0];
-    for (int p = ch.s0; p < ch.s1; ++p) {
-      wide_off[p] = (int32_t)wo;
-      wo += wide_items(wide_seq[p]);
-    }
-  }
-  // the second list's 16-row item offsets in tail_seq order
-  if (!wide || tx == 0) {  // none (wide and tx are the same in every thread)
-    for (int p = ch.s0; p < ch.s1; ++p) tail_off[p] = 0;
-  } else {
-    auto last_items = [&](int i) {
+    auto last_items = [&](int p) -> int64_t {
+      if (S <= kPlanLdsSeqs) return tcnt[p];
+      const int i = tail_seq[p];
       const SeqWork w = seq_work(qsl[i + 1] - qsl[i], seq_lens[i], P, R, H, Hkv, fast, tile, wide);
       return w.tile - split_items(w);
     };
-    int64_t mine = 0;
-    for (int p = ch.s0; p < ch.s1; ++p) mine += last_items(tail_seq[p]);
-    int ls[1] = {(int)mine}, ltot[1];
-    block_exclusive_scan(ls, ltot);
-    int64_t lo = ls[0];
+    int64_t mw = 0, mt = 0;
     for (int p = ch.s0; p < ch.s1; ++p) {
-      tail_off[p] = (int32_t)lo;
-      lo += last_items(tail_seq[p]);
+      if (do_w) mw += wide_items(p);
+      if (do_t) mt += last_items(p);
+    }
+    int v2[2] = {(int)mw, (int)mt}, tot2[2];
+    if (do_w || do_t) block_exclusive_scan(v2, tot2);
+    int64_t a = v2[0], b = v2[1];
+    for (int p = ch.s0; p < ch.s1; ++p) {
+      wide_off[p] = do_w ? (int32_t)a : 0;
+      tail_off[p] = do_t ? (int32_t)b : 0;
+      if (do_w) a += wide_items(p);
+      if (do_t) b += last_items(p);
     }
   }
   if (t == 0) {
