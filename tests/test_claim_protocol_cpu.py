@@ -1,5 +1,6 @@
-"""A CPU replay of the work-claiming protocol of the persistent attention
-kernels (attend_step_bf16_kernel and leave_and_reset, csrc/attention.hip):
+"""A CPU replay of the work-claiming protocols of the persistent attention
+kernels (attend_step_bf16_kernel with leave_and_reset, and attend_tile_kernel
+with its last-claim reset, csrc/attention.hip):
 workgroups as coroutines that interleave their atomic operations in random
 orders. Each kernel's counters are touched only by atomic operations on
 single words, so any interleaving of those operations is a possible
@@ -10,7 +11,9 @@ launches of different shapes:
     past its queue's length reaches an item body (the bodies index the plan's
     arrays with it);
   * the counters are all zero again when a launch ends (the last workgroup to
-    leave resets them), so the next launch starts from zero without a memset.
+    leave resets them; in the tile kernel, the claim that returns the
+    queue's last value), so the next launch starts from zero without a
+    memset.
 """
 
 import random
@@ -94,3 +97,45 @@ def test_a_launch_without_its_reset_would_skip_items():
     ran = run_launch(rng, 8, 10, 0, ctr)
     dec = sorted(it for d, it in ran if d)
     assert dec == list(range(3, 10))
+
+
+def tile_workgroup(b, grid, n_items, ctr, ran):
+    """attend_tile_kernel's claim loop for workgroup b: queue x = b % 8 holds
+    items x, x + 8, ... below n_items; workgroup b starts on item
+    (b // 8) * 8 + x, claims the next before running the current one, and the
+    claimer whose claim returns the queue's last value (its item count - 1)
+    zeroes the queue's counter. Yields at every atomic operation."""
+    xcd = b % XCDS
+    per_queue = (grid + XCDS - 1 - xcd) // XCDS
+    n_q = (n_items - xcd + XCDS - 1) // XCDS if n_items > xcd else 0
+    it = (b // XCDS) * XCDS + xcd
+    while it < n_items:
+        yield
+        c = ctr[xcd]
+        ctr[xcd] += 1  # atomicAdd
+        if c == n_q - 1:
+            yield
+            ctr[xcd] = 0  # atomic store
+        c64 = per_queue + c
+        nxt = n_items if c64 < 0 or c64 * XCDS + xcd >= n_items else c64 * XCDS + xcd
+        assert 0 <= it < n_items
+        ran.append(it)
+        it = nxt
+
+
+def test_tile_queues_run_every_item_once_and_reset_on_the_last_claim():
+    rng = random.Random(2)
+    ctr = [0] * XCDS
+    for trial in range(400):
+        grid = rng.choice([8, 9, 16, 24, 64, 96])
+        n_items = rng.choice([0, 1, 5, 8, 9, 40, 200, 777])
+        ran = []
+        live = [tile_workgroup(b, grid, n_items, ctr, ran) for b in range(grid)]
+        while live:
+            g = rng.choice(live)
+            try:
+                next(g)
+            except StopIteration:
+                live.remove(g)
+        assert sorted(ran) == list(range(n_items)), (trial, grid, n_items)
+        assert ctr == [0] * XCDS, (trial, grid, n_items, ctr)

@@ -276,8 +276,9 @@ __device__ __forceinline__ SeqWork seq_work(int q, int c, int P, int R, int H, i
   w.wide = wd ? (int64_t)Hkv * cdiv(q * (H / Hkv), kWideRows) : 0;
   w.gen = (bw || tl) ? 0 : (int64_t)max(q, 0) * H * w.np;
   // a split decode sequence also keeps one arrival counter per KV head in
-  // the rows after its partials
-  w.rows = w.np > 1 ? (int64_t)q * H * w.np + (bw ? Hkv : 0) : 0;
+  // the rows after its partials, a split 16-row tile sequence one per (KV
+  // head, row block)
+  w.rows = w.np > 1 ? (int64_t)q * H * w.np + (bw ? Hkv : w.tile > 0 ? w.tile / w.np : 0) : 0;
   return w;
 }
 
@@ -480,7 +481,7 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
     const SeqWork w = seq_work(q, c, P, R, H, Hkv, fast, tile, wide);
     f += w.full, g += w.gen, r += w.rows, x += w.tile, tl += w.tail, wd += w.wide;
     xs += split_items(w);
-    cm += w.np > 1 && !is_bw(q, c, fast);
+    cm += w.np > 1 && w.gen > 0;  // the combine kernel merges only the generic kernel's splits
     if (w.tail) {  // contexts are often alike: the wavefront's first key aggregated
       const int key = tail_key(c);
       bucket_add<false>(hist, key, __builtin_amdgcn_readfirstlane(key));
@@ -536,10 +537,10 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(
       desc[tf + bucket_add<true>(hist, key, __builtin_amdgcn_readfirstlane(key))] =
           make_int4(i, c / R, c, qs);
     }
-    if (w.np > 1 && !is_bw(q, c, fast)) cmb_seq[co++] = i;
-    if (w.np > 1 && is_bw(q, c, fast))  // arrival counters start at 0
-      for (int k = 0; k < Hkv; ++k)
-        reinterpret_cast<int32_t*>(ml + ro + (int64_t)H * w.np + k)[0] = 0;
+    if (w.np > 1 && w.gen > 0) cmb_seq[co++] = i;
+    if (w.np > 1 && w.gen == 0)  // arrival counters start at 0
+      for (int64_t k = (int64_t)q * H * w.np; k < w.rows; ++k)
+        reinterpret_cast<int32_t*>(ml + ro + k)[0] = 0;
     fo += w.full, go += w.gen, ro += w.rows, xo += split_items(w);
   });
   // 32-row item offsets in wide_seq order and the second 16-row list's in
@@ -772,8 +773,9 @@ __device__ __forceinline__ uint4 load16_kv(const void* p) {
 // over all 64 banks.
 template <typename T, int D, int RW>
 struct TileLds;
+// (16-byte aligned: the K rows are read 16 bytes at a time)
 template <int D, int RW>
-struct TileLds<uint16_t, D, RW> {
+struct alignas(16) TileLds<uint16_t, D, RW> {
   static constexpr int kRow = D + 8;  // K row stride (bf16), 16-byte aligned
   // V rows as in the cache (key-major), read transposed by ds_read_b64_tr_b16:
   // a PV operand read takes 8 bytes of each of 4 (RW 16: 8) keys per 16 dims,
@@ -784,6 +786,7 @@ struct TileLds<uint16_t, D, RW> {
   static constexpr int kUnits = kTileKeys * kChunks / 256;
   uint16_t k[kTileKeys * kRow];
   uint16_t v[kTileKeys * vRow];
+  int last;  // the item's workgroup arrived last among its row block's partitions
 };
 
 // 4 bf16 of a PV operand from LDS by the transposing read: lane i of each
@@ -796,7 +799,7 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
   return __builtin_bit_cast(uint2, r);
 }
 template <int D, int RW>
-struct TileLds<float, D, RW> {
+struct alignas(16) TileLds<float, D, RW> {
   static constexpr int kRow = D + 1;
   static constexpr int vRow = D + 1;
   static constexpr int kChunks = D / 4;        // float4 chunks per head row
@@ -804,6 +807,7 @@ struct TileLds<float, D, RW> {
   static constexpr int vUnits = 0;             // V goes with K (same key, chunk)
   float k[kTileKeys * kRow];
   float v[kTileKeys * vRow];
+  int last;  // the item's workgroup arrived last among its row block's partitions
 };
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
@@ -849,6 +853,144 @@ __device__ __forceinline__ int item_tid() {
   out, query, q_stride, kc, vc, bt, bt_stride, seq_lens, qsl, S, H, Hkv, bs_log2, kv_hm,      \
       scale_log2, desc, nparts, split_base, ml, po
 
+
+// Two floats as one 64-bit word (for 8-byte device-scope stores and loads).
+__device__ __forceinline__ uint64_t pack2(float lo, float hi) {
+  return (uint64_t)__float_as_uint(lo) | ((uint64_t)__float_as_uint(hi) << 32);
+}
+__device__ __forceinline__ float lo_f(uint64_t w) { return __uint_as_float((uint32_t)w); }
+__device__ __forceinline__ float hi_f(uint64_t w) { return __uint_as_float((uint32_t)(w >> 32)); }
+
+// One output row's merge of np partitions written by other workgroups
+// (device-scope loads): lane p holds partition p's (max, sum) and weight, 64
+// partitions at a time; every lane sums its two dims over the partitions with
+// the weights read lane by lane, four partitions' loads in flight (relaxed
+// atomic loads are not batched by the compiler unless written out).
+// xrow: the lane's dims of partition 0; xstride: 8-byte words between
+// partitions. Returns the normalised pair.
+__device__ __forceinline__ float2 merge_partitions(const uint64_t* mlw, const uint64_t* xrow,
+                                                   int64_t xstride, int np, int lane) {
+  auto ld = [](const uint64_t* a) {
+    return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  float M = -__builtin_inff();
+  for (int p = lane; p < np; p += 64) M = fmaxf(M, lo_f(ld(mlw + p)));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+  float L = 0.f, a0 = 0.f, a1 = 0.f;
+  for (int p0 = 0; p0 < np; p0 += 64) {
+    float wgt = 0.f;
+    if (p0 + lane < np) {
+      const uint64_t v = ld(mlw + p0 + lane);
+      wgt = lo_f(v) == -__builtin_inff() ? 0.f : exp2_fast(lo_f(v) - M);
+      L += hi_f(v) * wgt;
+    }
+    auto wt = [&](int u) {
+      return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), u));
+    };
+    const int cnt = min(64, np - p0);
+    const uint64_t* src = xrow + (int64_t)p0 * xstride;
+    int u = 0;
+    for (; u + 4 <= cnt; u += 4) {
+      const uint64_t x0 = ld(src + (int64_t)u * xstride);
+      const uint64_t x1 = ld(src + (int64_t)(u + 1) * xstride);
+      const uint64_t x2 = ld(src + (int64_t)(u + 2) * xstride);
+      const uint64_t x3 = ld(src + (int64_t)(u + 3) * xstride);
+      a0 += lo_f(x0) * wt(u), a1 += hi_f(x0) * wt(u);
+      a0 += lo_f(x1) * wt(u + 1), a1 += hi_f(x1) * wt(u + 1);
+      a0 += lo_f(x2) * wt(u + 2), a1 += hi_f(x2) * wt(u + 2);
+      a0 += lo_f(x3) * wt(u + 3), a1 += hi_f(x3) * wt(u + 3);
+    }
+    for (; u < cnt; ++u) {
+      const uint64_t x = ld(src + (int64_t)u * xstride);
+      a0 += lo_f(x) * wt(u), a1 += hi_f(x) * wt(u);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  return make_float2(a0 * inv, a1 * inv);
+}
+
+// The merged output rows r_begin .. r_end - 1 of one (sequence, KV head)
+// row block (row r: query r / rep, head kvh rep + r % rep; the sequence's
+// first token tok0) from its np partitions' device-scope partials at
+// base: wavefront w takes rows r_begin + w, r_begin + w + kWv, ... in groups
+// of kMergeRows, lane l dims 2l and 2l + 1, with every load of a group issued
+// before the first sum (np <= kMergeFew; longer splits row by row). Groups of
+// 5 rows take a spec-verify row block (5 queries x 4 heads) in one round on 4
+// wavefronts; kernels whose item body needs fewer registers use groups of 2,
+// so that the merge does not raise their register count.
+constexpr int kMergeFew = 8;
+template <typename T, int D, int kWv, int kMergeRows>
+__device__ __forceinline__ void merge_tile_rows(T* __restrict__ out, int H, int rep, int kvh,
+                                                int r_begin, int r_end, int tok0, int np,
+                                                int64_t base, const float2* ml, const float* po,
+                                                int wave, int lane) {
+  static_assert(D % 2 == 0 && D <= 128, "dim pairs per lane");
+  const bool pair_ok = 2 * lane < D;
+  const int dp = pair_ok ? lane : 0;  // lanes past the row read pair 0 and store nothing
+  auto ld = [](const uint64_t* a) {
+    return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  auto row_at = [&](int r) {  // the row's first partial row
+    const int j = r / rep;
+    return base + (int64_t)(j * H + kvh * rep + (r - j * rep)) * np;
+  };
+  auto store = [&](int r, float o0, float o1) {
+    const int j = r / rep;
+    T* dst = out + ((int64_t)(tok0 + j) * H + kvh * rep + (r - j * rep)) * D + 2 * lane;
+    if (!pair_ok) return;
+    if constexpr (sizeof(T) == 2)
+      *reinterpret_cast<uint32_t*>(dst) = cvt_pk_bf16(o0, o1);
+    else
+      *reinterpret_cast<float2*>(dst) = make_float2(o0, o1);
+  };
+  if (np > kMergeFew) {
+    for (int r = r_begin + wave; r < r_end; r += kWv) {
+      const int64_t rb = row_at(r);
+      const float2 o = merge_partitions(reinterpret_cast<const uint64_t*>(ml + rb),
+                                        reinterpret_cast<const uint64_t*>(po + rb * D) + dp, D / 2,
+                                        np, lane);
+      store(r, o.x, o.y);
+    }
+    return;
+  }
+  for (int r0 = r_begin + wave; r0 < r_end; r0 += kWv * kMergeRows) {
+    uint64_t mv[kMergeRows], xv[kMergeRows][kMergeFew];
+#pragma unroll
+    for (int g = 0; g < kMergeRows; ++g) {
+      const int64_t rb = row_at(min(r0 + kWv * g, r_end - 1));
+      mv[g] = ld(reinterpret_cast<const uint64_t*>(ml + rb) + min(lane, np - 1));
+#pragma unroll
+      for (int u = 0; u < kMergeFew; ++u)
+        xv[g][u] = ld(reinterpret_cast<const uint64_t*>(po + (rb + min(u, np - 1)) * D) + dp);
+    }
+#pragma unroll
+    for (int g = 0; g < kMergeRows; ++g) {
+      const int r = r0 + kWv * g;
+      if (r >= r_end) break;  // uniform over the wavefront
+      const float m = lo_f(mv[g]);
+      float M = lane < np ? m : -__builtin_inff();
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+      const float wgt = lane < np && m != -__builtin_inff() ? exp2_fast(m - M) : 0.f;
+      float L = lane < np ? hi_f(mv[g]) * wgt : 0.f;
+      float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+      for (int u = 0; u < kMergeFew; ++u) {
+        if (u >= np) break;  // uniform
+        const float wt =
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), u));
+        a0 += lo_f(xv[g][u]) * wt, a1 += hi_f(xv[g][u]) * wt;
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      store(r, a0 * inv, a1 * inv);
+    }
+  }
+}
 
 // One workgroup item of the tile kernel (kWv wavefronts; the caller's LDS).
 // item_off holds the first item of each sequence, in sequence order, or (32-row
@@ -1335,17 +1477,48 @@ __device__ __forceinline__ void tile_body(TileLds<T, D, RW>& lds, int it, int pa
             }
           }
       } else {
+        // the partial at device scope (written through to the point of
+        // coherence of all XCDs), for the row block's last workgroup
         const int64_t prow = (int64_t)split_base[i] + (int64_t)(j * H + head) * np + part;
-        float* dst = po + prow * D;
+        uint64_t* dst = reinterpret_cast<uint64_t*>(po + prow * D);
 #pragma unroll
         for (int u = 0; u < kDT; ++u)
 #pragma unroll
           for (int b4 = 0; b4 < kCV / 4; ++b4) {
             const int d = kW ? 32 * u + 8 * b4 + 4 * grp : 16 * u + 4 * grp;
-            *reinterpret_cast<float4*>(dst + d) = make_float4(
-                acc[u][4 * b4], acc[u][4 * b4 + 1], acc[u][4 * b4 + 2], acc[u][4 * b4 + 3]);
+            __hip_atomic_store(dst + d / 2, pack2(acc[u][4 * b4], acc[u][4 * b4 + 1]),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(dst + d / 2 + 1, pack2(acc[u][4 * b4 + 2], acc[u][4 * b4 + 3]),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           }
-        if (grp == 0) ml[prow] = make_float2(m_run, l_row);
+        if (grp == 0)
+          __hip_atomic_store(reinterpret_cast<uint64_t*>(ml + prow), pack2(m_run, l_row),
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    if (np > 1) {  // uniform over the workgroup (32-row items are never split)
+      // Split rows are merged in the kernel by the last workgroup to finish a
+      // partition of the row block, as the bandwidth decode kernel merges its
+      // ranges: partial stores completed, then one device-scope arrival on
+      // the row block's counter (after the sequence's partial rows; the plan
+      // zeroes it, the last arrival resets it); the last reads every
+      // partition's partial with device-scope loads.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's stores have completed
+      __syncthreads();  // every thread's have
+      const int nrb = cdiv(nrows, kItemRows);
+      if (tid == 0) {
+        int32_t* cnt = reinterpret_cast<int32_t*>(ml + split_base[i] + (int64_t)q_len * H * np +
+                                                  kvh * nrb + rb);
+        const int prev = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lds.last = prev == np - 1;
+        if (prev == np - 1) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      if (lds.last) {
+        asm volatile("" ::: "memory");  // no load below moves above the arrival
+        merge_tile_rows<T, D, kWv, kDeep ? 5 : 2>(out, H, rep, kvh, rbase,
+                                                  min(nrows, rbase + kItemRows), qsl[i], np,
+                                                  (int64_t)split_base[i], ml, po, wave, lane);
       }
     }
   }
@@ -1400,10 +1573,21 @@ __global__ void __launch_bounds__(64 * kWv) __attribute__((amdgpu_waves_per_eu(2
   const int xcd = blockIdx.x % kXcds;
   const int per_queue = ((int)gridDim.x + kXcds - 1 - xcd) / kXcds;  // workgroups serving it
   int it = (blockIdx.x / kXcds) * kXcds + xcd;
+  // The queue's items are xcd, xcd + 8, ... below n_items (n_q of them).
+  // Every item processed makes one claim, so the claims on the queue's
+  // counter return 0 .. n_q - 1, and the one that returns n_q - 1 is the
+  // counter's last use in this run: its claimer zeroes it for the next run.
+  // (An exit count instead, every workgroup's atomic on one address at the
+  // end of the launch, cost tens of microseconds.)
+  const int n_q = n_items > xcd ? (n_items - xcd + kXcds - 1) / kXcds : 0;
   while (it < n_items) {
     int nxt = 0;
-    if (threadIdx.x == 0)
-      nxt = claimed_item(per_queue + (int64_t)atomicAdd(counters + xcd, 1), kXcds, xcd, n_items);
+    if (threadIdx.x == 0) {
+      const int c = atomicAdd(counters + xcd, 1);
+      if (c == n_q - 1)
+        __hip_atomic_store(counters + xcd, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      nxt = claimed_item(per_queue + (int64_t)c, kXcds, xcd, n_items);
+    }
     tile_body<T, D, RW, false, kWv, TKV>(lds, it, 0, P, item_off, item_seq, VL_ATTN_ARGS);
     __syncthreads();  // the item is done with the LDS; claim_lds has been read
     if (threadIdx.x == 0) claim_lds = nxt;
@@ -1426,13 +1610,6 @@ __device__ __forceinline__ float dot8(const uint4& a, const uint4& b, float c) {
                                       __builtin_bit_cast(bf16x2_t, b.w), c, false);
   return c;
 }
-
-// Two floats as one 64-bit word (for 8-byte device-scope stores and loads).
-__device__ __forceinline__ uint64_t pack2(float lo, float hi) {
-  return (uint64_t)__float_as_uint(lo) | ((uint64_t)__float_as_uint(hi) << 32);
-}
-__device__ __forceinline__ float lo_f(uint64_t w) { return __uint_as_float((uint32_t)w); }
-__device__ __forceinline__ float hi_f(uint64_t w) { return __uint_as_float((uint32_t)(w >> 32)); }
 
 // Reduce over lanes that share (lane & 3): xor 4, 8, 16, 32.
 __device__ __forceinline__ float stride4_max(float v) {
@@ -1476,57 +1653,6 @@ __device__ __forceinline__ float row_transpose_sum16(const float (&v)[16], int c
   const float lo = y[0] + VL_DPP(0.f, y[0], 0xB1, 0xF);
   const float hi = y[1] + VL_DPP(0.f, y[1], 0xB1, 0xF);
   return (c & 1) ? hi : lo;
-}
-
-// One output row's merge of np partitions written by other workgroups
-// (device-scope loads): lane p holds partition p's (max, sum) and weight, 64
-// partitions at a time; every lane sums its two dims over the partitions with
-// the weights read lane by lane, four partitions' loads in flight (relaxed
-// atomic loads are not batched by the compiler unless written out).
-// xrow: the lane's dims of partition 0; xstride: 8-byte words between
-// partitions. Returns the normalised pair.
-__device__ __forceinline__ float2 merge_partitions(const uint64_t* mlw, const uint64_t* xrow,
-                                                   int64_t xstride, int np, int lane) {
-  auto ld = [](const uint64_t* a) {
-    return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  };
-  float M = -__builtin_inff();
-  for (int p = lane; p < np; p += 64) M = fmaxf(M, lo_f(ld(mlw + p)));
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
-  float L = 0.f, a0 = 0.f, a1 = 0.f;
-  for (int p0 = 0; p0 < np; p0 += 64) {
-    float wgt = 0.f;
-    if (p0 + lane < np) {
-      const uint64_t v = ld(mlw + p0 + lane);
-      wgt = lo_f(v) == -__builtin_inff() ? 0.f : exp2_fast(lo_f(v) - M);
-      L += hi_f(v) * wgt;
-    }
-    auto wt = [&](int u) {
-      return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), u));
-    };
-    const int cnt = min(64, np - p0);
-    const uint64_t* src = xrow + (int64_t)p0 * xstride;
-    int u = 0;
-    for (; u + 4 <= cnt; u += 4) {
-      const uint64_t x0 = ld(src + (int64_t)u * xstride);
-      const uint64_t x1 = ld(src + (int64_t)(u + 1) * xstride);
-      const uint64_t x2 = ld(src + (int64_t)(u + 2) * xstride);
-      const uint64_t x3 = ld(src + (int64_t)(u + 3) * xstride);
-      a0 += lo_f(x0) * wt(u), a1 += hi_f(x0) * wt(u);
-      a0 += lo_f(x1) * wt(u + 1), a1 += hi_f(x1) * wt(u + 1);
-      a0 += lo_f(x2) * wt(u + 2), a1 += hi_f(x2) * wt(u + 2);
-      a0 += lo_f(x3) * wt(u + 3), a1 += hi_f(x3) * wt(u + 3);
-    }
-    for (; u < cnt; ++u) {
-      const uint64_t x = ld(src + (int64_t)u * xstride);
-      a0 += lo_f(x) * wt(u), a1 += hi_f(x) * wt(u);
-    }
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) L += __shfl_xor(L, o, 64);
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  return make_float2(a0 * inv, a1 * inv);
 }
 
 // One workgroup item = (decode sequence, KV head, range of the context);
@@ -2311,11 +2437,8 @@ __global__ void __launch_bounds__(256) combine_kernel(
     T* __restrict__ out, const int32_t* __restrict__ qsl, int H, int D,
     const int32_t* __restrict__ hdr, const int32_t* __restrict__ cmb_seq,
     const int32_t* __restrict__ nparts, const int32_t* __restrict__ split_base,
-    const float2* __restrict__ ml, const float* __restrict__ po, int32_t* tile_counters) {
+    const float2* __restrict__ ml, const float* __restrict__ po) {
   constexpr int kDk = kMaxHeadDim / 64;
-  // every tile launch of this run has ended: zero their queue counters for the next
-  if (blockIdx.x == 0 && threadIdx.x < 16)
-    __hip_atomic_store(tile_counters + threadIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t items = (int64_t)hdr[12] * H;
   for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
@@ -2691,12 +2814,14 @@ int do_run(const Args& a, int max_q, int min_q, int max_ctx, void* ws, size_t ws
         a.kv_layout == VL_KV_HEAD_MAJOR ? 1 : 0, sl2, L.hdr, L.gen_off,
         L.nparts, L.split_base, L.ml, L.po);
     VL_CHECK_LAUNCH();
+    // the generic kernel's split rows; the other kernels merge their own
+    // one workgroup per (split sequence, query head) item, at most S * H of them
+    const int cmb_grid =
+        (int)std::min<int64_t>((int64_t)ncu * 8, std::max<int64_t>((int64_t)a.S * a.H, 1));
+    combine_kernel<T><<<cmb_grid, 256, 0, st>>>((T*)a.out, a.qsl, a.H, a.D, L.hdr, L.cmb_seq,
+                                              L.nparts, L.split_base, L.ml, L.po);
+    VL_CHECK_LAUNCH();
   }
-  // one workgroup per (split sequence, query head) item, at most S * H of them
-  const int cmb_grid = (int)std::min<int64_t>((int64_t)ncu * 8, std::max<int64_t>((int64_t)a.S * a.H, 1));
-  combine_kernel<T><<<cmb_grid, 256, 0, st>>>((T*)a.out, a.qsl, a.H, a.D, L.hdr, L.cmb_seq,
-                                            L.nparts, L.split_base, L.ml, L.po, L.hdr + 26);
-  VL_CHECK_LAUNCH();
   return VL_OK;
 }
 
@@ -2726,7 +2851,8 @@ extern "C" size_t vl_paged_attention_workspace_size(int num_seqs, int num_tokens
   // multi-query rows split into partitions of kPart0 tokens or more (at most 64)
   const int64_t split_tokens = num_tokens < S * kSplitMaxQ ? num_tokens : S * kSplitMaxQ;
   int64_t parts = std::min<int64_t>(std::max<int64_t>(cdiv64(ctx, kPart0), 1), 64);
-  const int64_t rows_tile = parts > 1 ? split_tokens * H * parts : 0;
+  // (and a split sequence's arrival counters, at most one row per query row)
+  const int64_t rows_tile = parts > 1 ? split_tokens * H * (parts + 1) : 0;
   // decode ranges: as short as 64 tokens for small batches, at most a few
   // items per resident workgroup (plus one short range per sequence) and at
   // most kRangeMax (2048) tokens long otherwise
