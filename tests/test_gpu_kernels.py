@@ -302,8 +302,9 @@ def test_greedy_verify_matches_oracle():
 
 @pytest.mark.parametrize("V,stride", [(1003, 1003), (1003, 1004), (32000, 32000), (9, 12)])
 def test_greedy_verify_edge_rows(V, stride):
-    """vl_greedy_verify (one workgroup per sequence, rows two at a time, the
-    scan ending at the first mismatch) against the oracle's verify: ties to
+    """vl_greedy_verify (each row read in chunks whose argmax keys meet in one
+    atomic maximum per row; the sequence's last workgroup writes the picks up
+    to the first mismatch) against the oracle's verify: ties to
     the lowest index, NaN rows (the first NaN wins), rows of -inf, a vocab
     that is not a multiple of 4, rows that are not 16-byte aligned (odd
     stride: the scalar path), no drafts, every draft accepted (the bonus

@@ -106,8 +106,8 @@ __global__ void __launch_bounds__(256) argmax_rows_kernel(const float* __restric
 // bonus row when every draft matched), -1 after, and num_accepted; it clears
 // the counter. Rows past a sequence's drafts have no workgroups at work.
 constexpr int kVerifyThreads = 256;
-constexpr int kVerifyUnroll = 8;
-constexpr int kChunkFloats = 4 * kVerifyUnroll * kVerifyThreads;  // 8192
+constexpr int kVerifyUnroll = 16;
+constexpr int kChunkFloats = 4 * kVerifyUnroll * kVerifyThreads;  // 16384
 constexpr int kNoIndex = 0x7fffffff;
 
 // The key of value v at index idx: high word the value's order (every NaN
