@@ -187,53 +187,59 @@ __device__ __forceinline__ int wave_upper_bound_le(const int32_t* a, int n, int 
 
 // Exclusive scan of one int64 per thread across the workgroup; returns the
 // thread's offset and writes the total to *total.
+// x plus the 64-bit value DPP control kCtrl moves into this lane (0 where
+// it moves none, or in rows outside kRowMask)
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ unsigned long long dpp_add64(unsigned long long x) {
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)x, kCtrl, kRowMask, 0xF, false);
+  const int hi =
+      __builtin_amdgcn_update_dpp(0, (int)(unsigned)(x >> 32), kCtrl, kRowMask, 0xF, false);
+  return x + (((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+
+// Inclusive prefix sum over the 64 lanes of a wavefront by DPP: within each
+// row of 16 lanes by shifts of 1, 2, 4 and 8, then row 0's total into row 1
+// and row 2's into row 3 (row_bcast:15), then the first two rows' total into
+// rows 2 and 3 (row_bcast:31). Lanes without a source add 0.
+__device__ __forceinline__ int wave_incl_scan_dpp(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return x;
+}
+
 // Exclusive prefix sums over the plan workgroup of N values per thread at
-// once (v is replaced by its prefix; total gets the sums): a shuffle scan
-// within each wavefront, a shuffle scan of the wavefront totals by the first
-// wavefront, then every thread adds its wavefront's offset. Three barriers
-// for all N values. The counts are item, row and sequence counts, which the
-// plan stores as int32.
+// once (v is replaced by its prefix; total gets the sums): a DPP scan within
+// each wavefront, then every thread adds the totals of the wavefronts before
+// its own from LDS. Two barriers for all N values. The counts are item, row
+// and sequence counts, which the plan stores as int32.
 template <int N>
 __device__ void block_exclusive_scan(int (&v)[N], int (&total)[N]) {
   constexpr int kWaves = kPlanThreads / 64;
-  __shared__ int wsum[kWaves + 1][N];  // wavefront offsets, then the total
+  __shared__ int wsum[kWaves][N];  // wavefront totals
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   int incl[N];
 #pragma unroll
-  for (int k = 0; k < N; ++k) incl[k] = v[k];
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1)  // the N scans interleaved
-#pragma unroll
-    for (int k = 0; k < N; ++k) {
-      const int a = __shfl_up(incl[k], o, 64);
-      if (lane >= o) incl[k] += a;
-    }
+  for (int k = 0; k < N; ++k) incl[k] = wave_incl_scan_dpp(v[k]);
   if (lane == 63)
 #pragma unroll
     for (int k = 0; k < N; ++k) wsum[w][k] = incl[k];
   __syncthreads();
-  if (w == 0) {
-    int x[N], inc[N];
-#pragma unroll
-    for (int k = 0; k < N; ++k) x[k] = inc[k] = lane < kWaves ? wsum[lane][k] : 0;
-#pragma unroll
-    for (int o = 1; o < kWaves; o <<= 1)
-#pragma unroll
-      for (int k = 0; k < N; ++k) {
-        const int a = __shfl_up(inc[k], o, 64);
-        if (lane >= o) inc[k] += a;
-      }
-#pragma unroll
-    for (int k = 0; k < N; ++k) {
-      if (lane < kWaves) wsum[lane][k] = inc[k] - x[k];
-      if (lane == kWaves - 1) wsum[kWaves][k] = inc[k];
-    }
-  }
-  __syncthreads();
+  // every thread adds the totals of the wavefronts before its own
 #pragma unroll
   for (int k = 0; k < N; ++k) {
-    v[k] = wsum[w][k] + incl[k] - v[k];
-    total[k] = wsum[kWaves][k];
+    int off = 0, tot = 0;
+#pragma unroll
+    for (int u = 0; u < kWaves; ++u) {
+      const int s = wsum[u][k];
+      off += u < w ? s : 0;
+      tot += s;
+    }
+    v[k] = off + incl[k] - v[k];
+    total[k] = tot;
   }
   __syncthreads();  // wsum may be reused
 }
@@ -298,11 +304,20 @@ template <int N>
 __device__ __forceinline__ void plan_sum(unsigned long long (&v)[N],
                                          unsigned long long (*red)[N]) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // the wavefront's sum in lane 63 by DPP steps on the two 32-bit halves
+  // (quad and row permutes, then row_bcast:15 and row_bcast:31)
 #pragma unroll
-  for (int k = 0; k < N; ++k)
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v[k] += __shfl_xor(v[k], o, 64);
-  if (lane == 0)
+  for (int k = 0; k < N; ++k) {
+    unsigned long long x = v[k];
+    x = dpp_add64<0xB1, 0xF>(x);   // quad_perm [1, 0, 3, 2]
+    x = dpp_add64<0x4E, 0xF>(x);   // quad_perm [2, 3, 0, 1]
+    x = dpp_add64<0x141, 0xF>(x);  // row_half_mirror
+    x = dpp_add64<0x140, 0xF>(x);  // row_mirror
+    x = dpp_add64<0x142, 0xA>(x);  // row_bcast:15
+    x = dpp_add64<0x143, 0xC>(x);  // row_bcast:31
+    v[k] = x;
+  }
+  if (lane == 63)
 #pragma unroll
     for (int k = 0; k < N; ++k) red[w][k] = v[k];
   __syncthreads();
