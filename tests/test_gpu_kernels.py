@@ -845,3 +845,41 @@ def test_decode_attention_wo_refuses_other_batches():
         o.decode_attention_wo(parts, dev(b["q"]), dev(b["k_cache"]), dev(b["v_cache"]),
                               dev(b["block_tables"]), dev(b["seq_lens"]), dev(b["qsl"]),
                               b["scale"], 16, wo, 3000)
+
+
+@pytest.mark.parametrize("dtype,D,decode", [("bf16", 128, False), ("bf16", 128, True),
+                                             ("f32", 48, True)])
+def test_split_rows_merged_in_kernel_over_repeated_runs(dtype, D, decode):
+    """Short-query sequences over long contexts split into partitions that the
+    kernel running them merges itself (the row block's last workgroup; no
+    combine launch): one plan, then four runs as a model's layers run them.
+    Every run gives the same bits and matches the oracle, so the arrival
+    counters and the queue counters are back at zero after each run; the mix
+    of lengths puts short last partitions behind full ones (the bf16
+    longest-first order) and sequences that are not split beside split ones.
+    bf16 with a decode among them runs in the one-launch step kernel, without
+    in the tile kernel; fp32 in the fp32 tile kernel."""
+    o = ops()
+    seqs = [(5, 9000), (5, 300), (3, 20000), (16, 5000), (5, 64), (2, 12345), (5, 4097)]
+    if decode:
+        seqs.insert(3, (1, 7000))
+    H, Hkv = (32, 8) if dtype == "bf16" else (8, 4)
+    b = make_batch(seqs, H, Hkv, D, 16, seed=D + 3)
+    tdt = torch.float32 if dtype == "f32" else torch.bfloat16
+    q = dev(b["q"], tdt)
+    kc, vc = caches(b, tdt, "token")
+    S, T = len(seqs), b["q"].shape[0]
+    ws = o.AttentionWorkspace().get(o.paged_attention_workspace_size(S, T, H, D,
+                                                                     int(b["seq_lens"].max())))
+    bt, lens, qsl = dev(b["block_tables"]), dev(b["seq_lens"]), dev(b["qsl"])
+    o.paged_attention_plan(q, kc, lens, qsl, 16, ws)
+    outs = []
+    for _ in range(4):
+        out = torch.full_like(q, float("nan"))
+        o.paged_attention_run(out, q, kc, vc, bt, lens, qsl, b["scale"], 16, ws,
+                              max_query_len=16, min_query_len=1 if decode else 2)
+        outs.append(to_np(out))
+    want = expected(b, dtype)
+    for got in outs:
+        assert np.array_equal(got.view(np.uint8), outs[0].view(np.uint8))
+        check(got, want, dtype)
