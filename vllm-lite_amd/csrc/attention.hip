@@ -22,8 +22,10 @@
 //           wavefronts) when the head dim has an instantiation, else to the
 //           generic kernel (one wavefront per (sequence, query, head,
 //           partition)); a batch holding both kinds runs in the one step
-//           kernel. Split multi-query sequences are merged by the combine
-//           kernel (max-rescaled log-sum-exp).
+//           kernel. Split sequences are merged (max-rescaled log-sum-exp)
+//           by the last workgroup to finish a partition of them, in the
+//           bandwidth, tile and step kernels, and by the combine kernel
+//           after the generic one.
 //
 // Softmax runs in the base-2 domain: scores are pre-multiplied by
 // scale * log2(e) and exponentiated with exp2, which is the same function.
@@ -48,7 +50,8 @@ constexpr int kHdrInts = 64;  // [0] bandwidth-kernel items [1] generic items [2
                               // queue and the 8 tile queues, workgroups finished
                               // [26..33] 16-row tile kernel: work counters of its 8
                               // queues; [34..41] the same for the 32-row kernel
-                              // (zeroed by the plan, then by every combine launch)
+                              // (zeroed by the plan, then by the claim that
+                              // returns each queue's last value)
 constexpr int kPlanThreads = 256;
 constexpr int kMaxHeadDim = 256;
 constexpr int kSplitMaxQ = 16;  // only sequences with <= this many queries split their context
@@ -1575,7 +1578,8 @@ __device__ __forceinline__ int claimed_item(int64_t c, int stride, int base, int
 // block, so with 8 KV heads each XCD's L2 holds the K/V of its own KV head,
 // which the sequence's other row blocks read again; the plan orders the
 // items longest first, so the launch ends on short ones. The counters are
-// zeroed by the plan and by the combine launch that follows every run.
+// zeroed by the plan and, at the end of every run, by the claims that return
+// each queue's last value (below).
 template <typename T, int D, int RW, int kWv, typename TKV = T>
 __global__ void __launch_bounds__(64 * kWv) __attribute__((amdgpu_waves_per_eu(2))) attend_tile_kernel(
     VL_ATTN_PARAMS_KV(T, TKV), const int32_t* __restrict__ hdr, const int32_t* __restrict__ item_off,
