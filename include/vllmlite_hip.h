@@ -142,7 +142,10 @@ int vl_paged_attention(void* out, const void* query, int64_t query_stride, const
  * workspace, which must come from a _plan call with the same lengths, head
  * counts, head_dim, block_size, dtype and workspace size (stream-ordered before
  * it; the plan does not depend on kv_layout). vl_paged_attention is _plan
- * followed by _run.
+ * followed by _run. A run also uses the workspace as scratch (split partials,
+ * work and arrival counters, which it leaves at zero for the next run of the
+ * same plan): runs on one workspace must not overlap (one stream, or ordered
+ * by events).
  */
 int vl_paged_attention_plan(const int32_t* seq_lens, const int32_t* query_start_loc,
                             int num_seqs, int num_tokens, int num_heads, int num_kv_heads,
